@@ -1,0 +1,222 @@
+/*
+ * molt_amd.h - C ABI of the MI355X (gfx950) NF4 QLoRA hot-path library
+ * (libmolt_amd.so).
+ *
+ * The reference (PraveenNimilka/MOLT) is Python; its hot path reaches GPU
+ * code through bitsandbytes, cuBLAS (torch.nn.functional.linear under bf16
+ * autocast) and two Triton kernels. Each entry point below replaces one of
+ * those calls and cites it (paths relative to the reference's src/molt_stream/).
+ *
+ * Conventions
+ *  - Plain device pointers, element counts, strides (in elements) and scalars.
+ *    bf16 tensors are passed as uint16_t bit patterns.
+ *  - Every entry point launches asynchronously on `stream` (a hipStream_t;
+ *    NULL = the legacy default stream), never synchronises and never
+ *    allocates: any workspace is passed in by the caller.
+ *  - Return 0 on success or a MOLT_E* code; molt_amd_last_error() then holds a
+ *    thread-local message. The library keeps no mutable state between calls.
+ *  - NF4 weights: `rows x cols` row-major elements, two 4-bit codes per byte,
+ *    `nibble_order` 1 = element 2i in the high nibble (bitsandbytes,
+ *    methods/nf4_backward.py:97-98), 0 = element 2i in the low nibble
+ *    (streaming/nf4.py:62). Blocks of `block_size` consecutive flat elements
+ *    share one absmax. Dequantised value = bf16_rne(fp32(code[nibble] * scale)).
+ */
+#ifndef MOLT_AMD_H
+#define MOLT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOLT_OK 0
+#define MOLT_EINVAL 1        /* bad shape, stride, pointer or argument */
+#define MOLT_EUNSUPPORTED 2  /* valid request this library does not implement */
+#define MOLT_ELAUNCH 3       /* the HIP runtime refused a launch */
+#define MOLT_EWORKSPACE 4    /* caller workspace too small */
+
+#define MOLT_DTYPE_BF16 0
+#define MOLT_DTYPE_F32 1
+
+/* A quantised NF4 matrix. Either `scales` (one fp32 per block) is set, or the
+ * nested statistics (`absmax_q`, `absmax2`, `code2`, `offset`) are, with
+ * scale = fp32(fp32(code2[absmax_q[b]] * absmax2[b / dq_block]) + offset)
+ * (methods/nf4_backward.py:145-164). */
+typedef struct molt_nf4_weight {
+  const uint8_t* packed;
+  const float* scales;
+  const uint8_t* absmax_q;
+  const float* absmax2;
+  const float* code2;
+  const float* code;       /* 16 fp32 NF4 levels (quant_state.code) */
+  float offset;
+  int32_t nested;
+  int32_t block_size;
+  int32_t dq_block;        /* nested block of absmax values (256) */
+  int32_t nibble_order;
+  int64_t rows;            /* N = out_features */
+  int64_t cols;            /* K = in_features  */
+} molt_nf4_weight;
+
+/* ------------------------------------------------------------------------ */
+/* Library                                                                   */
+/* ------------------------------------------------------------------------ */
+const char* molt_amd_last_error(void);
+const char* molt_amd_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* NF4 codec                                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* Dense decode of an NF4 matrix to bf16 or fp32 (`out` holds rows*cols).
+ * Replaces bitsandbytes.functional.dequantize_4bit at methods/nf4_lora.py:97-98,
+ * methods/gated_replay.py:244, methods/nf4_layer_cache.py:51-53, and
+ * NF4DevicePayload.dequantize at streaming/nf4.py:29-35. */
+int molt_nf4_dequantize(const molt_nf4_weight* w, void* out, int32_t out_dtype, void* stream);
+
+/* Nested absmax -> fp32 scale per block (`out` holds ceil(rows*cols/block_size)).
+ * Replaces resolved_nf4_scales at methods/nf4_backward.py:145-164. */
+int molt_nf4_resolve_scales(const molt_nf4_weight* w, float* out, void* stream);
+
+/* Blockwise NF4 quantisation: fp32 absmax per block (clamped to FLT_MIN),
+ * code = first index of the nearest code to fp32(x / absmax); zero padding to a
+ * whole block. `packed` holds ceil(padded/2) bytes, `absmax` ceil(n/block) floats.
+ * Replaces NF4Tensor.quantize (streaming/nf4.py:46-68) and the NF4 part of
+ * bitsandbytes.functional.quantize_4bit (training/qlora.py:332-337). */
+int molt_nf4_quantize(const void* x, int32_t x_dtype, int64_t n, int32_t block_size,
+                      int32_t nibble_order, const float* code, uint8_t* packed,
+                      float* absmax, void* stream);
+
+/* Double quantisation of block absmax values (compress_statistics=True):
+ * offset = fp32(fp64 sum / n); q = first index of the nearest code2 value to
+ * fp32((absmax - offset) / absmax2[j]), absmax2[j] = max |absmax - offset| over
+ * each `dq_block` values. `offset_out` is one device float. Needs
+ * molt_nf4_double_quantize_workspace() bytes of workspace.
+ * Replaces the nested statistics of bitsandbytes quantize_4bit (training/qlora.py:332-337). */
+size_t molt_nf4_double_quantize_workspace(int64_t n);
+int molt_nf4_double_quantize(const float* absmax, int64_t n, int32_t dq_block,
+                             const float* code2, uint8_t* q, float* absmax2,
+                             float* offset_out, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* NF4 + LoRA linear                                                         */
+/* ------------------------------------------------------------------------ */
+
+/* Low-rank projection out[M, r] = bf16( sum_d z(m, d) * bf16(lora[q, d]) ).
+ *  z_mode 0: z = Z (bf16 [M, D], row stride ldz);
+ *  z_mode 1: z = bf16(bf16(silu(Z)) * Z2) (SwiGLU replay; Z = gate, Z2 = up);
+ *  z_mode 2: z = bf16(Z * z_scale)     (scale-before-matmul, methods/nf4_lora.py:87-90).
+ *  lora_layout 0: lora is [r, D] (LoRA A); 1: lora is [D, r] (LoRA B).
+ * Replaces the rank-r GEMMs F.linear(x, lora_a) (methods/nf4_lora.py:49) and
+ * scaled_grad @ lora_b (methods/nf4_lora.py:89-90). */
+int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t ldz, int32_t z_mode,
+                      float z_scale, int64_t M, int64_t D, const float* lora,
+                      int32_t lora_layout, int32_t r, uint16_t* out, int64_t ldo,
+                      void* stream);
+
+/* Y[M, N] = bf16( X . deq(W)^T + T . bf16(s * B)^T ), fp32 accumulation, with
+ * X bf16 [M, K], T bf16 [M, r] = molt_lora_project(X, lora_a) and B fp32 [N, r]
+ * (row stride r). `w->scales` must be resolved fp32 scales. r = 0 skips LoRA.
+ * Replaces bnb.matmul_4bit + the LoRA epilogue at methods/nf4_lora.py:43-50 and
+ * methods/gated_replay.py:211-224. */
+int molt_nf4_lora_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,
+                          const uint16_t* t, int64_t ldt, const float* lora_b, int32_t r,
+                          float scaling, uint16_t* y, int64_t ldy, void* stream);
+
+/* Gate and up projections of a gated MLP in one launch, sharing X:
+ *   gate = bf16(X . deq(Wg)^T + T[:, :r] . bf16(sg Bg)^T)
+ *   up   = bf16(X . deq(Wu)^T + T[:, r:] . bf16(su Bu)^T)
+ *   h    = bf16(bf16(silu(gate)) * up)
+ * with T bf16 [M, 2r] = [X . Ag^T | X . Au^T]. A workgroup owns gate and up of
+ * the same intermediate columns, so h is formed in registers from the two
+ * accumulators. Outputs are bf16 [M, I] with row stride ldo.
+ * Replaces the gate_proj/up_proj calls and `F.silu(gate) * up` of
+ * methods/gated_replay.py:78-94,290-291 (and benchmarks/qualified_path_measure.py:404-432). */
+int molt_nf4_gateup_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* wg,
+                            const molt_nf4_weight* wu, const uint16_t* t, int64_t ldt,
+                            const float* bg, const float* bu, int32_t r, float sg, float su,
+                            uint16_t* gate, uint16_t* up, uint16_t* h, int64_t ldo, void* stream);
+
+/* dX[M, K] = bf16( dY . deq(W) + U . bf16(lora_scale * A) ), U bf16 [M, r] (for
+ * the scheduled backward U = molt_lora_project(dY, lora_b, z_mode 2, s) and
+ * lora_scale = 1), A fp32 [r, K] (row stride K). r = 0 skips LoRA.
+ * Replaces the dX half of _ScheduledNF4LoRA.backward (methods/nf4_lora.py:86-101)
+ * and packed_nf4_backward_input / packed_nf4_lora_backward_input
+ * (methods/nf4_backward.py:167-284). */
+int molt_nf4_lora_backward_input(const uint16_t* dy, int64_t lddy, int64_t M,
+                                 const molt_nf4_weight* w, const uint16_t* u, int64_t ldu,
+                                 const float* lora_a, int32_t r, float lora_scale, uint16_t* dx,
+                                 int64_t lddx, void* stream);
+
+/* dX = dY0 . deq(W0) + dY1 . deq(W1) + U0 . bf16(A0) + U1 . bf16(A1): the input
+ * gradient of the gate and up projections of a gated MLP in one contraction
+ * (methods/gated_replay.py:167-186). */
+int molt_nf4_lora_backward_input_pair(const uint16_t* dy0, const uint16_t* dy1, int64_t lddy,
+                                      int64_t M, const molt_nf4_weight* w0,
+                                      const molt_nf4_weight* w1, const uint16_t* u0,
+                                      const uint16_t* u1, int64_t ldu, const float* a0,
+                                      const float* a1, int32_t r, uint16_t* dx, int64_t lddx,
+                                      void* stream);
+
+/* SwiGLU backward fused into the down projection's input gradient
+ * (methods/gated_replay.py:376-387; kernels/gated_activation.py:44-51):
+ * dh = bf16(dY . deq(Wd) + U . bf16(Ad)); dg = bf16(bf16(dh * up) * silu'(gate)),
+ * du = bf16(dh * bf16(silu(gate))). gate, up, dg, du are bf16 [M, I] with row
+ * stride ldg; dh is never stored. */
+int molt_nf4_swiglu_backward(const uint16_t* dy, int64_t lddy, int64_t M,
+                             const molt_nf4_weight* wd, const uint16_t* u, int64_t ldu,
+                             const float* lora_a, int32_t r, const uint16_t* gate,
+                             const uint16_t* up, int64_t ldg, uint16_t* dgate, uint16_t* dup,
+                             void* stream);
+
+/* LoRA weight gradient out = scale * L^T . R over M rows, fp32:
+ *  L bf16 [M, P] (l_mode 0) or SwiGLU replay of (L, L2) (l_mode 1); R bf16 [M, Q].
+ *  out_layout 0: out[P, Q] (dB = s dY^T T, methods/nf4_lora.py:102);
+ *  out_layout 1: out[Q, P] (dA = U^T X, methods/nf4_lora.py:103).
+ * Deterministic: a fixed split of M, partials summed in split order. */
+size_t molt_lora_grad_workspace(int64_t M, int64_t P, int64_t Q);
+int molt_lora_grad(const uint16_t* l, const uint16_t* l2, int64_t ldl, int32_t l_mode,
+                   const uint16_t* rmat, int64_t ldr, int64_t M, int64_t P, int64_t Q,
+                   float scale, float* out, int32_t out_layout, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Skinny-M NF4 GEMV (M <= 16)                                               */
+/* ------------------------------------------------------------------------ */
+
+/* Y[M, N] = bf16( X . (code[W] * scale)^T + T . bf16(s * B)^T ) for M <= 16,
+ * reading the nested statistics (or fp32 scales) directly. T bf16 [M, r] from
+ * molt_lora_project; r = 0 skips LoRA. Requires cols % 64 == 0 and
+ * block_size == 64. Workspace: molt_nf4_gemv_workspace() bytes; its first
+ * `counter` bytes must be zero before the first call and are left zero.
+ * Replaces the bnb.matmul_4bit decode path (training/qlora.py:1332-1358). */
+size_t molt_nf4_gemv_workspace(int64_t M, int64_t N, int64_t K);
+int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,
+                  const uint16_t* t, int64_t ldt, const float* lora_b, int32_t r,
+                  float scaling, uint16_t* y, int64_t ldy, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* SwiGLU elementwise                                                        */
+/* ------------------------------------------------------------------------ */
+
+/* h = g * sigmoid(g) * u in fp32, stored in the input dtype
+ * (kernels/gated_activation.py:29-36). With round_silu = 1 (bf16 only) silu(g)
+ * is rounded to bf16 before the product, as `F.silu(gate) * up` under bf16
+ * autocast does (methods/gated_replay.py:291). dtype: MOLT_DTYPE_BF16 or _F32. */
+int molt_silu_mul_forward(const void* gate, const void* up, void* out, int64_t n,
+                          int32_t dtype, int32_t round_silu, void* stream);
+
+/* dg = dh*u*sig*(1 + g*(1 - sig)), du = dh*g*sig in fp32
+ * (kernels/gated_activation.py:38-51). */
+int molt_silu_mul_backward(const void* grad, const void* gate, const void* up, void* dgate,
+                           void* dup, int64_t n, int32_t dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOLT_AMD_H */

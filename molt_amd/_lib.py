@@ -1,0 +1,102 @@
+"""ctypes binding of libmolt_amd.so (the C ABI declared in include/molt_amd.h).
+
+torch is imported before the library is opened so that its
+``libamdhip64.so.7`` (SONAME-identical to ROCm's) satisfies the library's HIP
+dependency: one HIP runtime per process, so torch stream handles and device
+pointers are valid arguments. There is no CPU fallback: every op raises when
+the library is missing or no GPU is present.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
+
+from .errors import CapabilityError
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmolt_amd.so"
+
+MOLT_OK, MOLT_EINVAL, MOLT_EUNSUPPORTED, MOLT_ELAUNCH, MOLT_EWORKSPACE = 0, 1, 2, 3, 4
+DTYPE_BF16, DTYPE_F32 = 0, 1
+
+_p = C.c_void_p
+_i64 = C.c_int64
+_i32 = C.c_int32
+_f32 = C.c_float
+_sz = C.c_size_t
+
+
+class NF4Weight(C.Structure):
+    """Mirror of ``molt_nf4_weight``."""
+    _fields_ = [
+        ("packed", _p), ("scales", _p), ("absmax_q", _p), ("absmax2", _p),
+        ("code2", _p), ("code", _p), ("offset", _f32), ("nested", _i32),
+        ("block_size", _i32), ("dq_block", _i32), ("nibble_order", _i32),
+        ("rows", _i64), ("cols", _i64),
+    ]
+
+
+_W = C.POINTER(NF4Weight)
+
+# name -> (restype, argtypes); the exact list of include/molt_amd.h.
+SIGNATURES: dict[str, tuple] = {
+    "molt_amd_last_error": (C.c_char_p, []),
+    "molt_amd_version": (C.c_char_p, []),
+    "molt_nf4_dequantize": (C.c_int, [_W, _p, _i32, _p]),
+    "molt_nf4_resolve_scales": (C.c_int, [_W, _p, _p]),
+    "molt_nf4_quantize": (C.c_int, [_p, _i32, _i64, _i32, _i32, _p, _p, _p, _p]),
+    "molt_nf4_double_quantize_workspace": (_sz, [_i64]),
+    "molt_nf4_double_quantize": (C.c_int, [_p, _i64, _i32, _p, _p, _p, _p, _p, _sz, _p]),
+    "molt_lora_project": (C.c_int, [_p, _p, _i64, _i32, _f32, _i64, _i64, _p, _i32, _i32, _p, _i64, _p]),
+    "molt_nf4_lora_forward": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _f32, _p, _i64, _p]),
+    "molt_nf4_gateup_forward": (C.c_int, [_p, _i64, _i64, _W, _W, _p, _i64, _p, _p, _i32, _f32, _f32,
+                                          _p, _p, _p, _i64, _p]),
+    "molt_nf4_lora_backward_input": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _f32, _p, _i64, _p]),
+    "molt_nf4_lora_backward_input_pair": (C.c_int, [_p, _p, _i64, _i64, _W, _W, _p, _p, _i64, _p, _p,
+                                                    _i32, _p, _i64, _p]),
+    "molt_nf4_swiglu_backward": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _p, _p, _i64, _p, _p,
+                                           _p]),
+    "molt_lora_grad_workspace": (_sz, [_i64, _i64, _i64]),
+    "molt_lora_grad": (C.c_int, [_p, _p, _i64, _i32, _p, _i64, _i64, _i64, _i64, _f32, _p, _i32, _p, _sz,
+                                 _p]),
+    "molt_nf4_gemv_workspace": (_sz, [_i64, _i64, _i64]),
+    "molt_nf4_gemv": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _f32, _p, _i64, _p, _sz, _p]),
+    "molt_silu_mul_forward": (C.c_int, [_p, _p, _p, _i64, _i32, _i32, _p]),
+    "molt_silu_mul_backward": (C.c_int, [_p, _p, _p, _p, _p, _i64, _i32, _p]),
+}
+
+_lock = threading.Lock()
+_lib: C.CDLL | None = None
+
+
+def load(path: Path | str | None = None) -> C.CDLL:
+    """Open the library (once) and bind every declared symbol."""
+    global _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        target = Path(path) if path is not None else LIB_PATH
+        if not target.exists():
+            raise CapabilityError(
+                f"{target} is not built; run `python -m molt_amd.build` (hipcc, gfx950)")
+        lib = C.CDLL(str(target))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def check(rc: int) -> None:
+    if rc == MOLT_OK:
+        return
+    msg = (load().molt_amd_last_error() or b"").decode(errors="replace")
+    if rc == MOLT_EUNSUPPORTED:
+        raise CapabilityError(msg)
+    if rc in (MOLT_EINVAL, MOLT_EWORKSPACE):
+        raise ValueError(msg)
+    raise RuntimeError(msg)

@@ -1,0 +1,91 @@
+// C ABI glue: thread-local error reporting and the NF4+LoRA GEMM entry points
+// declared in include/molt_amd.h (the kernels live in nf4_gemm.hip).
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/molt_amd.h"
+
+namespace molt {
+
+static thread_local char g_last_error[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(MOLT_ELAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return MOLT_OK;
+}
+
+}  // namespace molt
+
+extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w0,
+                                          const molt_nf4_weight* w1, const uint16_t* t, int64_t ldt, int lr,
+                                          const float* b0, const float* b1, int64_t ldb, int r, float s0, float s1,
+                                          uint16_t* y0, uint16_t* y1, uint16_t* y2, int64_t ldy,
+                                          hipStream_t stream);
+extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* dy1, int64_t lddy, int64_t M,
+                                           const molt_nf4_weight* w0, const molt_nf4_weight* w1,
+                                           const uint16_t* u0, const uint16_t* u1, int64_t ldu, const float* a0,
+                                           const float* a1, int64_t lda, int r, float lora_scale, uint16_t* dx,
+                                           int64_t lddx, const uint16_t* gate, const uint16_t* up, uint16_t* dg, uint16_t* du,
+                                           int64_t ldg, hipStream_t stream);
+
+extern "C" {
+
+const char* molt_amd_last_error(void) { return molt::g_last_error; }
+
+const char* molt_amd_version(void) { return "molt_amd 0.1.0 gfx950"; }
+
+int molt_nf4_lora_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,
+                          const uint16_t* t, int64_t ldt, const float* lora_b, int32_t r, float scaling,
+                          uint16_t* y, int64_t ldy, void* stream) {
+  if (!w) return molt::set_error(MOLT_EINVAL, "molt_nf4_lora_forward: null weight");
+  return molt_nf4_lora_forward_impl(x, ldx, M, w, nullptr, t, ldt, r, lora_b, nullptr, r, r, scaling, scaling,
+                                    y, nullptr, nullptr, ldy, (hipStream_t)stream);
+}
+
+int molt_nf4_gateup_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* wg,
+                            const molt_nf4_weight* wu, const uint16_t* t, int64_t ldt, const float* bg,
+                            const float* bu, int32_t r, float sg, float su, uint16_t* gate, uint16_t* up,
+                            uint16_t* h, int64_t ldo, void* stream) {
+  if (!wg || !wu) return molt::set_error(MOLT_EINVAL, "molt_nf4_gateup_forward: null weight");
+  return molt_nf4_lora_forward_impl(x, ldx, M, wg, wu, t, ldt, 2 * r, bg, bu, r, r, sg, su, gate, up, h, ldo,
+                                    (hipStream_t)stream);
+}
+
+int molt_nf4_lora_backward_input(const uint16_t* dy, int64_t lddy, int64_t M, const molt_nf4_weight* w,
+                                 const uint16_t* u, int64_t ldu, const float* lora_a, int32_t r, float lora_scale,
+                                 uint16_t* dx, int64_t lddx, void* stream) {
+  if (!w) return molt::set_error(MOLT_EINVAL, "molt_nf4_lora_backward_input: null weight");
+  return molt_nf4_lora_backward_impl(dy, nullptr, lddy, M, w, nullptr, u, nullptr, ldu, lora_a, nullptr, w->cols,
+                                     r, lora_scale, dx, lddx, nullptr, nullptr, nullptr, nullptr, 0,
+                                     (hipStream_t)stream);
+}
+
+int molt_nf4_lora_backward_input_pair(const uint16_t* dy0, const uint16_t* dy1, int64_t lddy, int64_t M,
+                                      const molt_nf4_weight* w0, const molt_nf4_weight* w1, const uint16_t* u0,
+                                      const uint16_t* u1, int64_t ldu, const float* a0, const float* a1,
+                                      int32_t r, uint16_t* dx, int64_t lddx, void* stream) {
+  if (!w0 || !w1) return molt::set_error(MOLT_EINVAL, "molt_nf4_lora_backward_input_pair: null weight");
+  return molt_nf4_lora_backward_impl(dy0, dy1, lddy, M, w0, w1, u0, u1, ldu, a0, a1, w0->cols, r, 1.0f, dx, lddx,
+                                     nullptr, nullptr, nullptr, nullptr, 0, (hipStream_t)stream);
+}
+
+int molt_nf4_swiglu_backward(const uint16_t* dy, int64_t lddy, int64_t M, const molt_nf4_weight* wd,
+                             const uint16_t* u, int64_t ldu, const float* lora_a, int32_t r, const uint16_t* gate,
+                             const uint16_t* up, int64_t ldg, uint16_t* dgate, uint16_t* dup, void* stream) {
+  if (!wd) return molt::set_error(MOLT_EINVAL, "molt_nf4_swiglu_backward: null weight");
+  if (!dgate) return molt::set_error(MOLT_EINVAL, "molt_nf4_swiglu_backward: null dgate");
+  return molt_nf4_lora_backward_impl(dy, nullptr, lddy, M, wd, nullptr, u, nullptr, ldu, lora_a, nullptr, wd->cols,
+                                     r, 1.0f, nullptr, 0, gate, up, dgate, dup, ldg, (hipStream_t)stream);
+}
+
+}  // extern "C"

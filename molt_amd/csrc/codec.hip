@@ -1,0 +1,347 @@
+// NF4 codec kernels (gfx950): dequantise, resolve nested scales, quantise,
+// double-quantise. Every arithmetic step is a single IEEE fp32 operation in a
+// fixed order (explicit __fmul_rn/__fadd_rn so nothing is contracted into an
+// FMA), which makes the results bit-exact against the CPU restatement.
+#include "common.h"
+
+namespace molt {
+namespace {
+
+constexpr int CODEC_NT = 256;
+
+struct ScaleSrc {
+  const float* scales;
+  const uint8_t* q; const float* absmax2; const float* code2; float offset; int dq_block;
+  int nested;
+};
+
+// scale = fp32(fp32(code2[q] * absmax2[b / dq]) + offset), or the fp32 scale itself.
+MOLT_DEV float block_scale(const ScaleSrc& s, int64_t b) {
+  if (!s.nested) return s.scales[b];
+  return __fadd_rn(__fmul_rn(s.code2[s.q[b]], s.absmax2[b / s.dq_block]), s.offset);
+}
+
+// ---------------------------------------------------------------- dequantise
+// One thread per 16 packed bytes (32 elements). Byte -> code pair from a
+// 256-entry LDS table, times the block scale, rounded once to the output dtype.
+template <int OUT_F32, bool BLK32>
+__global__ __launch_bounds__(CODEC_NT) void dequant_kernel(const uint8_t* __restrict__ packed,
+                                                           ScaleSrc ss, const float* __restrict__ code,
+                                                           int order, int64_t n, int block,
+                                                           void* __restrict__ out) {
+  __shared__ float2 tab[256];
+  {
+    const int b = threadIdx.x;
+    const int hi = b >> 4, lo = b & 15;
+    tab[b] = make_float2(code[order ? hi : lo], code[order ? lo : hi]);
+  }
+  __syncthreads();
+  const int64_t chunks = (n + 31) / 32;
+  for (int64_t c = (int64_t)blockIdx.x * CODEC_NT + threadIdx.x; c < chunks;
+       c += (int64_t)gridDim.x * CODEC_NT) {
+    const int64_t e0 = c * 32;
+    const bool full = e0 + 32 <= n;
+    u32x4_t q;
+    if (full) {
+      q = *reinterpret_cast<const u32x4_t*>(packed + c * 16);
+    } else {
+      uint8_t tmp[16];
+      const int64_t nbytes = (n - e0 + 1) / 2;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) tmp[i] = i < nbytes ? packed[c * 16 + i] : 0;
+      q = __builtin_bit_cast(u32x4_t, tmp);
+    }
+    float v[32];
+    if (BLK32) {
+      const float sc = block_scale(ss, e0 / block);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float2 p = tab[(q[i >> 2] >> (8 * (i & 3))) & 0xffu];
+        v[2 * i] = __fmul_rn(p.x, sc);
+        v[2 * i + 1] = __fmul_rn(p.y, sc);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float2 p = tab[(q[i >> 2] >> (8 * (i & 3))) & 0xffu];
+        const int64_t ea = e0 + 2 * i, eb = ea + 1;
+        v[2 * i] = ea < n ? __fmul_rn(p.x, block_scale(ss, ea / block)) : 0.0f;
+        v[2 * i + 1] = eb < n ? __fmul_rn(p.y, block_scale(ss, eb / block)) : 0.0f;
+      }
+    }
+    if (OUT_F32) {
+      float* o = reinterpret_cast<float*>(out) + e0;
+      if (full) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          *reinterpret_cast<f32x4_t*>(o + 4 * i) = f32x4_t{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+      } else {
+        for (int i = 0; i < 32; ++i)
+          if (e0 + i < n) o[i] = v[i];
+      }
+    } else {
+      uint16_t* o = reinterpret_cast<uint16_t*>(out) + e0;
+      if (full) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          u32x4_t w;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(v[8 * i + 2 * j], v[8 * i + 2 * j + 1]);
+          *reinterpret_cast<u32x4_t*>(o + 8 * i) = w;
+        }
+      } else {
+        for (int i = 0; i < 32; ++i)
+          if (e0 + i < n) o[i] = bf16_bits(v[i]);
+      }
+    }
+  }
+}
+
+__global__ void resolve_kernel(ScaleSrc ss, int64_t nblocks, float* __restrict__ out) {
+  for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblocks;
+       b += (int64_t)gridDim.x * blockDim.x)
+    out[b] = block_scale(ss, b);
+}
+
+// ------------------------------------------------------------------ quantise
+// One wave per block: absmax by wave reduction (max is order independent),
+// then each element's code is the first index of the minimum |x/absmax - code|.
+MOLT_DEV float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+template <int IN_BF16>
+__global__ __launch_bounds__(CODEC_NT) void quantize_kernel(const void* __restrict__ x, int64_t n,
+                                                            int block, int order,
+                                                            const float* __restrict__ code,
+                                                            uint8_t* __restrict__ packed,
+                                                            float* __restrict__ absmax,
+                                                            int64_t nblocks) {
+  __shared__ float cb[16];
+  if (threadIdx.x < 16) cb[threadIdx.x] = code[threadIdx.x];
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int64_t waves = (int64_t)gridDim.x * (CODEC_NT / 64);
+  auto load = [&](int64_t i) -> float {
+    if (i >= n) return 0.0f;
+    if (IN_BF16) return bf16_to_f32(reinterpret_cast<const uint16_t*>(x)[i]);
+    return reinterpret_cast<const float*>(x)[i];
+  };
+  for (int64_t b = (int64_t)blockIdx.x * (CODEC_NT / 64) + (threadIdx.x >> 6); b < nblocks; b += waves) {
+    const int64_t base = b * block;
+    float m = 0.0f;
+    for (int i = lane; i < block; i += 64) m = fmaxf(m, fabsf(load(base + i)));
+    m = wave_max(m);
+    const float am = fmaxf(m, 1.17549435e-38f);
+    if (lane == 0) absmax[b] = am;
+    // pairs: lane handles elements (2j, 2j+1) of the block
+    for (int j = lane; j < block / 2; j += 64) {
+      uint32_t idx[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const float nv = load(base + 2 * j + t) / am;
+        float best = fabsf(nv - cb[0]);
+        uint32_t bi = 0;
+#pragma unroll
+        for (int c = 1; c < 16; ++c) {
+          const float d = fabsf(nv - cb[c]);
+          if (d < best) { best = d; bi = (uint32_t)c; }
+        }
+        idx[t] = bi;
+      }
+      packed[(base >> 1) + j] = (uint8_t)(order ? ((idx[0] << 4) | idx[1]) : (idx[0] | (idx[1] << 4)));
+    }
+  }
+}
+
+// ------------------------------------------------------------ double quantise
+// offset = fp32(S / n) with S the fp64 sum in a fixed tree: each workgroup
+// sums a chunk of 4096 values (thread t adds values 16t..16t+15 left to right,
+// then a halving tree over the 256 threads); chunk sums are added left to right.
+constexpr int DQ_CHUNK = 4096;
+
+__global__ __launch_bounds__(CODEC_NT) void dq_chunk_sum_kernel(const float* __restrict__ a, int64_t n,
+                                                                double* __restrict__ partial) {
+  __shared__ double red[CODEC_NT];
+  const int64_t base = (int64_t)blockIdx.x * DQ_CHUNK + threadIdx.x * 16;
+  double s = 0.0;
+  for (int i = 0; i < 16; ++i) {
+    const int64_t k = base + i;
+    s += k < n ? (double)a[k] : 0.0;
+  }
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int stride = CODEC_NT / 2; stride >= 1; stride >>= 1) {
+    if (threadIdx.x < stride) red[threadIdx.x] += red[threadIdx.x + stride];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
+}
+
+__global__ void dq_offset_kernel(const double* __restrict__ partial, int64_t chunks, int64_t n,
+                                 float* __restrict__ offset) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  double s = 0.0;
+  for (int64_t i = 0; i < chunks; ++i) s += partial[i];
+  *offset = (float)(s / (double)n);
+}
+
+// One workgroup per dq block (<= 256 values): absmax2 over |absmax - offset|,
+// then the first index of the nearest code2 entry for each value.
+__global__ __launch_bounds__(CODEC_NT) void dq_quant_kernel(const float* __restrict__ a, int64_t n, int dq,
+                                                            const float* __restrict__ code2,
+                                                            const float* __restrict__ offset,
+                                                            uint8_t* __restrict__ q,
+                                                            float* __restrict__ absmax2) {
+  __shared__ float cb[256];
+  __shared__ float wmax[CODEC_NT / 64];
+  cb[threadIdx.x] = code2[threadIdx.x];
+  const float off = *offset;
+  const int64_t b = blockIdx.x;
+  float mx = 0.0f;
+  for (int i = threadIdx.x; i < dq; i += CODEC_NT) {
+    const int64_t k = b * dq + i;
+    if (k < n) mx = fmaxf(mx, fabsf(__fsub_rn(a[k], off)));
+  }
+  mx = wave_max(mx);
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  float am = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  am = fmaxf(am, 1.17549435e-38f);
+  if (threadIdx.x == 0) absmax2[b] = am;
+  for (int i = threadIdx.x; i < dq; i += CODEC_NT) {
+    const int64_t k = b * dq + i;
+    if (k >= n) continue;
+    const float nv = __fsub_rn(a[k], off) / am;
+    float best = fabsf(nv - cb[0]);
+    int bi = 0;
+    for (int c = 1; c < 256; ++c) {
+      const float d = fabsf(nv - cb[c]);
+      if (d < best) { best = d; bi = c; }
+    }
+    q[k] = (uint8_t)bi;
+  }
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int make_scale_src(const molt_nf4_weight* w, ScaleSrc& s, const char* who) {
+  s = ScaleSrc{};
+  s.nested = w->nested != 0;
+  if (s.nested) {
+    MOLT_REQUIRE(w->absmax_q && w->absmax2 && w->code2 && w->dq_block > 0, MOLT_EINVAL,
+                 "%s: nested statistics incomplete", who);
+    s.q = w->absmax_q; s.absmax2 = w->absmax2; s.code2 = w->code2; s.offset = w->offset;
+    s.dq_block = w->dq_block;
+  } else {
+    MOLT_REQUIRE(w->scales, MOLT_EINVAL, "%s: scales missing", who);
+    s.scales = w->scales;
+  }
+  return MOLT_OK;
+}
+
+unsigned grid_for(int64_t items, int64_t per_block) {
+  int64_t g = (items + per_block - 1) / per_block;
+  if (g > 8192) g = 8192;
+  if (g < 1) g = 1;
+  return (unsigned)g;
+}
+
+}  // namespace
+}  // namespace molt
+
+using namespace molt;
+
+extern "C" int molt_nf4_dequantize(const molt_nf4_weight* w, void* out, int32_t out_dtype, void* stream) {
+  const char* who = "molt_nf4_dequantize";
+  MOLT_REQUIRE(w && w->packed && w->code && out, MOLT_EINVAL, "%s: null argument", who);
+  MOLT_REQUIRE(out_dtype == MOLT_DTYPE_BF16 || out_dtype == MOLT_DTYPE_F32, MOLT_EINVAL, "%s: bad dtype", who);
+  MOLT_REQUIRE(w->rows >= 0 && w->cols >= 0 && w->block_size > 0, MOLT_EINVAL, "%s: bad shape", who);
+  MOLT_REQUIRE(w->nibble_order == 0 || w->nibble_order == 1, MOLT_EINVAL, "%s: bad nibble order", who);
+  ScaleSrc ss;
+  int rc = make_scale_src(w, ss, who);
+  if (rc) return rc;
+  const int64_t n = w->rows * w->cols;
+  if (n == 0) return MOLT_OK;
+  MOLT_REQUIRE(aligned(w->packed, 16), MOLT_EINVAL, "%s: packed data must be 16-byte aligned", who);
+  MOLT_REQUIRE(aligned(out, 16), MOLT_EINVAL, "%s: output must be 16-byte aligned", who);
+  const bool blk32 = w->block_size % 32 == 0;
+  const unsigned grid = grid_for((n + 31) / 32, CODEC_NT);
+  hipStream_t st = (hipStream_t)stream;
+#define MOLT_DQ(F32, B32)                                                                        \
+  hipLaunchKernelGGL((dequant_kernel<F32, B32>), dim3(grid), dim3(CODEC_NT), 0, st, w->packed, ss, \
+                     w->code, w->nibble_order, n, w->block_size, out)
+  if (out_dtype == MOLT_DTYPE_F32) {
+    if (blk32) MOLT_DQ(1, true); else MOLT_DQ(1, false);
+  } else {
+    if (blk32) MOLT_DQ(0, true); else MOLT_DQ(0, false);
+  }
+#undef MOLT_DQ
+  return check_launch(who);
+}
+
+extern "C" int molt_nf4_resolve_scales(const molt_nf4_weight* w, float* out, void* stream) {
+  const char* who = "molt_nf4_resolve_scales";
+  MOLT_REQUIRE(w && out && w->block_size > 0, MOLT_EINVAL, "%s: null argument", who);
+  ScaleSrc ss;
+  int rc = make_scale_src(w, ss, who);
+  if (rc) return rc;
+  const int64_t nblocks = ceil_div64(w->rows * w->cols, w->block_size);
+  if (nblocks == 0) return MOLT_OK;
+  hipLaunchKernelGGL(resolve_kernel, dim3(grid_for(nblocks, 256)), dim3(256), 0, (hipStream_t)stream, ss,
+                     nblocks, out);
+  return check_launch(who);
+}
+
+extern "C" int molt_nf4_quantize(const void* x, int32_t x_dtype, int64_t n, int32_t block_size,
+                                 int32_t nibble_order, const float* code, uint8_t* packed, float* absmax,
+                                 void* stream) {
+  const char* who = "molt_nf4_quantize";
+  MOLT_REQUIRE(x && code && packed && absmax, MOLT_EINVAL, "%s: null argument", who);
+  MOLT_REQUIRE(n > 0 && block_size >= 16 && block_size % 2 == 0, MOLT_EINVAL,
+               "%s: invalid tensor or NF4 block size", who);
+  MOLT_REQUIRE(x_dtype == MOLT_DTYPE_BF16 || x_dtype == MOLT_DTYPE_F32, MOLT_EINVAL, "%s: bad dtype", who);
+  MOLT_REQUIRE(nibble_order == 0 || nibble_order == 1, MOLT_EINVAL, "%s: bad nibble order", who);
+  const int64_t nblocks = ceil_div64(n, block_size);
+  const unsigned grid = grid_for(nblocks, CODEC_NT / 64);
+  hipStream_t st = (hipStream_t)stream;
+  if (x_dtype == MOLT_DTYPE_BF16)
+    hipLaunchKernelGGL((quantize_kernel<1>), dim3(grid), dim3(CODEC_NT), 0, st, x, n, block_size, nibble_order,
+                       code, packed, absmax, nblocks);
+  else
+    hipLaunchKernelGGL((quantize_kernel<0>), dim3(grid), dim3(CODEC_NT), 0, st, x, n, block_size, nibble_order,
+                       code, packed, absmax, nblocks);
+  return check_launch(who);
+}
+
+extern "C" size_t molt_nf4_double_quantize_workspace(int64_t n) {
+  if (n <= 0) return 0;
+  return (size_t)ceil_div64(n, DQ_CHUNK) * sizeof(double);
+}
+
+extern "C" int molt_nf4_double_quantize(const float* absmax, int64_t n, int32_t dq_block, const float* code2,
+                                        uint8_t* q, float* absmax2, float* offset_out, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  const char* who = "molt_nf4_double_quantize";
+  MOLT_REQUIRE(absmax && code2 && q && absmax2 && offset_out, MOLT_EINVAL, "%s: null argument", who);
+  MOLT_REQUIRE(n > 0 && dq_block > 0 && dq_block <= 4096, MOLT_EINVAL, "%s: bad shape", who);
+  const int64_t chunks = ceil_div64(n, DQ_CHUNK);
+  MOLT_REQUIRE(workspace && workspace_bytes >= (size_t)chunks * sizeof(double), MOLT_EWORKSPACE,
+               "%s: workspace too small", who);
+  MOLT_REQUIRE(aligned(workspace, 8), MOLT_EINVAL, "%s: workspace must be 8-byte aligned", who);
+  hipStream_t st = (hipStream_t)stream;
+  double* partial = (double*)workspace;
+  hipLaunchKernelGGL(dq_chunk_sum_kernel, dim3((unsigned)chunks), dim3(CODEC_NT), 0, st, absmax, n, partial);
+  int rc = check_launch(who);
+  if (rc) return rc;
+  hipLaunchKernelGGL(dq_offset_kernel, dim3(1), dim3(64), 0, st, partial, chunks, n, offset_out);
+  rc = check_launch(who);
+  if (rc) return rc;
+  const int64_t nb = ceil_div64(n, dq_block);
+  MOLT_REQUIRE(nb < (1ll << 31), MOLT_EINVAL, "%s: too many blocks", who);
+  hipLaunchKernelGGL(dq_quant_kernel, dim3((unsigned)nb), dim3(CODEC_NT), 0, st, absmax, n, dq_block, code2,
+                     offset_out, q, absmax2);
+  return check_launch(who);
+}

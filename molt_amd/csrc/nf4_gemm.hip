@@ -1,0 +1,609 @@
+// NF4-fused bf16 MFMA GEMMs for the NF4+LoRA linear (gfx950).
+//
+// Forward   Y[M,N]  = X[M,K] . deq(W[N,K])^T + T[M,r] . bf16(s B[N,r])^T
+// Backward  dX[M,K] = dY[M,N] . deq(W[N,K])  + U[M,r] . bf16(A[r,K])
+//
+// The NF4 weight is dequantised while it is staged into LDS: packed bytes are
+// read with 16-byte (forward) or 2-byte-per-row patch (backward) loads, each
+// byte is looked up in a 256-entry LDS table of fp32 code pairs, multiplied by
+// the block's fp32 scale and rounded to bf16 (the same bf16 values
+// bitsandbytes.functional.dequantize_4bit produces), then fed to
+// v_mfma_f32_32x32x16_bf16 with fp32 accumulation. The backward stages an
+// 8-row x 4-column patch per thread and transposes it in registers, so the
+// contraction index (a row of W) becomes contiguous in LDS.
+//
+// The rank-r LoRA term is folded into the same accumulator as extra
+// contraction steps: the A-side operand is T (or U) and the W-side operand is
+// the fp32 adapter matrix scaled and rounded to bf16, so the output is rounded
+// to bf16 exactly once.
+//
+// Gate/up pairing (forward): one workgroup computes gate and up for the same
+// 64 intermediate columns. Each wave's 64-row W sub-tile holds 32 gate rows
+// then the 32 up rows of the same columns, so a lane owns gate and up of the
+// same (m, i) and the epilogue writes g, u and h = bf16(bf16(silu(g)) u).
+#include "mfma_core.h"
+
+namespace molt {
+namespace {
+
+constexpr int BM = 128;        // X rows per workgroup tile
+constexpr int BN = 128;        // W rows (forward) / output columns (backward) per tile
+constexpr int WAVES_M = 2, WAVES_N = 2;
+constexpr int NT = 64 * WAVES_M * WAVES_N;
+constexpr int WROWS = BN / WAVES_N;   // 64
+constexpr int WCOLS = BM / WAVES_M;   // 64
+constexpr int TM = WROWS / 32, TN = WCOLS / 32;
+constexpr int GROUP_M = 8;
+
+enum { EPI_STORE = 0, EPI_GATEUP = 1, EPI_SWIGLU_BWD = 2 };
+
+struct FwdParams {
+  const uint16_t* x; int64_t ldx; int64_t M; int64_t K;
+  const uint8_t* packed[2]; const float* scales[2];
+  int64_t N;                 // rows of each weight
+  const float* code; int order; int block_size;
+  const uint16_t* t; int64_t ldt; int lr;      // LoRA contraction length (0 = none)
+  const float* lb[2]; int64_t ldlb; int r; float s[2];
+  uint16_t* y[3]; int64_t ldy;                 // single: y[0]; pair: g, u, h
+  int vec_out;
+};
+
+struct BwdParams {
+  const uint16_t* dy[2]; int64_t lddy; int64_t M;
+  const uint8_t* packed[2]; const float* scales[2];
+  int64_t Nw;                // contraction length per segment (rows of W)
+  int64_t Kw;                // output columns (cols of W)
+  const float* code; int order; int block_size; int nseg;
+  const uint16_t* u[2]; int64_t ldu; int r;
+  const float* la[2]; int64_t ldla; float la_scale;
+  uint16_t* dx; int64_t lddx;
+  const uint16_t* gate; const uint16_t* up; uint16_t* dg; uint16_t* du; int64_t ldg;
+  int vec_out;
+};
+
+struct Smem {
+  uint16_t xs[2][BM * LDSW];
+  uint16_t ws[2][BN * LDSW];
+  float2 tab[256];
+  float code16[16];
+};
+
+MOLT_DEV float silu_f32(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
+
+MOLT_DEV uint32_t dequant_pair(const float2* tab, uint32_t byte, float sc) {
+  const float2 c = tab[byte];
+  return pack_bf16x2(c.x * sc, c.y * sc);
+}
+
+// ------------------------------------------------------------ X-side staging
+struct AReg { u32x4_t v[BM * BK / 8 / NT]; };
+constexpr int A_PT = BM * BK / 8 / NT;  // 16-byte chunks per thread (4)
+
+MOLT_DEV void a_issue(AReg& ar, const uint16_t* __restrict__ a, int64_t lda, int64_t m0,
+                      int64_t M, int64_t k0, int tid) {
+#pragma unroll
+  for (int c = 0; c < A_PT; ++c) {
+    const int idx = tid + c * NT;
+    const int row = idx >> 3, col = (idx & 7) * 8;
+    const int64_t m = m0 + row;
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (m < M) v = *reinterpret_cast<const u32x4_t*>(a + m * lda + k0 + col);
+    ar.v[c] = v;
+  }
+}
+
+MOLT_DEV void a_commit(const AReg& ar, uint16_t* xs, int tid) {
+#pragma unroll
+  for (int c = 0; c < A_PT; ++c) {
+    const int idx = tid + c * NT;
+    const int row = idx >> 3, col = (idx & 7) * 8;
+    *reinterpret_cast<u32x4_t*>(xs + row * LDSW + col) = ar.v[c];
+  }
+}
+
+// Element-wise X-side staging with full bounds checks (tails, odd strides, LoRA steps).
+MOLT_DEV void a_generic(uint16_t* xs, const uint16_t* __restrict__ a, int64_t lda, int64_t m0,
+                        int64_t M, int64_t k0, int64_t L, int tid) {
+  for (int e = tid; e < BM * BK; e += NT) {
+    const int row = e / BK, j = e % BK;
+    const int64_t m = m0 + row, k = k0 + j;
+    xs[row * LDSW + j] = (m < M && k < L) ? a[m * lda + k] : (uint16_t)0;
+  }
+}
+
+// ------------------------------------------------ forward W-side (row-contract)
+// LDS row R of the W tile -> (weight index, weight row).
+MOLT_DEV void fwd_row(int R, int64_t tn, bool pair, int& which, int64_t& n) {
+  if (pair) {
+    which = (R >> 5) & 1;
+    n = tn * (BN / 2) + (R >> 6) * 32 + (R & 31);
+  } else {
+    which = 0;
+    n = tn * BN + R;
+  }
+}
+
+struct WRowReg { u32x4_t q; float sc; };
+
+MOLT_DEV void wrow_issue(WRowReg& wr, const FwdParams& p, int64_t tn, bool pair, int64_t k0, int tid) {
+  const int R = tid >> 1, half = tid & 1;
+  int which; int64_t n;
+  fwd_row(R, tn, pair, which, n);
+  const int64_t k = k0 + 32 * half;
+  u32x4_t q = {0u, 0u, 0u, 0u};
+  float sc = 0.0f;
+  if (n < p.N) {
+    const int64_t flat = n * p.K + k;
+    q = *reinterpret_cast<const u32x4_t*>(p.packed[which] + (flat >> 1));
+    sc = p.scales[which][flat >> 6];
+  }
+  wr.q = q;
+  wr.sc = sc;
+}
+
+MOLT_DEV void wrow_commit(const WRowReg& wr, uint16_t* ws, const float2* tab, int tid) {
+  const int R = tid >> 1, half = tid & 1;
+  uint16_t* dst = ws + R * LDSW + 32 * half;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t w = wr.q[d];
+    u32x4_t o;
+    o[0] = dequant_pair(tab, w & 0xffu, wr.sc);
+    o[1] = dequant_pair(tab, (w >> 8) & 0xffu, wr.sc);
+    o[2] = dequant_pair(tab, (w >> 16) & 0xffu, wr.sc);
+    o[3] = dequant_pair(tab, w >> 24, wr.sc);
+    *reinterpret_cast<u32x4_t*>(dst + 8 * d) = o;
+  }
+}
+
+MOLT_DEV void wrow_generic(uint16_t* ws, const FwdParams& p, int64_t tn, bool pair, int64_t k0,
+                           const float* code16, int tid) {
+  for (int e = tid; e < BN * BK; e += NT) {
+    const int R = e / BK, j = e % BK;
+    int which; int64_t n;
+    fwd_row(R, tn, pair, which, n);
+    const int64_t k = k0 + j;
+    uint16_t v = 0;
+    if (n < p.N && k < p.K) {
+      const int64_t f = n * p.K + k;
+      const int nib = nf4_nibble(p.packed[which], f, p.order);
+      v = bf16_bits(code16[nib] * p.scales[which][f / p.block_size]);
+    }
+    ws[R * LDSW + j] = v;
+  }
+}
+
+// LoRA step (forward): W-side row R holds bf16(s * B[n, j - off]) for its window.
+MOLT_DEV void wrow_lora(uint16_t* ws, const FwdParams& p, int64_t tn, bool pair, int64_t k0, int tid) {
+  for (int e = tid; e < BN * BK; e += NT) {
+    const int R = e / BK, j = e % BK;
+    int which; int64_t n;
+    fwd_row(R, tn, pair, which, n);
+    const int64_t c = k0 + j - (int64_t)which * p.r;  // column inside this weight's adapter
+    uint16_t v = 0;
+    if (n < p.N && c >= 0 && c < p.r) v = bf16_bits(p.s[which] * p.lb[which][n * p.ldlb + c]);
+    ws[R * LDSW + j] = v;
+  }
+}
+
+// --------------------------------------------- backward W-side (column-contract)
+// Thread patch: 8 contraction rows x 4 output columns.
+constexpr int CG = BN / 4;  // 32 column groups
+static_assert(CG * 8 == NT, "backward patch layout needs BN/4 * 8 == threads");
+
+struct WColReg { uint32_t q[8]; float sc[8]; };
+
+MOLT_DEV void wcol_issue(WColReg& wr, const BwdParams& p, int seg, int64_t tn, int64_t c0, int tid) {
+  const int cg = tid % CG, rg = tid / CG;
+  const int64_t col = tn * BN + 4 * cg;
+  const bool ok = col < p.Kw;
+  const uint8_t* packed = p.packed[seg];
+  const float* scales = p.scales[seg];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int64_t c = c0 + 8 * rg + r;
+    uint32_t q = 0;
+    float sc = 0.0f;
+    if (ok) {
+      const int64_t flat = c * p.Kw + col;
+      q = *reinterpret_cast<const uint16_t*>(packed + (flat >> 1));
+      sc = scales[flat >> 6];
+    }
+    wr.q[r] = q;
+    wr.sc[r] = sc;
+  }
+}
+
+MOLT_DEV void wcol_commit(const WColReg& wr, uint16_t* ws, const float2* tab, int tid) {
+  const int cg = tid % CG, rg = tid / CG;
+  float v[8][4];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const float2 p0 = tab[wr.q[r] & 0xffu];
+    const float2 p1 = tab[(wr.q[r] >> 8) & 0xffu];
+    v[r][0] = p0.x * wr.sc[r];
+    v[r][1] = p0.y * wr.sc[r];
+    v[r][2] = p1.x * wr.sc[r];
+    v[r][3] = p1.y * wr.sc[r];
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    u32x4_t o;
+    o[0] = pack_bf16x2(v[0][j], v[1][j]);
+    o[1] = pack_bf16x2(v[2][j], v[3][j]);
+    o[2] = pack_bf16x2(v[4][j], v[5][j]);
+    o[3] = pack_bf16x2(v[6][j], v[7][j]);
+    *reinterpret_cast<u32x4_t*>(ws + (4 * cg + j) * LDSW + 8 * rg) = o;
+  }
+}
+
+MOLT_DEV void wcol_generic(uint16_t* ws, const BwdParams& p, int seg, int64_t tn, int64_t c0,
+                           const float* code16, int tid) {
+  for (int e = tid; e < BN * BK; e += NT) {
+    const int R = e % BN, j = e / BN;   // consecutive threads walk the contiguous output dim
+    const int64_t col = tn * BN + R, c = c0 + j;
+    uint16_t v = 0;
+    if (col < p.Kw && c < p.Nw) {
+      const int64_t f = c * p.Kw + col;
+      const int nib = nf4_nibble(p.packed[seg], f, p.order);
+      v = bf16_bits(code16[nib] * p.scales[seg][f / p.block_size]);
+    }
+    ws[R * LDSW + j] = v;
+  }
+}
+
+MOLT_DEV void wcol_lora(uint16_t* ws, const BwdParams& p, int seg, int64_t tn, int64_t c0, int tid) {
+  const float* a = p.la[seg];
+  for (int e = tid; e < BN * BK; e += NT) {
+    const int R = e % BN, j = e / BN;
+    const int64_t col = tn * BN + R, c = c0 + j;
+    uint16_t v = 0;
+    if (col < p.Kw && c < p.r) v = bf16_bits(p.la_scale * a[c * p.ldla + col]);
+    ws[R * LDSW + j] = v;
+  }
+}
+
+// --------------------------------------------------------------- epilogues
+MOLT_DEV void store4(uint16_t* __restrict__ out, int64_t ld, int64_t m, int64_t n, int64_t N,
+                     const float* v, bool vec) {
+  uint16_t* dst = out + m * ld + n;
+  if (vec && n + 3 < N) {
+    u32x2_t o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    *reinterpret_cast<u32x2_t*>(dst) = o;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (n + e < N) dst[e] = bf16_bits(v[e]);
+  }
+}
+
+MOLT_DEV void load4(const uint16_t* __restrict__ src, int64_t ld, int64_t m, int64_t n, int64_t N,
+                    float* v, bool vec) {
+  const uint16_t* s = src + m * ld + n;
+  if (vec && n + 3 < N) {
+    const u32x2_t w = *reinterpret_cast<const u32x2_t*>(s);
+    v[0] = bf16_lo(w[0]); v[1] = bf16_hi(w[0]); v[2] = bf16_lo(w[1]); v[3] = bf16_hi(w[1]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = (n + e < N) ? bf16_to_f32(s[e]) : 0.0f;
+  }
+}
+
+// ------------------------------------------------------------------ kernels
+template <bool PAIR, bool ALIGNED>
+__global__ __launch_bounds__(NT) void nf4_fwd_kernel(const FwdParams p) {
+  __shared__ Smem sm;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+
+  const int64_t cols_per_tile = PAIR ? BN / 2 : BN;
+  const int64_t nt_m = ceil_div64(p.M, BM), nt_n = ceil_div64(p.N, cols_per_tile);
+  int64_t tm, tn;
+  grouped_tile(xcd_tile(blockIdx.x, nt_m * nt_n), nt_m, nt_n, GROUP_M, tm, tn);
+  const int64_t m0 = tm * BM;
+
+  build_pair_table(sm.tab, p.code, p.order);
+  if (tid < 16) sm.code16[tid] = p.code[tid];
+
+  const int ks = (int)ceil_div64(p.K, BK);
+  const int ls = p.lr > 0 ? (int)ceil_div64(p.lr, BK) : 0;
+  const int total = ks + ls;
+
+  f32x16_t acc[TM][TN];
+  zero_acc(acc);
+  AReg ar;
+  WRowReg wr;
+
+  auto issue = [&](int s) {
+    if (ALIGNED && s < ks) {
+      a_issue(ar, p.x, p.ldx, m0, p.M, (int64_t)s * BK, tid);
+      wrow_issue(wr, p, tn, PAIR, (int64_t)s * BK, tid);
+    }
+  };
+  auto commit = [&](int s, int buf) {
+    uint16_t* xs = sm.xs[buf];
+    uint16_t* ws = sm.ws[buf];
+    if (s < ks) {
+      if (ALIGNED) {
+        a_commit(ar, xs, tid);
+        wrow_commit(wr, ws, sm.tab, tid);
+      } else {
+        a_generic(xs, p.x, p.ldx, m0, p.M, (int64_t)s * BK, p.K, tid);
+        wrow_generic(ws, p, tn, PAIR, (int64_t)s * BK, sm.code16, tid);
+      }
+    } else {
+      const int64_t c0 = (int64_t)(s - ks) * BK;
+      a_generic(xs, p.t, p.ldt, m0, p.M, c0, p.lr, tid);
+      wrow_lora(ws, p, tn, PAIR, c0, tid);
+    }
+  };
+
+  __syncthreads();  // pair table ready
+  issue(0);
+  commit(0, 0);
+  __syncthreads();
+  for (int s = 0; s < total; ++s) {
+    const int cur = s & 1;
+    if (s + 1 < total) issue(s + 1);
+    mfma_step<TM, TN>(sm.ws[cur], sm.xs[cur], wn * WROWS, wm * WCOLS, acc, lane);
+    if (s + 1 < total) commit(s + 1, cur ^ 1);
+    __syncthreads();
+  }
+
+  const bool vec = p.vec_out != 0;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t m = m0 + wm * WCOLS + j * 32 + (lane & 31);
+    if (m >= p.M) continue;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      if (!PAIR) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int64_t n = tn * BN + wn * WROWS + i * 32 + 8 * g + 4 * (lane >> 5);
+          float v[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+          store4(p.y[0], p.ldy, m, n, p.N, v, vec);
+        }
+      } else {
+        const int64_t n = tn * (BN / 2) + wn * 32 + 8 * g + 4 * (lane >> 5);
+        float gv[4], uv[4], hv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          gv[e] = round_bf16(acc[0][j][4 * g + e]);
+          uv[e] = round_bf16(acc[1][j][4 * g + e]);
+          hv[e] = round_bf16(silu_f32(gv[e])) * uv[e];
+        }
+        store4(p.y[0], p.ldy, m, n, p.N, gv, vec);
+        store4(p.y[1], p.ldy, m, n, p.N, uv, vec);
+        store4(p.y[2], p.ldy, m, n, p.N, hv, vec);
+      }
+    }
+  }
+}
+
+template <int EPI, bool ALIGNED>
+__global__ __launch_bounds__(NT) void nf4_bwd_kernel(const BwdParams p) {
+  __shared__ Smem sm;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+
+  const int64_t nt_m = ceil_div64(p.M, BM), nt_n = ceil_div64(p.Kw, BN);
+  int64_t tm, tn;
+  grouped_tile(xcd_tile(blockIdx.x, nt_m * nt_n), nt_m, nt_n, GROUP_M, tm, tn);
+  const int64_t m0 = tm * BM;
+
+  build_pair_table(sm.tab, p.code, p.order);
+  if (tid < 16) sm.code16[tid] = p.code[tid];
+
+  const int ks = (int)ceil_div64(p.Nw, BK);        // steps per NF4 segment
+  const int lsteps = p.r > 0 ? (int)ceil_div64(p.r, BK) : 0;
+  const int total = p.nseg * ks + p.nseg * lsteps;
+
+  f32x16_t acc[TM][TN];
+  zero_acc(acc);
+  AReg ar;
+  WColReg wr;
+
+  auto issue = [&](int s) {
+    if (ALIGNED && s < p.nseg * ks) {
+      const int seg = s / ks;
+      const int64_t c0 = (int64_t)(s % ks) * BK;
+      a_issue(ar, p.dy[seg], p.lddy, m0, p.M, c0, tid);
+      wcol_issue(wr, p, seg, tn, c0, tid);
+    }
+  };
+  auto commit = [&](int s, int buf) {
+    uint16_t* xs = sm.xs[buf];
+    uint16_t* ws = sm.ws[buf];
+    if (s < p.nseg * ks) {
+      const int seg = s / ks;
+      const int64_t c0 = (int64_t)(s % ks) * BK;
+      if (ALIGNED) {
+        a_commit(ar, xs, tid);
+        wcol_commit(wr, ws, sm.tab, tid);
+      } else {
+        a_generic(xs, p.dy[seg], p.lddy, m0, p.M, c0, p.Nw, tid);
+        wcol_generic(ws, p, seg, tn, c0, sm.code16, tid);
+      }
+    } else {
+      const int ls = s - p.nseg * ks;
+      const int seg = ls / lsteps;
+      const int64_t c0 = (int64_t)(ls % lsteps) * BK;
+      a_generic(xs, p.u[seg], p.ldu, m0, p.M, c0, p.r, tid);
+      wcol_lora(ws, p, seg, tn, c0, tid);
+    }
+  };
+
+  __syncthreads();
+  issue(0);
+  commit(0, 0);
+  __syncthreads();
+  for (int s = 0; s < total; ++s) {
+    const int cur = s & 1;
+    if (s + 1 < total) issue(s + 1);
+    mfma_step<TM, TN>(sm.ws[cur], sm.xs[cur], wn * WROWS, wm * WCOLS, acc, lane);
+    if (s + 1 < total) commit(s + 1, cur ^ 1);
+    __syncthreads();
+  }
+
+  const bool vec = p.vec_out != 0;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t m = m0 + wm * WCOLS + j * 32 + (lane & 31);
+    if (m >= p.M) continue;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t n = tn * BN + wn * WROWS + i * 32 + 8 * g + 4 * (lane >> 5);
+        float v[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        if (EPI == EPI_STORE) {
+          store4(p.dx, p.lddx, m, n, p.Kw, v, vec);
+        } else {
+          float gv[4], uv[4], dgv[4], duv[4];
+          load4(p.gate, p.ldg, m, n, p.Kw, gv, vec);
+          load4(p.up, p.ldg, m, n, p.Kw, uv, vec);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float dh = round_bf16(v[e]);
+            const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-gv[e]));
+            duv[e] = dh * round_bf16(gv[e] * sg);
+            dgv[e] = round_bf16(dh * uv[e]) * (sg * (1.0f + gv[e] * (1.0f - sg)));
+          }
+          store4(p.dg, p.ldg, m, n, p.Kw, dgv, vec);
+          store4(p.du, p.ldg, m, n, p.Kw, duv, vec);
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- host helpers
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int check_weight_for_gemm(const molt_nf4_weight* w, const char* who) {
+  MOLT_REQUIRE(w && w->packed && w->code, MOLT_EINVAL, "%s: weight, packed and code are required", who);
+  MOLT_REQUIRE(w->scales, MOLT_EINVAL, "%s: resolved fp32 scales are required (molt_nf4_resolve_scales)", who);
+  MOLT_REQUIRE(w->rows > 0 && w->cols > 0, MOLT_EINVAL, "%s: empty weight", who);
+  MOLT_REQUIRE(w->block_size >= 2 && w->block_size % 2 == 0, MOLT_EINVAL, "%s: bad block size %d", who, w->block_size);
+  MOLT_REQUIRE(w->nibble_order == 0 || w->nibble_order == 1, MOLT_EINVAL, "%s: bad nibble order", who);
+  return MOLT_OK;
+}
+
+bool same_format(const molt_nf4_weight* a, const molt_nf4_weight* b) {
+  return a->rows == b->rows && a->cols == b->cols && a->block_size == b->block_size &&
+         a->nibble_order == b->nibble_order && a->code == b->code;
+}
+
+}  // namespace
+}  // namespace molt
+
+using namespace molt;
+
+extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_t M,
+                                          const molt_nf4_weight* w0, const molt_nf4_weight* w1,
+                                          const uint16_t* t, int64_t ldt, int lr,
+                                          const float* b0, const float* b1, int64_t ldb, int r,
+                                          float s0, float s1, uint16_t* y0, uint16_t* y1,
+                                          uint16_t* y2, int64_t ldy, hipStream_t stream) {
+  const char* who = "molt_nf4_lora_forward";
+  int rc = check_weight_for_gemm(w0, who);
+  if (rc) return rc;
+  const bool pair = w1 != nullptr;
+  if (pair) {
+    rc = check_weight_for_gemm(w1, who);
+    if (rc) return rc;
+    MOLT_REQUIRE(same_format(w0, w1), MOLT_EINVAL, "%s: gate and up weights must share shape and format", who);
+  }
+  MOLT_REQUIRE(x && M >= 0 && ldx >= w0->cols, MOLT_EINVAL, "%s: bad X", who);
+  MOLT_REQUIRE(y0 && ldy >= w0->rows, MOLT_EINVAL, "%s: bad Y", who);
+  MOLT_REQUIRE(!pair || (y1 && y2), MOLT_EINVAL, "%s: pair needs g, u and h outputs", who);
+  MOLT_REQUIRE(lr == 0 || (t && ldt >= lr && b0 && (!pair || b1) && r > 0 && ldb >= r), MOLT_EINVAL,
+               "%s: bad LoRA operands", who);
+  if (M == 0) return MOLT_OK;
+
+  FwdParams p{};
+  p.x = x; p.ldx = ldx; p.M = M; p.K = w0->cols;
+  p.packed[0] = w0->packed; p.scales[0] = w0->scales;
+  p.packed[1] = pair ? w1->packed : w0->packed; p.scales[1] = pair ? w1->scales : w0->scales;
+  p.N = w0->rows; p.code = w0->code; p.order = w0->nibble_order; p.block_size = w0->block_size;
+  p.t = t; p.ldt = ldt; p.lr = lr;
+  p.lb[0] = b0; p.lb[1] = pair ? b1 : b0; p.ldlb = ldb; p.r = r; p.s[0] = s0; p.s[1] = s1;
+  p.y[0] = y0; p.y[1] = y1; p.y[2] = y2; p.ldy = ldy;
+  p.vec_out = (ldy % 4 == 0) && aligned(y0, 8) && (!pair || (aligned(y1, 8) && aligned(y2, 8)));
+
+  const bool al = (p.K % 64 == 0) && p.block_size == 64 && ldx % 8 == 0 && aligned(x, 16) &&
+                  aligned(w0->packed, 16) && (!pair || aligned(w1->packed, 16));
+  const int64_t cols_per_tile = pair ? BN / 2 : BN;
+  const int64_t tiles = ceil_div64(M, BM) * ceil_div64(p.N, cols_per_tile);
+  MOLT_REQUIRE(tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
+  dim3 grid((unsigned)tiles), block(NT);
+  if (pair) {
+    if (al) hipLaunchKernelGGL((nf4_fwd_kernel<true, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((nf4_fwd_kernel<true, false>), grid, block, 0, stream, p);
+  } else {
+    if (al) hipLaunchKernelGGL((nf4_fwd_kernel<false, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((nf4_fwd_kernel<false, false>), grid, block, 0, stream, p);
+  }
+  return check_launch(who);
+}
+
+extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* dy1, int64_t lddy,
+                                           int64_t M, const molt_nf4_weight* w0,
+                                           const molt_nf4_weight* w1, const uint16_t* u0,
+                                           const uint16_t* u1, int64_t ldu, const float* a0,
+                                           const float* a1, int64_t lda, int r, float lora_scale,
+                                           uint16_t* dx, int64_t lddx, const uint16_t* gate, const uint16_t* up,
+                                           uint16_t* dg, uint16_t* du, int64_t ldg,
+                                           hipStream_t stream) {
+  const char* who = "molt_nf4_lora_backward_input";
+  int rc = check_weight_for_gemm(w0, who);
+  if (rc) return rc;
+  const int nseg = w1 ? 2 : 1;
+  if (w1) {
+    rc = check_weight_for_gemm(w1, who);
+    if (rc) return rc;
+    MOLT_REQUIRE(same_format(w0, w1), MOLT_EINVAL, "%s: paired weights must share shape and format", who);
+    MOLT_REQUIRE(dy1, MOLT_EINVAL, "%s: second gradient missing", who);
+  }
+  const bool swiglu = dg != nullptr;
+  MOLT_REQUIRE(dy0 && M >= 0 && lddy >= w0->rows, MOLT_EINVAL, "%s: bad dY", who);
+  MOLT_REQUIRE(r == 0 || (u0 && ldu >= r && a0 && lda >= w0->cols && (nseg == 1 || (u1 && a1))),
+               MOLT_EINVAL, "%s: bad LoRA operands", who);
+  if (swiglu) {
+    MOLT_REQUIRE(gate && up && du && ldg >= w0->cols && nseg == 1, MOLT_EINVAL, "%s: bad SwiGLU operands", who);
+  } else {
+    MOLT_REQUIRE(dx && lddx >= w0->cols, MOLT_EINVAL, "%s: bad dX", who);
+  }
+  if (M == 0) return MOLT_OK;
+
+  BwdParams p{};
+  p.dy[0] = dy0; p.dy[1] = w1 ? dy1 : dy0; p.lddy = lddy; p.M = M;
+  p.packed[0] = w0->packed; p.scales[0] = w0->scales;
+  p.packed[1] = w1 ? w1->packed : w0->packed; p.scales[1] = w1 ? w1->scales : w0->scales;
+  p.Nw = w0->rows; p.Kw = w0->cols;
+  p.code = w0->code; p.order = w0->nibble_order; p.block_size = w0->block_size; p.nseg = nseg;
+  p.u[0] = u0; p.u[1] = w1 ? u1 : u0; p.ldu = ldu; p.r = r;
+  p.la[0] = a0; p.la[1] = w1 ? a1 : a0; p.ldla = lda; p.la_scale = lora_scale;
+  p.dx = dx; p.lddx = lddx;
+  p.gate = gate; p.up = up; p.dg = dg; p.du = du; p.ldg = ldg;
+  if (swiglu)
+    p.vec_out = ldg % 4 == 0 && aligned(gate, 8) && aligned(up, 8) && aligned(dg, 8) && aligned(du, 8);
+  else
+    p.vec_out = lddx % 4 == 0 && aligned(dx, 8);
+
+  const bool al = (p.Nw % 64 == 0) && (p.Kw % 64 == 0) && p.block_size == 64 && lddy % 8 == 0 &&
+                  aligned(dy0, 16) && (nseg == 1 || aligned(dy1, 16)) && aligned(w0->packed, 2) &&
+                  (nseg == 1 || aligned(w1->packed, 2));
+  const int64_t tiles = ceil_div64(M, BM) * ceil_div64(p.Kw, BN);
+  MOLT_REQUIRE(tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
+  dim3 grid((unsigned)tiles), block(NT);
+  if (swiglu) {
+    if (al) hipLaunchKernelGGL((nf4_bwd_kernel<EPI_SWIGLU_BWD, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((nf4_bwd_kernel<EPI_SWIGLU_BWD, false>), grid, block, 0, stream, p);
+  } else {
+    if (al) hipLaunchKernelGGL((nf4_bwd_kernel<EPI_STORE, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((nf4_bwd_kernel<EPI_STORE, false>), grid, block, 0, stream, p);
+  }
+  return check_launch(who);
+}

@@ -1,0 +1,397 @@
+"""Gated NF4-LoRA MLP on MI355X: the drop-in for
+``molt_stream.methods.gated_replay`` (methods/gated_replay.py:211-607), plus a
+fully fused gate/up/down autograd node.
+
+``asymmetric_gated_nf4_lora`` keeps the reference contract (gate and up come
+from their own projection nodes; only the down projection and SwiGLU are
+inside this node; up can be rematerialised or offloaded to pinned host
+memory). Backward runs the down projection's input gradient and the SwiGLU
+backward as ONE NF4-fused GEMM whose epilogue writes ``dgate`` and ``dup``
+(``dh`` never reaches HBM), and the down adapter's ``dA = U^T h`` replays
+``h = bf16(bf16(silu(g)) u)`` in registers while staging ``g`` and ``u``.
+
+``fused_gated_nf4_lora_mlp`` takes all three projections (the shape of
+``_ResidualRecipeGatedNF4LoRA``, methods/gated_replay.py:50-208): gate and up
+are ONE dual-accumulator GEMM that also emits ``h``; only ``g`` and ``u`` are
+saved, and backward computes ``dX = dg deq(Wg) + du deq(Wu) + LoRA`` as one
+contraction over 2I.
+"""
+from __future__ import annotations
+
+from types import MethodType
+from typing import Any
+
+import torch
+
+from .. import ops
+from ..errors import CapabilityError
+from ..nf4 import _rows_cols, nibble_order, resolved_nf4_scales
+from .nf4_lora import nf4_lora_module_types
+
+
+def _nf4_lora_forward(x: torch.Tensor, packed_weight: torch.Tensor, lora_a: torch.Tensor,
+                      lora_b: torch.Tensor, quant_state: Any, scaling: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """(Y, T) for ``Y = X deq(W)^T + s (X A^T) B^T`` (methods/gated_replay.py:211-224)."""
+    n, k = _rows_cols(quant_state.shape)
+    flat = x.reshape(-1, k)
+    t = ops.lora_project(flat, None, 0, 1.0, lora_a, 0)
+    y = ops.nf4_lora_forward(flat, packed_weight.reshape(-1), resolved_nf4_scales(quant_state),
+                             quant_state.code, n, k, nibble_order(quant_state), int(quant_state.blocksize),
+                             t, lora_b, float(scaling))
+    return y.reshape(*x.shape[:-1], n), t
+
+
+class _AsymmetricGatedNF4LoRA(torch.autograd.Function):
+    """methods/gated_replay.py:256-407."""
+
+    @staticmethod
+    def forward(ctx: Any, x, gate, up, up_packed_weight, up_lora_a, up_lora_b, down_packed_weight,
+                down_lora_a, down_lora_b, up_quant_state, down_quant_state, up_scaling, down_scaling,
+                rematerialize_up, offload_up, host_up, offload_gate, host_gate):
+        if x.device.type != "cuda" or x.dtype != torch.bfloat16:
+            raise CapabilityError("asymmetric gated replay requires CUDA BF16 tensors")
+        ctx.up_quant_state = up_quant_state
+        ctx.down_quant_state = down_quant_state
+        ctx.up_scaling = float(up_scaling)
+        ctx.down_scaling = float(down_scaling)
+        ctx.rematerialize_up = bool(rematerialize_up)
+        ctx.offload_up = bool(offload_up)
+        ctx.offload_gate = bool(offload_gate)
+        if ctx.rematerialize_up and ctx.offload_up:
+            raise CapabilityError("up projection cannot be replayed and offloaded")
+        if ctx.offload_up:
+            if host_up.device.type != "cpu" or not host_up.is_pinned():
+                raise CapabilityError("gated activation offload requires pinned host storage")
+            if host_up.shape != up.shape or host_up.dtype != up.dtype:
+                raise CapabilityError("gated activation host storage must match the up result")
+        if ctx.offload_gate:
+            if host_gate.device.type != "cpu" or not host_gate.is_pinned():
+                raise CapabilityError("gated activation offload requires pinned gate storage")
+            if host_gate.shape != gate.shape or host_gate.dtype != gate.dtype:
+                raise CapabilityError("gated activation host storage must match the gate result")
+        gated = ops.silu_mul_forward(gate, up, True)
+        result, low_rank = _nf4_lora_forward(gated, down_packed_weight, down_lora_a, down_lora_b,
+                                             down_quant_state, down_scaling)
+        del gated
+        if ctx.offload_up:
+            host_up.copy_(up.detach(), non_blocking=True)
+        if ctx.offload_gate:
+            host_gate.copy_(gate.detach(), non_blocking=True)
+        saved = (x, host_gate if ctx.offload_gate else gate, up_packed_weight, up_lora_a, up_lora_b,
+                 down_packed_weight, down_lora_a, down_lora_b, low_rank)
+        if ctx.offload_up:
+            saved += (host_up,)
+        elif not ctx.rematerialize_up:
+            saved += (up,)
+        ctx.save_for_backward(*saved)
+        return result
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx: Any, grad_output: torch.Tensor):
+        (x, stored_gate, up_packed_weight, up_lora_a, up_lora_b, down_packed_weight, down_lora_a,
+         down_lora_b, low_rank, *retained) = ctx.saved_tensors
+        gate = stored_gate.to(grad_output.device, non_blocking=True) if ctx.offload_gate else stored_gate
+        if ctx.rematerialize_up:
+            up, _ = _nf4_lora_forward(x, up_packed_weight, up_lora_a, up_lora_b, ctx.up_quant_state,
+                                      ctx.up_scaling)
+        elif ctx.offload_up:
+            up = retained[0].to(grad_output.device, non_blocking=True)
+        else:
+            up = retained[0]
+        qs = ctx.down_quant_state
+        h_dim, i_dim = _rows_cols(qs.shape)
+        dy = grad_output.reshape(-1, h_dim).to(torch.bfloat16)
+        g2, u2 = gate.reshape(-1, i_dim), up.reshape(-1, i_dim)
+        grad_through_b = ops.lora_project(dy, None, 2, ctx.down_scaling, down_lora_b, 1)
+        grad_gate, grad_up = ops.nf4_swiglu_backward(dy, down_packed_weight.reshape(-1), resolved_nf4_scales(qs),
+                                                     qs.code, h_dim, i_dim, nibble_order(qs), grad_through_b,
+                                                     down_lora_a, g2, u2)
+        grad_down_a = ops.lora_grad(g2, u2, 1, grad_through_b, 1.0, 1)
+        grad_down_b = ops.lora_grad(dy, None, 0, low_rank, ctx.down_scaling, 0)
+        return (None, grad_gate.reshape(gate.shape), grad_up.reshape(up.shape), None, None, None, None,
+                grad_down_a.to(down_lora_a.dtype), grad_down_b.to(down_lora_b.dtype),
+                None, None, None, None, None, None, None, None, None)
+
+
+def asymmetric_gated_nf4_lora(
+    x: torch.Tensor,
+    gate: torch.Tensor,
+    up: torch.Tensor,
+    up_packed_weight: torch.Tensor,
+    up_lora_a: torch.Tensor,
+    up_lora_b: torch.Tensor,
+    down_packed_weight: torch.Tensor,
+    down_lora_a: torch.Tensor,
+    down_lora_b: torch.Tensor,
+    up_quant_state: Any,
+    down_quant_state: Any,
+    up_scaling: float,
+    down_scaling: float,
+    rematerialize_up: bool = True,
+    offload_up: bool = False,
+    host_up: torch.Tensor | None = None,
+    offload_gate: bool = False,
+    host_gate: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """methods/gated_replay.py:410-457."""
+    if offload_up and host_up is None:
+        raise CapabilityError("gated activation offload requires a host buffer")
+    if host_up is None:
+        host_up = torch.empty(0)
+    if offload_gate and host_gate is None:
+        raise CapabilityError("gated activation offload requires a gate host buffer")
+    if host_gate is None:
+        host_gate = torch.empty(0)
+    return _AsymmetricGatedNF4LoRA.apply(
+        x, gate, up, up_packed_weight, up_lora_a, up_lora_b, down_packed_weight, down_lora_a,
+        down_lora_b, up_quant_state, down_quant_state, up_scaling, down_scaling, rematerialize_up,
+        offload_up, host_up, offload_gate, host_gate,
+    )
+
+
+# --------------------------------------------------------------------------
+# Fully fused gate/up/down node
+# --------------------------------------------------------------------------
+class _FusedGatedNF4LoRA(torch.autograd.Function):
+    """Gated NF4-LoRA MLP with gate/up as one dual-accumulator GEMM and the
+    SwiGLU backward fused into the down projection's input gradient."""
+
+    @staticmethod
+    def forward(ctx: Any, x, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_packed, down_a,
+                down_b, gate_qs, up_qs, down_qs, gate_scaling, up_scaling, down_scaling):
+        if x.device.type != "cuda" or x.dtype != torch.bfloat16:
+            raise CapabilityError("fused gated NF4-LoRA MLP requires CUDA BF16 tensors")
+        for t in (gate_a, gate_b, up_a, up_b, down_a, down_b):
+            if t.dtype != torch.float32:
+                raise CapabilityError("fused gated NF4-LoRA MLP requires FP32 adapter masters")
+        i_dim, h_dim = _rows_cols(gate_qs.shape)
+        if _rows_cols(up_qs.shape) != (i_dim, h_dim) or _rows_cols(down_qs.shape) != (h_dim, i_dim):
+            raise ValueError("gate/up must be [I, H] and down [H, I]")
+        if nibble_order(gate_qs) != nibble_order(up_qs) or int(gate_qs.blocksize) != 64 \
+                or int(up_qs.blocksize) != 64 or int(down_qs.blocksize) != 64:
+            raise CapabilityError("fused gated MLP requires NF4 block size 64 with a shared packing")
+        r = gate_a.shape[0]
+        if up_a.shape[0] != r:
+            raise ValueError("gate and up adapters must share a rank")
+        flat = x.reshape(-1, h_dim)
+        t_gu = ops.lora_project(flat, None, 0, 1.0, torch.cat([gate_a, up_a], 0), 0)
+        code = gate_qs.code
+        gate, up, gated = ops.nf4_gateup_forward(
+            flat, gate_packed.reshape(-1), resolved_nf4_scales(gate_qs), up_packed.reshape(-1),
+            resolved_nf4_scales(up_qs), code, i_dim, h_dim, nibble_order(gate_qs), t_gu, gate_b, up_b,
+            float(gate_scaling), float(up_scaling))
+        t_d = ops.lora_project(gated, None, 0, 1.0, down_a, 0)
+        y = ops.nf4_lora_forward(gated, down_packed.reshape(-1), resolved_nf4_scales(down_qs), down_qs.code,
+                                 h_dim, i_dim, nibble_order(down_qs), 64, t_d, down_b, float(down_scaling))
+        del gated  # replayed in backward from (gate, up)
+        ctx.qs = (gate_qs, up_qs, down_qs)
+        ctx.scaling = (float(gate_scaling), float(up_scaling), float(down_scaling))
+        ctx.dims = (h_dim, i_dim, r)
+        ctx.input_shape = x.shape
+        ctx.save_for_backward(flat, gate, up, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed, up_a, up_b,
+                              down_packed, down_a, down_b)
+        return y.reshape(*x.shape[:-1], h_dim)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx: Any, grad_output: torch.Tensor):
+        (flat, gate, up, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_packed, down_a,
+         down_b) = ctx.saved_tensors
+        gate_qs, up_qs, down_qs = ctx.qs
+        s_g, s_u, s_d = ctx.scaling
+        h_dim, i_dim, r = ctx.dims
+        dy = grad_output.reshape(-1, h_dim).to(torch.bfloat16)
+        u_d = ops.lora_project(dy, None, 2, s_d, down_b, 1)
+        dg, du = ops.nf4_swiglu_backward(dy, down_packed.reshape(-1), resolved_nf4_scales(down_qs), down_qs.code,
+                                         h_dim, i_dim, nibble_order(down_qs), u_d, down_a, gate, up)
+        u_g = ops.lora_project(dg, None, 2, s_g, gate_b, 1)
+        u_u = ops.lora_project(du, None, 2, s_u, up_b, 1)
+        dx = ops.nf4_lora_backward_input_pair(
+            dg, du, gate_packed.reshape(-1), resolved_nf4_scales(gate_qs), up_packed.reshape(-1),
+            resolved_nf4_scales(up_qs), gate_qs.code, i_dim, h_dim, nibble_order(gate_qs), u_g, u_u, gate_a,
+            up_a)
+        d_down_a = ops.lora_grad(gate, up, 1, u_d, 1.0, 1)
+        d_down_b = ops.lora_grad(dy, None, 0, t_d, s_d, 0)
+        d_gate_a = ops.lora_grad(flat, None, 0, u_g, 1.0, 1)
+        d_gate_b = ops.lora_grad(dg, None, 0, t_gu[:, :r], s_g, 0)
+        d_up_a = ops.lora_grad(flat, None, 0, u_u, 1.0, 1)
+        d_up_b = ops.lora_grad(du, None, 0, t_gu[:, r:], s_u, 0)
+        return (dx.reshape(ctx.input_shape), None, d_gate_a, d_gate_b, None, d_up_a, d_up_b, None, d_down_a,
+                d_down_b, None, None, None, None, None, None)
+
+
+def fused_gated_nf4_lora_mlp(
+    x: torch.Tensor,
+    gate_packed_weight: torch.Tensor, gate_lora_a: torch.Tensor, gate_lora_b: torch.Tensor,
+    up_packed_weight: torch.Tensor, up_lora_a: torch.Tensor, up_lora_b: torch.Tensor,
+    down_packed_weight: torch.Tensor, down_lora_a: torch.Tensor, down_lora_b: torch.Tensor,
+    gate_quant_state: Any, up_quant_state: Any, down_quant_state: Any,
+    gate_scaling: float, up_scaling: float, down_scaling: float,
+) -> torch.Tensor:
+    """``down(silu(gate(x)) * up(x))`` with NF4-LoRA projections as one autograd node."""
+    return _FusedGatedNF4LoRA.apply(
+        x, gate_packed_weight, gate_lora_a, gate_lora_b, up_packed_weight, up_lora_a, up_lora_b,
+        down_packed_weight, down_lora_a, down_lora_b, gate_quant_state, up_quant_state, down_quant_state,
+        gate_scaling, up_scaling, down_scaling)
+
+
+# --------------------------------------------------------------------------
+# Patchers (methods/gated_replay.py:460-607)
+# --------------------------------------------------------------------------
+def _adapter_parts(module: torch.nn.Module) -> tuple[Any, ...] | None:
+    active = list(module.active_adapters)
+    if len(active) != 1:
+        return None
+    adapter = active[0]
+    if (
+        adapter not in module.lora_A
+        or adapter in module.lora_variant
+        or module.use_dora.get(adapter, False)
+        or not isinstance(module.lora_dropout[adapter], torch.nn.Identity)
+        or module.base_layer.bias is not None
+    ):
+        return None
+    return (
+        module.base_layer.weight,
+        module.lora_A[adapter].weight,
+        module.lora_B[adapter].weight,
+        module.base_layer.weight.quant_state,
+        float(module.scaling[adapter]),
+    )
+
+
+def _asymmetric_mlp_forward(module: torch.nn.Module, x: torch.Tensor, *args: Any, **kwargs: Any) -> torch.Tensor:
+    if (
+        args
+        or kwargs
+        or not torch.is_grad_enabled()
+        or x.dtype != torch.bfloat16
+        or not torch.is_autocast_enabled("cuda")
+        or torch.get_autocast_dtype("cuda") != torch.bfloat16
+    ):
+        return module._molt_original_forward(x, *args, **kwargs)
+    up_parts = _adapter_parts(module.up_proj)
+    down_parts = _adapter_parts(module.down_proj)
+    if up_parts is None or down_parts is None:
+        return module._molt_original_forward(x, *args, **kwargs)
+    gate = module.gate_proj(x)
+    up = module.up_proj(x)
+    if module._molt_offload_up:
+        host_up = getattr(module, "_molt_host_up", None)
+        if host_up is None or host_up.shape != up.shape or host_up.dtype != up.dtype:
+            if torch.cuda.is_current_stream_capturing():
+                raise CapabilityError("gated activation host storage was not warmed up")
+            host_up = torch.empty_like(up, device="cpu", pin_memory=True)
+            module._molt_host_up = host_up
+    else:
+        host_up = None
+    if module._molt_offload_gate:
+        host_gate = getattr(module, "_molt_host_gate", None)
+        if host_gate is None or host_gate.shape != gate.shape or host_gate.dtype != gate.dtype:
+            if torch.cuda.is_current_stream_capturing():
+                raise CapabilityError("gated activation gate storage was not warmed up")
+            host_gate = torch.empty_like(gate, device="cpu", pin_memory=True)
+            module._molt_host_gate = host_gate
+    else:
+        host_gate = None
+    return asymmetric_gated_nf4_lora(
+        x, gate, up, up_parts[0], up_parts[1], up_parts[2], down_parts[0], down_parts[1], down_parts[2],
+        up_parts[3], down_parts[3], up_parts[4], down_parts[4], module._molt_rematerialize_up,
+        module._molt_offload_up, host_up, module._molt_offload_gate, host_gate,
+    )
+
+
+def _compatible_mlps(model: torch.nn.Module) -> list[torch.nn.Module]:
+    types = nf4_lora_module_types()
+    found = []
+    for module in model.modules():
+        if hasattr(module, "_molt_original_forward"):
+            continue
+        if not all(hasattr(module, name) for name in ("gate_proj", "up_proj", "down_proj", "act_fn")):
+            continue
+        if not all(isinstance(getattr(module, name), types) for name in ("gate_proj", "up_proj", "down_proj")):
+            continue
+        if type(module.act_fn).__name__ not in {"SiLU", "SiLUActivation"}:
+            continue
+        if _adapter_parts(module.up_proj) is None or _adapter_parts(module.down_proj) is None:
+            continue
+        found.append(module)
+    return found
+
+
+def enable_asymmetric_gated_replay(
+    model: torch.nn.Module,
+    *,
+    rematerialize_up: bool = True,
+    rematerialize_blocks: int | None = None,
+    offload_blocks: int = 0,
+    offload_gate_blocks: int = 0,
+) -> int:
+    """Patch structurally compatible SiLU-gated NF4-LoRA MLP blocks
+    (methods/gated_replay.py:540-607)."""
+    if rematerialize_blocks is not None and rematerialize_blocks < 0:
+        raise ValueError("rematerialize_blocks cannot be negative")
+    if offload_blocks < 0:
+        raise ValueError("offload_blocks cannot be negative")
+    if offload_gate_blocks < 0:
+        raise ValueError("offload_gate_blocks cannot be negative")
+    if rematerialize_up and (offload_blocks or offload_gate_blocks):
+        raise ValueError("up projection replay and offload are mutually exclusive")
+    compatible = _compatible_mlps(model)
+    if not compatible:
+        raise CapabilityError("No compatible SiLU-gated PEFT NF4 MLP blocks were found")
+    if rematerialize_blocks is not None and rematerialize_blocks > len(compatible):
+        raise CapabilityError(
+            f"requested {rematerialize_blocks} replay blocks but only "
+            f"{len(compatible)} compatible blocks were found"
+        )
+    if offload_blocks > len(compatible):
+        raise CapabilityError(
+            f"requested {offload_blocks} offload blocks but only "
+            f"{len(compatible)} compatible blocks were found"
+        )
+    if offload_gate_blocks > len(compatible):
+        raise CapabilityError(
+            f"requested {offload_gate_blocks} gate offload blocks but only "
+            f"{len(compatible)} compatible blocks were found"
+        )
+    selected = len(compatible) if rematerialize_blocks is None else rematerialize_blocks
+    patched = 0
+    for index, module in enumerate(compatible):
+        module._molt_original_forward = module.forward
+        module._molt_rematerialize_up = bool(rematerialize_up and index < selected)
+        module._molt_offload_up = bool(index < offload_blocks)
+        module._molt_offload_gate = bool(index < offload_gate_blocks)
+        module.forward = MethodType(_asymmetric_mlp_forward, module)
+        patched += 1
+    return patched
+
+
+def _fused_mlp_forward(module: torch.nn.Module, x: torch.Tensor, *args: Any, **kwargs: Any) -> torch.Tensor:
+    if (
+        args
+        or kwargs
+        or x.dtype != torch.bfloat16
+        or not torch.is_autocast_enabled("cuda")
+        or torch.get_autocast_dtype("cuda") != torch.bfloat16
+    ):
+        return module._molt_original_forward(x, *args, **kwargs)
+    parts = [_adapter_parts(getattr(module, n)) for n in ("gate_proj", "up_proj", "down_proj")]
+    if any(p is None for p in parts):
+        return module._molt_original_forward(x, *args, **kwargs)
+    g, u, d = parts
+    return fused_gated_nf4_lora_mlp(x, g[0], g[1], g[2], u[0], u[1], u[2], d[0], d[1], d[2], g[3], u[3], d[3],
+                                    g[4], u[4], d[4])
+
+
+def enable_fused_gated_nf4_lora(model: torch.nn.Module) -> int:
+    """Route every compatible SiLU-gated NF4-LoRA MLP through
+    :func:`fused_gated_nf4_lora_mlp` (gate and up adapters must be active)."""
+    compatible = [m for m in _compatible_mlps(model) if _adapter_parts(m.gate_proj) is not None]
+    if not compatible:
+        raise CapabilityError("No compatible SiLU-gated PEFT NF4 MLP blocks were found")
+    for module in compatible:
+        module._molt_original_forward = module.forward
+        module.forward = MethodType(_fused_mlp_forward, module)
+    return len(compatible)

@@ -1,0 +1,549 @@
+"""torch.library custom ops over the C ABI of libmolt_amd.so.
+
+Each op checks devices, dtypes and shapes, allocates its outputs (and any
+workspace) with the PyTorch caching allocator and launches on the current
+stream of the input's device. Fake (meta) implementations are registered so
+the ops trace under torch.compile and pass ``torch.library.opcheck``. The
+registration pattern follows the reference's own custom op
+(kernels/frozen_linear_cross_entropy.py:335-392).
+
+There is no CPU path: a CPU tensor raises CapabilityError.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from .errors import CapabilityError
+
+NS = "molt_amd"
+
+
+def _require_gpu(*tensors: Optional[Tensor], what: str) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise CapabilityError(f"{what} requires CUDA tensors on a ROCm GPU (got {t.device})")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"{what}: tensors on different devices ({dev} vs {t.device})")
+    if dev is None:
+        raise ValueError(f"{what}: no tensor arguments")
+    return dev
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _ptr(t: Optional[Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _bf16(t: Tensor, name: str, what: str) -> Tensor:
+    if t.dtype != torch.bfloat16:
+        raise CapabilityError(f"{what} requires BF16 {name} (got {t.dtype})")
+    return t.contiguous()
+
+
+def _f32(t: Tensor) -> Tensor:
+    return t.detach().to(torch.float32).contiguous()
+
+
+def _weight(packed: Tensor, scales: Optional[Tensor], code: Tensor, rows: int, cols: int,
+            block_size: int, order: int, absmax_q: Optional[Tensor] = None,
+            absmax2: Optional[Tensor] = None, code2: Optional[Tensor] = None,
+            offset: float = 0.0, dq_block: int = 256) -> _lib.NF4Weight:
+    w = _lib.NF4Weight()
+    w.packed = packed.data_ptr()
+    w.scales = _ptr(scales)
+    w.absmax_q = _ptr(absmax_q)
+    w.absmax2 = _ptr(absmax2)
+    w.code2 = _ptr(code2)
+    w.code = code.data_ptr()
+    w.offset = float(offset)
+    w.nested = int(absmax_q is not None)
+    w.block_size = int(block_size)
+    w.dq_block = int(dq_block)
+    w.nibble_order = int(order)
+    w.rows = int(rows)
+    w.cols = int(cols)
+    # keep every tensor whose address the descriptor holds alive until the launch
+    w.keepalive = (packed, scales, code, absmax_q, absmax2, code2)
+    return w
+
+
+def _check_packed(packed: Tensor, rows: int, cols: int, what: str) -> Tensor:
+    if packed.dtype != torch.uint8:
+        raise CapabilityError(f"{what} requires uint8 packed NF4 weights")
+    if packed.numel() * 2 < rows * cols:
+        raise ValueError(f"{what}: packed weight holds {packed.numel()} bytes, "
+                         f"{(rows * cols + 1) // 2} needed for {rows}x{cols}")
+    return packed.contiguous()
+
+
+# Optional per-launch event probe: name -> list of (start, end) torch.cuda.Event
+# pairs recorded on the launch stream around each call of that entry point.
+_probes: dict[str, list] = {}
+
+
+def probe_events(name: str, enable: bool = True) -> list:
+    """Start (or stop) recording HIP events around every launch of the C entry
+    point ``name``; returns the list that collects (start, end) pairs."""
+    if enable:
+        return _probes.setdefault(name, [])
+    return _probes.pop(name, [])
+
+
+def _call(fn_name: str, *args) -> None:
+    lib = _lib.load()
+    pairs = _probes.get(fn_name)
+    if pairs is None:
+        _lib.check(getattr(lib, fn_name)(*args))
+        return
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    _lib.check(getattr(lib, fn_name)(*args))
+    end.record()
+    pairs.append((start, end))
+
+
+# ----------------------------------------------------------------- codec
+@torch.library.custom_op(f"{NS}::nf4_dequantize", mutates_args=())
+def nf4_dequantize(packed: Tensor, scales: Tensor, code: Tensor, rows: int, cols: int,
+                   block_size: int, order: int, out_dtype: torch.dtype) -> Tensor:
+    """bf16/fp32 decode with resolved fp32 scales (streaming/nf4.py:29-35)."""
+    what = "NF4 dequantize"
+    dev = _require_gpu(packed, scales, code, what=what)
+    packed = _check_packed(packed, rows, cols, what)
+    out = torch.empty((rows, cols), device=dev, dtype=out_dtype)
+    w = _weight(packed, _f32(scales), _f32(code), rows, cols, block_size, order)
+    dt = _lib.DTYPE_F32 if out_dtype == torch.float32 else _lib.DTYPE_BF16
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise CapabilityError(f"{what}: output dtype {out_dtype} unsupported (bf16, fp32)")
+    _call("molt_nf4_dequantize", C.byref(w), out.data_ptr(), dt, _stream(dev))
+    return out
+
+
+@nf4_dequantize.register_fake
+def _(packed, scales, code, rows, cols, block_size, order, out_dtype):
+    return packed.new_empty((rows, cols), dtype=out_dtype)
+
+
+@torch.library.custom_op(f"{NS}::nf4_dequantize_nested", mutates_args=())
+def nf4_dequantize_nested(packed: Tensor, absmax_q: Tensor, absmax2: Tensor, code2: Tensor,
+                          code: Tensor, offset: float, rows: int, cols: int, block_size: int,
+                          dq_block: int, order: int, out_dtype: torch.dtype) -> Tensor:
+    """bitsandbytes.functional.dequantize_4bit with nested absmax
+    (methods/nf4_lora.py:97-98)."""
+    what = "NF4 dequantize"
+    dev = _require_gpu(packed, absmax_q, absmax2, code2, code, what=what)
+    packed = _check_packed(packed, rows, cols, what)
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise CapabilityError(f"{what}: output dtype {out_dtype} unsupported (bf16, fp32)")
+    out = torch.empty((rows, cols), device=dev, dtype=out_dtype)
+    w = _weight(packed, None, _f32(code), rows, cols, block_size, order, absmax_q.contiguous(),
+                _f32(absmax2), _f32(code2), offset, dq_block)
+    dt = _lib.DTYPE_F32 if out_dtype == torch.float32 else _lib.DTYPE_BF16
+    _call("molt_nf4_dequantize", C.byref(w), out.data_ptr(), dt, _stream(dev))
+    return out
+
+
+@nf4_dequantize_nested.register_fake
+def _(packed, absmax_q, absmax2, code2, code, offset, rows, cols, block_size, dq_block, order, out_dtype):
+    return packed.new_empty((rows, cols), dtype=out_dtype)
+
+
+@torch.library.custom_op(f"{NS}::nf4_resolve_scales", mutates_args=())
+def nf4_resolve_scales(absmax_q: Tensor, absmax2: Tensor, code2: Tensor, offset: float,
+                       dq_block: int) -> Tensor:
+    """fp32 block scales from nested statistics (methods/nf4_backward.py:145-164)."""
+    dev = _require_gpu(absmax_q, absmax2, code2, what="NF4 scale resolution")
+    q = absmax_q.contiguous()
+    out = torch.empty(q.numel(), device=dev, dtype=torch.float32)
+    # rows*cols only matter through ceil(n / block_size); describe n = nblocks with block 1
+    w = _weight(torch.empty(1, dtype=torch.uint8, device=dev), None,
+                torch.empty(16, device=dev), 1, q.numel(), 1, 1, q, _f32(absmax2), _f32(code2),
+                offset, dq_block)
+    _call("molt_nf4_resolve_scales", C.byref(w), out.data_ptr(), _stream(dev))
+    return out
+
+
+@nf4_resolve_scales.register_fake
+def _(absmax_q, absmax2, code2, offset, dq_block):
+    return absmax_q.new_empty(absmax_q.numel(), dtype=torch.float32)
+
+
+@torch.library.custom_op(f"{NS}::nf4_quantize", mutates_args=())
+def nf4_quantize(x: Tensor, block_size: int, order: int, code: Tensor) -> tuple[Tensor, Tensor]:
+    """Blockwise NF4 codes + fp32 absmax (streaming/nf4.py:46-68)."""
+    what = "NF4 quantize"
+    dev = _require_gpu(x, code, what=what)
+    if x.numel() == 0 or block_size < 16 or block_size % 2:
+        raise ValueError("invalid tensor or NF4 block size")
+    if x.dtype == torch.bfloat16:
+        src, dt = x.contiguous(), _lib.DTYPE_BF16
+    else:
+        src, dt = x.detach().to(torch.float32).contiguous(), _lib.DTYPE_F32
+    n = src.numel()
+    nblocks = -(-n // block_size)
+    packed = torch.empty(nblocks * block_size // 2, device=dev, dtype=torch.uint8)
+    absmax = torch.empty(nblocks, device=dev, dtype=torch.float32)
+    _call("molt_nf4_quantize", src.data_ptr(), dt, n, block_size, order, _f32(code).data_ptr(),
+          packed.data_ptr(), absmax.data_ptr(), _stream(dev))
+    return packed, absmax
+
+
+@nf4_quantize.register_fake
+def _(x, block_size, order, code):
+    nblocks = -(-x.numel() // block_size)
+    return (x.new_empty(nblocks * block_size // 2, dtype=torch.uint8),
+            x.new_empty(nblocks, dtype=torch.float32))
+
+
+@torch.library.custom_op(f"{NS}::nf4_double_quantize", mutates_args=())
+def nf4_double_quantize(absmax: Tensor, code2: Tensor, dq_block: int) -> tuple[Tensor, Tensor, Tensor]:
+    """Nested statistics (bitsandbytes compress_statistics=True)."""
+    dev = _require_gpu(absmax, code2, what="NF4 double quantize")
+    a = _f32(absmax)
+    n = a.numel()
+    q = torch.empty(n, device=dev, dtype=torch.uint8)
+    absmax2 = torch.empty(-(-n // dq_block), device=dev, dtype=torch.float32)
+    offset = torch.empty((), device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    ws_bytes = int(lib.molt_nf4_double_quantize_workspace(n))
+    ws = torch.empty(max(ws_bytes, 8), device=dev, dtype=torch.uint8)
+    _call("molt_nf4_double_quantize", a.data_ptr(), n, dq_block, _f32(code2).data_ptr(), q.data_ptr(),
+          absmax2.data_ptr(), offset.data_ptr(), ws.data_ptr(), ws_bytes, _stream(dev))
+    return q, absmax2, offset
+
+
+@nf4_double_quantize.register_fake
+def _(absmax, code2, dq_block):
+    n = absmax.numel()
+    return (absmax.new_empty(n, dtype=torch.uint8), absmax.new_empty(-(-n // dq_block)),
+            absmax.new_empty(()))
+
+
+# ------------------------------------------------------------ NF4 + LoRA
+@torch.library.custom_op(f"{NS}::lora_project", mutates_args=())
+def lora_project(z: Tensor, z2: Optional[Tensor], mode: int, zscale: float, lora: Tensor,
+                 layout: int) -> Tensor:
+    """out[M, r] = bf16(z . bf16(lora)^T) (methods/nf4_lora.py:49,86-90)."""
+    what = "LoRA projection"
+    dev = _require_gpu(z, z2, lora, what=what)
+    z = _bf16(z, "activations", what)
+    z2 = None if z2 is None else _bf16(z2, "activations", what)
+    if z.dim() != 2:
+        raise ValueError(f"{what}: expected a 2-D activation")
+    m, d = z.shape
+    lw = _f32(lora)
+    r = lw.shape[0] if layout == 0 else lw.shape[1]
+    if (lw.shape[1] if layout == 0 else lw.shape[0]) != d:
+        raise ValueError(f"{what}: adapter width {tuple(lw.shape)} does not match activation width {d}")
+    out = torch.empty((m, r), device=dev, dtype=torch.bfloat16)
+    _call("molt_lora_project", z.data_ptr(), _ptr(z2), d, mode, zscale, m, d, lw.data_ptr(), layout, r,
+          out.data_ptr(), r, _stream(dev))
+    return out
+
+
+@lora_project.register_fake
+def _(z, z2, mode, zscale, lora, layout):
+    r = lora.shape[0] if layout == 0 else lora.shape[1]
+    return z.new_empty((z.shape[0], r), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op(f"{NS}::nf4_lora_forward", mutates_args=())
+def nf4_lora_forward(x: Tensor, packed: Tensor, scales: Tensor, code: Tensor, rows: int, cols: int,
+                     order: int, block_size: int, t: Optional[Tensor], lora_b: Optional[Tensor],
+                     scaling: float) -> Tensor:
+    """Y = X deq(W)^T + T bf16(s B)^T (methods/nf4_lora.py:43-50)."""
+    what = "NF4-LoRA forward"
+    dev = _require_gpu(x, packed, scales, code, t, lora_b, what=what)
+    x = _bf16(x, "activations", what)
+    if x.dim() != 2 or x.shape[1] != cols:
+        raise ValueError(f"{what}: input width {tuple(x.shape)} does not match in_features {cols}")
+    packed = _check_packed(packed, rows, cols, what)
+    y = torch.empty((x.shape[0], rows), device=dev, dtype=torch.bfloat16)
+    w = _weight(packed, _f32(scales), _f32(code), rows, cols, block_size, order)
+    r = 0
+    tt = bb = None
+    if t is not None:
+        tt = _bf16(t, "low-rank activations", what)
+        bb = _f32(lora_b)
+        r = tt.shape[1]
+        if bb.shape != (rows, r):
+            raise ValueError(f"{what}: LoRA B shape {tuple(bb.shape)} != ({rows}, {r})")
+    _call("molt_nf4_lora_forward", x.data_ptr(), cols, x.shape[0], C.byref(w), _ptr(tt), max(r, 1),
+          _ptr(bb), r, float(scaling), y.data_ptr(), rows, _stream(dev))
+    return y
+
+
+@nf4_lora_forward.register_fake
+def _(x, packed, scales, code, rows, cols, order, block_size, t, lora_b, scaling):
+    return x.new_empty((x.shape[0], rows), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op(f"{NS}::nf4_gateup_forward", mutates_args=())
+def nf4_gateup_forward(x: Tensor, packed_g: Tensor, scales_g: Tensor, packed_u: Tensor,
+                       scales_u: Tensor, code: Tensor, rows: int, cols: int, order: int,
+                       t: Optional[Tensor], lora_bg: Optional[Tensor], lora_bu: Optional[Tensor],
+                       sg: float, su: float) -> tuple[Tensor, Tensor, Tensor]:
+    """gate, up and h = bf16(bf16(silu(gate)) up) in one launch
+    (methods/gated_replay.py:78-94,290-291)."""
+    what = "NF4-LoRA gate/up forward"
+    dev = _require_gpu(x, packed_g, scales_g, packed_u, scales_u, code, t, what=what)
+    x = _bf16(x, "activations", what)
+    if x.dim() != 2 or x.shape[1] != cols:
+        raise ValueError(f"{what}: input width {tuple(x.shape)} does not match in_features {cols}")
+    pg = _check_packed(packed_g, rows, cols, what)
+    pu = _check_packed(packed_u, rows, cols, what)
+    cd = _f32(code)
+    wg = _weight(pg, _f32(scales_g), cd, rows, cols, 64, order)
+    wu = _weight(pu, _f32(scales_u), cd, rows, cols, 64, order)
+    m = x.shape[0]
+    outs = [torch.empty((m, rows), device=dev, dtype=torch.bfloat16) for _ in range(3)]
+    r = 0
+    tt = bg = bu = None
+    if t is not None:
+        tt = _bf16(t, "low-rank activations", what)
+        r = tt.shape[1] // 2
+        bg, bu = _f32(lora_bg), _f32(lora_bu)
+        if bg.shape != (rows, r) or bu.shape != (rows, r):
+            raise ValueError(f"{what}: LoRA B shapes {tuple(bg.shape)}, {tuple(bu.shape)} != ({rows}, {r})")
+    _call("molt_nf4_gateup_forward", x.data_ptr(), cols, m, C.byref(wg), C.byref(wu), _ptr(tt),
+          max(2 * r, 1), _ptr(bg), _ptr(bu), r, float(sg), float(su), outs[0].data_ptr(),
+          outs[1].data_ptr(), outs[2].data_ptr(), rows, _stream(dev))
+    return outs[0], outs[1], outs[2]
+
+
+@nf4_gateup_forward.register_fake
+def _(x, packed_g, scales_g, packed_u, scales_u, code, rows, cols, order, t, lora_bg, lora_bu, sg, su):
+    return tuple(x.new_empty((x.shape[0], rows), dtype=torch.bfloat16) for _ in range(3))
+
+
+@torch.library.custom_op(f"{NS}::nf4_lora_backward_input", mutates_args=())
+def nf4_lora_backward_input(dy: Tensor, packed: Tensor, scales: Tensor, code: Tensor, rows: int,
+                            cols: int, order: int, block_size: int, u: Optional[Tensor],
+                            lora_a: Optional[Tensor], lora_scale: float) -> Tensor:
+    """dX = dY deq(W) + U bf16(lora_scale A) (methods/nf4_lora.py:86-101;
+    methods/nf4_backward.py:167-284)."""
+    what = "NF4-LoRA backward"
+    dev = _require_gpu(dy, packed, scales, code, u, lora_a, what=what)
+    dy = _bf16(dy, "gradients", what)
+    if dy.dim() != 2 or dy.shape[1] != rows:
+        raise ValueError("gradient width must match the NF4 output dimension")
+    packed = _check_packed(packed, rows, cols, what)
+    dx = torch.empty((dy.shape[0], cols), device=dev, dtype=torch.bfloat16)
+    w = _weight(packed, _f32(scales), _f32(code), rows, cols, block_size, order)
+    r = 0
+    uu = aa = None
+    if u is not None:
+        uu = _bf16(u, "LoRA gradients", what)
+        aa = _f32(lora_a)
+        r = uu.shape[1]
+        if uu.shape[0] != dy.shape[0]:
+            raise ValueError("LoRA gradient rows must match the output gradient")
+        if aa.dim() != 2 or aa.shape != (r, cols):
+            raise ValueError("LoRA gradient and A matrix dimensions are incompatible")
+    _call("molt_nf4_lora_backward_input", dy.data_ptr(), rows, dy.shape[0], C.byref(w), _ptr(uu),
+          max(r, 1), _ptr(aa), r, float(lora_scale), dx.data_ptr(), cols, _stream(dev))
+    return dx
+
+
+@nf4_lora_backward_input.register_fake
+def _(dy, packed, scales, code, rows, cols, order, block_size, u, lora_a, lora_scale):
+    return dy.new_empty((dy.shape[0], cols), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op(f"{NS}::nf4_lora_backward_input_pair", mutates_args=())
+def nf4_lora_backward_input_pair(dy0: Tensor, dy1: Tensor, packed0: Tensor, scales0: Tensor,
+                                 packed1: Tensor, scales1: Tensor, code: Tensor, rows: int, cols: int,
+                                 order: int, u0: Optional[Tensor], u1: Optional[Tensor],
+                                 a0: Optional[Tensor], a1: Optional[Tensor]) -> Tensor:
+    """dX of the gate and up projections in one contraction
+    (methods/gated_replay.py:167-186)."""
+    what = "NF4-LoRA paired backward"
+    dev = _require_gpu(dy0, dy1, packed0, scales0, packed1, scales1, code, u0, u1, a0, a1, what=what)
+    dy0 = _bf16(dy0, "gradients", what)
+    dy1 = _bf16(dy1, "gradients", what)
+    if dy0.shape != dy1.shape or dy0.dim() != 2 or dy0.shape[1] != rows:
+        raise ValueError("gradient width must match the NF4 output dimension")
+    p0 = _check_packed(packed0, rows, cols, what)
+    p1 = _check_packed(packed1, rows, cols, what)
+    cd = _f32(code)
+    w0 = _weight(p0, _f32(scales0), cd, rows, cols, 64, order)
+    w1 = _weight(p1, _f32(scales1), cd, rows, cols, 64, order)
+    m = dy0.shape[0]
+    dx = torch.empty((m, cols), device=dev, dtype=torch.bfloat16)
+    r = 0
+    uu0 = uu1 = aa0 = aa1 = None
+    if u0 is not None:
+        uu0, uu1 = _bf16(u0, "LoRA gradients", what), _bf16(u1, "LoRA gradients", what)
+        aa0, aa1 = _f32(a0), _f32(a1)
+        r = uu0.shape[1]
+        if uu1.shape != uu0.shape or aa0.shape != (r, cols) or aa1.shape != (r, cols):
+            raise ValueError("LoRA gradient and A matrix dimensions are incompatible")
+    _call("molt_nf4_lora_backward_input_pair", dy0.data_ptr(), dy1.data_ptr(), rows, m, C.byref(w0),
+          C.byref(w1), _ptr(uu0), _ptr(uu1), max(r, 1), _ptr(aa0), _ptr(aa1), r, dx.data_ptr(), cols,
+          _stream(dev))
+    return dx
+
+
+@nf4_lora_backward_input_pair.register_fake
+def _(dy0, dy1, packed0, scales0, packed1, scales1, code, rows, cols, order, u0, u1, a0, a1):
+    return dy0.new_empty((dy0.shape[0], cols), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op(f"{NS}::nf4_swiglu_backward", mutates_args=())
+def nf4_swiglu_backward(dy: Tensor, packed: Tensor, scales: Tensor, code: Tensor, rows: int, cols: int,
+                        order: int, u: Optional[Tensor], lora_a: Optional[Tensor], gate: Tensor,
+                        up: Tensor) -> tuple[Tensor, Tensor]:
+    """(dgate, dup) from dY through the down projection and SwiGLU
+    (methods/gated_replay.py:376-387); dh is never stored."""
+    what = "NF4-LoRA SwiGLU backward"
+    dev = _require_gpu(dy, packed, scales, code, u, lora_a, gate, up, what=what)
+    dy = _bf16(dy, "gradients", what)
+    gate = _bf16(gate, "gate", what)
+    up = _bf16(up, "up", what)
+    if dy.dim() != 2 or dy.shape[1] != rows:
+        raise ValueError("gradient width must match the NF4 output dimension")
+    if gate.shape != (dy.shape[0], cols) or up.shape != gate.shape:
+        raise ValueError(f"{what}: gate/up shape must be ({dy.shape[0]}, {cols})")
+    packed = _check_packed(packed, rows, cols, what)
+    w = _weight(packed, _f32(scales), _f32(code), rows, cols, 64, order)
+    dg = torch.empty_like(gate)
+    du = torch.empty_like(up)
+    r = 0
+    uu = aa = None
+    if u is not None:
+        uu, aa = _bf16(u, "LoRA gradients", what), _f32(lora_a)
+        r = uu.shape[1]
+        if aa.shape != (r, cols):
+            raise ValueError("LoRA gradient and A matrix dimensions are incompatible")
+    _call("molt_nf4_swiglu_backward", dy.data_ptr(), rows, dy.shape[0], C.byref(w), _ptr(uu), max(r, 1),
+          _ptr(aa), r, gate.data_ptr(), up.data_ptr(), cols, dg.data_ptr(), du.data_ptr(), _stream(dev))
+    return dg, du
+
+
+@nf4_swiglu_backward.register_fake
+def _(dy, packed, scales, code, rows, cols, order, u, lora_a, gate, up):
+    return torch.empty_like(gate), torch.empty_like(up)
+
+
+@torch.library.custom_op(f"{NS}::lora_grad", mutates_args=())
+def lora_grad(l: Tensor, l2: Optional[Tensor], mode: int, rmat: Tensor, scale: float,
+              layout: int) -> Tensor:
+    """scale * L^T R in fp32: dB = s dY^T T (layout 0, [P, Q]) and dA = U^T X
+    (layout 1, [Q, P]) (methods/nf4_lora.py:102-103)."""
+    what = "LoRA gradient"
+    dev = _require_gpu(l, l2, rmat, what=what)
+    l = _bf16(l, "activations", what)
+    l2 = None if l2 is None else _bf16(l2, "activations", what)
+    rmat = _bf16(rmat, "low-rank operand", what)
+    if l.dim() != 2 or rmat.dim() != 2 or l.shape[0] != rmat.shape[0]:
+        raise ValueError(f"{what}: row counts differ ({tuple(l.shape)} vs {tuple(rmat.shape)})")
+    m, p = l.shape
+    q = rmat.shape[1]
+    out = torch.empty((p, q) if layout == 0 else (q, p), device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    ws_bytes = int(lib.molt_lora_grad_workspace(m, p, q))
+    ws = torch.empty(max(ws_bytes, 4), device=dev, dtype=torch.uint8)
+    _call("molt_lora_grad", l.data_ptr(), _ptr(l2), p, mode, rmat.data_ptr(), q, m, p, q, float(scale),
+          out.data_ptr(), layout, ws.data_ptr(), ws_bytes, _stream(dev))
+    return out
+
+
+@lora_grad.register_fake
+def _(l, l2, mode, rmat, scale, layout):
+    p, q = l.shape[1], rmat.shape[1]
+    return l.new_empty((p, q) if layout == 0 else (q, p), dtype=torch.float32)
+
+
+# ------------------------------------------------------------------ GEMV
+@torch.library.custom_op(f"{NS}::nf4_gemv", mutates_args=())
+def nf4_gemv(x: Tensor, packed: Tensor, scales: Optional[Tensor], absmax_q: Optional[Tensor],
+             absmax2: Optional[Tensor], code2: Optional[Tensor], offset: float, dq_block: int,
+             code: Tensor, rows: int, cols: int, order: int, t: Optional[Tensor],
+             lora_b: Optional[Tensor], scaling: float) -> Tensor:
+    """Skinny-M (<= 16 tokens) NF4 GEMV with the LoRA add-on (decode path of
+    training/qlora.py:1332-1358)."""
+    what = "NF4 GEMV"
+    dev = _require_gpu(x, packed, code, t, lora_b, what=what)
+    x = _bf16(x, "activations", what)
+    if x.dim() != 2 or x.shape[1] != cols or not 1 <= x.shape[0] <= 16:
+        raise ValueError(f"{what}: needs 1..16 rows of width {cols}, got {tuple(x.shape)}")
+    packed = _check_packed(packed, rows, cols, what)
+    m = x.shape[0]
+    nested = absmax_q is not None
+    w = _weight(packed, None if nested else _f32(scales), _f32(code), rows, cols, 64, order,
+                absmax_q.contiguous() if nested else None, _f32(absmax2) if nested else None,
+                _f32(code2) if nested else None, offset, dq_block)
+    y = torch.empty((m, rows), device=dev, dtype=torch.bfloat16)
+    r = 0
+    tt = bb = None
+    if t is not None:
+        tt, bb = _bf16(t, "low-rank activations", what), _f32(lora_b)
+        r = tt.shape[1]
+        if bb.shape != (rows, r):
+            raise ValueError(f"{what}: LoRA B shape {tuple(bb.shape)} != ({rows}, {r})")
+    lib = _lib.load()
+    ws_bytes = int(lib.molt_nf4_gemv_workspace(m, rows, cols))
+    ws = torch.zeros(max(ws_bytes, 256), device=dev, dtype=torch.uint8)
+    _call("molt_nf4_gemv", x.data_ptr(), cols, m, C.byref(w), _ptr(tt), max(r, 1), _ptr(bb), r,
+          float(scaling), y.data_ptr(), rows, ws.data_ptr(), ws_bytes, _stream(dev))
+    return y
+
+
+@nf4_gemv.register_fake
+def _(x, packed, scales, absmax_q, absmax2, code2, offset, dq_block, code, rows, cols, order, t, lora_b,
+      scaling):
+    return x.new_empty((x.shape[0], rows), dtype=torch.bfloat16)
+
+
+# --------------------------------------------------------------- SwiGLU
+def _sw_dtype(t: Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return _lib.DTYPE_BF16
+    if t.dtype == torch.float32:
+        return _lib.DTYPE_F32
+    raise CapabilityError(f"fused SiLU multiply supports bf16 and fp32 (got {t.dtype})")
+
+
+@torch.library.custom_op(f"{NS}::silu_mul_forward", mutates_args=())
+def silu_mul_forward(gate: Tensor, up: Tensor, round_silu: bool) -> Tensor:
+    """h = silu(g) * u (kernels/gated_activation.py:29-36)."""
+    dev = _require_gpu(gate, up, what="fused SiLU multiply")
+    g, u = gate.contiguous(), up.contiguous()
+    out = torch.empty_like(g)
+    _call("molt_silu_mul_forward", g.data_ptr(), u.data_ptr(), out.data_ptr(), g.numel(), _sw_dtype(g),
+          int(round_silu), _stream(dev))
+    return out
+
+
+@silu_mul_forward.register_fake
+def _(gate, up, round_silu):
+    return torch.empty_like(gate)
+
+
+@torch.library.custom_op(f"{NS}::silu_mul_backward", mutates_args=())
+def silu_mul_backward(grad: Tensor, gate: Tensor, up: Tensor) -> tuple[Tensor, Tensor]:
+    """(dgate, dup) of h = silu(g) * u (kernels/gated_activation.py:38-51)."""
+    dev = _require_gpu(grad, gate, up, what="fused SiLU multiply")
+    d, g, u = grad.contiguous(), gate.contiguous(), up.contiguous()
+    dg, du = torch.empty_like(g), torch.empty_like(u)
+    _call("molt_silu_mul_backward", d.data_ptr(), g.data_ptr(), u.data_ptr(), dg.data_ptr(), du.data_ptr(),
+          g.numel(), _sw_dtype(g), _stream(dev))
+    return dg, du
+
+
+@silu_mul_backward.register_fake
+def _(grad, gate, up):
+    return torch.empty_like(gate), torch.empty_like(up)

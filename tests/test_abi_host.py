@@ -1,0 +1,130 @@
+"""CPU-only checks: the C ABI library loads and exports every function declared
+in include/molt_amd.h; the Python boundary mirrors the reference's error
+behaviour without touching a GPU."""
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import molt_amd
+from molt_amd import _lib
+from molt_amd.errors import CapabilityError
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "molt_amd.h"
+
+
+def _declared() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(molt_\w+)\s*\(", text, flags=re.M))
+
+
+def test_library_exports_every_declared_symbol():
+    declared = _declared()
+    assert len(declared) >= 18
+    lib = _lib.load()
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(_lib.SIGNATURES) == declared
+    assert lib.molt_amd_version().startswith(b"molt_amd")
+
+
+def test_workspace_queries_need_no_gpu():
+    lib = _lib.load()
+    assert lib.molt_nf4_double_quantize_workspace(917504) == 224 * 8
+    assert lib.molt_lora_grad_workspace(8192, 4096, 64) > 0
+    assert lib.molt_nf4_gemv_workspace(1, 4096, 4096) >= 0
+    assert lib.molt_nf4_gemv_workspace(0, 4096, 4096) == 0
+
+
+def test_invalid_arguments_return_codes_without_a_gpu():
+    lib = _lib.load()
+    rc = lib.molt_nf4_quantize(None, 0, 10, 64, 1, None, None, None, None)
+    assert rc == _lib.MOLT_EINVAL
+    assert b"null" in lib.molt_amd_last_error()
+    w = _lib.NF4Weight()
+    w.rows, w.cols, w.block_size = 4, 4, 64
+    rc = lib.molt_nf4_gemv(None, 4, 32, w, None, 1, None, 0, 0.0, None, 4, None, 0, None)
+    assert rc == _lib.MOLT_EINVAL
+    with pytest.raises(ValueError):
+        _lib.check(_lib.MOLT_EINVAL)
+    with pytest.raises(CapabilityError):
+        _lib.check(_lib.MOLT_EUNSUPPORTED)
+
+
+def test_scheduled_nf4_lora_refuses_cpu():
+    """tests/kernels/test_nf4_lora.py:82-93."""
+    from molt_amd.methods import scheduled_nf4_lora
+
+    class QuantState:
+        pass
+
+    x = torch.randn(2, 4, requires_grad=True)
+    packed = torch.zeros(8, 1, dtype=torch.uint8)
+    a = torch.randn(2, 4, requires_grad=True)
+    b = torch.randn(4, 2, requires_grad=True)
+    with pytest.raises(Exception, match="requires CUDA"):
+        scheduled_nf4_lora(x, packed, a, b, QuantState(), 1.0)
+
+
+def test_module_suffix_filter_refuses_when_no_compatible_projection():
+    """tests/kernels/test_nf4_lora.py:96-103."""
+    from molt_amd.methods import enable_scheduled_nf4_lora
+
+    with pytest.raises(CapabilityError, match="down_proj"):
+        enable_scheduled_nf4_lora(torch.nn.Sequential(torch.nn.Linear(4, 4)), module_suffixes=("down_proj",))
+
+
+def test_gated_replay_patcher_validates_arguments():
+    from molt_amd.methods import enable_asymmetric_gated_replay
+
+    model = torch.nn.Sequential(torch.nn.Linear(4, 4))
+    with pytest.raises(ValueError, match="negative"):
+        enable_asymmetric_gated_replay(model, offload_blocks=-1)
+    with pytest.raises(ValueError, match="mutually exclusive"):
+        enable_asymmetric_gated_replay(model, offload_blocks=1)
+    with pytest.raises(CapabilityError, match="No compatible"):
+        enable_asymmetric_gated_replay(model)
+
+
+def test_fused_silu_multiply_rejects_mismatch_and_cpu():
+    """tests/kernels/test_gated_activation.py:45-47; CPU tensors are refused
+    (no host fallback on the shipped path)."""
+    from molt_amd.kernels import fused_silu_multiply
+
+    with pytest.raises(ValueError, match="identical"):
+        fused_silu_multiply(torch.randn(2, 3), torch.randn(2, 4))
+    with pytest.raises(CapabilityError, match="CUDA"):
+        fused_silu_multiply(torch.randn(2, 3), torch.randn(2, 3))
+
+
+def test_codec_front_ends_refuse_cpu():
+    with pytest.raises(CapabilityError):
+        molt_amd.quantize_4bit(torch.randn(8, 64))
+    from molt_amd import ops
+
+    with pytest.raises(CapabilityError):
+        ops.nf4_dequantize(torch.zeros(4, dtype=torch.uint8), torch.ones(1), molt_amd.NF4_CODEBOOK, 1, 8, 64, 1,
+                           torch.bfloat16)
+
+
+def test_quant_state_shape_and_dynamic_map():
+    qs = molt_amd.QuantState(torch.zeros(4), (8, 32), molt_amd.NF4_CODEBOOK, 64)
+    assert qs.quant_type == "nf4" and not qs.nested and qs.shape == torch.Size([8, 32])
+    m = molt_amd.dynamic_map()
+    assert m.shape == (256,) and bool((m[1:] > m[:-1]).all())
+
+
+def test_fake_impls_give_shapes_without_a_gpu():
+    from molt_amd import ops
+
+    with torch._subclasses.fake_tensor.FakeTensorMode():
+        x = torch.empty(10, 128, dtype=torch.bfloat16, device="cuda")
+        a = torch.empty(4, 128, device="cuda")
+        t = ops.lora_project(x, None, 0, 1.0, a, 0)
+        assert t.shape == (10, 4)
+        g = ops.lora_grad(x, None, 0, t, 1.0, 1)
+        assert g.shape == (4, 128) and g.dtype == torch.float32

@@ -1,0 +1,88 @@
+"""Skinny-M NF4 GEMV (M <= 16) with the LoRA add-on vs the fp64 oracle."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import nf4_oracle as O
+from tests._util import assert_close_fro, bf16_values, np_f32, oracle_weight, seeded, uniform
+
+import molt_amd
+from molt_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _gemv(x, packed, qs, t=None, b=None, s=0.0, nested=True):
+    rows, cols = int(qs.shape[0]), int(qs.shape[1])
+    if nested and qs.nested:
+        s2 = qs.state2
+        return ops.nf4_gemv(x, packed.reshape(-1), None, qs.absmax, s2.absmax, s2.code, float(qs.offset),
+                            int(s2.blocksize), qs.code, rows, cols, qs.nibble_order, t, b, s)
+    return ops.nf4_gemv(x, packed.reshape(-1), molt_amd.resolved_nf4_scales(qs), None, None, None, 0.0, 256,
+                        qs.code, rows, cols, qs.nibble_order, t, b, s)
+
+
+@pytest.mark.parametrize("n,k", [(64, 64), (256, 512), (1024, 4096), (96, 192), (4096, 4096)])
+@pytest.mark.parametrize("m", [1, 2, 4, 8, 16])
+def test_gemv_matches_oracle(n, k, m):
+    print(f"gemv n={n} k={k} m={m}", flush=True)
+    w = seeded((n, k), 50 + n, std=0.02, dtype=torch.float32)
+    packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True)
+    x = seeded((m, k), 60 + m)
+    y = _gemv(x, packed, qs)
+    wo = oracle_weight(packed, qs).dequant_bf16().astype(np.float64)
+    assert_close_fro(np_f32(y), bf16_values(x) @ wo.T, what="Y")
+
+
+@pytest.mark.parametrize("m", [1, 5, 16])
+def test_gemv_with_lora_matches_oracle(m):
+    n, k, r, s = 1024, 4096, 16, 2.0
+    w = seeded((n, k), 70, std=0.02, dtype=torch.float32)
+    packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True)
+    x = seeded((m, k), 71)
+    a = uniform((r, k), 72, 1.0 / np.sqrt(k))
+    b = seeded((n, r), 73, std=0.01, dtype=torch.float32)
+    t = ops.lora_project(x, None, 0, 1.0, a, 0)
+    y = _gemv(x, packed, qs, t, b, s)
+    wo = oracle_weight(packed, qs).dequant_bf16().astype(np.float64)
+    ref = O.lora_linear_forward(bf16_values(x), wo, bf16_values(a), bf16_values(b), s)
+    assert_close_fro(np_f32(y), ref, what="Y")
+
+
+def test_gemv_resolved_scales_and_low_nibble_layout():
+    w = seeded((512, 1024), 80, std=0.02, dtype=torch.float32)
+    packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=False, nibble_order=0)
+    x = seeded((3, 1024), 81)
+    y = _gemv(x, packed, qs, nested=False)
+    wo = oracle_weight(packed, qs).dequant_bf16().astype(np.float64)
+    assert_close_fro(np_f32(y), bf16_values(x) @ wo.T, what="Y")
+
+
+def test_gemv_repeat_is_deterministic_and_workspace_reusable():
+    w = seeded((14336, 4096), 90, std=0.02, dtype=torch.float32)
+    packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True)
+    del w
+    x = seeded((16, 4096), 91)
+    first = _gemv(x, packed, qs)
+    for _ in range(3):
+        assert torch.equal(_gemv(x, packed, qs), first)
+    xs = seeded((2, 4096), 92)
+    wo = oracle_weight(packed, qs).dequant_bf16()
+    ref = bf16_values(xs) @ wo.astype(np.float64).T
+    assert_close_fro(np_f32(_gemv(xs, packed, qs)), ref, what="Y")
+    # property at full size: the GEMV row equals the GEMM row for the same token
+    ref16 = bf16_values(x) @ wo.astype(np.float64).T
+    assert_close_fro(np_f32(first), ref16, what="Y16")
+
+
+def test_gemv_rejects_unsupported_geometry():
+    w = seeded((64, 96), 1, std=0.02, dtype=torch.float32)
+    packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=False)
+    with pytest.raises(molt_amd.CapabilityError, match="cols"):
+        _gemv(seeded((2, 96), 2), packed, qs, nested=False)
+    w2 = seeded((64, 128), 1, std=0.02, dtype=torch.float32)
+    packed2, qs2 = molt_amd.quantize_4bit(w2, blocksize=64, compress_statistics=False)
+    with pytest.raises(ValueError, match="1..16"):
+        _gemv(seeded((17, 128), 2), packed2, qs2, nested=False)

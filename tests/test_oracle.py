@@ -1,0 +1,252 @@
+"""Pins for the CPU oracle (no GPU). Each check is independent of the formula
+it checks: a published construction, torch's own implementation, the
+reference's own CPU tests, exact arithmetic, or per-element brute force."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import nf4_oracle as O
+
+
+# --------------------------------------------------------------- codebook
+def _qlora_normal_map(offset: float = 0.9677083) -> np.ndarray:
+    """NF4 levels from the QLoRA construction: normal quantiles, 8 positive and
+    7 negative, plus zero, normalised by the largest."""
+    from scipy.stats import norm
+
+    v1 = norm.ppf(np.linspace(offset, 0.5, 9)[:-1])
+    v3 = -norm.ppf(np.linspace(offset, 0.5, 8)[:-1])
+    values = np.sort(np.concatenate([v1, [0.0], v3]))
+    return values / values.max()
+
+
+def test_codebook_matches_qlora_normal_quantiles():
+    ref = _qlora_normal_map()
+    assert O.NF4_CODE.shape == (16,)
+    np.testing.assert_allclose(O.NF4_CODE.astype(np.float64), ref, rtol=0, atol=2e-7)
+    assert O.NF4_CODE[7] == 0.0 and O.NF4_CODE[0] == -1.0 and O.NF4_CODE[15] == 1.0
+    assert np.all(np.diff(O.NF4_CODE) > 0)
+
+
+def test_package_codebook_is_the_oracle_codebook():
+    import molt_amd
+
+    assert np.array_equal(molt_amd.NF4_CODEBOOK.numpy().view(np.uint32), O.NF4_CODE.view(np.uint32))
+
+
+# ------------------------------------------------------------ bf16 rounding
+def test_bf16_rne_matches_torch():
+    rng = np.random.default_rng(5)
+    x = np.concatenate([
+        rng.normal(0, 1, 20000).astype(np.float32),
+        rng.normal(0, 1e-30, 2000).astype(np.float32),
+        (rng.integers(0, 2**32, 20000, dtype=np.uint64).astype(np.uint32)).view(np.float32),
+    ])
+    x = x[np.isfinite(x)]
+    ours = O.bf16_rne_bits(x)
+    theirs = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, theirs)
+
+
+# ----------------------------------------------- reference's own CPU test
+def test_reference_storage_and_rms_error():
+    """tests/test_molt_stream_nf4.py:9-15 restated on the oracle."""
+    torch.manual_seed(1)
+    value = torch.randn(64, 64).numpy()
+    t = O.quantize_cleanroom(value, block_size=64)
+    restored = t.dequant_f32()
+    assert O.storage_bytes(t) == value.size // 2 + value.size // 64 * 4
+    assert float(np.sqrt(np.mean((restored - value) ** 2))) < 0.15
+
+
+# --------------------------------------------------------------- quantise
+def _brute_codes(block: np.ndarray, code: np.ndarray) -> tuple[list[int], np.float32]:
+    absmax = np.float32(0.0)
+    for v in block:
+        absmax = max(absmax, np.float32(abs(np.float32(v))))
+    absmax = max(absmax, O.FP32_TINY)
+    out = []
+    for v in block:
+        nv = np.float32(np.float32(v) / absmax)
+        best, bi = None, 0
+        for i, c in enumerate(code):
+            d = np.float32(abs(np.float32(nv - c)))
+            if best is None or d < best:
+                best, bi = d, i
+        out.append(bi)
+    return out, absmax
+
+
+@pytest.mark.parametrize("n,block", [(40, 16), (64, 64), (130, 64), (50, 32)])
+def test_quantize_matches_per_element_brute_force(n, block):
+    rng = np.random.default_rng(n + block)
+    x = rng.normal(0, 1, n).astype(np.float32)
+    idx, absmax = O.quantize_blocks(x, block)
+    padded = np.concatenate([x, np.zeros((-n) % block, np.float32)])
+    for b in range(padded.size // block):
+        codes, am = _brute_codes(padded[b * block:(b + 1) * block], O.NF4_CODE)
+        assert absmax[b] == am
+        assert list(idx[b * block:(b + 1) * block]) == codes
+
+
+def test_exact_codes_round_trip_and_midpoint_ties():
+    # every code times a set of power-of-two and odd scales survives exactly
+    for s in (np.float32(1.0), np.float32(0.5), np.float32(3.0), np.float32(1e-3)):
+        x = (O.NF4_CODE * s).astype(np.float32)
+        idx, absmax = O.quantize_blocks(np.concatenate([x, x]), 32)
+        assert np.array_equal(idx[:16], np.arange(16))
+        assert np.array_equal(O.dequantize_f32(idx, absmax, 32)[:16], x)
+    # at an exact fp32 tie the lower code wins (first index of the minimum)
+    lo, hi = O.NF4_CODE[9], O.NF4_CODE[10]
+    for m in (np.float32((np.float64(lo) + np.float64(hi)) / 2),
+              np.nextafter(np.float32((np.float64(lo) + np.float64(hi)) / 2), np.float32(1))):
+        block = np.array([1.0, m] + [0.0] * 14, np.float32)
+        d_lo, d_hi = np.float32(abs(m - lo)), np.float32(abs(m - hi))
+        idx, _ = O.quantize_blocks(block, 16)
+        assert idx[1] == (9 if d_lo <= d_hi else 10)
+
+
+def test_quantize_invariants():
+    rng = np.random.default_rng(11)
+    x = rng.normal(0, 0.02, 64 * 50).astype(np.float32)
+    idx, absmax = O.quantize_blocks(x, 64)
+    deq = O.dequantize_f32(idx, absmax, 64)
+    gaps = np.diff(O.NF4_CODE.astype(np.float64)).max()
+    blk = np.repeat(absmax, 64)
+    assert np.all(np.abs(deq - x) <= gaps / 2 * blk * (1 + 1e-6))
+    assert np.all(np.sign(deq[np.abs(x) > blk * 0.05]) == np.sign(x[np.abs(x) > blk * 0.05]))
+    # the block maximum maps to +-1
+    for b in range(50):
+        j = np.argmax(np.abs(x[b * 64:(b + 1) * 64]))
+        assert idx[b * 64 + j] in (0, 15)
+
+
+@pytest.mark.parametrize("order", [O.NIBBLE_LOW_FIRST, O.NIBBLE_HIGH_FIRST])
+def test_pack_unpack_against_python_loop(order):
+    rng = np.random.default_rng(order)
+    idx = rng.integers(0, 16, 37).astype(np.uint8)
+    packed = O.pack_nibbles(idx, order)
+    for i in range(37):
+        byte = int(packed[i // 2])
+        first = (byte & 15) if order == O.NIBBLE_LOW_FIRST else (byte >> 4)
+        second = (byte >> 4) if order == O.NIBBLE_LOW_FIRST else (byte & 15)
+        assert idx[i] == (first if i % 2 == 0 else second)
+    assert np.array_equal(O.unpack_nibbles(packed, order, 37), idx)
+
+
+def test_dequant_bf16_is_rne_of_fp32_product():
+    rng = np.random.default_rng(3)
+    idx = rng.integers(0, 16, 4096).astype(np.uint8)
+    scales = np.abs(rng.normal(0, 0.05, 64)).astype(np.float32)
+    prod = torch.from_numpy(O.NF4_CODE)[torch.from_numpy(idx.astype(np.int64))] * \
+        torch.from_numpy(scales).repeat_interleave(64)
+    ref = prod.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.dequantize_bf16_bits(idx, scales, 64), ref)
+
+
+# ------------------------------------------------------ double quantise
+def test_offset_is_the_mean_to_one_ulp():
+    rng = np.random.default_rng(7)
+    for n in (1, 255, 4096, 4097, 100003):
+        a = (np.abs(rng.normal(0, 0.02, n)) + 1e-5).astype(np.float32)
+        off = O.absmax_offset(a)
+        exact = math.fsum(a.astype(np.float64)) / n
+        assert abs(float(off) - exact) <= float(np.spacing(np.float32(exact)))
+
+
+def test_double_quant_bound_and_representable_values():
+    rng = np.random.default_rng(9)
+    absmax = (np.abs(rng.normal(0, 0.02, 3000)) + 1e-4).astype(np.float32)
+    q, absmax2, offset, code2 = O.double_quantize(absmax)
+    scales = O.resolve_scales(q, absmax2, code2, offset)
+    gap = np.diff(code2.astype(np.float64)).max()
+    bound = np.repeat(absmax2, 256)[:absmax.size] * gap / 2 + 4 * np.spacing(absmax)
+    assert np.all(np.abs(scales.astype(np.float64) - absmax) <= bound)
+    # values that are exactly offset + code2[j] * absmax2 decode exactly
+    code_vals = np.array([code2[255], code2[200], code2[128], code2[10], code2[0]], np.float32)
+    a = np.concatenate([absmax[:251], np.zeros(5, np.float32)])
+    q2, am2, off2, _ = O.double_quantize(a, code2)
+    j = np.argmax(np.abs(a - off2))
+    assert q2[j] in (0, 255)
+    assert code_vals.size == 5
+
+
+def test_dynamic_map_structure():
+    """bitsandbytes' create_dynamic_map: PARITY UNPINNED (bitsandbytes absent);
+    only its structure is checked."""
+    m = O.dynamic_map()
+    assert m.shape == (256,) and m.dtype == np.float32
+    assert np.all(np.diff(m) > 0)
+    assert m[-1] == 1.0 and 0.0 in m and m[0] > -1.0 and m[0] < -0.99
+
+
+# ----------------------------------------------------- GEMM-level algebra
+def _autograd_lora(x, w, a, b, s, dy):
+    xt, at, bt = (torch.tensor(v, dtype=torch.float64, requires_grad=True) for v in (x, a, b))
+    wt = torch.tensor(w, dtype=torch.float64)
+    y = xt @ wt.T + s * ((xt @ at.T) @ bt.T)
+    y.backward(torch.tensor(dy, dtype=torch.float64))
+    return y.detach().numpy(), xt.grad.numpy(), at.grad.numpy(), bt.grad.numpy()
+
+
+def test_lora_linear_algebra_matches_autograd():
+    rng = np.random.default_rng(21)
+    m, k, n, r, s = 9, 13, 11, 3, 0.3
+    x, w = rng.normal(size=(m, k)), rng.normal(size=(n, k))
+    a, b, dy = rng.normal(size=(r, k)), rng.normal(size=(n, r)), rng.normal(size=(m, n))
+    y, dx, da, db = _autograd_lora(x, w, a, b, s, dy)
+    np.testing.assert_allclose(O.lora_linear_forward(x, w, a, b, s), y, rtol=1e-12, atol=1e-12)
+    gx, ga, gb = O.lora_linear_backward(x, w, a, b, s, dy)
+    np.testing.assert_allclose(gx, dx, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(ga, da, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(gb, db, rtol=1e-12, atol=1e-12)
+
+
+def test_swiglu_matches_torch_silu():
+    """kernels/gated_activation.py fp32 closed form vs F.silu autograd; also the
+    reference CPU test's tolerance (tests/kernels/test_gated_activation.py:10-26)."""
+    rng = np.random.default_rng(3401)
+    g, u, dh = (rng.normal(size=(3, 5, 17)) for _ in range(3))
+    gt = torch.tensor(g, requires_grad=True)
+    ut = torch.tensor(u, requires_grad=True)
+    h = torch.nn.functional.silu(gt) * ut
+    h.backward(torch.tensor(dh))
+    np.testing.assert_allclose(O.swiglu_forward(g, u), h.detach().numpy(), rtol=1e-12, atol=1e-12)
+    dg, du = O.swiglu_backward(g, u, dh)
+    np.testing.assert_allclose(dg, gt.grad.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(du, ut.grad.numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_gated_mlp_algebra_matches_autograd():
+    rng = np.random.default_rng(1221)
+    m, hd, idim, r, s = 7, 10, 12, 3, 2.0
+    x = rng.normal(size=(m, hd))
+    wg, wu, wd = rng.normal(size=(idim, hd)), rng.normal(size=(idim, hd)), rng.normal(size=(hd, idim))
+    ag, au, ad = rng.normal(size=(r, hd)), rng.normal(size=(r, hd)), rng.normal(size=(r, idim))
+    bg, bu, bd = rng.normal(size=(idim, r)), rng.normal(size=(idim, r)), rng.normal(size=(hd, r))
+    dy = rng.normal(size=(m, hd))
+    T = lambda v, g=True: torch.tensor(v, dtype=torch.float64, requires_grad=g)  # noqa: E731
+    xt, agt, aut, adt, bgt, but, bdt = T(x), T(ag), T(au), T(ad), T(bg), T(bu), T(bd)
+    wgt, wut, wdt = T(wg, False), T(wu, False), T(wd, False)
+    lin = lambda z, w, a, b: z @ w.T + s * ((z @ a.T) @ b.T)  # noqa: E731
+    g, u = lin(xt, wgt, agt, bgt), lin(xt, wut, aut, but)
+    y = lin(torch.nn.functional.silu(g) * u, wdt, adt, bdt)
+    y.backward(torch.tensor(dy))
+    yo, saved = O.gated_mlp_forward(x, wg, wu, wd, ag, bg, au, bu, ad, bd, s, bf16_storage=False)
+    np.testing.assert_allclose(yo, y.detach().numpy(), rtol=1e-11, atol=1e-11)
+    dx, grads = O.gated_mlp_backward(x, wg, wu, wd, ag, bg, au, bu, ad, bd, s, dy, saved, bf16_storage=False)
+    np.testing.assert_allclose(dx, xt.grad.numpy(), rtol=1e-10, atol=1e-10)
+    for got, ref in zip(grads, (agt, bgt, aut, but, adt, bdt)):
+        np.testing.assert_allclose(got, ref.grad.numpy(), rtol=1e-10, atol=1e-10)
+
+
+def test_rel_fro_detects_a_dropped_lora_term():
+    rng = np.random.default_rng(2)
+    x, w = rng.normal(size=(32, 64)), rng.normal(size=(48, 64)) * 0.02
+    a, b = rng.normal(size=(8, 64)) / 8, rng.normal(size=(48, 8)) * 0.1
+    full = O.lora_linear_forward(x, w, a, b, 2.0)
+    assert O.rel_fro(x @ w.T, full) > 5e-3
