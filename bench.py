@@ -100,7 +100,7 @@ def gemv_sweep(dev, reps: int = 20):
             t = ops.lora_project(x, None, 0, 1.0, a, 0)
             y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
             ws_bytes = int(lib.molt_nf4_gemv_workspace(m, n, k))
-            ws = torch.zeros(max(ws_bytes, 256), device=dev, dtype=torch.uint8)
+            ws = torch.zeros(max(ws_bytes, 256), device=dev, dtype=torch.uint8)   # unused when 0 bytes
             torch.cuda.synchronize()
 
             def launch_all():

@@ -188,10 +188,13 @@ int molt_lora_grad(const uint16_t* l, const uint16_t* l2, int64_t ldl, int32_t l
 /* ------------------------------------------------------------------------ */
 
 /* Y[M, N] = bf16( X . (code[W] * scale)^T + T . bf16(s * B)^T ) for M <= 16,
- * reading the nested statistics (or fp32 scales) directly. T bf16 [M, r] from
- * molt_lora_project; r = 0 skips LoRA. Requires cols % 64 == 0 and
- * block_size == 64. Workspace: molt_nf4_gemv_workspace() bytes; its first
- * `counter` bytes must be zero before the first call and are left zero.
+ * reading the nested statistics (or fp32 scales) directly; the block scale is
+ * applied once per 64-element block sum, so each weight enters as its NF4 code
+ * rounded to bf16 times the fp32 scale. T bf16 [M, r] from molt_lora_project,
+ * B fp32 [N, r] (row stride r); r = 0 skips LoRA. Requires cols % 64 == 0,
+ * block_size == 64 and a power-of-two dq_block. molt_nf4_gemv_workspace()
+ * returns the workspace size (0: the kernel needs none; the arguments are kept
+ * so callers need not change if a later kernel does).
  * Replaces the bnb.matmul_4bit decode path (training/qlora.py:1332-1358). */
 size_t molt_nf4_gemv_workspace(int64_t M, int64_t N, int64_t K);
 int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,

@@ -1,7 +1,9 @@
 // NF4 codec kernels (gfx950): dequantise, resolve nested scales, quantise,
 // double-quantise. Every arithmetic step is a single IEEE fp32 operation in a
-// fixed order (explicit __fmul_rn/__fadd_rn so nothing is contracted into an
-// FMA), which makes the results bit-exact against the CPU restatement.
+// fixed order, which makes the results bit-exact against the CPU restatement.
+// `fp contract(off)` keeps a multiply and the following add from being fused
+// into one FMA; it applies to the raw operators written here (it does not
+// reach the operators inside HIP's __fmul_rn/__fadd_rn, so those are not used).
 #include "common.h"
 
 namespace molt {
@@ -17,8 +19,10 @@ struct ScaleSrc {
 
 // scale = fp32(fp32(code2[q] * absmax2[b / dq]) + offset), or the fp32 scale itself.
 MOLT_DEV float block_scale(const ScaleSrc& s, int64_t b) {
+#pragma clang fp contract(off)
   if (!s.nested) return s.scales[b];
-  return __fadd_rn(__fmul_rn(s.code2[s.q[b]], s.absmax2[b / s.dq_block]), s.offset);
+  const float prod = s.code2[s.q[b]] * s.absmax2[b / s.dq_block];
+  return prod + s.offset;
 }
 
 // ---------------------------------------------------------------- dequantise
@@ -57,16 +61,16 @@ __global__ __launch_bounds__(CODEC_NT) void dequant_kernel(const uint8_t* __rest
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const float2 p = tab[(q[i >> 2] >> (8 * (i & 3))) & 0xffu];
-        v[2 * i] = __fmul_rn(p.x, sc);
-        v[2 * i + 1] = __fmul_rn(p.y, sc);
+        v[2 * i] = p.x * sc;
+        v[2 * i + 1] = p.y * sc;
       }
     } else {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const float2 p = tab[(q[i >> 2] >> (8 * (i & 3))) & 0xffu];
         const int64_t ea = e0 + 2 * i, eb = ea + 1;
-        v[2 * i] = ea < n ? __fmul_rn(p.x, block_scale(ss, ea / block)) : 0.0f;
-        v[2 * i + 1] = eb < n ? __fmul_rn(p.y, block_scale(ss, eb / block)) : 0.0f;
+        v[2 * i] = ea < n ? p.x * block_scale(ss, ea / block) : 0.0f;
+        v[2 * i + 1] = eb < n ? p.y * block_scale(ss, eb / block) : 0.0f;
       }
     }
     if (OUT_F32) {
@@ -203,7 +207,7 @@ __global__ __launch_bounds__(CODEC_NT) void dq_quant_kernel(const float* __restr
   float mx = 0.0f;
   for (int i = threadIdx.x; i < dq; i += CODEC_NT) {
     const int64_t k = b * dq + i;
-    if (k < n) mx = fmaxf(mx, fabsf(__fsub_rn(a[k], off)));
+    if (k < n) mx = fmaxf(mx, fabsf(a[k] - off));
   }
   mx = wave_max(mx);
   if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
@@ -214,7 +218,7 @@ __global__ __launch_bounds__(CODEC_NT) void dq_quant_kernel(const float* __restr
   for (int i = threadIdx.x; i < dq; i += CODEC_NT) {
     const int64_t k = b * dq + i;
     if (k >= n) continue;
-    const float nv = __fsub_rn(a[k], off) / am;
+    const float nv = (a[k] - off) / am;
     float best = fabsf(nv - cb[0]);
     int bi = 0;
     for (int c = 1; c < 256; ++c) {

@@ -21,6 +21,8 @@
 // 64 intermediate columns. Each wave's 64-row W sub-tile holds 32 gate rows
 // then the 32 up rows of the same columns, so a lane owns gate and up of the
 // same (m, i) and the epilogue writes g, u and h = bf16(bf16(silu(g)) u).
+#include <stdlib.h>
+
 #include "mfma_core.h"
 
 namespace molt {
@@ -69,6 +71,14 @@ struct Smem {
 };
 
 MOLT_DEV float silu_f32(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
+
+// Two-way select of a kernel-argument array element. Indexing the argument
+// struct with a lane-dependent index makes the compiler fetch the pointer
+// with a vector memory load (and wait for every outstanding load before
+// using it); a select of the two scalar values keeps it in registers.
+template <typename T>
+MOLT_DEV T sel2(T a, T b, int i) { return i ? b : a; }
+#define sel(arr, i) sel2((arr)[0], (arr)[1], (i))
 
 MOLT_DEV uint32_t dequant_pair(const float2* tab, uint32_t byte, float sc) {
   const float2 c = tab[byte];
@@ -134,8 +144,8 @@ MOLT_DEV void wrow_issue(WRowReg& wr, const FwdParams& p, int64_t tn, bool pair,
   float sc = 0.0f;
   if (n < p.N) {
     const int64_t flat = n * p.K + k;
-    q = *reinterpret_cast<const u32x4_t*>(p.packed[which] + (flat >> 1));
-    sc = p.scales[which][flat >> 6];
+    q = *reinterpret_cast<const u32x4_t*>(sel(p.packed, which) + (flat >> 1));
+    sc = sel(p.scales, which)[flat >> 6];
   }
   wr.q = q;
   wr.sc = sc;
@@ -166,8 +176,8 @@ MOLT_DEV void wrow_generic(uint16_t* ws, const FwdParams& p, int64_t tn, bool pa
     uint16_t v = 0;
     if (n < p.N && k < p.K) {
       const int64_t f = n * p.K + k;
-      const int nib = nf4_nibble(p.packed[which], f, p.order);
-      v = bf16_bits(code16[nib] * p.scales[which][f / p.block_size]);
+      const int nib = nf4_nibble(sel(p.packed, which), f, p.order);
+      v = bf16_bits(code16[nib] * sel(p.scales, which)[f / p.block_size]);
     }
     ws[R * LDSW + j] = v;
   }
@@ -181,7 +191,7 @@ MOLT_DEV void wrow_lora(uint16_t* ws, const FwdParams& p, int64_t tn, bool pair,
     fwd_row(R, tn, pair, which, n);
     const int64_t c = k0 + j - (int64_t)which * p.r;  // column inside this weight's adapter
     uint16_t v = 0;
-    if (n < p.N && c >= 0 && c < p.r) v = bf16_bits(p.s[which] * p.lb[which][n * p.ldlb + c]);
+    if (n < p.N && c >= 0 && c < p.r) v = bf16_bits((which ? p.s[1] : p.s[0]) * sel(p.lb, which)[n * p.ldlb + c]);
     ws[R * LDSW + j] = v;
   }
 }
@@ -197,8 +207,8 @@ MOLT_DEV void wcol_issue(WColReg& wr, const BwdParams& p, int seg, int64_t tn, i
   const int cg = tid % CG, rg = tid / CG;
   const int64_t col = tn * BN + 4 * cg;
   const bool ok = col < p.Kw;
-  const uint8_t* packed = p.packed[seg];
-  const float* scales = p.scales[seg];
+  const uint8_t* packed = sel(p.packed, seg);
+  const float* scales = sel(p.scales, seg);
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
     const int64_t c = c0 + 8 * rg + r;
@@ -245,15 +255,15 @@ MOLT_DEV void wcol_generic(uint16_t* ws, const BwdParams& p, int seg, int64_t tn
     uint16_t v = 0;
     if (col < p.Kw && c < p.Nw) {
       const int64_t f = c * p.Kw + col;
-      const int nib = nf4_nibble(p.packed[seg], f, p.order);
-      v = bf16_bits(code16[nib] * p.scales[seg][f / p.block_size]);
+      const int nib = nf4_nibble(sel(p.packed, seg), f, p.order);
+      v = bf16_bits(code16[nib] * sel(p.scales, seg)[f / p.block_size]);
     }
     ws[R * LDSW + j] = v;
   }
 }
 
 MOLT_DEV void wcol_lora(uint16_t* ws, const BwdParams& p, int seg, int64_t tn, int64_t c0, int tid) {
-  const float* a = p.la[seg];
+  const float* a = sel(p.la, seg);
   for (int e = tid; e < BN * BK; e += NT) {
     const int R = e % BN, j = e / BN;
     const int64_t col = tn * BN + R, c = c0 + j;
@@ -408,7 +418,7 @@ __global__ __launch_bounds__(NT) void nf4_bwd_kernel(const BwdParams p) {
     if (ALIGNED && s < p.nseg * ks) {
       const int seg = s / ks;
       const int64_t c0 = (int64_t)(s % ks) * BK;
-      a_issue(ar, p.dy[seg], p.lddy, m0, p.M, c0, tid);
+      a_issue(ar, sel(p.dy, seg), p.lddy, m0, p.M, c0, tid);
       wcol_issue(wr, p, seg, tn, c0, tid);
     }
   };
@@ -422,14 +432,14 @@ __global__ __launch_bounds__(NT) void nf4_bwd_kernel(const BwdParams p) {
         a_commit(ar, xs, tid);
         wcol_commit(wr, ws, sm.tab, tid);
       } else {
-        a_generic(xs, p.dy[seg], p.lddy, m0, p.M, c0, p.Nw, tid);
+        a_generic(xs, sel(p.dy, seg), p.lddy, m0, p.M, c0, p.Nw, tid);
         wcol_generic(ws, p, seg, tn, c0, sm.code16, tid);
       }
     } else {
       const int ls = s - p.nseg * ks;
       const int seg = ls / lsteps;
       const int64_t c0 = (int64_t)(ls % lsteps) * BK;
-      a_generic(xs, p.u[seg], p.ldu, m0, p.M, c0, p.r, tid);
+      a_generic(xs, sel(p.u, seg), p.ldu, m0, p.M, c0, p.r, tid);
       wcol_lora(ws, p, seg, tn, c0, tid);
     }
   };
@@ -478,8 +488,491 @@ __global__ __launch_bounds__(NT) void nf4_bwd_kernel(const BwdParams p) {
   }
 }
 
+// ======================================================================
+// Large-tile kernels for aligned shapes (K, contraction and output widths
+// multiples of 64, NF4 block 64): 256 x 256 workgroup tile, 4 waves of
+// 128 x 128 (16 accumulator tiles per wave, so each 16-byte LDS fragment
+// feeds four MFMAs; the 256 fp32 accumulators live in AGPRs), one-deep
+// register prefetch (the global loads of step s+1 are in flight during the
+// MFMAs of step s and are dequantised into the other LDS buffer after), and
+// an unpadded LDS layout whose 16-byte chunks are XOR-swizzled by
+// (row ^ row/8) & 7 so that fragment reads, row-major stores and the
+// backward's transposed patch stores are all bank-conflict free.
+// ======================================================================
+namespace big {
+
+constexpr int BM = 256, BN = 256, NT = 256, WAVES_M = 2;
+constexpr int WROWS = 128, WCOLS = 128, TM = 4, TN = 4, LD = 64;
+constexpr int GROUP_M = 4;
+
+constexpr int EP_LD = 256 + 8;   // epilogue tile row stride (bf16), 16-byte aligned rows
+
+struct Smem {
+  union {
+    struct {
+      uint16_t xs[2][BM * LD];
+      uint16_t ws[2][BN * LD];
+      float2 tab[256];
+    };
+    uint16_t ep[BM * EP_LD];       // epilogue staging, reused after the main loop
+  };
+};
+
+MOLT_DEV int loff(int R, int c) { return R * LD + ((c ^ ((R ^ (R >> 3)) & 7)) << 3); }
+
+// Per-lane fragment geometry: the first LDS row this lane reads in each
+// operand, and its half (which 8-element chunk of a 16-deep MFMA step).
+struct FragOff { int arow, brow, h; };
+
+MOLT_DEV void frag_offsets(FragOff& f, int arow0, int brow0, int lane) {
+  f.arow = arow0 + (lane & 31);
+  f.brow = brow0 + (lane & 31);
+  f.h = lane >> 5;
+}
+
+MOLT_DEV void load_frags(const uint16_t* __restrict__ ws, const uint16_t* __restrict__ xs, const FragOff& f, int kk,
+                         bf16x8_t (&a)[TM], bf16x8_t (&b)[TN]) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+    a[i] = *reinterpret_cast<const bf16x8_t*>(ws + loff(f.arow + 32 * i, 2 * kk + f.h));
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+    b[j] = *reinterpret_cast<const bf16x8_t*>(xs + loff(f.brow + 32 * j, 2 * kk + f.h));
+}
+
+// One BK step: four 16-deep sub-steps of 16 MFMAs each. Fragments are double
+// buffered: the LDS reads of sub-step kk+1 are issued before the MFMAs of
+// sub-step kk, so LDS latency hides under matrix work; the scheduling barrier
+// after each sub-step bounds the live fragments to two sets (64 VGPRs).
+MOLT_DEV void compute(const uint16_t* __restrict__ ws, const uint16_t* __restrict__ xs, const FragOff& f,
+                      f32x16_t (&acc)[TM][TN]) {
+  bf16x8_t a[2][TM], b[2][TN];
+  load_frags(ws, xs, f, 0, a[0], b[0]);
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    if (kk < 3) load_frags(ws, xs, f, kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kk & 1][i], b[kk & 1][j], acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// ---- X side (row-major, contraction contiguous): direct global -> LDS loads.
+// global_load_lds_dwordx4 writes lane l's 16 bytes to LDS at M0 + 16 l, so
+// each wave-level load fills one contiguous 1 KB of the tile; every lane
+// fetches the global chunk whose swizzled LDS slot is its own. No VGPRs hold
+// X and no LDS store instructions are issued for it. Loads are branch-free:
+// an out-of-range row is clamped to the last valid one (such rows only reach
+// output rows the epilogue never stores).
+typedef __attribute__((address_space(1))) const void* gptr_t;
+typedef __attribute__((address_space(3))) void* lptr_t;
+
+MOLT_DEV void x_issue_lds(uint16_t* xs, const uint16_t* __restrict__ a, int64_t lda, int64_t m0, int64_t M,
+                          int64_t k0, int wave, int lane) {
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int blk = wave * 8 + c;            // 1 KB block of the 32 KB tile
+    const int pos = blk * 64 + lane;         // 16-byte slot in the tile
+    const int R = pos >> 3, slot = pos & 7;
+    const int ch = slot ^ ((R ^ (R >> 3)) & 7);
+    const int64_t m = min(m0 + R, M - 1);
+    __builtin_amdgcn_global_load_lds((gptr_t)(a + m * lda + k0 + 8 * ch), (lptr_t)(xs + blk * 512), 16, 0, 0);
+  }
+}
+
+// ---- forward W side (row-contract): 2 chunks of 16 packed bytes per thread
+MOLT_DEV void fwd_row(int R, int64_t tn, bool pair, int& which, int64_t& n) {
+  if (pair) {
+    const int sub = (R >> 5) & 3;
+    which = sub >> 1;
+    n = tn * (BN / 2) + (R >> 7) * 64 + (sub & 1) * 32 + (R & 31);
+  } else {
+    which = 0;
+    n = tn * BN + R;
+  }
+}
+
+struct WRReg { u32x4_t q[2]; float sc[2]; };
+
+MOLT_DEV void wr_issue(WRReg& w, const FwdParams& p, int64_t tn, bool pair, int64_t k0, int tid) {
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int idx = tid + NT * c;
+    const int R = idx >> 1, half = idx & 1;
+    int which; int64_t n;
+    fwd_row(R, tn, pair, which, n);
+    const int64_t flat = min(n, p.N - 1) * p.K + k0 + 32 * half;
+    w.q[c] = *reinterpret_cast<const u32x4_t*>(sel(p.packed, which) + (flat >> 1));
+    w.sc[c] = sel(p.scales, which)[flat >> 6];
+  }
+}
+
+MOLT_DEV void wr_commit(const WRReg& w, uint16_t* ws, const float2* tab, int tid) {
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int idx = tid + NT * c;
+    const int R = idx >> 1, half = idx & 1;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const uint32_t q = w.q[c][d];
+      u32x4_t o;
+      o[0] = dequant_pair(tab, q & 0xffu, w.sc[c]);
+      o[1] = dequant_pair(tab, (q >> 8) & 0xffu, w.sc[c]);
+      o[2] = dequant_pair(tab, (q >> 16) & 0xffu, w.sc[c]);
+      o[3] = dequant_pair(tab, q >> 24, w.sc[c]);
+      *reinterpret_cast<u32x4_t*>(ws + loff(R, 4 * half + d)) = o;
+    }
+  }
+}
+
+// ---- backward W side (column-contract): one 8-row x 8-column patch per thread
+struct WCReg { uint32_t q[8]; float sc[8]; };
+
+MOLT_DEV void wc_issue(WCReg& w, const BwdParams& p, int seg, int64_t tn, int64_t c0, int tid) {
+  const int cg = tid & 31, rg = tid >> 5;
+  const int64_t col = min(tn * BN + 8 * cg, p.Kw - 8);
+  const uint8_t* packed = sel(p.packed, seg);
+  const float* scales = sel(p.scales, seg);
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int64_t flat = (c0 + 8 * rg + r) * p.Kw + col;
+    w.q[r] = *reinterpret_cast<const uint32_t*>(packed + (flat >> 1));
+    w.sc[r] = scales[flat >> 6];
+  }
+}
+
+MOLT_DEV void wc_commit(const WCReg& w, uint16_t* ws, const float2* tab, int tid) {
+  const int cg = tid & 31, rg = tid >> 5;
+  float v[8][8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const float2 c = tab[(w.q[r] >> (8 * b)) & 0xffu];
+      v[r][2 * b] = c.x * w.sc[r];
+      v[r][2 * b + 1] = c.y * w.sc[r];
+    }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    u32x4_t o;
+    o[0] = pack_bf16x2(v[0][j], v[1][j]);
+    o[1] = pack_bf16x2(v[2][j], v[3][j]);
+    o[2] = pack_bf16x2(v[4][j], v[5][j]);
+    o[3] = pack_bf16x2(v[6][j], v[7][j]);
+    *reinterpret_cast<u32x4_t*>(ws + loff(8 * cg + j, rg)) = o;
+  }
+}
+
+// ---- element-wise staging for the LoRA contraction steps (swizzled layout)
+MOLT_DEV void lora_a_stage(uint16_t* xs, const uint16_t* __restrict__ t, int64_t ldt, int64_t m0, int64_t M,
+                           int64_t c0, int64_t L, int tid) {
+  for (int e = tid; e < BM * BK; e += NT) {
+    const int R = e >> 6, k = e & 63;
+    const int64_t m = m0 + R, c = c0 + k;
+    xs[loff(R, k >> 3) + (k & 7)] = (m < M && c < L) ? t[m * ldt + c] : (uint16_t)0;
+  }
+}
+
+MOLT_DEV void lora_wrow_stage(uint16_t* ws, const FwdParams& p, int64_t tn, bool pair, int64_t c0, int tid) {
+  for (int e = tid; e < BN * BK; e += NT) {
+    const int R = e >> 6, k = e & 63;
+    int which; int64_t n;
+    fwd_row(R, tn, pair, which, n);
+    const int64_t c = c0 + k - (int64_t)which * p.r;
+    uint16_t v = 0;
+    if (n < p.N && c >= 0 && c < p.r) v = bf16_bits((which ? p.s[1] : p.s[0]) * sel(p.lb, which)[n * p.ldlb + c]);
+    ws[loff(R, k >> 3) + (k & 7)] = v;
+  }
+}
+
+MOLT_DEV void lora_wcol_stage(uint16_t* ws, const BwdParams& p, int seg, int64_t tn, int64_t c0, int tid) {
+  const float* a = sel(p.la, seg);
+  for (int e = tid; e < BN * BK; e += NT) {
+    const int R = e % BN, k = e / BN;
+    const int64_t col = tn * BN + R, c = c0 + k;
+    uint16_t v = 0;
+    if (col < p.Kw && c < p.r) v = bf16_bits(p.la_scale * a[c * p.ldla + col]);
+    ws[loff(R, k >> 3) + (k & 7)] = v;
+  }
+}
+
+// ---- LDS-staged epilogues
+// acc[i][j] holds C[W row][X row]: W row = wn*128 + 32i + 8(e/4) + 4(lane/32) + e%4,
+// X row = wm*128 + 32j + lane%32. The staged tile is ep[X row][W row] in bf16.
+MOLT_DEV void stage_acc(uint16_t* ep, const f32x16_t (&acc)[TM][TN], int wm, int wn, int lane) {
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int row = wm * WCOLS + j * 32 + (lane & 31);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int col = wn * WROWS + i * 32 + 8 * g + 4 * (lane >> 5);
+        u32x2_t o = {pack_bf16x2(acc[i][j][4 * g], acc[i][j][4 * g + 1]),
+                     pack_bf16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3])};
+        *reinterpret_cast<u32x2_t*>(ep + row * EP_LD + col) = o;
+      }
+  }
+}
+
+// Pair layout: subtiles 0,1 of a wave are gate and 2,3 the up rows of the same
+// 64 intermediate columns. Staged as ep[X row][c] with c in 0..127 = gate of
+// intermediate column tn*128 + c and 128 + c = up of the same column.
+MOLT_DEV void stage_acc_pair(uint16_t* ep, const f32x16_t (&acc)[TM][TN], int wm, int wn, int lane) {
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int row = wm * WCOLS + j * 32 + (lane & 31);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int col = (i >> 1) * 128 + wn * 64 + (i & 1) * 32 + 8 * g + 4 * (lane >> 5);
+        u32x2_t o = {pack_bf16x2(acc[i][j][4 * g], acc[i][j][4 * g + 1]),
+                     pack_bf16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3])};
+        *reinterpret_cast<u32x2_t*>(ep + row * EP_LD + col) = o;
+      }
+  }
+}
+
+MOLT_DEV void gateup_store(const uint16_t* ep, const FwdParams& p, int64_t m0, int64_t tn, int tid) {
+  // 256 rows x 16 chunks of 8 intermediate columns
+  for (int q = tid; q < BM * 16; q += NT) {
+    const int row = q >> 4, ch = q & 15;
+    const int64_t m = m0 + row, n = tn * (BN / 2) + 8 * ch;
+    if (m >= p.M || n >= p.N) continue;
+    const u32x4_t gw = *reinterpret_cast<const u32x4_t*>(ep + row * EP_LD + 8 * ch);
+    const u32x4_t uw = *reinterpret_cast<const u32x4_t*>(ep + row * EP_LD + 128 + 8 * ch);
+    u32x4_t hw;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float h0 = round_bf16(silu_f32(bf16_lo(gw[e]))) * bf16_lo(uw[e]);
+      const float h1 = round_bf16(silu_f32(bf16_hi(gw[e]))) * bf16_hi(uw[e]);
+      hw[e] = pack_bf16x2(h0, h1);
+    }
+    const int64_t off = m * p.ldy + n;
+    if (p.vec_out && n + 8 <= p.N) {
+      *reinterpret_cast<u32x4_t*>(p.y[0] + off) = gw;
+      *reinterpret_cast<u32x4_t*>(p.y[1] + off) = uw;
+      *reinterpret_cast<u32x4_t*>(p.y[2] + off) = hw;
+    } else {
+      for (int e = 0; e < 8 && n + e < p.N; ++e) {
+        const int w = e >> 1, sh = (e & 1) * 16;
+        p.y[0][off + e] = (uint16_t)(gw[w] >> sh);
+        p.y[1][off + e] = (uint16_t)(uw[w] >> sh);
+        p.y[2][off + e] = (uint16_t)(hw[w] >> sh);
+      }
+    }
+  }
+}
+
+MOLT_DEV void swiglu_bwd_store(const uint16_t* ep, const BwdParams& p, int64_t m0, int64_t tn, int tid) {
+  // 256 rows x 32 chunks of 8 intermediate columns
+  for (int q = tid; q < BM * 32; q += NT) {
+    const int row = q >> 5, ch = q & 31;
+    const int64_t m = m0 + row, n = tn * BN + 8 * ch;
+    if (m >= p.M || n >= p.Kw) continue;
+    const u32x4_t dh = *reinterpret_cast<const u32x4_t*>(ep + row * EP_LD + 8 * ch);
+    const int64_t off = m * p.ldg + n;
+    u32x4_t gw, uw;
+    if (p.vec_out && n + 8 <= p.Kw) {
+      gw = *reinterpret_cast<const u32x4_t*>(p.gate + off);
+      uw = *reinterpret_cast<const u32x4_t*>(p.up + off);
+    } else {
+      uint16_t gt[8], ut[8];
+      for (int e = 0; e < 8; ++e) {
+        gt[e] = n + e < p.Kw ? p.gate[off + e] : (uint16_t)0;
+        ut[e] = n + e < p.Kw ? p.up[off + e] : (uint16_t)0;
+      }
+      gw = __builtin_bit_cast(u32x4_t, gt);
+      uw = __builtin_bit_cast(u32x4_t, ut);
+    }
+    u32x4_t dgw, duw;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float dgo[2], duo[2];
+      const float dhv[2] = {bf16_lo(dh[e]), bf16_hi(dh[e])};
+      const float gv[2] = {bf16_lo(gw[e]), bf16_hi(gw[e])};
+      const float uv[2] = {bf16_lo(uw[e]), bf16_hi(uw[e])};
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-gv[t]));
+        duo[t] = dhv[t] * round_bf16(gv[t] * sg);
+        dgo[t] = round_bf16(dhv[t] * uv[t]) * (sg * (1.0f + gv[t] * (1.0f - sg)));
+      }
+      dgw[e] = pack_bf16x2(dgo[0], dgo[1]);
+      duw[e] = pack_bf16x2(duo[0], duo[1]);
+    }
+    if (p.vec_out && n + 8 <= p.Kw) {
+      *reinterpret_cast<u32x4_t*>(p.dg + off) = dgw;
+      *reinterpret_cast<u32x4_t*>(p.du + off) = duw;
+    } else {
+      for (int e = 0; e < 8 && n + e < p.Kw; ++e) {
+        const int w = e >> 1, sh = (e & 1) * 16;
+        p.dg[off + e] = (uint16_t)(dgw[w] >> sh);
+        p.du[off + e] = (uint16_t)(duw[w] >> sh);
+      }
+    }
+  }
+}
+
+template <bool PAIR>
+__global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
+  __shared__ Smem sm;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+  const int64_t cols_per_tile = PAIR ? BN / 2 : BN;
+  const int64_t nt_m = ceil_div64(p.M, BM), nt_n = ceil_div64(p.N, cols_per_tile);
+  int64_t tm, tn;
+  grouped_tile(xcd_tile(blockIdx.x, nt_m * nt_n), nt_m, nt_n, GROUP_M, tm, tn);
+  const int64_t m0 = tm * BM;
+  build_pair_table(sm.tab, p.code, p.order);
+
+  FragOff fo;
+  frag_offsets(fo, wn * WROWS, wm * WCOLS, lane);
+  f32x16_t acc[TM][TN];
+  zero_acc(acc);
+
+  // One-deep prefetch: X of step s+1 streams straight into the other LDS
+  // buffer and the packed NF4 bytes of step s+1 into registers while the
+  // MFMAs of step s run; the bytes are then dequantised into LDS.
+  const int ks = (int)(p.K / BK);
+  WRReg wr;
+  x_issue_lds(sm.xs[0], p.x, p.ldx, m0, p.M, 0, wave, lane);
+  wr_issue(wr, p, tn, PAIR, 0, tid);
+  __syncthreads();  // pair table
+  wr_commit(wr, sm.ws[0], sm.tab, tid);
+  __syncthreads();
+  for (int s = 0; s < ks; ++s) {
+    const int cur = s & 1;
+    if (s + 1 < ks) {
+      x_issue_lds(sm.xs[cur ^ 1], p.x, p.ldx, m0, p.M, (int64_t)(s + 1) * BK, wave, lane);
+      wr_issue(wr, p, tn, PAIR, (int64_t)(s + 1) * BK, tid);
+    }
+    compute(sm.ws[cur], sm.xs[cur], fo, acc);
+    if (s + 1 < ks) wr_commit(wr, sm.ws[cur ^ 1], sm.tab, tid);
+    __syncthreads();
+  }
+  for (int64_t c0 = 0; c0 < p.lr; c0 += BK) {
+    lora_a_stage(sm.xs[0], p.t, p.ldt, m0, p.M, c0, p.lr, tid);
+    lora_wrow_stage(sm.ws[0], p, tn, PAIR, c0, tid);
+    __syncthreads();
+    compute(sm.ws[0], sm.xs[0], fo, acc);
+    __syncthreads();
+  }
+
+  if (!PAIR) {
+    const bool vec = p.vec_out != 0;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t m = m0 + wm * WCOLS + j * 32 + (lane & 31);
+      if (m >= p.M) continue;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int64_t n = tn * BN + wn * WROWS + i * 32 + 8 * g + 4 * (lane >> 5);
+          float v[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+          store4(p.y[0], p.ldy, m, n, p.N, v, vec);
+        }
+      }
+    }
+    return;
+  }
+  // Gate/up pair: stage bf16 gate (columns 0..127) and up (128..255) of the
+  // tile in LDS, then form h = bf16(bf16(silu(g)) u) cooperatively with
+  // 16-byte loads and stores.
+  // (the LoRA tail ended with a barrier, so the LDS operand buffers are free)
+  stage_acc_pair(sm.ep, acc, wm, wn, lane);
+  __syncthreads();
+  gateup_store(sm.ep, p, m0, tn, tid);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
+  __shared__ Smem sm;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+  const int64_t nt_m = ceil_div64(p.M, BM), nt_n = ceil_div64(p.Kw, BN);
+  int64_t tm, tn;
+  grouped_tile(xcd_tile(blockIdx.x, nt_m * nt_n), nt_m, nt_n, GROUP_M, tm, tn);
+  const int64_t m0 = tm * BM;
+  build_pair_table(sm.tab, p.code, p.order);
+
+  FragOff fo;
+  frag_offsets(fo, wn * WROWS, wm * WCOLS, lane);
+  f32x16_t acc[TM][TN];
+  zero_acc(acc);
+
+  const int kseg = (int)(p.Nw / BK);
+  const int ks = p.nseg * kseg;
+  WCReg wr;
+  auto issue = [&](int s, uint16_t* xs) {
+    const int seg = s / kseg;
+    const int64_t c0 = (int64_t)(s - seg * kseg) * BK;
+    x_issue_lds(xs, sel(p.dy, seg), p.lddy, m0, p.M, c0, wave, lane);
+    wc_issue(wr, p, seg, tn, c0, tid);
+  };
+  issue(0, sm.xs[0]);
+  __syncthreads();  // pair table
+  wc_commit(wr, sm.ws[0], sm.tab, tid);
+  __syncthreads();
+  for (int s = 0; s < ks; ++s) {
+    const int cur = s & 1;
+    if (s + 1 < ks) issue(s + 1, sm.xs[cur ^ 1]);
+    compute(sm.ws[cur], sm.xs[cur], fo, acc);
+    if (s + 1 < ks) wc_commit(wr, sm.ws[cur ^ 1], sm.tab, tid);
+    __syncthreads();
+  }
+  for (int seg = 0; seg < p.nseg && p.r > 0; ++seg) {
+    for (int64_t c0 = 0; c0 < p.r; c0 += BK) {
+      lora_a_stage(sm.xs[0], sel(p.u, seg), p.ldu, m0, p.M, c0, p.r, tid);
+      lora_wcol_stage(sm.ws[0], p, seg, tn, c0, tid);
+      __syncthreads();
+      compute(sm.ws[0], sm.xs[0], fo, acc);
+      __syncthreads();
+    }
+  }
+
+  if (EPI == EPI_STORE) {
+    const bool vec = p.vec_out != 0;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t m = m0 + wm * WCOLS + j * 32 + (lane & 31);
+      if (m >= p.M) continue;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int64_t n = tn * BN + wn * WROWS + i * 32 + 8 * g + 4 * (lane >> 5);
+          float v[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+          store4(p.dx, p.lddx, m, n, p.Kw, v, vec);
+        }
+      }
+    }
+    return;
+  }
+  // SwiGLU backward: stage dh = bf16(acc) of the tile in LDS, then compute
+  // dgate/dup cooperatively with 16-byte loads of gate/up and 16-byte stores.
+  stage_acc(sm.ep, acc, wm, wn, lane);
+  __syncthreads();
+  swiglu_bwd_store(sm.ep, p, m0, tn, tid);
+}
+
+}  // namespace big
+
 // ------------------------------------------------------------- host helpers
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Below this many 256 x 256 tiles the 128 x 128 kernels fill the 256 CUs
+// better. MOLT_AMD_BIG_TILE_MIN overrides the threshold (tests use it to run
+// the large-tile kernels at small shapes).
+int64_t big_tile_min() {
+  const char* e = getenv("MOLT_AMD_BIG_TILE_MIN");
+  return e ? atoll(e) : 256;
+}
 
 int check_weight_for_gemm(const molt_nf4_weight* w, const char* who) {
   MOLT_REQUIRE(w && w->packed && w->code, MOLT_EINVAL, "%s: weight, packed and code are required", who);
@@ -534,6 +1027,14 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
 
   const bool al = (p.K % 64 == 0) && p.block_size == 64 && ldx % 8 == 0 && aligned(x, 16) &&
                   aligned(w0->packed, 16) && (!pair || aligned(w1->packed, 16));
+  const int64_t big_tiles = ceil_div64(M, big::BM) * ceil_div64(p.N, pair ? big::BN / 2 : big::BN);
+  if (al && big_tiles >= big_tile_min()) {
+    MOLT_REQUIRE(big_tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
+    dim3 grid((unsigned)big_tiles), block(big::NT);
+    if (pair) hipLaunchKernelGGL((big::fwd_kernel<true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((big::fwd_kernel<false>), grid, block, 0, stream, p);
+    return check_launch(who);
+  }
   const int64_t cols_per_tile = pair ? BN / 2 : BN;
   const int64_t tiles = ceil_div64(M, BM) * ceil_div64(p.N, cols_per_tile);
   MOLT_REQUIRE(tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
@@ -595,6 +1096,15 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
   const bool al = (p.Nw % 64 == 0) && (p.Kw % 64 == 0) && p.block_size == 64 && lddy % 8 == 0 &&
                   aligned(dy0, 16) && (nseg == 1 || aligned(dy1, 16)) && aligned(w0->packed, 2) &&
                   (nseg == 1 || aligned(w1->packed, 2));
+  const int64_t big_tiles = ceil_div64(M, big::BM) * ceil_div64(p.Kw, big::BN);
+  if (al && aligned(w0->packed, 4) && (nseg == 1 || aligned(w1->packed, 4)) &&
+      big_tiles >= big_tile_min()) {
+    MOLT_REQUIRE(big_tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
+    dim3 grid((unsigned)big_tiles), block(big::NT);
+    if (swiglu) hipLaunchKernelGGL((big::bwd_kernel<EPI_SWIGLU_BWD>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((big::bwd_kernel<EPI_STORE>), grid, block, 0, stream, p);
+    return check_launch(who);
+  }
   const int64_t tiles = ceil_div64(M, BM) * ceil_div64(p.Kw, BN);
   MOLT_REQUIRE(tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
   dim3 grid((unsigned)tiles), block(NT);
