@@ -135,6 +135,52 @@ def gemv_sweep(dev, reps: int = 20):
     return out
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "gateup_fwd_cfg4_hbm_traffic.txt"
+
+
+def measured_traffic():
+    """HBM bytes per launch of the gate/up kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (each scaled by the same counter's reading
+    for a copy of known size); None when no such summary is present."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
+def profile_kernel(which: str, reps: int) -> int:
+    """Run one kernel `reps` times at cfg4 shapes, for rocprofv3 counter passes:
+    'gateup' = the fused gate/up NF4-LoRA GEMM, 'copy' = a 1 GiB device copy
+    (1 GiB read + 1 GiB written) that calibrates FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    from molt_amd import ops
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    if which == "copy":
+        src = torch.ones(2**30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(reps):
+            dst.copy_(src)
+    else:
+        H, I, r, alpha, M = 4096, 14336, 64, 128.0, 8192
+        projs, x, _dy, s = make_mlp(H, I, r, alpha, M, 1337, dev)
+        (pg, qg, ag, bg), (pu, qu, au, bu) = projs[0], projs[1]
+        import molt_amd
+        sg, su = molt_amd.resolved_nf4_scales(qg), molt_amd.resolved_nf4_scales(qu)
+        with torch.no_grad():
+            t = ops.lora_project(x.detach(), None, 0, 1.0, torch.cat([ag, au]).detach(), 0)
+            for _ in range(reps):
+                ops.nf4_gateup_forward(x.detach(), pg.reshape(-1), sg, pu.reshape(-1), su, qg.code, I, H, 1, t,
+                                       bg.detach(), bu.detach(), s, s)
+    torch.cuda.synchronize()
+    log(f"profile-kernel {which}: {reps} launches done")
+    return 0
+
+
 def cpu_baseline(seconds_budget: float = 20.0):
     """Oracle restatement of MOLT's eager CPU path on cfg1 (numpy fp32)."""
     import numpy as np
@@ -196,6 +242,9 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=8192, help="M (default: cfg4's 8 x 1024)")
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile-kernel", choices=("gateup", "copy"),
+                    help="only launch one kernel (for rocprofv3 --pmc passes) and exit")
+    ap.add_argument("--reps", type=int, default=3, help="launches for --profile-kernel")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -203,6 +252,9 @@ def main() -> int:
               "(the data-parallel sharding design is described in DESIGN.md). Run with --gpus 1.",
               file=sys.stderr)
         return 2
+
+    if args.profile_kernel:
+        return profile_kernel(args.profile_kernel, args.reps)
 
     import torch
     from molt_amd import ops
@@ -245,7 +297,8 @@ def main() -> int:
         "step_tflops": round(step_tflops, 1),
         "roofline": {"kernel": "nf4_fwd_kernel<pair> (fused gate/up NF4-LoRA GEMM)", "bound": "mfma",
                      "achieved": round(k_tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(k_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(k_tflops / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(),
+                     "traffic_unit": "bytes/launch (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)",
                      "avg_launch_ms": round(k_ms, 4), "launches": len(pairs),
                      "flop_per_launch": k_flop},
     }

@@ -105,17 +105,21 @@ int molt_nf4_double_quantize(const float* absmax, int64_t n, int32_t dq_block,
 /* NF4 + LoRA linear                                                         */
 /* ------------------------------------------------------------------------ */
 
-/* Low-rank projection out[M, r] = bf16( sum_d z(m, d) * bf16(lora[q, d]) ).
+/* Low-rank projection out[M, r] = bf16( sum_d z(m, d) * bf16(lora[q, d]) ), r <= 128.
  *  z_mode 0: z = Z (bf16 [M, D], row stride ldz);
  *  z_mode 1: z = bf16(bf16(silu(Z)) * Z2) (SwiGLU replay; Z = gate, Z2 = up);
  *  z_mode 2: z = bf16(Z * z_scale)     (scale-before-matmul, methods/nf4_lora.py:87-90).
  *  lora_layout 0: lora is [r, D] (LoRA A); 1: lora is [D, r] (LoRA B).
  * Replaces the rank-r GEMMs F.linear(x, lora_a) (methods/nf4_lora.py:49) and
- * scaled_grad @ lora_b (methods/nf4_lora.py:89-90). */
+ * scaled_grad @ lora_b (methods/nf4_lora.py:89-90). The adapter is first
+ * converted to bf16 into the caller's workspace (16-byte aligned, at least
+ * molt_lora_project_workspace(D, r) bytes), so concurrent calls need
+ * separate workspaces. */
+size_t molt_lora_project_workspace(int64_t D, int32_t r);
 int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t ldz, int32_t z_mode,
                       float z_scale, int64_t M, int64_t D, const float* lora,
                       int32_t lora_layout, int32_t r, uint16_t* out, int64_t ldo,
-                      void* stream);
+                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* Y[M, N] = bf16( X . deq(W)^T + T . bf16(s * B)^T ), fp32 accumulation, with
  * X bf16 [M, K], T bf16 [M, r] = molt_lora_project(X, lora_a) and B fp32 [N, r]

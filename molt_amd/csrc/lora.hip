@@ -1,5 +1,6 @@
-// Rank-r LoRA kernels (gfx950): the low-rank projection T = z . bf16(A)^T and
-// the adapter gradients dA = U^T X, dB = s dY^T T.
+// Rank-r LoRA kernels (gfx950): the low-rank projection T = z . bf16(W)^T and
+// the adapter gradients dA = U^T X, dB = s dY^T T. Both stream one large
+// [M, D] activation from HBM once; the rank-r side is small and L2-resident.
 #include "mfma_core.h"
 
 namespace molt {
@@ -14,211 +15,293 @@ MOLT_DEV float ztrans(float a, float b, int mode, float s) {
   return a;
 }
 
-// ------------------------------------------------------------------------
-// Projection out[M, R] = bf16(sum_d z(m, d) * bf16(W(q, d))).
-// Workgroup = 4 waves over one 32-row slab of z and 64 outputs q; wave w
-// takes every 4th 64-wide contraction step and the four partial tiles are
-// summed in wave order through LDS (deterministic). Operands go straight
-// from global memory to MFMA registers: lane half h covers contraction
-// [d0 + 32h, +32), split across the four 16-deep MFMA sub-steps.
-// ------------------------------------------------------------------------
-constexpr int PJ_M = 32, PJ_Q = 64, PJ_WAVES = 4;
-
-struct ProjParams {
-  const uint16_t* z; const uint16_t* z2; int64_t ldz; int mode; float zs;
-  int64_t M, D;
-  const float* w; int layout; int R;     // layout 0: W(q,d) = w[q*D + d]; 1: w[d*R + q]
-  uint16_t* out; int64_t ldo;
-  int vec;                               // z rows 16-byte loadable
+// Eight consecutive bf16 elements of one row of a [rows, C] operand (and of
+// the up tensor for the SwiGLU replay), as loaded. With VEC (rows 16-byte
+// aligned, C % 8 == 0) they are one 16-byte load from a clamped address, and
+// the transform and the zero mask outside the matrix are applied only when
+// the chunk is consumed, so the load stays in flight until then. Without VEC
+// the elements are loaded one by one and transformed at once.
+struct Chunk {
+  u32x4_t a, b;
+  bool ok;
 };
 
-MOLT_DEV bf16x8_t load_z8(const ProjParams& p, int64_t m, int64_t d) {
-  float v[8];
-  if (m < p.M && p.vec && d + 8 <= p.D) {
-    const u32x4_t a = *reinterpret_cast<const u32x4_t*>(p.z + m * p.ldz + d);
-    u32x4_t b = {0u, 0u, 0u, 0u};
-    if (p.mode == 1) b = *reinterpret_cast<const u32x4_t*>(p.z2 + m * p.ldz + d);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[2 * e] = ztrans(bf16_lo(a[e]), bf16_lo(b[e]), p.mode, p.zs);
-      v[2 * e + 1] = ztrans(bf16_hi(a[e]), bf16_hi(b[e]), p.mode, p.zs);
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float x = 0.0f;
-      if (m < p.M && d + e < p.D) {
-        const float a = bf16_to_f32(p.z[m * p.ldz + d + e]);
-        const float b = p.mode == 1 ? bf16_to_f32(p.z2[m * p.ldz + d + e]) : 0.0f;
-        x = ztrans(a, b, p.mode, p.zs);
-      }
-      v[e] = x;
-    }
+template <bool VEC, bool REPLAY>
+MOLT_DEV void chunk_load(Chunk& c, const uint16_t* __restrict__ z, const uint16_t* __restrict__ z2, int64_t ld,
+                         int mode, float s, int64_t m, int64_t rows, int64_t col, int64_t C) {
+  if (VEC) {
+    c.ok = m < rows && col < C;
+    const int64_t off = c.ok ? m * ld + col : 0;
+    c.a = *reinterpret_cast<const u32x4_t*>(z + off);
+    if (REPLAY) c.b = *reinterpret_cast<const u32x4_t*>(z2 + off);
+    return;
   }
-  u32x4_t o;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
-  return __builtin_bit_cast(bf16x8_t, o);
-}
-
-MOLT_DEV bf16x8_t load_w8(const ProjParams& p, int64_t q, int64_t d) {
   float v[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     float x = 0.0f;
-    if (q < p.R && d + e < p.D) x = p.layout == 0 ? p.w[q * p.D + d + e] : p.w[(d + e) * p.R + q];
+    if (m < rows && col + e < C) {
+      const float a = bf16_to_f32(z[m * ld + col + e]);
+      const float b = mode == 1 ? bf16_to_f32(z2[m * ld + col + e]) : 0.0f;
+      x = ztrans(a, b, mode, s);
+    }
     v[e] = x;
   }
-  u32x4_t o;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
-  return __builtin_bit_cast(bf16x8_t, o);
+  for (int e = 0; e < 4; ++e) c.a[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+  c.ok = true;
 }
 
-__global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_kernel(const ProjParams p) {
-  __shared__ float red[PJ_WAVES - 1][2][16][64];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t m0 = (int64_t)blockIdx.x * PJ_M;
-  const int64_t q0 = (int64_t)blockIdx.y * PJ_Q;
-  const int r = lane & 31, h = lane >> 5;
-  const int64_t steps = ceil_div64(p.D, BK);
-
-  f32x16_t acc[2];
+template <bool VEC, bool REPLAY>
+MOLT_DEV u32x4_t chunk_value(const Chunk& c, int mode, float s) {
+  if (!VEC) return c.a;
+  u32x4_t o = c.a;
+  if (REPLAY || mode == 2) {
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[t][e] = 0.0f;
-
-  for (int64_t s = wave; s < steps; s += PJ_WAVES) {
-    const int64_t d0 = s * BK + 32 * h;
-    bf16x8_t zf[4], wf[2][4];
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      zf[kk] = load_z8(p, m0 + r, d0 + 8 * kk);
-#pragma unroll
-      for (int t = 0; t < 2; ++t) wf[t][kk] = load_w8(p, q0 + t * 32 + r, d0 + 8 * kk);
+    for (int e = 0; e < 4; ++e) {
+      const float lo = REPLAY ? ztrans(bf16_lo(c.a[e]), bf16_lo(c.b[e]), 1, s) : bf16_lo(c.a[e]) * s;
+      const float hi = REPLAY ? ztrans(bf16_hi(c.a[e]), bf16_hi(c.b[e]), 1, s) : bf16_hi(c.a[e]) * s;
+      o[e] = pack_bf16x2(lo, hi);
     }
+  }
+  const uint32_t keep = c.ok ? 0xffffffffu : 0u;
+  return o & keep;
+}
+
+// ------------------------------------------------------------------------
+// Projection out[M, R] = bf16(sum_d z(m, d) * bf16(W(q, d))).
+//
+// The adapter matrix is first packed to bf16 in MFMA fragment order:
+// fragment (step, t, kk), lane l holds W(q = 32 t + l % 32, d) for the 8
+// consecutive d = 64 step + 32 (l / 32) + 8 kk + e, so every fragment load is
+// one coalesced 1 KB read (the packed matrix stays in L2). A workgroup owns
+// 32 MT rows of z and all R outputs; each wave applies a W fragment to its MT
+// 32-row z tiles. The 8 waves take every 8th 64-deep step, with the next
+// step's z and W fragments in flight while the current step's MFMAs run, and
+// their partial tiles are summed in wave order through LDS.
+// ------------------------------------------------------------------------
+constexpr int PJ_WAVES = 8, PJ_TQ_MAX = 4;
+
+__global__ void lora_pack_kernel(const float* __restrict__ w, int layout, int R, int64_t D, int tq,
+                                 int64_t steps, uint16_t* __restrict__ wp) {
+  const int64_t total = steps * tq * 4 * 64;
+  for (int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; f < total;
+       f += (int64_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(f & 63);
+    const int64_t rest = f >> 6;
+    const int kk = (int)(rest & 3);
+    const int64_t st = rest >> 2;
+    const int t = (int)(st % tq);
+    const int64_t step = st / tq;
+    const int q = 32 * t + (lane & 31);
+    const int64_t d0 = 64 * step + 32 * (lane >> 5) + 8 * kk;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t d = d0 + e;
+      v[e] = (q < R && d < D) ? (layout == 0 ? w[(int64_t)q * D + d] : w[d * R + q]) : 0.0f;
+    }
+    u32x4_t o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+    *reinterpret_cast<u32x4_t*>(wp + f * 8) = o;
+  }
+}
+
+struct ProjParams {
+  const uint16_t* z; const uint16_t* z2; int64_t ldz; int mode; float zs;
+  int64_t M, D; int R;
+  const uint16_t* wp;
+  uint16_t* out; int64_t ldo;
+};
+
+template <int MT, bool VEC, bool REPLAY>
+MOLT_DEV void proj_load_z(Chunk (&z)[MT][4], const ProjParams& p, int64_t s, int64_t m0, int lane) {
+  const int h = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
+      chunk_load<VEC, REPLAY>(z[i][kk], p.z, p.z2, p.ldz, p.mode, p.zs, m0 + 32 * i + (lane & 31), p.M,
+                              s * BK + 32 * h + 8 * kk, p.D);
+}
+
+template <int TQ>
+MOLT_DEV void proj_load_w(u32x4_t (&w)[TQ][4], const ProjParams& p, int64_t s, int lane) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[t][kk], zf[kk], acc[t], 0, 0, 0);
+  for (int t = 0; t < TQ; ++t)
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      w[t][kk] = *reinterpret_cast<const u32x4_t*>(p.wp + (((s * TQ + t) * 4 + kk) * 64 + lane) * 8);
+}
+
+template <int TQ, int MT, bool VEC, bool REPLAY>
+MOLT_DEV void proj_mfma(const Chunk (&z)[MT][4], const u32x4_t (&w)[TQ][4], const ProjParams& p,
+                        f32x16_t (&acc)[MT][TQ]) {
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const bf16x8_t zv = __builtin_bit_cast(bf16x8_t, chunk_value<VEC, REPLAY>(z[i][kk], p.mode, p.zs));
+#pragma unroll
+      for (int t = 0; t < TQ; ++t)
+        acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, w[t][kk]), zv,
+                                                            acc[i][t], 0, 0, 0);
+    }
+}
+
+template <int TQ, int MT, bool VEC, bool REPLAY>
+__global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_kernel(const ProjParams p) {
+  __shared__ f32x16_t red[PJ_WAVES - 1][64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t m0 = (int64_t)blockIdx.x * (32 * MT);
+  const int64_t steps = ceil_div64(p.D, BK);
+
+  f32x16_t acc[MT][TQ];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int t = 0; t < TQ; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][t][e] = 0.0f;
+
+  // Two z fragment sets alternate, so each step's activation loads (from HBM)
+  // are issued a step ahead; the step's adapter fragments (L2 hits) are
+  // issued just before them. Loads are never skipped (past the end they
+  // repeat the last step), so the wait before each MFMA batch is a fixed count.
+  if (wave < steps) {
+    Chunk za[MT][4], zb[MT][4];
+    u32x4_t w[TQ][4];
+    int64_t s = wave;
+    proj_load_z<MT, VEC, REPLAY>(za, p, s, m0, lane);
+    for (;;) {
+      proj_load_w<TQ>(w, p, s, lane);
+      proj_load_z<MT, VEC, REPLAY>(zb, p, s + PJ_WAVES < steps ? s + PJ_WAVES : steps - 1, m0, lane);
+      proj_mfma<TQ, MT, VEC, REPLAY>(za, w, p, acc);
+      s += PJ_WAVES;
+      if (s >= steps) break;
+      proj_load_w<TQ>(w, p, s, lane);
+      proj_load_z<MT, VEC, REPLAY>(za, p, s + PJ_WAVES < steps ? s + PJ_WAVES : steps - 1, m0, lane);
+      proj_mfma<TQ, MT, VEC, REPLAY>(zb, w, p, acc);
+      s += PJ_WAVES;
+      if (s >= steps) break;
+    }
   }
 
-  if (wave > 0) {
+  // Partial tiles are summed in wave order, one (i, t) tile at a time.
+  const int h = lane >> 5;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+  for (int i = 0; i < MT; ++i)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) red[wave - 1][t][e][lane] = acc[t][e];
-  }
-  __syncthreads();
-  if (wave != 0) return;
+    for (int t = 0; t < TQ; ++t) {
+      if (wave > 0) red[wave - 1][lane] = acc[i][t];
+      __syncthreads();
+      if (wave == 0) {
+        f32x16_t v = acc[i][t];
 #pragma unroll
-  for (int w = 0; w < PJ_WAVES - 1; ++w)
+        for (int w = 0; w < PJ_WAVES - 1; ++w) v += red[w][lane];
+        // v is C[q][m]: column m = lane % 32, rows q = 32 t + 8 (e/4) + 4 h + e%4.
+        const int64_t m = m0 + 32 * i + (lane & 31);
+        if (m < p.M) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[t][e] += red[w][t][e][lane];
-
-  // acc[t] is C[q][m]: column m = lane % 32, rows q = 8(e/4) + 4h + e%4.
-  const int64_t m = m0 + r;
-  if (m >= p.M) return;
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int64_t q = q0 + t * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-      if (q < p.R) p.out[m * p.ldo + q] = bf16_bits(acc[t][e]);
+          for (int e = 0; e < 16; ++e) {
+            const int q = 32 * t + 8 * (e >> 2) + 4 * h + (e & 3);
+            if (q < p.R) p.out[m * p.ldo + q] = bf16_bits(v[e]);
+          }
+        }
+      }
+      __syncthreads();
     }
 }
 
 // ------------------------------------------------------------------------
-// Gradient partials: part[s][p][q] = sum over the s-th slice of M of
-// L(m, p) * R(m, q). Both operands are staged into LDS transposed (the
-// contraction index m contiguous) from 8-row x 4-column register patches.
+// Gradient partials part[s][p][q] = sum over the s-th slice of M of
+// L(m, p) R(m, q). Both operands are loaded as 8 x 8 patches (8 rows of M,
+// 16 bytes each) and transposed in registers (v_perm) so that M, the
+// contraction index, is contiguous in LDS. One-deep register prefetch with
+// double-buffered LDS; the splits are summed in split order afterwards.
 // ------------------------------------------------------------------------
-constexpr int GR_P = 128, GR_Q = 64;
-constexpr int GR_NT = 256;
+constexpr int GR_P = 128, GR_Q = 64, GR_NT = 256;
 constexpr int GR_WROWS = 64, GR_WCOLS = 32;   // waves 2 (p) x 2 (q)
 
 struct GradParams {
   const uint16_t* l; const uint16_t* l2; int64_t ldl; int mode;
   const uint16_t* rm; int64_t ldr;
   int64_t M, P, Q;
-  int64_t slice;             // rows of M per split (multiple of BK)
-  float* part;               // [S][P][Q]
-  int vec;                   // 8-byte patch loads allowed
+  int64_t slice;
+  float* part;
 };
 
-MOLT_DEV void load_patch4(const uint16_t* __restrict__ src, const uint16_t* __restrict__ src2,
-                          int mode, int64_t ld, int64_t m, int64_t c, int64_t M, int64_t C,
-                          bool vec, float* v) {
-  if (m < M && vec && c + 4 <= C) {
-    const u32x2_t a = *reinterpret_cast<const u32x2_t*>(src + m * ld + c);
-    float x[4] = {bf16_lo(a[0]), bf16_hi(a[0]), bf16_lo(a[1]), bf16_hi(a[1])};
-    if (mode == 1) {
-      const u32x2_t b = *reinterpret_cast<const u32x2_t*>(src2 + m * ld + c);
-      float y[4] = {bf16_lo(b[0]), bf16_hi(b[0]), bf16_lo(b[1]), bf16_hi(b[1])};
+struct Patch { Chunk v[8]; };
+
+// Which operand and patch a thread stages: waves 0-1 stage the 8 x 16 L
+// patches of a 64 x 128 tile, wave 2 the 8 x 8 R patches of a 64 x 64 tile,
+// wave 3 none. Within a patch group, mg (the 8-row group) varies fastest so
+// the transposed 16-byte LDS stores of neighbouring lanes land in one row.
+MOLT_DEV bool patch_role(int wave, int lane, bool& is_l, int& mg, int& cg) {
+  mg = lane & 7;
+  cg = (lane >> 3) + (wave == 1 ? 8 : 0);
+  is_l = wave < 2;
+  return wave < 3;
+}
+
+template <bool VEC, bool REPLAY>
+MOLT_DEV void patch_load(Patch& pt, const GradParams& p, int wave, int lane, int64_t m0, int64_t mend,
+                         int64_t p0, int64_t q0) {
+  bool is_l; int mg, cg;
+  if (!patch_role(wave, lane, is_l, mg, cg)) return;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) x[e] = round_bf16(round_bf16(silu_f32(x[e])) * y[e]);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = x[e];
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float x = 0.0f;
-      if (m < M && c + e < C) {
-        x = bf16_to_f32(src[m * ld + c + e]);
-        if (mode == 1) x = round_bf16(round_bf16(silu_f32(x)) * bf16_to_f32(src2[m * ld + c + e]));
-      }
-      v[e] = x;
-    }
+  for (int r = 0; r < 8; ++r) {
+    const int64_t m = m0 + 8 * mg + r;
+    if (is_l) chunk_load<VEC, REPLAY>(pt.v[r], p.l, p.l2, p.ldl, p.mode, 1.0f, m, mend, p0 + 8 * cg, p.P);
+    else chunk_load<VEC, false>(pt.v[r], p.rm, nullptr, p.ldr, 0, 1.0f, m, mend, q0 + 8 * cg, p.Q);
   }
 }
 
-// Stage a (8*8 rows of M) x (4*CGS columns) tile transposed into LDS rows.
-template <int CGS>
-MOLT_DEV void stage_t(uint16_t* dst, const uint16_t* src, const uint16_t* src2, int mode, int64_t ld,
-                      int64_t m0, int64_t c0, int64_t M, int64_t mend, int64_t C, bool vec, int tid) {
-  if (tid >= CGS * 8) return;
-  const int cg = tid % CGS, rg = tid / CGS;
-  float v[8][4];
+template <bool VEC, bool REPLAY>
+MOLT_DEV void patch_store(const Patch& pt, const GradParams& p, uint16_t* ls, uint16_t* rs, int wave, int lane) {
+  bool is_l; int mg, cg;
+  if (!patch_role(wave, lane, is_l, mg, cg)) return;
+  u32x4_t v[8];
 #pragma unroll
-  for (int rr = 0; rr < 8; ++rr) {
-    const int64_t m = m0 + 8 * rg + rr;
-    load_patch4(src, src2, mode, ld, m, c0 + 4 * cg, m < mend ? M : 0, C, vec, v[rr]);
-  }
+  for (int r = 0; r < 8; ++r)
+    v[r] = is_l ? chunk_value<VEC, REPLAY>(pt.v[r], p.mode, 1.0f) : chunk_value<VEC, false>(pt.v[r], 0, 1.0f);
+  uint16_t* dst = is_l ? ls : rs;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int c = 0; c < 8; ++c) {
+    const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
     u32x4_t o;
-    o[0] = pack_bf16x2(v[0][j], v[1][j]);
-    o[1] = pack_bf16x2(v[2][j], v[3][j]);
-    o[2] = pack_bf16x2(v[4][j], v[5][j]);
-    o[3] = pack_bf16x2(v[6][j], v[7][j]);
-    *reinterpret_cast<u32x4_t*>(dst + (4 * cg + j) * LDSW + 8 * rg) = o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = __builtin_amdgcn_perm(v[2 * k + 1][c >> 1], v[2 * k][c >> 1], sel);
+    *reinterpret_cast<u32x4_t*>(dst + (8 * cg + c) * LDSW + 8 * mg) = o;
   }
 }
 
+template <bool VEC, bool REPLAY>
 __global__ __launch_bounds__(GR_NT) void lora_grad_kernel(const GradParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t ls[GR_P * LDSW];
-  __shared__ __attribute__((aligned(16))) uint16_t rs[GR_Q * LDSW];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ __attribute__((aligned(16))) uint16_t ls[2][GR_P * LDSW];
+  __shared__ __attribute__((aligned(16))) uint16_t rs[2][GR_Q * LDSW];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wp = wave & 1, wq = wave >> 1;
   const int64_t p0 = (int64_t)blockIdx.x * GR_P;
   const int64_t q0 = (int64_t)blockIdx.y * GR_Q;
   const int64_t mbeg = (int64_t)blockIdx.z * p.slice;
-  int64_t mend = mbeg + p.slice;
-  if (mend > p.M) mend = p.M;
-  const bool vec = p.vec != 0;
+  const int64_t mend = mbeg + p.slice < p.M ? mbeg + p.slice : p.M;
+  const int steps = (int)ceil_div64(mend - mbeg, BK);
 
   f32x16_t acc[2][1];
   zero_acc(acc);
-  for (int64_t m0 = mbeg; m0 < mend; m0 += BK) {
-    stage_t<GR_P / 4>(ls, p.l, p.l2, p.mode, p.ldl, m0, p0, p.M, mend, p.P, vec, tid);
-    stage_t<GR_Q / 4>(rs, p.rm, nullptr, 0, p.ldr, m0, q0, p.M, mend, p.Q, vec, tid);
-    __syncthreads();
-    mfma_step<2, 1>(ls, rs, wp * GR_WROWS, wq * GR_WCOLS, acc, lane);
+  Patch pt;
+  patch_load<VEC, REPLAY>(pt, p, wave, lane, mbeg, mend, p0, q0);
+  patch_store<VEC, REPLAY>(pt, p, ls[0], rs[0], wave, lane);
+  __syncthreads();
+  for (int s = 0; s < steps; ++s) {
+    const int cur = s & 1;
+    if (s + 1 < steps) patch_load<VEC, REPLAY>(pt, p, wave, lane, mbeg + (int64_t)(s + 1) * BK, mend, p0, q0);
+    mfma_step<2, 1>(ls[cur], rs[cur], wp * GR_WROWS, wq * GR_WCOLS, acc, lane);
+    if (s + 1 < steps) patch_store<VEC, REPLAY>(pt, p, ls[cur ^ 1], rs[cur ^ 1], wave, lane);
     __syncthreads();
   }
 
@@ -233,6 +316,11 @@ __global__ __launch_bounds__(GR_NT) void lora_grad_kernel(const GradParams p) {
       const int64_t pp = p0 + wp * GR_WROWS + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
       if (pp < p.P) out[pp * p.Q + q] = acc[i][0][e];
     }
+}
+
+__global__ void zero_fill_kernel(float* __restrict__ out, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    out[i] = 0.0f;
 }
 
 __global__ void lora_grad_reduce_kernel(const float* __restrict__ part, int S, int64_t P, int64_t Q,
@@ -259,29 +347,79 @@ int grad_splits(int64_t M, int64_t P, int64_t Q) {
   return (int)s;
 }
 
+int64_t proj_tq(int r) { return (r + 31) / 32; }
+
 }  // namespace
 }  // namespace molt
 
 using namespace molt;
 
-extern "C" int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t ldz, int32_t z_mode,
-                                 float z_scale, int64_t M, int64_t D, const float* lora,
-                                 int32_t lora_layout, int32_t r, uint16_t* out, int64_t ldo,
+extern "C" size_t molt_lora_project_workspace(int64_t D, int32_t r) {
+  if (D <= 0 || r <= 0) return 0;
+  return (size_t)ceil_div64(D, BK) * (size_t)proj_tq(r) * 4 * 64 * 8 * sizeof(uint16_t);
+}
+
+extern "C" int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t ldz, int32_t z_mode, float z_scale,
+                                 int64_t M, int64_t D, const float* lora, int32_t lora_layout, int32_t r,
+                                 uint16_t* out, int64_t ldo, void* workspace, size_t workspace_bytes,
                                  void* stream) {
   const char* who = "molt_lora_project";
   MOLT_REQUIRE(z_mode >= 0 && z_mode <= 2, MOLT_EINVAL, "%s: bad z_mode %d", who, z_mode);
   MOLT_REQUIRE(lora_layout == 0 || lora_layout == 1, MOLT_EINVAL, "%s: bad lora_layout", who);
-  MOLT_REQUIRE(M >= 0 && D > 0 && r > 0 && r <= 1024, MOLT_EINVAL, "%s: bad shape M=%lld D=%lld r=%d", who,
-               (long long)M, (long long)D, r);
+  MOLT_REQUIRE(M >= 0 && D > 0 && r > 0, MOLT_EINVAL, "%s: bad shape M=%lld D=%lld r=%d", who, (long long)M,
+               (long long)D, r);
+  MOLT_REQUIRE(r <= 32 * PJ_TQ_MAX, MOLT_EUNSUPPORTED, "%s: rank %d > %d", who, r, 32 * PJ_TQ_MAX);
+  if (M == 0) return MOLT_OK;
   MOLT_REQUIRE(z && lora && out && ldz >= D && ldo >= r, MOLT_EINVAL, "%s: bad pointers/strides", who);
   MOLT_REQUIRE(z_mode != 1 || z2, MOLT_EINVAL, "%s: SwiGLU replay needs the up tensor", who);
-  if (M == 0) return MOLT_OK;
+  const size_t need = molt_lora_project_workspace(D, r);
+  MOLT_REQUIRE(workspace && workspace_bytes >= need && aligned(workspace, 16), MOLT_EWORKSPACE,
+               "%s: workspace %zu < %zu bytes (or not 16-byte aligned)", who, workspace_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  const int tq = (int)proj_tq(r);
+  const int64_t steps = ceil_div64(D, BK);
+  const int64_t frags = steps * tq * 4 * 64;
+  unsigned pblocks = (unsigned)((frags + 255) / 256);
+  if (pblocks > 4096) pblocks = 4096;
+  uint16_t* wp = (uint16_t*)workspace;
+  hipLaunchKernelGGL(lora_pack_kernel, dim3(pblocks), dim3(256), 0, st, lora, lora_layout, r, D, tq, steps, wp);
+  int rc = check_launch(who);
+  if (rc) return rc;
   ProjParams p{};
   p.z = z; p.z2 = z2; p.ldz = ldz; p.mode = z_mode; p.zs = z_scale;
-  p.M = M; p.D = D; p.w = lora; p.layout = lora_layout; p.R = r; p.out = out; p.ldo = ldo;
-  p.vec = ldz % 8 == 0 && aligned(z, 16) && (z_mode != 1 || aligned(z2, 16));
-  dim3 grid((unsigned)ceil_div64(M, PJ_M), (unsigned)ceil_div64(r, PJ_Q));
-  hipLaunchKernelGGL(lora_project_kernel, grid, dim3(64 * PJ_WAVES), 0, (hipStream_t)stream, p);
+  p.M = M; p.D = D; p.R = r; p.wp = wp; p.out = out; p.ldo = ldo;
+  const bool vec = D % 8 == 0 && ldz % 8 == 0 && aligned(z, 16) && (z_mode != 1 || aligned(z2, 16));
+  // Two 32-row tiles per workgroup halve the L2 reads of the packed adapter,
+  // once that still leaves a workgroup for every CU (ranks <= 64 only: the
+  // larger accumulator sets would not fit in registers).
+  const int mt = (vec && z_mode != 1 && M >= 64 * 256 && tq <= 2) ? 2 : 1;
+  dim3 grid((unsigned)ceil_div64(M, 32 * mt)), block(64 * PJ_WAVES);
+#define MOLT_PJ(TQ, MT, VEC, REPLAY) hipLaunchKernelGGL((lora_project_kernel<TQ, MT, VEC, REPLAY>), grid, block, 0, st, p)
+  if (!vec) {
+    switch (tq) {
+      case 1: MOLT_PJ(1, 1, false, false); break;
+      case 2: MOLT_PJ(2, 1, false, false); break;
+      case 3: MOLT_PJ(3, 1, false, false); break;
+      default: MOLT_PJ(4, 1, false, false); break;
+    }
+  } else if (z_mode == 1) {
+    switch (tq) {
+      case 1: MOLT_PJ(1, 1, true, true); break;
+      case 2: MOLT_PJ(2, 1, true, true); break;
+      case 3: MOLT_PJ(3, 1, true, true); break;
+      default: MOLT_PJ(4, 1, true, true); break;
+    }
+  } else {
+    switch (tq * 2 + mt - 1) {
+      case 2: MOLT_PJ(1, 1, true, false); break;
+      case 3: MOLT_PJ(1, 2, true, false); break;
+      case 4: MOLT_PJ(2, 1, true, false); break;
+      case 5: MOLT_PJ(2, 2, true, false); break;
+      case 6: MOLT_PJ(3, 1, true, false); break;
+      default: MOLT_PJ(4, 1, true, false); break;
+    }
+  }
+#undef MOLT_PJ
   return check_launch(who);
 }
 
@@ -291,20 +429,25 @@ extern "C" size_t molt_lora_grad_workspace(int64_t M, int64_t P, int64_t Q) {
 }
 
 extern "C" int molt_lora_grad(const uint16_t* l, const uint16_t* l2, int64_t ldl, int32_t l_mode,
-                              const uint16_t* rmat, int64_t ldr, int64_t M, int64_t P, int64_t Q,
-                              float scale, float* out, int32_t out_layout, void* workspace,
-                              size_t workspace_bytes, void* stream) {
+                              const uint16_t* rmat, int64_t ldr, int64_t M, int64_t P, int64_t Q, float scale,
+                              float* out, int32_t out_layout, void* workspace, size_t workspace_bytes,
+                              void* stream) {
   const char* who = "molt_lora_grad";
   MOLT_REQUIRE(l_mode == 0 || l_mode == 1, MOLT_EINVAL, "%s: bad l_mode", who);
   MOLT_REQUIRE(out_layout == 0 || out_layout == 1, MOLT_EINVAL, "%s: bad out_layout", who);
   MOLT_REQUIRE(M >= 0 && P > 0 && Q > 0, MOLT_EINVAL, "%s: bad shape", who);
-  MOLT_REQUIRE(l && rmat && out && ldl >= P && ldr >= Q, MOLT_EINVAL, "%s: bad pointers/strides", who);
-  MOLT_REQUIRE(l_mode == 0 || l2, MOLT_EINVAL, "%s: SwiGLU replay needs the up tensor", who);
+  MOLT_REQUIRE(out && ldl >= P && ldr >= Q, MOLT_EINVAL, "%s: bad pointers/strides", who);
   hipStream_t st = (hipStream_t)stream;
-  if (M == 0) {
-    MOLT_REQUIRE(hipMemsetAsync(out, 0, (size_t)P * Q * sizeof(float), st) == hipSuccess, MOLT_ELAUNCH,
-                 "%s: memset failed", who);
-    return MOLT_OK;
+  if (M != 0) {
+    MOLT_REQUIRE(l && rmat, MOLT_EINVAL, "%s: null operand", who);
+    MOLT_REQUIRE(l_mode == 0 || l2, MOLT_EINVAL, "%s: SwiGLU replay needs the up tensor", who);
+  } else {
+    // A fill kernel rather than hipMemsetAsync, so that the call stays
+    // correct when a caller captures it into a HIP graph.
+    const int64_t n = P * Q;
+    const unsigned blocks = (unsigned)(n / 256 + 1 < 4096 ? n / 256 + 1 : 4096);
+    hipLaunchKernelGGL(zero_fill_kernel, dim3(blocks), dim3(256), 0, st, out, n);
+    return check_launch(who);
   }
   const int S = grad_splits(M, P, Q);
   const size_t need = (size_t)S * P * Q * sizeof(float);
@@ -315,16 +458,19 @@ extern "C" int molt_lora_grad(const uint16_t* l, const uint16_t* l2, int64_t ldl
   p.M = M; p.P = P; p.Q = Q;
   p.slice = ceil_div64(ceil_div64(M, S), BK) * BK;
   p.part = (float*)workspace;
-  p.vec = ldl % 4 == 0 && ldr % 4 == 0 && aligned(l, 8) && aligned(rmat, 8) && (l_mode == 0 || aligned(l2, 8));
+  const bool vec = P % 8 == 0 && Q % 8 == 0 && ldl % 8 == 0 && ldr % 8 == 0 && aligned(l, 16) &&
+                   aligned(rmat, 16) && (l_mode == 0 || aligned(l2, 16));
   const int S_eff = (int)ceil_div64(M, p.slice);
   dim3 grid((unsigned)ceil_div64(P, GR_P), (unsigned)ceil_div64(Q, GR_Q), (unsigned)S_eff);
-  hipLaunchKernelGGL(lora_grad_kernel, grid, dim3(GR_NT), 0, st, p);
+  if (!vec) hipLaunchKernelGGL((lora_grad_kernel<false, false>), grid, dim3(GR_NT), 0, st, p);
+  else if (l_mode == 1) hipLaunchKernelGGL((lora_grad_kernel<true, true>), grid, dim3(GR_NT), 0, st, p);
+  else hipLaunchKernelGGL((lora_grad_kernel<true, false>), grid, dim3(GR_NT), 0, st, p);
   int rc = check_launch(who);
   if (rc) return rc;
   const int64_t n = P * Q;
   unsigned blocks = (unsigned)((n + 255) / 256);
   if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(lora_grad_reduce_kernel, dim3(blocks), dim3(256), 0, st, p.part, S_eff, P, Q, scale,
-                     out, out_layout);
+  hipLaunchKernelGGL(lora_grad_reduce_kernel, dim3(blocks), dim3(256), 0, st, p.part, S_eff, P, Q, scale, out,
+                     out_layout);
   return check_launch(who);
 }

@@ -1,0 +1,94 @@
+"""The rank-r LoRA kernels on their own: the projection T = z . bf16(W)^T
+(plain, SwiGLU-replayed and pre-scaled activations, both adapter layouts) and
+the adapter gradients scale * L^T R, against fp64 products of the same bf16
+operands. Shapes cover row, depth and rank tails, unaligned widths (the
+element-wise load path), every rank tile count up to 128, the two-tile row
+blocking of long inputs and the split-M reduction."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import nf4_oracle as O
+from tests._util import assert_close_fro, bf16_values, np_f32, seeded, uniform
+
+import molt_amd
+from molt_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _effective(z, z2, mode, scale):
+    """The activation the kernels contract, in fp64: z, bf16(bf16(silu(z)) z2) or bf16(scale z)."""
+    a = bf16_values(z)
+    if mode == 1:
+        b = bf16_values(z2)
+        return O.bf16_round(O.bf16_round(a / (1.0 + np.exp(-a))) * b).astype(np.float64)
+    if mode == 2:
+        return O.bf16_round(a * np.float32(scale)).astype(np.float64)
+    return a
+
+
+@pytest.mark.parametrize("m,d,r,mode,layout", [
+    (1, 64, 8, 0, 0),
+    (37, 200, 16, 0, 0),        # depth tail inside the last 64-deep step
+    (70, 203, 16, 0, 0),        # width not a multiple of 8: element-wise loads
+    (300, 4096, 64, 2, 1),      # pre-scaled dY against LoRA B ([D, r])
+    (129, 1000, 128, 0, 0),     # four 32-wide rank tiles
+    (64, 520, 96, 1, 0),        # SwiGLU replay, three rank tiles
+    (77, 130, 40, 1, 1),        # replay with unaligned width
+    (16424, 256, 64, 0, 0),     # two 32-row tiles per workgroup, row tail
+    (16384, 128, 32, 2, 1),
+])
+def test_lora_project(m, d, r, mode, layout):
+    print(f"lora_project m={m} d={d} r={r} mode={mode} layout={layout}", flush=True)
+    z = seeded((m, d), 1)
+    z2 = seeded((m, d), 2) if mode == 1 else None
+    w = uniform((r, d) if layout == 0 else (d, r), 3, 1 / np.sqrt(d))
+    scale = 0.75
+    out = ops.lora_project(z, z2, mode, scale, w, layout)
+    again = ops.lora_project(z, z2, mode, scale, w, layout)
+    assert torch.equal(out, again)
+    wr = bf16_values(w)
+    ref = _effective(z, z2, mode, scale) @ (wr.T if layout == 0 else wr)
+    assert out.shape == (m, r)
+    assert_close_fro(np_f32(out), O.bf16_round(ref), what="T")
+
+
+def test_lora_project_rejects_rank_above_128():
+    z = seeded((8, 64), 4)
+    w = uniform((160, 64), 5, 0.1)
+    with pytest.raises(molt_amd.CapabilityError):
+        ops.lora_project(z, None, 0, 1.0, w, 0)
+
+
+@pytest.mark.parametrize("m,p,q,mode,layout,scale", [
+    (5, 64, 8, 0, 0, 1.0),
+    (300, 200, 16, 0, 1, 1.0),
+    (1000, 203, 13, 0, 0, 0.5),   # unaligned widths: element-wise loads
+    (4099, 512, 64, 1, 1, 1.0),   # SwiGLU replay of L, row tail
+    (9000, 1024, 64, 0, 0, 2.0),  # split-M partials summed in order
+    (2048, 384, 128, 0, 1, 1.0),  # two rank tiles
+])
+def test_lora_grad(m, p, q, mode, layout, scale):
+    print(f"lora_grad m={m} p={p} q={q} mode={mode} layout={layout}", flush=True)
+    l = seeded((m, p), 6)
+    l2 = seeded((m, p), 7) if mode == 1 else None
+    rmat = seeded((m, q), 8)
+    out = ops.lora_grad(l, l2, mode, rmat, scale, layout)
+    again = ops.lora_grad(l, l2, mode, rmat, scale, layout)
+    assert torch.equal(out, again)
+    ref = scale * (_effective(l, l2, mode, 1.0).T @ bf16_values(rmat))
+    if layout == 1:
+        ref = ref.T
+    assert out.shape == ref.shape
+    assert_close_fro(np_f32(out), ref, tol=1e-5, what="grad")
+
+
+def test_lora_grad_empty_rows_gives_zeros():
+    l = torch.empty((0, 64), device="cuda", dtype=torch.bfloat16)
+    rmat = torch.empty((0, 16), device="cuda", dtype=torch.bfloat16)
+    out = ops.lora_grad(l, None, 0, rmat, 1.0, 1)
+    assert out.shape == (16, 64)
+    assert torch.count_nonzero(out).item() == 0
