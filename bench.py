@@ -96,6 +96,7 @@ def gemv_sweep(dev, reps: int = 20):
                             float(qs.offset), 256)
             descs.append(d)
         for m in (1, 2, 4, 8, 16):
+            log(f"gemv N={n} K={k} M={m} ...")
             x = torch.randn(m, k, generator=g).to(dev, torch.bfloat16)
             t = ops.lora_project(x, None, 0, 1.0, a, 0)
             y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)

@@ -3,19 +3,23 @@
 // Y[m, n] = sum_b scale(n, b) * sum_{k in block b} X[m, k] * code[W(n, k)]
 //           + sum_j T[m, j] * bf16(s * B[n, j])
 //
-// v_mfma_f32_16x16x32_bf16 with X as the 16-row operand (rows >= M are zero)
-// and the NF4 codes as the 16-column operand. Lane group g = lane/16 owns the
-// contiguous 16 elements [64b + 16g, +16) of block b (8 packed bytes, one
-// 8-byte load per row), split over two 32-deep MFMAs, so each MFMA pair sums
-// exactly one block and the block scale is applied once to its 16x16 result
-// instead of to every weight. Codes come from a 256-entry LDS table of bf16
-// code pairs indexed by the packed byte (the nibble order is folded into the
-// table), so a byte costs one byte-select and one LDS read.
+// v_mfma_f32_16x16x32_bf16 with X as the 16-row operand (rows >= M repeat
+// row 0 and are never stored) and the NF4 codes as the 16-column operand.
+// Lane group g = lane/16 owns the contiguous 16 elements [64b + 16g, +16) of
+// block b (8 packed bytes, one 8-byte load per row), split over two 32-deep
+// MFMAs, so each MFMA pair sums exactly one block and the block scale is
+// applied once to its 16x16 result instead of to every weight.
 //
-// A workgroup owns 16 rows and the whole of K: its 8 waves take contiguous
-// eighths of K, keep 8 blocks of loads in flight each, and are summed in
-// wave order through LDS. There is no cross-workgroup reduction, so no
-// device-scope fence (an L2 write-back per workgroup) is ever needed.
+// A workgroup (8 waves) owns 16 rows of W and all of K; its waves take
+// contiguous slices of K, keep a whole chunk of blocks in flight (8 blocks
+// when the u8 codes of 4 blocks can be read as one 4-byte load and share an
+// absmax2 entry, else 4), and are summed in wave order through LDS, so no
+// cross-workgroup reduction (and no device-scope fence) is needed. Codes come
+// from an LDS table of bf16 code pairs indexed by the packed byte, replicated
+// 32 times with the copy chosen by lane % 32, so the data-dependent lookups of
+// a half-wave hit 32 distinct banks. The LoRA term is one more MFMA step per
+// 32 ranks; its B rows are copied into LDS by direct global->LDS loads and T
+// is held in registers, both issued with the first weight chunk.
 #include "common.h"
 
 namespace molt {
@@ -23,10 +27,17 @@ namespace {
 
 constexpr int GV_WAVES = 8;
 constexpr int GV_NT = 64 * GV_WAVES;
-constexpr int GV_ROWS = 16;     // rows per workgroup (one MFMA column tile)
-constexpr int GV_U = 8;         // blocks per wave kept in flight
+constexpr int GV_TILES = 1;              // 16-row MFMA tiles per wave
+constexpr int GV_ROWS = 16 * GV_TILES;   // weight rows per workgroup
+// Blocks per wave chunk (all loads of a chunk are in flight together).
+template <bool Q4> constexpr int gv_u() { return Q4 ? 8 : 4; }
+constexpr int GV_RMAX = 128;             // largest LoRA rank
+constexpr int GV_TABW = 32;              // table copies (one per lane of a half-wave)
+constexpr int GV_LT = 16 * GV_RMAX / GV_NT;   // T elements per thread
 
 typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(1))) const void* gptr_t;
+typedef __attribute__((address_space(3))) void* lptr_t;
 
 struct GemvParams {
   const uint16_t* x; int64_t ldx; int M;
@@ -38,92 +49,235 @@ struct GemvParams {
   uint16_t* y; int64_t ldy;
 };
 
-MOLT_DEV float gv_scale(const GemvParams& p, const float* code2s, int64_t blk) {
+// One chunk of gv_u<Q4>() blocks. Q4 (nested statistics, 4-aligned blocks): the
+// u8 codes of a row's four blocks are one 4-byte load and share one absmax2
+// entry; otherwise one code (or resolved scale) load per block.
+template <bool Q4>
+struct GvChunk {
+  static constexpr int U = gv_u<Q4>();
+  u32x2_t w[U][GV_TILES];
+  u32x4_t xa[U], xb[U];
+  uint32_t q[Q4 ? U / 4 : U][GV_TILES];
+  float s[Q4 ? U / 4 : U][GV_TILES];
+};
+
+// Loads of one chunk. Every address is clamped into its tensor (past-the-end
+// blocks repeat the last one and are not consumed; rows past N or M feed only
+// outputs that are never stored), so no load is predicated. Offsets are 32-bit
+// (a weight holds < 2^31 bytes and blocks), added to the uniform base pointers.
+template <bool Q4>
+MOLT_DEV void gv_load(GvChunk<Q4>& c, const GemvParams& p, const uint32_t (&wofs)[GV_TILES],
+                      const uint32_t (&blk0)[GV_TILES], uint32_t xofs, int b, int b1) {
+#pragma unroll
+  for (int u = 0; u < gv_u<Q4>(); ++u) {
+    const uint32_t bb = (uint32_t)(b + u < b1 ? b + u : b1 - 1);
+    c.xa[u] = *reinterpret_cast<const u32x4_t*>(p.x + (xofs + 64u * bb));
+    c.xb[u] = *reinterpret_cast<const u32x4_t*>(p.x + (xofs + 64u * bb + 8u));
+#pragma unroll
+    for (int t = 0; t < GV_TILES; ++t) {
+      c.w[u][t] = *reinterpret_cast<const u32x2_t*>(p.packed + (wofs[t] + 32u * bb));
+      const uint32_t blk = blk0[t] + bb;
+      if (Q4) {
+        if (u % 4 == 0) {
+          // Whole 4-block units: a unit past the end repeats the last one
+          // (b1 - 4 is unit-aligned), so the 4-byte code load stays inside
+          // the row's codes.
+          const uint32_t qblk = blk0[t] + (uint32_t)(b + u < b1 ? b + u : b1 - 4);
+          c.q[u / 4][t] = *reinterpret_cast<const uint32_t*>(p.q + qblk);
+          c.s[u / 4][t] = p.absmax2[qblk >> p.dq_shift];
+        }
+      } else if (p.scales) {
+        c.s[u][t] = p.scales[blk];
+      } else {
+        c.q[u][t] = p.q[blk];
+        c.s[u][t] = p.absmax2[blk >> p.dq_shift];
+      }
+    }
+  }
+}
+
+MOLT_DEV float gv_scale(const GemvParams& p, const float* code2s, uint32_t q, float s) {
 #pragma clang fp contract(off)
-  if (p.scales) return p.scales[blk];
-  const float prod = code2s[p.q[blk]] * p.absmax2[blk >> p.dq_shift];
+  if (p.scales) return s;
+  const float prod = code2s[q & 0xffu] * s;
   return prod + p.offset;
 }
 
-__global__ __launch_bounds__(GV_NT) void nf4_gemv_kernel(const GemvParams p) {
-  __shared__ uint32_t tab[256];
-  __shared__ float code2s[256];
-  __shared__ f32x4_t red[GV_WAVES - 1][64];
+struct GvSmem {
+  union {
+    uint32_t tab[256 * GV_TABW];                          // bf16 code pair of byte b at [b * 32 + copy]
+    f32x4_t red[GV_WAVES - 1][GV_TILES][64];
+  };
+  float code2s[256];
+  float lb[GV_ROWS * GV_RMAX];                            // raw fp32 LoRA B rows n0.., row stride r
+  uint16_t lt[16 * GV_RMAX];                              // T rows 0..15, row stride r
+};
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (tid < 256) {
-    const int hi = tid >> 4, lo = tid & 15;
-    tab[tid] = pack_bf16x2(p.code[p.order ? hi : lo], p.code[p.order ? lo : hi]);
-    code2s[tid] = p.code2 ? p.code2[tid] : 0.0f;
+template <bool Q4>
+__global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(4))) void nf4_gemv_kernel(const GemvParams p) {
+  __shared__ GvSmem sm;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t n0 = (int64_t)blockIdx.x * GV_ROWS;
+  const int col = lane & 15, g = lane >> 4;
+  const int KB = p.K >> 6;
+  // Waves take contiguous slices of whole units (4 blocks under Q4).
+  constexpr int unit = Q4 ? 4 : 1;
+  const int units = KB / unit;
+  const int b0 = unit * (wave * units / GV_WAVES), b1 = unit * ((wave + 1) * units / GV_WAVES);
+  const int mc = col < p.M ? col : p.M - 1;
+  const uint32_t xofs = (uint32_t)(mc * p.ldx + 16 * g);
+  uint32_t wofs[GV_TILES], blk0[GV_TILES];
+#pragma unroll
+  for (int t = 0; t < GV_TILES; ++t) {
+    const int64_t n = n0 + 16 * t + col;
+    const int64_t nc = n < p.N ? n : p.N - 1;
+    wofs[t] = (uint32_t)(nc * (p.K >> 1) + 8 * g);
+    blk0[t] = (uint32_t)(nc * KB);
+  }
+
+  // Issue order: the codebooks (tiny, L2-resident), the first weight chunk,
+  // then the LoRA operands straight into LDS. Nothing waits until all of
+  // them are in flight.
+  // The codebook is read through the constant address space (scalar loads
+  // into SGPRs: one copy per wave instead of per lane).
+  typedef __attribute__((address_space(4))) const f32x4_t* cptr_t;
+  const cptr_t cbp = (cptr_t)p.code;
+  const f32x4_t cb0 = cbp[0], cb1 = cbp[1], cb2 = cbp[2], cb3 = cbp[3];
+  const float c2 = (p.code2 ? p.code2 : p.code)[p.code2 ? (tid & 255) : 0];
+  GvChunk<Q4> c;
+  if (b0 < b1) gv_load<Q4>(c, p, wofs, blk0, xofs, b0, b1);
+  const bool lora = p.r > 0;
+  if (lora) {
+    // B rows n0 .. n0+63 are contiguous (row stride r): 4-byte copies.
+    const int nb = GV_ROWS * p.r;
+    const int64_t bmax = p.N * p.r - 1;
+    for (int base = wave * 64; base < nb; base += GV_NT) {
+      int64_t e = n0 * p.r + base + lane;
+      e = e < bmax ? e : bmax;
+      __builtin_amdgcn_global_load_lds((gptr_t)(p.lb + e), (lptr_t)(sm.lb + base), 4, 0, 0);
+    }
+  }
+  // T rows 0 .. 15 (rows >= M repeat row 0) into registers; stored below.
+  uint32_t traw[GV_LT];
+#pragma unroll
+  for (int k = 0; k < GV_LT; ++k) {
+    traw[k] = 0;
+    if (lora) {
+      int i = tid + k * GV_NT;
+      i = i < 16 * p.r ? i : 0;
+      const int m = i / p.r, j = i - m * p.r;
+      traw[k] = p.t[(int64_t)(m < p.M ? m : 0) * p.ldt + j];
+    }
+  }
+
+  // Replicated code-pair table: this thread writes byte values b with low
+  // nibble tid / 32 (copy tid % 32) for every high nibble.
+  {
+    const float cv[16] = {cb0[0], cb0[1], cb0[2], cb0[3], cb1[0], cb1[1], cb1[2], cb1[3],
+                          cb2[0], cb2[1], cb2[2], cb2[3], cb3[0], cb3[1], cb3[2], cb3[3]};
+    const int lo = tid >> 5, copy = tid & 31;
+    float clo = cv[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) clo = lo == i ? cv[i] : clo;
+#pragma unroll
+    for (int hi = 0; hi < 16; ++hi) {
+      const float first = p.order ? cv[hi] : clo, second = p.order ? clo : cv[hi];
+      sm.tab[(hi * 16 + lo) * GV_TABW + copy] = pack_bf16x2(first, second);
+    }
+    if (tid < 256) sm.code2s[tid] = c2;
+  }
+  if (lora) {
+#pragma unroll
+    for (int k = 0; k < GV_LT; ++k) {
+      const int i = tid + k * GV_NT;
+      if (i < 16 * p.r) sm.lt[i] = (uint16_t)traw[k];
+    }
   }
   __syncthreads();
 
-  const int col = lane & 15, g = lane >> 4;
-  const int64_t n = (int64_t)blockIdx.x * GV_ROWS + col;
-  const bool rowok = n < p.N;
-  const bool mrow = col < p.M;             // A-operand row m = lane % 16
-  const int KB = p.K >> 6;
-  const int b0 = wave * KB / GV_WAVES, b1 = (wave + 1) * KB / GV_WAVES;
-  const uint8_t* wrow = p.packed + (rowok ? n : 0) * (int64_t)(p.K >> 1) + 8 * g;
-  const uint16_t* xrow = p.x + (int64_t)col * p.ldx + 16 * g;
-  const int64_t blk0 = (rowok ? n : 0) * (int64_t)KB;
-
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int b = b0; b < b1; b += GV_U) {
-    u32x2_t wq[GV_U];
-    u32x4_t xa[GV_U], xb[GV_U];
-    float sc[GV_U];
+  const uint32_t* tab = sm.tab + (lane & 31);
+  f32x4_t acc[GV_TILES];
 #pragma unroll
-    for (int u = 0; u < GV_U; ++u) {
-      const int bb = b + u;
-      const bool ok = bb < b1;
-      wq[u] = u32x2_t{0u, 0u};
-      xa[u] = u32x4_t{0u, 0u, 0u, 0u};
-      xb[u] = u32x4_t{0u, 0u, 0u, 0u};
-      sc[u] = 0.0f;
-      if (ok && rowok) {
-        wq[u] = *reinterpret_cast<const u32x2_t*>(wrow + 32 * bb);
-        sc[u] = gv_scale(p, code2s, blk0 + bb);
-      }
-      if (ok && mrow) {
-        xa[u] = *reinterpret_cast<const u32x4_t*>(xrow + 64 * bb);
-        xb[u] = *reinterpret_cast<const u32x4_t*>(xrow + 64 * bb + 8);
+  for (int t = 0; t < GV_TILES; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int b = b0; b < b1;) {
+#pragma unroll
+    for (int u = 0; u < gv_u<Q4>(); ++u) {
+      if (b + u >= b1) break;
+      const bf16x8v xa = __builtin_bit_cast(bf16x8v, c.xa[u]);
+      const bf16x8v xb = __builtin_bit_cast(bf16x8v, c.xb[u]);
+#pragma unroll
+      for (int t = 0; t < GV_TILES; ++t) {
+        u32x4_t w0, w1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          w0[j] = tab[((c.w[u][t][0] >> (8 * j)) & 0xffu) * GV_TABW];
+          w1[j] = tab[((c.w[u][t][1] >> (8 * j)) & 0xffu) * GV_TABW];
+        }
+        f32x4_t tmp = {0.f, 0.f, 0.f, 0.f};
+        tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, __builtin_bit_cast(bf16x8v, w0), tmp, 0, 0, 0);
+        tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb, __builtin_bit_cast(bf16x8v, w1), tmp, 0, 0, 0);
+        const float sc = Q4 ? gv_scale(p, sm.code2s, c.q[u / 4][t] >> (8 * (u % 4)), c.s[u / 4][t])
+                            : gv_scale(p, sm.code2s, c.q[u][t], c.s[u][t]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[t][e] += sc * tmp[e];
       }
     }
-#pragma unroll
-    for (int u = 0; u < GV_U; ++u) {
-      u32x4_t w0, w1;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        w0[j] = tab[(wq[u][0] >> (8 * j)) & 0xffu];
-        w1[j] = tab[(wq[u][1] >> (8 * j)) & 0xffu];
-      }
-      f32x4_t tmp = {0.f, 0.f, 0.f, 0.f};
-      tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, xa[u]),
-                                                    __builtin_bit_cast(bf16x8v, w0), tmp, 0, 0, 0);
-      tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, xb[u]),
-                                                    __builtin_bit_cast(bf16x8v, w1), tmp, 0, 0, 0);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc[e] += sc[u] * tmp[e];
-    }
+    b += gv_u<Q4>();
+    if (b < b1) gv_load<Q4>(c, p, wofs, blk0, xofs, b, b1);
   }
 
-  if (wave > 0) red[wave - 1][lane] = acc;
+  __syncthreads();                       // the table area becomes the reduction area
+  if (wave > 0) {
+#pragma unroll
+    for (int t = 0; t < GV_TILES; ++t) sm.red[wave - 1][t][lane] = acc[t];
+  }
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
-  for (int w = 0; w < GV_WAVES - 1; ++w) acc += red[w][lane];
-
-  // acc[e] is C[m][n] with m = 4 (lane / 16) + e.
-  if (!rowok) return;
+  for (int w = 0; w < GV_WAVES - 1; ++w)
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int m = 4 * g + e;
-    if (m >= p.M) continue;
-    float v = acc[e];
-    for (int j = 0; j < p.r; ++j)
-      v += bf16_to_f32(p.t[(int64_t)m * p.ldt + j]) * round_bf16(p.s * p.lb[n * p.r + j]);
-    p.y[(int64_t)m * p.ldy + n] = bf16_bits(v);
+    for (int t = 0; t < GV_TILES; ++t) acc[t] += sm.red[w][t][lane];
+
+  if (lora) {
+    // acc += T . bf16(s B)^T, 32 ranks per MFMA step (ranks past r are zero).
+    for (int j0 = 0; j0 < p.r; j0 += 32) {
+      u32x4_t ta;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int j = j0 + 8 * g + 2 * e;
+        const uint32_t lo = j < p.r ? sm.lt[col * p.r + j] : 0u;
+        const uint32_t hi = j + 1 < p.r ? sm.lt[col * p.r + j + 1] : 0u;
+        ta[e] = lo | (hi << 16);
+      }
+#pragma unroll
+      for (int t = 0; t < GV_TILES; ++t) {
+        const float* brow = sm.lb + (16 * t + col) * p.r;
+        u32x4_t bw;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = j0 + 8 * g + 2 * e;
+          const float lo = j < p.r ? round_bf16(p.s * brow[j]) : 0.0f;
+          const float hi = j + 1 < p.r ? round_bf16(p.s * brow[j + 1]) : 0.0f;
+          bw[e] = pack_bf16x2(lo, hi);
+        }
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, ta),
+                                                         __builtin_bit_cast(bf16x8v, bw), acc[t], 0, 0, 0);
+      }
+    }
+  }
+
+  // acc[t][e] is C[m][n] with m = 4 (lane / 16) + e, n = n0 + 16 t + lane % 16.
+#pragma unroll
+  for (int t = 0; t < GV_TILES; ++t) {
+    const int64_t n = n0 + 16 * t + col;
+    if (n >= p.N) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = 4 * g + e;
+      if (m >= p.M) continue;
+      p.y[(int64_t)m * p.ldy + n] = bf16_bits(acc[t][e]);
+    }
   }
 }
 
@@ -150,10 +304,13 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
   MOLT_REQUIRE(w->block_size == 64 && w->cols % 64 == 0, MOLT_EUNSUPPORTED,
                "%s: needs block_size 64 and cols %% 64 == 0", who);
   MOLT_REQUIRE(w->cols < (1ll << 30), MOLT_EUNSUPPORTED, "%s: cols too large", who);
+  MOLT_REQUIRE(w->rows * (w->cols / 2) < (1ll << 31) && M * ldx < (1ll << 30), MOLT_EUNSUPPORTED,
+               "%s: weight or activations too large for 32-bit offsets", who);
   MOLT_REQUIRE(w->rows > 0 && ldx >= w->cols && ldy >= w->rows, MOLT_EINVAL, "%s: bad shape/stride", who);
-  MOLT_REQUIRE(ldx % 8 == 0 && aligned(x, 16) && aligned(w->packed, 8), MOLT_EINVAL,
-               "%s: X rows must be 16-byte aligned and packed data 8-byte aligned", who);
+  MOLT_REQUIRE(ldx % 8 == 0 && aligned(x, 16) && aligned(w->packed, 8) && aligned(w->code, 16), MOLT_EINVAL,
+               "%s: X rows and the codebook must be 16-byte aligned and packed data 8-byte aligned", who);
   MOLT_REQUIRE(r >= 0 && (r == 0 || (t && lora_b && ldt >= r)), MOLT_EINVAL, "%s: bad LoRA operands", who);
+  MOLT_REQUIRE(r <= GV_RMAX, MOLT_EUNSUPPORTED, "%s: LoRA rank %d > %d", who, r, GV_RMAX);
   const bool nested = w->nested != 0;
   MOLT_REQUIRE(nested ? (w->absmax_q && w->absmax2 && w->code2 && w->dq_block > 0) : (w->scales != nullptr),
                MOLT_EINVAL, "%s: scale statistics missing", who);
@@ -170,8 +327,11 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
   p.dq_shift = shift;
   p.code = w->code; p.order = w->nibble_order;
   p.t = t; p.ldt = ldt; p.lb = lora_b; p.r = r; p.s = scaling; p.y = y; p.ldy = ldy;
-  const int64_t grid = ceil_div64(p.N, GV_ROWS);
-  MOLT_REQUIRE(grid < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
-  hipLaunchKernelGGL(nf4_gemv_kernel, dim3((unsigned)grid), dim3(GV_NT), 0, (hipStream_t)stream, p);
+  const int64_t groups = ceil_div64(p.N, GV_ROWS);
+  MOLT_REQUIRE(groups < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
+  hipStream_t st = (hipStream_t)stream;
+  const bool q4 = nested && (w->cols / 64) % 4 == 0 && w->dq_block >= 4 && aligned(w->absmax_q, 4);
+  if (q4) hipLaunchKernelGGL((nf4_gemv_kernel<true>), dim3((unsigned)groups), dim3(GV_NT), 0, st, p);
+  else hipLaunchKernelGGL((nf4_gemv_kernel<false>), dim3((unsigned)groups), dim3(GV_NT), 0, st, p);
   return check_launch(who);
 }

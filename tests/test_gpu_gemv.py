@@ -36,9 +36,11 @@ def test_gemv_matches_oracle(n, k, m):
     assert_close_fro(np_f32(y), bf16_values(x) @ wo.T, what="Y")
 
 
-@pytest.mark.parametrize("m", [1, 5, 16])
-def test_gemv_with_lora_matches_oracle(m):
-    n, k, r, s = 1024, 4096, 16, 2.0
+@pytest.mark.parametrize("m,n,r", [(1, 1024, 16), (5, 1024, 16), (16, 1024, 16), (3, 1000, 64),
+                                   (16, 520, 96), (2, 256, 128)])
+def test_gemv_with_lora_matches_oracle(m, n, r):
+    print(f"gemv lora m={m} n={n} r={r}", flush=True)
+    k, s = 4096, 2.0
     w = seeded((n, k), 70, std=0.02, dtype=torch.float32)
     packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True)
     x = seeded((m, k), 71)
@@ -86,3 +88,13 @@ def test_gemv_rejects_unsupported_geometry():
     packed2, qs2 = molt_amd.quantize_4bit(w2, blocksize=64, compress_statistics=False)
     with pytest.raises(ValueError, match="1..16"):
         _gemv(seeded((17, 128), 2), packed2, qs2, nested=False)
+
+
+def test_gemv_rejects_rank_above_128():
+    w = seeded((64, 128), 3, std=0.02, dtype=torch.float32)
+    packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True)
+    x = seeded((2, 128), 4)
+    t = seeded((2, 160), 5)
+    b = seeded((64, 160), 6, std=0.01, dtype=torch.float32)
+    with pytest.raises(molt_amd.CapabilityError, match="rank"):
+        _gemv(x, packed, qs, t, b, 1.0)
