@@ -490,19 +490,20 @@ __global__ __launch_bounds__(NT) void nf4_bwd_kernel(const BwdParams p) {
 
 // ======================================================================
 // Large-tile kernels for aligned shapes (K, contraction and output widths
-// multiples of 64, NF4 block 64): 256 x 256 workgroup tile, 4 waves of
-// 128 x 128 (16 accumulator tiles per wave, so each 16-byte LDS fragment
-// feeds four MFMAs; the 256 fp32 accumulators live in AGPRs), one-deep
-// register prefetch (the global loads of step s+1 are in flight during the
-// MFMAs of step s and are dequantised into the other LDS buffer after), and
-// an unpadded LDS layout whose 16-byte chunks are XOR-swizzled by
-// (row ^ row/8) & 7 so that fragment reads, row-major stores and the
+// multiples of 64, NF4 block 64): 256 x 256 workgroup tile, 8 waves of
+// 128 W rows x 64 X rows (8 accumulator tiles, 128 registers per wave), so
+// two waves share each SIMD and one's memory or dequantisation work fills
+// the other's MFMA gaps. The next step's loads are spread over the MFMA
+// sub-steps of the current one (X straight into LDS, the packed NF4 bytes
+// into registers, dequantised into the other LDS buffer during the last
+// sub-step), and the LDS layout is unpadded with 16-byte chunks XOR-swizzled
+// by (row ^ row/8) & 7, so fragment reads, row-major stores and the
 // backward's transposed patch stores are all bank-conflict free.
 // ======================================================================
 namespace big {
 
-constexpr int BM = 256, BN = 256, NT = 256, WAVES_M = 2;
-constexpr int WROWS = 128, WCOLS = 128, TM = 4, TN = 4, LD = 64;
+constexpr int BM = 256, BN = 256, NT = 512, WAVES_M = 4;
+constexpr int WROWS = 128, WCOLS = 64, TM = 4, TN = 2, LD = 64;
 constexpr int GROUP_M = 4;
 
 constexpr int EP_LD = 256 + 8;   // epilogue tile row stride (bf16), 16-byte aligned rows
@@ -560,6 +561,28 @@ MOLT_DEV void compute(const uint16_t* __restrict__ ws, const uint16_t* __restric
   }
 }
 
+// One BK step whose MFMA sub-steps carry the staging of the next step: the
+// stage callback runs before sub-step kk's MFMAs (the scheduling barrier keeps
+// its memory instructions there instead of hoisting them all to the top),
+// so the next step's loads and dequantisation overlap this step's MFMAs.
+template <typename F>
+MOLT_DEV void compute_staged(const uint16_t* __restrict__ ws, const uint16_t* __restrict__ xs, const FragOff& f,
+                             f32x16_t (&acc)[TM][TN], F&& stage) {
+  bf16x8_t a[2][TM], b[2][TN];
+  load_frags(ws, xs, f, 0, a[0], b[0]);
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    stage(kk);
+    if (kk < 3) load_frags(ws, xs, f, kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kk & 1][i], b[kk & 1][j], acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // ---- X side (row-major, contraction contiguous): direct global -> LDS loads.
 // global_load_lds_dwordx4 writes lane l's 16 bytes to LDS at M0 + 16 l, so
 // each wave-level load fills one contiguous 1 KB of the tile; every lane
@@ -573,8 +596,8 @@ typedef __attribute__((address_space(3))) void* lptr_t;
 MOLT_DEV void x_issue_lds(uint16_t* xs, const uint16_t* __restrict__ a, int64_t lda, int64_t m0, int64_t M,
                           int64_t k0, int wave, int lane) {
 #pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    const int blk = wave * 8 + c;            // 1 KB block of the 32 KB tile
+  for (int c = 0; c < 4; ++c) {
+    const int blk = wave * 4 + c;            // 1 KB block of the 32 KB tile
     const int pos = blk * 64 + lane;         // 16-byte slot in the tile
     const int R = pos >> 3, slot = pos & 7;
     const int ch = slot ^ ((R ^ (R >> 3)) & 7);
@@ -583,7 +606,17 @@ MOLT_DEV void x_issue_lds(uint16_t* xs, const uint16_t* __restrict__ a, int64_t 
   }
 }
 
-// ---- forward W side (row-contract): 2 chunks of 16 packed bytes per thread
+MOLT_DEV void x_issue_lds_one(uint16_t* xs, const uint16_t* __restrict__ a, int64_t lda, int64_t m0, int64_t M,
+                              int64_t k0, int wave, int lane, int c) {
+  const int blk = wave * 4 + c;            // 1 KB block of the 32 KB tile
+  const int pos = blk * 64 + lane;         // 16-byte slot in the tile
+  const int R = pos >> 3, slot = pos & 7;
+  const int ch = slot ^ ((R ^ (R >> 3)) & 7);
+  const int64_t m = min(m0 + R, M - 1);
+  __builtin_amdgcn_global_load_lds((gptr_t)(a + m * lda + k0 + 8 * ch), (lptr_t)(xs + blk * 512), 16, 0, 0);
+}
+
+// ---- forward W side (row-contract): one chunk of 16 packed bytes per thread
 MOLT_DEV void fwd_row(int R, int64_t tn, bool pair, int& which, int64_t& n) {
   if (pair) {
     const int sub = (R >> 5) & 3;
@@ -595,11 +628,11 @@ MOLT_DEV void fwd_row(int R, int64_t tn, bool pair, int& which, int64_t& n) {
   }
 }
 
-struct WRReg { u32x4_t q[2]; float sc[2]; };
+struct WRReg { u32x4_t q[1]; float sc[1]; };
 
 MOLT_DEV void wr_issue(WRReg& w, const FwdParams& p, int64_t tn, bool pair, int64_t k0, int tid) {
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
+  for (int c = 0; c < 1; ++c) {
     const int idx = tid + NT * c;
     const int R = idx >> 1, half = idx & 1;
     int which; int64_t n;
@@ -612,7 +645,7 @@ MOLT_DEV void wr_issue(WRReg& w, const FwdParams& p, int64_t tn, bool pair, int6
 
 MOLT_DEV void wr_commit(const WRReg& w, uint16_t* ws, const float2* tab, int tid) {
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
+  for (int c = 0; c < 1; ++c) {
     const int idx = tid + NT * c;
     const int R = idx >> 1, half = idx & 1;
 #pragma unroll
@@ -629,16 +662,16 @@ MOLT_DEV void wr_commit(const WRReg& w, uint16_t* ws, const float2* tab, int tid
 }
 
 // ---- backward W side (column-contract): one 8-row x 8-column patch per thread
-struct WCReg { uint32_t q[8]; float sc[8]; };
+struct WCReg { uint32_t q[4]; float sc[4]; };
 
 MOLT_DEV void wc_issue(WCReg& w, const BwdParams& p, int seg, int64_t tn, int64_t c0, int tid) {
-  const int cg = tid & 31, rg = tid >> 5;
+  const int cg = tid & 31, rg = tid >> 5;     // 32 column groups of 8, 16 row groups of 4
   const int64_t col = min(tn * BN + 8 * cg, p.Kw - 8);
   const uint8_t* packed = sel(p.packed, seg);
   const float* scales = sel(p.scales, seg);
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    const int64_t flat = (c0 + 8 * rg + r) * p.Kw + col;
+  for (int r = 0; r < 4; ++r) {
+    const int64_t flat = (c0 + 4 * rg + r) * p.Kw + col;
     w.q[r] = *reinterpret_cast<const uint32_t*>(packed + (flat >> 1));
     w.sc[r] = scales[flat >> 6];
   }
@@ -646,9 +679,9 @@ MOLT_DEV void wc_issue(WCReg& w, const BwdParams& p, int seg, int64_t tn, int64_
 
 MOLT_DEV void wc_commit(const WCReg& w, uint16_t* ws, const float2* tab, int tid) {
   const int cg = tid & 31, rg = tid >> 5;
-  float v[8][8];
+  float v[4][8];
 #pragma unroll
-  for (int r = 0; r < 8; ++r)
+  for (int r = 0; r < 4; ++r)
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const float2 c = tab[(w.q[r] >> (8 * b)) & 0xffu];
@@ -657,51 +690,110 @@ MOLT_DEV void wc_commit(const WCReg& w, uint16_t* ws, const float2* tab, int tid
     }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    u32x4_t o;
+    u32x2_t o;
     o[0] = pack_bf16x2(v[0][j], v[1][j]);
     o[1] = pack_bf16x2(v[2][j], v[3][j]);
-    o[2] = pack_bf16x2(v[4][j], v[5][j]);
-    o[3] = pack_bf16x2(v[6][j], v[7][j]);
-    *reinterpret_cast<u32x4_t*>(ws + loff(8 * cg + j, rg)) = o;
+    *reinterpret_cast<u32x2_t*>(ws + loff(8 * cg + j, rg >> 1) + 4 * (rg & 1)) = o;
   }
 }
 
-// ---- element-wise staging for the LoRA contraction steps (swizzled layout)
+// ---- staging of the LoRA contraction steps (swizzled layout). Each thread
+// handles whole 8-element chunks: all of its global loads are issued before
+// any LDS store, 16-byte vector loads where the chunk lies inside the operand
+// and is aligned, element loads (with zeros outside) otherwise.
+MOLT_DEV bool al16(const void* q) { return ((uintptr_t)q & 15) == 0; }
+
 MOLT_DEV void lora_a_stage(uint16_t* xs, const uint16_t* __restrict__ t, int64_t ldt, int64_t m0, int64_t M,
                            int64_t c0, int64_t L, int tid) {
-  for (int e = tid; e < BM * BK; e += NT) {
-    const int R = e >> 6, k = e & 63;
-    const int64_t m = m0 + R, c = c0 + k;
-    xs[loff(R, k >> 3) + (k & 7)] = (m < M && c < L) ? t[m * ldt + c] : (uint16_t)0;
+  constexpr int CH = BM * (BK / 8) / NT;
+  const bool vec = al16(t) && ldt % 8 == 0;
+  u32x4_t v[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int q = tid + NT * c, R = q >> 3, ch = q & 7;
+    const int64_t m = m0 + R, k = c0 + 8 * ch;
+    if (vec && m < M && k + 8 <= L) {
+      v[c] = *reinterpret_cast<const u32x4_t*>(t + m * ldt + k);
+    } else {
+      uint16_t e[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) e[i] = (m < M && k + i < L) ? t[m * ldt + k + i] : (uint16_t)0;
+      v[c] = __builtin_bit_cast(u32x4_t, e);
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int q = tid + NT * c;
+    *reinterpret_cast<u32x4_t*>(xs + loff(q >> 3, q & 7)) = v[c];
   }
 }
 
 MOLT_DEV void lora_wrow_stage(uint16_t* ws, const FwdParams& p, int64_t tn, bool pair, int64_t c0, int tid) {
-  for (int e = tid; e < BN * BK; e += NT) {
-    const int R = e >> 6, k = e & 63;
+  constexpr int CH = BN * (BK / 8) / NT;
+  u32x4_t o[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int q = tid + NT * c, R = q >> 3, ch = q & 7;
     int which; int64_t n;
     fwd_row(R, tn, pair, which, n);
-    const int64_t c = c0 + k - (int64_t)which * p.r;
-    uint16_t v = 0;
-    if (n < p.N && c >= 0 && c < p.r) v = bf16_bits((which ? p.s[1] : p.s[0]) * sel(p.lb, which)[n * p.ldlb + c]);
-    ws[loff(R, k >> 3) + (k & 7)] = v;
+    const float* lb = sel(p.lb, which);
+    const float s = which ? p.s[1] : p.s[0];
+    const int64_t cc = c0 + 8 * ch - (int64_t)which * p.r;   // first rank of the chunk
+    float f[8];
+    if (n < p.N && cc >= 0 && cc + 8 <= p.r && al16(lb + n * p.ldlb + cc)) {
+      const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(lb + n * p.ldlb + cc);
+      const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(lb + n * p.ldlb + cc + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { f[i] = lo[i]; f[4 + i] = hi[i]; }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = (n < p.N && cc + i >= 0 && cc + i < p.r) ? lb[n * p.ldlb + cc + i] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[c][i] = pack_bf16x2(s * f[2 * i], s * f[2 * i + 1]);
+  }
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int q = tid + NT * c;
+    *reinterpret_cast<u32x4_t*>(ws + loff(q >> 3, q & 7)) = o[c];
   }
 }
 
+// Backward W side: element (output column R, rank c0 + k) = bf16(scale * A[c0 + k][col]).
+// A thread loads a 4-rank x 8-column patch of A (16-byte loads along the
+// columns) and transposes it so the ranks become contiguous in LDS.
 MOLT_DEV void lora_wcol_stage(uint16_t* ws, const BwdParams& p, int seg, int64_t tn, int64_t c0, int tid) {
+  static_assert(NT == 512, "one 4 x 8 patch per thread");
   const float* a = sel(p.la, seg);
-  for (int e = tid; e < BN * BK; e += NT) {
-    const int R = e % BN, k = e / BN;
-    const int64_t col = tn * BN + R, c = c0 + k;
-    uint16_t v = 0;
-    if (col < p.Kw && c < p.r) v = bf16_bits(p.la_scale * a[c * p.ldla + col]);
-    ws[loff(R, k >> 3) + (k & 7)] = v;
+  const int cg = tid & 31, rg = tid >> 5;            // 32 column groups of 8, 16 rank groups of 4
+  const int64_t col = tn * BN + 8 * cg;
+  float v[4][8];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t c = c0 + 4 * rg + r;
+    const float* row = a + c * p.ldla + col;
+    if (c < p.r && col + 8 <= p.Kw && al16(row)) {
+      const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(row);
+      const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(row + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { v[r][i] = lo[i]; v[r][4 + i] = hi[i]; }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[r][i] = (c < p.r && col + i < p.Kw) ? row[i] : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    u32x2_t o;
+    o[0] = pack_bf16x2(p.la_scale * v[0][j], p.la_scale * v[1][j]);
+    o[1] = pack_bf16x2(p.la_scale * v[2][j], p.la_scale * v[3][j]);
+    *reinterpret_cast<u32x2_t*>(ws + loff(8 * cg + j, rg >> 1) + 4 * (rg & 1)) = o;
   }
 }
 
 // ---- LDS-staged epilogues
-// acc[i][j] holds C[W row][X row]: W row = wn*128 + 32i + 8(e/4) + 4(lane/32) + e%4,
-// X row = wm*128 + 32j + lane%32. The staged tile is ep[X row][W row] in bf16.
+// acc[i][j] holds C[W row][X row]: W row = wn*WROWS + 32i + 8(e/4) + 4(lane/32) + e%4,
+// X row = wm*WCOLS + 32j + lane%32. The staged tile is ep[X row][W row] in bf16.
 MOLT_DEV void stage_acc(uint16_t* ep, const f32x16_t (&acc)[TM][TN], int wm, int wn, int lane) {
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
@@ -845,16 +937,25 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
   __syncthreads();  // pair table
   wr_commit(wr, sm.ws[0], sm.tab, tid);
   __syncthreads();
-  for (int s = 0; s < ks; ++s) {
+  for (int s = 0; s + 1 < ks; ++s) {
     const int cur = s & 1;
-    if (s + 1 < ks) {
-      x_issue_lds(sm.xs[cur ^ 1], p.x, p.ldx, m0, p.M, (int64_t)(s + 1) * BK, wave, lane);
-      wr_issue(wr, p, tn, PAIR, (int64_t)(s + 1) * BK, tid);
-    }
-    compute(sm.ws[cur], sm.xs[cur], fo, acc);
-    if (s + 1 < ks) wr_commit(wr, sm.ws[cur ^ 1], sm.tab, tid);
+    const int64_t k1 = (int64_t)(s + 1) * BK;
+    compute_staged(sm.ws[cur], sm.xs[cur], fo, acc, [&](int kk) {
+      if (kk == 0) {
+        wr_issue(wr, p, tn, PAIR, k1, tid);
+        x_issue_lds_one(sm.xs[cur ^ 1], p.x, p.ldx, m0, p.M, k1, wave, lane, 0);
+        x_issue_lds_one(sm.xs[cur ^ 1], p.x, p.ldx, m0, p.M, k1, wave, lane, 1);
+      } else if (kk == 1) {
+        x_issue_lds_one(sm.xs[cur ^ 1], p.x, p.ldx, m0, p.M, k1, wave, lane, 2);
+        x_issue_lds_one(sm.xs[cur ^ 1], p.x, p.ldx, m0, p.M, k1, wave, lane, 3);
+      } else if (kk == 3) {
+        wr_commit(wr, sm.ws[cur ^ 1], sm.tab, tid);
+      }
+    });
     __syncthreads();
   }
+  compute(sm.ws[(ks - 1) & 1], sm.xs[(ks - 1) & 1], fo, acc);
+  __syncthreads();
   for (int64_t c0 = 0; c0 < p.lr; c0 += BK) {
     lora_a_stage(sm.xs[0], p.t, p.ldt, m0, p.M, c0, p.lr, tid);
     lora_wrow_stage(sm.ws[0], p, tn, PAIR, c0, tid);
@@ -909,23 +1010,32 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
   const int kseg = (int)(p.Nw / BK);
   const int ks = p.nseg * kseg;
   WCReg wr;
-  auto issue = [&](int s, uint16_t* xs) {
-    const int seg = s / kseg;
-    const int64_t c0 = (int64_t)(s - seg * kseg) * BK;
-    x_issue_lds(xs, sel(p.dy, seg), p.lddy, m0, p.M, c0, wave, lane);
-    wc_issue(wr, p, seg, tn, c0, tid);
-  };
-  issue(0, sm.xs[0]);
+  x_issue_lds(sm.xs[0], sel(p.dy, 0), p.lddy, m0, p.M, 0, wave, lane);
+  wc_issue(wr, p, 0, tn, 0, tid);
   __syncthreads();  // pair table
   wc_commit(wr, sm.ws[0], sm.tab, tid);
   __syncthreads();
-  for (int s = 0; s < ks; ++s) {
+  for (int s = 0; s + 1 < ks; ++s) {
     const int cur = s & 1;
-    if (s + 1 < ks) issue(s + 1, sm.xs[cur ^ 1]);
-    compute(sm.ws[cur], sm.xs[cur], fo, acc);
-    if (s + 1 < ks) wc_commit(wr, sm.ws[cur ^ 1], sm.tab, tid);
+    const int seg = (s + 1) / kseg;
+    const int64_t c1 = (int64_t)(s + 1 - seg * kseg) * BK;
+    const uint16_t* dyn = sel(p.dy, seg);
+    compute_staged(sm.ws[cur], sm.xs[cur], fo, acc, [&](int kk) {
+      if (kk == 0) {
+        wc_issue(wr, p, seg, tn, c1, tid);
+        x_issue_lds_one(sm.xs[cur ^ 1], dyn, p.lddy, m0, p.M, c1, wave, lane, 0);
+        x_issue_lds_one(sm.xs[cur ^ 1], dyn, p.lddy, m0, p.M, c1, wave, lane, 1);
+      } else if (kk == 1) {
+        x_issue_lds_one(sm.xs[cur ^ 1], dyn, p.lddy, m0, p.M, c1, wave, lane, 2);
+        x_issue_lds_one(sm.xs[cur ^ 1], dyn, p.lddy, m0, p.M, c1, wave, lane, 3);
+      } else if (kk == 3) {
+        wc_commit(wr, sm.ws[cur ^ 1], sm.tab, tid);
+      }
+    });
     __syncthreads();
   }
+  compute(sm.ws[(ks - 1) & 1], sm.xs[(ks - 1) & 1], fo, acc);
+  __syncthreads();
   for (int seg = 0; seg < p.nseg && p.r > 0; ++seg) {
     for (int64_t c0 = 0; c0 < p.r; c0 += BK) {
       lora_a_stage(sm.xs[0], sel(p.u, seg), p.ldu, m0, p.M, c0, p.r, tid);
