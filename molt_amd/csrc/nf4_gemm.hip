@@ -505,24 +505,64 @@ namespace big {
 constexpr int BM = 256, BN = 256, NT = 512, WAVES_M = 4;
 constexpr int WROWS = 128, WCOLS = 64, TM = 4, TN = 2, LD = 64;
 constexpr int GROUP_M = 4;
+constexpr int BUF = BM * LD;     // bf16 elements of one operand buffer (32 KB)
+constexpr int TABC = 16;         // interleaved copies of the code-pair table
+constexpr int EP_LD = 256 + 8;   // (128 x 128 path and backward) epilogue tile row stride
 
-constexpr int EP_LD = 256 + 8;   // epilogue tile row stride (bf16), 16-byte aligned rows
+// Operand buffer layout. A row holds 64 contraction elements as 8 chunks of
+// 16 B; chunks 0-3 (elements 0..31) of all rows form the first 16 KB half of
+// the buffer, chunks 4-7 the second. Within a half a row is 64 B and its four
+// chunk positions are XOR-swizzled by (R >> 2) & 3, so a ds_read_b128 of one
+// chunk over 16 consecutive rows hits 16 distinct bank groups. Rows 32 apart
+// share the swizzle and the halves are a constant 16 KB apart, so every
+// fragment read of a step is one of two per-lane base addresses plus an
+// immediate offset.
+MOLT_DEV int loff(int R, int c) { return (c >> 2) * (BUF / 2) + R * 32 + (((c & 3) ^ ((R >> 2) & 3)) << 3); }
 
-struct Smem {
-  union {
-    struct {
-      uint16_t xs[2][BM * LD];
-      uint16_t ws[2][BN * LD];
-      float2 tab[256];
-    };
-    uint16_t ep[BM * EP_LD];       // epilogue staging, reused after the main loop
-  };
-};
+// Global -> LDS DMA writes lane l's 16 bytes to (block base + 16 l): block blk
+// (1 KB) of a buffer holds 16 rows of one half. Returns the row and first
+// contraction element the lane must fetch for that slot.
+MOLT_DEV void dma_slot(int blk, int lane, int& R, int& k) {
+  R = ((blk & 15) << 4) + (lane >> 2);
+  k = 32 * (blk >> 4) + 8 * ((lane & 3) ^ ((R >> 2) & 3));
+}
 
-MOLT_DEV int loff(int R, int c) { return R * LD + ((c ^ ((R ^ (R >> 3)) & 7)) << 3); }
+// Kernel-argument pointers and the 16 codes stay in scalar registers or are
+// read once; see build_tab.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// Per-lane fragment geometry: the first LDS row this lane reads in each
-// operand, and its half (which 8-element chunk of a 16-deep MFMA step).
+// Buffer resource over [p, p + bytes): loads through it are bounds-checked by
+// the hardware (out-of-range lanes read zero) and take a 32-bit per-lane byte
+// offset plus a uniform scalar offset, so no per-step 64-bit address math.
+MOLT_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+MOLT_DEV u32x4_t buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, 0);
+}
+MOLT_DEV uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, soff, 0);
+}
+// 16 bytes per lane from global straight into LDS at dst + 16 * lane (dst uniform).
+MOLT_DEV void buf_load_lds16(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t off, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, off, soff, 0, 0);
+}
+// vmcnt(0) with the other counters untouched.
+MOLT_DEV void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Code-pair table, TABC interleaved copies: entry (byte b, copy c) at b * TABC + c
+// holds (code[first nibble], code[second nibble]). Lane l reads copy l % TABC,
+// which spreads the data-dependent lookups of a wave over TABC bank pairs.
+MOLT_DEV void build_tab(float2* tab, const float* __restrict__ code, int order, int tid) {
+  const float cv = code[tid & 15];
+#pragma unroll
+  for (int k = 0; k < 256 * TABC / NT; ++k) {
+    const int i = tid + k * NT, b = i / TABC;
+    const float ch = __shfl(cv, b >> 4), cl = __shfl(cv, b & 15);
+    tab[i] = order ? make_float2(ch, cl) : make_float2(cl, ch);
+  }
+}
+
 struct FragOff { int arow, brow, h; };
 
 MOLT_DEV void frag_offsets(FragOff& f, int arow0, int brow0, int lane) {
@@ -541,10 +581,16 @@ MOLT_DEV void load_frags(const uint16_t* __restrict__ ws, const uint16_t* __rest
     b[j] = *reinterpret_cast<const bf16x8_t*>(xs + loff(f.brow + 32 * j, 2 * kk + f.h));
 }
 
-// One BK step: four 16-deep sub-steps of 16 MFMAs each. Fragments are double
-// buffered: the LDS reads of sub-step kk+1 are issued before the MFMAs of
-// sub-step kk, so LDS latency hides under matrix work; the scheduling barrier
-// after each sub-step bounds the live fragments to two sets (64 VGPRs).
+MOLT_DEV void mfma_set(const bf16x8_t (&a)[TM], const bf16x8_t (&b)[TN], f32x16_t (&acc)[TM][TN]) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+}
+
+// One BK step from LDS (used by the LoRA steps): four 16-deep sub-steps, the
+// fragment reads of sub-step kk+1 issued before the MFMAs of kk.
 MOLT_DEV void compute(const uint16_t* __restrict__ ws, const uint16_t* __restrict__ xs, const FragOff& f,
                       f32x16_t (&acc)[TM][TN]) {
   bf16x8_t a[2][TM], b[2][TN];
@@ -552,71 +598,26 @@ MOLT_DEV void compute(const uint16_t* __restrict__ ws, const uint16_t* __restric
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
     if (kk < 3) load_frags(ws, xs, f, kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kk & 1][i], b[kk & 1][j], acc[i][j], 0, 0, 0);
+    mfma_set(a[kk & 1], b[kk & 1], acc);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
 
-// One BK step whose MFMA sub-steps carry the staging of the next step: the
-// stage callback runs before sub-step kk's MFMAs (the scheduling barrier keeps
-// its memory instructions there instead of hoisting them all to the top),
-// so the next step's loads and dequantisation overlap this step's MFMAs.
-template <typename F>
-MOLT_DEV void compute_staged(const uint16_t* __restrict__ ws, const uint16_t* __restrict__ xs, const FragOff& f,
-                             f32x16_t (&acc)[TM][TN], F&& stage) {
-  bf16x8_t a[2][TM], b[2][TN];
-  load_frags(ws, xs, f, 0, a[0], b[0]);
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    stage(kk);
-    if (kk < 3) load_frags(ws, xs, f, kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kk & 1][i], b[kk & 1][j], acc[i][j], 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-  }
+// Instruction interleave of one 16-deep sub-step: each of the 8 MFMAs is
+// followed by one or two LDS reads and a few VALU instructions, so the LDS
+// queue and the VALU stay busy in the shadow of the matrix core instead of
+// stalling the wave in bursts.
+MOLT_DEV void interleave_substep() {
+#define MOLT_SGB(nds)                                   \
+  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    \
+  __builtin_amdgcn_sched_group_barrier(0x100, nds, 0);  \
+  __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+  MOLT_SGB(2) MOLT_SGB(2) MOLT_SGB(1) MOLT_SGB(1) MOLT_SGB(1) MOLT_SGB(1) MOLT_SGB(1) MOLT_SGB(1)
+#undef MOLT_SGB
+  __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
 }
 
-// ---- X side (row-major, contraction contiguous): direct global -> LDS loads.
-// global_load_lds_dwordx4 writes lane l's 16 bytes to LDS at M0 + 16 l, so
-// each wave-level load fills one contiguous 1 KB of the tile; every lane
-// fetches the global chunk whose swizzled LDS slot is its own. No VGPRs hold
-// X and no LDS store instructions are issued for it. Loads are branch-free:
-// an out-of-range row is clamped to the last valid one (such rows only reach
-// output rows the epilogue never stores).
-typedef __attribute__((address_space(1))) const void* gptr_t;
-typedef __attribute__((address_space(3))) void* lptr_t;
-
-MOLT_DEV void x_issue_lds(uint16_t* xs, const uint16_t* __restrict__ a, int64_t lda, int64_t m0, int64_t M,
-                          int64_t k0, int wave, int lane) {
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int blk = wave * 4 + c;            // 1 KB block of the 32 KB tile
-    const int pos = blk * 64 + lane;         // 16-byte slot in the tile
-    const int R = pos >> 3, slot = pos & 7;
-    const int ch = slot ^ ((R ^ (R >> 3)) & 7);
-    const int64_t m = min(m0 + R, M - 1);
-    __builtin_amdgcn_global_load_lds((gptr_t)(a + m * lda + k0 + 8 * ch), (lptr_t)(xs + blk * 512), 16, 0, 0);
-  }
-}
-
-MOLT_DEV void x_issue_lds_one(uint16_t* xs, const uint16_t* __restrict__ a, int64_t lda, int64_t m0, int64_t M,
-                              int64_t k0, int wave, int lane, int c) {
-  const int blk = wave * 4 + c;            // 1 KB block of the 32 KB tile
-  const int pos = blk * 64 + lane;         // 16-byte slot in the tile
-  const int R = pos >> 3, slot = pos & 7;
-  const int ch = slot ^ ((R ^ (R >> 3)) & 7);
-  const int64_t m = min(m0 + R, M - 1);
-  __builtin_amdgcn_global_load_lds((gptr_t)(a + m * lda + k0 + 8 * ch), (lptr_t)(xs + blk * 512), 16, 0, 0);
-}
-
-// ---- forward W side (row-contract): one chunk of 16 packed bytes per thread
+// ---- forward W side (row-contract): 16 packed bytes (32 elements of one row) per thread
 MOLT_DEV void fwd_row(int R, int64_t tn, bool pair, int& which, int64_t& n) {
   if (pair) {
     const int sub = (R >> 5) & 3;
@@ -628,73 +629,22 @@ MOLT_DEV void fwd_row(int R, int64_t tn, bool pair, int& which, int64_t& n) {
   }
 }
 
-struct WRReg { u32x4_t q[1]; float sc[1]; };
+struct WBytes { u32x4_t q; float sc; };
 
-MOLT_DEV void wr_issue(WRReg& w, const FwdParams& p, int64_t tn, bool pair, int64_t k0, int tid) {
-#pragma unroll
-  for (int c = 0; c < 1; ++c) {
-    const int idx = tid + NT * c;
-    const int R = idx >> 1, half = idx & 1;
-    int which; int64_t n;
-    fwd_row(R, tn, pair, which, n);
-    const int64_t flat = min(n, p.N - 1) * p.K + k0 + 32 * half;
-    w.q[c] = *reinterpret_cast<const u32x4_t*>(sel(p.packed, which) + (flat >> 1));
-    w.sc[c] = sel(p.scales, which)[flat >> 6];
-  }
+MOLT_DEV void w_lookup(const WBytes& w, const float2* tabc, int d, float2 (&c)[4]) {
+  const uint32_t q = w.q[d];
+  c[0] = tabc[(q & 0xffu) * TABC];
+  c[1] = tabc[((q >> 8) & 0xffu) * TABC];
+  c[2] = tabc[((q >> 16) & 0xffu) * TABC];
+  c[3] = tabc[(q >> 24) * TABC];
 }
 
-MOLT_DEV void wr_commit(const WRReg& w, uint16_t* ws, const float2* tab, int tid) {
+// bf16(code * scale) of 8 elements (the rounding of dequantize_4bit) into chunk 4 * half + d of row R.
+MOLT_DEV void w_finish(const float2 (&c)[4], float sc, uint16_t* ws, int tid, int d) {
+  u32x4_t o;
 #pragma unroll
-  for (int c = 0; c < 1; ++c) {
-    const int idx = tid + NT * c;
-    const int R = idx >> 1, half = idx & 1;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const uint32_t q = w.q[c][d];
-      u32x4_t o;
-      o[0] = dequant_pair(tab, q & 0xffu, w.sc[c]);
-      o[1] = dequant_pair(tab, (q >> 8) & 0xffu, w.sc[c]);
-      o[2] = dequant_pair(tab, (q >> 16) & 0xffu, w.sc[c]);
-      o[3] = dequant_pair(tab, q >> 24, w.sc[c]);
-      *reinterpret_cast<u32x4_t*>(ws + loff(R, 4 * half + d)) = o;
-    }
-  }
-}
-
-// ---- backward W side (column-contract): one 8-row x 8-column patch per thread
-struct WCReg { uint32_t q[4]; float sc[4]; };
-
-MOLT_DEV void wc_issue(WCReg& w, const BwdParams& p, int seg, int64_t tn, int64_t c0, int tid) {
-  const int cg = tid & 31, rg = tid >> 5;     // 32 column groups of 8, 16 row groups of 4
-  const int64_t col = min(tn * BN + 8 * cg, p.Kw - 8);
-  const uint8_t* packed = sel(p.packed, seg);
-  const float* scales = sel(p.scales, seg);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t flat = (c0 + 4 * rg + r) * p.Kw + col;
-    w.q[r] = *reinterpret_cast<const uint32_t*>(packed + (flat >> 1));
-    w.sc[r] = scales[flat >> 6];
-  }
-}
-
-MOLT_DEV void wc_commit(const WCReg& w, uint16_t* ws, const float2* tab, int tid) {
-  const int cg = tid & 31, rg = tid >> 5;
-  float v[4][8];
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const float2 c = tab[(w.q[r] >> (8 * b)) & 0xffu];
-      v[r][2 * b] = c.x * w.sc[r];
-      v[r][2 * b + 1] = c.y * w.sc[r];
-    }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    u32x2_t o;
-    o[0] = pack_bf16x2(v[0][j], v[1][j]);
-    o[1] = pack_bf16x2(v[2][j], v[3][j]);
-    *reinterpret_cast<u32x2_t*>(ws + loff(8 * cg + j, rg >> 1) + 4 * (rg & 1)) = o;
-  }
+  for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(c[e].x * sc, c[e].y * sc);
+  *reinterpret_cast<u32x4_t*>(ws + loff(tid >> 1, 4 * (tid & 1) + d)) = o;
 }
 
 // ---- staging of the LoRA contraction steps (swizzled layout). Each thread
@@ -759,6 +709,373 @@ MOLT_DEV void lora_wrow_stage(uint16_t* ws, const FwdParams& p, int64_t tn, bool
   }
 }
 
+// ---- epilogue staging of the 256 x 256 output tile in the four operand
+// buffers (64 rows each, unpadded), 16-byte chunks XOR-swizzled by row so the
+// column-strided fragment writes and the row-wise 16-byte reads are both
+// conflict-free.
+struct EpTile { uint16_t* b0; uint16_t* b1; uint16_t* b2; uint16_t* b3; };
+
+MOLT_DEV uint16_t* ep_at(const EpTile& e, int row, int col) {
+  const int c = row >> 6;
+  uint16_t* base = c == 0 ? e.b0 : c == 1 ? e.b1 : c == 2 ? e.b2 : e.b3;
+  return base + (row & 63) * 256 + ((((col >> 3) ^ (row & 31)) << 3) | (col & 7));
+}
+
+// Pair layout: subtiles 0,1 of a wave are gate and 2,3 the up rows of the same
+// 64 intermediate columns. Staged as [X row][c] with c in 0..127 = gate of
+// intermediate column tn*128 + c and 128 + c = up of the same column.
+MOLT_DEV void stage_acc_pair(const EpTile& ep, const f32x16_t (&acc)[TM][TN], int wm, int wn, int lane) {
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int row = wm * WCOLS + j * 32 + (lane & 31);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int col = (i >> 1) * 128 + wn * 64 + (i & 1) * 32 + 8 * g + 4 * (lane >> 5);
+        u32x2_t o = {pack_bf16x2(acc[i][j][4 * g], acc[i][j][4 * g + 1]),
+                     pack_bf16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3])};
+        *reinterpret_cast<u32x2_t*>(ep_at(ep, row, col)) = o;
+      }
+  }
+}
+
+MOLT_DEV void gateup_store(const EpTile& ep, const FwdParams& p, int64_t m0, int64_t tn, int tid) {
+  // 256 rows x 16 chunks of 8 intermediate columns
+#pragma unroll
+  for (int it = 0; it < BM * 16 / NT; ++it) {
+    const int q = tid + it * NT;
+    const int row = q >> 4, ch = q & 15;
+    const int64_t m = m0 + row, n = tn * (BN / 2) + 8 * ch;
+    if (m >= p.M || n >= p.N) continue;
+    const u32x4_t gw = *reinterpret_cast<const u32x4_t*>(ep_at(ep, row, 8 * ch));
+    const u32x4_t uw = *reinterpret_cast<const u32x4_t*>(ep_at(ep, row, 128 + 8 * ch));
+    u32x4_t hw;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float h0 = round_bf16(silu_f32(bf16_lo(gw[e]))) * bf16_lo(uw[e]);
+      const float h1 = round_bf16(silu_f32(bf16_hi(gw[e]))) * bf16_hi(uw[e]);
+      hw[e] = pack_bf16x2(h0, h1);
+    }
+    const int64_t off = m * p.ldy + n;
+    if (p.vec_out && n + 8 <= p.N) {
+      *reinterpret_cast<u32x4_t*>(p.y[0] + off) = gw;
+      *reinterpret_cast<u32x4_t*>(p.y[1] + off) = uw;
+      *reinterpret_cast<u32x4_t*>(p.y[2] + off) = hw;
+    } else {
+      for (int e = 0; e < 8 && n + e < p.N; ++e) {
+        const int w = e >> 1, sh = (e & 1) * 16;
+        p.y[0][off + e] = (uint16_t)(gw[w] >> sh);
+        p.y[1][off + e] = (uint16_t)(uw[w] >> sh);
+        p.y[2][off + e] = (uint16_t)(hw[w] >> sh);
+      }
+    }
+  }
+}
+
+// Forward NF4 GEMM, 256 x 256 tile, 8 waves of 128 (W rows) x 64 (X rows).
+//
+// Pipeline of step s (BK = 64 contraction elements), all from LDS buffer s&1:
+//  * the fragments of sub-step 0 are read while the MFMAs of the previous
+//    step's last sub-step run (those fragments were held in registers across
+//    the barrier, so the matrix core does not drain at every step);
+//  * X(s+1) streams global -> LDS (buffer-load DMA) into the other buffer;
+//  * the packed bytes of W(s+2) load into one register set while W(s+1), in
+//    the other, is dequantised into the other W buffer a quarter per
+//    sub-step, each quarter's table lookups one sub-step ahead of its use;
+//  * one vmcnt(0) + barrier at the end of the step.
+// Each operand buffer is its own __shared__ array and the loop is unrolled so
+// that buffer choice is static: the compiler can then tell the LDS reads of
+// one buffer from the DMA into the other and inserts no waits between them.
+// Requires K % 128 == 0 (an even number of steps) and block size 64.
+template <bool PAIR>
+__global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t xb0[BUF], xb1[BUF], wb0[BUF], wb1[BUF];
+  __shared__ float2 tab[256 * TABC];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+  const int64_t cols_per_tile = PAIR ? BN / 2 : BN;
+  const int64_t nt_m = ceil_div64(p.M, BM), nt_n = ceil_div64(p.N, cols_per_tile);
+  int64_t tm, tn;
+  grouped_tile(xcd_tile(blockIdx.x, nt_m * nt_n), nt_m, nt_n, GROUP_M, tm, tn);
+  const int64_t m0 = tm * BM;
+  build_tab(tab, p.code, p.order, tid);
+  const float2* tabc = tab + (lane & (TABC - 1));
+
+  FragOff fo;
+  frag_offsets(fo, wn * WROWS, wm * WCOLS, lane);
+  f32x16_t acc[TM][TN];
+  zero_acc(acc);
+
+  // X: the 16-byte slot each lane fills in the 1 KB blocks its wave owns.
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, ((p.M - 1) * p.ldx + p.K) * 2);
+  uint32_t xoff[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    int R, k;
+    dma_slot(wave * 4 + c, lane, R, k);
+    xoff[c] = (uint32_t)((min(m0 + R, p.M - 1) * p.ldx + k) * 2);
+  }
+  // W: row R = tid / 2, bytes [16 * half, +16) of the row's 32-byte slice of
+  // the step; the weight (gate or up) is uniform over a wave.
+  int which; int64_t n;
+  fwd_row(tid >> 1, tn, PAIR, which, n);
+  which = __builtin_amdgcn_readfirstlane(which);
+  n = min(n, p.N - 1);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(which ? p.packed[1] : p.packed[0], p.N * p.K / 2);
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(which ? p.scales[1] : p.scales[0], p.N * p.K / 64 * 4);
+  const uint32_t woff = (uint32_t)(n * p.K / 2 + 16 * (tid & 1));
+  const uint32_t soff = (uint32_t)(n * p.K / 64 * 4);
+
+  auto x_load = [&](uint16_t* dst, int64_t k0) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) buf_load_lds16(xr, dst + (wave * 4 + c) * 512, xoff[c], (uint32_t)(k0 * 2));
+  };
+  auto w_load = [&](WBytes& w, int64_t k0) {
+    w.q = buf_load16(wr, woff, (uint32_t)(k0 >> 1));
+    w.sc = __builtin_bit_cast(float, buf_load4(sr, soff, (uint32_t)((k0 >> 6) * 4)));
+  };
+
+  const int ks = (int)(p.K / BK);
+  const int64_t klast = p.K - BK;
+  WBytes r0, r1;
+  x_load(xb0, 0);
+  w_load(r0, 0);
+  wait_vm0();
+  __syncthreads();  // table, X(0)
+  {
+    float2 c[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) { w_lookup(r0, tabc, d, c); w_finish(c, r0.sc, wb0, tid, d); }
+  }
+  w_load(r0, min((int64_t)BK, klast));
+  wait_vm0();
+  __syncthreads();
+
+  bf16x8_t a[2][TM], b[2][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) a[1][i] = bf16x8_t{};
+#pragma unroll
+  for (int j = 0; j < TN; ++j) b[1][j] = bf16x8_t{};
+
+  auto step = [&](int s, const WBytes& cw, WBytes& nw, const uint16_t* xc, const uint16_t* wc, uint16_t* xn,
+                  uint16_t* wnx) {
+    const int64_t k1 = min((int64_t)(s + 1) * BK, klast), k2 = min((int64_t)(s + 2) * BK, klast);
+    float2 c[4];
+    load_frags(wc, xc, fo, 0, a[0], b[0]);
+    mfma_set(a[1], b[1], acc);
+    x_load(xn, k1);
+    w_load(nw, k2);
+    w_lookup(cw, tabc, 0, c);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < 3; ++kk) {
+      load_frags(wc, xc, fo, kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
+      mfma_set(a[kk & 1], b[kk & 1], acc);
+      w_finish(c, cw.sc, wnx, tid, kk);
+      w_lookup(cw, tabc, kk + 1, c);
+      interleave_substep();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    w_finish(c, cw.sc, wnx, tid, 3);
+    wait_vm0();
+    __syncthreads();
+  };
+  // W(s + 1) sits in r0 during even steps and in r1 during odd ones; the LDS buffers alternate likewise.
+  for (int s = 0; s < ks; s += 2) {
+    step(s, r0, r1, xb0, wb0, xb1, wb1);
+    step(s + 1, r1, r0, xb1, wb1, xb0, wb0);
+  }
+  mfma_set(a[1], b[1], acc);
+  for (int64_t c0 = 0; c0 < p.lr; c0 += BK) {
+    lora_a_stage(xb0, p.t, p.ldt, m0, p.M, c0, p.lr, tid);
+    lora_wrow_stage(wb0, p, tn, PAIR, c0, tid);
+    __syncthreads();
+    compute(wb0, xb0, fo, acc);
+    __syncthreads();
+  }
+
+  if (!PAIR) {
+    const bool vec = p.vec_out != 0;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t m = m0 + wm * WCOLS + j * 32 + (lane & 31);
+      if (m >= p.M) continue;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int64_t nn = tn * BN + wn * WROWS + i * 32 + 8 * g + 4 * (lane >> 5);
+          float v[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+          store4(p.y[0], p.ldy, m, nn, p.N, v, vec);
+        }
+      }
+    }
+    return;
+  }
+  // Gate/up pair: stage bf16 gate and up of the tile in LDS, then form
+  // h = bf16(bf16(silu(g)) u) cooperatively with 16-byte loads and stores.
+  const EpTile ep{xb0, xb1, wb0, wb1};
+  stage_acc_pair(ep, acc, wm, wn, lane);
+  __syncthreads();
+  gateup_store(ep, p, m0, tn, tid);
+}
+
+// ===== backward (column-contract) kernel =====
+// The backward tile keeps the layout it was tuned for: rows of 128 B with the
+// 16-byte chunk position XOR-swizzled by (R ^ R >> 3) & 7 (the transposed
+// 8-byte dequant writes of consecutive output columns spread over the banks).
+namespace bwd {
+MOLT_DEV int loff(int R, int c) { return R * LD + ((c ^ ((R ^ (R >> 3)) & 7)) << 3); }
+MOLT_DEV void dma_slot(int blk, int lane, int& R, int& k) {
+  const int pos = blk * 64 + lane;
+  R = pos >> 3;
+  k = 8 * ((pos & 7) ^ ((R ^ (R >> 3)) & 7));
+}
+MOLT_DEV void b_load_frags(const uint16_t* __restrict__ ws, const uint16_t* __restrict__ xs, const FragOff& f, int kk,
+                         bf16x8_t (&a)[TM], bf16x8_t (&b)[TN]) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+    a[i] = *reinterpret_cast<const bf16x8_t*>(ws + loff(f.arow + 32 * i, 2 * kk + f.h));
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+    b[j] = *reinterpret_cast<const bf16x8_t*>(xs + loff(f.brow + 32 * j, 2 * kk + f.h));
+}
+MOLT_DEV void b_compute(const uint16_t* __restrict__ ws, const uint16_t* __restrict__ xs, const FragOff& f,
+                      f32x16_t (&acc)[TM][TN]) {
+  bf16x8_t a[2][TM], b[2][TN];
+  b_load_frags(ws, xs, f, 0, a[0], b[0]);
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    if (kk < 3) b_load_frags(ws, xs, f, kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
+    mfma_set(a[kk & 1], b[kk & 1], acc);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+MOLT_DEV void b_lora_a_stage(uint16_t* xs, const uint16_t* __restrict__ t, int64_t ldt, int64_t m0, int64_t M,
+                           int64_t c0, int64_t L, int tid) {
+  constexpr int CH = BM * (BK / 8) / NT;
+  const bool vec = al16(t) && ldt % 8 == 0;
+  u32x4_t v[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int q = tid + NT * c, R = q >> 3, ch = q & 7;
+    const int64_t m = m0 + R, k = c0 + 8 * ch;
+    if (vec && m < M && k + 8 <= L) {
+      v[c] = *reinterpret_cast<const u32x4_t*>(t + m * ldt + k);
+    } else {
+      uint16_t e[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) e[i] = (m < M && k + i < L) ? t[m * ldt + k + i] : (uint16_t)0;
+      v[c] = __builtin_bit_cast(u32x4_t, e);
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int q = tid + NT * c;
+    *reinterpret_cast<u32x4_t*>(xs + loff(q >> 3, q & 7)) = v[c];
+  }
+}
+struct Smem {
+  union {
+    struct {
+      uint16_t xs[2][BM * LD];
+      uint16_t ws[2][BN * LD];
+      float2 tab[256];
+    };
+    uint16_t ep[BM * EP_LD];       // epilogue staging, reused after the main loop
+  };
+};
+
+// ---- X side (row-major, contraction contiguous): direct global -> LDS loads.
+// global_load_lds_dwordx4 writes lane l's 16 bytes to LDS at M0 + 16 l, so
+// each wave-level load fills one contiguous 1 KB of the tile; every lane
+// fetches the global chunk whose swizzled LDS slot is its own. No VGPRs hold
+// X and no LDS store instructions are issued for it. Loads are branch-free:
+// an out-of-range row is clamped to the last valid one (such rows only reach
+// output rows the epilogue never stores).
+typedef __attribute__((address_space(1))) const void* gptr_t;
+typedef __attribute__((address_space(3))) void* lptr_t;
+
+MOLT_DEV void x_issue_lds(uint16_t* xs, const uint16_t* __restrict__ a, int64_t lda, int64_t m0, int64_t M,
+                          int64_t k0, int wave, int lane) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int blk = wave * 4 + c;            // 1 KB block of the 32 KB tile
+    int R, k;
+    dma_slot(blk, lane, R, k);
+    const int64_t m = min(m0 + R, M - 1);
+    __builtin_amdgcn_global_load_lds((gptr_t)(a + m * lda + k0 + k), (lptr_t)(xs + blk * 512), 16, 0, 0);
+  }
+}
+
+MOLT_DEV void x_issue_lds_one(uint16_t* xs, const uint16_t* __restrict__ a, int64_t lda, int64_t m0, int64_t M,
+                              int64_t k0, int wave, int lane, int c) {
+  const int blk = wave * 4 + c;            // 1 KB block of the 32 KB tile
+  int R, k;
+  dma_slot(blk, lane, R, k);
+  const int64_t m = min(m0 + R, M - 1);
+  __builtin_amdgcn_global_load_lds((gptr_t)(a + m * lda + k0 + k), (lptr_t)(xs + blk * 512), 16, 0, 0);
+}
+
+// One BK step whose MFMA sub-steps carry the staging of the next step: the
+// stage callback runs before sub-step kk's MFMAs (the scheduling barrier keeps
+// its memory instructions there instead of hoisting them all to the top),
+// so the next step's loads and dequantisation overlap this step's MFMAs.
+template <typename F>
+MOLT_DEV void compute_staged(const uint16_t* __restrict__ ws, const uint16_t* __restrict__ xs, const FragOff& f,
+                             f32x16_t (&acc)[TM][TN], F&& stage) {
+  bf16x8_t a[2][TM], b[2][TN];
+  b_load_frags(ws, xs, f, 0, a[0], b[0]);
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    stage(kk);
+    if (kk < 3) b_load_frags(ws, xs, f, kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kk & 1][i], b[kk & 1][j], acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// ---- backward W side (column-contract): one 8-row x 8-column patch per thread
+struct WCReg { uint32_t q[4]; float sc[4]; };
+
+MOLT_DEV void wc_issue(WCReg& w, const BwdParams& p, int seg, int64_t tn, int64_t c0, int tid) {
+  const int cg = tid & 31, rg = tid >> 5;     // 32 column groups of 8, 16 row groups of 4
+  const int64_t col = min(tn * BN + 8 * cg, p.Kw - 8);
+  const uint8_t* packed = sel(p.packed, seg);
+  const float* scales = sel(p.scales, seg);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t flat = (c0 + 4 * rg + r) * p.Kw + col;
+    w.q[r] = *reinterpret_cast<const uint32_t*>(packed + (flat >> 1));
+    w.sc[r] = scales[flat >> 6];
+  }
+}
+
+MOLT_DEV void wc_commit(const WCReg& w, uint16_t* ws, const float2* tab, int tid) {
+  const int cg = tid & 31, rg = tid >> 5;
+  float v[4][8];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const float2 c = tab[(w.q[r] >> (8 * b)) & 0xffu];
+      v[r][2 * b] = c.x * w.sc[r];
+      v[r][2 * b + 1] = c.y * w.sc[r];
+    }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    u32x2_t o;
+    o[0] = pack_bf16x2(v[0][j], v[1][j]);
+    o[1] = pack_bf16x2(v[2][j], v[3][j]);
+    *reinterpret_cast<u32x2_t*>(ws + loff(8 * cg + j, rg >> 1) + 4 * (rg & 1)) = o;
+  }
+}
+
 // Backward W side: element (output column R, rank c0 + k) = bf16(scale * A[c0 + k][col]).
 // A thread loads a 4-rank x 8-column patch of A (16-byte loads along the
 // columns) and transposes it so the ranks become contiguous in LDS.
@@ -807,56 +1124,6 @@ MOLT_DEV void stage_acc(uint16_t* ep, const f32x16_t (&acc)[TM][TN], int wm, int
                      pack_bf16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3])};
         *reinterpret_cast<u32x2_t*>(ep + row * EP_LD + col) = o;
       }
-  }
-}
-
-// Pair layout: subtiles 0,1 of a wave are gate and 2,3 the up rows of the same
-// 64 intermediate columns. Staged as ep[X row][c] with c in 0..127 = gate of
-// intermediate column tn*128 + c and 128 + c = up of the same column.
-MOLT_DEV void stage_acc_pair(uint16_t* ep, const f32x16_t (&acc)[TM][TN], int wm, int wn, int lane) {
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int row = wm * WCOLS + j * 32 + (lane & 31);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int col = (i >> 1) * 128 + wn * 64 + (i & 1) * 32 + 8 * g + 4 * (lane >> 5);
-        u32x2_t o = {pack_bf16x2(acc[i][j][4 * g], acc[i][j][4 * g + 1]),
-                     pack_bf16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3])};
-        *reinterpret_cast<u32x2_t*>(ep + row * EP_LD + col) = o;
-      }
-  }
-}
-
-MOLT_DEV void gateup_store(const uint16_t* ep, const FwdParams& p, int64_t m0, int64_t tn, int tid) {
-  // 256 rows x 16 chunks of 8 intermediate columns
-  for (int q = tid; q < BM * 16; q += NT) {
-    const int row = q >> 4, ch = q & 15;
-    const int64_t m = m0 + row, n = tn * (BN / 2) + 8 * ch;
-    if (m >= p.M || n >= p.N) continue;
-    const u32x4_t gw = *reinterpret_cast<const u32x4_t*>(ep + row * EP_LD + 8 * ch);
-    const u32x4_t uw = *reinterpret_cast<const u32x4_t*>(ep + row * EP_LD + 128 + 8 * ch);
-    u32x4_t hw;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float h0 = round_bf16(silu_f32(bf16_lo(gw[e]))) * bf16_lo(uw[e]);
-      const float h1 = round_bf16(silu_f32(bf16_hi(gw[e]))) * bf16_hi(uw[e]);
-      hw[e] = pack_bf16x2(h0, h1);
-    }
-    const int64_t off = m * p.ldy + n;
-    if (p.vec_out && n + 8 <= p.N) {
-      *reinterpret_cast<u32x4_t*>(p.y[0] + off) = gw;
-      *reinterpret_cast<u32x4_t*>(p.y[1] + off) = uw;
-      *reinterpret_cast<u32x4_t*>(p.y[2] + off) = hw;
-    } else {
-      for (int e = 0; e < 8 && n + e < p.N; ++e) {
-        const int w = e >> 1, sh = (e & 1) * 16;
-        p.y[0][off + e] = (uint16_t)(gw[w] >> sh);
-        p.y[1][off + e] = (uint16_t)(uw[w] >> sh);
-        p.y[2][off + e] = (uint16_t)(hw[w] >> sh);
-      }
-    }
   }
 }
 
@@ -910,87 +1177,6 @@ MOLT_DEV void swiglu_bwd_store(const uint16_t* ep, const BwdParams& p, int64_t m
   }
 }
 
-template <bool PAIR>
-__global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
-  __shared__ Smem sm;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
-  const int64_t cols_per_tile = PAIR ? BN / 2 : BN;
-  const int64_t nt_m = ceil_div64(p.M, BM), nt_n = ceil_div64(p.N, cols_per_tile);
-  int64_t tm, tn;
-  grouped_tile(xcd_tile(blockIdx.x, nt_m * nt_n), nt_m, nt_n, GROUP_M, tm, tn);
-  const int64_t m0 = tm * BM;
-  build_pair_table(sm.tab, p.code, p.order);
-
-  FragOff fo;
-  frag_offsets(fo, wn * WROWS, wm * WCOLS, lane);
-  f32x16_t acc[TM][TN];
-  zero_acc(acc);
-
-  // One-deep prefetch: X of step s+1 streams straight into the other LDS
-  // buffer and the packed NF4 bytes of step s+1 into registers while the
-  // MFMAs of step s run; the bytes are then dequantised into LDS.
-  const int ks = (int)(p.K / BK);
-  WRReg wr;
-  x_issue_lds(sm.xs[0], p.x, p.ldx, m0, p.M, 0, wave, lane);
-  wr_issue(wr, p, tn, PAIR, 0, tid);
-  __syncthreads();  // pair table
-  wr_commit(wr, sm.ws[0], sm.tab, tid);
-  __syncthreads();
-  for (int s = 0; s + 1 < ks; ++s) {
-    const int cur = s & 1;
-    const int64_t k1 = (int64_t)(s + 1) * BK;
-    compute_staged(sm.ws[cur], sm.xs[cur], fo, acc, [&](int kk) {
-      if (kk == 0) {
-        wr_issue(wr, p, tn, PAIR, k1, tid);
-        x_issue_lds_one(sm.xs[cur ^ 1], p.x, p.ldx, m0, p.M, k1, wave, lane, 0);
-        x_issue_lds_one(sm.xs[cur ^ 1], p.x, p.ldx, m0, p.M, k1, wave, lane, 1);
-      } else if (kk == 1) {
-        x_issue_lds_one(sm.xs[cur ^ 1], p.x, p.ldx, m0, p.M, k1, wave, lane, 2);
-        x_issue_lds_one(sm.xs[cur ^ 1], p.x, p.ldx, m0, p.M, k1, wave, lane, 3);
-      } else if (kk == 3) {
-        wr_commit(wr, sm.ws[cur ^ 1], sm.tab, tid);
-      }
-    });
-    __syncthreads();
-  }
-  compute(sm.ws[(ks - 1) & 1], sm.xs[(ks - 1) & 1], fo, acc);
-  __syncthreads();
-  for (int64_t c0 = 0; c0 < p.lr; c0 += BK) {
-    lora_a_stage(sm.xs[0], p.t, p.ldt, m0, p.M, c0, p.lr, tid);
-    lora_wrow_stage(sm.ws[0], p, tn, PAIR, c0, tid);
-    __syncthreads();
-    compute(sm.ws[0], sm.xs[0], fo, acc);
-    __syncthreads();
-  }
-
-  if (!PAIR) {
-    const bool vec = p.vec_out != 0;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t m = m0 + wm * WCOLS + j * 32 + (lane & 31);
-      if (m >= p.M) continue;
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int64_t n = tn * BN + wn * WROWS + i * 32 + 8 * g + 4 * (lane >> 5);
-          float v[4] = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-          store4(p.y[0], p.ldy, m, n, p.N, v, vec);
-        }
-      }
-    }
-    return;
-  }
-  // Gate/up pair: stage bf16 gate (columns 0..127) and up (128..255) of the
-  // tile in LDS, then form h = bf16(bf16(silu(g)) u) cooperatively with
-  // 16-byte loads and stores.
-  // (the LoRA tail ended with a barrier, so the LDS operand buffers are free)
-  stage_acc_pair(sm.ep, acc, wm, wn, lane);
-  __syncthreads();
-  gateup_store(sm.ep, p, m0, tn, tid);
-}
-
 template <int EPI>
 __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
   __shared__ Smem sm;
@@ -1034,14 +1220,14 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
     });
     __syncthreads();
   }
-  compute(sm.ws[(ks - 1) & 1], sm.xs[(ks - 1) & 1], fo, acc);
+  b_compute(sm.ws[(ks - 1) & 1], sm.xs[(ks - 1) & 1], fo, acc);
   __syncthreads();
   for (int seg = 0; seg < p.nseg && p.r > 0; ++seg) {
     for (int64_t c0 = 0; c0 < p.r; c0 += BK) {
-      lora_a_stage(sm.xs[0], sel(p.u, seg), p.ldu, m0, p.M, c0, p.r, tid);
+      b_lora_a_stage(sm.xs[0], sel(p.u, seg), p.ldu, m0, p.M, c0, p.r, tid);
       lora_wcol_stage(sm.ws[0], p, seg, tn, c0, tid);
       __syncthreads();
-      compute(sm.ws[0], sm.xs[0], fo, acc);
+      b_compute(sm.ws[0], sm.xs[0], fo, acc);
       __syncthreads();
     }
   }
@@ -1071,6 +1257,7 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
   swiglu_bwd_store(sm.ep, p, m0, tn, tid);
 }
 
+}  // namespace bwd
 }  // namespace big
 
 // ------------------------------------------------------------- host helpers
@@ -1138,7 +1325,12 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
   const bool al = (p.K % 64 == 0) && p.block_size == 64 && ldx % 8 == 0 && aligned(x, 16) &&
                   aligned(w0->packed, 16) && (!pair || aligned(w1->packed, 16));
   const int64_t big_tiles = ceil_div64(M, big::BM) * ceil_div64(p.N, pair ? big::BN / 2 : big::BN);
-  if (al && big_tiles >= big_tile_min()) {
+  // The 256 x 256 kernel runs an even number of 64-deep steps and addresses X,
+  // the packed bytes and the scales through 32-bit buffer offsets.
+  const int64_t lim = 0x7fffffffll;
+  const bool big_ok = al && p.K % 128 == 0 && ((M - 1) * ldx + p.K) * 2 <= lim && p.N * p.K / 2 <= lim &&
+                      p.N * p.K / 16 <= lim;
+  if (big_ok && big_tiles >= big_tile_min()) {
     MOLT_REQUIRE(big_tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
     dim3 grid((unsigned)big_tiles), block(big::NT);
     if (pair) hipLaunchKernelGGL((big::fwd_kernel<true>), grid, block, 0, stream, p);
@@ -1211,8 +1403,8 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
       big_tiles >= big_tile_min()) {
     MOLT_REQUIRE(big_tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
     dim3 grid((unsigned)big_tiles), block(big::NT);
-    if (swiglu) hipLaunchKernelGGL((big::bwd_kernel<EPI_SWIGLU_BWD>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((big::bwd_kernel<EPI_STORE>), grid, block, 0, stream, p);
+    if (swiglu) hipLaunchKernelGGL((big::bwd::bwd_kernel<EPI_SWIGLU_BWD>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((big::bwd::bwd_kernel<EPI_STORE>), grid, block, 0, stream, p);
     return check_launch(who);
   }
   const int64_t tiles = ceil_div64(M, BM) * ceil_div64(p.Kw, BN);
