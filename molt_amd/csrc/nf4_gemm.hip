@@ -509,22 +509,31 @@ constexpr int BUF = BM * LD;     // bf16 elements of one operand buffer (32 KB)
 constexpr int TABC = 16;         // interleaved copies of the code-pair table
 constexpr int EP_LD = 256 + 8;   // (128 x 128 path and backward) epilogue tile row stride
 
-// Operand buffer layout. A row holds 64 contraction elements as 8 chunks of
-// 16 B; chunks 0-3 (elements 0..31) of all rows form the first 16 KB half of
-// the buffer, chunks 4-7 the second. Within a half a row is 64 B and its four
-// chunk positions are XOR-swizzled by (R >> 2) & 3, so a ds_read_b128 of one
-// chunk over 16 consecutive rows hits 16 distinct bank groups. Rows 32 apart
-// share the swizzle and the halves are a constant 16 KB apart, so every
-// fragment read of a step is one of two per-lane base addresses plus an
-// immediate offset.
-MOLT_DEV int loff(int R, int c) { return (c >> 2) * (BUF / 2) + R * 32 + (((c & 3) ^ ((R >> 2) & 3)) << 3); }
+// Operand buffer layout. A tile row holds 64 contraction elements as 8 chunks
+// of 16 B; chunks 0-3 (elements 0..31) of all rows form the first 16 KB half of
+// the buffer, chunks 4-7 the second. Within a half a row is 64 B. Row R is
+// stored at physical row P = R ^ ((R >> 3) & 3) and its four chunk positions
+// are XOR-swizzled by ((P >> 2) ^ (P >> 7)) & 3. Then
+//  * a ds_read_b128 of one chunk over 16 consecutive rows hits 16 distinct
+//    bank groups (the fragment reads),
+//  * 16-byte writes of one chunk over 32 consecutive rows, and 4-byte writes of
+//    32 rows spaced 8 apart (the backward's transposed dequant), spread over
+//    all 64 banks,
+//  * rows 32 apart inside a 128-row block differ by a constant, so with the
+//    halves a constant 16 KB apart every fragment read of a step is one of two
+//    per-lane base offsets plus an immediate.
+MOLT_DEV int loff(int R, int c) {
+  const int P = R ^ ((R >> 3) & 3);
+  return (c >> 2) * (BUF / 2) + P * 32 + ((((c & 3) ^ (P >> 2) ^ (P >> 7)) & 3) << 3);
+}
 
 // Global -> LDS DMA writes lane l's 16 bytes to (block base + 16 l): block blk
-// (1 KB) of a buffer holds 16 rows of one half. Returns the row and first
-// contraction element the lane must fetch for that slot.
+// (1 KB) of a buffer holds physical rows 16 (blk & 15) .. +15 of half blk >> 4.
+// Returns the tile row and first contraction element the lane must fetch.
 MOLT_DEV void dma_slot(int blk, int lane, int& R, int& k) {
-  R = ((blk & 15) << 4) + (lane >> 2);
-  k = 32 * (blk >> 4) + 8 * ((lane & 3) ^ ((R >> 2) & 3));
+  const int P = ((blk & 15) << 4) + (lane >> 2);
+  R = P ^ ((P >> 3) & 3);
+  k = 32 * (blk >> 4) + 8 * (((lane & 3) ^ (P >> 2) ^ (P >> 7)) & 3);
 }
 
 // Kernel-argument pointers and the 16 codes stay in scalar registers or are
@@ -563,22 +572,30 @@ MOLT_DEV void build_tab(float2* tab, const float* __restrict__ code, int order, 
   }
 }
 
-struct FragOff { int arow, brow, h; };
+// Per-lane fragment offsets: lane l supplies row (l % 32) of each 32-row
+// subtile and the 8-element half (l / 32) of a 16-deep sub-step. Sub-step kk
+// reads chunk 2 kk + l / 32: its offset is base[kk & 1] + (kk >> 1) * BUF / 2,
+// and subtile i adds 32 rows = 1024 elements.
+struct FragOff { int a[2], b[2]; };
 
 MOLT_DEV void frag_offsets(FragOff& f, int arow0, int brow0, int lane) {
-  f.arow = arow0 + (lane & 31);
-  f.brow = brow0 + (lane & 31);
-  f.h = lane >> 5;
+  const int h = lane >> 5;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    f.a[q] = loff(arow0 + (lane & 31), 2 * q + h);
+    f.b[q] = loff(brow0 + (lane & 31), 2 * q + h);
+  }
 }
 
 MOLT_DEV void load_frags(const uint16_t* __restrict__ ws, const uint16_t* __restrict__ xs, const FragOff& f, int kk,
                          bf16x8_t (&a)[TM], bf16x8_t (&b)[TN]) {
+  const int hoff = (kk >> 1) * (BUF / 2);
 #pragma unroll
   for (int i = 0; i < TM; ++i)
-    a[i] = *reinterpret_cast<const bf16x8_t*>(ws + loff(f.arow + 32 * i, 2 * kk + f.h));
+    a[i] = *reinterpret_cast<const bf16x8_t*>(ws + f.a[kk & 1] + hoff + 1024 * i);
 #pragma unroll
   for (int j = 0; j < TN; ++j)
-    b[j] = *reinterpret_cast<const bf16x8_t*>(xs + loff(f.brow + 32 * j, 2 * kk + f.h));
+    b[j] = *reinterpret_cast<const bf16x8_t*>(xs + f.b[kk & 1] + hoff + 1024 * j);
 }
 
 MOLT_DEV void mfma_set(const bf16x8_t (&a)[TM], const bf16x8_t (&b)[TN], f32x16_t (&acc)[TM][TN]) {
@@ -922,163 +939,56 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
 }
 
 // ===== backward (column-contract) kernel =====
-// The backward tile keeps the layout it was tuned for: rows of 128 B with the
-// 16-byte chunk position XOR-swizzled by (R ^ R >> 3) & 7 (the transposed
-// 8-byte dequant writes of consecutive output columns spread over the banks).
-namespace bwd {
-MOLT_DEV int loff(int R, int c) { return R * LD + ((c ^ ((R ^ (R >> 3)) & 7)) << 3); }
-MOLT_DEV void dma_slot(int blk, int lane, int& R, int& k) {
-  const int pos = blk * 64 + lane;
-  R = pos >> 3;
-  k = 8 * ((pos & 7) ^ ((R ^ (R >> 3)) & 7));
+// dX[M, Kw] = sum over segments of dY_seg[M, Nw] . deq(W_seg[Nw, Kw]) (+ LoRA).
+// A tile row on the W side is an output column (a column of W); the
+// contraction runs over rows of W. A thread dequantises a 4-row x 8-column
+// patch (four 4-byte loads, one scale per row) and writes it transposed: rows
+// (0, 1) and (2, 3) of the patch become bf16 pairs in 8 consecutive tile rows.
+struct WPatch { uint32_t q[4]; float sc[4]; };
+
+// Lookups of byte b of the four patch rows: columns 2b, 2b + 1.
+MOLT_DEV void wp_lookup(const WPatch& w, const float2* tabc, int b, float2 (&c)[4]) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) c[r] = tabc[((w.q[r] >> (8 * b)) & 0xffu) * TABC];
 }
-MOLT_DEV void b_load_frags(const uint16_t* __restrict__ ws, const uint16_t* __restrict__ xs, const FragOff& f, int kk,
-                         bf16x8_t (&a)[TM], bf16x8_t (&b)[TN]) {
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-    a[i] = *reinterpret_cast<const bf16x8_t*>(ws + loff(f.arow + 32 * i, 2 * kk + f.h));
-#pragma unroll
-  for (int j = 0; j < TN; ++j)
-    b[j] = *reinterpret_cast<const bf16x8_t*>(xs + loff(f.brow + 32 * j, 2 * kk + f.h));
+
+// bf16(code * scale) of columns 2b and 2b + 1, each as two bf16 pairs (patch rows 0,1 and 2,3).
+MOLT_DEV void wp_finish(const float2 (&c)[4], const float (&sc)[4], u32x2_t& ce, u32x2_t& co) {
+  ce[0] = pack_bf16x2(c[0].x * sc[0], c[1].x * sc[1]);
+  ce[1] = pack_bf16x2(c[2].x * sc[2], c[3].x * sc[3]);
+  co[0] = pack_bf16x2(c[0].y * sc[0], c[1].y * sc[1]);
+  co[1] = pack_bf16x2(c[2].y * sc[2], c[3].y * sc[3]);
 }
-MOLT_DEV void b_compute(const uint16_t* __restrict__ ws, const uint16_t* __restrict__ xs, const FragOff& f,
-                      f32x16_t (&acc)[TM][TN]) {
-  bf16x8_t a[2][TM], b[2][TN];
-  b_load_frags(ws, xs, f, 0, a[0], b[0]);
+
+// Columns k and k + 4 of the thread's patch. Lanes l and l + 32 hold the two
+// 4-row halves (rg even / odd) of the same 8 contraction rows: one
+// v_permlane32_swap per dword gives lane l all 8 rows of column k and lane
+// l + 32 all 8 rows of column k + 4, written as one 16-byte chunk each.
+MOLT_DEV void wp_swap_write(const u32x2_t& lo, const u32x2_t& hi, uint16_t* ws, int cg, int rg, int k) {
+  u32x4_t o;
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    if (kk < 3) b_load_frags(ws, xs, f, kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
-    mfma_set(a[kk & 1], b[kk & 1], acc);
-    __builtin_amdgcn_sched_barrier(0);
+  for (int d = 0; d < 2; ++d) {
+    const auto r = __builtin_amdgcn_permlane32_swap(lo[d], hi[d], false, false);
+    o[d] = r[0];
+    o[2 + d] = r[1];
   }
-}
-MOLT_DEV void b_lora_a_stage(uint16_t* xs, const uint16_t* __restrict__ t, int64_t ldt, int64_t m0, int64_t M,
-                           int64_t c0, int64_t L, int tid) {
-  constexpr int CH = BM * (BK / 8) / NT;
-  const bool vec = al16(t) && ldt % 8 == 0;
-  u32x4_t v[CH];
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int q = tid + NT * c, R = q >> 3, ch = q & 7;
-    const int64_t m = m0 + R, k = c0 + 8 * ch;
-    if (vec && m < M && k + 8 <= L) {
-      v[c] = *reinterpret_cast<const u32x4_t*>(t + m * ldt + k);
-    } else {
-      uint16_t e[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) e[i] = (m < M && k + i < L) ? t[m * ldt + k + i] : (uint16_t)0;
-      v[c] = __builtin_bit_cast(u32x4_t, e);
-    }
-  }
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int q = tid + NT * c;
-    *reinterpret_cast<u32x4_t*>(xs + loff(q >> 3, q & 7)) = v[c];
-  }
-}
-struct Smem {
-  union {
-    struct {
-      uint16_t xs[2][BM * LD];
-      uint16_t ws[2][BN * LD];
-      float2 tab[256];
-    };
-    uint16_t ep[BM * EP_LD];       // epilogue staging, reused after the main loop
-  };
-};
-
-// ---- X side (row-major, contraction contiguous): direct global -> LDS loads.
-// global_load_lds_dwordx4 writes lane l's 16 bytes to LDS at M0 + 16 l, so
-// each wave-level load fills one contiguous 1 KB of the tile; every lane
-// fetches the global chunk whose swizzled LDS slot is its own. No VGPRs hold
-// X and no LDS store instructions are issued for it. Loads are branch-free:
-// an out-of-range row is clamped to the last valid one (such rows only reach
-// output rows the epilogue never stores).
-typedef __attribute__((address_space(1))) const void* gptr_t;
-typedef __attribute__((address_space(3))) void* lptr_t;
-
-MOLT_DEV void x_issue_lds(uint16_t* xs, const uint16_t* __restrict__ a, int64_t lda, int64_t m0, int64_t M,
-                          int64_t k0, int wave, int lane) {
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int blk = wave * 4 + c;            // 1 KB block of the 32 KB tile
-    int R, k;
-    dma_slot(blk, lane, R, k);
-    const int64_t m = min(m0 + R, M - 1);
-    __builtin_amdgcn_global_load_lds((gptr_t)(a + m * lda + k0 + k), (lptr_t)(xs + blk * 512), 16, 0, 0);
-  }
+  *reinterpret_cast<u32x4_t*>(ws + loff(8 * cg + k + 4 * (rg & 1), rg >> 1)) = o;
 }
 
-MOLT_DEV void x_issue_lds_one(uint16_t* xs, const uint16_t* __restrict__ a, int64_t lda, int64_t m0, int64_t M,
-                              int64_t k0, int wave, int lane, int c) {
-  const int blk = wave * 4 + c;            // 1 KB block of the 32 KB tile
-  int R, k;
-  dma_slot(blk, lane, R, k);
-  const int64_t m = min(m0 + R, M - 1);
-  __builtin_amdgcn_global_load_lds((gptr_t)(a + m * lda + k0 + k), (lptr_t)(xs + blk * 512), 16, 0, 0);
+// Whole patch (prologue): all four column pairs.
+MOLT_DEV void wp_commit(const WPatch& w, const float2* tabc, uint16_t* ws, int cg, int rg) {
+  float2 c[4];
+  u32x2_t col[8];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) { wp_lookup(w, tabc, b, c); wp_finish(c, w.sc, col[2 * b], col[2 * b + 1]); }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) wp_swap_write(col[k], col[k + 4], ws, cg, rg, k);
 }
 
-// One BK step whose MFMA sub-steps carry the staging of the next step: the
-// stage callback runs before sub-step kk's MFMAs (the scheduling barrier keeps
-// its memory instructions there instead of hoisting them all to the top),
-// so the next step's loads and dequantisation overlap this step's MFMAs.
-template <typename F>
-MOLT_DEV void compute_staged(const uint16_t* __restrict__ ws, const uint16_t* __restrict__ xs, const FragOff& f,
-                             f32x16_t (&acc)[TM][TN], F&& stage) {
-  bf16x8_t a[2][TM], b[2][TN];
-  b_load_frags(ws, xs, f, 0, a[0], b[0]);
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    stage(kk);
-    if (kk < 3) b_load_frags(ws, xs, f, kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kk & 1][i], b[kk & 1][j], acc[i][j], 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
-// ---- backward W side (column-contract): one 8-row x 8-column patch per thread
-struct WCReg { uint32_t q[4]; float sc[4]; };
-
-MOLT_DEV void wc_issue(WCReg& w, const BwdParams& p, int seg, int64_t tn, int64_t c0, int tid) {
-  const int cg = tid & 31, rg = tid >> 5;     // 32 column groups of 8, 16 row groups of 4
-  const int64_t col = min(tn * BN + 8 * cg, p.Kw - 8);
-  const uint8_t* packed = sel(p.packed, seg);
-  const float* scales = sel(p.scales, seg);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t flat = (c0 + 4 * rg + r) * p.Kw + col;
-    w.q[r] = *reinterpret_cast<const uint32_t*>(packed + (flat >> 1));
-    w.sc[r] = scales[flat >> 6];
-  }
-}
-
-MOLT_DEV void wc_commit(const WCReg& w, uint16_t* ws, const float2* tab, int tid) {
-  const int cg = tid & 31, rg = tid >> 5;
-  float v[4][8];
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const float2 c = tab[(w.q[r] >> (8 * b)) & 0xffu];
-      v[r][2 * b] = c.x * w.sc[r];
-      v[r][2 * b + 1] = c.y * w.sc[r];
-    }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    u32x2_t o;
-    o[0] = pack_bf16x2(v[0][j], v[1][j]);
-    o[1] = pack_bf16x2(v[2][j], v[3][j]);
-    *reinterpret_cast<u32x2_t*>(ws + loff(8 * cg + j, rg >> 1) + 4 * (rg & 1)) = o;
-  }
-}
-
-// Backward W side: element (output column R, rank c0 + k) = bf16(scale * A[c0 + k][col]).
-// A thread loads a 4-rank x 8-column patch of A (16-byte loads along the
-// columns) and transposes it so the ranks become contiguous in LDS.
+// Backward W side of a LoRA step: element (output column R, rank c0 + k) =
+// bf16(scale * A[c0 + k][col]). A thread loads a 4-rank x 8-column patch of A
+// (16-byte loads along the columns) and transposes it so the ranks become
+// contiguous in LDS.
 MOLT_DEV void lora_wcol_stage(uint16_t* ws, const BwdParams& p, int seg, int64_t tn, int64_t c0, int tid) {
   static_assert(NT == 512, "one 4 x 8 patch per thread");
   const float* a = sel(p.la, seg);
@@ -1108,10 +1018,9 @@ MOLT_DEV void lora_wcol_stage(uint16_t* ws, const BwdParams& p, int seg, int64_t
   }
 }
 
-// ---- LDS-staged epilogues
 // acc[i][j] holds C[W row][X row]: W row = wn*WROWS + 32i + 8(e/4) + 4(lane/32) + e%4,
-// X row = wm*WCOLS + 32j + lane%32. The staged tile is ep[X row][W row] in bf16.
-MOLT_DEV void stage_acc(uint16_t* ep, const f32x16_t (&acc)[TM][TN], int wm, int wn, int lane) {
+// X row = wm*WCOLS + 32j + lane%32. Staged as [X row][W row] in bf16.
+MOLT_DEV void stage_acc(const EpTile& ep, const f32x16_t (&acc)[TM][TN], int wm, int wn, int lane) {
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int row = wm * WCOLS + j * 32 + (lane & 31);
@@ -1122,18 +1031,22 @@ MOLT_DEV void stage_acc(uint16_t* ep, const f32x16_t (&acc)[TM][TN], int wm, int
         const int col = wn * WROWS + i * 32 + 8 * g + 4 * (lane >> 5);
         u32x2_t o = {pack_bf16x2(acc[i][j][4 * g], acc[i][j][4 * g + 1]),
                      pack_bf16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3])};
-        *reinterpret_cast<u32x2_t*>(ep + row * EP_LD + col) = o;
+        *reinterpret_cast<u32x2_t*>(ep_at(ep, row, col)) = o;
       }
   }
 }
 
-MOLT_DEV void swiglu_bwd_store(const uint16_t* ep, const BwdParams& p, int64_t m0, int64_t tn, int tid) {
+// SwiGLU backward epilogue (kernels/gated_activation.py:47-51 with MOLT's bf16
+// rounding points): dh comes from the staged tile, gate/up from HBM.
+MOLT_DEV void swiglu_bwd_store(const EpTile& ep, const BwdParams& p, int64_t m0, int64_t tn, int tid) {
   // 256 rows x 32 chunks of 8 intermediate columns
-  for (int q = tid; q < BM * 32; q += NT) {
+#pragma unroll 2
+  for (int it = 0; it < BM * 32 / NT; ++it) {
+    const int q = tid + it * NT;
     const int row = q >> 5, ch = q & 31;
     const int64_t m = m0 + row, n = tn * BN + 8 * ch;
     if (m >= p.M || n >= p.Kw) continue;
-    const u32x4_t dh = *reinterpret_cast<const u32x4_t*>(ep + row * EP_LD + 8 * ch);
+    const u32x4_t dh = *reinterpret_cast<const u32x4_t*>(ep_at(ep, row, 8 * ch));
     const int64_t off = m * p.ldg + n;
     u32x4_t gw, uw;
     if (p.vec_out && n + 8 <= p.Kw) {
@@ -1177,57 +1090,150 @@ MOLT_DEV void swiglu_bwd_store(const uint16_t* ep, const BwdParams& p, int64_t m
   }
 }
 
+// Interleave of one backward sub-step: 8 MFMAs, their LDS reads and VALU,
+// then NW transposed-patch writes.
+template <int NW>
+MOLT_DEV void interleave_substep_bwd() {
+#define MOLT_SGB(nds)                                   \
+  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    \
+  __builtin_amdgcn_sched_group_barrier(0x100, nds, 0);  \
+  __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+  MOLT_SGB(2) MOLT_SGB(2) MOLT_SGB(1) MOLT_SGB(1) MOLT_SGB(1) MOLT_SGB(1) MOLT_SGB(1) MOLT_SGB(1)
+#undef MOLT_SGB
+  if (NW) __builtin_amdgcn_sched_group_barrier(0x200, NW, 0);
+}
+
+// Backward NF4 GEMM, 256 (X rows) x 256 (output columns) tile, 8 waves of
+// 128 x 64, the same pipeline as the forward kernel: X = dY of the step's
+// segment by buffer-load DMA one step ahead, the W patch bytes one step ahead
+// in registers, dequantised (one patch row per sub-step) into the other W
+// buffer, last sub-step's MFMAs carried across the barrier. Requires
+// Nw % 64 == 0, Kw % 8 == 0, an even number of steps and block size 64.
 template <int EPI>
 __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
-  __shared__ Smem sm;
+  __shared__ __attribute__((aligned(16))) uint16_t xb0[BUF], xb1[BUF], wb0[BUF], wb1[BUF];
+  __shared__ float2 tab[256 * TABC];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WAVES_M, wn = wave / WAVES_M;
   const int64_t nt_m = ceil_div64(p.M, BM), nt_n = ceil_div64(p.Kw, BN);
   int64_t tm, tn;
   grouped_tile(xcd_tile(blockIdx.x, nt_m * nt_n), nt_m, nt_n, GROUP_M, tm, tn);
   const int64_t m0 = tm * BM;
-  build_pair_table(sm.tab, p.code, p.order);
+  build_tab(tab, p.code, p.order, tid);
+  const float2* tabc = tab + (lane & (TABC - 1));
 
   FragOff fo;
   frag_offsets(fo, wn * WROWS, wm * WCOLS, lane);
   f32x16_t acc[TM][TN];
   zero_acc(acc);
 
+  // X (dY of a segment): per-lane DMA slots, one resource per segment.
+  const int64_t xbytes = ((p.M - 1) * p.lddy + p.Nw) * 2;
+  const __amdgpu_buffer_rsrc_t xr0 = make_rsrc(p.dy[0], xbytes), xr1 = make_rsrc(p.dy[1], xbytes);
+  uint32_t xoff[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    int R, k;
+    dma_slot(wave * 4 + c, lane, R, k);
+    xoff[c] = (uint32_t)((min(m0 + R, p.M - 1) * p.lddy + k) * 2);
+  }
+  // W patch: rows c0 + 4 rg + r (r = 0..3), columns col .. col + 7.
+  const int cg = tid & 31, rg = tid >> 5;
+  const int64_t col = min(tn * BN + 8 * cg, p.Kw - 8);
+  const int64_t wbytes = p.Nw * p.Kw / 2, sbytes = p.Nw * p.Kw / 16;
+  const __amdgpu_buffer_rsrc_t wr0 = make_rsrc(p.packed[0], wbytes), wr1 = make_rsrc(p.packed[1], wbytes);
+  const __amdgpu_buffer_rsrc_t sr0 = make_rsrc(p.scales[0], sbytes), sr1 = make_rsrc(p.scales[1], sbytes);
+  const uint32_t woff = (uint32_t)(4 * rg * (p.Kw / 2) + col / 2);
+  const uint32_t soff = (uint32_t)((4 * rg * (p.Kw / 64) + col / 64) * 4);
+
   const int kseg = (int)(p.Nw / BK);
   const int ks = p.nseg * kseg;
-  WCReg wr;
-  x_issue_lds(sm.xs[0], sel(p.dy, 0), p.lddy, m0, p.M, 0, wave, lane);
-  wc_issue(wr, p, 0, tn, 0, tid);
-  __syncthreads();  // pair table
-  wc_commit(wr, sm.ws[0], sm.tab, tid);
+  // step -> (segment, first contraction row), clamped to the last step
+  auto seg_of = [&](int s) { return min(s, ks - 1) / kseg; };
+  auto c0_of = [&](int s) { const int t = min(s, ks - 1); return (int64_t)(t - (t / kseg) * kseg) * BK; };
+  auto x_load = [&](uint16_t* dst, int s) {
+    const __amdgpu_buffer_rsrc_t xr = seg_of(s) ? xr1 : xr0;
+    const uint32_t so = (uint32_t)(c0_of(s) * 2);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) buf_load_lds16(xr, dst + (wave * 4 + c) * 512, xoff[c], so);
+  };
+  auto w_load = [&](WPatch& w, int s) {
+    const int sg = seg_of(s);
+    const __amdgpu_buffer_rsrc_t wr = sg ? wr1 : wr0, sr = sg ? sr1 : sr0;
+    const int64_t c0 = c0_of(s);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      w.q[r] = buf_load4(wr, woff, (uint32_t)((c0 + r) * (p.Kw / 2)));
+      w.sc[r] = __builtin_bit_cast(float, buf_load4(sr, soff, (uint32_t)((c0 + r) * (p.Kw / 64) * 4)));
+    }
+  };
+
+  WPatch r0, r1;
+  x_load(xb0, 0);
+  w_load(r0, 0);
+  wait_vm0();
+  __syncthreads();  // table, X(0)
+  wp_commit(r0, tabc, wb0, cg, rg);
+  w_load(r0, 1);
+  wait_vm0();
   __syncthreads();
-  for (int s = 0; s + 1 < ks; ++s) {
-    const int cur = s & 1;
-    const int seg = (s + 1) / kseg;
-    const int64_t c1 = (int64_t)(s + 1 - seg * kseg) * BK;
-    const uint16_t* dyn = sel(p.dy, seg);
-    compute_staged(sm.ws[cur], sm.xs[cur], fo, acc, [&](int kk) {
-      if (kk == 0) {
-        wc_issue(wr, p, seg, tn, c1, tid);
-        x_issue_lds_one(sm.xs[cur ^ 1], dyn, p.lddy, m0, p.M, c1, wave, lane, 0);
-        x_issue_lds_one(sm.xs[cur ^ 1], dyn, p.lddy, m0, p.M, c1, wave, lane, 1);
-      } else if (kk == 1) {
-        x_issue_lds_one(sm.xs[cur ^ 1], dyn, p.lddy, m0, p.M, c1, wave, lane, 2);
-        x_issue_lds_one(sm.xs[cur ^ 1], dyn, p.lddy, m0, p.M, c1, wave, lane, 3);
-      } else if (kk == 3) {
-        wc_commit(wr, sm.ws[cur ^ 1], sm.tab, tid);
-      }
-    });
+
+  bf16x8_t a[2][TM], b[2][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) a[1][i] = bf16x8_t{};
+#pragma unroll
+  for (int j = 0; j < TN; ++j) b[1][j] = bf16x8_t{};
+
+  // Dequant of W(s+1) across the sub-steps: column pairs (0,1), (4,5) then
+  // (2,3), (6,7), each pair's lookups one sub-step ahead; columns k and k + 4
+  // are written together after the lane exchange.
+  auto step = [&](int s, const WPatch& cw, WPatch& nw, const uint16_t* xc, const uint16_t* wc, uint16_t* xn,
+                  uint16_t* wnx) {
+    float2 c[4];
+    u32x2_t c0, c1, c4, c5;
+    load_frags(wc, xc, fo, 0, a[0], b[0]);
+    mfma_set(a[1], b[1], acc);
+    x_load(xn, s + 1);
+    w_load(nw, s + 2);
+    wp_lookup(cw, tabc, 0, c);
+    __builtin_amdgcn_sched_barrier(0);
+    load_frags(wc, xc, fo, 1, a[1], b[1]);
+    mfma_set(a[0], b[0], acc);
+    wp_finish(c, cw.sc, c0, c1);
+    wp_lookup(cw, tabc, 2, c);
+    interleave_substep_bwd<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    load_frags(wc, xc, fo, 2, a[0], b[0]);
+    mfma_set(a[1], b[1], acc);
+    wp_finish(c, cw.sc, c4, c5);
+    wp_swap_write(c0, c4, wnx, cg, rg, 0);
+    wp_swap_write(c1, c5, wnx, cg, rg, 1);
+    wp_lookup(cw, tabc, 1, c);
+    interleave_substep_bwd<2>();
+    __builtin_amdgcn_sched_barrier(0);
+    load_frags(wc, xc, fo, 3, a[1], b[1]);
+    mfma_set(a[0], b[0], acc);
+    wp_finish(c, cw.sc, c0, c1);
+    wp_lookup(cw, tabc, 3, c);
+    interleave_substep_bwd<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    wp_finish(c, cw.sc, c4, c5);
+    wp_swap_write(c0, c4, wnx, cg, rg, 2);
+    wp_swap_write(c1, c5, wnx, cg, rg, 3);
+    wait_vm0();
     __syncthreads();
+  };
+  for (int s = 0; s < ks; s += 2) {
+    step(s, r0, r1, xb0, wb0, xb1, wb1);
+    step(s + 1, r1, r0, xb1, wb1, xb0, wb0);
   }
-  b_compute(sm.ws[(ks - 1) & 1], sm.xs[(ks - 1) & 1], fo, acc);
-  __syncthreads();
+  mfma_set(a[1], b[1], acc);
   for (int seg = 0; seg < p.nseg && p.r > 0; ++seg) {
     for (int64_t c0 = 0; c0 < p.r; c0 += BK) {
-      b_lora_a_stage(sm.xs[0], sel(p.u, seg), p.ldu, m0, p.M, c0, p.r, tid);
-      lora_wcol_stage(sm.ws[0], p, seg, tn, c0, tid);
+      lora_a_stage(xb0, sel(p.u, seg), p.ldu, m0, p.M, c0, p.r, tid);
+      lora_wcol_stage(wb0, p, seg, tn, c0, tid);
       __syncthreads();
-      b_compute(sm.ws[0], sm.xs[0], fo, acc);
+      compute(wb0, xb0, fo, acc);
       __syncthreads();
     }
   }
@@ -1250,14 +1256,14 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
     }
     return;
   }
-  // SwiGLU backward: stage dh = bf16(acc) of the tile in LDS, then compute
-  // dgate/dup cooperatively with 16-byte loads of gate/up and 16-byte stores.
-  stage_acc(sm.ep, acc, wm, wn, lane);
+  // SwiGLU backward: stage dh = bf16(acc) of the tile, then compute dgate/dup
+  // cooperatively with 16-byte loads of gate/up and 16-byte stores.
+  const EpTile ep{xb0, xb1, wb0, wb1};
+  stage_acc(ep, acc, wm, wn, lane);
   __syncthreads();
-  swiglu_bwd_store(sm.ep, p, m0, tn, tid);
+  swiglu_bwd_store(ep, p, m0, tn, tid);
 }
 
-}  // namespace bwd
 }  // namespace big
 
 // ------------------------------------------------------------- host helpers
@@ -1399,12 +1405,17 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
                   aligned(dy0, 16) && (nseg == 1 || aligned(dy1, 16)) && aligned(w0->packed, 2) &&
                   (nseg == 1 || aligned(w1->packed, 2));
   const int64_t big_tiles = ceil_div64(M, big::BM) * ceil_div64(p.Kw, big::BN);
-  if (al && aligned(w0->packed, 4) && (nseg == 1 || aligned(w1->packed, 4)) &&
-      big_tiles >= big_tile_min()) {
+  // The 256 x 256 kernel runs an even number of 64-deep steps and addresses dY,
+  // the packed bytes and the scales through 32-bit buffer offsets.
+  const int64_t lim = 0x7fffffffll;
+  const bool big_ok = al && aligned(w0->packed, 4) && (nseg == 1 || aligned(w1->packed, 4)) &&
+                      (nseg * (p.Nw / 64)) % 2 == 0 && ((M - 1) * lddy + p.Nw) * 2 <= lim &&
+                      p.Nw * p.Kw / 2 <= lim && p.Nw * p.Kw / 16 <= lim;
+  if (big_ok && big_tiles >= big_tile_min()) {
     MOLT_REQUIRE(big_tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
     dim3 grid((unsigned)big_tiles), block(big::NT);
-    if (swiglu) hipLaunchKernelGGL((big::bwd::bwd_kernel<EPI_SWIGLU_BWD>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((big::bwd::bwd_kernel<EPI_STORE>), grid, block, 0, stream, p);
+    if (swiglu) hipLaunchKernelGGL((big::bwd_kernel<EPI_SWIGLU_BWD>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((big::bwd_kernel<EPI_STORE>), grid, block, 0, stream, p);
     return check_launch(who);
   }
   const int64_t tiles = ceil_div64(M, BM) * ceil_div64(p.Kw, BN);
