@@ -281,6 +281,170 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(4))) void
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Streaming dot-product variant for M == 1 (decode). A wave owns RW whole
+// rows of W; every lane loads 16 contiguous packed bytes (32 elements, half a
+// block) per 1 KB piece of a row, so each load instruction is 1 KB of one
+// row, and all of a wave's loads are issued before any is used (one HBM round
+// trip per launch). Codes come from the replicated LDS table of bf16 code
+// pairs and meet X through v_dot2_f32_bf16 (X staged once per workgroup in
+// LDS); the block scale multiplies each lane's half-block sum, and the 64
+// lanes of a row are summed by butterfly shuffles. Requires K % 2048 == 0.
+constexpr int GD_WAVES = 8;
+constexpr int GD_NT = 64 * GD_WAVES;
+constexpr int GD_MAXL = 16;               // 1 KB pieces per wave
+constexpr int GD_XPAD = 8;                // bf16 elements of X row padding
+
+struct GdSmem {
+  uint32_t tab[256 * GV_TABW];
+  float code2s[256];
+};
+
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+
+template <int RW, int IPR>
+__global__ __launch_bounds__(GD_NT) void nf4_gemv_dot_kernel(const GemvParams p) {
+  constexpr int MM = 1;                                               // decode: one row of X
+  __shared__ GdSmem sm;
+  extern __shared__ __attribute__((aligned(16))) uint16_t gd_xs[];      // X, K elements
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  constexpr int NL = RW * IPR;                                        // 1 KB pieces per wave
+  static_assert(NL <= GD_MAXL, "pieces per wave");
+  const int64_t n0 = ((int64_t)blockIdx.x * GD_WAVES + wave) * RW;
+  const int KB = p.K >> 6;
+
+  typedef __attribute__((address_space(4))) const f32x4_t* cptr_t;
+  const cptr_t cbp = (cptr_t)p.code;
+  const f32x4_t cb0 = cbp[0], cb1 = cbp[1], cb2 = cbp[2], cb3 = cbp[3];
+
+  // X first (16-byte chunks into registers), so that the wait before its LDS
+  // stores, and the barrier after them, do not wait for the weight stream.
+  constexpr int XCH = IPR * 256, XIT = (XCH + GD_NT - 1) / GD_NT;    // 16-byte chunks of X
+  u32x4_t xr[XIT];
+#pragma unroll
+  for (int it = 0; it < XIT; ++it) {
+    const int c = tid + it * GD_NT < XCH ? tid + it * GD_NT : XCH - 1;
+    xr[it] = *reinterpret_cast<const u32x4_t*>(p.x + 8 * c);
+  }
+  const float c2 = p.code2 ? p.code2[tid & 255] : 0.0f;
+
+  // all weight pieces and their block statistics, up front and piece by piece
+  // (piece j = row j / IPR, 1 KB piece j % IPR), so piece 0 can be used first
+  u32x4_t w[NL];
+  uint32_t qv[NL];
+  float sv[NL];
+  const bool nested = p.scales == nullptr;
+#pragma unroll
+  for (int j = 0; j < NL; ++j) {
+    const int r = j / IPR, i = j - r * IPR;
+    const int64_t n = n0 + r < p.N ? n0 + r : p.N - 1;
+    w[j] = *reinterpret_cast<const u32x4_t*>(p.packed + (uint32_t)(n * (p.K >> 1) + 1024 * i + 16 * lane));
+    const uint32_t blk = (uint32_t)(n * KB + 32 * i + (lane >> 1));
+    if (nested) {
+      qv[j] = p.q[blk];
+      sv[j] = p.absmax2[blk >> p.dq_shift];
+    } else {
+      qv[j] = 0;
+      sv[j] = p.scales[blk];
+    }
+  }
+  // LoRA operands, also up front: lane j (and j + 64) holds T[j] and B[n, j] of its rows
+  float lt[2] = {0.0f, 0.0f}, lbv[RW][2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int jr = lane + 64 * q;
+    const bool on = jr < p.r;
+    if (on) lt[q] = bf16_to_f32(p.t[jr]);
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int64_t n = n0 + r < p.N ? n0 + r : p.N - 1;
+      lbv[r][q] = on ? p.lb[n * p.r + jr] : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < XIT; ++it)
+    if (tid + it * GD_NT < XCH) *reinterpret_cast<u32x4_t*>(gd_xs + 8 * (tid + it * GD_NT)) = xr[it];
+  {
+    const float cv[16] = {cb0[0], cb0[1], cb0[2], cb0[3], cb1[0], cb1[1], cb1[2], cb1[3],
+                          cb2[0], cb2[1], cb2[2], cb2[3], cb3[0], cb3[1], cb3[2], cb3[3]};
+    static_assert(GV_TABW == 32 && GD_NT % 512 == 0 && GD_NT <= 8192, "table build covers 256 x 32 entries");
+    constexpr int HS = GD_NT / 512;                                    // high nibbles per pass
+    const int lo = (tid >> 5) & 15, copy = tid & 31, h0 = tid >> 9;
+    float clo = cv[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) clo = lo == i ? cv[i] : clo;
+#pragma unroll
+    for (int k = 0; k < 16 / HS; ++k) {
+      const int hi = h0 + HS * k;
+      float chi = cv[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) chi = hi == i ? cv[i] : chi;
+      const float first = p.order ? chi : clo, second = p.order ? clo : chi;
+      sm.tab[(hi * 16 + lo) * GV_TABW + copy] = pack_bf16x2(first, second);
+    }
+    if (tid < 256) sm.code2s[tid] = c2;
+  }
+  __syncthreads();
+
+  const uint32_t* tab = sm.tab + (lane & 31);
+  const int xrow = p.K + GD_XPAD;
+  float acc[RW][MM];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int m = 0; m < MM; ++m) acc[r][m] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NL; ++j) {
+    const int r = j / IPR, i = j - r * IPR;
+    const int k0 = 2048 * i + 32 * lane;                               // first element of the piece
+    float bs[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) bs[m] = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {                                      // 4 bytes per dword, 8 elements
+      u32x4_t xv[MM];
+#pragma unroll
+      for (int m = 0; m < MM; ++m) xv[m] = *reinterpret_cast<const u32x4_t*>(gd_xs + m * xrow + k0 + 8 * h);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t pair = tab[((w[j][h] >> (8 * b)) & 0xffu) * GV_TABW];
+#pragma unroll
+        for (int m = 0; m < MM; ++m) {
+          // copy the element out first: __builtin_bit_cast of a vector-element
+          // lvalue reads element 0 with this compiler
+          const uint32_t xw = xv[m][b];
+          bs[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, pair),
+                                                 __builtin_bit_cast(bf16x2v, xw), bs[m], false);
+        }
+      }
+    }
+    const float sc = gv_scale(p, sm.code2s, qv[j], sv[j]);
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      acc[r][m] += sc * bs[m];
+      asm volatile("" : "+v"(acc[r][m]));   // materialise here: keeps each piece's lookups short-lived
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // LoRA partials join the row sums; butterfly sum over the wave; lane r stores row r
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    float v = acc[r][0] + (lt[0] * round_bf16(p.s * lbv[r][0]) + lt[1] * round_bf16(p.s * lbv[r][1]));
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) v += __shfl_xor(v, sh);
+    acc[r][0] = v;
+  }
+  if (lane < RW) {
+    float v = acc[0][0];
+#pragma unroll
+    for (int r = 1; r < RW; ++r) v = lane == r ? acc[r][0] : v;
+    const int64_t n = n0 + lane;
+    if (n < p.N) p.y[n] = bf16_bits(v);
+  }
+}
+
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 }  // namespace
@@ -330,6 +494,26 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
   const int64_t groups = ceil_div64(p.N, GV_ROWS);
   MOLT_REQUIRE(groups < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
   hipStream_t st = (hipStream_t)stream;
+  // Decode (M == 1): streaming dot-product kernel; rows per wave grow while the
+  // grid still has at least 192 workgroups of GD_WAVES waves. (At M >= 2 the
+  // MFMA kernel below is faster: the dot kernel's VALU and LDS work scale with M.)
+  if (M == 1 && (w->cols == 4096 || w->cols == 14336) && aligned(w->packed, 16)) {
+    const int ipr = (int)(w->cols / 2048);
+    int rw = 1;
+    while (rw < 4 && 2 * rw * ipr <= GD_MAXL && w->rows / (2 * rw * GD_WAVES) >= 192) rw *= 2;
+    const int64_t wgs = ceil_div64(w->rows, (int64_t)rw * GD_WAVES);
+    const size_t dyn = (size_t)(w->cols + GD_XPAD) * 2;
+    MOLT_REQUIRE(wgs < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
+#define MOLT_GD(RWv, IPRv) \
+    hipLaunchKernelGGL((nf4_gemv_dot_kernel<RWv, IPRv>), dim3((unsigned)wgs), dim3(GD_NT), dyn, st, p)
+    if (ipr == 2) {
+      if (rw == 1) MOLT_GD(1, 2); else if (rw == 2) MOLT_GD(2, 2); else MOLT_GD(4, 2);
+    } else {
+      if (rw == 1) MOLT_GD(1, 7); else MOLT_GD(2, 7);
+    }
+#undef MOLT_GD
+    return check_launch(who);
+  }
   const bool q4 = nested && (w->cols / 64) % 4 == 0 && w->dq_block >= 4 && aligned(w->absmax_q, 4);
   if (q4) hipLaunchKernelGGL((nf4_gemv_kernel<true>), dim3((unsigned)groups), dim3(GV_NT), 0, st, p);
   else hipLaunchKernelGGL((nf4_gemv_kernel<false>), dim3((unsigned)groups), dim3(GV_NT), 0, st, p);

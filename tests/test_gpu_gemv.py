@@ -36,7 +36,8 @@ def test_gemv_matches_oracle(n, k, m):
     assert_close_fro(np_f32(y), bf16_values(x) @ wo.T, what="Y")
 
 
-@pytest.mark.parametrize("m,n,r", [(1, 1024, 16), (5, 1024, 16), (16, 1024, 16), (3, 1000, 64),
+@pytest.mark.parametrize("m,n,r", [(1, 1024, 16), (1, 1000, 96), (1, 4100, 128), (5, 1024, 16), (16, 1024, 16),
+                                   (3, 1000, 64),
                                    (16, 520, 96), (2, 256, 128)])
 def test_gemv_with_lora_matches_oracle(m, n, r):
     print(f"gemv lora m={m} n={n} r={r}", flush=True)
@@ -51,6 +52,24 @@ def test_gemv_with_lora_matches_oracle(m, n, r):
     wo = oracle_weight(packed, qs).dequant_bf16().astype(np.float64)
     ref = O.lora_linear_forward(bf16_values(x), wo, bf16_values(a), bf16_values(b), s)
     assert_close_fro(np_f32(y), ref, what="Y")
+
+
+@pytest.mark.parametrize("m,n,k,nested,order", [(1, 1000, 4096, True, 1), (1, 520, 4096, False, 0),
+                                                 (1, 776, 14336, True, 1), (1, 264, 14336, False, 1),
+                                                 (1, 4104, 14336, True, 0), (1, 2056, 4096, True, 1),
+                                                 (1, 14344, 4096, True, 1), (3, 520, 4096, False, 0),
+                                                 (2, 776, 14336, True, 1), (4, 2056, 4096, True, 1)])
+def test_gemv_decode_shapes_match_oracle(m, n, k, nested, order):
+    # K = 4096 / 14336 with M == 1 take the streaming dot-product decode kernel
+    # (every rows-per-wave choice of it); ragged row counts exercise its clamped
+    # loads and guarded stores. M = 2..4 cover the MFMA kernel at the same shapes.
+    print(f"gemv decode m={m} n={n} k={k} nested={nested} order={order}", flush=True)
+    w = seeded((n, k), 100 + n, std=0.02, dtype=torch.float32)
+    packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=nested, nibble_order=order)
+    x = seeded((m, k), 101 + m)
+    y = _gemv(x, packed, qs, nested=nested)
+    wo = oracle_weight(packed, qs).dequant_bf16().astype(np.float64)
+    assert_close_fro(np_f32(y), bf16_values(x) @ wo.T, what="Y")
 
 
 def test_gemv_resolved_scales_and_low_nibble_layout():
