@@ -296,7 +296,7 @@ def main() -> int:
                    "nf4_block": 64, "double_quant": True, "parallelism": "single GPU"},
         "mfma_util_pct": round(100 * step_tflops / PEAK_BF16_TFLOPS, 2),
         "step_tflops": round(step_tflops, 1),
-        "roofline": {"kernel": "nf4_fwd_kernel<pair> (fused gate/up NF4-LoRA GEMM)", "bound": "mfma",
+        "roofline": {"kernel": "big::fwd_kernel<true> (fused gate/up NF4-LoRA GEMM)", "bound": "mfma",
                      "achieved": round(k_tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(k_tflops / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(),
                      "traffic_unit": "bytes/launch (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)",
