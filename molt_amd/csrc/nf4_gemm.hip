@@ -656,12 +656,26 @@ MOLT_DEV void w_lookup(const WBytes& w, const float2* tabc, int d, float2 (&c)[4
   c[3] = tabc[(q >> 24) * TABC];
 }
 
+// Forward dequant slot of a thread: tile row R and 16-byte half of the row's
+// 32-byte slice of the step. A ds_write_b128 is served 8 consecutive lanes
+// per cycle over 32 banks, i.e. by the 16-byte slot (4 (P & 1) + chunk
+// position) mod 8 of each lane. The 8 lanes of a group therefore take
+// physical rows {0, 1, 4, 5, 8, 9, 12, 13} (+2, +16) of one half, whose slots
+// all differ; the two halves of a row sit in lanes l and l + 8, so the global
+// load of a row's 32 bytes stays within one instruction.
+MOLT_DEV void wslot(int tid, int& R, int& half) {
+  const int l = tid & 63, g = l & 7;
+  half = (l >> 3) & 1;
+  const int P = 32 * (tid >> 6) + 16 * (l >> 5) + 2 * ((l >> 4) & 1) + (g & 1) + 4 * (g >> 1);
+  R = P ^ ((P >> 3) & 3);
+}
+
 // bf16(code * scale) of 8 elements (the rounding of dequantize_4bit) into chunk 4 * half + d of row R.
-MOLT_DEV void w_finish(const float2 (&c)[4], float sc, uint16_t* ws, int tid, int d) {
+MOLT_DEV void w_finish(const float2 (&c)[4], float sc, uint16_t* ws, int R, int half, int d) {
   u32x4_t o;
 #pragma unroll
   for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(c[e].x * sc, c[e].y * sc);
-  *reinterpret_cast<u32x4_t*>(ws + loff(tid >> 1, 4 * (tid & 1) + d)) = o;
+  *reinterpret_cast<u32x4_t*>(ws + loff(R, 4 * half + d)) = o;
 }
 
 // ---- staging of the LoRA contraction steps (swizzled layout). Each thread
@@ -833,15 +847,17 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
     dma_slot(wave * 4 + c, lane, R, k);
     xoff[c] = (uint32_t)((min(m0 + R, p.M - 1) * p.ldx + k) * 2);
   }
-  // W: row R = tid / 2, bytes [16 * half, +16) of the row's 32-byte slice of
-  // the step; the weight (gate or up) is uniform over a wave.
+  // W: row wR, bytes [16 * wh, +16) of the row's 32-byte slice of the step
+  // (wslot); a wave covers 32 rows, so the weight (gate or up) is uniform over it.
+  int wR, wh;
+  wslot(tid, wR, wh);
   int which; int64_t n;
-  fwd_row(tid >> 1, tn, PAIR, which, n);
+  fwd_row(wR, tn, PAIR, which, n);
   which = __builtin_amdgcn_readfirstlane(which);
   n = min(n, p.N - 1);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(which ? p.packed[1] : p.packed[0], p.N * p.K / 2);
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(which ? p.scales[1] : p.scales[0], p.N * p.K / 64 * 4);
-  const uint32_t woff = (uint32_t)(n * p.K / 2 + 16 * (tid & 1));
+  const uint32_t woff = (uint32_t)(n * p.K / 2 + 16 * wh);
   const uint32_t soff = (uint32_t)(n * p.K / 64 * 4);
 
   auto x_load = [&](uint16_t* dst, int64_t k0) {
@@ -852,7 +868,6 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
     w.q = buf_load16(wr, woff, (uint32_t)(k0 >> 1));
     w.sc = __builtin_bit_cast(float, buf_load4(sr, soff, (uint32_t)((k0 >> 6) * 4)));
   };
-
   const int ks = (int)(p.K / BK);
   const int64_t klast = p.K - BK;
   WBytes r0, r1;
@@ -863,7 +878,7 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
   {
     float2 c[4];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) { w_lookup(r0, tabc, d, c); w_finish(c, r0.sc, wb0, tid, d); }
+    for (int d = 0; d < 4; ++d) { w_lookup(r0, tabc, d, c); w_finish(c, r0.sc, wb0, wR, wh, d); }
   }
   w_load(r0, min((int64_t)BK, klast));
   wait_vm0();
@@ -889,12 +904,12 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
     for (int kk = 0; kk < 3; ++kk) {
       load_frags(wc, xc, fo, kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
       mfma_set(a[kk & 1], b[kk & 1], acc);
-      w_finish(c, cw.sc, wnx, tid, kk);
+      w_finish(c, cw.sc, wnx, wR, wh, kk);
       w_lookup(cw, tabc, kk + 1, c);
       interleave_substep();
       __builtin_amdgcn_sched_barrier(0);
     }
-    w_finish(c, cw.sc, wnx, tid, 3);
+    w_finish(c, cw.sc, wnx, wR, wh, 3);
     wait_vm0();
     __syncthreads();
   };
@@ -1137,8 +1152,16 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
     dma_slot(wave * 4 + c, lane, R, k);
     xoff[c] = (uint32_t)((min(m0 + R, p.M - 1) * p.lddy + k) * 2);
   }
-  // W patch: rows c0 + 4 rg + r (r = 0..3), columns col .. col + 7.
-  const int cg = tid & 31, rg = tid >> 5;
+  // W patch: rows c0 + 4 rg + r (r = 0..3), columns col .. col + 7; lanes l and
+  // l + 32 take rank groups 2m and 2m + 1 of the same columns (the permlane32
+  // swap pairs them) and a wave's 32 column groups cover 256 contiguous columns,
+  // so each 4-byte load instruction reads 128 contiguous bytes of two rows.
+  // A ds_write_b128 is served 8 consecutive lanes per cycle by the 16-byte slot
+  // (4 (P & 1) + chunk position) mod 8; for the transposed store of row
+  // 8 cg + k (+4) the slot varies with cg bits 0 and 4 only, so lane bits 0 and
+  // 1 carry them (two lanes per slot instead of four).
+  const int cg = (lane & 1) | (((lane >> 2) & 1) << 1) | (((lane >> 3) & 3) << 2) | (((lane >> 1) & 1) << 4);
+  const int rg = tid >> 5;
   const int64_t col = min(tn * BN + 8 * cg, p.Kw - 8);
   const int64_t wbytes = p.Nw * p.Kw / 2, sbytes = p.Nw * p.Kw / 16;
   const __amdgpu_buffer_rsrc_t wr0 = make_rsrc(p.packed[0], wbytes), wr1 = make_rsrc(p.packed[1], wbytes);
