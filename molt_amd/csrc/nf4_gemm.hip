@@ -559,6 +559,19 @@ MOLT_DEV void buf_load_lds16(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t off, 
 // vmcnt(0) with the other counters untouched.
 MOLT_DEV void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Workgroup barrier without __syncthreads()'s release fence: the fence makes
+// the compiler drain every outstanding vector-memory op, including register
+// loads of packed weight bytes that are only used a step later. The caller
+// waits explicitly (vmcnt) for the DMA other waves will read; this wave's own
+// LDS stores are waited for here, and the empty asm statements keep the
+// compiler from moving memory accesses across the barrier.
+MOLT_DEV void step_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);              // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Code-pair table, TABC interleaved copies: entry (byte b, copy c) at b * TABC + c
 // holds (code[first nibble], code[second nibble]). Lane l reads copy l % TABC,
 // which spreads the data-dependent lookups of a wave over TABC bank pairs.
@@ -910,8 +923,8 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
       __builtin_amdgcn_sched_barrier(0);
     }
     w_finish(c, cw.sc, wnx, wR, wh, 3);
-    wait_vm0();
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0x0F72);            // vmcnt(2): X(s + 1) landed; W(s + 2) bytes may fly
+    step_barrier();
   };
   // W(s + 1) sits in r0 during even steps and in r1 during odd ones; the LDS buffers alternate likewise.
   for (int s = 0; s < ks; s += 2) {
@@ -1243,8 +1256,8 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
     wp_finish(c, cw.sc, c4, c5);
     wp_swap_write(c0, c4, wnx, cg, rg, 2);
     wp_swap_write(c1, c5, wnx, cg, rg, 3);
-    wait_vm0();
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0x0F78);            // vmcnt(8): X(s + 1) landed; W(s + 2) patch may fly
+    step_barrier();
   };
   for (int s = 0; s < ks; s += 2) {
     step(s, r0, r1, xb0, wb0, xb1, wb1);
