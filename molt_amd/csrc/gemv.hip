@@ -20,6 +20,8 @@
 // a half-wave hit 32 distinct banks. The LoRA term is one more MFMA step per
 // 32 ranks; its B rows are copied into LDS by direct global->LDS loads and T
 // is held in registers, both issued with the first weight chunk.
+#include <algorithm>
+
 #include "common.h"
 
 namespace molt {
@@ -283,17 +285,20 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(4))) void
 
 
 // ---------------------------------------------------------------------------
-// Streaming dot-product variant for M == 1 (decode). A wave owns RW whole
-// rows of W; every lane loads 16 contiguous packed bytes (32 elements, half a
-// block) per 1 KB piece of a row, so each load instruction is 1 KB of one
-// row, and all of a wave's loads are issued before any is used (one HBM round
-// trip per launch). Codes come from the replicated LDS table of bf16 code
-// pairs and meet X through v_dot2_f32_bf16 (X staged once per workgroup in
-// LDS); the block scale multiplies each lane's half-block sum, and the 64
+// Streaming dot-product variant for M == 1 (decode). Each wave walks rows of W
+// in rounds: round j covers RW rows at j * (grid waves * RW) + (this wave's
+// index) * RW, so every round of the grid reads a contiguous band of W. A
+// lane reads 16 contiguous packed bytes (32 elements, half a block) of each
+// 1 KB piece of a row, so each load instruction is 1 KB of one row. The loads
+// of a round (weight pieces, block statistics, LoRA B entries) are issued two
+// rounds ahead into three rotating register sets, so the dot-product work of
+// round j overlaps the HBM stream of rounds j + 1 and j + 2. Codes come from
+// the replicated LDS table of bf16 code pairs and meet X (staged once per
+// workgroup in LDS) through v_dot2_f32_bf16; the block scale multiplies each
+// lane's half-block sum, lane j < r adds T[j] bf16(s B[n, j]), and the 64
 // lanes of a row are summed by butterfly shuffles. Requires K % 2048 == 0.
 constexpr int GD_WAVES = 8;
 constexpr int GD_NT = 64 * GD_WAVES;
-constexpr int GD_MAXL = 16;               // 1 KB pieces per wave
 constexpr int GD_XPAD = 8;                // bf16 elements of X row padding
 
 struct GdSmem {
@@ -304,15 +309,100 @@ struct GdSmem {
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 
 template <int RW, int IPR>
-__global__ __launch_bounds__(GD_NT) void nf4_gemv_dot_kernel(const GemvParams p) {
-  constexpr int MM = 1;                                               // decode: one row of X
+struct GdRound {
+  u32x4_t w[RW * IPR];
+  uint32_t q[RW * IPR];
+  float s[RW * IPR];
+  float lb[RW][2];
+};
+
+// Loads of one round (rows n0 .. n0 + RW - 1, clamped to the matrix).
+template <int RW, int IPR>
+MOLT_DEV void gd_load(GdRound<RW, IPR>& R, const GemvParams& p, int64_t n0, int lane, int KB) {
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int64_t n = n0 + r < p.N ? n0 + r : p.N - 1;
+#pragma unroll
+    for (int i = 0; i < IPR; ++i) {
+      const int j = r * IPR + i;
+      R.w[j] = *reinterpret_cast<const u32x4_t*>(p.packed + (uint32_t)(n * (p.K >> 1) + 1024 * i + 16 * lane));
+      const uint32_t blk = (uint32_t)(n * KB + 32 * i + (lane >> 1));
+      if (p.scales) {
+        R.q[j] = 0;
+        R.s[j] = p.scales[blk];
+      } else {
+        R.q[j] = p.q[blk];
+        R.s[j] = p.absmax2[blk >> p.dq_shift];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int jr = lane + 64 * q;
+      R.lb[r][q] = jr < p.r ? p.lb[n * p.r + jr] : 0.0f;
+    }
+  }
+}
+
+// Dot products of one round and the stores of its rows.
+template <int RW, int IPR>
+MOLT_DEV void gd_compute(const GdRound<RW, IPR>& R, const GemvParams& p, const uint32_t* tab, const uint16_t* xs,
+                         const float* code2s, const float (&lt)[2], int64_t n0, int lane) {
+  float acc[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < IPR; ++i) {                                      // piece i of every row: X read once
+    float bs[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) bs[r] = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {                                      // 4 bytes per dword, 8 elements
+      const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xs + 8 * (256 * i + 64 * h + lane));
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        // copy the element out first: __builtin_bit_cast of a vector-element
+        // lvalue reads element 0 with this compiler
+        const uint32_t xw = xv[b];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          const uint32_t pair = tab[((R.w[r * IPR + i][h] >> (8 * b)) & 0xffu) * GV_TABW];
+          bs[r] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, pair), __builtin_bit_cast(bf16x2v, xw),
+                                                  bs[r], false);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      acc[r] += gv_scale(p, code2s, R.q[r * IPR + i], R.s[r * IPR + i]) * bs[r];
+      asm volatile("" : "+v"(acc[r]));                                // keeps each piece's lookups short-lived
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // LoRA partials join the row sums; butterfly sum over the wave; lane r stores row r
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    float v = acc[r] + (lt[0] * round_bf16(p.s * R.lb[r][0]) + lt[1] * round_bf16(p.s * R.lb[r][1]));
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) v += __shfl_xor(v, sh);
+    acc[r] = v;
+  }
+  if (lane < RW) {
+    float v = acc[0];
+#pragma unroll
+    for (int r = 1; r < RW; ++r) v = lane == r ? acc[r] : v;
+    const int64_t n = n0 + lane;
+    if (n < p.N) p.y[n] = bf16_bits(v);
+  }
+}
+
+template <int RW, int IPR>
+__global__ __launch_bounds__(GD_NT) void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
   __shared__ GdSmem sm;
   extern __shared__ __attribute__((aligned(16))) uint16_t gd_xs[];      // X, K elements
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  constexpr int NL = RW * IPR;                                        // 1 KB pieces per wave
-  static_assert(NL <= GD_MAXL, "pieces per wave");
-  const int64_t n0 = ((int64_t)blockIdx.x * GD_WAVES + wave) * RW;
+  const int64_t stride = (int64_t)gridDim.x * GD_WAVES * RW;          // rows per round of the grid
+  const int64_t nb = ((int64_t)blockIdx.x * GD_WAVES + wave) * RW;    // first row of round 0
   const int KB = p.K >> 6;
 
   typedef __attribute__((address_space(4))) const f32x4_t* cptr_t;
@@ -329,43 +419,23 @@ __global__ __launch_bounds__(GD_NT) void nf4_gemv_dot_kernel(const GemvParams p)
     xr[it] = *reinterpret_cast<const u32x4_t*>(p.x + 8 * c);
   }
   const float c2 = p.code2 ? p.code2[tid & 255] : 0.0f;
+  float lt[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+    if (lane + 64 * q < p.r) lt[q] = bf16_to_f32(p.t[lane + 64 * q]);
 
-  // all weight pieces and their block statistics, up front and piece by piece
-  // (piece j = row j / IPR, 1 KB piece j % IPR), so piece 0 can be used first
-  u32x4_t w[NL];
-  uint32_t qv[NL];
-  float sv[NL];
-  const bool nested = p.scales == nullptr;
+  GdRound<RW, IPR> b0, b1, b2;
+  gd_load(b0, p, nb, lane, KB);
+  if (rounds > 1) gd_load(b1, p, nb + stride, lane, KB);
+
+  // X in LDS by (piece, dword, lane): 16-byte chunk c = 256 i + 4 l + h (elements
+  // 2048 i + 32 l + 8 h ..) sits at 256 i + 64 h + l, so the reads of a piece's
+  // dword h by the 64 lanes are 1 KB contiguous (bank-conflict free).
 #pragma unroll
-  for (int j = 0; j < NL; ++j) {
-    const int r = j / IPR, i = j - r * IPR;
-    const int64_t n = n0 + r < p.N ? n0 + r : p.N - 1;
-    w[j] = *reinterpret_cast<const u32x4_t*>(p.packed + (uint32_t)(n * (p.K >> 1) + 1024 * i + 16 * lane));
-    const uint32_t blk = (uint32_t)(n * KB + 32 * i + (lane >> 1));
-    if (nested) {
-      qv[j] = p.q[blk];
-      sv[j] = p.absmax2[blk >> p.dq_shift];
-    } else {
-      qv[j] = 0;
-      sv[j] = p.scales[blk];
-    }
+  for (int it = 0; it < XIT; ++it) {
+    const int c = tid + it * GD_NT;
+    if (c < XCH) *reinterpret_cast<u32x4_t*>(gd_xs + 8 * ((c & ~255) | ((c & 3) << 6) | ((c >> 2) & 63))) = xr[it];
   }
-  // LoRA operands, also up front: lane j (and j + 64) holds T[j] and B[n, j] of its rows
-  float lt[2] = {0.0f, 0.0f}, lbv[RW][2];
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int jr = lane + 64 * q;
-    const bool on = jr < p.r;
-    if (on) lt[q] = bf16_to_f32(p.t[jr]);
-#pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      const int64_t n = n0 + r < p.N ? n0 + r : p.N - 1;
-      lbv[r][q] = on ? p.lb[n * p.r + jr] : 0.0f;
-    }
-  }
-#pragma unroll
-  for (int it = 0; it < XIT; ++it)
-    if (tid + it * GD_NT < XCH) *reinterpret_cast<u32x4_t*>(gd_xs + 8 * (tid + it * GD_NT)) = xr[it];
   {
     const float cv[16] = {cb0[0], cb0[1], cb0[2], cb0[3], cb1[0], cb1[1], cb1[2], cb1[3],
                           cb2[0], cb2[1], cb2[2], cb2[3], cb3[0], cb3[1], cb3[2], cb3[3]};
@@ -389,59 +459,15 @@ __global__ __launch_bounds__(GD_NT) void nf4_gemv_dot_kernel(const GemvParams p)
   __syncthreads();
 
   const uint32_t* tab = sm.tab + (lane & 31);
-  const int xrow = p.K + GD_XPAD;
-  float acc[RW][MM];
-#pragma unroll
-  for (int r = 0; r < RW; ++r)
-#pragma unroll
-    for (int m = 0; m < MM; ++m) acc[r][m] = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NL; ++j) {
-    const int r = j / IPR, i = j - r * IPR;
-    const int k0 = 2048 * i + 32 * lane;                               // first element of the piece
-    float bs[MM];
-#pragma unroll
-    for (int m = 0; m < MM; ++m) bs[m] = 0.0f;
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {                                      // 4 bytes per dword, 8 elements
-      u32x4_t xv[MM];
-#pragma unroll
-      for (int m = 0; m < MM; ++m) xv[m] = *reinterpret_cast<const u32x4_t*>(gd_xs + m * xrow + k0 + 8 * h);
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const uint32_t pair = tab[((w[j][h] >> (8 * b)) & 0xffu) * GV_TABW];
-#pragma unroll
-        for (int m = 0; m < MM; ++m) {
-          // copy the element out first: __builtin_bit_cast of a vector-element
-          // lvalue reads element 0 with this compiler
-          const uint32_t xw = xv[m][b];
-          bs[m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, pair),
-                                                 __builtin_bit_cast(bf16x2v, xw), bs[m], false);
-        }
-      }
-    }
-    const float sc = gv_scale(p, sm.code2s, qv[j], sv[j]);
-#pragma unroll
-    for (int m = 0; m < MM; ++m) {
-      acc[r][m] += sc * bs[m];
-      asm volatile("" : "+v"(acc[r][m]));   // materialise here: keeps each piece's lookups short-lived
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  // LoRA partials join the row sums; butterfly sum over the wave; lane r stores row r
-#pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    float v = acc[r][0] + (lt[0] * round_bf16(p.s * lbv[r][0]) + lt[1] * round_bf16(p.s * lbv[r][1]));
-#pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) v += __shfl_xor(v, sh);
-    acc[r][0] = v;
-  }
-  if (lane < RW) {
-    float v = acc[0][0];
-#pragma unroll
-    for (int r = 1; r < RW; ++r) v = lane == r ? acc[r][0] : v;
-    const int64_t n = n0 + lane;
-    if (n < p.N) p.y[n] = bf16_bits(v);
+  for (int j = 0; j < rounds; j += 3) {
+    if (j + 2 < rounds) gd_load(b2, p, nb + (j + 2) * stride, lane, KB);
+    gd_compute(b0, p, tab, gd_xs, sm.code2s, lt, nb + j * stride, lane);
+    if (j + 1 >= rounds) break;
+    if (j + 3 < rounds) gd_load(b0, p, nb + (j + 3) * stride, lane, KB);
+    gd_compute(b1, p, tab, gd_xs, sm.code2s, lt, nb + (j + 1) * stride, lane);
+    if (j + 2 >= rounds) break;
+    if (j + 4 < rounds) gd_load(b1, p, nb + (j + 4) * stride, lane, KB);
+    gd_compute(b2, p, tab, gd_xs, sm.code2s, lt, nb + (j + 2) * stride, lane);
   }
 }
 
@@ -494,24 +520,25 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
   const int64_t groups = ceil_div64(p.N, GV_ROWS);
   MOLT_REQUIRE(groups < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
   hipStream_t st = (hipStream_t)stream;
-  // Decode (M == 1): streaming dot-product kernel; rows per wave grow while the
-  // grid still has at least 192 workgroups of GD_WAVES waves. (At M >= 2 the
-  // MFMA kernel below is faster: the dot kernel's VALU and LDS work scale with M.)
+  // Decode (M == 1): streaming dot-product kernel, one row per wave per round,
+  // as many workgroups as fit on the GPU at once (two per CU at K = 4096, one at
+  // K = 14336, whose three rounds of 7 KB per wave need ~190 registers); the
+  // waves loop over the rounds.
   if (M == 1 && (w->cols == 4096 || w->cols == 14336) && aligned(w->packed, 16)) {
     const int ipr = (int)(w->cols / 2048);
-    int rw = 1;
-    while (rw < 4 && 2 * rw * ipr <= GD_MAXL && w->rows / (2 * rw * GD_WAVES) >= 192) rw *= 2;
-    const int64_t wgs = ceil_div64(w->rows, (int64_t)rw * GD_WAVES);
-    const size_t dyn = (size_t)(w->cols + GD_XPAD) * 2;
-    MOLT_REQUIRE(wgs < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
-#define MOLT_GD(RWv, IPRv) \
-    hipLaunchKernelGGL((nf4_gemv_dot_kernel<RWv, IPRv>), dim3((unsigned)wgs), dim3(GD_NT), dyn, st, p)
-    if (ipr == 2) {
-      if (rw == 1) MOLT_GD(1, 2); else if (rw == 2) MOLT_GD(2, 2); else MOLT_GD(4, 2);
-    } else {
-      if (rw == 1) MOLT_GD(1, 7); else MOLT_GD(2, 7);
+    static int cu_count[64];                                  // per device, filled on first use
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+      if (cu_count[dev] == 0) hipDeviceGetAttribute(&cu_count[dev], hipDeviceAttributeMultiprocessorCount, dev);
+      if (cu_count[dev] > 0) cus = cu_count[dev];
     }
-#undef MOLT_GD
+    const int rw = 1;                                         // rows per wave per round
+    const int64_t waves = std::min<int64_t>(ceil_div64(w->rows, rw), (int64_t)cus * GD_WAVES * (ipr == 2 ? 2 : 1));
+    const int64_t wgs = ceil_div64(waves, GD_WAVES);
+    const int rounds = (int)ceil_div64(w->rows, wgs * GD_WAVES * rw);
+    const size_t dyn = (size_t)(w->cols + GD_XPAD) * 2;
+    if (ipr == 2) hipLaunchKernelGGL((nf4_gemv_dot_kernel<1, 2>), dim3((unsigned)wgs), dim3(GD_NT), dyn, st, p, rounds);
+    else hipLaunchKernelGGL((nf4_gemv_dot_kernel<1, 7>), dim3((unsigned)wgs), dim3(GD_NT), dyn, st, p, rounds);
     return check_launch(who);
   }
   const bool q4 = nested && (w->cols / 64) % 4 == 0 && w->dq_block >= 4 && aligned(w->absmax_q, 4);
