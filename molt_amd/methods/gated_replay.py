@@ -213,9 +213,10 @@ class _FusedGatedNF4LoRA(torch.autograd.Function):
             up_a)
         d_down_a = ops.lora_grad(gate, up, 1, u_d, 1.0, 1)
         d_down_b = ops.lora_grad(dy, None, 0, t_d, s_d, 0)
-        d_gate_a = ops.lora_grad(flat, None, 0, u_g, 1.0, 1)
+        # dA_gate and dA_up both contract X: one pass over X with [U_g | U_u]
+        d_gu_a = ops.lora_grad(flat, None, 0, torch.cat([u_g, u_u], 1), 1.0, 1)
+        d_gate_a, d_up_a = d_gu_a[:r], d_gu_a[r:]
         d_gate_b = ops.lora_grad(dg, None, 0, t_gu[:, :r], s_g, 0)
-        d_up_a = ops.lora_grad(flat, None, 0, u_u, 1.0, 1)
         d_up_b = ops.lora_grad(du, None, 0, t_gu[:, r:], s_u, 0)
         return (dx.reshape(ctx.input_shape), None, d_gate_a, d_gate_b, None, d_up_a, d_up_b, None, d_down_a,
                 d_down_b, None, None, None, None, None, None)
