@@ -471,6 +471,198 @@ __global__ __launch_bounds__(GD_NT) void nf4_gemv_dot_kernel(const GemvParams p,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Streaming MFMA variant for 2 <= M <= 16 at K = 4096. A workgroup walks
+// 16-row groups of W (group blockIdx.x + j * gridDim.x in round j); its 8
+// waves split K, wave w owning blocks 8w .. 8w + 7 of every row, so each
+// wave's X fragments (16 rows of X, 128 bytes per lane) are loaded once and
+// stay in registers. A round's loads (8 bytes per lane per block, the block
+// statistics, and for waves w < r / 32 the LoRA B rows of rank chunk w) are
+// issued two rounds ahead into three rotating register sets. Per block, two
+// v_mfma_f32_16x16x32_bf16 over bf16 code pairs from the replicated LDS table
+// give the block's partial products, scaled by the block scale in fp32 (as in
+// nf4_gemv_kernel); the 8 waves' 16 x 16 partials are summed through a
+// double-buffered LDS area, one barrier per round.
+constexpr int GM_WAVES = 8;
+constexpr int GM_NT = 64 * GM_WAVES;
+
+// mode 0: resolved fp32 scales; 1: nested, one u8 code per block; 2: nested,
+// the codes of 4 blocks in one 4-byte load sharing one absmax2 entry.
+template <int SM>
+struct GmRound {
+  static constexpr int NS = SM == 2 ? 2 : 8;
+  u32x2_t w[8];
+  uint32_t q[NS];
+  float s[NS];
+  f32x4_t lb[2];
+};
+
+struct GmSmem {
+  uint32_t tab[256 * GV_TABW];                            // bf16 code pair of byte b at [b * 32 + copy]
+  float code2s[256];
+  f32x4_t red[2][GM_WAVES][64];
+};
+
+template <int SM>
+MOLT_DEV void gm_load(GmRound<SM>& R, const GemvParams& p, int64_t grp, int wave, int col, int g, bool lora) {
+  const int64_t n = 16 * grp + col < p.N ? 16 * grp + col : p.N - 1;
+  const uint32_t blk0 = (uint32_t)(n * 64 + 8 * wave);                 // K = 4096: 64 blocks per row
+  const uint32_t wofs = (uint32_t)(n * 2048 + 256 * wave + 8 * g);
+#pragma unroll
+  for (int b = 0; b < 8; ++b) R.w[b] = *reinterpret_cast<const u32x2_t*>(p.packed + wofs + 32u * b);
+  if (SM == 2) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      R.q[u] = *reinterpret_cast<const uint32_t*>(p.q + blk0 + 4 * u);
+      R.s[u] = p.absmax2[(blk0 + 4 * u) >> p.dq_shift];
+    }
+  } else {
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      if (SM == 0) {
+        R.q[b] = 0;
+        R.s[b] = p.scales[blk0 + b];
+      } else {
+        R.q[b] = p.q[blk0 + b];
+        R.s[b] = p.absmax2[(blk0 + b) >> p.dq_shift];
+      }
+    }
+  }
+  if (lora) {
+    const int j = 32 * wave + 8 * g;                                   // first rank of the lane's 8
+    const float* br = p.lb + n * p.r + j;
+    const bool full = j + 8 <= p.r && (((uintptr_t)br) & 15) == 0;
+    if (full) {
+      R.lb[0] = *reinterpret_cast<const f32x4_t*>(br);
+      R.lb[1] = *reinterpret_cast<const f32x4_t*>(br + 4);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = j + e < p.r ? p.lb[n * p.r + j + e] : 0.0f;
+        R.lb[e >> 2][e & 3] = v;
+      }
+    }
+  }
+}
+
+template <int SM>
+MOLT_DEV f32x4_t gm_compute(const GmRound<SM>& R, const GemvParams& p, const uint32_t* tab, const float* code2s,
+                            const u32x4_t (&xf)[8][2], const u32x4_t& tf, bool lora) {
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    u32x4_t w0, w1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      w0[j] = tab[((R.w[b][0] >> (8 * j)) & 0xffu) * GV_TABW];
+      w1[j] = tab[((R.w[b][1] >> (8 * j)) & 0xffu) * GV_TABW];
+    }
+    f32x4_t tmp = {0.f, 0.f, 0.f, 0.f};
+    tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, xf[b][0]),
+                                                  __builtin_bit_cast(bf16x8v, w0), tmp, 0, 0, 0);
+    tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, xf[b][1]),
+                                                  __builtin_bit_cast(bf16x8v, w1), tmp, 0, 0, 0);
+    const float sc = SM == 2 ? gv_scale(p, code2s, R.q[b / 4] >> (8 * (b % 4)), R.s[b / 4])
+                             : gv_scale(p, code2s, R.q[b], R.s[b]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += sc * tmp[e];
+  }
+  if (lora) {
+    u32x4_t bw;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      bw[e] = pack_bf16x2(p.s * R.lb[e >> 1][2 * (e & 1)], p.s * R.lb[e >> 1][2 * (e & 1) + 1]);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, tf), __builtin_bit_cast(bf16x8v, bw),
+                                                  acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+template <int SM>
+__global__ __launch_bounds__(GM_NT) void nf4_gemv_ms_kernel(const GemvParams p, int rounds) {
+  __shared__ GmSmem sm;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, g = lane >> 4;
+  const bool lora = 32 * wave < p.r;                                   // this wave's rank chunk
+
+  typedef __attribute__((address_space(4))) const f32x4_t* cptr_t;
+  const cptr_t cbp = (cptr_t)p.code;
+  const f32x4_t cb0 = cbp[0], cb1 = cbp[1], cb2 = cbp[2], cb3 = cbp[3];
+  const float c2 = p.code2 ? p.code2[tid & 255] : 0.0f;
+
+  // X fragments of the wave's K slice (rows >= M repeat row M - 1; their
+  // outputs are never stored) and the wave's T fragment.
+  u32x4_t xf[8][2];
+  {
+    const int mc = col < p.M ? col : p.M - 1;
+    const uint16_t* xr = p.x + (int64_t)mc * p.ldx + 512 * wave + 16 * g;
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) xf[b][h] = *reinterpret_cast<const u32x4_t*>(xr + 64 * b + 8 * h);
+  }
+  u32x4_t tf = {0u, 0u, 0u, 0u};
+  if (lora) {
+    const int mc = col < p.M ? col : p.M - 1;
+    uint16_t e[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = 32 * wave + 8 * g + i;
+      e[i] = j < p.r ? p.t[(int64_t)mc * p.ldt + j] : (uint16_t)0;
+    }
+    tf = __builtin_bit_cast(u32x4_t, e);
+  }
+
+  GmRound<SM> b0, b1, b2;
+  const int64_t g0 = blockIdx.x, gs = gridDim.x;
+  gm_load(b0, p, g0, wave, col, g, lora);
+  if (rounds > 1) gm_load(b1, p, g0 + gs, wave, col, g, lora);
+
+  {
+    const float cv[16] = {cb0[0], cb0[1], cb0[2], cb0[3], cb1[0], cb1[1], cb1[2], cb1[3],
+                          cb2[0], cb2[1], cb2[2], cb2[3], cb3[0], cb3[1], cb3[2], cb3[3]};
+    static_assert(GV_TABW == 32 && GM_NT == 512, "table build covers 256 x 32 entries");
+    const int lo = (tid >> 5) & 15, copy = tid & 31;
+    float clo = cv[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) clo = lo == i ? cv[i] : clo;
+#pragma unroll
+    for (int hi = 0; hi < 16; ++hi) {
+      const float first = p.order ? cv[hi] : clo, second = p.order ? clo : cv[hi];
+      sm.tab[(hi * 16 + lo) * GV_TABW + copy] = pack_bf16x2(first, second);
+    }
+    if (tid < 256) sm.code2s[tid] = c2;
+  }
+  __syncthreads();
+  const uint32_t* tab = sm.tab + (lane & 31);
+
+  // Round j: partials into red[j & 1], barrier, threads 0..255 sum and store.
+  auto finish = [&](const f32x4_t& acc, int j) {
+    sm.red[j & 1][wave][lane] = acc;
+    __syncthreads();
+    if (tid < 256) {
+      const int ln = tid >> 2, e = tid & 3;
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < GM_WAVES; ++w) v += sm.red[j & 1][w][ln][e];
+      const int m = 4 * (ln >> 4) + e;
+      const int64_t n = 16 * (g0 + (int64_t)j * gs) + (ln & 15);
+      if (m < p.M && n < p.N) p.y[(int64_t)m * p.ldy + n] = bf16_bits(v);
+    }
+  };
+  for (int j = 0; j < rounds; j += 3) {
+    if (j + 2 < rounds) gm_load(b2, p, g0 + (j + 2) * gs, wave, col, g, lora);
+    finish(gm_compute(b0, p, tab, sm.code2s, xf, tf, lora), j);
+    if (j + 1 >= rounds) break;
+    if (j + 3 < rounds) gm_load(b0, p, g0 + (j + 3) * gs, wave, col, g, lora);
+    finish(gm_compute(b1, p, tab, sm.code2s, xf, tf, lora), j + 1);
+    if (j + 2 >= rounds) break;
+    if (j + 4 < rounds) gm_load(b1, p, g0 + (j + 4) * gs, wave, col, g, lora);
+    finish(gm_compute(b2, p, tab, sm.code2s, xf, tf, lora), j + 2);
+  }
+}
+
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 }  // namespace
@@ -539,6 +731,25 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
     const size_t dyn = (size_t)(w->cols + GD_XPAD) * 2;
     if (ipr == 2) hipLaunchKernelGGL((nf4_gemv_dot_kernel<1, 2>), dim3((unsigned)wgs), dim3(GD_NT), dyn, st, p, rounds);
     else hipLaunchKernelGGL((nf4_gemv_dot_kernel<1, 7>), dim3((unsigned)wgs), dim3(GD_NT), dyn, st, p, rounds);
+    return check_launch(who);
+  }
+  // 2 <= M <= 16 at K = 4096: streaming MFMA kernel over 16-row groups, one
+  // workgroup per CU (the 8 waves split K).
+  if (w->cols == 4096 && aligned(w->packed, 8) && aligned(x, 16) && ldx % 8 == 0 &&
+      (r == 0 || (ldt >= r))) {
+    static int cu_count2[64];
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+      if (cu_count2[dev] == 0) hipDeviceGetAttribute(&cu_count2[dev], hipDeviceAttributeMultiprocessorCount, dev);
+      if (cu_count2[dev] > 0) cus = cu_count2[dev];
+    }
+    const int64_t groups16 = ceil_div64(w->rows, 16);
+    const int64_t wgs = std::min<int64_t>(groups16, cus);
+    const int rounds = (int)ceil_div64(groups16, wgs);
+    const bool q4u = nested && w->dq_block >= 4 && aligned(w->absmax_q, 4);
+    if (!nested) hipLaunchKernelGGL((nf4_gemv_ms_kernel<0>), dim3((unsigned)wgs), dim3(GM_NT), 0, st, p, rounds);
+    else if (q4u) hipLaunchKernelGGL((nf4_gemv_ms_kernel<2>), dim3((unsigned)wgs), dim3(GM_NT), 0, st, p, rounds);
+    else hipLaunchKernelGGL((nf4_gemv_ms_kernel<1>), dim3((unsigned)wgs), dim3(GM_NT), 0, st, p, rounds);
     return check_launch(who);
   }
   const bool q4 = nested && (w->cols / 64) % 4 == 0 && w->dq_block >= 4 && aligned(w->absmax_q, 4);
