@@ -72,6 +72,30 @@ def test_gemv_decode_shapes_match_oracle(m, n, k, nested, order):
     assert_close_fro(np_f32(y), bf16_values(x) @ wo.T, what="Y")
 
 
+@pytest.mark.parametrize("m,n", [(3, 1000), (16, 264)])
+def test_gemv_nested_codes_at_odd_address(m, n):
+    # u8 block codes 1 byte past a 4-byte boundary: the K = 4096 MFMA kernel's
+    # per-block code loads (no 4-block code words) with LoRA rank chunks 0..2.
+    print(f"gemv odd-address codes m={m} n={n}", flush=True)
+    k, r, s = 4096, 80, 2.0
+    w = seeded((n, k), 110 + n, std=0.02, dtype=torch.float32)
+    packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True)
+    buf = torch.zeros(qs.absmax.numel() + 16, device=qs.absmax.device, dtype=torch.uint8)
+    codes = buf[1:1 + qs.absmax.numel()]
+    codes.copy_(qs.absmax)
+    assert codes.data_ptr() % 4 == 1
+    x = seeded((m, k), 111 + m)
+    a = uniform((r, k), 112, 1.0 / np.sqrt(k))
+    b = seeded((n, r), 113, std=0.01, dtype=torch.float32)
+    t = ops.lora_project(x, None, 0, 1.0, a, 0)
+    s2 = qs.state2
+    y = ops.nf4_gemv(x, packed.reshape(-1), None, codes, s2.absmax, s2.code, float(qs.offset), int(s2.blocksize),
+                     qs.code, n, k, qs.nibble_order, t, b, s)
+    wo = oracle_weight(packed, qs).dequant_bf16().astype(np.float64)
+    ref = O.lora_linear_forward(bf16_values(x), wo, bf16_values(a), bf16_values(b), s)
+    assert_close_fro(np_f32(y), ref, what="Y")
+
+
 def test_gemv_resolved_scales_and_low_nibble_layout():
     w = seeded((512, 1024), 80, std=0.02, dtype=torch.float32)
     packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=False, nibble_order=0)
