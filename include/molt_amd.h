@@ -197,8 +197,9 @@ int molt_lora_grad(const uint16_t* l, const uint16_t* l2, int64_t ldl, int32_t l
  * rounded to bf16 times the fp32 scale. T bf16 [M, r] from molt_lora_project,
  * B fp32 [N, r] (row stride r); r = 0 skips LoRA. Requires cols % 64 == 0,
  * block_size == 64 and a power-of-two dq_block. molt_nf4_gemv_workspace()
- * returns the workspace size (0: the kernel needs none; the arguments are kept
- * so callers need not change if a later kernel does).
+ * returns the workspace size: fp32 partials (slices x M x N) when the kernel
+ * for 2 <= M <= 16 splits K over workgroups (K = 14336: four slices), else 0.
+ * Concurrent calls need separate workspaces.
  * Replaces the bnb.matmul_4bit decode path (training/qlora.py:1332-1358). */
 size_t molt_nf4_gemv_workspace(int64_t M, int64_t N, int64_t K);
 int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,

@@ -472,11 +472,14 @@ __global__ __launch_bounds__(GD_NT) void nf4_gemv_dot_kernel(const GemvParams p,
 }
 
 // ---------------------------------------------------------------------------
-// Streaming MFMA variant for 2 <= M <= 16 at K = 4096. A workgroup walks
-// 16-row groups of W (group blockIdx.x + j * gridDim.x in round j); its 8
-// waves split K, wave w owning blocks 8w .. 8w + 7 of every row, so each
-// wave's X fragments (16 rows of X, 128 bytes per lane) are loaded once and
-// stay in registers. A round's loads (8 bytes per lane per block, the block
+// Streaming MFMA variant for 2 <= M <= 16 and K a multiple of 3584 or 4096.
+// A workgroup walks 16-row groups of W (group blockIdx.x + j * gridDim.x in
+// round j) over one K slice of NW * 512 elements (slice blockIdx.y); its
+// first NW waves split the slice, wave w owning blocks 8w .. 8w + 7 of the
+// slice in every row, so each wave's X fragments (16 rows of X, 128 bytes
+// per lane) are loaded once and stay in registers. With one slice the
+// outputs are stored as bf16; with several (K = 14336: four slices of 3584)
+// each slice writes fp32 partials that gm_reduce_kernel sums in slice order. A round's loads (8 bytes per lane per block, the block
 // statistics, and for waves w < r / 32 the LoRA B rows of rank chunk w) are
 // issued two rounds ahead into three rotating register sets. Per block, two
 // v_mfma_f32_16x16x32_bf16 over bf16 code pairs from the replicated LDS table
@@ -504,10 +507,11 @@ struct GmSmem {
 };
 
 template <int SM>
-MOLT_DEV void gm_load(GmRound<SM>& R, const GemvParams& p, int64_t grp, int wave, int col, int g, bool lora) {
+MOLT_DEV void gm_load(GmRound<SM>& R, const GemvParams& p, int64_t grp, int kw, int col, int g, bool lora) {
+  // kw: first element of the wave's 512-element K range
   const int64_t n = 16 * grp + col < p.N ? 16 * grp + col : p.N - 1;
-  const uint32_t blk0 = (uint32_t)(n * 64 + 8 * wave);                 // K = 4096: 64 blocks per row
-  const uint32_t wofs = (uint32_t)(n * 2048 + 256 * wave + 8 * g);
+  const uint32_t blk0 = (uint32_t)(n * (p.K >> 6) + (kw >> 6));
+  const uint32_t wofs = (uint32_t)(n * (p.K >> 1) + (kw >> 1) + 8 * g);
 #pragma unroll
   for (int b = 0; b < 8; ++b) R.w[b] = *reinterpret_cast<const u32x2_t*>(p.packed + wofs + 32u * b);
   if (SM == 2) {
@@ -529,7 +533,7 @@ MOLT_DEV void gm_load(GmRound<SM>& R, const GemvParams& p, int64_t grp, int wave
     }
   }
   if (lora) {
-    const int j = 32 * wave + 8 * g;                                   // first rank of the lane's 8
+    const int j = 32 * ((kw >> 9) & 7) + 8 * g;                        // rank chunk = wave index
     const float* br = p.lb + n * p.r + j;
     const bool full = j + 8 <= p.r && (((uintptr_t)br) & 15) == 0;
     if (full) {
@@ -578,13 +582,16 @@ MOLT_DEV f32x4_t gm_compute(const GmRound<SM>& R, const GemvParams& p, const uin
   return acc;
 }
 
-template <int SM>
-__global__ __launch_bounds__(GM_NT) void nf4_gemv_ms_kernel(const GemvParams p, int rounds) {
+template <int SM, int NW>
+__global__ __launch_bounds__(GM_NT) void nf4_gemv_ms_kernel(const GemvParams p, int rounds, float* part) {
+  static_assert(NW >= 4 && NW <= GM_WAVES, "K slice of NW x 512 elements");
   __shared__ GmSmem sm;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, g = lane >> 4;
-  const bool lora = 32 * wave < p.r;                                   // this wave's rank chunk
+  const bool active = NW == GM_WAVES || wave < NW;                     // waves >= NW only help reduce
+  const int kw = (int)blockIdx.y * NW * 512 + 512 * wave;              // the wave's K range
+  const bool lora = active && blockIdx.y == 0 && 32 * wave < p.r;      // rank chunk `wave`, slice 0 only
 
   typedef __attribute__((address_space(4))) const f32x4_t* cptr_t;
   const cptr_t cbp = (cptr_t)p.code;
@@ -594,9 +601,9 @@ __global__ __launch_bounds__(GM_NT) void nf4_gemv_ms_kernel(const GemvParams p, 
   // X fragments of the wave's K slice (rows >= M repeat row M - 1; their
   // outputs are never stored) and the wave's T fragment.
   u32x4_t xf[8][2];
-  {
+  if (active) {
     const int mc = col < p.M ? col : p.M - 1;
-    const uint16_t* xr = p.x + (int64_t)mc * p.ldx + 512 * wave + 16 * g;
+    const uint16_t* xr = p.x + (int64_t)mc * p.ldx + kw + 16 * g;
 #pragma unroll
     for (int b = 0; b < 8; ++b)
 #pragma unroll
@@ -616,8 +623,8 @@ __global__ __launch_bounds__(GM_NT) void nf4_gemv_ms_kernel(const GemvParams p, 
 
   GmRound<SM> b0, b1, b2;
   const int64_t g0 = blockIdx.x, gs = gridDim.x;
-  gm_load(b0, p, g0, wave, col, g, lora);
-  if (rounds > 1) gm_load(b1, p, g0 + gs, wave, col, g, lora);
+  if (active) gm_load(b0, p, g0, kw, col, g, lora);
+  if (active && rounds > 1) gm_load(b1, p, g0 + gs, kw, col, g, lora);
 
   {
     const float cv[16] = {cb0[0], cb0[1], cb0[2], cb0[3], cb1[0], cb1[1], cb1[2], cb1[3],
@@ -637,30 +644,47 @@ __global__ __launch_bounds__(GM_NT) void nf4_gemv_ms_kernel(const GemvParams p, 
   __syncthreads();
   const uint32_t* tab = sm.tab + (lane & 31);
 
-  // Round j: partials into red[j & 1], barrier, threads 0..255 sum and store.
+  // Round j: partials into red[j & 1], barrier, threads 0..255 sum (in wave
+  // order) and store bf16, or an fp32 partial of this K slice.
   auto finish = [&](const f32x4_t& acc, int j) {
-    sm.red[j & 1][wave][lane] = acc;
+    if (active) sm.red[j & 1][wave][lane] = acc;
     __syncthreads();
     if (tid < 256) {
       const int ln = tid >> 2, e = tid & 3;
       float v = 0.0f;
 #pragma unroll
-      for (int w = 0; w < GM_WAVES; ++w) v += sm.red[j & 1][w][ln][e];
+      for (int w = 0; w < NW; ++w) v += sm.red[j & 1][w][ln][e];
       const int m = 4 * (ln >> 4) + e;
       const int64_t n = 16 * (g0 + (int64_t)j * gs) + (ln & 15);
-      if (m < p.M && n < p.N) p.y[(int64_t)m * p.ldy + n] = bf16_bits(v);
+      if (m < p.M && n < p.N) {
+        if (gridDim.y == 1) p.y[(int64_t)m * p.ldy + n] = bf16_bits(v);
+        else part[((int64_t)blockIdx.y * p.M + m) * p.N + n] = v;
+      }
     }
   };
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
   for (int j = 0; j < rounds; j += 3) {
-    if (j + 2 < rounds) gm_load(b2, p, g0 + (j + 2) * gs, wave, col, g, lora);
-    finish(gm_compute(b0, p, tab, sm.code2s, xf, tf, lora), j);
+    if (active && j + 2 < rounds) gm_load(b2, p, g0 + (j + 2) * gs, kw, col, g, lora);
+    finish(active ? gm_compute(b0, p, tab, sm.code2s, xf, tf, lora) : zero, j);
     if (j + 1 >= rounds) break;
-    if (j + 3 < rounds) gm_load(b0, p, g0 + (j + 3) * gs, wave, col, g, lora);
-    finish(gm_compute(b1, p, tab, sm.code2s, xf, tf, lora), j + 1);
+    if (active && j + 3 < rounds) gm_load(b0, p, g0 + (j + 3) * gs, kw, col, g, lora);
+    finish(active ? gm_compute(b1, p, tab, sm.code2s, xf, tf, lora) : zero, j + 1);
     if (j + 2 >= rounds) break;
-    if (j + 4 < rounds) gm_load(b1, p, g0 + (j + 4) * gs, wave, col, g, lora);
-    finish(gm_compute(b2, p, tab, sm.code2s, xf, tf, lora), j + 2);
+    if (active && j + 4 < rounds) gm_load(b1, p, g0 + (j + 4) * gs, kw, col, g, lora);
+    finish(active ? gm_compute(b2, p, tab, sm.code2s, xf, tf, lora) : zero, j + 2);
   }
+}
+
+// Y[m, n] = bf16(sum over K slices of the fp32 partials), slices in order.
+__global__ void gm_reduce_kernel(const float* __restrict__ part, int slices, int M, int64_t N,
+                                 uint16_t* __restrict__ y, int64_t ldy) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)M * N) return;
+  const int m = (int)(i / N);
+  const int64_t n = i - (int64_t)m * N;
+  float v = 0.0f;
+  for (int k = 0; k < slices; ++k) v += part[(int64_t)k * M * N + i];
+  y[(int64_t)m * ldy + n] = bf16_bits(v);
 }
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
@@ -670,16 +694,32 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 using namespace molt;
 
+namespace molt {
+namespace {
+// K slices of the streaming MFMA kernel (2 <= M <= 16): 0 when it does not apply.
+int gm_slices(int64_t M, int64_t K, int& nw) {
+  nw = 8;
+  if (M < 2 || M > 16 || K % 512 != 0) return 0;
+  const int64_t chunks = K / 512;
+  if (chunks == 8) return 1;
+  if (chunks % 7 == 0 && chunks / 7 <= 8) { nw = 7; return (int)(chunks / 7); }
+  if (chunks % 8 == 0 && chunks / 8 <= 8) return (int)(chunks / 8);
+  return 0;
+}
+}  // namespace
+}  // namespace molt
+
 extern "C" size_t molt_nf4_gemv_workspace(int64_t M, int64_t N, int64_t K) {
-  (void)M; (void)N; (void)K;
-  return 0;   // the kernel needs no workspace; the argument is kept for callers
+  // fp32 partials of the K slices when the streaming MFMA kernel splits K
+  int nw = 8;
+  const int ks = gm_slices(M, K, nw);
+  return ks > 1 ? (size_t)ks * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
 extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,
                              const uint16_t* t, int64_t ldt, const float* lora_b, int32_t r, float scaling,
                              uint16_t* y, int64_t ldy, void* workspace, size_t workspace_bytes,
                              void* stream) {
-  (void)workspace; (void)workspace_bytes;
   const char* who = "molt_nf4_gemv";
   MOLT_REQUIRE(w && w->packed && w->code && x && y, MOLT_EINVAL, "%s: null argument", who);
   MOLT_REQUIRE(M >= 1 && M <= 16, MOLT_EUNSUPPORTED, "%s: M=%lld outside 1..16", who, (long long)M);
@@ -733,10 +773,15 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
     else hipLaunchKernelGGL((nf4_gemv_dot_kernel<1, 7>), dim3((unsigned)wgs), dim3(GD_NT), dyn, st, p, rounds);
     return check_launch(who);
   }
-  // 2 <= M <= 16 at K = 4096: streaming MFMA kernel over 16-row groups, one
-  // workgroup per CU (the 8 waves split K).
-  if (w->cols == 4096 && aligned(w->packed, 8) && aligned(x, 16) && ldx % 8 == 0 &&
-      (r == 0 || (ldt >= r))) {
+  // 2 <= M <= 16, K of 8 (or a multiple of 7 or 8) 512-element chunks:
+  // streaming MFMA kernel over 16-row groups, one workgroup per CU, K split
+  // over the waves (and, past 4096, over workgroups with fp32 partials).
+  int gm_nw = 8;
+  const int gm_ks = gm_slices(M, w->cols, gm_nw);
+  if (gm_ks > 0 && aligned(w->packed, 8) && aligned(x, 16) && ldx % 8 == 0) {
+    const size_t need = molt_nf4_gemv_workspace(M, w->rows, w->cols);
+    MOLT_REQUIRE(workspace_bytes >= need && (need == 0 || aligned(workspace, 16)), MOLT_EWORKSPACE,
+                 "%s: workspace of %zu bytes (16-byte aligned) needed, got %zu", who, need, workspace_bytes);
     static int cu_count2[64];
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
@@ -744,12 +789,23 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
       if (cu_count2[dev] > 0) cus = cu_count2[dev];
     }
     const int64_t groups16 = ceil_div64(w->rows, 16);
-    const int64_t wgs = std::min<int64_t>(groups16, cus);
+    const int64_t wgs = std::max<int64_t>(1, std::min<int64_t>(groups16, cus / gm_ks));
     const int rounds = (int)ceil_div64(groups16, wgs);
     const bool q4u = nested && w->dq_block >= 4 && aligned(w->absmax_q, 4);
-    if (!nested) hipLaunchKernelGGL((nf4_gemv_ms_kernel<0>), dim3((unsigned)wgs), dim3(GM_NT), 0, st, p, rounds);
-    else if (q4u) hipLaunchKernelGGL((nf4_gemv_ms_kernel<2>), dim3((unsigned)wgs), dim3(GM_NT), 0, st, p, rounds);
-    else hipLaunchKernelGGL((nf4_gemv_ms_kernel<1>), dim3((unsigned)wgs), dim3(GM_NT), 0, st, p, rounds);
+    float* part = gm_ks > 1 ? static_cast<float*>(workspace) : nullptr;
+    const dim3 grid((unsigned)wgs, (unsigned)gm_ks);
+#define MOLT_GM(SMv, NWv) hipLaunchKernelGGL((nf4_gemv_ms_kernel<SMv, NWv>), grid, dim3(GM_NT), 0, st, p, rounds, part)
+    if (gm_nw == 8) {
+      if (!nested) MOLT_GM(0, 8); else if (q4u) MOLT_GM(2, 8); else MOLT_GM(1, 8);
+    } else {
+      if (!nested) MOLT_GM(0, 7); else if (q4u) MOLT_GM(2, 7); else MOLT_GM(1, 7);
+    }
+#undef MOLT_GM
+    if (gm_ks > 1) {
+      const int64_t n = M * w->rows;
+      hipLaunchKernelGGL(gm_reduce_kernel, dim3((unsigned)ceil_div64(n, 256)), dim3(256), 0, st, part, gm_ks,
+                         (int)M, w->rows, y, ldy);
+    }
     return check_launch(who);
   }
   const bool q4 = nested && (w->cols / 64) % 4 == 0 && w->dq_block >= 4 && aligned(w->absmax_q, 4);

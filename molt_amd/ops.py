@@ -498,7 +498,7 @@ def nf4_gemv(x: Tensor, packed: Tensor, scales: Optional[Tensor], absmax_q: Opti
             raise ValueError(f"{what}: LoRA B shape {tuple(bb.shape)} != ({rows}, {r})")
     lib = _lib.load()
     ws_bytes = int(lib.molt_nf4_gemv_workspace(m, rows, cols))
-    ws = torch.zeros(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     _call("molt_nf4_gemv", x.data_ptr(), cols, m, C.byref(w), _ptr(tt), max(r, 1), _ptr(bb), r,
           float(scaling), y.data_ptr(), rows, _ptr(ws), ws_bytes, _stream(dev))
     return y

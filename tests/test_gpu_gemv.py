@@ -96,6 +96,24 @@ def test_gemv_nested_codes_at_odd_address(m, n):
     assert_close_fro(np_f32(y), ref, what="Y")
 
 
+@pytest.mark.parametrize("m,n,r", [(16, 1000, 64), (2, 4100, 16), (7, 520, 128)])
+def test_gemv_split_k_with_lora_matches_oracle(m, n, r):
+    # K = 14336 with M >= 2: four K slices of fp32 partials summed by a second kernel.
+    print(f"gemv split-K m={m} n={n} r={r}", flush=True)
+    k, s = 14336, 2.0
+    w = seeded((n, k), 120 + n, std=0.02, dtype=torch.float32)
+    packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True)
+    x = seeded((m, k), 121 + m)
+    a = uniform((r, k), 122, 1.0 / np.sqrt(k))
+    b = seeded((n, r), 123, std=0.01, dtype=torch.float32)
+    t = ops.lora_project(x, None, 0, 1.0, a, 0)
+    y = _gemv(x, packed, qs, t, b, s)
+    assert torch.equal(y, _gemv(x, packed, qs, t, b, s))
+    wo = oracle_weight(packed, qs).dequant_bf16().astype(np.float64)
+    ref = O.lora_linear_forward(bf16_values(x), wo, bf16_values(a), bf16_values(b), s)
+    assert_close_fro(np_f32(y), ref, what="Y")
+
+
 def test_gemv_resolved_scales_and_low_nibble_layout():
     w = seeded((512, 1024), 80, std=0.02, dtype=torch.float32)
     packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=False, nibble_order=0)
