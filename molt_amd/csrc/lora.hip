@@ -219,8 +219,8 @@ __global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_kernel(const ProjP
 // Gradient partials part[s][p][q] = sum over the s-th slice of M of
 // L(m, p) R(m, q). Both operands are loaded as 8 x 8 patches (8 rows of M,
 // 16 bytes each) and transposed in registers (v_perm) so that M, the
-// contraction index, is contiguous in LDS. One-deep register prefetch with
-// double-buffered LDS; the splits are summed in split order afterwards.
+// contraction index, is contiguous in LDS. One-deep register prefetch; the
+// splits are summed in split order afterwards.
 // ------------------------------------------------------------------------
 constexpr int GR_P = 128, GR_Q = 64, GR_NT = 256;
 constexpr int GR_WROWS = 64, GR_WCOLS = 32;   // waves 2 (p) x 2 (q)
@@ -280,8 +280,12 @@ MOLT_DEV void patch_store(const Patch& pt, const GradParams& p, uint16_t* ls, ui
 
 template <bool VEC, bool REPLAY>
 __global__ __launch_bounds__(GR_NT) void lora_grad_kernel(const GradParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t ls[2][GR_P * LDSW];
-  __shared__ __attribute__((aligned(16))) uint16_t rs[2][GR_Q * LDSW];
+  // One LDS tile (27 KB: three workgroups per CU) where the registers allow
+  // three; the SwiGLU-replay variant, held to two by its registers, double-
+  // buffers instead and saves a barrier per step.
+  constexpr int NB = REPLAY ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) uint16_t ls[NB][GR_P * LDSW];
+  __shared__ __attribute__((aligned(16))) uint16_t rs[NB][GR_Q * LDSW];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wp = wave & 1, wq = wave >> 1;
@@ -297,12 +301,23 @@ __global__ __launch_bounds__(GR_NT) void lora_grad_kernel(const GradParams p) {
   patch_load<VEC, REPLAY>(pt, p, wave, lane, mbeg, mend, p0, q0);
   patch_store<VEC, REPLAY>(pt, p, ls[0], rs[0], wave, lane);
   __syncthreads();
-  for (int s = 0; s < steps; ++s) {
-    const int cur = s & 1;
-    if (s + 1 < steps) patch_load<VEC, REPLAY>(pt, p, wave, lane, mbeg + (int64_t)(s + 1) * BK, mend, p0, q0);
-    mfma_step<2, 1>(ls[cur], rs[cur], wp * GR_WROWS, wq * GR_WCOLS, acc, lane);
-    if (s + 1 < steps) patch_store<VEC, REPLAY>(pt, p, ls[cur ^ 1], rs[cur ^ 1], wave, lane);
-    __syncthreads();
+  if constexpr (NB == 2) {
+    for (int s = 0; s < steps; ++s) {
+      const int cur = s & 1;
+      if (s + 1 < steps) patch_load<VEC, REPLAY>(pt, p, wave, lane, mbeg + (int64_t)(s + 1) * BK, mend, p0, q0);
+      mfma_step<2, 1>(ls[cur], rs[cur], wp * GR_WROWS, wq * GR_WCOLS, acc, lane);
+      if (s + 1 < steps) patch_store<VEC, REPLAY>(pt, p, ls[cur ^ 1], rs[cur ^ 1], wave, lane);
+      __syncthreads();
+    }
+  } else {
+    for (int s = 0; s < steps; ++s) {
+      if (s + 1 < steps) patch_load<VEC, REPLAY>(pt, p, wave, lane, mbeg + (int64_t)(s + 1) * BK, mend, p0, q0);
+      mfma_step<2, 1>(ls[0], rs[0], wp * GR_WROWS, wq * GR_WCOLS, acc, lane);
+      if (s + 1 >= steps) break;
+      __syncthreads();                               // the single tile is consumed
+      patch_store<VEC, REPLAY>(pt, p, ls[0], rs[0], wave, lane);
+      __syncthreads();
+    }
   }
 
   // acc[i][0] is C[p][q]: column q = lane % 32, rows p = 8(e/4) + 4(lane/32) + e%4.
