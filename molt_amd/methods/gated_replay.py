@@ -159,7 +159,7 @@ class _FusedGatedNF4LoRA(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx: Any, x, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_packed, down_a,
-                down_b, gate_qs, up_qs, down_qs, gate_scaling, up_scaling, down_scaling):
+                down_b, gate_qs, up_qs, down_qs, gate_scaling, up_scaling, down_scaling, save_gated):
         if x.device.type != "cuda" or x.dtype != torch.bfloat16:
             raise CapabilityError("fused gated NF4-LoRA MLP requires CUDA BF16 tensors")
         for t in (gate_a, gate_b, up_a, up_b, down_a, down_b):
@@ -184,20 +184,21 @@ class _FusedGatedNF4LoRA(torch.autograd.Function):
         t_d = ops.lora_project(gated, None, 0, 1.0, down_a, 0)
         y = ops.nf4_lora_forward(gated, down_packed.reshape(-1), resolved_nf4_scales(down_qs), down_qs.code,
                                  h_dim, i_dim, nibble_order(down_qs), 64, t_d, down_b, float(down_scaling))
-        del gated  # replayed in backward from (gate, up)
+        if not save_gated:
+            gated = None  # replayed in backward from (gate, up)
         ctx.qs = (gate_qs, up_qs, down_qs)
         ctx.scaling = (float(gate_scaling), float(up_scaling), float(down_scaling))
         ctx.dims = (h_dim, i_dim, r)
         ctx.input_shape = x.shape
-        ctx.save_for_backward(flat, gate, up, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed, up_a, up_b,
-                              down_packed, down_a, down_b)
+        ctx.save_for_backward(flat, gate, up, gated, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed, up_a,
+                              up_b, down_packed, down_a, down_b)
         return y.reshape(*x.shape[:-1], h_dim)
 
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx: Any, grad_output: torch.Tensor):
-        (flat, gate, up, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_packed, down_a,
-         down_b) = ctx.saved_tensors
+        (flat, gate, up, gated, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_packed,
+         down_a, down_b) = ctx.saved_tensors
         gate_qs, up_qs, down_qs = ctx.qs
         s_g, s_u, s_d = ctx.scaling
         h_dim, i_dim, r = ctx.dims
@@ -211,7 +212,10 @@ class _FusedGatedNF4LoRA(torch.autograd.Function):
             dg, du, gate_packed.reshape(-1), resolved_nf4_scales(gate_qs), up_packed.reshape(-1),
             resolved_nf4_scales(up_qs), gate_qs.code, i_dim, h_dim, nibble_order(gate_qs), u_g, u_u, gate_a,
             up_a)
-        d_down_a = ops.lora_grad(gate, up, 1, u_d, 1.0, 1)
+        if gated is not None:   # h kept from the forward: bitwise the replayed value
+            d_down_a = ops.lora_grad(gated, None, 0, u_d, 1.0, 1)
+        else:
+            d_down_a = ops.lora_grad(gate, up, 1, u_d, 1.0, 1)
         d_down_b = ops.lora_grad(dy, None, 0, t_d, s_d, 0)
         # dA_gate and dA_up both contract X: one pass over X with [U_g | U_u]
         d_gu_a = ops.lora_grad(flat, None, 0, torch.cat([u_g, u_u], 1), 1.0, 1)
@@ -219,7 +223,7 @@ class _FusedGatedNF4LoRA(torch.autograd.Function):
         d_gate_b = ops.lora_grad(dg, None, 0, t_gu[:, :r], s_g, 0)
         d_up_b = ops.lora_grad(du, None, 0, t_gu[:, r:], s_u, 0)
         return (dx.reshape(ctx.input_shape), None, d_gate_a, d_gate_b, None, d_up_a, d_up_b, None, d_down_a,
-                d_down_b, None, None, None, None, None, None)
+                d_down_b, None, None, None, None, None, None, None)
 
 
 def fused_gated_nf4_lora_mlp(
@@ -228,13 +232,18 @@ def fused_gated_nf4_lora_mlp(
     up_packed_weight: torch.Tensor, up_lora_a: torch.Tensor, up_lora_b: torch.Tensor,
     down_packed_weight: torch.Tensor, down_lora_a: torch.Tensor, down_lora_b: torch.Tensor,
     gate_quant_state: Any, up_quant_state: Any, down_quant_state: Any,
-    gate_scaling: float, up_scaling: float, down_scaling: float,
+    gate_scaling: float, up_scaling: float, down_scaling: float, save_gated: bool = True,
 ) -> torch.Tensor:
-    """``down(silu(gate(x)) * up(x))`` with NF4-LoRA projections as one autograd node."""
+    """``down(silu(gate(x)) * up(x))`` with NF4-LoRA projections as one autograd node.
+
+    ``save_gated`` keeps ``h = silu(gate) * up`` (bf16 [tokens, I]) for the
+    backward, whose down-adapter gradient then reads h instead of replaying it
+    from gate and up (half the bytes, no SiLU). ``False`` replays it, as the
+    reference's gated-replay node does, saving that memory."""
     return _FusedGatedNF4LoRA.apply(
         x, gate_packed_weight, gate_lora_a, gate_lora_b, up_packed_weight, up_lora_a, up_lora_b,
         down_packed_weight, down_lora_a, down_lora_b, gate_quant_state, up_quant_state, down_quant_state,
-        gate_scaling, up_scaling, down_scaling)
+        gate_scaling, up_scaling, down_scaling, bool(save_gated))
 
 
 # --------------------------------------------------------------------------

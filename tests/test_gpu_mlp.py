@@ -61,6 +61,27 @@ def test_fused_gated_mlp_matches_oracle(hidden, inter, r, m):
         assert_close_fro(np_f32(leaf.grad), ref, what=name)
 
 
+@pytest.mark.parametrize("hidden,inter,r,m", [(128, 256, 8, 32), (256, 448, 64, 200)])
+def test_fused_gated_mlp_saved_h_equals_replay(hidden, inter, r, m):
+    # Keeping h from the forward must give bit-identical gradients to replaying it.
+    s = 2.0
+    projs = [_proj(inter, hidden, r, 50), _proj(inter, hidden, r, 60), _proj(hidden, inter, r, 70)]
+    (pg, qg, _, _), (pu, qu, _, _), (pd, qd, _, _) = projs
+    dy = seeded((m, hidden), 81)
+    runs = []
+    for save in (True, False):
+        x = seeded((m, hidden), 80).requires_grad_()
+        leaves = []
+        for _, _, a, b in projs:
+            leaves += [a.clone().requires_grad_(), b.clone().requires_grad_()]
+        y = fused_gated_nf4_lora_mlp(x, pg, leaves[0], leaves[1], pu, leaves[2], leaves[3], pd, leaves[4],
+                                     leaves[5], qg, qu, qd, s, s, s, save_gated=save)
+        y.backward(dy)
+        runs.append([y.detach(), x.grad] + [leaf.grad for leaf in leaves])
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("hidden,intermediate", [(64, 96), (128, 256)])
 @pytest.mark.parametrize("rematerialize_up,offload_up,offload_gate",
                          [(False, False, False), (True, False, False), (False, True, False),
