@@ -509,31 +509,26 @@ constexpr int BUF = BM * LD;     // bf16 elements of one operand buffer (32 KB)
 constexpr int TABC = 16;         // interleaved copies of the code-pair table
 constexpr int EP_LD = 256 + 8;   // (128 x 128 path and backward) epilogue tile row stride
 
-// Operand buffer layout. A tile row holds 64 contraction elements as 8 chunks
-// of 16 B; chunks 0-3 (elements 0..31) of all rows form the first 16 KB half of
-// the buffer, chunks 4-7 the second. Within a half a row is 64 B. Row R is
-// stored at physical row P = R ^ ((R >> 3) & 3) and its four chunk positions
-// are XOR-swizzled by ((P >> 2) ^ (P >> 7)) & 3. Then
-//  * a ds_read_b128 of one chunk over 16 consecutive rows hits 16 distinct
-//    bank groups (the fragment reads),
-//  * 16-byte writes of one chunk over 32 consecutive rows, and 4-byte writes of
-//    32 rows spaced 8 apart (the backward's transposed dequant), spread over
-//    all 64 banks,
-//  * rows 32 apart inside a 128-row block differ by a constant, so with the
-//    halves a constant 16 KB apart every fragment read of a step is one of two
-//    per-lane base offsets plus an immediate.
-MOLT_DEV int loff(int R, int c) {
-  const int P = R ^ ((R >> 3) & 3);
-  return (c >> 2) * (BUF / 2) + P * 32 + ((((c & 3) ^ (P >> 2) ^ (P >> 7)) & 3) << 3);
-}
+// Operand buffer layout. A tile row holds its 64 contraction elements as 8
+// chunks of 16 B in one 128-byte line, row R at 128 R, chunk c at position
+// c ^ f(R) with f(R) = (R ^ ((R >> 3) & 3)) & 7. Then
+//  * a ds_read_b128 of one chunk over 16 consecutive rows (served 16 lanes per
+//    cycle over 64 banks) hits 16 distinct 16-byte bank groups: rows R and
+//    R + 8 of the group differ in R & 1 or in f (the fragment reads);
+//  * a 1 KB DMA block is 8 whole rows, so each 128-byte line of X is one
+//    request (half-line requests doubled the L1 traffic);
+//  * f(R + 32) = f(R), so the subtiles of a fragment read are one per-lane
+//    base offset (XOR-ed with the sub-step) plus an immediate of 32 rows.
+MOLT_DEV int lswz(int R) { return (R ^ ((R >> 3) & 3)) & 7; }
+MOLT_DEV int loff(int R, int c) { return R * 64 + ((c ^ lswz(R)) << 3); }
 
 // Global -> LDS DMA writes lane l's 16 bytes to (block base + 16 l): block blk
-// (1 KB) of a buffer holds physical rows 16 (blk & 15) .. +15 of half blk >> 4.
-// Returns the tile row and first contraction element the lane must fetch.
+// (1 KB) of a buffer holds rows 8 blk .. 8 blk + 7, lane l filling position
+// l % 8 of row 8 blk + l / 8. Returns the tile row and first contraction
+// element the lane must fetch.
 MOLT_DEV void dma_slot(int blk, int lane, int& R, int& k) {
-  const int P = ((blk & 15) << 4) + (lane >> 2);
-  R = P ^ ((P >> 3) & 3);
-  k = 32 * (blk >> 4) + 8 * (((lane & 3) ^ (P >> 2) ^ (P >> 7)) & 3);
+  R = 8 * blk + (lane >> 3);
+  k = 8 * ((lane & 7) ^ lswz(R));
 }
 
 // Kernel-argument pointers and the 16 codes stay in scalar registers or are
@@ -587,28 +582,26 @@ MOLT_DEV void build_tab(float2* tab, const float* __restrict__ code, int order, 
 
 // Per-lane fragment offsets: lane l supplies row (l % 32) of each 32-row
 // subtile and the 8-element half (l / 32) of a 16-deep sub-step. Sub-step kk
-// reads chunk 2 kk + l / 32: its offset is base[kk & 1] + (kk >> 1) * BUF / 2,
-// and subtile i adds 32 rows = 1024 elements.
-struct FragOff { int a[2], b[2]; };
+// reads chunk 2 kk + l / 32, whose position is (h ^ f(R)) ^ 2 kk: its offset
+// is base ^ (kk << 4) (the XOR touches only the position bits); subtile i adds
+// 32 rows = 2048 elements.
+struct FragOff { int a, b; };
 
 MOLT_DEV void frag_offsets(FragOff& f, int arow0, int brow0, int lane) {
   const int h = lane >> 5;
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    f.a[q] = loff(arow0 + (lane & 31), 2 * q + h);
-    f.b[q] = loff(brow0 + (lane & 31), 2 * q + h);
-  }
+  f.a = loff(arow0 + (lane & 31), h);
+  f.b = loff(brow0 + (lane & 31), h);
 }
 
 MOLT_DEV void load_frags(const uint16_t* __restrict__ ws, const uint16_t* __restrict__ xs, const FragOff& f, int kk,
                          bf16x8_t (&a)[TM], bf16x8_t (&b)[TN]) {
-  const int hoff = (kk >> 1) * (BUF / 2);
+  const int ao = f.a ^ (kk << 4), bo = f.b ^ (kk << 4);
 #pragma unroll
   for (int i = 0; i < TM; ++i)
-    a[i] = *reinterpret_cast<const bf16x8_t*>(ws + f.a[kk & 1] + hoff + 1024 * i);
+    a[i] = *reinterpret_cast<const bf16x8_t*>(ws + ao + 2048 * i);
 #pragma unroll
   for (int j = 0; j < TN; ++j)
-    b[j] = *reinterpret_cast<const bf16x8_t*>(xs + f.b[kk & 1] + hoff + 1024 * j);
+    b[j] = *reinterpret_cast<const bf16x8_t*>(xs + bo + 2048 * j);
 }
 
 MOLT_DEV void mfma_set(const bf16x8_t (&a)[TM], const bf16x8_t (&b)[TN], f32x16_t (&acc)[TM][TN]) {
@@ -671,16 +664,14 @@ MOLT_DEV void w_lookup(const WBytes& w, const float2* tabc, int d, float2 (&c)[4
 
 // Forward dequant slot of a thread: tile row R and 16-byte half of the row's
 // 32-byte slice of the step. A ds_write_b128 is served 8 consecutive lanes
-// per cycle over 32 banks, i.e. by the 16-byte slot (4 (P & 1) + chunk
-// position) mod 8 of each lane. The 8 lanes of a group therefore take
-// physical rows {0, 1, 4, 5, 8, 9, 12, 13} (+2, +16) of one half, whose slots
-// all differ; the two halves of a row sit in lanes l and l + 8, so the global
-// load of a row's 32 bytes stays within one instruction.
+// per cycle over 32 banks, i.e. by the lane's 16-byte slot (its chunk
+// position c ^ f(R)) mod 8. The 8 lanes of a group take 8 consecutive rows of
+// one half, whose f(R) all differ; the two halves of a row sit in lanes l and
+// l + 8, so the global load of a row's 32 bytes stays within one instruction.
 MOLT_DEV void wslot(int tid, int& R, int& half) {
-  const int l = tid & 63, g = l & 7;
+  const int l = tid & 63;
   half = (l >> 3) & 1;
-  const int P = 32 * (tid >> 6) + 16 * (l >> 5) + 2 * ((l >> 4) & 1) + (g & 1) + 4 * (g >> 1);
-  R = P ^ ((P >> 3) & 3);
+  R = 32 * (tid >> 6) + 8 * (l >> 4) + (l & 7);
 }
 
 // bf16(code * scale) of 8 elements (the rounding of dequantize_4bit) into chunk 4 * half + d of row R.
@@ -1169,10 +1160,10 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
   // l + 32 take rank groups 2m and 2m + 1 of the same columns (the permlane32
   // swap pairs them) and a wave's 32 column groups cover 256 contiguous columns,
   // so each 4-byte load instruction reads 128 contiguous bytes of two rows.
-  // A ds_write_b128 is served 8 consecutive lanes per cycle by the 16-byte slot
-  // (4 (P & 1) + chunk position) mod 8; for the transposed store of row
-  // 8 cg + k (+4) the slot varies with cg bits 0 and 4 only, so lane bits 0 and
-  // 1 carry them (two lanes per slot instead of four).
+  // A ds_write_b128 is served 8 consecutive lanes per cycle by the lane's
+  // 16-byte slot (chunk position) mod 8; for the transposed store of row
+  // R = 8 cg + k (+4) the position is m ^ f(R) and f(R) varies with cg & 3
+  // only, so lane bits 0 and 2 carry those (two lanes per slot).
   const int cg = (lane & 1) | (((lane >> 2) & 1) << 1) | (((lane >> 3) & 3) << 2) | (((lane >> 1) & 1) << 4);
   const int rg = tid >> 5;
   const int64_t col = min(tn * BN + 8 * cg, p.Kw - 8);
