@@ -5,8 +5,9 @@ Llama-3-8B MLP shape (BASELINE cfg4: H=4096, I=14336, r=64, alpha=128,
 M=8192 tokens), including every adapter gradient. Inputs are synthetic, seeded
 and already resident in HBM. Also reported: the roofline of the dominant
 kernel (the fused gate/up NF4 GEMM) from HIP events recorded around its
-launches on its own stream during the timed steps, the skinny-M NF4 GEMV sweep
-(cfg5, HBM GB/s), and the CPU baseline (the oracle's restatement of MOLT's
+launches on its own stream during the timed steps, the frozen RMSNorm kernels
+and the RMSNorm-replay recipe step, the skinny-M NF4 GEMV sweep (cfg5, HBM
+GB/s), and the CPU baseline (the oracle's restatement of MOLT's
 eager CPU path, cfg1, numpy fp32 on the host cores).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
@@ -136,6 +137,71 @@ def gemv_sweep(dev, reps: int = 20):
     return out
 
 
+def rmsnorm_bench(dev, projs, dy, s, M, H, steps: int, reps: int = 5):
+    """Frozen RMSNorm at the cfg4 residual shape ([M, H] bf16, bf16 weight):
+    forward and backward kernel time (HIP events over `reps` rounds of
+    launches over distinct input copies) against their algorithmic bytes, and the gated-MLP step through the RMSNorm-replay
+    recipe (norm forward + _ResidualRecipeGatedNF4LoRA + norm backward), which
+    saves the residual instead of the normalised input."""
+    import torch
+    from molt_amd import ops
+    from molt_amd.kernels.frozen_rmsnorm import _FrozenRMSNormFunction
+    from molt_amd.methods.gated_replay import _ResidualRecipeGatedNF4LoRA
+
+    g = torch.Generator(device="cpu").manual_seed(7)
+    src = torch.randn(M, H, generator=g).to(dev, torch.bfloat16)
+    w = (1.0 + 0.2 * torch.randn(H, generator=g)).to(dev, torch.bfloat16)
+    gy = torch.randn(M, H, generator=g).to(dev, torch.bfloat16)
+    eps = 1e-6
+    # rotate over distinct copies (>= 512 MiB of inputs) so that the kernels
+    # read HBM, not the 256 MB Infinity Cache
+    copies = max(2, math.ceil(512 * 2**20 / (M * H * 2)))
+    srcs = [src.clone() for _ in range(copies)]
+    gys = [gy.clone() for _ in range(copies)]
+    out = {}
+    for name, fn, nbytes in (("forward", lambda j: ops.rmsnorm_forward(srcs[j], w, eps, 0.0), 2 * M * H * 2 + H * 2),
+                             ("backward", lambda j: ops.rmsnorm_backward(gys[j], srcs[j], w, eps, 0.0),
+                              3 * M * H * 2 + H * 2)):
+        for j in range(copies):
+            fn(j)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for j in range(reps * copies):
+            fn(j % copies)
+        e1.record()
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * copies)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"us": round(us, 2), "bytes": nbytes, "GB_s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+        log(f"rmsnorm {name} M={M} H={H}: {us:.2f} us, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM)")
+
+    del srcs, gys
+    (pg, qg, ag, bg), (pu, qu, au, bu), (pd, qd, ad, bd) = projs
+    source = src.clone().requires_grad_()
+
+    def step():
+        for t in (source, ag, bg, au, bu, ad, bd):
+            t.grad = None
+        normalized = _FrozenRMSNormFunction.apply(source, w, eps, 0.0)
+        y = _ResidualRecipeGatedNF4LoRA.apply(source, normalized, pg, ag, bg, pu, au, bu, pd, ad, bd, qg, qu, qd,
+                                              s, s, s, w, eps, 0.0)
+        y.backward(dy)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    out["recipe_step_ms"] = round(ms, 4)
+    out["recipe_tokens_s"] = round(M / (ms * 1e-3), 1)
+    log(f"RMSNorm-replay recipe step (norm fwd + gated MLP fwd/bwd + norm bwd): {ms:.3f} ms, {M / (ms * 1e-3):.0f} tok/s")
+    return out
+
+
 TRAFFIC_FILE = ROOT / "profiles" / "gateup_fwd_cfg4_hbm_traffic.txt"
 
 
@@ -243,6 +309,7 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=8192, help="M (default: cfg4's 8 x 1024)")
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-norm", action="store_true", help="skip the RMSNorm / norm-replay recipe measurement")
     ap.add_argument("--profile-kernel", choices=("gateup", "copy"),
                     help="only launch one kernel (for rocprofv3 --pmc passes) and exit")
     ap.add_argument("--reps", type=int, default=3, help="launches for --profile-kernel")
@@ -303,6 +370,8 @@ def main() -> int:
                      "avg_launch_ms": round(k_ms, 4), "launches": len(pairs),
                      "flop_per_launch": k_flop},
     }
+    if not args.no_norm:
+        result["rmsnorm"] = rmsnorm_bench(dev, projs, dy, s, M, H, args.steps)
     if not args.no_gemv:
         sweep = gemv_sweep(dev)
         result["gemv"] = sweep

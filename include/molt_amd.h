@@ -223,6 +223,29 @@ int molt_silu_mul_forward(const void* gate, const void* up, void* out, int64_t n
 int molt_silu_mul_backward(const void* grad, const void* gate, const void* up, void* dgate,
                            void* dup, int64_t n, int32_t dtype, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Frozen RMSNorm (forward, norm replay, backward)                           */
+/* ------------------------------------------------------------------------ */
+
+/* Row-wise over H: inv = rsqrt(sum(fp32(x)^2) * (1/H) + eps),
+ * out = bf16(fp32(fp32(x) * inv) * (fp32(w) + offset)). x is bf16 or fp32
+ * (x_dtype) with row stride ldx, weight bf16 or fp32 [H], out bf16 with row
+ * stride ldo. inv_rms (fp32 [M], may be NULL) receives inv of every row.
+ * Replaces _FrozenRMSNormFunction.forward (kernels/frozen_rmsnorm.py:10-23) and
+ * _RMSNormReplayRecipe.materialize (methods/gated_replay.py:22-30). */
+int molt_rmsnorm_forward(const void* x, int32_t x_dtype, int64_t ldx, int64_t M, int64_t H,
+                         const void* weight, int32_t w_dtype, float eps, float offset,
+                         uint16_t* out, int64_t ldo, float* inv_rms, void* stream);
+
+/* Frozen-weight backward: n = fp32(x) * inv, g = fp32(dy) * (fp32(w) + offset),
+ * dx = inv * (g - n * sum(g * n) * (1/H)), stored in x's dtype with row stride
+ * lddx; inv is recomputed from x. dy is bf16.
+ * Replaces _FrozenRMSNormFunction.backward (kernels/frozen_rmsnorm.py:25-37). */
+int molt_rmsnorm_backward(const uint16_t* dy, int64_t lddy, const void* x, int32_t x_dtype,
+                          int64_t ldx, int64_t M, int64_t H, const void* weight,
+                          int32_t w_dtype, float eps, float offset, void* dx, int64_t lddx,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

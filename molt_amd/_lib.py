@@ -67,6 +67,9 @@ SIGNATURES: dict[str, tuple] = {
     "molt_nf4_gemv": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _f32, _p, _i64, _p, _sz, _p]),
     "molt_silu_mul_forward": (C.c_int, [_p, _p, _p, _i64, _i32, _i32, _p]),
     "molt_silu_mul_backward": (C.c_int, [_p, _p, _p, _p, _p, _i64, _i32, _p]),
+    "molt_rmsnorm_forward": (C.c_int, [_p, _i32, _i64, _i64, _i64, _p, _i32, _f32, _f32, _p, _i64, _p, _p]),
+    "molt_rmsnorm_backward": (C.c_int, [_p, _i64, _p, _i32, _i64, _i64, _i64, _p, _i32, _f32, _f32, _p, _i64,
+                                        _p]),
 }
 
 _lock = threading.Lock()

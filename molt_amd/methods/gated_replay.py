@@ -18,6 +18,7 @@ contraction over 2I.
 """
 from __future__ import annotations
 
+from dataclasses import dataclass
 from types import MethodType
 from typing import Any
 
@@ -153,6 +154,67 @@ def asymmetric_gated_nf4_lora(
 # --------------------------------------------------------------------------
 # Fully fused gate/up/down node
 # --------------------------------------------------------------------------
+def _fused_forward(x, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_packed, down_a, down_b,
+                   gate_qs, up_qs, down_qs, gate_scaling, up_scaling, down_scaling):
+    """Forward of the fused gated MLP on ``x`` [..., H]: gate/up as one
+    dual-accumulator GEMM that also emits h, then the down projection.
+    Returns (y [tokens, H], gate, up, h, T_gu, T_d, (H, I, r))."""
+    if x.device.type != "cuda" or x.dtype != torch.bfloat16:
+        raise CapabilityError("fused gated NF4-LoRA MLP requires CUDA BF16 tensors")
+    for t in (gate_a, gate_b, up_a, up_b, down_a, down_b):
+        if t.dtype != torch.float32:
+            raise CapabilityError("fused gated NF4-LoRA MLP requires FP32 adapter masters")
+    i_dim, h_dim = _rows_cols(gate_qs.shape)
+    if _rows_cols(up_qs.shape) != (i_dim, h_dim) or _rows_cols(down_qs.shape) != (h_dim, i_dim):
+        raise ValueError("gate/up must be [I, H] and down [H, I]")
+    if nibble_order(gate_qs) != nibble_order(up_qs) or int(gate_qs.blocksize) != 64 \
+            or int(up_qs.blocksize) != 64 or int(down_qs.blocksize) != 64:
+        raise CapabilityError("fused gated MLP requires NF4 block size 64 with a shared packing")
+    r = gate_a.shape[0]
+    if up_a.shape[0] != r:
+        raise ValueError("gate and up adapters must share a rank")
+    flat = x.reshape(-1, h_dim)
+    t_gu = ops.lora_project(flat, None, 0, 1.0, torch.cat([gate_a, up_a], 0), 0)
+    gate, up, gated = ops.nf4_gateup_forward(
+        flat, gate_packed.reshape(-1), resolved_nf4_scales(gate_qs), up_packed.reshape(-1),
+        resolved_nf4_scales(up_qs), gate_qs.code, i_dim, h_dim, nibble_order(gate_qs), t_gu, gate_b, up_b,
+        float(gate_scaling), float(up_scaling))
+    t_d = ops.lora_project(gated, None, 0, 1.0, down_a, 0)
+    y = ops.nf4_lora_forward(gated, down_packed.reshape(-1), resolved_nf4_scales(down_qs), down_qs.code,
+                             h_dim, i_dim, nibble_order(down_qs), 64, t_d, down_b, float(down_scaling))
+    return y, gate, up, gated, t_gu, t_d, (h_dim, i_dim, r)
+
+
+def _fused_backward(grad_output, flat, gate, up, gated, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed,
+                    up_a, up_b, down_packed, down_a, down_b, qs, scaling, dims):
+    """Backward of the fused gated MLP. ``flat`` is the projections' input
+    [tokens, H]; ``gated`` is h when the forward kept it, else None (replayed
+    from gate and up). Returns (dX [tokens, H], dA_g, dB_g, dA_u, dB_u, dA_d, dB_d)."""
+    gate_qs, up_qs, down_qs = qs
+    s_g, s_u, s_d = scaling
+    h_dim, i_dim, r = dims
+    dy = grad_output.reshape(-1, h_dim).to(torch.bfloat16)
+    u_d = ops.lora_project(dy, None, 2, s_d, down_b, 1)
+    dg, du = ops.nf4_swiglu_backward(dy, down_packed.reshape(-1), resolved_nf4_scales(down_qs), down_qs.code,
+                                     h_dim, i_dim, nibble_order(down_qs), u_d, down_a, gate, up)
+    u_g = ops.lora_project(dg, None, 2, s_g, gate_b, 1)
+    u_u = ops.lora_project(du, None, 2, s_u, up_b, 1)
+    dx = ops.nf4_lora_backward_input_pair(
+        dg, du, gate_packed.reshape(-1), resolved_nf4_scales(gate_qs), up_packed.reshape(-1),
+        resolved_nf4_scales(up_qs), gate_qs.code, i_dim, h_dim, nibble_order(gate_qs), u_g, u_u, gate_a,
+        up_a)
+    if gated is not None:   # h kept from the forward: bitwise the replayed value
+        d_down_a = ops.lora_grad(gated, None, 0, u_d, 1.0, 1)
+    else:
+        d_down_a = ops.lora_grad(gate, up, 1, u_d, 1.0, 1)
+    d_down_b = ops.lora_grad(dy, None, 0, t_d, s_d, 0)
+    # dA_gate and dA_up both contract X: one pass over X with [U_g | U_u]
+    d_gu_a = ops.lora_grad(flat, None, 0, torch.cat([u_g, u_u], 1), 1.0, 1)
+    d_gate_b = ops.lora_grad(dg, None, 0, t_gu[:, :r], s_g, 0)
+    d_up_b = ops.lora_grad(du, None, 0, t_gu[:, r:], s_u, 0)
+    return dx, d_gu_a[:r], d_gate_b, d_gu_a[r:], d_up_b, d_down_a, d_down_b
+
+
 class _FusedGatedNF4LoRA(torch.autograd.Function):
     """Gated NF4-LoRA MLP with gate/up as one dual-accumulator GEMM and the
     SwiGLU backward fused into the down projection's input gradient."""
@@ -160,70 +222,29 @@ class _FusedGatedNF4LoRA(torch.autograd.Function):
     @staticmethod
     def forward(ctx: Any, x, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_packed, down_a,
                 down_b, gate_qs, up_qs, down_qs, gate_scaling, up_scaling, down_scaling, save_gated):
-        if x.device.type != "cuda" or x.dtype != torch.bfloat16:
-            raise CapabilityError("fused gated NF4-LoRA MLP requires CUDA BF16 tensors")
-        for t in (gate_a, gate_b, up_a, up_b, down_a, down_b):
-            if t.dtype != torch.float32:
-                raise CapabilityError("fused gated NF4-LoRA MLP requires FP32 adapter masters")
-        i_dim, h_dim = _rows_cols(gate_qs.shape)
-        if _rows_cols(up_qs.shape) != (i_dim, h_dim) or _rows_cols(down_qs.shape) != (h_dim, i_dim):
-            raise ValueError("gate/up must be [I, H] and down [H, I]")
-        if nibble_order(gate_qs) != nibble_order(up_qs) or int(gate_qs.blocksize) != 64 \
-                or int(up_qs.blocksize) != 64 or int(down_qs.blocksize) != 64:
-            raise CapabilityError("fused gated MLP requires NF4 block size 64 with a shared packing")
-        r = gate_a.shape[0]
-        if up_a.shape[0] != r:
-            raise ValueError("gate and up adapters must share a rank")
-        flat = x.reshape(-1, h_dim)
-        t_gu = ops.lora_project(flat, None, 0, 1.0, torch.cat([gate_a, up_a], 0), 0)
-        code = gate_qs.code
-        gate, up, gated = ops.nf4_gateup_forward(
-            flat, gate_packed.reshape(-1), resolved_nf4_scales(gate_qs), up_packed.reshape(-1),
-            resolved_nf4_scales(up_qs), code, i_dim, h_dim, nibble_order(gate_qs), t_gu, gate_b, up_b,
-            float(gate_scaling), float(up_scaling))
-        t_d = ops.lora_project(gated, None, 0, 1.0, down_a, 0)
-        y = ops.nf4_lora_forward(gated, down_packed.reshape(-1), resolved_nf4_scales(down_qs), down_qs.code,
-                                 h_dim, i_dim, nibble_order(down_qs), 64, t_d, down_b, float(down_scaling))
+        y, gate, up, gated, t_gu, t_d, dims = _fused_forward(
+            x, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_packed, down_a, down_b, gate_qs,
+            up_qs, down_qs, gate_scaling, up_scaling, down_scaling)
         if not save_gated:
             gated = None  # replayed in backward from (gate, up)
         ctx.qs = (gate_qs, up_qs, down_qs)
         ctx.scaling = (float(gate_scaling), float(up_scaling), float(down_scaling))
-        ctx.dims = (h_dim, i_dim, r)
+        ctx.dims = dims
         ctx.input_shape = x.shape
-        ctx.save_for_backward(flat, gate, up, gated, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed, up_a,
-                              up_b, down_packed, down_a, down_b)
-        return y.reshape(*x.shape[:-1], h_dim)
+        ctx.save_for_backward(x.reshape(-1, dims[0]), gate, up, gated, t_gu, t_d, gate_packed, gate_a, gate_b,
+                              up_packed, up_a, up_b, down_packed, down_a, down_b)
+        return y.reshape(*x.shape[:-1], dims[0])
 
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx: Any, grad_output: torch.Tensor):
         (flat, gate, up, gated, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_packed,
          down_a, down_b) = ctx.saved_tensors
-        gate_qs, up_qs, down_qs = ctx.qs
-        s_g, s_u, s_d = ctx.scaling
-        h_dim, i_dim, r = ctx.dims
-        dy = grad_output.reshape(-1, h_dim).to(torch.bfloat16)
-        u_d = ops.lora_project(dy, None, 2, s_d, down_b, 1)
-        dg, du = ops.nf4_swiglu_backward(dy, down_packed.reshape(-1), resolved_nf4_scales(down_qs), down_qs.code,
-                                         h_dim, i_dim, nibble_order(down_qs), u_d, down_a, gate, up)
-        u_g = ops.lora_project(dg, None, 2, s_g, gate_b, 1)
-        u_u = ops.lora_project(du, None, 2, s_u, up_b, 1)
-        dx = ops.nf4_lora_backward_input_pair(
-            dg, du, gate_packed.reshape(-1), resolved_nf4_scales(gate_qs), up_packed.reshape(-1),
-            resolved_nf4_scales(up_qs), gate_qs.code, i_dim, h_dim, nibble_order(gate_qs), u_g, u_u, gate_a,
-            up_a)
-        if gated is not None:   # h kept from the forward: bitwise the replayed value
-            d_down_a = ops.lora_grad(gated, None, 0, u_d, 1.0, 1)
-        else:
-            d_down_a = ops.lora_grad(gate, up, 1, u_d, 1.0, 1)
-        d_down_b = ops.lora_grad(dy, None, 0, t_d, s_d, 0)
-        # dA_gate and dA_up both contract X: one pass over X with [U_g | U_u]
-        d_gu_a = ops.lora_grad(flat, None, 0, torch.cat([u_g, u_u], 1), 1.0, 1)
-        d_gate_a, d_up_a = d_gu_a[:r], d_gu_a[r:]
-        d_gate_b = ops.lora_grad(dg, None, 0, t_gu[:, :r], s_g, 0)
-        d_up_b = ops.lora_grad(du, None, 0, t_gu[:, r:], s_u, 0)
-        return (dx.reshape(ctx.input_shape), None, d_gate_a, d_gate_b, None, d_up_a, d_up_b, None, d_down_a,
-                d_down_b, None, None, None, None, None, None, None)
+        dx, dag, dbg, dau, dbu, dad, dbd = _fused_backward(
+            grad_output, flat, gate, up, gated, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed, up_a, up_b,
+            down_packed, down_a, down_b, ctx.qs, ctx.scaling, ctx.dims)
+        return (dx.reshape(ctx.input_shape), None, dag, dbg, None, dau, dbu, None, dad, dbd,
+                None, None, None, None, None, None, None)
 
 
 def fused_gated_nf4_lora_mlp(
@@ -244,6 +265,111 @@ def fused_gated_nf4_lora_mlp(
         x, gate_packed_weight, gate_lora_a, gate_lora_b, up_packed_weight, up_lora_a, up_lora_b,
         down_packed_weight, down_lora_a, down_lora_b, gate_quant_state, up_quant_state, down_quant_state,
         gate_scaling, up_scaling, down_scaling, bool(save_gated))
+
+
+# --------------------------------------------------------------------------
+# RMSNorm replay (methods/gated_replay.py:13-208)
+# --------------------------------------------------------------------------
+@dataclass
+class _RMSNormReplayRecipe:
+    """What recomputes the normalised MLP input from the residual stream
+    (methods/gated_replay.py:13-30); ``materialize`` runs the HIP RMSNorm
+    forward, bitwise the output of FrozenRMSNormBF16 on the same source."""
+    source: torch.Tensor
+    weight: torch.Tensor
+    eps: float
+    weight_offset: float
+    packed_count: int = 0
+    target: torch.Tensor | None = None
+
+    def materialize(self) -> torch.Tensor:
+        return ops.rmsnorm_forward(self.source, self.weight, float(self.eps), float(self.weight_offset))
+
+
+def _replayable_norm_forward(module: torch.nn.Module, hidden: torch.Tensor, *args: Any,
+                             **kwargs: Any) -> torch.Tensor:
+    """Norm forward that leaves a replay recipe on its target MLP when the
+    output is bf16 under grad mode (methods/gated_replay.py:33-47)."""
+    result = module._molt_original_forward(hidden, *args, **kwargs)
+    target_mlp = module._molt_target_mlp
+    if torch.is_grad_enabled() and result.dtype == torch.bfloat16:
+        target_mlp._molt_norm_replay_recipe = _RMSNormReplayRecipe(
+            source=hidden, weight=module.weight, eps=float(module.variance_epsilon),
+            weight_offset=float(module.weight_offset), target=result)
+    else:
+        target_mlp._molt_norm_replay_recipe = None
+    return result
+
+
+class _ResidualRecipeGatedNF4LoRA(torch.autograd.Function):
+    """Gated NF4+LoRA MLP that retains the residual instead of the normalised
+    input (methods/gated_replay.py:50-208).
+
+    Forward is the fused gated MLP on ``normalized``. It saves the residual
+    ``source``, gate and up (h is replayed from them, as the reference does),
+    and the two rank-r projections. Backward re-materialises the normalised
+    input from the source with the RMSNorm kernel and runs the fused backward;
+    it returns the gradient of ``normalized`` (the norm's own node carries it
+    to the residual) and the six adapter gradients."""
+
+    @staticmethod
+    def forward(ctx: Any, source, normalized, gate_packed_weight, gate_lora_a, gate_lora_b, up_packed_weight,
+                up_lora_a, up_lora_b, down_packed_weight, down_lora_a, down_lora_b, gate_quant_state,
+                up_quant_state, down_quant_state, gate_scaling, up_scaling, down_scaling, norm_weight,
+                norm_eps, norm_weight_offset):
+        if source.shape != normalized.shape:
+            raise ValueError("the residual source and the normalised input must have the same shape")
+        y, gate, up, _, t_gu, t_d, dims = _fused_forward(
+            normalized, gate_packed_weight, gate_lora_a, gate_lora_b, up_packed_weight, up_lora_a, up_lora_b,
+            down_packed_weight, down_lora_a, down_lora_b, gate_quant_state, up_quant_state, down_quant_state,
+            gate_scaling, up_scaling, down_scaling)
+        ctx.qs = (gate_quant_state, up_quant_state, down_quant_state)
+        ctx.scaling = (float(gate_scaling), float(up_scaling), float(down_scaling))
+        ctx.dims = dims
+        ctx.input_shape = normalized.shape
+        ctx.norm_eps = float(norm_eps)
+        ctx.norm_weight_offset = float(norm_weight_offset)
+        ctx.save_for_backward(source, gate, up, t_gu, t_d, gate_packed_weight, gate_lora_a, gate_lora_b,
+                              up_packed_weight, up_lora_a, up_lora_b, down_packed_weight, down_lora_a,
+                              down_lora_b, norm_weight)
+        return y.reshape(*normalized.shape[:-1], dims[0])
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx: Any, grad_output: torch.Tensor):
+        (source, gate, up, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_packed, down_a,
+         down_b, norm_weight) = ctx.saved_tensors
+        normalized = _RMSNormReplayRecipe(source, norm_weight, ctx.norm_eps, ctx.norm_weight_offset).materialize()
+        dx, dag, dbg, dau, dbu, dad, dbd = _fused_backward(
+            grad_output, normalized.reshape(-1, ctx.dims[0]), gate, up, None, t_gu, t_d, gate_packed, gate_a,
+            gate_b, up_packed, up_a, up_b, down_packed, down_a, down_b, ctx.qs, ctx.scaling, ctx.dims)
+        return (None, dx.reshape(ctx.input_shape), None, dag, dbg, None, dau, dbu, None, dad, dbd,
+                None, None, None, None, None, None, None, None, None)
+
+
+def enable_rmsnorm_replay(model: torch.nn.Module) -> int:
+    """Wire each decoder layer's ``post_attention_layernorm`` to its ``mlp``
+    with :func:`_replayable_norm_forward`, so an MLP patched by
+    :func:`enable_fused_gated_nf4_lora` keeps the residual instead of the
+    normalised input (``_ResidualRecipeGatedNF4LoRA``). The norm must carry
+    ``weight``, ``variance_epsilon`` and ``weight_offset`` (FrozenRMSNormBF16).
+    The reference defines the recipe but wires no caller; this is that wiring."""
+    wired = 0
+    for layer in model.modules():
+        norm = getattr(layer, "post_attention_layernorm", None)
+        mlp = getattr(layer, "mlp", None)
+        if norm is None or mlp is None or hasattr(norm, "_molt_target_mlp"):
+            continue
+        if not all(hasattr(norm, a) for a in ("weight", "variance_epsilon", "weight_offset")):
+            continue
+        norm._molt_original_forward = norm.forward
+        norm._molt_target_mlp = mlp
+        norm.forward = MethodType(_replayable_norm_forward, norm)
+        mlp._molt_norm_replay_recipe = None
+        wired += 1
+    if not wired:
+        raise CapabilityError("No frozen RMSNorm -> MLP pairs were found (run enable_frozen_rmsnorm_bf16 first)")
+    return wired
 
 
 # --------------------------------------------------------------------------
@@ -391,6 +517,12 @@ def _fused_mlp_forward(module: torch.nn.Module, x: torch.Tensor, *args: Any, **k
     if any(p is None for p in parts):
         return module._molt_original_forward(x, *args, **kwargs)
     g, u, d = parts
+    recipe = getattr(module, "_molt_norm_replay_recipe", None)
+    module._molt_norm_replay_recipe = None
+    if recipe is not None and recipe.target is x and recipe.source.shape == x.shape:
+        return _ResidualRecipeGatedNF4LoRA.apply(
+            recipe.source, x, g[0], g[1], g[2], u[0], u[1], u[2], d[0], d[1], d[2], g[3], u[3], d[3], g[4], u[4],
+            d[4], recipe.weight, recipe.eps, recipe.weight_offset)
     return fused_gated_nf4_lora_mlp(x, g[0], g[1], g[2], u[0], u[1], u[2], d[0], d[1], d[2], g[3], u[3], d[3],
                                     g[4], u[4], d[4])
 

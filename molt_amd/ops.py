@@ -549,3 +549,64 @@ def silu_mul_backward(grad: Tensor, gate: Tensor, up: Tensor) -> tuple[Tensor, T
 @silu_mul_backward.register_fake
 def _(grad, gate, up):
     return torch.empty_like(gate), torch.empty_like(up)
+
+
+# --------------------------------------------------------------------------
+# Frozen RMSNorm (kernels/frozen_rmsnorm.py:9-37, methods/gated_replay.py:22-30)
+# --------------------------------------------------------------------------
+def _rn_dtype(t: Tensor, what: str) -> int:
+    if t.dtype == torch.bfloat16:
+        return _lib.DTYPE_BF16
+    if t.dtype == torch.float32:
+        return _lib.DTYPE_F32
+    raise CapabilityError(f"frozen RMSNorm supports bf16 and fp32 {what} (got {t.dtype})")
+
+
+def _rn_check(x: Tensor, weight: Tensor) -> int:
+    if x.dim() == 0 or weight.dim() != 1 or weight.shape[0] != x.shape[-1]:
+        raise ValueError(f"frozen RMSNorm: weight {tuple(weight.shape)} does not match hidden {tuple(x.shape)}")
+    return int(x.shape[-1])
+
+
+@torch.library.custom_op(f"{NS}::rmsnorm_forward", mutates_args=())
+def rmsnorm_forward(x: Tensor, weight: Tensor, eps: float, offset: float) -> Tensor:
+    """bf16(fp32(x) * rsqrt(mean(fp32(x)^2) + eps) * (fp32(weight) + offset))
+    over the last dimension (kernels/frozen_rmsnorm.py:16-23)."""
+    dev = _require_gpu(x, weight, what="frozen RMSNorm")
+    h = _rn_check(x, weight)
+    xc, w = x.contiguous(), weight.detach().contiguous()
+    out = torch.empty(x.shape, dtype=torch.bfloat16, device=dev)
+    if out.numel() == 0:
+        return out
+    rows = xc.numel() // h
+    _call("molt_rmsnorm_forward", xc.data_ptr(), _rn_dtype(xc, "hidden"), h, rows, h, w.data_ptr(),
+          _rn_dtype(w, "weight"), float(eps), float(offset), out.data_ptr(), h, None, _stream(dev))
+    return out
+
+
+@rmsnorm_forward.register_fake
+def _(x, weight, eps, offset):
+    return torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+
+
+@torch.library.custom_op(f"{NS}::rmsnorm_backward", mutates_args=())
+def rmsnorm_backward(grad: Tensor, x: Tensor, weight: Tensor, eps: float, offset: float) -> Tensor:
+    """Input gradient of the frozen RMSNorm in x's dtype (kernels/frozen_rmsnorm.py:25-37)."""
+    dev = _require_gpu(grad, x, weight, what="frozen RMSNorm")
+    h = _rn_check(x, weight)
+    if grad.shape != x.shape:
+        raise ValueError(f"frozen RMSNorm: grad {tuple(grad.shape)} does not match hidden {tuple(x.shape)}")
+    dy = grad.to(torch.bfloat16).contiguous()
+    xc, w = x.contiguous(), weight.detach().contiguous()
+    dx = torch.empty_like(xc)
+    if dx.numel() == 0:
+        return dx
+    rows = xc.numel() // h
+    _call("molt_rmsnorm_backward", dy.data_ptr(), h, xc.data_ptr(), _rn_dtype(xc, "hidden"), h, rows, h,
+          w.data_ptr(), _rn_dtype(w, "weight"), float(eps), float(offset), dx.data_ptr(), h, _stream(dev))
+    return dx
+
+
+@rmsnorm_backward.register_fake
+def _(grad, x, weight, eps, offset):
+    return torch.empty_like(x)

@@ -34,6 +34,12 @@ Pinning (what independently checks each function; see ``tests/test_oracle.py``):
   the backward formulas are pinned against torch autograd of the forward
   expression in fp64, and SwiGLU against ``F.silu(g) * u``
   (``tests/kernels/test_gated_activation.py:10-26``).
+* ``rmsnorm_forward`` / ``rmsnorm_backward`` - fp64 algebra. The forward is
+  pinned by closed forms (a constant row maps to ``sign * (w + offset)`` at
+  eps = 0, scale invariance, unit RMS of the normalised row); the backward by
+  central differences of the forward in fp64 and by its two invariants
+  (zero gradient along x at eps = 0, and the closed form of the reference's
+  own test, ``tests/kernels/test_frozen_rmsnorm.py:6-53``).
 """
 from __future__ import annotations
 
@@ -393,6 +399,28 @@ def gated_mlp_backward(x, wg, wu, wd, ag, bg, au, bu, ad, bd, s, dy, saved, bf16
     dxg, dag, dbg = lora_linear_backward(x, wg, ag, bg, s, dg)
     dxu, dau, dbu = lora_linear_backward(x, wu, au, bu, s, du)
     return dxg + dxu, (dag, dbg, dau, dbu, dad, dbd)
+
+
+# --------------------------------------------------------------------------
+# Frozen RMSNorm (kernels/frozen_rmsnorm.py:9-37; methods/gated_replay.py:13-30)
+# --------------------------------------------------------------------------
+def rmsnorm_forward(x, w, eps, offset):
+    """``x * rsqrt(mean(x^2) + eps) * (w + offset)`` over the last axis
+    (kernels/frozen_rmsnorm.py:16-23; methods/gated_replay.py:22-30). fp64,
+    before the bf16 rounding of the output."""
+    x, w = _f64(x), _f64(w)
+    inv = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    return x * inv * (w + offset)
+
+
+def rmsnorm_backward(x, w, eps, offset, dy):
+    """Input gradient of the frozen-weight RMSNorm (kernels/frozen_rmsnorm.py:25-37):
+    ``inv * (g - n * mean(g * n))``, ``n = x * inv``, ``g = dy * (w + offset)``. fp64."""
+    x, w, dy = _f64(x), _f64(w), _f64(dy)
+    inv = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    n = x * inv
+    g = dy * (w + offset)
+    return inv * (g - n * np.mean(g * n, axis=-1, keepdims=True))
 
 
 # --------------------------------------------------------------------------

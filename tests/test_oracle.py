@@ -250,3 +250,63 @@ def test_rel_fro_detects_a_dropped_lora_term():
     a, b = rng.normal(size=(8, 64)) / 8, rng.normal(size=(48, 8)) * 0.1
     full = O.lora_linear_forward(x, w, a, b, 2.0)
     assert O.rel_fro(x @ w.T, full) > 5e-3
+
+
+# --------------------------------------------------------------- RMSNorm
+def test_rmsnorm_forward_closed_forms():
+    rng = np.random.default_rng(5)
+    w = rng.standard_normal(48)
+    # a constant row normalises to sign(c) * (w + offset) at eps = 0
+    for c in (3.25, -0.5):
+        x = np.full((2, 48), c)
+        for off in (0.0, 1.0):
+            np.testing.assert_allclose(O.rmsnorm_forward(x, w, 0.0, off), np.broadcast_to(np.sign(c) * (w + off), x.shape),
+                                       rtol=1e-14, atol=1e-14)
+    x = rng.standard_normal((5, 48))
+    # scale invariance at eps = 0, and unit RMS of the normalised row
+    np.testing.assert_allclose(O.rmsnorm_forward(7.5 * x, w, 0.0, 0.0), O.rmsnorm_forward(x, w, 0.0, 0.0),
+                               rtol=1e-13, atol=1e-13)
+    n = O.rmsnorm_forward(x, np.zeros(48), 0.0, 1.0)
+    np.testing.assert_allclose(np.mean(n * n, axis=-1), 1.0, rtol=1e-13)
+    # eps enters under the root: a zero row stays zero, a tiny row is damped
+    assert np.all(O.rmsnorm_forward(np.zeros((1, 48)), w, 1e-6, 0.0) == 0.0)
+    tiny = np.full((1, 48), 1e-4)
+    np.testing.assert_allclose(O.rmsnorm_forward(tiny, np.ones(48), 1e-6, 0.0),
+                               1e-4 / math.sqrt(1e-8 + 1e-6), rtol=1e-12)
+
+
+def test_rmsnorm_backward_matches_central_differences():
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((3, 16))
+    w = rng.standard_normal(16)
+    dy = rng.standard_normal((3, 16))
+    for eps, off in ((1e-6, 0.0), (0.3, 1.0)):
+        got = O.rmsnorm_backward(x, w, eps, off, dy)
+        num = np.zeros_like(x)
+        h = 1e-6
+        for i in range(x.shape[0]):
+            for j in range(x.shape[1]):
+                xp, xm = x.copy(), x.copy()
+                xp[i, j] += h
+                xm[i, j] -= h
+                num[i, j] = np.sum(dy * (O.rmsnorm_forward(xp, w, eps, off) - O.rmsnorm_forward(xm, w, eps, off))) / (2 * h)
+        np.testing.assert_allclose(got, num, rtol=1e-6, atol=1e-8)
+    # at eps = 0 the map is scale invariant, so the gradient is orthogonal to x
+    g0 = O.rmsnorm_backward(x, w, 0.0, 0.0, dy)
+    np.testing.assert_allclose(np.sum(g0 * x, axis=-1), 0.0, atol=1e-12)
+
+
+def test_rmsnorm_oracle_matches_reference_test_algebra():
+    """The closed form of the reference's own test (tests/kernels/test_frozen_rmsnorm.py:6-53),
+    evaluated by torch autograd in fp64."""
+    torch.manual_seed(23)
+    w = torch.randn(64, dtype=torch.float64)
+    x = torch.randn(8, 64, dtype=torch.float64, requires_grad=True)
+    dy = torch.randn(8, 64, dtype=torch.float64)
+    for off in (0.0, 1.0):
+        ref = x * torch.rsqrt(x.square().mean(-1, keepdim=True) + 1e-6) * (w + off)
+        (gx,) = torch.autograd.grad(ref, x, dy)
+        np.testing.assert_allclose(O.rmsnorm_forward(x.detach().numpy(), w.numpy(), 1e-6, off),
+                                   ref.detach().numpy(), rtol=1e-13, atol=1e-13)
+        np.testing.assert_allclose(O.rmsnorm_backward(x.detach().numpy(), w.numpy(), 1e-6, off, dy.numpy()),
+                                   gx.numpy(), rtol=1e-12, atol=1e-12)
