@@ -6,7 +6,8 @@ M=8192 tokens), including every adapter gradient. Inputs are synthetic, seeded
 and already resident in HBM. Also reported: the roofline of the dominant
 kernel (the fused gate/up NF4 GEMM) from HIP events recorded around its
 launches on its own stream during the timed steps, the frozen RMSNorm kernels
-and the RMSNorm-replay recipe step, the skinny-M NF4 GEMV sweep (cfg5, HBM
+and the RMSNorm-replay recipe step, every NF4-LoRA projection shape of the
+cfg3 decoder (attention and MLP, forward + backward), the skinny-M NF4 GEMV sweep (cfg5, HBM
 GB/s), and the CPU baseline (the oracle's restatement of MOLT's
 eager CPU path, cfg1, numpy fp32 on the host cores).
 
@@ -202,6 +203,51 @@ def rmsnorm_bench(dev, projs, dy, s, M, H, steps: int, reps: int = 5):
     return out
 
 
+def projection_sweep(dev, reps: int = 10):
+    """Every NF4-LoRA projection of the cfg3 decoder (Qwen2.5-1.5B shapes:
+    H=1536, 12 q heads / 2 kv heads x 128, I=8960, r=16, M=4096 tokens)
+    through scheduled_nf4_lora, forward + backward (dX, dA, dB), with the
+    algorithmic FLOPs 4*M*N*K + 6*M*r*(N+K) per projection."""
+    import torch
+    import molt_amd
+    from molt_amd.methods import scheduled_nf4_lora
+
+    M, r, s = 4096, 16, 2.0
+    g = torch.Generator(device="cpu").manual_seed(9)
+    out = []
+    for name, n, k in (("q_proj/o_proj", 1536, 1536), ("k_proj/v_proj", 256, 1536), ("gate_proj/up_proj", 8960, 1536),
+                       ("down_proj", 1536, 8960)):
+        w = (torch.randn(n, k, generator=g) * 0.02).to(dev)
+        packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True)
+        del w
+        a = ((torch.rand(r, k, generator=g) * 2 - 1) / math.sqrt(k)).to(dev).requires_grad_()
+        b = (torch.randn(n, r, generator=g) * 0.01).to(dev).requires_grad_()
+        x = torch.randn(M, k, generator=g).to(dev, torch.bfloat16).requires_grad_()
+        dy = torch.randn(M, n, generator=g).to(dev, torch.bfloat16)
+
+        def run():
+            for t in (x, a, b):
+                t.grad = None
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                y = scheduled_nf4_lora(x, packed, a, b, qs, s)
+            y.backward(dy)
+
+        for _ in range(3):
+            run()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            run()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / reps
+        flop = 4 * M * n * k + 6 * M * r * (n + k)
+        tf = flop / (ms * 1e-3) / 1e12
+        out.append({"proj": name, "N": n, "K": k, "M": M, "r": r, "ms_fwd_bwd": round(ms, 4), "TFLOP_s": round(tf, 1),
+                    "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)})
+        log(f"cfg3 {name} N={n} K={k} M={M}: fwd+bwd {ms:.3f} ms, {tf:.0f} TFLOP/s ({100 * tf / PEAK_BF16_TFLOPS:.1f}%)")
+    return out
+
+
 TRAFFIC_FILE = ROOT / "profiles" / "gateup_fwd_cfg4_hbm_traffic.txt"
 
 
@@ -310,6 +356,7 @@ def main() -> int:
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-norm", action="store_true", help="skip the RMSNorm / norm-replay recipe measurement")
+    ap.add_argument("--no-proj", action="store_true", help="skip the cfg3 projection sweep")
     ap.add_argument("--profile-kernel", choices=("gateup", "copy"),
                     help="only launch one kernel (for rocprofv3 --pmc passes) and exit")
     ap.add_argument("--reps", type=int, default=3, help="launches for --profile-kernel")
@@ -372,6 +419,8 @@ def main() -> int:
     }
     if not args.no_norm:
         result["rmsnorm"] = rmsnorm_bench(dev, projs, dy, s, M, H, args.steps)
+    if not args.no_proj:
+        result["cfg3_projections"] = projection_sweep(dev)
     if not args.no_gemv:
         sweep = gemv_sweep(dev)
         result["gemv"] = sweep

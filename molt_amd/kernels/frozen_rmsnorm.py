@@ -52,13 +52,13 @@ class _FrozenRMSNormFunction(torch.autograd.Function):
         ctx.save_for_backward(hidden, weight)
         ctx.eps = float(eps)
         ctx.weight_offset = float(weight_offset)
-        return ops.rmsnorm_forward(hidden, weight, float(eps), float(weight_offset))
+        return ops.direct.rmsnorm_forward(hidden, weight, float(eps), float(weight_offset))
 
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx: Any, grad_output: torch.Tensor):
         hidden, weight = ctx.saved_tensors
-        grad_hidden = ops.rmsnorm_backward(grad_output, hidden, weight, ctx.eps, ctx.weight_offset)
+        grad_hidden = ops.direct.rmsnorm_backward(grad_output, hidden, weight, ctx.eps, ctx.weight_offset)
         return grad_hidden, None, None, None
 
 

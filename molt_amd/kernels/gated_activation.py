@@ -22,7 +22,7 @@ class _FusedSiLUMultiply(torch.autograd.Function):
         if gate.device.type != "cuda":
             raise CapabilityError("fused SiLU multiply requires CUDA tensors on a ROCm GPU")
         g, u = gate.contiguous(), up.contiguous()
-        out = ops.silu_mul_forward(g, u, False)
+        out = ops.direct.silu_mul_forward(g, u, False)
         ctx.original_shape = gate.shape
         ctx.save_for_backward(g, u)
         return out
@@ -31,7 +31,7 @@ class _FusedSiLUMultiply(torch.autograd.Function):
     @torch.autograd.function.once_differentiable
     def backward(ctx: Any, grad_output: torch.Tensor):
         gate, up = ctx.saved_tensors
-        dg, du = ops.silu_mul_backward(grad_output.contiguous().to(gate.dtype), gate, up)
+        dg, du = ops.direct.silu_mul_backward(grad_output.contiguous().to(gate.dtype), gate, up)
         return dg.reshape(ctx.original_shape), du.reshape(ctx.original_shape)
 
 

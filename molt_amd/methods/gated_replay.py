@@ -35,8 +35,8 @@ def _nf4_lora_forward(x: torch.Tensor, packed_weight: torch.Tensor, lora_a: torc
     """(Y, T) for ``Y = X deq(W)^T + s (X A^T) B^T`` (methods/gated_replay.py:211-224)."""
     n, k = _rows_cols(quant_state.shape)
     flat = x.reshape(-1, k)
-    t = ops.lora_project(flat, None, 0, 1.0, lora_a, 0)
-    y = ops.nf4_lora_forward(flat, packed_weight.reshape(-1), resolved_nf4_scales(quant_state),
+    t = ops.direct.lora_project(flat, None, 0, 1.0, lora_a, 0)
+    y = ops.direct.nf4_lora_forward(flat, packed_weight.reshape(-1), resolved_nf4_scales(quant_state),
                              quant_state.code, n, k, nibble_order(quant_state), int(quant_state.blocksize),
                              t, lora_b, float(scaling))
     return y.reshape(*x.shape[:-1], n), t
@@ -70,7 +70,7 @@ class _AsymmetricGatedNF4LoRA(torch.autograd.Function):
                 raise CapabilityError("gated activation offload requires pinned gate storage")
             if host_gate.shape != gate.shape or host_gate.dtype != gate.dtype:
                 raise CapabilityError("gated activation host storage must match the gate result")
-        gated = ops.silu_mul_forward(gate, up, True)
+        gated = ops.direct.silu_mul_forward(gate, up, True)
         result, low_rank = _nf4_lora_forward(gated, down_packed_weight, down_lora_a, down_lora_b,
                                              down_quant_state, down_scaling)
         del gated
@@ -104,12 +104,12 @@ class _AsymmetricGatedNF4LoRA(torch.autograd.Function):
         h_dim, i_dim = _rows_cols(qs.shape)
         dy = grad_output.reshape(-1, h_dim).to(torch.bfloat16)
         g2, u2 = gate.reshape(-1, i_dim), up.reshape(-1, i_dim)
-        grad_through_b = ops.lora_project(dy, None, 2, ctx.down_scaling, down_lora_b, 1)
-        grad_gate, grad_up = ops.nf4_swiglu_backward(dy, down_packed_weight.reshape(-1), resolved_nf4_scales(qs),
+        grad_through_b = ops.direct.lora_project(dy, None, 2, ctx.down_scaling, down_lora_b, 1)
+        grad_gate, grad_up = ops.direct.nf4_swiglu_backward(dy, down_packed_weight.reshape(-1), resolved_nf4_scales(qs),
                                                      qs.code, h_dim, i_dim, nibble_order(qs), grad_through_b,
                                                      down_lora_a, g2, u2)
-        grad_down_a = ops.lora_grad(g2, u2, 1, grad_through_b, 1.0, 1)
-        grad_down_b = ops.lora_grad(dy, None, 0, low_rank, ctx.down_scaling, 0)
+        grad_down_a = ops.direct.lora_grad(g2, u2, 1, grad_through_b, 1.0, 1)
+        grad_down_b = ops.direct.lora_grad(dy, None, 0, low_rank, ctx.down_scaling, 0)
         return (None, grad_gate.reshape(gate.shape), grad_up.reshape(up.shape), None, None, None, None,
                 grad_down_a.to(down_lora_a.dtype), grad_down_b.to(down_lora_b.dtype),
                 None, None, None, None, None, None, None, None, None)
@@ -174,13 +174,13 @@ def _fused_forward(x, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_p
     if up_a.shape[0] != r:
         raise ValueError("gate and up adapters must share a rank")
     flat = x.reshape(-1, h_dim)
-    t_gu = ops.lora_project(flat, None, 0, 1.0, torch.cat([gate_a, up_a], 0), 0)
-    gate, up, gated = ops.nf4_gateup_forward(
+    t_gu = ops.direct.lora_project(flat, None, 0, 1.0, torch.cat([gate_a, up_a], 0), 0)
+    gate, up, gated = ops.direct.nf4_gateup_forward(
         flat, gate_packed.reshape(-1), resolved_nf4_scales(gate_qs), up_packed.reshape(-1),
         resolved_nf4_scales(up_qs), gate_qs.code, i_dim, h_dim, nibble_order(gate_qs), t_gu, gate_b, up_b,
         float(gate_scaling), float(up_scaling))
-    t_d = ops.lora_project(gated, None, 0, 1.0, down_a, 0)
-    y = ops.nf4_lora_forward(gated, down_packed.reshape(-1), resolved_nf4_scales(down_qs), down_qs.code,
+    t_d = ops.direct.lora_project(gated, None, 0, 1.0, down_a, 0)
+    y = ops.direct.nf4_lora_forward(gated, down_packed.reshape(-1), resolved_nf4_scales(down_qs), down_qs.code,
                              h_dim, i_dim, nibble_order(down_qs), 64, t_d, down_b, float(down_scaling))
     return y, gate, up, gated, t_gu, t_d, (h_dim, i_dim, r)
 
@@ -194,24 +194,24 @@ def _fused_backward(grad_output, flat, gate, up, gated, t_gu, t_d, gate_packed, 
     s_g, s_u, s_d = scaling
     h_dim, i_dim, r = dims
     dy = grad_output.reshape(-1, h_dim).to(torch.bfloat16)
-    u_d = ops.lora_project(dy, None, 2, s_d, down_b, 1)
-    dg, du = ops.nf4_swiglu_backward(dy, down_packed.reshape(-1), resolved_nf4_scales(down_qs), down_qs.code,
+    u_d = ops.direct.lora_project(dy, None, 2, s_d, down_b, 1)
+    dg, du = ops.direct.nf4_swiglu_backward(dy, down_packed.reshape(-1), resolved_nf4_scales(down_qs), down_qs.code,
                                      h_dim, i_dim, nibble_order(down_qs), u_d, down_a, gate, up)
-    u_g = ops.lora_project(dg, None, 2, s_g, gate_b, 1)
-    u_u = ops.lora_project(du, None, 2, s_u, up_b, 1)
-    dx = ops.nf4_lora_backward_input_pair(
+    u_g = ops.direct.lora_project(dg, None, 2, s_g, gate_b, 1)
+    u_u = ops.direct.lora_project(du, None, 2, s_u, up_b, 1)
+    dx = ops.direct.nf4_lora_backward_input_pair(
         dg, du, gate_packed.reshape(-1), resolved_nf4_scales(gate_qs), up_packed.reshape(-1),
         resolved_nf4_scales(up_qs), gate_qs.code, i_dim, h_dim, nibble_order(gate_qs), u_g, u_u, gate_a,
         up_a)
     if gated is not None:   # h kept from the forward: bitwise the replayed value
-        d_down_a = ops.lora_grad(gated, None, 0, u_d, 1.0, 1)
+        d_down_a = ops.direct.lora_grad(gated, None, 0, u_d, 1.0, 1)
     else:
-        d_down_a = ops.lora_grad(gate, up, 1, u_d, 1.0, 1)
-    d_down_b = ops.lora_grad(dy, None, 0, t_d, s_d, 0)
+        d_down_a = ops.direct.lora_grad(gate, up, 1, u_d, 1.0, 1)
+    d_down_b = ops.direct.lora_grad(dy, None, 0, t_d, s_d, 0)
     # dA_gate and dA_up both contract X: one pass over X with [U_g | U_u]
-    d_gu_a = ops.lora_grad(flat, None, 0, torch.cat([u_g, u_u], 1), 1.0, 1)
-    d_gate_b = ops.lora_grad(dg, None, 0, t_gu[:, :r], s_g, 0)
-    d_up_b = ops.lora_grad(du, None, 0, t_gu[:, r:], s_u, 0)
+    d_gu_a = ops.direct.lora_grad(flat, None, 0, torch.cat([u_g, u_u], 1), 1.0, 1)
+    d_gate_b = ops.direct.lora_grad(dg, None, 0, t_gu[:, :r], s_g, 0)
+    d_up_b = ops.direct.lora_grad(du, None, 0, t_gu[:, r:], s_u, 0)
     return dx, d_gu_a[:r], d_gate_b, d_gu_a[r:], d_up_b, d_down_a, d_down_b
 
 
@@ -283,7 +283,7 @@ class _RMSNormReplayRecipe:
     target: torch.Tensor | None = None
 
     def materialize(self) -> torch.Tensor:
-        return ops.rmsnorm_forward(self.source, self.weight, float(self.eps), float(self.weight_offset))
+        return ops.direct.rmsnorm_forward(self.source, self.weight, float(self.eps), float(self.weight_offset))
 
 
 def _replayable_norm_forward(module: torch.nn.Module, hidden: torch.Tensor, *args: Any,

@@ -50,7 +50,7 @@ def packed_nf4_backward_input(
     (methods/nf4_backward.py:167-217)."""
     flat, n, k = _prepare(grad_output, quant_state, "packed NF4 backward")
     resolved = resolved_nf4_scales(quant_state) if scales is None else scales
-    out = ops.nf4_lora_backward_input(flat, packed_weight.reshape(-1), resolved, quant_state.code, n, k,
+    out = ops.direct.nf4_lora_backward_input(flat, packed_weight.reshape(-1), resolved, quant_state.code, n, k,
                                       nibble_order(quant_state), int(quant_state.blocksize), None, None, 1.0)
     return out.reshape(*grad_output.shape[:-1], k)
 
@@ -77,7 +77,7 @@ def packed_nf4_lora_backward_input(
     if lora_a.ndim != 2 or flat_lora.shape[1] != lora_a.shape[0] or lora_a.shape[1] != k:
         raise ValueError("LoRA gradient and A matrix dimensions are incompatible")
     resolved = resolved_nf4_scales(quant_state) if scales is None else scales
-    out = ops.nf4_lora_backward_input(flat, packed_weight.reshape(-1), resolved, quant_state.code, n, k,
+    out = ops.direct.nf4_lora_backward_input(flat, packed_weight.reshape(-1), resolved, quant_state.code, n, k,
                                       nibble_order(quant_state), int(quant_state.blocksize), flat_lora,
                                       lora_a, float(scaling))
     return out.reshape(*grad_output.shape[:-1], k)

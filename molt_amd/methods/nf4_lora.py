@@ -58,8 +58,8 @@ class _ScheduledNF4LoRA(torch.autograd.Function):
             )
         flat_x = x.reshape(-1, k)
         scales = resolved_nf4_scales(quant_state)
-        low_rank = ops.lora_project(flat_x, None, 0, 1.0, lora_a, 0)
-        result = ops.nf4_lora_forward(flat_x, packed_weight.reshape(-1), scales, quant_state.code, n, k,
+        low_rank = ops.direct.lora_project(flat_x, None, 0, 1.0, lora_a, 0)
+        result = ops.direct.nf4_lora_forward(flat_x, packed_weight.reshape(-1), scales, quant_state.code, n, k,
                                       nibble_order(quant_state), int(quant_state.blocksize), low_rank,
                                       lora_b, float(scaling))
         ctx.quant_state = quant_state
@@ -80,11 +80,11 @@ class _ScheduledNF4LoRA(torch.autograd.Function):
         flat_x = x.reshape(-1, k)
         flat_grad = grad_output.reshape(-1, n).to(torch.bfloat16)
         scales = resolved_nf4_scales(qs)
-        grad_through_b = ops.lora_project(flat_grad, None, 2, ctx.scaling, lora_b, 1)
-        grad_x = ops.nf4_lora_backward_input(flat_grad, packed_weight.reshape(-1), scales, qs.code, n, k,
+        grad_through_b = ops.direct.lora_project(flat_grad, None, 2, ctx.scaling, lora_b, 1)
+        grad_x = ops.direct.nf4_lora_backward_input(flat_grad, packed_weight.reshape(-1), scales, qs.code, n, k,
                                              nibble_order(qs), int(qs.blocksize), grad_through_b, lora_a, 1.0)
-        grad_a = ops.lora_grad(flat_x, None, 0, grad_through_b, 1.0, 1)
-        grad_b = ops.lora_grad(flat_grad, None, 0, low_rank, ctx.scaling, 0)
+        grad_a = ops.direct.lora_grad(flat_x, None, 0, grad_through_b, 1.0, 1)
+        grad_b = ops.direct.lora_grad(flat_grad, None, 0, low_rank, ctx.scaling, 0)
         return (grad_x.reshape(ctx.input_shape), None, grad_a.to(lora_a.dtype), grad_b.to(lora_b.dtype),
                 None, None, None)
 

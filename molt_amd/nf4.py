@@ -140,14 +140,14 @@ def quantize_4bit(A: torch.Tensor, blocksize: int = 64, compress_statistics: boo
         raise CapabilityError("NF4 quantization requires a CUDA tensor on a ROCm GPU")
     dev = A.device
     cb = (NF4_CODEBOOK if code is None else code).to(dev, torch.float32)
-    packed, absmax = ops.nf4_quantize(A, blocksize, nibble_order, cb)
+    packed, absmax = ops.direct.nf4_quantize(A, blocksize, nibble_order, cb)
     n = A.numel()
     packed = packed[: (n + 1) // 2].reshape(-1, 1)
     dtype = A.dtype if A.dtype in (torch.bfloat16, torch.float16, torch.float32) else torch.bfloat16
     if not compress_statistics:
         return packed, QuantState(absmax, A.shape, cb, blocksize, "nf4", dtype, None, None, nibble_order)
     code2 = dynamic_map().to(dev)
-    q, absmax2, offset = ops.nf4_double_quantize(absmax, code2, 256)
+    q, absmax2, offset = ops.direct.nf4_double_quantize(absmax, code2, 256)
     state2 = QuantState(absmax2, (absmax2.numel(),), code2, 256, "dynamic", torch.float32)
     qs = QuantState(q, A.shape, cb, blocksize, "nf4", dtype, offset, state2, nibble_order)
     return packed, qs
@@ -163,7 +163,7 @@ def resolved_nf4_scales(quant_state: Any) -> torch.Tensor:
         return cached
     if quant_state.nested:
         s2 = quant_state.state2
-        scales = ops.nf4_resolve_scales(quant_state.absmax, s2.absmax, s2.code, _offset(quant_state),
+        scales = ops.direct.nf4_resolve_scales(quant_state.absmax, s2.absmax, s2.code, _offset(quant_state),
                                         int(s2.blocksize))
     else:
         scales = quant_state.absmax.float()
@@ -182,11 +182,11 @@ def dequantize_4bit(A: torch.Tensor, quant_state: Any, out_dtype: torch.dtype | 
     packed = A.reshape(-1)
     if quant_state.nested:
         s2 = quant_state.state2
-        dense = ops.nf4_dequantize_nested(packed, quant_state.absmax, s2.absmax, s2.code, quant_state.code,
+        dense = ops.direct.nf4_dequantize_nested(packed, quant_state.absmax, s2.absmax, s2.code, quant_state.code,
                                           _offset(quant_state), n_rows, n_cols, int(quant_state.blocksize),
                                           int(s2.blocksize), nibble_order(quant_state), dtype)
     else:
-        dense = ops.nf4_dequantize(packed, quant_state.absmax, quant_state.code, n_rows, n_cols,
+        dense = ops.direct.nf4_dequantize(packed, quant_state.absmax, quant_state.code, n_rows, n_cols,
                                    int(quant_state.blocksize), nibble_order(quant_state), dtype)
     return dense.reshape(quant_state.shape)
 
@@ -218,7 +218,7 @@ class NF4DevicePayload:
         if self.packed.device.type != "cuda":
             raise CapabilityError("NF4 dequantize requires CUDA tensors on a ROCm GPU")
         out_dtype = torch.float32 if dtype not in (torch.bfloat16, torch.float32) else dtype
-        dense = ops.nf4_dequantize(self.packed, self.scales, NF4_CODEBOOK.to(self.packed.device), 1,
+        dense = ops.direct.nf4_dequantize(self.packed, self.scales, NF4_CODEBOOK.to(self.packed.device), 1,
                                    self.elements, self.block_size, NIBBLE_LOW_FIRST, out_dtype)
         return dense.reshape(self.shape).to(dtype)
 
@@ -242,7 +242,7 @@ class NF4Tensor:
         if not torch.cuda.is_available():
             raise CapabilityError("NF4 quantization requires a ROCm GPU")
         src = value.detach().float().to(device)
-        packed, scales = ops.nf4_quantize(src, block_size, NIBBLE_LOW_FIRST, NF4_CODEBOOK.to(device))
+        packed, scales = ops.direct.nf4_quantize(src, block_size, NIBBLE_LOW_FIRST, NF4_CODEBOOK.to(device))
         packed, scales = packed.cpu(), scales.cpu()
         if pin_memory:
             packed, scales = packed.pin_memory(), scales.pin_memory()

@@ -40,7 +40,45 @@ def _require_gpu(*tensors: Optional[Tensor], what: str) -> torch.device:
 
 
 def _stream(dev: torch.device) -> int:
-    return torch.cuda.current_stream(dev).cuda_stream
+    """Raw handle of the device's current stream (what the kernels launch on)."""
+    return _raw_stream(dev.index if dev.index is not None else torch.cuda.current_device())
+
+
+def _raw_stream_fallback(index: int) -> int:
+    return torch.cuda.current_stream(index).cuda_stream
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", _raw_stream_fallback)
+
+# Implementations of the registered ops, by name. The autograd nodes of the
+# hot path call them through ``direct`` in eager mode: the dispatcher costs
+# about 13 us per call on the host, more than the GPU time of the small
+# projections. Under torch.compile ``direct`` returns the registered op.
+_RAW: dict = {}
+
+
+def _custom_op(qualname: str, mutates_args=()):
+    def deco(fn):
+        _RAW[qualname.split("::", 1)[1]] = fn
+        return torch.library.custom_op(qualname, mutates_args=mutates_args)(fn)
+    return deco
+
+
+class _Direct:
+    def __getattr__(self, name: str):
+        raw, op = _RAW[name], globals()[name]
+
+        def call(*args, **kwargs):
+            if torch.compiler.is_compiling():
+                return op(*args, **kwargs)
+            return raw(*args, **kwargs)
+
+        call.__name__ = name
+        setattr(self, name, call)
+        return call
+
+
+direct = _Direct()
 
 
 def _ptr(t: Optional[Tensor]) -> Optional[int]:
@@ -102,12 +140,20 @@ def probe_events(name: str, enable: bool = True) -> list:
     return _probes.pop(name, [])
 
 
+_FNS: dict = {}
+
+
 def _call(fn_name: str, *args) -> None:
-    lib = _lib.load()
-    pairs = _probes.get(fn_name)
+    fn = _FNS.get(fn_name)
+    if fn is None:
+        fn = _FNS[fn_name] = getattr(_lib.load(), fn_name)
+    pairs = _probes.get(fn_name) if _probes else None
     if pairs is None:
-        _lib.check(getattr(lib, fn_name)(*args))
+        rc = fn(*args)
+        if rc:
+            _lib.check(rc)
         return
+    lib = _lib.load()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     _lib.check(getattr(lib, fn_name)(*args))
@@ -116,7 +162,7 @@ def _call(fn_name: str, *args) -> None:
 
 
 # ----------------------------------------------------------------- codec
-@torch.library.custom_op(f"{NS}::nf4_dequantize", mutates_args=())
+@_custom_op(f"{NS}::nf4_dequantize", mutates_args=())
 def nf4_dequantize(packed: Tensor, scales: Tensor, code: Tensor, rows: int, cols: int,
                    block_size: int, order: int, out_dtype: torch.dtype) -> Tensor:
     """bf16/fp32 decode with resolved fp32 scales (streaming/nf4.py:29-35)."""
@@ -137,7 +183,7 @@ def _(packed, scales, code, rows, cols, block_size, order, out_dtype):
     return packed.new_empty((rows, cols), dtype=out_dtype)
 
 
-@torch.library.custom_op(f"{NS}::nf4_dequantize_nested", mutates_args=())
+@_custom_op(f"{NS}::nf4_dequantize_nested", mutates_args=())
 def nf4_dequantize_nested(packed: Tensor, absmax_q: Tensor, absmax2: Tensor, code2: Tensor,
                           code: Tensor, offset: float, rows: int, cols: int, block_size: int,
                           dq_block: int, order: int, out_dtype: torch.dtype) -> Tensor:
@@ -161,7 +207,7 @@ def _(packed, absmax_q, absmax2, code2, code, offset, rows, cols, block_size, dq
     return packed.new_empty((rows, cols), dtype=out_dtype)
 
 
-@torch.library.custom_op(f"{NS}::nf4_resolve_scales", mutates_args=())
+@_custom_op(f"{NS}::nf4_resolve_scales", mutates_args=())
 def nf4_resolve_scales(absmax_q: Tensor, absmax2: Tensor, code2: Tensor, offset: float,
                        dq_block: int) -> Tensor:
     """fp32 block scales from nested statistics (methods/nf4_backward.py:145-164)."""
@@ -181,7 +227,7 @@ def _(absmax_q, absmax2, code2, offset, dq_block):
     return absmax_q.new_empty(absmax_q.numel(), dtype=torch.float32)
 
 
-@torch.library.custom_op(f"{NS}::nf4_quantize", mutates_args=())
+@_custom_op(f"{NS}::nf4_quantize", mutates_args=())
 def nf4_quantize(x: Tensor, block_size: int, order: int, code: Tensor) -> tuple[Tensor, Tensor]:
     """Blockwise NF4 codes + fp32 absmax (streaming/nf4.py:46-68)."""
     what = "NF4 quantize"
@@ -208,7 +254,7 @@ def _(x, block_size, order, code):
             x.new_empty(nblocks, dtype=torch.float32))
 
 
-@torch.library.custom_op(f"{NS}::nf4_double_quantize", mutates_args=())
+@_custom_op(f"{NS}::nf4_double_quantize", mutates_args=())
 def nf4_double_quantize(absmax: Tensor, code2: Tensor, dq_block: int) -> tuple[Tensor, Tensor, Tensor]:
     """Nested statistics (bitsandbytes compress_statistics=True)."""
     dev = _require_gpu(absmax, code2, what="NF4 double quantize")
@@ -233,7 +279,7 @@ def _(absmax, code2, dq_block):
 
 
 # ------------------------------------------------------------ NF4 + LoRA
-@torch.library.custom_op(f"{NS}::lora_project", mutates_args=())
+@_custom_op(f"{NS}::lora_project", mutates_args=())
 def lora_project(z: Tensor, z2: Optional[Tensor], mode: int, zscale: float, lora: Tensor,
                  layout: int) -> Tensor:
     """out[M, r] = bf16(z . bf16(lora)^T) (methods/nf4_lora.py:49,86-90)."""
@@ -262,7 +308,7 @@ def _(z, z2, mode, zscale, lora, layout):
     return z.new_empty((z.shape[0], r), dtype=torch.bfloat16)
 
 
-@torch.library.custom_op(f"{NS}::nf4_lora_forward", mutates_args=())
+@_custom_op(f"{NS}::nf4_lora_forward", mutates_args=())
 def nf4_lora_forward(x: Tensor, packed: Tensor, scales: Tensor, code: Tensor, rows: int, cols: int,
                      order: int, block_size: int, t: Optional[Tensor], lora_b: Optional[Tensor],
                      scaling: float) -> Tensor:
@@ -293,7 +339,7 @@ def _(x, packed, scales, code, rows, cols, order, block_size, t, lora_b, scaling
     return x.new_empty((x.shape[0], rows), dtype=torch.bfloat16)
 
 
-@torch.library.custom_op(f"{NS}::nf4_gateup_forward", mutates_args=())
+@_custom_op(f"{NS}::nf4_gateup_forward", mutates_args=())
 def nf4_gateup_forward(x: Tensor, packed_g: Tensor, scales_g: Tensor, packed_u: Tensor,
                        scales_u: Tensor, code: Tensor, rows: int, cols: int, order: int,
                        t: Optional[Tensor], lora_bg: Optional[Tensor], lora_bu: Optional[Tensor],
@@ -331,7 +377,7 @@ def _(x, packed_g, scales_g, packed_u, scales_u, code, rows, cols, order, t, lor
     return tuple(x.new_empty((x.shape[0], rows), dtype=torch.bfloat16) for _ in range(3))
 
 
-@torch.library.custom_op(f"{NS}::nf4_lora_backward_input", mutates_args=())
+@_custom_op(f"{NS}::nf4_lora_backward_input", mutates_args=())
 def nf4_lora_backward_input(dy: Tensor, packed: Tensor, scales: Tensor, code: Tensor, rows: int,
                             cols: int, order: int, block_size: int, u: Optional[Tensor],
                             lora_a: Optional[Tensor], lora_scale: float) -> Tensor:
@@ -365,7 +411,7 @@ def _(dy, packed, scales, code, rows, cols, order, block_size, u, lora_a, lora_s
     return dy.new_empty((dy.shape[0], cols), dtype=torch.bfloat16)
 
 
-@torch.library.custom_op(f"{NS}::nf4_lora_backward_input_pair", mutates_args=())
+@_custom_op(f"{NS}::nf4_lora_backward_input_pair", mutates_args=())
 def nf4_lora_backward_input_pair(dy0: Tensor, dy1: Tensor, packed0: Tensor, scales0: Tensor,
                                  packed1: Tensor, scales1: Tensor, code: Tensor, rows: int, cols: int,
                                  order: int, u0: Optional[Tensor], u1: Optional[Tensor],
@@ -404,7 +450,7 @@ def _(dy0, dy1, packed0, scales0, packed1, scales1, code, rows, cols, order, u0,
     return dy0.new_empty((dy0.shape[0], cols), dtype=torch.bfloat16)
 
 
-@torch.library.custom_op(f"{NS}::nf4_swiglu_backward", mutates_args=())
+@_custom_op(f"{NS}::nf4_swiglu_backward", mutates_args=())
 def nf4_swiglu_backward(dy: Tensor, packed: Tensor, scales: Tensor, code: Tensor, rows: int, cols: int,
                         order: int, u: Optional[Tensor], lora_a: Optional[Tensor], gate: Tensor,
                         up: Tensor) -> tuple[Tensor, Tensor]:
@@ -440,7 +486,7 @@ def _(dy, packed, scales, code, rows, cols, order, u, lora_a, gate, up):
     return torch.empty_like(gate), torch.empty_like(up)
 
 
-@torch.library.custom_op(f"{NS}::lora_grad", mutates_args=())
+@_custom_op(f"{NS}::lora_grad", mutates_args=())
 def lora_grad(l: Tensor, l2: Optional[Tensor], mode: int, rmat: Tensor, scale: float,
               layout: int) -> Tensor:
     """scale * L^T R in fp32: dB = s dY^T T (layout 0, [P, Q]) and dA = U^T X
@@ -470,7 +516,7 @@ def _(l, l2, mode, rmat, scale, layout):
 
 
 # ------------------------------------------------------------------ GEMV
-@torch.library.custom_op(f"{NS}::nf4_gemv", mutates_args=())
+@_custom_op(f"{NS}::nf4_gemv", mutates_args=())
 def nf4_gemv(x: Tensor, packed: Tensor, scales: Optional[Tensor], absmax_q: Optional[Tensor],
              absmax2: Optional[Tensor], code2: Optional[Tensor], offset: float, dq_block: int,
              code: Tensor, rows: int, cols: int, order: int, t: Optional[Tensor],
@@ -519,7 +565,7 @@ def _sw_dtype(t: Tensor) -> int:
     raise CapabilityError(f"fused SiLU multiply supports bf16 and fp32 (got {t.dtype})")
 
 
-@torch.library.custom_op(f"{NS}::silu_mul_forward", mutates_args=())
+@_custom_op(f"{NS}::silu_mul_forward", mutates_args=())
 def silu_mul_forward(gate: Tensor, up: Tensor, round_silu: bool) -> Tensor:
     """h = silu(g) * u (kernels/gated_activation.py:29-36)."""
     dev = _require_gpu(gate, up, what="fused SiLU multiply")
@@ -535,7 +581,7 @@ def _(gate, up, round_silu):
     return torch.empty_like(gate)
 
 
-@torch.library.custom_op(f"{NS}::silu_mul_backward", mutates_args=())
+@_custom_op(f"{NS}::silu_mul_backward", mutates_args=())
 def silu_mul_backward(grad: Tensor, gate: Tensor, up: Tensor) -> tuple[Tensor, Tensor]:
     """(dgate, dup) of h = silu(g) * u (kernels/gated_activation.py:38-51)."""
     dev = _require_gpu(grad, gate, up, what="fused SiLU multiply")
@@ -568,7 +614,7 @@ def _rn_check(x: Tensor, weight: Tensor) -> int:
     return int(x.shape[-1])
 
 
-@torch.library.custom_op(f"{NS}::rmsnorm_forward", mutates_args=())
+@_custom_op(f"{NS}::rmsnorm_forward", mutates_args=())
 def rmsnorm_forward(x: Tensor, weight: Tensor, eps: float, offset: float) -> Tensor:
     """bf16(fp32(x) * rsqrt(mean(fp32(x)^2) + eps) * (fp32(weight) + offset))
     over the last dimension (kernels/frozen_rmsnorm.py:16-23)."""
@@ -589,7 +635,7 @@ def _(x, weight, eps, offset):
     return torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
 
 
-@torch.library.custom_op(f"{NS}::rmsnorm_backward", mutates_args=())
+@_custom_op(f"{NS}::rmsnorm_backward", mutates_args=())
 def rmsnorm_backward(grad: Tensor, x: Tensor, weight: Tensor, eps: float, offset: float) -> Tensor:
     """Input gradient of the frozen RMSNorm in x's dtype (kernels/frozen_rmsnorm.py:25-37)."""
     dev = _require_gpu(grad, x, weight, what="frozen RMSNorm")

@@ -1,0 +1,158 @@
+"""Load-time preparation of a (tiny, randomly initialised) Llama decoder for
+the NF4 QLoRA path on the GPU: every projection quantised bit-exactly as the
+oracle does, the patchers wired onto the prepared model, one decoder layer's
+MLP block (with the RMSNorm-replay recipe) and its attention projections
+(including the grouped-query k/v shapes) against the fp64 oracle, and the
+bitsandbytes 4-bit serialisation round trip through a safetensors file."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from oracle import nf4_oracle as O
+from tests._util import assert_close_fro, bf16_values, np_f32, oracle_weight, seeded
+
+import molt_amd
+from molt_amd.kernels import enable_frozen_rmsnorm_bf16
+from molt_amd.loading import load_prequantized_nf4, nf4_state_dict, prepare_nf4_qlora, quantize_linears_nf4
+from molt_amd.methods import enable_fused_gated_nf4_lora, enable_rmsnorm_replay, enable_scheduled_nf4_lora
+from molt_amd.modules import NF4Linear, NF4LoRALinear
+
+pytestmark = pytest.mark.gpu
+
+H, I, HEADS, KV = 128, 256, 4, 2
+
+
+def _llama(seed: int = 0):
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(hidden_size=H, intermediate_size=I, num_hidden_layers=2, num_attention_heads=HEADS,
+                      num_key_value_heads=KV, vocab_size=64, tie_word_embeddings=False, rms_norm_eps=1e-6)
+    torch.manual_seed(seed)
+    return LlamaForCausalLM(cfg)
+
+
+def _prepared(r=8, alpha=16.0):
+    model = _llama()
+    prepare_nf4_qlora(model, r, alpha)
+    g = torch.Generator(device="cpu").manual_seed(11)
+    for m in model.modules():
+        if isinstance(m, NF4LoRALinear):   # non-zero B so that every LoRA gradient is exercised
+            m.lora_B["default"].weight.data.copy_(torch.randn(m.lora_B["default"].weight.shape, generator=g) * 0.01)
+    return model
+
+
+def test_prepare_quantises_every_projection_bit_exact():
+    model = _llama()
+    dense = {n: m.weight.detach().clone() for n, m in model.named_modules() if isinstance(m, nn.Linear)}
+    prepare_nf4_qlora(model, 8, 16.0)
+    wrapped = {n: m for n, m in model.named_modules() if isinstance(m, NF4LoRALinear)}
+    assert len(wrapped) == 14
+    assert isinstance(model.lm_head, nn.Linear) and model.lm_head.weight.dtype == torch.bfloat16
+    assert model.lm_head.weight.device.type == "cuda" and not model.lm_head.weight.requires_grad
+    trainable = [n for n, p in model.named_parameters() if p.requires_grad]
+    assert len(trainable) == 28 and all("lora_" in n for n in trainable)
+    for name, mod in wrapped.items():
+        print(f"check {name}", flush=True)
+        w = mod.base_layer.weight
+        ow = O.quantize_bnb_layout(dense[name].numpy(), 64, nested=True)
+        assert np.array_equal(w.reshape(-1).cpu().numpy(), ow.packed[: w.numel()])
+        qs = w.quant_state
+        assert np.array_equal(qs.absmax.cpu().numpy(), ow.q)
+        assert np.float32(float(qs.offset)).view(np.uint32) == np.float32(ow.offset).view(np.uint32)
+        scales = molt_amd.resolved_nf4_scales(qs)
+        assert np.array_equal(np_f32(scales).view(np.uint32), ow.scales.view(np.uint32))
+        assert mod.lora_A["default"].weight.dtype == torch.float32 and mod.scaling["default"] == 2.0
+
+
+def test_prepared_decoder_layer_runs_through_the_patched_path():
+    model = _prepared()
+    assert enable_frozen_rmsnorm_bf16(model) == 5
+    assert enable_scheduled_nf4_lora(model, module_suffixes=("q_proj", "k_proj", "v_proj", "o_proj")) == 8
+    assert enable_fused_gated_nf4_lora(model) == 2
+    assert enable_rmsnorm_replay(model) == 2
+    layer = model.model.layers[1]
+    m, s = 48, 2.0
+
+    # MLP block: residual -> frozen RMSNorm -> fused gated MLP (recipe) -> residual add
+    resid = seeded((m, H), 21, std=1.3).requires_grad_()
+    dy = seeded((m, H), 22)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        mlp_out = layer.mlp(layer.post_attention_layernorm(resid))
+        out = resid + mlp_out
+    assert "ResidualRecipe" in type(mlp_out.grad_fn).__name__
+    out.backward(dy)
+    norm = layer.post_attention_layernorm
+    projs = [layer.mlp.gate_proj, layer.mlp.up_proj, layer.mlp.down_proj]
+    ws = [oracle_weight(p.base_layer.weight, p.base_layer.weight.quant_state).dequant_bf16().astype(np.float64)
+          for p in projs]
+    av = []
+    for p in projs:
+        av += [bf16_values(p.lora_A["default"].weight), bf16_values(p.lora_B["default"].weight)]
+    xs, wn = bf16_values(resid), bf16_values(norm.weight)
+    xn = O.bf16_round(O.rmsnorm_forward(xs, wn, 1e-6, 0.0).astype(np.float32)).astype(np.float64)
+    ry, saved = O.gated_mlp_forward(xn, ws[0], ws[1], ws[2], *av, s)
+    rdx, rgrads = O.gated_mlp_backward(xn, ws[0], ws[1], ws[2], *av, s, bf16_values(dy), saved)
+    rdres = bf16_values(dy) + O.rmsnorm_backward(xs, wn, 1e-6, 0.0, O.bf16_round(rdx.astype(np.float32)))
+    assert_close_fro(np_f32(mlp_out), ry, what="MLP out")
+    assert_close_fro(np_f32(resid.grad), rdres, what="d_residual")
+    leaves = []
+    for p in projs:
+        leaves += [p.lora_A["default"].weight, p.lora_B["default"].weight]
+    for leaf, ref, name in zip(leaves, rgrads, ("dA_gate", "dB_gate", "dA_up", "dB_up", "dA_down", "dB_down")):
+        assert_close_fro(np_f32(leaf.grad), ref, what=name)
+
+    # attention projections (k/v: 128 -> 64, grouped-query) through the scheduled NF4-LoRA op
+    x = seeded((m, H), 23).requires_grad_()
+    for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
+        mod = getattr(layer.self_attn, name)
+        x.grad = None
+        dyp = seeded((m, mod.out_features), 24)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = mod(x)
+        assert "ScheduledNF4LoRA" in type(y.grad_fn).__name__, name
+        y.backward(dyp)
+        w = oracle_weight(mod.base_layer.weight, mod.base_layer.weight.quant_state).dequant_bf16().astype(np.float64)
+        a, b = bf16_values(mod.lora_A["default"].weight), bf16_values(mod.lora_B["default"].weight)
+        ry = O.lora_linear_forward(bf16_values(x), w, a, b, s)
+        rdx, rda, rdb = O.lora_linear_backward(bf16_values(x), w, a, b, s, bf16_values(dyp))
+        assert_close_fro(np_f32(y), ry, what=f"{name} Y")
+        assert_close_fro(np_f32(x.grad), rdx, what=f"{name} dX")
+        assert_close_fro(np_f32(mod.lora_A["default"].weight.grad), rda, what=f"{name} dA")
+        assert_close_fro(np_f32(mod.lora_B["default"].weight.grad), rdb, what=f"{name} dB")
+
+
+def test_bitsandbytes_serialisation_round_trip(tmp_path):
+    from safetensors.torch import load_file, save_file
+
+    src = _llama(seed=5)
+    for p in src.parameters():
+        p.requires_grad_(False)
+    assert quantize_linears_nf4(src, "all-linear") == 14
+    state = nf4_state_dict(src)
+    assert state["model.layers.0.mlp.gate_proj.weight"].shape == (I * H // 2, 1)
+    assert "model.layers.0.mlp.gate_proj.weight.quant_state.bitsandbytes__nf4" in state
+    path = tmp_path / "model.safetensors"
+    save_file(state, str(path))
+    loaded = load_file(str(path))
+
+    dst = _llama(seed=6)                       # different random weights everywhere
+    assert load_prequantized_nf4(dst, loaded) == 14
+    rest = {k: v for k, v in loaded.items() if not any(k.startswith(p + ".weight") for p, m in dst.named_modules()
+                                                        if isinstance(m, NF4Linear))}
+    missing, unexpected = dst.load_state_dict(rest, strict=False)
+    assert not unexpected, unexpected
+    for (na, a), (nb, b) in zip(src.named_modules(), dst.named_modules()):
+        assert na == nb
+        if isinstance(a, NF4Linear):
+            assert isinstance(b, NF4Linear)
+            qa, qb = a.weight.quant_state, b.weight.quant_state
+            assert torch.equal(a.weight.reshape(-1).cpu(), b.weight.reshape(-1).cpu())
+            assert torch.equal(qa.absmax.cpu(), qb.absmax.cpu()) and torch.equal(qa.code.cpu(), qb.code.cpu())
+            assert torch.equal(qa.state2.absmax.cpu(), qb.state2.absmax.cpu())
+            assert torch.equal(qa.state2.code.cpu(), qb.state2.code.cpu())
+            assert float(qa.offset) == float(qb.offset) and tuple(qa.shape) == tuple(qb.shape)
+            assert torch.equal(molt_amd.dequantize_4bit(a.weight, qa), molt_amd.dequantize_4bit(b.weight, qb))
+    assert torch.equal(src.model.norm.weight, dst.model.norm.weight.to(src.model.norm.weight.device))
