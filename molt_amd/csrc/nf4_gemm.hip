@@ -1056,30 +1056,46 @@ MOLT_DEV void stage_acc(const EpTile& ep, const f32x16_t (&acc)[TM][TN], int wm,
 }
 
 // SwiGLU backward epilogue (kernels/gated_activation.py:47-51 with MOLT's bf16
-// rounding points): dh comes from the staged tile, gate/up from HBM.
-MOLT_DEV void swiglu_bwd_store(const EpTile& ep, const BwdParams& p, int64_t m0, int64_t tn, int tid) {
-  // 256 rows x 32 chunks of 8 intermediate columns
-#pragma unroll 2
-  for (int it = 0; it < BM * 32 / NT; ++it) {
+// rounding points): dh comes from the staged tile, gate/up from HBM. A thread
+// owns SW_IT chunks of 8 intermediate columns (rows q / 32, chunk q % 32 for
+// q = tid + NT * it); swiglu_load issues all of its gate/up loads at once, so
+// they are in flight while the tile is staged and the workgroup synchronises.
+constexpr int SW_IT = BM * 32 / NT;
+struct SwigluIn { u32x4_t g[SW_IT], u[SW_IT]; };
+
+MOLT_DEV void swiglu_load(SwigluIn& in, const BwdParams& p, int64_t m0, int64_t tn, int tid) {
+#pragma unroll
+  for (int it = 0; it < SW_IT; ++it) {
+    const int q = tid + it * NT;
+    const int64_t m = m0 + (q >> 5), n = tn * BN + 8 * (q & 31);
+    const int64_t off = m * p.ldg + n;
+    if (m < p.M && p.vec_out && n + 8 <= p.Kw) {
+      in.g[it] = *reinterpret_cast<const u32x4_t*>(p.gate + off);
+      in.u[it] = *reinterpret_cast<const u32x4_t*>(p.up + off);
+    } else {
+      uint16_t gt[8], ut[8];
+      for (int e = 0; e < 8; ++e) {
+        const bool ok = m < p.M && n + e < p.Kw;
+        gt[e] = ok ? p.gate[off + e] : (uint16_t)0;
+        ut[e] = ok ? p.up[off + e] : (uint16_t)0;
+      }
+      in.g[it] = __builtin_bit_cast(u32x4_t, gt);
+      in.u[it] = __builtin_bit_cast(u32x4_t, ut);
+    }
+  }
+}
+
+MOLT_DEV void swiglu_bwd_store(const EpTile& ep, const BwdParams& p, int64_t m0, int64_t tn, int tid,
+                               const SwigluIn& in) {
+#pragma unroll
+  for (int it = 0; it < SW_IT; ++it) {
     const int q = tid + it * NT;
     const int row = q >> 5, ch = q & 31;
     const int64_t m = m0 + row, n = tn * BN + 8 * ch;
     if (m >= p.M || n >= p.Kw) continue;
     const u32x4_t dh = *reinterpret_cast<const u32x4_t*>(ep_at(ep, row, 8 * ch));
+    const u32x4_t gw = in.g[it], uw = in.u[it];
     const int64_t off = m * p.ldg + n;
-    u32x4_t gw, uw;
-    if (p.vec_out && n + 8 <= p.Kw) {
-      gw = *reinterpret_cast<const u32x4_t*>(p.gate + off);
-      uw = *reinterpret_cast<const u32x4_t*>(p.up + off);
-    } else {
-      uint16_t gt[8], ut[8];
-      for (int e = 0; e < 8; ++e) {
-        gt[e] = n + e < p.Kw ? p.gate[off + e] : (uint16_t)0;
-        ut[e] = n + e < p.Kw ? p.up[off + e] : (uint16_t)0;
-      }
-      gw = __builtin_bit_cast(u32x4_t, gt);
-      uw = __builtin_bit_cast(u32x4_t, ut);
-    }
     u32x4_t dgw, duw;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -1287,8 +1303,10 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
   // cooperatively with 16-byte loads of gate/up and 16-byte stores.
   const EpTile ep{xb0, xb1, wb0, wb1};
   stage_acc(ep, acc, wm, wn, lane);
+  SwigluIn in;
+  swiglu_load(in, p, m0, tn, tid);
   __syncthreads();
-  swiglu_bwd_store(ep, p, m0, tn, tid);
+  swiglu_bwd_store(ep, p, m0, tn, tid, in);
 }
 
 }  // namespace big
