@@ -7,7 +7,8 @@ and already resident in HBM. Also reported: the roofline of the dominant
 kernel (the fused gate/up NF4 GEMM) from HIP events recorded around its
 launches on its own stream during the timed steps, the frozen RMSNorm kernels
 and the RMSNorm-replay recipe step, every NF4-LoRA projection shape of the
-cfg3 decoder (attention and MLP, forward + backward), the skinny-M NF4 GEMV sweep (cfg5, HBM
+cfg3 decoder (attention and MLP, forward + backward), the frozen LM head with
+its chunked cross-entropy, the skinny-M NF4 GEMV sweep (cfg5, HBM
 GB/s), and the CPU baseline (the oracle's restatement of MOLT's
 eager CPU path, cfg1, numpy fp32 on the host cores).
 
@@ -248,6 +249,61 @@ def projection_sweep(dev, reps: int = 10):
     return out
 
 
+def lm_head_bench(dev, steps: int = 5):
+    """The frozen LM head of the cfg3 decoder (Qwen2.5-1.5B: vocabulary
+    151,936 x hidden 1,536, bf16) over M=4096 tokens in chunks of 256 through
+    frozen_linear_cross_entropy: loss and hidden gradient (two hipBLASLt GEMMs
+    per chunk, 4*M*V*H FLOPs in all, plus the HIP row reduction). The row
+    kernel alone is timed on one [256, V] chunk against its algorithmic bytes
+    (read the logits once, write the gradient once)."""
+    import torch
+    from molt_amd import ops
+    from molt_amd.kernels.frozen_linear_cross_entropy import frozen_linear_cross_entropy
+
+    V, H, M, chunk = 151936, 1536, 4096, 256
+    g = torch.Generator(device="cpu").manual_seed(11)
+    w = (torch.randn(V, H, generator=g) * 0.02).to(dev, torch.bfloat16)
+    h = torch.randn(M, H, generator=g).to(dev, torch.bfloat16).requires_grad_()
+    t = torch.randint(0, V, (M,), generator=g).to(dev)
+
+    def run():
+        h.grad = None
+        frozen_linear_cross_entropy(h, w, t, chunk).backward()
+
+    for _ in range(2):
+        run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    flop = 4 * M * V * H
+    tf = flop / (ms * 1e-3) / 1e12
+    logits = torch.randn(chunk, V, generator=g).to(dev, torch.bfloat16)
+    tc = t[:chunk].contiguous()
+    copies = [logits.clone() for _ in range(8)]
+    for c in copies:
+        ops.cross_entropy_rows(c, tc, float(M), True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for c in copies:
+        ops.cross_entropy_rows(c, tc, float(M), True)
+    e1.record()
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / len(copies)
+    nbytes = 2 * chunk * V * 2
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"LM head V={V} H={H} M={M} chunk={chunk}: loss+grad {ms:.3f} ms, {tf:.0f} TFLOP/s "
+        f"({100 * tf / PEAK_BF16_TFLOPS:.1f}%); row kernel {us:.1f} us per chunk, {gbs:.0f} GB/s "
+        f"({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM)")
+    return {"vocab": V, "hidden": H, "tokens": M, "chunk": chunk, "ms_loss_and_grad": round(ms, 4),
+            "TFLOP_s": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+            "row_kernel_us_per_chunk": round(us, 2), "row_kernel_GB_s": round(gbs, 1),
+            "row_kernel_frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+
+
 TRAFFIC_FILE = ROOT / "profiles" / "gateup_fwd_cfg4_hbm_traffic.txt"
 
 
@@ -357,6 +413,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-norm", action="store_true", help="skip the RMSNorm / norm-replay recipe measurement")
     ap.add_argument("--no-proj", action="store_true", help="skip the cfg3 projection sweep")
+    ap.add_argument("--no-head", action="store_true", help="skip the LM head + cross-entropy measurement")
     ap.add_argument("--profile-kernel", choices=("gateup", "copy"),
                     help="only launch one kernel (for rocprofv3 --pmc passes) and exit")
     ap.add_argument("--reps", type=int, default=3, help="launches for --profile-kernel")
@@ -421,6 +478,8 @@ def main() -> int:
         result["rmsnorm"] = rmsnorm_bench(dev, projs, dy, s, M, H, args.steps)
     if not args.no_proj:
         result["cfg3_projections"] = projection_sweep(dev)
+    if not args.no_head:
+        result["lm_head"] = lm_head_bench(dev)
     if not args.no_gemv:
         sweep = gemv_sweep(dev)
         result["gemv"] = sweep

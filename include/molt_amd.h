@@ -246,6 +246,21 @@ int molt_rmsnorm_backward(const uint16_t* dy, int64_t lddy, const void* x, int32
                           int32_t w_dtype, float eps, float offset, void* dx, int64_t lddx,
                           void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Frozen-head cross-entropy                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* Row-wise cross-entropy of a chunk of logits (bf16 or fp32 [rows, vocab],
+ * row stride ld) against int64 targets, reduced in fp32 with an online
+ * log-sum-exp: loss[i] = (lse_i - l[i, y_i]) / total for 0 <= y_i < vocab, else
+ * 0. With grad non-NULL also grad[i, j] = (softmax_ij - [j == y_i]) / total in
+ * the logits' dtype (row stride ldg); grad may alias the logits (in place).
+ * Replaces the fused Triton reductions of the frozen LM head
+ * (kernels/frozen_linear_cross_entropy.py:26-139, kernels/split_frozen_loss.py:56-89). */
+int molt_cross_entropy_rows(const void* logits, int32_t dtype, int64_t ld, int64_t rows, int64_t vocab,
+                            const int64_t* targets, float total, float* loss, void* grad, int64_t ldg,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

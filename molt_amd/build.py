@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OUT_DIR = PKG / "_lib"
 LIB = OUT_DIR / "libmolt_amd.so"
-SOURCES = ["capi.cpp", "codec.hip", "gemv.hip", "lora.hip", "nf4_gemm.hip", "rmsnorm.hip", "swiglu.hip"]
+SOURCES = ["capi.cpp", "ce.hip", "codec.hip", "gemv.hip", "lora.hip", "nf4_gemm.hip", "rmsnorm.hip", "swiglu.hip"]
 ARCH = "gfx950"
 
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]

@@ -1,0 +1,192 @@
+// Row-wise cross-entropy over a chunk of logits (gfx950): the fused reduction
+// of the frozen-head loss (kernels/frozen_linear_cross_entropy.py:26-139).
+//
+// For row i with target y (valid when 0 <= y < V):
+//   lse     = m + log(sum_j exp(l_j - m)),  m = max_j l_j       (fp32)
+//   loss_i  = valid ? (lse - l_y) / total : 0
+//   grad_ij = (exp(l_j - m) / d - [valid && j == y]) / total   (stored in the logits' dtype)
+// Invalid targets give a zero loss and a softmax gradient, as the reference's
+// fused kernel does (kernels/frozen_linear_cross_entropy.py:97-139).
+//
+// One workgroup owns a row. Pass 1 keeps a per-thread online (max, sum) and
+// combines them across the workgroup; pass 2 re-reads the row (from the
+// L2 / Infinity Cache: a row of Qwen's 151,936-entry vocabulary is 297 KB of
+// bf16) and writes the gradient, in place when `grad` aliases the logits:
+// every element is read by the thread that overwrites it, and the target
+// logit is read in pass 1.
+#include "common.h"
+
+namespace molt {
+namespace {
+
+constexpr int CE_NT = 1024;   // 16 waves per row: enough loads in flight for one workgroup per CU
+
+template <bool F32>
+MOLT_DEV float ce_ld(const void* p, int64_t i) {
+  if constexpr (F32) return reinterpret_cast<const float*>(p)[i];
+  else return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+
+template <bool F32>
+MOLT_DEV void ce_ld8(const void* p, int64_t i, float (&v)[8]) {
+  if constexpr (F32) {
+    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(reinterpret_cast<const float*>(p) + i);
+    const f32x4_t b = *reinterpret_cast<const f32x4_t*>(reinterpret_cast<const float*>(p) + i + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { v[e] = a[e]; v[4 + e] = b[e]; }
+  } else {
+    const u32x4_t q = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(p) + i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { v[2 * e] = bf16_lo(q[e]); v[2 * e + 1] = bf16_hi(q[e]); }
+  }
+}
+
+template <bool F32>
+MOLT_DEV void ce_st8(void* p, int64_t i, const float (&v)[8]) {
+  if constexpr (F32) {
+    f32x4_t a, b;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { a[e] = v[e]; b[e] = v[4 + e]; }
+    *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(p) + i) = a;
+    *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(p) + i + 4) = b;
+  } else {
+    u32x4_t q;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+    *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(p) + i) = q;
+  }
+}
+
+template <bool F32>
+MOLT_DEV void ce_st(void* p, int64_t i, float v) {
+  if constexpr (F32) reinterpret_cast<float*>(p)[i] = v;
+  else reinterpret_cast<uint16_t*>(p)[i] = bf16_bits(v);
+}
+
+// (m, d) online pair: d = sum exp(x - m); merging rescales the smaller max.
+MOLT_DEV void ce_merge(float& m, float& d, float m2, float d2) {
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;   // both empty
+  d = (d > 0.0f ? d * expf(m - mn) : 0.0f) + (d2 > 0.0f ? d2 * expf(m2 - mn) : 0.0f);
+  m = mn;
+}
+
+MOLT_DEV void ce_add(float& m, float& d, float x) {
+  if (x > m) {
+    d = (d > 0.0f ? d * expf(m - x) : 0.0f) + 1.0f;
+    m = x;
+  } else {
+    d += expf(x - m);
+  }
+}
+
+struct CeParams {
+  const void* logits; int64_t ld;
+  int64_t rows, V;
+  const int64_t* targets;
+  float total;
+  float* loss;
+  void* grad; int64_t ldg;
+};
+
+template <bool F32, bool VEC, bool GRAD>
+__global__ __launch_bounds__(CE_NT) void ce_kernel(const CeParams p) {
+  __shared__ float red_m[CE_NT / 64], red_d[CE_NT / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const void* lrow = F32 ? (const void*)(reinterpret_cast<const float*>(p.logits) + row * p.ld)
+                         : (const void*)(reinterpret_cast<const uint16_t*>(p.logits) + row * p.ld);
+  const int64_t y = p.targets[row];
+  const bool valid = y >= 0 && y < p.V;
+  const float ly = valid ? ce_ld<F32>(lrow, y) : 0.0f;
+
+  float m = -INFINITY, d = 0.0f;
+  if constexpr (VEC) {
+    for (int64_t i = 8 * (int64_t)tid; i < p.V; i += 8 * CE_NT) {
+      float v[8];
+      ce_ld8<F32>(lrow, i, v);
+      float bm = v[0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) bm = fmaxf(bm, v[e]);
+      float bs = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bs += expf(v[e] - bm);
+      ce_merge(m, d, bm, bs);
+    }
+  } else {
+    for (int64_t i = tid; i < p.V; i += CE_NT) ce_add(m, d, ce_ld<F32>(lrow, i));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float m2 = __shfl_xor(m, o, 64), d2 = __shfl_xor(d, o, 64);
+    ce_merge(m, d, m2, d2);
+  }
+  if (lane == 0) { red_m[wave] = m; red_d[wave] = d; }
+  __syncthreads();
+  m = red_m[0];
+  d = red_d[0];
+#pragma unroll
+  for (int w = 1; w < CE_NT / 64; ++w) ce_merge(m, d, red_m[w], red_d[w]);
+
+  if (tid == 0) p.loss[row] = valid ? (m + logf(d) - ly) / p.total : 0.0f;
+  if constexpr (GRAD) {
+    void* grow = F32 ? (void*)(reinterpret_cast<float*>(p.grad) + row * p.ldg)
+                     : (void*)(reinterpret_cast<uint16_t*>(p.grad) + row * p.ldg);
+    const float inv_d = 1.0f / d;
+    if constexpr (VEC) {
+      for (int64_t i = 8 * (int64_t)tid; i < p.V; i += 8 * CE_NT) {
+        float v[8];
+        ce_ld8<F32>(lrow, i, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float t = (valid && i + e == y) ? 1.0f : 0.0f;
+          v[e] = (expf(v[e] - m) * inv_d - t) / p.total;
+        }
+        ce_st8<F32>(grow, i, v);
+      }
+    } else {
+      for (int64_t i = tid; i < p.V; i += CE_NT) {
+        const float t = (valid && i == y) ? 1.0f : 0.0f;
+        ce_st<F32>(grow, i, (expf(ce_ld<F32>(lrow, i) - m) * inv_d - t) / p.total);
+      }
+    }
+  }
+}
+
+bool ce_a16(const void* q) { return ((uintptr_t)q & 15) == 0; }
+
+}  // namespace
+}  // namespace molt
+
+using namespace molt;
+
+extern "C" int molt_cross_entropy_rows(const void* logits, int32_t dtype, int64_t ld, int64_t rows, int64_t vocab,
+                                       const int64_t* targets, float total, float* loss, void* grad, int64_t ldg,
+                                       void* stream) {
+  const char* who = "molt_cross_entropy_rows";
+  MOLT_REQUIRE(dtype == MOLT_DTYPE_BF16 || dtype == MOLT_DTYPE_F32, MOLT_EINVAL, "%s: dtype must be bf16 or fp32",
+               who);
+  MOLT_REQUIRE(rows >= 0 && vocab > 0 && ld >= vocab && (!grad || ldg >= vocab), MOLT_EINVAL,
+               "%s: bad shape (rows=%lld vocab=%lld)", who, (long long)rows, (long long)vocab);
+  MOLT_REQUIRE(total > 0.0f, MOLT_EINVAL, "%s: total token count must be positive", who);
+  if (rows == 0) return MOLT_OK;
+  MOLT_REQUIRE(logits && targets && loss, MOLT_EINVAL, "%s: null pointer", who);
+  MOLT_REQUIRE(rows < (1ll << 31), MOLT_EINVAL, "%s: too many rows", who);
+  const bool f32 = dtype == MOLT_DTYPE_F32;
+  const int es = f32 ? 4 : 2;
+  const bool vec = vocab % 8 == 0 && ce_a16(logits) && (ld * es) % 16 == 0 &&
+                   (!grad || (ce_a16(grad) && (ldg * es) % 16 == 0));
+  CeParams p{logits, ld, rows, vocab, targets, total, loss, grad, ldg};
+  const dim3 grid((unsigned)rows), block(CE_NT);
+  hipStream_t st = (hipStream_t)stream;
+#define MOLT_CE_LAUNCH(F, V, G) hipLaunchKernelGGL((ce_kernel<F, V, G>), grid, block, 0, st, p)
+  if (grad) {
+    if (f32) { if (vec) MOLT_CE_LAUNCH(true, true, true); else MOLT_CE_LAUNCH(true, false, true); }
+    else { if (vec) MOLT_CE_LAUNCH(false, true, true); else MOLT_CE_LAUNCH(false, false, true); }
+  } else {
+    if (f32) { if (vec) MOLT_CE_LAUNCH(true, true, false); else MOLT_CE_LAUNCH(true, false, false); }
+    else { if (vec) MOLT_CE_LAUNCH(false, true, false); else MOLT_CE_LAUNCH(false, false, false); }
+  }
+#undef MOLT_CE_LAUNCH
+  return check_launch(who);
+}

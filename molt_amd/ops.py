@@ -64,18 +64,31 @@ def _custom_op(qualname: str, mutates_args=()):
     return deco
 
 
+def _plain(args) -> bool:
+    """True when every tensor argument is an ordinary tensor (not a fake,
+    functional or other subclass tensor of a tracing pass)."""
+    for a in args:
+        if isinstance(a, Tensor) and type(a) is not Tensor and type(a) is not torch.nn.Parameter:
+            return False
+    return True
+
+
 class _Direct:
     def __getattr__(self, name: str):
-        raw, op = _RAW[name], globals()[name]
+        raw, op = _RAW.get(name) or _late_raw(name), globals()[name]
 
         def call(*args, **kwargs):
-            if torch.compiler.is_compiling():
+            if torch.compiler.is_compiling() or not _plain(args):
                 return op(*args, **kwargs)
             return raw(*args, **kwargs)
 
         call.__name__ = name
         setattr(self, name, call)
         return call
+
+
+def _late_raw(name: str):
+    raise AttributeError(f"molt_amd.ops has no registered op {name!r}")
 
 
 direct = _Direct()
@@ -656,3 +669,32 @@ def rmsnorm_backward(grad: Tensor, x: Tensor, weight: Tensor, eps: float, offset
 @rmsnorm_backward.register_fake
 def _(grad, x, weight, eps, offset):
     return torch.empty_like(x)
+
+
+# --------------------------------------------------------------------------
+# Frozen-head cross-entropy (kernels/frozen_linear_cross_entropy.py:26-139)
+# --------------------------------------------------------------------------
+@_custom_op(f"{NS}::cross_entropy_rows", mutates_args=("logits",))
+def cross_entropy_rows(logits: Tensor, targets: Tensor, total: float, with_grad: bool) -> Tensor:
+    """Per-row loss ``(lse - l_y) / total`` (0 for targets outside [0, vocab));
+    with ``with_grad`` the logits are overwritten in place by
+    ``(softmax - onehot(y)) / total`` in their own dtype."""
+    dev = _require_gpu(logits, targets, what="cross-entropy")
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("cross-entropy: logits must be a row-major [rows, vocab] matrix")
+    if targets.dtype != torch.long or targets.shape != (logits.shape[0],):
+        raise ValueError("cross-entropy: targets must be int64 [rows]")
+    dt = _lib.DTYPE_BF16 if logits.dtype == torch.bfloat16 else _lib.DTYPE_F32
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise CapabilityError(f"cross-entropy supports bf16 and fp32 logits (got {logits.dtype})")
+    rows, vocab = logits.shape
+    loss = torch.empty(rows, device=dev, dtype=torch.float32)
+    tg = targets.contiguous()
+    _call("molt_cross_entropy_rows", logits.data_ptr(), dt, logits.stride(0), rows, vocab, tg.data_ptr(),
+          float(total), loss.data_ptr(), logits.data_ptr() if with_grad else None, logits.stride(0), _stream(dev))
+    return loss
+
+
+@cross_entropy_rows.register_fake
+def _(logits, targets, total, with_grad):
+    return logits.new_empty((logits.shape[0],), dtype=torch.float32)

@@ -40,6 +40,10 @@ Pinning (what independently checks each function; see ``tests/test_oracle.py``):
   central differences of the forward in fp64 and by its two invariants
   (zero gradient along x at eps = 0, and the closed form of the reference's
   own test, ``tests/kernels/test_frozen_rmsnorm.py:6-53``).
+* ``cross_entropy_rows`` - pinned against torch's ``F.cross_entropy`` and its
+  autograd gradient in fp64 for valid targets, by central differences of the
+  summed loss, and by the invariants of the invalid-target rows (zero loss,
+  a softmax gradient that sums to 1/total).
 """
 from __future__ import annotations
 
@@ -421,6 +425,29 @@ def rmsnorm_backward(x, w, eps, offset, dy):
     n = x * inv
     g = dy * (w + offset)
     return inv * (g - n * np.mean(g * n, axis=-1, keepdims=True))
+
+
+# --------------------------------------------------------------------------
+# Frozen-head cross-entropy (kernels/frozen_linear_cross_entropy.py:26-139)
+# --------------------------------------------------------------------------
+def cross_entropy_rows(logits, targets, total):
+    """Per-row loss ``(lse - l_y) / total`` and gradient
+    ``(softmax - onehot(y)) / total``; a target outside [0, vocab) gives a zero
+    loss and the plain softmax gradient, as the fused kernel's ``valid_target``
+    mask does (kernels/frozen_linear_cross_entropy.py:97-139). fp64."""
+    z = _f64(logits)
+    t = np.asarray(targets, dtype=np.int64)
+    m = z.max(axis=1, keepdims=True)
+    e = np.exp(z - m)
+    d = e.sum(axis=1, keepdims=True)
+    lse = (m + np.log(d))[:, 0]
+    valid = (t >= 0) & (t < z.shape[1])
+    rows = np.arange(z.shape[0])
+    ly = np.where(valid, z[rows, np.where(valid, t, 0)], 0.0)
+    loss = np.where(valid, (lse - ly) / total, 0.0)
+    grad = e / d
+    grad[rows[valid], t[valid]] -= 1.0
+    return loss, grad / total
 
 
 # --------------------------------------------------------------------------

@@ -310,3 +310,37 @@ def test_rmsnorm_oracle_matches_reference_test_algebra():
                                    ref.detach().numpy(), rtol=1e-13, atol=1e-13)
         np.testing.assert_allclose(O.rmsnorm_backward(x.detach().numpy(), w.numpy(), 1e-6, off, dy.numpy()),
                                    gx.numpy(), rtol=1e-12, atol=1e-12)
+
+
+# --------------------------------------------------------------- cross-entropy
+def test_cross_entropy_rows_matches_torch_and_differences():
+    from torch.nn import functional as F
+
+    rng = np.random.default_rng(8)
+    z = rng.standard_normal((6, 37)) * 3.0
+    t = rng.integers(0, 37, 6)
+    loss, grad = O.cross_entropy_rows(z, t, 6.0)
+    zt = torch.tensor(z, requires_grad=True)
+    ref = F.cross_entropy(zt, torch.tensor(t), reduction="mean")
+    (gref,) = torch.autograd.grad(ref, zt)
+    np.testing.assert_allclose(loss.sum(), ref.item(), rtol=1e-13)
+    np.testing.assert_allclose(grad, gref.numpy(), rtol=1e-12, atol=1e-15)
+    # central differences of the summed loss
+    h = 1e-6
+    for i, j in ((0, 0), (3, int(t[3])), (5, 36)):
+        zp, zm = z.copy(), z.copy()
+        zp[i, j] += h
+        zm[i, j] -= h
+        num = (O.cross_entropy_rows(zp, t, 6.0)[0].sum() - O.cross_entropy_rows(zm, t, 6.0)[0].sum()) / (2 * h)
+        np.testing.assert_allclose(grad[i, j], num, rtol=1e-6, atol=2e-9)
+
+
+def test_cross_entropy_rows_invalid_targets():
+    rng = np.random.default_rng(9)
+    z = rng.standard_normal((3, 10))
+    t = np.array([-100, 10, 4])
+    loss, grad = O.cross_entropy_rows(z, t, 3.0)
+    assert loss[0] == 0.0 and loss[1] == 0.0 and loss[2] > 0.0
+    np.testing.assert_allclose(grad[:2].sum(axis=1), 1.0 / 3.0, rtol=1e-14)
+    np.testing.assert_allclose(grad[2].sum(), 0.0, atol=1e-15)
+    assert np.all(grad[:2] > 0)
