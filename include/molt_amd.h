@@ -113,9 +113,10 @@ int molt_nf4_double_quantize(const float* absmax, int64_t n, int32_t dq_block,
  * Replaces the rank-r GEMMs F.linear(x, lora_a) (methods/nf4_lora.py:49) and
  * scaled_grad @ lora_b (methods/nf4_lora.py:89-90). The adapter is first
  * converted to bf16 into the caller's workspace (16-byte aligned, at least
- * molt_lora_project_workspace(D, r) bytes), so concurrent calls need
- * separate workspaces. */
-size_t molt_lora_project_workspace(int64_t D, int32_t r);
+ * molt_lora_project_workspace(M, D, r) bytes), which also holds the fp32
+ * partials when the contraction is split over workgroups (small M); concurrent
+ * calls need separate workspaces. */
+size_t molt_lora_project_workspace(int64_t M, int64_t D, int32_t r);
 int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t ldz, int32_t z_mode,
                       float z_scale, int64_t M, int64_t D, const float* lora,
                       int32_t lora_layout, int32_t r, uint16_t* out, int64_t ldo,

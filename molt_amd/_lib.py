@@ -49,7 +49,7 @@ SIGNATURES: dict[str, tuple] = {
     "molt_nf4_quantize": (C.c_int, [_p, _i32, _i64, _i32, _i32, _p, _p, _p, _p]),
     "molt_nf4_double_quantize_workspace": (_sz, [_i64]),
     "molt_nf4_double_quantize": (C.c_int, [_p, _i64, _i32, _p, _p, _p, _p, _p, _sz, _p]),
-    "molt_lora_project_workspace": (_sz, [_i64, _i32]),
+    "molt_lora_project_workspace": (_sz, [_i64, _i64, _i32]),
     "molt_lora_project": (C.c_int, [_p, _p, _i64, _i32, _f32, _i64, _i64, _p, _i32, _i32, _p, _i64, _p, _sz,
                                     _p]),
     "molt_nf4_lora_forward": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _f32, _p, _i64, _p]),

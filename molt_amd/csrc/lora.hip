@@ -113,6 +113,7 @@ struct ProjParams {
   int64_t M, D; int R;
   const uint16_t* wp;
   uint16_t* out; int64_t ldo;
+  float* part;          // K split: fp32 partials [ks][M][32 TQ]
 };
 
 template <int MT, bool VEC, bool REPLAY>
@@ -150,13 +151,19 @@ MOLT_DEV void proj_mfma(const Chunk (&z)[MT][4], const u32x4_t (&w)[TQ][4], cons
     }
 }
 
-template <int TQ, int MT, bool VEC, bool REPLAY>
+// With KS > 1 the 64-deep steps are split into KS contiguous ranges, one per
+// workgroup of blockIdx.y, and each writes its fp32 partial tile; a second
+// kernel sums the KS partials in range order and rounds to bf16 (more
+// workgroups in flight for small M, same result on every run).
+template <int TQ, int MT, bool VEC, bool REPLAY, int KS>
 __global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_kernel(const ProjParams p) {
   __shared__ f32x16_t red[PJ_WAVES - 1][64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t m0 = (int64_t)blockIdx.x * (32 * MT);
-  const int64_t steps = ceil_div64(p.D, BK);
+  const int64_t all_steps = ceil_div64(p.D, BK);
+  const int64_t s_begin = KS > 1 ? all_steps * blockIdx.y / KS : 0;
+  const int64_t steps = KS > 1 ? all_steps * (blockIdx.y + 1) / KS : all_steps;   // end of this range
 
   f32x16_t acc[MT][TQ];
 #pragma unroll
@@ -170,10 +177,10 @@ __global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_kernel(const ProjP
   // are issued a step ahead; the step's adapter fragments (L2 hits) are
   // issued just before them. Loads are never skipped (past the end they
   // repeat the last step), so the wait before each MFMA batch is a fixed count.
-  if (wave < steps) {
+  if (s_begin + wave < steps) {
     Chunk za[MT][4], zb[MT][4];
     u32x4_t w[TQ][4];
-    int64_t s = wave;
+    int64_t s = s_begin + wave;
     proj_load_z<MT, VEC, REPLAY>(za, p, s, m0, lane);
     for (;;) {
       proj_load_w<TQ>(w, p, s, lane);
@@ -207,12 +214,25 @@ __global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_kernel(const ProjP
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const int q = 32 * t + 8 * (e >> 2) + 4 * h + (e & 3);
-            if (q < p.R) p.out[m * p.ldo + q] = bf16_bits(v[e]);
+            if (KS > 1) p.part[((int64_t)blockIdx.y * p.M + m) * (32 * TQ) + q] = v[e];
+            else if (q < p.R) p.out[m * p.ldo + q] = bf16_bits(v[e]);
           }
         }
       }
       __syncthreads();
     }
+}
+
+__global__ void proj_reduce_kernel(const float* __restrict__ part, int ks, int64_t M, int R, int RP,
+                                   uint16_t* __restrict__ out, int64_t ldo) {
+  const int64_t n = M * R;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = i / R;
+    const int q = (int)(i - m * R);
+    float v = part[m * RP + q];
+    for (int k = 1; k < ks; ++k) v += part[((int64_t)k * M + m) * RP + q];
+    out[m * ldo + q] = bf16_bits(v);
+  }
 }
 
 // ------------------------------------------------------------------------
@@ -369,9 +389,30 @@ int64_t proj_tq(int r) { return (r + 31) / 32; }
 
 using namespace molt;
 
-extern "C" size_t molt_lora_project_workspace(int64_t D, int32_t r) {
-  if (D <= 0 || r <= 0) return 0;
+// Row tiles per workgroup: two 32-row tiles halve the L2 reads of the packed
+// adapter (ranks <= 64 only: larger accumulator sets would not fit in
+// registers). K split: the steps are split two or four ways (at least 16
+// steps per range) until there is a workgroup for every CU.
+int proj_mt(int64_t M, int tq, bool vec, int z_mode) {
+  return (vec && z_mode != 1 && M >= 64 * 64 && tq <= 2) ? 2 : 1;
+}
+
+int proj_ksplit(int64_t M, int64_t D, int mt) {
+  const int64_t tiles = ceil_div64(M, 32 * mt), steps = ceil_div64(D, BK);
+  int ks = 1;
+  while (ks < 4 && tiles * ks < 256 && steps / (2 * ks) >= 16) ks *= 2;
+  return ks;
+}
+
+size_t proj_packed_bytes(int64_t D, int32_t r) {
   return (size_t)ceil_div64(D, BK) * (size_t)proj_tq(r) * 4 * 64 * 8 * sizeof(uint16_t);
+}
+
+extern "C" size_t molt_lora_project_workspace(int64_t M, int64_t D, int32_t r) {
+  if (D <= 0 || r <= 0 || M < 0) return 0;
+  const int ks = proj_ksplit(M, D, proj_mt(M, (int)proj_tq(r), true, 0));
+  const size_t part = ks > 1 ? (size_t)ks * (size_t)M * (size_t)(32 * proj_tq(r)) * sizeof(float) : 0;
+  return proj_packed_bytes(D, r) + part;
 }
 
 extern "C" int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t ldz, int32_t z_mode, float z_scale,
@@ -387,7 +428,7 @@ extern "C" int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t 
   if (M == 0) return MOLT_OK;
   MOLT_REQUIRE(z && lora && out && ldz >= D && ldo >= r, MOLT_EINVAL, "%s: bad pointers/strides", who);
   MOLT_REQUIRE(z_mode != 1 || z2, MOLT_EINVAL, "%s: SwiGLU replay needs the up tensor", who);
-  const size_t need = molt_lora_project_workspace(D, r);
+  const size_t need = molt_lora_project_workspace(M, D, r);
   MOLT_REQUIRE(workspace && workspace_bytes >= need && aligned(workspace, 16), MOLT_EWORKSPACE,
                "%s: workspace %zu < %zu bytes (or not 16-byte aligned)", who, workspace_bytes, need);
   hipStream_t st = (hipStream_t)stream;
@@ -403,13 +444,19 @@ extern "C" int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t 
   ProjParams p{};
   p.z = z; p.z2 = z2; p.ldz = ldz; p.mode = z_mode; p.zs = z_scale;
   p.M = M; p.D = D; p.R = r; p.wp = wp; p.out = out; p.ldo = ldo;
+  p.part = (float*)((char*)workspace + proj_packed_bytes(D, r));
   const bool vec = D % 8 == 0 && ldz % 8 == 0 && aligned(z, 16) && (z_mode != 1 || aligned(z2, 16));
-  // Two 32-row tiles per workgroup halve the L2 reads of the packed adapter,
-  // once that still leaves a workgroup for every CU (ranks <= 64 only: the
-  // larger accumulator sets would not fit in registers).
-  const int mt = (vec && z_mode != 1 && M >= 64 * 256 && tq <= 2) ? 2 : 1;
-  dim3 grid((unsigned)ceil_div64(M, 32 * mt)), block(64 * PJ_WAVES);
-#define MOLT_PJ(TQ, MT, VEC, REPLAY) hipLaunchKernelGGL((lora_project_kernel<TQ, MT, VEC, REPLAY>), grid, block, 0, st, p)
+  const int mt = proj_mt(M, tq, vec, z_mode);
+  const int ks = vec ? proj_ksplit(M, D, mt) : 1;
+  dim3 grid((unsigned)ceil_div64(M, 32 * mt), (unsigned)ks), block(64 * PJ_WAVES);
+#define MOLT_PJK(TQ, MT, VEC, REPLAY, KS) \
+  hipLaunchKernelGGL((lora_project_kernel<TQ, MT, VEC, REPLAY, KS>), grid, block, 0, st, p)
+#define MOLT_PJ(TQ, MT, VEC, REPLAY)                        \
+  do {                                                      \
+    if (ks == 4) MOLT_PJK(TQ, MT, VEC, REPLAY, 4);          \
+    else if (ks == 2) MOLT_PJK(TQ, MT, VEC, REPLAY, 2);     \
+    else MOLT_PJK(TQ, MT, VEC, REPLAY, 1);                  \
+  } while (0)
   if (!vec) {
     switch (tq) {
       case 1: MOLT_PJ(1, 1, false, false); break;
@@ -435,6 +482,14 @@ extern "C" int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t 
     }
   }
 #undef MOLT_PJ
+#undef MOLT_PJK
+  if (ks > 1) {
+    rc = check_launch(who);
+    if (rc) return rc;
+    int64_t rb = ceil_div64(M * r, 256);
+    if (rb > 4096) rb = 4096;
+    hipLaunchKernelGGL(proj_reduce_kernel, dim3((unsigned)rb), dim3(256), 0, st, p.part, ks, M, r, 32 * tq, out, ldo);
+  }
   return check_launch(who);
 }
 

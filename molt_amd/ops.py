@@ -308,7 +308,7 @@ def lora_project(z: Tensor, z2: Optional[Tensor], mode: int, zscale: float, lora
     if (lw.shape[1] if layout == 0 else lw.shape[0]) != d:
         raise ValueError(f"{what}: adapter width {tuple(lw.shape)} does not match activation width {d}")
     out = torch.empty((m, r), device=dev, dtype=torch.bfloat16)
-    ws_bytes = int(_lib.load().molt_lora_project_workspace(d, r))
+    ws_bytes = int(_lib.load().molt_lora_project_workspace(m, d, r))
     ws = torch.empty(max(ws_bytes, 16), device=dev, dtype=torch.uint8)
     _call("molt_lora_project", z.data_ptr(), _ptr(z2), d, mode, zscale, m, d, lw.data_ptr(), layout, r,
           out.data_ptr(), r, ws.data_ptr(), ws_bytes, _stream(dev))
