@@ -1,6 +1,8 @@
 // Rank-r LoRA kernels (gfx950): the low-rank projection T = z . bf16(W)^T and
 // the adapter gradients dA = U^T X, dB = s dY^T T. Both stream one large
 // [M, D] activation from HBM once; the rank-r side is small and L2-resident.
+#include <stdlib.h>
+
 #include "mfma_core.h"
 
 namespace molt {
@@ -209,6 +211,135 @@ __global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_kernel(const ProjP
 #pragma unroll
         for (int w = 0; w < PJ_WAVES - 1; ++w) v += red[w][lane];
         // v is C[q][m]: column m = lane % 32, rows q = 32 t + 8 (e/4) + 4 h + e%4.
+        const int64_t m = m0 + 32 * i + (lane & 31);
+        if (m < p.M) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int q = 32 * t + 8 * (e >> 2) + 4 * h + (e & 3);
+            if (KS > 1) p.part[((int64_t)blockIdx.y * p.M + m) * (32 * TQ) + q] = v[e];
+            else if (q < p.R) p.out[m * p.ldo + q] = bf16_bits(v[e]);
+          }
+        }
+      }
+      __syncthreads();
+    }
+}
+
+// DMA-staged variant (plain or pre-scaled z, rows 16-byte aligned, D % 64 ==
+// 0): each wave streams its steps of z through a private pair of LDS buffers
+// by buffer-load DMA. DMA instruction c of a step loads rows 8c .. 8c + 7 with
+// 8 lanes per row, so every load covers whole 128-byte lines (the direct
+// fragment loads touch 32 rows per instruction, 32 bytes of each line); the
+// MFMA fragments are then read back with ds_read_b128. Chunk j of row r sits
+// at position j ^ f(r), f(r) = (r ^ (r >> 3)) & 7 restricted as below, which
+// keeps the 16-row fragment reads free of bank conflicts.
+MOLT_DEV int pj_swz(int r) { return (r ^ ((r >> 3) & 3)) & 7; }
+
+typedef __attribute__((address_space(3))) void* pj_lds_t;
+
+MOLT_DEV __amdgpu_buffer_rsrc_t pj_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+MOLT_DEV void pj_dma16(__amdgpu_buffer_rsrc_t r, uint16_t* dst, uint32_t off, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (pj_lds_t)dst, 16, off, soff, 0, 0);
+}
+
+// Wait until at most n vector-memory ops are outstanding (n = 4 or 8), with
+// compiler barriers so no LDS read moves above the wait.
+MOLT_DEV void pj_wait_vm(int n) {
+  asm volatile("" ::: "memory");
+  if (n == 8) __builtin_amdgcn_s_waitcnt(0x0F78);
+  else if (n == 4) __builtin_amdgcn_s_waitcnt(0x0F74);
+  else __builtin_amdgcn_s_waitcnt(0x0F70);
+  asm volatile("" ::: "memory");
+}
+
+template <int TQ, int MT, int KS>
+__global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_dma_kernel(const ProjParams p) {
+  __shared__ f32x16_t red[PJ_WAVES - 1][64];
+  __shared__ __attribute__((aligned(16))) uint16_t zs[PJ_WAVES][2][32 * MT * BK];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5;
+  const int64_t m0 = (int64_t)blockIdx.x * (32 * MT);
+  const int64_t all_steps = p.D / BK;
+  const int64_t s_begin = KS > 1 ? all_steps * blockIdx.y / KS : 0;
+  const int64_t s_end = KS > 1 ? all_steps * (blockIdx.y + 1) / KS : all_steps;
+
+  f32x16_t acc[MT][TQ];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int t = 0; t < TQ; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][t][e] = 0.0f;
+
+  if (s_begin + wave < s_end) {
+    const __amdgpu_buffer_rsrc_t zr = pj_rsrc(p.z, ((p.M - 1) * p.ldz + p.D) * 2);
+    uint32_t zoff[4 * MT];
+#pragma unroll
+    for (int c = 0; c < 4 * MT; ++c) {
+      const int r = 8 * c + (lane >> 3);
+      const int64_t m = min(m0 + r, p.M - 1);
+      zoff[c] = (uint32_t)((m * p.ldz + 8 * ((lane & 7) ^ pj_swz(r))) * 2);
+    }
+    int foff[MT][4];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int r = 32 * i + (lane & 31);
+        foff[i][kk] = r * BK + (((4 * h + kk) ^ pj_swz(r)) << 3);
+      }
+    auto dma = [&](int64_t s, uint16_t* dst) {
+#pragma unroll
+      for (int c = 0; c < 4 * MT; ++c) pj_dma16(zr, dst + c * 512, zoff[c], (uint32_t)(s * BK * 2));
+    };
+    u32x4_t w[TQ][4];
+    int64_t s = s_begin + wave;
+    int b = 0;
+    dma(s, zs[wave][0]);
+    for (;;) {
+      proj_load_w<TQ>(w, p, s, lane);
+      const int64_t sn = s + PJ_WAVES < s_end ? s + PJ_WAVES : s_end - 1;
+      dma(sn, zs[wave][b ^ 1]);
+      // this step's DMA (issued before the adapter loads) has landed; the next one may fly
+      pj_wait_vm(4 * MT);
+      const uint16_t* zc = zs[wave][b];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          u32x4_t zv = *reinterpret_cast<const u32x4_t*>(zc + foff[i][kk]);
+          if (p.mode == 2) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              zv[e] = pack_bf16x2(bf16_lo(zv[e]) * p.zs, bf16_hi(zv[e]) * p.zs);
+          }
+          const bf16x8_t zb = __builtin_bit_cast(bf16x8_t, zv);
+#pragma unroll
+          for (int t = 0; t < TQ; ++t)
+            acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, w[t][kk]), zb,
+                                                                acc[i][t], 0, 0, 0);
+        }
+      s += PJ_WAVES;
+      if (s >= s_end) break;
+      b ^= 1;
+    }
+    pj_wait_vm(0);   // the last (repeated) DMA before the kernel ends
+  }
+
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int t = 0; t < TQ; ++t) {
+      if (wave > 0) red[wave - 1][lane] = acc[i][t];
+      __syncthreads();
+      if (wave == 0) {
+        f32x16_t v = acc[i][t];
+#pragma unroll
+        for (int w2 = 0; w2 < PJ_WAVES - 1; ++w2) v += red[w2][lane];
         const int64_t m = m0 + 32 * i + (lane & 31);
         if (m < p.M) {
 #pragma unroll
@@ -457,7 +588,23 @@ extern "C" int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t 
     else if (ks == 2) MOLT_PJK(TQ, MT, VEC, REPLAY, 2);     \
     else MOLT_PJK(TQ, MT, VEC, REPLAY, 1);                  \
   } while (0)
-  if (!vec) {
+  const bool dma = vec && z_mode != 1 && D % BK == 0 && getenv("MOLT_AMD_PJ_NODMA") == nullptr;
+#define MOLT_PJD(TQ, MT)                                                                                       \
+  do {                                                                                                         \
+    if (ks == 4) hipLaunchKernelGGL((lora_project_dma_kernel<TQ, MT, 4>), grid, block, 0, st, p);               \
+    else if (ks == 2) hipLaunchKernelGGL((lora_project_dma_kernel<TQ, MT, 2>), grid, block, 0, st, p);          \
+    else hipLaunchKernelGGL((lora_project_dma_kernel<TQ, MT, 1>), grid, block, 0, st, p);                       \
+  } while (0)
+  if (dma) {
+    switch (tq * 2 + mt - 1) {
+      case 2: MOLT_PJD(1, 1); break;
+      case 3: MOLT_PJD(1, 2); break;
+      case 4: MOLT_PJD(2, 1); break;
+      case 5: MOLT_PJD(2, 2); break;
+      case 6: MOLT_PJD(3, 1); break;
+      default: MOLT_PJD(4, 1); break;
+    }
+  } else if (!vec) {
     switch (tq) {
       case 1: MOLT_PJ(1, 1, false, false); break;
       case 2: MOLT_PJ(2, 1, false, false); break;
@@ -483,6 +630,7 @@ extern "C" int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t 
   }
 #undef MOLT_PJ
 #undef MOLT_PJK
+#undef MOLT_PJD
   if (ks > 1) {
     rc = check_launch(who);
     if (rc) return rc;
