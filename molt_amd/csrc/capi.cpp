@@ -83,6 +83,7 @@ int molt_nf4_swiglu_backward(const uint16_t* dy, int64_t lddy, int64_t M, const 
                              const uint16_t* u, int64_t ldu, const float* lora_a, int32_t r, const uint16_t* gate,
                              const uint16_t* up, int64_t ldg, uint16_t* dgate, uint16_t* dup, void* stream) {
   if (!wd) return molt::set_error(MOLT_EINVAL, "molt_nf4_swiglu_backward: null weight");
+  if (M == 0) return MOLT_OK;   // an empty token batch: the outputs are empty too (their pointers may be null)
   if (!dgate) return molt::set_error(MOLT_EINVAL, "molt_nf4_swiglu_backward: null dgate");
   return molt_nf4_lora_backward_impl(dy, nullptr, lddy, M, wd, nullptr, u, nullptr, ldu, lora_a, nullptr, wd->cols,
                                      r, 1.0f, nullptr, 0, gate, up, dgate, dup, ldg, (hipStream_t)stream);

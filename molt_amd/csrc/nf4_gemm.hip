@@ -554,6 +554,17 @@ MOLT_DEV void buf_load_lds16(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t off, 
 // vmcnt(0) with the other counters untouched.
 MOLT_DEV void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// The end of a step waits with a partial vmcnt that counts the register loads
+// of the next-but-one step as the only ones allowed to stay in flight; that
+// holds only if every DMA of the step is issued before them. vmcnt counts in
+// issue order, so the scheduler must not move a register load above a DMA
+// (it did: two X DMA blocks then landed after the barrier, and other waves
+// read stale LDS rows). Compiler and scheduling barrier between the two groups.
+MOLT_DEV void dma_then_loads() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // Workgroup barrier without __syncthreads()'s release fence: the fence makes
 // the compiler drain every outstanding vector-memory op, including register
 // loads of packed weight bytes that are only used a step later. The caller
@@ -901,6 +912,7 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
     load_frags(wc, xc, fo, 0, a[0], b[0]);
     mfma_set(a[1], b[1], acc);
     x_load(xn, k1);
+    dma_then_loads();
     w_load(nw, k2);
     w_lookup(cw, tabc, 0, c);
     __builtin_amdgcn_sched_barrier(0);
@@ -1237,6 +1249,7 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
     load_frags(wc, xc, fo, 0, a[0], b[0]);
     mfma_set(a[1], b[1], acc);
     x_load(xn, s + 1);
+    dma_then_loads();
     w_load(nw, s + 2);
     wp_lookup(cw, tabc, 0, c);
     __builtin_amdgcn_sched_barrier(0);
@@ -1356,12 +1369,12 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
     if (rc) return rc;
     MOLT_REQUIRE(same_format(w0, w1), MOLT_EINVAL, "%s: gate and up weights must share shape and format", who);
   }
-  MOLT_REQUIRE(x && M >= 0 && ldx >= w0->cols, MOLT_EINVAL, "%s: bad X", who);
-  MOLT_REQUIRE(y0 && ldy >= w0->rows, MOLT_EINVAL, "%s: bad Y", who);
-  MOLT_REQUIRE(!pair || (y1 && y2), MOLT_EINVAL, "%s: pair needs g, u and h outputs", who);
-  MOLT_REQUIRE(lr == 0 || (t && ldt >= lr && b0 && (!pair || b1) && r > 0 && ldb >= r), MOLT_EINVAL,
+  MOLT_REQUIRE(M >= 0 && ldx >= w0->cols, MOLT_EINVAL, "%s: bad X", who);
+  MOLT_REQUIRE(ldy >= w0->rows, MOLT_EINVAL, "%s: bad Y", who);
+  MOLT_REQUIRE(lr == 0 || (ldt >= lr && b0 && (!pair || b1) && r > 0 && ldb >= r), MOLT_EINVAL,
                "%s: bad LoRA operands", who);
-  if (M == 0) return MOLT_OK;
+  if (M == 0) return MOLT_OK;   // an empty token batch: no pointers are read (they may be null)
+  MOLT_REQUIRE(x && y0 && (!pair || (y1 && y2)) && (lr == 0 || t), MOLT_EINVAL, "%s: null X, Y or T", who);
 
   FwdParams p{};
   p.x = x; p.ldx = ldx; p.M = M; p.K = w0->cols;
@@ -1418,18 +1431,20 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
     rc = check_weight_for_gemm(w1, who);
     if (rc) return rc;
     MOLT_REQUIRE(same_format(w0, w1), MOLT_EINVAL, "%s: paired weights must share shape and format", who);
-    MOLT_REQUIRE(dy1, MOLT_EINVAL, "%s: second gradient missing", who);
   }
   const bool swiglu = dg != nullptr;
-  MOLT_REQUIRE(dy0 && M >= 0 && lddy >= w0->rows, MOLT_EINVAL, "%s: bad dY", who);
-  MOLT_REQUIRE(r == 0 || (u0 && ldu >= r && a0 && lda >= w0->cols && (nseg == 1 || (u1 && a1))),
-               MOLT_EINVAL, "%s: bad LoRA operands", who);
+  MOLT_REQUIRE(M >= 0 && lddy >= w0->rows, MOLT_EINVAL, "%s: bad dY", who);
+  MOLT_REQUIRE(r == 0 || (ldu >= r && a0 && lda >= w0->cols && (nseg == 1 || a1)), MOLT_EINVAL,
+               "%s: bad LoRA operands", who);
   if (swiglu) {
-    MOLT_REQUIRE(gate && up && du && ldg >= w0->cols && nseg == 1, MOLT_EINVAL, "%s: bad SwiGLU operands", who);
+    MOLT_REQUIRE(ldg >= w0->cols && nseg == 1, MOLT_EINVAL, "%s: bad SwiGLU operands", who);
   } else {
-    MOLT_REQUIRE(dx && lddx >= w0->cols, MOLT_EINVAL, "%s: bad dX", who);
+    MOLT_REQUIRE(lddx >= w0->cols, MOLT_EINVAL, "%s: bad dX", who);
   }
-  if (M == 0) return MOLT_OK;
+  if (M == 0) return MOLT_OK;   // an empty token batch: no pointers are read (they may be null)
+  MOLT_REQUIRE(dy0 && (nseg == 1 || dy1), MOLT_EINVAL, "%s: null gradient", who);
+  MOLT_REQUIRE(r == 0 || (u0 && (nseg == 1 || u1)), MOLT_EINVAL, "%s: null LoRA gradient", who);
+  MOLT_REQUIRE(swiglu ? (gate && up && du) : dx != nullptr, MOLT_EINVAL, "%s: null output", who);
 
   BwdParams p{};
   p.dy[0] = dy0; p.dy[1] = w1 ? dy1 : dy0; p.lddy = lddy; p.M = M;
