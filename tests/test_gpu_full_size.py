@@ -79,3 +79,32 @@ def test_empty_token_batches():
     with torch.autocast("cuda", dtype=torch.bfloat16):
         z = scheduled_nf4_lora(x, pg, ag, bg, qg, s)
     assert z.shape == (0, 256)
+
+
+@pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)])
+def test_cfg5_gemv_full_shapes_repeat_bitwise_and_match_oracle(n, k):
+    """Every cfg5 decode shape at M in {1, 2, 16} with the r = 16 LoRA add-on:
+    repeated calls are bitwise equal, and a sample of outputs matches the oracle."""
+    from molt_amd import ops
+
+    print(f"cfg5 gemv N={n} K={k}", flush=True)
+    w = seeded((n, k), 500 + n + k, std=0.02, dtype=torch.float32)
+    packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True)
+    del w
+    s2 = qs.state2
+    a = uniform((16, k), 501, 1.0 / np.sqrt(k))
+    b = seeded((n, 16), 502, std=0.01, dtype=torch.float32)
+    ow = oracle_weight(packed, qs).dequant_f32().astype(np.float64)
+    for m in (1, 2, 16):
+        x = seeded((m, k), 503 + m)
+        t = ops.lora_project(x, None, 0, 1.0, a, 0)
+
+        def run():
+            return ops.nf4_gemv(x, packed.reshape(-1), None, qs.absmax, s2.absmax, s2.code, float(qs.offset),
+                                int(s2.blocksize), qs.code, n, k, 1, t, b, 2.0)
+
+        y1, y2 = run(), run()
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2), f"M={m}: repeated GEMV calls differ"
+        ref = bf16_values(x) @ ow.T + 2.0 * (bf16_values(t) @ bf16_values(b).T)
+        assert_close_fro(np_f32(y1), ref, what=f"GEMV M={m}")
