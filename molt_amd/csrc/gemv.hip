@@ -24,6 +24,8 @@
 
 #include "common.h"
 
+#include <stdlib.h>
+
 namespace molt {
 namespace {
 
@@ -285,7 +287,7 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(4))) void
 
 
 // ---------------------------------------------------------------------------
-// Streaming dot-product variant for M == 1 (decode). Each wave walks rows of W
+// Streaming dot-product variant for M <= 4 (decode). Each wave walks rows of W
 // in rounds: round j covers RW rows at j * (grid waves * RW) + (this wave's
 // index) * RW, so every round of the grid reads a contiguous band of W. A
 // lane reads 16 contiguous packed bytes (32 elements, half a block) of each
@@ -296,7 +298,9 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(4))) void
 // the replicated LDS table of bf16 code pairs and meet X (staged once per
 // workgroup in LDS) through v_dot2_f32_bf16; the block scale multiplies each
 // lane's half-block sum, lane j < r adds T[j] bf16(s B[n, j]), and the 64
-// lanes of a row are summed by butterfly shuffles. Requires K % 2048 == 0.
+// lanes of a row are summed by butterfly shuffles. MX rows of X (the tokens,
+// M <= MX; rows past M repeat row M - 1 and are not stored) share each code
+// lookup, one dot2 per token. Requires K % 2048 == 0.
 constexpr int GD_WAVES = 8;
 constexpr int GD_NT = 64 * GD_WAVES;
 constexpr int GD_XPAD = 8;                // bf16 elements of X row padding
@@ -343,62 +347,88 @@ MOLT_DEV void gd_load(GdRound<RW, IPR>& R, const GemvParams& p, int64_t n0, int 
   }
 }
 
-// Dot products of one round and the stores of its rows.
-template <int RW, int IPR>
+// Dot products of one round and the stores of its rows. X row m sits at
+// xs + m * xstride (elements).
+template <int RW, int IPR, int MX>
 MOLT_DEV void gd_compute(const GdRound<RW, IPR>& R, const GemvParams& p, const uint32_t* tab, const uint16_t* xs,
-                         const float* code2s, const float (&lt)[2], int64_t n0, int lane) {
-  float acc[RW];
+                         int xstride, const float* code2s, const float (&lt)[MX][2], int64_t n0, int lane) {
+  float acc[RW][MX];
 #pragma unroll
-  for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int m = 0; m < MX; ++m) acc[r][m] = 0.0f;
 #pragma unroll
   for (int i = 0; i < IPR; ++i) {                                      // piece i of every row: X read once
-    float bs[RW];
+    float bs[RW][MX];
 #pragma unroll
-    for (int r = 0; r < RW; ++r) bs[r] = 0.0f;
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int m = 0; m < MX; ++m) bs[r][m] = 0.0f;
 #pragma unroll
     for (int h = 0; h < 4; ++h) {                                      // 4 bytes per dword, 8 elements
-      const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xs + 8 * (256 * i + 64 * h + lane));
+      u32x4_t xv[MX];
+#pragma unroll
+      for (int m = 0; m < MX; ++m)
+        xv[m] = *reinterpret_cast<const u32x4_t*>(xs + m * xstride + 8 * (256 * i + 64 * h + lane));
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        // copy the element out first: __builtin_bit_cast of a vector-element
-        // lvalue reads element 0 with this compiler
-        const uint32_t xw = xv[b];
 #pragma unroll
         for (int r = 0; r < RW; ++r) {
           const uint32_t pair = tab[((R.w[r * IPR + i][h] >> (8 * b)) & 0xffu) * GV_TABW];
-          bs[r] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, pair), __builtin_bit_cast(bf16x2v, xw),
-                                                  bs[r], false);
+#pragma unroll
+          for (int m = 0; m < MX; ++m) {
+            // copy the element out first: __builtin_bit_cast of a vector-element
+            // lvalue reads element 0 with this compiler
+            const uint32_t xw = xv[m][b];
+            bs[r][m] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, pair),
+                                                       __builtin_bit_cast(bf16x2v, xw), bs[r][m], false);
+          }
         }
       }
     }
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
-      acc[r] += gv_scale(p, code2s, R.q[r * IPR + i], R.s[r * IPR + i]) * bs[r];
-      asm volatile("" : "+v"(acc[r]));                                // keeps each piece's lookups short-lived
+      const float sc = gv_scale(p, code2s, R.q[r * IPR + i], R.s[r * IPR + i]);
+#pragma unroll
+      for (int m = 0; m < MX; ++m) {
+        acc[r][m] += sc * bs[r][m];
+        asm volatile("" : "+v"(acc[r][m]));                           // keeps each piece's lookups short-lived
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
   }
-  // LoRA partials join the row sums; butterfly sum over the wave; lane r stores row r
+  // LoRA partials join the row sums; butterfly sum over the wave; lane
+  // r * MX + m stores row r of token m
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
-    float v = acc[r] + (lt[0] * round_bf16(p.s * R.lb[r][0]) + lt[1] * round_bf16(p.s * R.lb[r][1]));
+    const float b0 = round_bf16(p.s * R.lb[r][0]), b1 = round_bf16(p.s * R.lb[r][1]);
 #pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) v += __shfl_xor(v, sh);
-    acc[r] = v;
+    for (int m = 0; m < MX; ++m) {
+      float v = acc[r][m] + (lt[m][0] * b0 + lt[m][1] * b1);
+#pragma unroll
+      for (int sh = 32; sh >= 1; sh >>= 1) v += __shfl_xor(v, sh);
+      acc[r][m] = v;
+    }
   }
-  if (lane < RW) {
-    float v = acc[0];
+  if (lane < RW * MX) {
+    float v = acc[0][0];
 #pragma unroll
-    for (int r = 1; r < RW; ++r) v = lane == r ? acc[r] : v;
-    const int64_t n = n0 + lane;
-    if (n < p.N) p.y[n] = bf16_bits(v);
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int m = 0; m < MX; ++m) v = lane == r * MX + m ? acc[r][m] : v;
+    const int rr = lane / MX, m = lane % MX;
+    const int64_t n = n0 + rr;
+    if (n < p.N && m < p.M) p.y[(int64_t)m * p.ldy + n] = bf16_bits(v);
   }
 }
 
-template <int RW, int IPR>
-__global__ __launch_bounds__(GD_NT) void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
+// At K = 4096 with up to two X rows the kernel is held to 128 registers, so two
+// workgroups fit on a CU.
+template <int RW, int IPR, int MX>
+__global__ __launch_bounds__(GD_NT) __attribute__((amdgpu_waves_per_eu(IPR == 2 && MX <= 2 ? 4 : 1)))
+void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
   __shared__ GdSmem sm;
-  extern __shared__ __attribute__((aligned(16))) uint16_t gd_xs[];      // X, K elements
+  extern __shared__ __attribute__((aligned(16))) uint16_t gd_xs[];      // X, MX rows of K + GD_XPAD elements
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t stride = (int64_t)gridDim.x * GD_WAVES * RW;          // rows per round of the grid
@@ -411,18 +441,24 @@ __global__ __launch_bounds__(GD_NT) void nf4_gemv_dot_kernel(const GemvParams p,
 
   // X first (16-byte chunks into registers), so that the wait before its LDS
   // stores, and the barrier after them, do not wait for the weight stream.
-  constexpr int XCH = IPR * 256, XIT = (XCH + GD_NT - 1) / GD_NT;    // 16-byte chunks of X
+  constexpr int XCH = IPR * 256, XIT = (MX * XCH + GD_NT - 1) / GD_NT;   // 16-byte chunks of X
+  const int xstride = p.K + GD_XPAD;
   u32x4_t xr[XIT];
 #pragma unroll
   for (int it = 0; it < XIT; ++it) {
-    const int c = tid + it * GD_NT < XCH ? tid + it * GD_NT : XCH - 1;
-    xr[it] = *reinterpret_cast<const u32x4_t*>(p.x + 8 * c);
+    const int c = tid + it * GD_NT < MX * XCH ? tid + it * GD_NT : MX * XCH - 1;
+    const int m = c / XCH < p.M ? c / XCH : p.M - 1;
+    xr[it] = *reinterpret_cast<const u32x4_t*>(p.x + m * p.ldx + 8 * (c % XCH));
   }
   const float c2 = p.code2 ? p.code2[tid & 255] : 0.0f;
-  float lt[2] = {0.0f, 0.0f};
+  float lt[MX][2];
 #pragma unroll
-  for (int q = 0; q < 2; ++q)
-    if (lane + 64 * q < p.r) lt[q] = bf16_to_f32(p.t[lane + 64 * q]);
+  for (int m = 0; m < MX; ++m) {
+    const int mm = m < p.M ? m : p.M - 1;
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      lt[m][q] = lane + 64 * q < p.r ? bf16_to_f32(p.t[mm * p.ldt + lane + 64 * q]) : 0.0f;
+  }
 
   GdRound<RW, IPR> b0, b1, b2;
   gd_load(b0, p, nb, lane, KB);
@@ -434,7 +470,10 @@ __global__ __launch_bounds__(GD_NT) void nf4_gemv_dot_kernel(const GemvParams p,
 #pragma unroll
   for (int it = 0; it < XIT; ++it) {
     const int c = tid + it * GD_NT;
-    if (c < XCH) *reinterpret_cast<u32x4_t*>(gd_xs + 8 * ((c & ~255) | ((c & 3) << 6) | ((c >> 2) & 63))) = xr[it];
+    const int m = c / XCH, cc = c % XCH;
+    if (c < MX * XCH)
+      *reinterpret_cast<u32x4_t*>(gd_xs + m * xstride + 8 * ((cc & ~255) | ((cc & 3) << 6) | ((cc >> 2) & 63))) =
+          xr[it];
   }
   {
     const float cv[16] = {cb0[0], cb0[1], cb0[2], cb0[3], cb1[0], cb1[1], cb1[2], cb1[3],
@@ -461,13 +500,13 @@ __global__ __launch_bounds__(GD_NT) void nf4_gemv_dot_kernel(const GemvParams p,
   const uint32_t* tab = sm.tab + (lane & 31);
   for (int j = 0; j < rounds; j += 3) {
     if (j + 2 < rounds) gd_load(b2, p, nb + (j + 2) * stride, lane, KB);
-    gd_compute(b0, p, tab, gd_xs, sm.code2s, lt, nb + j * stride, lane);
+    gd_compute(b0, p, tab, gd_xs, xstride, sm.code2s, lt, nb + j * stride, lane);
     if (j + 1 >= rounds) break;
     if (j + 3 < rounds) gd_load(b0, p, nb + (j + 3) * stride, lane, KB);
-    gd_compute(b1, p, tab, gd_xs, sm.code2s, lt, nb + (j + 1) * stride, lane);
+    gd_compute(b1, p, tab, gd_xs, xstride, sm.code2s, lt, nb + (j + 1) * stride, lane);
     if (j + 2 >= rounds) break;
     if (j + 4 < rounds) gd_load(b1, p, nb + (j + 4) * stride, lane, KB);
-    gd_compute(b2, p, tab, gd_xs, sm.code2s, lt, nb + (j + 2) * stride, lane);
+    gd_compute(b2, p, tab, gd_xs, xstride, sm.code2s, lt, nb + (j + 2) * stride, lane);
   }
 }
 
@@ -752,11 +791,20 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
   const int64_t groups = ceil_div64(p.N, GV_ROWS);
   MOLT_REQUIRE(groups < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
   hipStream_t st = (hipStream_t)stream;
-  // Decode (M == 1): streaming dot-product kernel, one row per wave per round,
-  // as many workgroups as fit on the GPU at once (two per CU at K = 4096, one at
-  // K = 14336, whose three rounds of 7 KB per wave need ~190 registers); the
-  // waves loop over the rounds.
-  if (M == 1 && (w->cols == 4096 || w->cols == 14336) && aligned(w->packed, 16)) {
+  // Decode: streaming dot-product kernel, one row per wave per round, as many
+  // workgroups as fit on the GPU at once (two per CU at K = 4096 with up to two
+  // tokens, else one; at K = 14336 three rounds of 7 KB per wave need ~190
+  // registers); the waves loop over the rounds. M = 2 runs with two X rows, 3
+  // and 4 with four. It serves M <= 2, and M = 3, 4 where it measured faster
+  // than the MFMA kernel (K = 14336, or at most 2048 rows); MOLT_AMD_GEMV_DOT_M
+  // (0..4) replaces that rule by a plain bound on M.
+  static const int dot_max_m = [] {
+    const char* e = getenv("MOLT_AMD_GEMV_DOT_M");
+    const int v = e ? atoi(e) : -1;
+    return v < -1 ? -1 : (v > 4 ? 4 : v);
+  }();
+  const bool dot_m = dot_max_m >= 0 ? M <= dot_max_m : (M <= 2 || (M <= 4 && (w->cols == 14336 || w->rows <= 2048)));
+  if (dot_m && (w->cols == 4096 || w->cols == 14336) && aligned(w->packed, 16)) {
     const int ipr = (int)(w->cols / 2048);
     static int cu_count[64];                                  // per device, filled on first use
     int dev = 0, cus = 256;
@@ -765,12 +813,21 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
       if (cu_count[dev] > 0) cus = cu_count[dev];
     }
     const int rw = 1;                                         // rows per wave per round
-    const int64_t waves = std::min<int64_t>(ceil_div64(w->rows, rw), (int64_t)cus * GD_WAVES * (ipr == 2 ? 2 : 1));
+    const int mx = M == 1 ? 1 : (M == 2 ? 2 : 4);             // X rows held by the kernel
+    // two workgroups per CU only where the kernel fits in 128 registers
+    const int per_cu = ipr == 2 && mx <= 2 ? 2 : 1;
+    const int64_t waves = std::min<int64_t>(ceil_div64(w->rows, rw), (int64_t)cus * GD_WAVES * per_cu);
     const int64_t wgs = ceil_div64(waves, GD_WAVES);
     const int rounds = (int)ceil_div64(w->rows, wgs * GD_WAVES * rw);
-    const size_t dyn = (size_t)(w->cols + GD_XPAD) * 2;
-    if (ipr == 2) hipLaunchKernelGGL((nf4_gemv_dot_kernel<1, 2>), dim3((unsigned)wgs), dim3(GD_NT), dyn, st, p, rounds);
-    else hipLaunchKernelGGL((nf4_gemv_dot_kernel<1, 7>), dim3((unsigned)wgs), dim3(GD_NT), dyn, st, p, rounds);
+    const size_t dyn = (size_t)mx * (w->cols + GD_XPAD) * 2;
+#define MOLT_GD(IPRv, MXv) \
+  hipLaunchKernelGGL((nf4_gemv_dot_kernel<1, IPRv, MXv>), dim3((unsigned)wgs), dim3(GD_NT), dyn, st, p, rounds)
+    if (ipr == 2) {
+      if (mx == 1) MOLT_GD(2, 1); else if (mx == 2) MOLT_GD(2, 2); else MOLT_GD(2, 4);
+    } else {
+      if (mx == 1) MOLT_GD(7, 1); else if (mx == 2) MOLT_GD(7, 2); else MOLT_GD(7, 4);
+    }
+#undef MOLT_GD
     return check_launch(who);
   }
   // 2 <= M <= 16, K of 8 (or a multiple of 7 or 8) 512-element chunks:

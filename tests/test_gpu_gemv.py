@@ -58,11 +58,14 @@ def test_gemv_with_lora_matches_oracle(m, n, r):
                                                  (1, 776, 14336, True, 1), (1, 264, 14336, False, 1),
                                                  (1, 4104, 14336, True, 0), (1, 2056, 4096, True, 1),
                                                  (1, 14344, 4096, True, 1), (3, 520, 4096, False, 0),
-                                                 (2, 776, 14336, True, 1), (4, 2056, 4096, True, 1)])
+                                                 (2, 776, 14336, True, 1), (4, 2056, 4096, True, 1),
+                                                 (2, 4104, 4096, False, 0), (3, 264, 14336, True, 0),
+                                                 (4, 4100, 14336, False, 1), (4, 2048, 4096, True, 1)])
 def test_gemv_decode_shapes_match_oracle(m, n, k, nested, order):
-    # K = 4096 / 14336 with M == 1 take the streaming dot-product decode kernel
-    # (every rows-per-wave choice of it); ragged row counts exercise its clamped
-    # loads and guarded stores. M = 2..4 cover the MFMA kernel at the same shapes.
+    # K = 4096 / 14336 take the streaming dot-product decode kernel at M <= 2,
+    # and at M = 3, 4 when K = 14336 or N <= 2048 (two or four X rows; M = 3
+    # repeats the last row and stores three); ragged row counts exercise its
+    # clamped loads and guarded stores. (4, 2056, 4096) covers the MFMA kernel.
     print(f"gemv decode m={m} n={n} k={k} nested={nested} order={order}", flush=True)
     w = seeded((n, k), 100 + n, std=0.02, dtype=torch.float32)
     packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=nested, nibble_order=order)
@@ -70,6 +73,25 @@ def test_gemv_decode_shapes_match_oracle(m, n, k, nested, order):
     y = _gemv(x, packed, qs, nested=nested)
     wo = oracle_weight(packed, qs).dequant_bf16().astype(np.float64)
     assert_close_fro(np_f32(y), bf16_values(x) @ wo.T, what="Y")
+
+
+@pytest.mark.parametrize("m,n,k,r", [(2, 1000, 14336, 16), (3, 4100, 14336, 128), (4, 776, 14336, 96),
+                                     (3, 1024, 4096, 64), (2, 4096, 4096, 16)])
+def test_gemv_decode_tokens_with_lora_match_oracle(m, n, k, r):
+    # Multi-token decode kernel with the LoRA add-on: every token row has its
+    # own T row; r = 128 fills both halves of the lanes' rank slots.
+    print(f"gemv decode lora m={m} n={n} k={k} r={r}", flush=True)
+    s = 2.0
+    w = seeded((n, k), 110 + m, std=0.02, dtype=torch.float32)
+    packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True)
+    x = seeded((m, k), 111 + r)
+    a = uniform((r, k), 112, 1.0 / np.sqrt(k))
+    b = seeded((n, r), 113, std=0.01, dtype=torch.float32)
+    t = ops.lora_project(x, None, 0, 1.0, a, 0)
+    y = _gemv(x, packed, qs, t, b, s)
+    wo = oracle_weight(packed, qs).dequant_bf16().astype(np.float64)
+    ref = O.lora_linear_forward(bf16_values(x), wo, bf16_values(a), bf16_values(b), s)
+    assert_close_fro(np_f32(y), ref, what="Y")
 
 
 @pytest.mark.parametrize("m,n", [(3, 1000), (16, 264)])
