@@ -348,10 +348,12 @@ MOLT_DEV void gd_load(GdRound<RW, IPR>& R, const GemvParams& p, int64_t n0, int 
 }
 
 // Dot products of one round and the stores of its rows. X row m sits at
-// xs + m * xstride (elements).
-template <int RW, int IPR, int MX>
+// xs + m * xstride (elements); with XREG (one token) the lane's X chunks are
+// xg[4 i + h] in registers instead.
+template <int RW, int IPR, int MX, bool XREG>
 MOLT_DEV void gd_compute(const GdRound<RW, IPR>& R, const GemvParams& p, const uint32_t* tab, const uint16_t* xs,
-                         int xstride, const float* code2s, const float (&lt)[MX][2], int64_t n0, int lane) {
+                         int xstride, const u32x4_t* xg, const float* code2s, const float (&lt)[MX][2], int64_t n0,
+                         int lane) {
   float acc[RW][MX];
 #pragma unroll
   for (int r = 0; r < RW; ++r)
@@ -369,7 +371,7 @@ MOLT_DEV void gd_compute(const GdRound<RW, IPR>& R, const GemvParams& p, const u
       u32x4_t xv[MX];
 #pragma unroll
       for (int m = 0; m < MX; ++m)
-        xv[m] = *reinterpret_cast<const u32x4_t*>(xs + m * xstride + 8 * (256 * i + 64 * h + lane));
+        xv[m] = XREG ? xg[4 * i + h] : *reinterpret_cast<const u32x4_t*>(xs + m * xstride + 8 * (256 * i + 64 * h + lane));
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
 #pragma unroll
@@ -441,9 +443,19 @@ void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
 
   // X first (16-byte chunks into registers), so that the wait before its LDS
   // stores, and the barrier after them, do not wait for the weight stream.
-  constexpr int XCH = IPR * 256, XIT = (MX * XCH + GD_NT - 1) / GD_NT;   // 16-byte chunks of X
+  // One token at K = 4096: the lane's 64 elements of X (16-byte chunks
+  // 256 i + 4 lane + h, the elements its weight bytes multiply) stay in
+  // registers, read straight from memory; otherwise X is staged in LDS.
+  constexpr bool XREG = IPR == 2 && MX == 1;
+  constexpr int XCH = IPR * 256, XIT = XREG ? 0 : (MX * XCH + GD_NT - 1) / GD_NT;   // 16-byte chunks of X
   const int xstride = p.K + GD_XPAD;
-  u32x4_t xr[XIT];
+  u32x4_t xr[XIT > 0 ? XIT : 1];
+  u32x4_t xg[XREG ? 4 * IPR : 1];
+  if constexpr (XREG) {
+#pragma unroll
+    for (int c = 0; c < 4 * IPR; ++c)
+      xg[c] = *reinterpret_cast<const u32x4_t*>(p.x + 8 * (256 * (c >> 2) + 4 * lane + (c & 3)));
+  }
 #pragma unroll
   for (int it = 0; it < XIT; ++it) {
     const int c = tid + it * GD_NT < MX * XCH ? tid + it * GD_NT : MX * XCH - 1;
@@ -500,13 +512,13 @@ void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
   const uint32_t* tab = sm.tab + (lane & 31);
   for (int j = 0; j < rounds; j += 3) {
     if (j + 2 < rounds) gd_load(b2, p, nb + (j + 2) * stride, lane, KB);
-    gd_compute(b0, p, tab, gd_xs, xstride, sm.code2s, lt, nb + j * stride, lane);
+    gd_compute<RW, IPR, MX, XREG>(b0, p, tab, gd_xs, xstride, xg, sm.code2s, lt, nb + j * stride, lane);
     if (j + 1 >= rounds) break;
     if (j + 3 < rounds) gd_load(b0, p, nb + (j + 3) * stride, lane, KB);
-    gd_compute(b1, p, tab, gd_xs, xstride, sm.code2s, lt, nb + (j + 1) * stride, lane);
+    gd_compute<RW, IPR, MX, XREG>(b1, p, tab, gd_xs, xstride, xg, sm.code2s, lt, nb + (j + 1) * stride, lane);
     if (j + 2 >= rounds) break;
     if (j + 4 < rounds) gd_load(b1, p, nb + (j + 4) * stride, lane, KB);
-    gd_compute(b2, p, tab, gd_xs, xstride, sm.code2s, lt, nb + (j + 2) * stride, lane);
+    gd_compute<RW, IPR, MX, XREG>(b2, p, tab, gd_xs, xstride, xg, sm.code2s, lt, nb + (j + 2) * stride, lane);
   }
 }
 
@@ -819,7 +831,7 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
     const int64_t waves = std::min<int64_t>(ceil_div64(w->rows, rw), (int64_t)cus * GD_WAVES * per_cu);
     const int64_t wgs = ceil_div64(waves, GD_WAVES);
     const int rounds = (int)ceil_div64(w->rows, wgs * GD_WAVES * rw);
-    const size_t dyn = (size_t)mx * (w->cols + GD_XPAD) * 2;
+    const size_t dyn = ipr == 2 && mx == 1 ? 0 : (size_t)mx * (w->cols + GD_XPAD) * 2;   // X in registers
 #define MOLT_GD(IPRv, MXv) \
   hipLaunchKernelGGL((nf4_gemv_dot_kernel<1, IPRv, MXv>), dim3((unsigned)wgs), dim3(GD_NT), dyn, st, p, rounds)
     if (ipr == 2) {
