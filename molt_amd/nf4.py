@@ -43,32 +43,27 @@ NF4_CODEBOOK = torch.tensor(
 def dynamic_map(signed: bool = True, max_exponent_bits: int = 7, total_bits: int = 8) -> torch.Tensor:
     """The 256-entry dynamic quantisation map of bitsandbytes'
     ``create_dynamic_map`` (bitsandbytes 0.50.2; the dependency is not part of
-    the reference tree), used as ``state2.code`` for nested absmax. Values are
-    computed in fp32."""
-    data: list[float] = []
+    the reference tree), used as ``state2.code`` for nested absmax.
+
+    Decade i (of ``max_exponent_bits``) holds the midpoints of an fp32
+    ``linspace(0.1, 1, 2**i + 1)`` scaled by ``10**(i - 6)`` (the scale rounded
+    to fp32, the product in fp32), with both signs when ``signed``; 0 and 1
+    complete the table, which is returned sorted."""
     non_sign_bits = total_bits - 1
-    additional = 2 ** (non_sign_bits - max_exponent_bits) - 1
-    i = 0
-    for i in range(max_exponent_bits):
-        items = (2 ** (i + non_sign_bits - max_exponent_bits) + 1 if signed
-                 else 2 ** (i + non_sign_bits - max_exponent_bits + 1) + 1)
-        bounds = torch.linspace(0.1, 1.0, items, dtype=torch.float64).to(torch.float32)
-        means = (bounds[:-1] + bounds[1:]) / 2.0
-        mag = torch.tensor(10.0 ** (-(max_exponent_bits - 1) + i), dtype=torch.float32)
-        data += (mag * means).tolist()
-        if signed:
-            data += (-(mag * means)).tolist()
-    if additional > 0:
-        bounds = torch.linspace(0.1, 1.0, additional + 1, dtype=torch.float64).to(torch.float32)
-        means = (bounds[:-1] + bounds[1:]) / 2.0
-        mag = torch.tensor(10.0 ** (-(max_exponent_bits - 1) + i), dtype=torch.float32)
-        data += (mag * means).tolist()
-        if signed:
-            data += (-(mag * means)).tolist()
-    data.append(0.0)
-    data.append(1.0)
-    data += [0.0] * (2 ** total_bits - len(data))
-    return torch.tensor(sorted(data), dtype=torch.float32)
+    extra = 2 ** (non_sign_bits - max_exponent_bits) - 1
+    plan = [(i, 2 ** (i + non_sign_bits - max_exponent_bits + (0 if signed else 1)) + 1)
+            for i in range(max_exponent_bits)]
+    if extra > 0:
+        plan.append((max_exponent_bits - 1, extra + 1))
+    parts = [torch.tensor([0.0, 1.0])]
+    for decade, points in plan:
+        edges = torch.linspace(0.1, 1.0, points, dtype=torch.float32)
+        mids = (edges[1:] + edges[:-1]) / 2.0
+        level = mids * (10.0 ** (decade - (max_exponent_bits - 1)))
+        parts += [level, -level] if signed else [level]
+    table = torch.cat(parts)
+    table = torch.cat([table, torch.zeros(2 ** total_bits - table.numel())])
+    return torch.sort(table).values
 
 
 class QuantState:

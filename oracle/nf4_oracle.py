@@ -22,18 +22,27 @@ Pinning (what independently checks each function; see ``tests/test_oracle.py``):
   on tiny inputs for both nibble orders.
 * ``bf16_rne`` - pinned against torch's own fp32->bf16 conversion.
 * ``dequantize`` - pinned by the round-trip and torch-conversion checks above.
-* ``double_quantize`` / ``resolve_scales`` - pinned by the exact round trip
-  of representable absmax values and the bound
-  ``|resolved - absmax| <= absmax2 * max_gap(code2) / 2``.
-* ``dynamic_map`` - bitsandbytes' ``create_dynamic_map`` (bitsandbytes 0.50.2,
-  a dependency absent from the reference tree and from this image). Only its
-  structural invariants are checked: PARITY UNPINNED against bitsandbytes'
-  own table. The kernels read the table as data, so this affects only which
-  table the build's quantiser writes, never the dequant arithmetic.
+* ``absmax_offset`` - pinned against ``math.fsum`` (1 fp32 ulp).
+* ``double_quantize`` / ``resolve_scales`` - pinned by blocks whose values
+  decode exactly (centred value 0 or the block maximum) or to a closed form,
+  with a different absmax2 per block; by the error bound
+  ``|resolved - absmax| <= absmax2 * max_gap(code2) / 2``; and, for the
+  rounding order, by torch CPU fp32 ``mul`` then ``add_`` (the two ops of
+  methods/nf4_backward.py:157-160) on inputs where a fused multiply-add
+  rounds differently.
+* ``linspace_f32`` / ``dynamic_map`` - bitsandbytes' ``create_dynamic_map``
+  (bitsandbytes 0.50.2, a dependency absent from the reference tree and from
+  this image). Pinned against torch's fp32 ``linspace``, the closed form of
+  each entry (2 ulp) and the entry count per decade. Whether bitsandbytes'
+  linspace is fp32 (as restated) or fp64 rounded to fp32 changes 22 entries
+  by 1 ulp: that choice is PARITY UNPINNED. The kernels read the table as
+  data, so it only decides which table the build's quantiser writes.
 * ``lora_linear_*``, ``swiglu_*``, ``gated_mlp_*`` - fp64 textbook algebra;
   the backward formulas are pinned against torch autograd of the forward
   expression in fp64, and SwiGLU against ``F.silu(g) * u``
   (``tests/kernels/test_gated_activation.py:10-26``).
+* ``lora_linear_forward_bf16_points`` - the reference's autocast rounding
+  points, pinned against the same forward run as torch CPU bf16 ops.
 * ``rmsnorm_forward`` / ``rmsnorm_backward`` - fp64 algebra. The forward is
   pinned by closed forms (a constant row maps to ``sign * (w + offset)`` at
   eps = 0, scale invariance, unit RMS of the normalised row); the backward by
@@ -157,32 +166,53 @@ def dequantize_bf16_bits(idx, scales, block_size, code=NF4_CODE) -> np.ndarray:
 # --------------------------------------------------------------------------
 # Double quantisation of absmax (bitsandbytes compress_statistics=True)
 # --------------------------------------------------------------------------
+def linspace_f32(start: float, end: float, steps: int) -> np.ndarray:
+    """fp32 ``torch.linspace(start, end, steps)`` as its CPU kernel computes it:
+    ``step = fl32((end - start) / (steps - 1))``; the first half is
+    ``fma(step, i, start)`` and the second ``end - step * (steps - 1 - i)``,
+    each rounded once to fp32 (``step * i`` is exact in fp64 here, so the fp64
+    expression below is that single rounding)."""
+    s, e = np.float32(start), np.float32(end)
+    if steps == 1:
+        return np.array([s], np.float32)
+    step = np.float32((e - s) / np.float32(steps - 1))
+    idx = np.arange(steps, dtype=np.float64)
+    head = np.float64(s) + np.float64(step) * idx
+    tail = np.float64(e) - np.float64(step) * (steps - 1 - idx)
+    return np.where(idx < steps // 2, head, tail).astype(np.float32)
+
+
 def dynamic_map(signed: bool = True, max_exponent_bits: int = 7, total_bits: int = 8) -> np.ndarray:
     """Restatement of bitsandbytes' ``create_dynamic_map`` (bitsandbytes 0.50.2,
-    not vendored in the reference; pinned in uv.lock:46-47). PARITY UNPINNED:
-    only structural invariants are checked. Values are computed in fp32."""
+    not vendored in the reference; version pinned in uv.lock:46-47): for each
+    decade i the midpoints of an fp32 ``linspace(0.1, 1, 2**i + 1)``, scaled by
+    ``fl32(10**(i - 6))`` in fp32, with both signs, plus 0 and 1, sorted.
+
+    Pinned (tests/test_oracle.py) against torch's own fp32 linspace, the closed
+    form ``10**(i-6) * (b_j + b_{j+1}) / 2`` with ``b_j = 0.1 + 0.9 j / 2**i``
+    to 2 ulp per entry, and the entry count per decade. Whether bitsandbytes'
+    linspace runs in fp32 (restated here) or in fp64 then rounded changes 22
+    of the 256 entries by 1 ulp; that choice is PARITY UNPINNED (the library
+    is absent). The kernels read the table as data, so it only decides which
+    table this build's quantiser writes."""
     data: list[float] = []
     non_sign_bits = total_bits - 1
     additional = 2 ** (non_sign_bits - max_exponent_bits) - 1
-    i = 0
-    for i in range(max_exponent_bits):
-        items = 2 ** (i + non_sign_bits - max_exponent_bits) + 1 if signed else \
-            2 ** (i + non_sign_bits - max_exponent_bits + 1) + 1
-        bounds = np.linspace(0.1, 1.0, items, dtype=np.float32)
-        means = ((bounds[:-1] + bounds[1:]) / np.float32(2.0)).astype(np.float32)
-        mag = np.float32(10.0 ** (-(max_exponent_bits - 1) + i))
-        data += (mag * means).astype(np.float32).tolist()
-        if signed:
-            data += (-(mag * means)).astype(np.float32).tolist()
+    decades = list(range(max_exponent_bits))
+    counts = [(2 ** (i + non_sign_bits - max_exponent_bits) + 1) if signed
+              else (2 ** (i + non_sign_bits - max_exponent_bits + 1) + 1) for i in decades]
     if additional > 0:
-        bounds = np.linspace(0.1, 1.0, additional + 1, dtype=np.float32)
+        decades.append(max_exponent_bits - 1)
+        counts.append(additional + 1)
+    for i, items in zip(decades, counts):
+        bounds = linspace_f32(0.1, 1.0, items)
         means = ((bounds[:-1] + bounds[1:]) / np.float32(2.0)).astype(np.float32)
         mag = np.float32(10.0 ** (-(max_exponent_bits - 1) + i))
-        data += (mag * means).astype(np.float32).tolist()
+        vals = (mag * means).astype(np.float32)
+        data += vals.tolist()
         if signed:
-            data += (-(mag * means)).astype(np.float32).tolist()
-    data.append(0.0)
-    data.append(1.0)
+            data += (-vals).tolist()
+    data += [0.0, 1.0]
     data += [0.0] * (2 ** total_bits - len(data))
     return np.sort(np.array(data, dtype=np.float32))
 

@@ -158,7 +158,7 @@ def test_offset_is_the_mean_to_one_ulp():
         assert abs(float(off) - exact) <= float(np.spacing(np.float32(exact)))
 
 
-def test_double_quant_bound_and_representable_values():
+def test_double_quant_error_bound():
     rng = np.random.default_rng(9)
     absmax = (np.abs(rng.normal(0, 0.02, 3000)) + 1e-4).astype(np.float32)
     q, absmax2, offset, code2 = O.double_quantize(absmax)
@@ -166,22 +166,86 @@ def test_double_quant_bound_and_representable_values():
     gap = np.diff(code2.astype(np.float64)).max()
     bound = np.repeat(absmax2, 256)[:absmax.size] * gap / 2 + 4 * np.spacing(absmax)
     assert np.all(np.abs(scales.astype(np.float64) - absmax) <= bound)
-    # values that are exactly offset + code2[j] * absmax2 decode exactly
-    code_vals = np.array([code2[255], code2[200], code2[128], code2[10], code2[0]], np.float32)
-    a = np.concatenate([absmax[:251], np.zeros(5, np.float32)])
-    q2, am2, off2, _ = O.double_quantize(a, code2)
-    j = np.argmax(np.abs(a - off2))
-    assert q2[j] in (0, 255)
-    assert code_vals.size == 5
 
 
-def test_dynamic_map_structure():
-    """bitsandbytes' create_dynamic_map: PARITY UNPINNED (bitsandbytes absent);
-    only its structure is checked."""
+def test_double_quant_representable_values_decode_exactly():
+    """Blocks built from ``v`` (centred value 0, code 0.0), ``v + K_b d`` (centred
+    value = the block's absmax2, code 1.0) and ``v - K_b d`` (equal counts, so
+    the mean is exactly v) with dyadic v, d: the first two kinds decode to
+    themselves exactly, the third to ``fl32(fl32(code2[0] K_b d) + v)``. K_b
+    differs per block, so an absmax2 taken from the wrong block fails."""
+    v, d = np.float32(0.015625), np.float32(2.0 ** -12)
+    code2 = O.dynamic_map()
+    blocks = []
+    for b in range(6):
+        k = np.float32(b + 3)
+        blk = np.array([v] * 128 + [v + k * d] * 64 + [v - k * d] * 64, np.float32)
+        blocks.append(np.random.default_rng(b).permutation(blk))
+    a = np.concatenate(blocks)
+    q, absmax2, offset, _ = O.double_quantize(a, code2)
+    assert offset == v
+    assert np.array_equal(absmax2, (np.arange(6, dtype=np.float32) + 3) * d)
+    scales = O.resolve_scales(q, absmax2, code2, offset)
+    low = a < v
+    assert np.array_equal(scales[~low], a[~low])
+    kd = np.repeat(absmax2, 256)[low]
+    expect = (np.float32(code2[0]) * kd).astype(np.float32) + v
+    assert np.array_equal(scales[low], expect.astype(np.float32))
+
+
+def test_resolve_scales_two_roundings_match_torch():
+    """``dequantize_blockwise(...).float()`` then ``.add_(offset)`` as two fp32
+    ops (methods/nf4_backward.py:157-160), restated with torch CPU tensors. The
+    inputs include cases where one fused multiply-add would round differently,
+    and the test checks that such cases are present."""
+    rng = np.random.default_rng(17)
+    code2 = O.dynamic_map()
+    n = 1 << 16
+    q = rng.integers(0, 256, n).astype(np.uint8)
+    absmax2 = (np.abs(rng.normal(0, 0.01, n // 256)) + 1e-4).astype(np.float32)
+    offset = np.float32(0.0137)
+    ours = O.resolve_scales(q, absmax2, code2, offset)
+    prod = torch.from_numpy(code2)[torch.from_numpy(q.astype(np.int64))] * \
+        torch.from_numpy(absmax2).repeat_interleave(256)
+    prod.add_(float(offset))
+    assert np.array_equal(ours, prod.numpy())
+    fused = (code2[q].astype(np.float64) * np.repeat(absmax2, 256).astype(np.float64)
+             + np.float64(offset)).astype(np.float32)
+    assert np.count_nonzero(fused != ours) > 0
+
+
+def test_dynamic_map_linspace_is_torch_fp32():
+    for steps in (2, 3, 5, 9, 17, 33, 65, 129):
+        ref = torch.linspace(0.1, 1.0, steps, dtype=torch.float32).numpy()
+        assert np.array_equal(O.linspace_f32(0.1, 1.0, steps), ref), steps
+
+
+def test_dynamic_map_closed_form():
+    """Entry j of decade i is ``10**(i-6) * (b_j + b_{j+1}) / 2``,
+    ``b_j = 0.1 + 0.9 j / 2**i``, within 2 fp32 ulp; decade i holds 2**i
+    positive and 2**i negative entries; 0 and 1 are present; 256 entries."""
     m = O.dynamic_map()
     assert m.shape == (256,) and m.dtype == np.float32
-    assert np.all(np.diff(m) > 0)
-    assert m[-1] == 1.0 and 0.0 in m and m[0] > -1.0 and m[0] < -0.99
+    expect = []
+    for i in range(7):
+        j = np.arange(2 ** i, dtype=np.float64)
+        b0, b1 = 0.1 + 0.9 * j / 2 ** i, 0.1 + 0.9 * (j + 1) / 2 ** i
+        expect.append(10.0 ** (i - 6) * (b0 + b1) / 2)
+    pos = np.concatenate(expect)
+    closed = np.sort(np.concatenate([pos, -pos, [0.0, 1.0]]))
+    ulp = np.spacing(np.abs(closed).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(m.astype(np.float64) - closed) <= 2 * ulp)
+    for i in range(7):
+        lo, hi = 10.0 ** (i - 6) * 0.1, 10.0 ** (i - 6)
+        assert np.count_nonzero((m > lo) & (m < hi)) == 2 ** i
+        assert np.count_nonzero((m < -lo) & (m > -hi)) == 2 ** i
+    assert m[-1] == 1.0 and np.count_nonzero(m == 0.0) == 1 and np.all(np.diff(m) > 0)
+
+
+def test_product_dynamic_map_is_the_oracle_table():
+    import molt_amd
+
+    assert np.array_equal(molt_amd.dynamic_map().numpy(), O.dynamic_map())
 
 
 # ----------------------------------------------------- GEMM-level algebra
@@ -250,6 +314,32 @@ def test_rel_fro_detects_a_dropped_lora_term():
     a, b = rng.normal(size=(8, 64)) / 8, rng.normal(size=(48, 8)) * 0.1
     full = O.lora_linear_forward(x, w, a, b, 2.0)
     assert O.rel_fro(x @ w.T, full) > 5e-3
+
+
+def test_bf16_points_forward_matches_torch_bf16_ops():
+    """The reference's autocast forward (methods/nf4_lora.py:43-50) run as torch
+    CPU bf16 ops: ``base = bf16(X W^T)``, ``low = F.linear(x, A)``,
+    ``base + F.linear(low, B) * s``, every op returning bf16. The restatement
+    uses fp64 inner products, torch accumulates in fp32, so a few elements may
+    round to the neighbouring bf16 value; a dropped rounding point or term moves
+    far more."""
+    g = torch.Generator().manual_seed(23)
+    m, k, n, r, s = 64, 256, 96, 16, 2.0
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16)
+    a = torch.randn(r, k, generator=g) / 16
+    b = torch.randn(n, r, generator=g) * 0.01
+    base = (x.float() @ w.float().T).to(torch.bfloat16)
+    low = torch.nn.functional.linear(x, a.to(torch.bfloat16))
+    ref = base + torch.nn.functional.linear(low, b.to(torch.bfloat16)) * s
+    assert ref.dtype == torch.bfloat16
+    ours = O.lora_linear_forward_bf16_points(x.float().numpy(), w.float().numpy(), a.numpy(), b.numpy(), s)
+    ref = ref.float().numpy()
+    assert np.mean(ours == ref) >= 0.995
+    ulp = np.spacing(O.bf16_round(np.abs(ref))) * 2 ** 16
+    assert np.all(np.abs(ours - ref) <= 2 * ulp)
+    no_round = O.lora_linear_forward(x.float().numpy(), w.float().numpy(), a.numpy(), b.numpy(), s)
+    assert np.mean(O.bf16_round(no_round) == ref) < 0.9
 
 
 # --------------------------------------------------------------- RMSNorm
