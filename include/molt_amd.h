@@ -14,7 +14,8 @@
  *    NULL = the legacy default stream), never synchronises and never
  *    allocates: any workspace is passed in by the caller.
  *  - Return 0 on success or a MOLT_E* code; molt_amd_last_error() then holds a
- *    thread-local message. The library keeps no mutable state between calls.
+ *    thread-local message. The only state kept between calls is the set of
+ *    kernel-choice settings (molt_amd_set_tuning) and per-device constants.
  *  - NF4 weights: `rows x cols` row-major elements, two 4-bit codes per byte,
  *    `nibble_order` 1 = element 2i in the high nibble (bitsandbytes,
  *    methods/nf4_backward.py:97-98), 0 = element 2i in the low nibble
@@ -65,6 +66,25 @@ typedef struct molt_nf4_weight {
 /* ------------------------------------------------------------------------ */
 const char* molt_amd_last_error(void);
 const char* molt_amd_version(void);
+
+/* Kernel-choice settings. Each starts from its environment variable, read once
+ * when the library first needs it, and can be changed at run time; the value in
+ * force when an entry point is called applies to that call. No counterpart in
+ * the reference (its kernel choices are Triton autotuning and fixed
+ * geometries); used by tests and benchmarks to pin a kernel path.
+ *   MOLT_TUNE_BIG_TILE_MIN  (MOLT_AMD_BIG_TILE_MIN, default 256): fewest
+ *       256 x 256 output tiles for which the GEMMs use the large-tile kernels.
+ *   MOLT_TUNE_GEMV_DOT_M    (MOLT_AMD_GEMV_DOT_M, default -1 = per-shape rule,
+ *       else 0..4): largest token count for the streaming dot-product GEMV.
+ *   MOLT_TUNE_LORA_DMA      (0 when MOLT_AMD_PJ_NODMA is set, else 1): LDS DMA
+ *       staging in the LoRA projection.
+ * molt_amd_set_tuning returns MOLT_EINVAL for an unknown key or a value out of
+ * range; molt_amd_get_tuning returns -2 for an unknown key. */
+#define MOLT_TUNE_BIG_TILE_MIN 0
+#define MOLT_TUNE_GEMV_DOT_M 1
+#define MOLT_TUNE_LORA_DMA 2
+int molt_amd_set_tuning(int32_t key, int64_t value);
+int64_t molt_amd_get_tuning(int32_t key);
 
 /* ------------------------------------------------------------------------ */
 /* NF4 codec                                                                 */

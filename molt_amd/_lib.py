@@ -20,6 +20,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmolt_amd.so"
 
 MOLT_OK, MOLT_EINVAL, MOLT_EUNSUPPORTED, MOLT_ELAUNCH, MOLT_EWORKSPACE = 0, 1, 2, 3, 4
 DTYPE_BF16, DTYPE_F32 = 0, 1
+TUNING_KEYS = {"big_tile_min": 0, "gemv_dot_m": 1, "lora_dma": 2}   # MOLT_TUNE_* of include/molt_amd.h
 
 _p = C.c_void_p
 _i64 = C.c_int64
@@ -44,6 +45,8 @@ _W = C.POINTER(NF4Weight)
 SIGNATURES: dict[str, tuple] = {
     "molt_amd_last_error": (C.c_char_p, []),
     "molt_amd_version": (C.c_char_p, []),
+    "molt_amd_set_tuning": (C.c_int, [_i32, _i64]),
+    "molt_amd_get_tuning": (_i64, [_i32]),
     "molt_nf4_dequantize": (C.c_int, [_W, _p, _i32, _p]),
     "molt_nf4_resolve_scales": (C.c_int, [_W, _p, _p]),
     "molt_nf4_quantize": (C.c_int, [_p, _i32, _i64, _i32, _i32, _p, _p, _p, _p]),
@@ -106,3 +109,34 @@ def check(rc: int) -> None:
     if rc in (MOLT_EINVAL, MOLT_EWORKSPACE):
         raise ValueError(msg)
     raise RuntimeError(msg)
+
+
+class tuning:
+    """Kernel-choice settings of the library (``molt_amd_set_tuning``), as a
+    context manager that restores the previous values on exit::
+
+        with tuning(big_tile_min=1):   # force the 256 x 256 tile GEMMs
+            ...
+
+    Keys: ``big_tile_min``, ``gemv_dot_m``, ``lora_dma``. Settings are process
+    wide; callers that change them concurrently race."""
+
+    def __init__(self, **values: int) -> None:
+        unknown = set(values) - set(TUNING_KEYS)
+        if unknown:
+            raise ValueError(f"unknown tuning keys {sorted(unknown)}; known: {sorted(TUNING_KEYS)}")
+        self.values = values
+        self.saved: dict[str, int] = {}
+
+    def __enter__(self) -> "tuning":
+        lib = load()
+        for name, value in self.values.items():
+            key = TUNING_KEYS[name]
+            self.saved[name] = int(lib.molt_amd_get_tuning(key))
+            check(lib.molt_amd_set_tuning(key, int(value)))
+        return self
+
+    def __exit__(self, *exc) -> None:
+        lib = load()
+        for name, value in self.saved.items():
+            check(lib.molt_amd_set_tuning(TUNING_KEYS[name], value))

@@ -3,6 +3,9 @@
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
+
+#include <atomic>
 
 #include "../../include/molt_amd.h"
 
@@ -24,6 +27,50 @@ int check_launch(const char* what) {
   return MOLT_OK;
 }
 
+// Kernel-choice settings: initialised from the environment once (a function-
+// local static, so the first use from any thread reads it exactly once), then
+// changed only through molt_amd_set_tuning. Entry points read them with one
+// relaxed atomic load per call.
+namespace {
+struct Tuning {
+  std::atomic<int64_t> v[3];
+  Tuning() {
+    const char* e = getenv("MOLT_AMD_BIG_TILE_MIN");
+    v[MOLT_TUNE_BIG_TILE_MIN].store(e ? atoll(e) : 256);
+    e = getenv("MOLT_AMD_GEMV_DOT_M");
+    const int64_t m = e ? atoll(e) : -1;
+    v[MOLT_TUNE_GEMV_DOT_M].store(m < -1 ? -1 : (m > 4 ? 4 : m));
+    v[MOLT_TUNE_LORA_DMA].store(getenv("MOLT_AMD_PJ_NODMA") ? 0 : 1);
+  }
+};
+Tuning& tuning() {
+  static Tuning t;
+  return t;
+}
+bool tuning_ok(int32_t key, int64_t value) {
+  switch (key) {
+    case MOLT_TUNE_BIG_TILE_MIN: return value >= 0;
+    case MOLT_TUNE_GEMV_DOT_M: return value >= -1 && value <= 4;
+    case MOLT_TUNE_LORA_DMA: return value == 0 || value == 1;
+    default: return false;
+  }
+}
+}  // namespace
+
+int64_t tuning_value(int32_t key) { return tuning().v[key].load(std::memory_order_relaxed); }
+
+int device_cus() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 }  // namespace molt
 
 extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w0,
@@ -42,7 +89,18 @@ extern "C" {
 
 const char* molt_amd_last_error(void) { return molt::g_last_error; }
 
-const char* molt_amd_version(void) { return "molt_amd 0.1.0 gfx950"; }
+const char* molt_amd_version(void) { return "molt_amd 0.2.0 gfx950"; }
+
+int molt_amd_set_tuning(int32_t key, int64_t value) {
+  if (!molt::tuning_ok(key, value))
+    return molt::set_error(MOLT_EINVAL, "molt_amd_set_tuning: key %d does not accept %lld", key, (long long)value);
+  molt::tuning().v[key].store(value, std::memory_order_relaxed);
+  return MOLT_OK;
+}
+
+int64_t molt_amd_get_tuning(int32_t key) {
+  return key >= 0 && key <= MOLT_TUNE_LORA_DMA ? molt::tuning_value(key) : -2;
+}
 
 int molt_nf4_lora_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,
                           const uint16_t* t, int64_t ldt, const float* lora_b, int32_t r, float scaling,

@@ -43,6 +43,8 @@ MOLT_DEV float fast_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
 namespace molt {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+int64_t tuning_value(int32_t key);   // a MOLT_TUNE_* setting (molt_amd_set_tuning)
+int device_cus();                    // compute units of the current device, cached per device
 }  // namespace molt
 
 #define MOLT_REQUIRE(cond, code, ...)              \

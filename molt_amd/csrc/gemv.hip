@@ -808,22 +808,13 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
   // tokens, else one; at K = 14336 three rounds of 7 KB per wave need ~190
   // registers); the waves loop over the rounds. M = 2 runs with two X rows, 3
   // and 4 with four. It serves M <= 2, and M = 3, 4 where it measured faster
-  // than the MFMA kernel (K = 14336, or at most 2048 rows); MOLT_AMD_GEMV_DOT_M
-  // (0..4) replaces that rule by a plain bound on M.
-  static const int dot_max_m = [] {
-    const char* e = getenv("MOLT_AMD_GEMV_DOT_M");
-    const int v = e ? atoi(e) : -1;
-    return v < -1 ? -1 : (v > 4 ? 4 : v);
-  }();
+  // than the MFMA kernel (K = 14336, or at most 2048 rows); the
+  // MOLT_TUNE_GEMV_DOT_M setting (0..4) replaces that rule by a plain bound on M.
+  const int dot_max_m = (int)molt::tuning_value(MOLT_TUNE_GEMV_DOT_M);
   const bool dot_m = dot_max_m >= 0 ? M <= dot_max_m : (M <= 2 || (M <= 4 && (w->cols == 14336 || w->rows <= 2048)));
   if (dot_m && (w->cols == 4096 || w->cols == 14336) && aligned(w->packed, 16)) {
     const int ipr = (int)(w->cols / 2048);
-    static int cu_count[64];                                  // per device, filled on first use
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
-      if (cu_count[dev] == 0) hipDeviceGetAttribute(&cu_count[dev], hipDeviceAttributeMultiprocessorCount, dev);
-      if (cu_count[dev] > 0) cus = cu_count[dev];
-    }
+    const int cus = molt::device_cus();
     const int rw = 1;                                         // rows per wave per round
     const int mx = M == 1 ? 1 : (M == 2 ? 2 : 4);             // X rows held by the kernel
     // two workgroups per CU only where the kernel fits in 128 registers
@@ -851,12 +842,7 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
     const size_t need = molt_nf4_gemv_workspace(M, w->rows, w->cols);
     MOLT_REQUIRE(workspace_bytes >= need && (need == 0 || aligned(workspace, 16)), MOLT_EWORKSPACE,
                  "%s: workspace of %zu bytes (16-byte aligned) needed, got %zu", who, need, workspace_bytes);
-    static int cu_count2[64];
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
-      if (cu_count2[dev] == 0) hipDeviceGetAttribute(&cu_count2[dev], hipDeviceAttributeMultiprocessorCount, dev);
-      if (cu_count2[dev] > 0) cus = cu_count2[dev];
-    }
+    const int cus = molt::device_cus();
     const int64_t groups16 = ceil_div64(w->rows, 16);
     const int64_t wgs = std::max<int64_t>(1, std::min<int64_t>(groups16, cus / gm_ks));
     const int rounds = (int)ceil_div64(groups16, wgs);

@@ -588,7 +588,7 @@ extern "C" int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t 
     else if (ks == 2) MOLT_PJK(TQ, MT, VEC, REPLAY, 2);     \
     else MOLT_PJK(TQ, MT, VEC, REPLAY, 1);                  \
   } while (0)
-  const bool dma = vec && z_mode != 1 && D % BK == 0 && getenv("MOLT_AMD_PJ_NODMA") == nullptr;
+  const bool dma = vec && z_mode != 1 && D % BK == 0 && molt::tuning_value(MOLT_TUNE_LORA_DMA) != 0;
 #define MOLT_PJD(TQ, MT)                                                                                       \
   do {                                                                                                         \
     if (ks == 4) hipLaunchKernelGGL((lora_project_dma_kernel<TQ, MT, 4>), grid, block, 0, st, p);               \

@@ -551,8 +551,14 @@ MOLT_DEV uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t sof
 MOLT_DEV void buf_load_lds16(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t off, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, off, soff, 0, 0);
 }
-// vmcnt(0) with the other counters untouched.
-MOLT_DEV void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// vmcnt(N) with the other counters untouched: wait until at most N of this
+// wave's vector-memory operations (loads, buffer-to-LDS DMA) are outstanding.
+template <int N>
+MOLT_DEV void wait_vm_at_most() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate is 4 bits here");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+MOLT_DEV void wait_vm0() { wait_vm_at_most<0>(); }
 
 // The end of a step waits with a partial vmcnt that counts the register loads
 // of the next-but-one step as the only ones allowed to stay in flight; that
@@ -663,7 +669,17 @@ MOLT_DEV void fwd_row(int R, int64_t tn, bool pair, int& which, int64_t& n) {
   }
 }
 
-struct WBytes { u32x4_t q; float sc; };
+// One thread's packed W bytes and block scale for one forward step. w_load
+// fetches them with exactly kLoads vector-memory instructions, issued after the
+// step's X DMA (dma_then_loads); the step's closing wait leaves exactly these in
+// flight, so kLoads is also that wait's vmcnt.
+struct WBytes {
+  u32x4_t q;
+  float sc;
+  static constexpr int kQLoads = sizeof(u32x4_t) / 16;   // 16 bytes per buffer_load_dwordx4
+  static constexpr int kLoads = kQLoads + 1;             // + the scale
+};
+static_assert(WBytes::kQLoads == 1 && WBytes::kLoads == 2, "w_load issues one 16-byte and one 4-byte load");
 
 MOLT_DEV void w_lookup(const WBytes& w, const float2* tabc, int d, float2 (&c)[4]) {
   const uint32_t q = w.q[d];
@@ -926,7 +942,7 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
       __builtin_amdgcn_sched_barrier(0);
     }
     w_finish(c, cw.sc, wnx, wR, wh, 3);
-    __builtin_amdgcn_s_waitcnt(0x0F72);            // vmcnt(2): X(s + 1) landed; W(s + 2) bytes may fly
+    wait_vm_at_most<WBytes::kLoads>();            // X(s + 1) landed; only W(s + 2)'s loads may fly
     step_barrier();
   };
   // W(s + 1) sits in r0 during even steps and in r1 during odd ones; the LDS buffers alternate likewise.
@@ -975,7 +991,15 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
 // contraction runs over rows of W. A thread dequantises a 4-row x 8-column
 // patch (four 4-byte loads, one scale per row) and writes it transposed: rows
 // (0, 1) and (2, 3) of the patch become bf16 pairs in 8 consecutive tile rows.
-struct WPatch { uint32_t q[4]; float sc[4]; };
+// One thread's backward W patch for one step: kRows rows of 8 packed codes
+// (4 bytes) and each row's block scale. w_load issues two 4-byte loads per row,
+// after the step's dY DMA, so kLoads is the closing wait's vmcnt.
+struct WPatch {
+  static constexpr int kRows = 4;
+  static constexpr int kLoads = 2 * kRows;
+  uint32_t q[kRows];
+  float sc[kRows];
+};
 
 // Lookups of byte b of the four patch rows: columns 2b, 2b + 1.
 MOLT_DEV void wp_lookup(const WPatch& w, const float2* tabc, int b, float2 (&c)[4]) {
@@ -1217,7 +1241,7 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
     const __amdgpu_buffer_rsrc_t wr = sg ? wr1 : wr0, sr = sg ? sr1 : sr0;
     const int64_t c0 = c0_of(s);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < WPatch::kRows; ++r) {   // WPatch::kLoads loads: two per row
       w.q[r] = buf_load4(wr, woff, (uint32_t)((c0 + r) * (p.Kw / 2)));
       w.sc[r] = __builtin_bit_cast(float, buf_load4(sr, soff, (uint32_t)((c0 + r) * (p.Kw / 64) * 4)));
     }
@@ -1276,7 +1300,7 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
     wp_finish(c, cw.sc, c4, c5);
     wp_swap_write(c0, c4, wnx, cg, rg, 2);
     wp_swap_write(c1, c5, wnx, cg, rg, 3);
-    __builtin_amdgcn_s_waitcnt(0x0F78);            // vmcnt(8): X(s + 1) landed; W(s + 2) patch may fly
+    wait_vm_at_most<WPatch::kLoads>();            // dY(s + 1) landed; only W(s + 2)'s loads may fly
     step_barrier();
   };
   for (int s = 0; s < ks; s += 2) {
@@ -1328,12 +1352,9 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 // Below this many 256 x 256 tiles the 128 x 128 kernels fill the 256 CUs
-// better. MOLT_AMD_BIG_TILE_MIN overrides the threshold (tests use it to run
-// the large-tile kernels at small shapes).
-int64_t big_tile_min() {
-  const char* e = getenv("MOLT_AMD_BIG_TILE_MIN");
-  return e ? atoll(e) : 256;
-}
+// better. The MOLT_TUNE_BIG_TILE_MIN setting overrides the threshold (tests use
+// it to run the large-tile kernels at small shapes).
+int64_t big_tile_min() { return molt::tuning_value(MOLT_TUNE_BIG_TILE_MIN); }
 
 int check_weight_for_gemm(const molt_nf4_weight* w, const char* who) {
   MOLT_REQUIRE(w && w->packed && w->code, MOLT_EINVAL, "%s: weight, packed and code are required", who);

@@ -62,43 +62,55 @@ class _FrozenRMSNormFunction(torch.autograd.Function):
         return grad_hidden, None, None, None
 
 
+_EPS_FIELDS = ("variance_epsilon", "eps")
+
+
+def _norm_epsilon(norm: nn.Module) -> float | None:
+    for field in _EPS_FIELDS:
+        value = getattr(norm, field, None)
+        if value is not None:
+            return float(value)
+    return None
+
+
 class FrozenRMSNormBF16(nn.Module):
-    """FP32 RMS reduction with a BF16 residual-stream contract
-    (kernels/frozen_rmsnorm.py:40-58)."""
+    """A decoder RMSNorm with a frozen weight, run by the HIP kernels: fp32
+    mean square, one bf16 rounding of the output, input gradient in the input's
+    dtype (kernels/frozen_rmsnorm.py:40-58). Built from the module it replaces,
+    sharing that module's weight parameter."""
 
     def __init__(self, original: nn.Module, *, weight_offset: float = 0.0) -> None:
         super().__init__()
-        weight = getattr(original, "weight", None)
-        eps = getattr(original, "variance_epsilon", getattr(original, "eps", None))
-        if not isinstance(weight, nn.Parameter) or weight.requires_grad or eps is None:
+        weight, eps = getattr(original, "weight", None), _norm_epsilon(original)
+        frozen = isinstance(weight, nn.Parameter) and not weight.requires_grad
+        if not frozen or eps is None:
             raise CapabilityError("RMSNorm replacement requires a frozen weight and epsilon")
         self.weight = weight
-        self.variance_epsilon = float(eps)
+        self.variance_epsilon = eps
         self.weight_offset = float(weight_offset)
 
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
-        return _FrozenRMSNormFunction.apply(hidden_states, self.weight, self.variance_epsilon,
-                                            self.weight_offset)
+        return _FrozenRMSNormFunction.apply(hidden_states, self.weight, self.variance_epsilon, self.weight_offset)
 
 
 def enable_frozen_rmsnorm_bf16(model: nn.Module) -> int:
-    """Replace every module whose class name contains "rmsnorm" with
-    FrozenRMSNormBF16 and the family's weight offset (kernels/frozen_rmsnorm.py:61-86)."""
+    """Replace every submodule whose class name contains "rmsnorm" by a
+    :class:`FrozenRMSNormBF16` with the decoder family's weight offset
+    (kernels/frozen_rmsnorm.py:61-86). Returns the number replaced."""
     family, offset = rmsnorm_weight_offset(model)
-    replacements: list[tuple[nn.Module, str, nn.Module]] = []
-    for parent in model.modules():
-        for name, child in parent.named_children():
-            if "rmsnorm" in type(child).__name__.lower():
-                replacements.append((parent, name, child))
-    if not replacements:
+    norms = [name for name, module in model.named_modules()
+             if name and "rmsnorm" in type(module).__name__.lower()]
+    if not norms:
         raise CapabilityError(f"{family} RMSNorm modules were not found")
-    for parent, name, child in replacements:
-        setattr(parent, name, FrozenRMSNormBF16(child, weight_offset=offset))
-    return len(replacements)
+    for name in norms:
+        parent_name, _, attr = name.rpartition(".")
+        parent = model.get_submodule(parent_name) if parent_name else model
+        setattr(parent, attr, FrozenRMSNormBF16(getattr(parent, attr), weight_offset=offset))
+    return len(norms)
 
 
 def enable_qwen2_frozen_rmsnorm_bf16(model: nn.Module) -> int:
-    """kernels/frozen_rmsnorm.py:89-97."""
+    """The Qwen2-only entry point (kernels/frozen_rmsnorm.py:89-97)."""
     if getattr(getattr(model, "config", None), "model_type", None) != "qwen2":
         raise CapabilityError("Qwen2 RMSNorm replacement requires model_type=qwen2")
     return enable_frozen_rmsnorm_bf16(model)

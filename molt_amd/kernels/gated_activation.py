@@ -5,13 +5,13 @@ Unlike the reference there is no eager CPU fallback: CPU tensors raise
 CapabilityError (the shipped path never computes on the host)."""
 from __future__ import annotations
 
-from types import MethodType
 from typing import Any
 
 import torch
 
 from .. import ops
 from ..errors import CapabilityError
+from ..patching import is_swapped, swap_forward
 
 
 class _FusedSiLUMultiply(torch.autograd.Function):
@@ -40,29 +40,30 @@ def fused_silu_multiply(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     return _FusedSiLUMultiply.apply(gate, up)
 
 
-def _fused_mlp_forward(module: torch.nn.Module, hidden: torch.Tensor) -> torch.Tensor:
-    return module.down_proj(fused_silu_multiply(module.gate_proj(hidden), module.up_proj(hidden)))
+_MLP_ORIGINAL = "_molt_original_mlp_forward"
+_GATED = ("gate_proj", "up_proj", "down_proj")
+
+
+def _silu_gated_forward(module: torch.nn.Module, hidden: torch.Tensor) -> torch.Tensor:
+    """``down(silu(gate(hidden)) * up(hidden))`` with the HIP SiLU-multiply."""
+    gate, up = module.gate_proj(hidden), module.up_proj(hidden)
+    return module.down_proj(fused_silu_multiply(gate, up))
 
 
 def enable_fused_silu_mlp(model: torch.nn.Module) -> int:
-    """Patch compatible SiLU-gated decoder MLPs without changing state keys
-    (kernels/gated_activation.py:106-130)."""
+    """Swap the forward of every gated MLP (a module with gate/up/down
+    projections) of a silu/swish model for :func:`_silu_gated_forward`; state
+    keys do not change (kernels/gated_activation.py:106-130). The replaced
+    forward is kept as ``_molt_original_mlp_forward``. Returns the count."""
     config = getattr(model, "config", None)
-    activation = str(getattr(config, "hidden_activation", getattr(config, "hidden_act", ""))).lower()
+    activation = str(getattr(config, "hidden_activation", None) or getattr(config, "hidden_act", "")).lower()
     family = str(getattr(config, "model_type", "<unknown>"))
     if activation not in {"silu", "swish"}:
-        raise CapabilityError(
-            f"fused SiLU MLP requires silu/swish, but {family} uses {activation or '<unknown>'}"
-        )
-    patched = 0
-    for module in model.modules():
-        if hasattr(module, "_molt_original_mlp_forward"):
-            continue
-        if not all(hasattr(module, name) for name in ("gate_proj", "up_proj", "down_proj")):
-            continue
-        module._molt_original_mlp_forward = module.forward
-        module.forward = MethodType(_fused_mlp_forward, module)
-        patched += 1
-    if patched == 0:
+        raise CapabilityError(f"fused SiLU MLP requires silu/swish, but {family} uses {activation or '<unknown>'}")
+    mlps = [m for m in model.modules()
+            if all(hasattr(m, n) for n in _GATED) and not is_swapped(m, _MLP_ORIGINAL)]
+    if not mlps:
         raise CapabilityError(f"No compatible {family} gated MLP modules found")
-    return patched
+    for mlp in mlps:
+        swap_forward(mlp, _silu_gated_forward, key=_MLP_ORIGINAL)
+    return len(mlps)

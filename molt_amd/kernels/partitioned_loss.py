@@ -11,104 +11,116 @@ Every backend requires CUDA tensors.
 """
 from __future__ import annotations
 
-from contextlib import nullcontext
 from typing import Any
 
 import torch
 from torch.nn import functional as F
 
+from .. import ops
 from ..errors import CapabilityError
 from .frozen_linear_cross_entropy import (_validate_inputs, frozen_linear_cross_entropy,
                                           frozen_linear_cross_entropy_loss_only, fused_frozen_loss_supported)
 
 
-def _autocast(device_type: str, enabled: bool, dtype: torch.dtype):
-    return torch.autocast(device_type=device_type, enabled=enabled, dtype=dtype) if device_type == "cuda" \
-        else nullcontext()
+def _compute_dtype(hidden: torch.Tensor, weight: torch.Tensor, autocast: torch.dtype | None) -> torch.dtype:
+    """dtype of ``F.linear(hidden, weight)``: the autocast dtype when CUDA
+    autocast was on at the forward, else the operands' promoted dtype."""
+    return autocast if autocast is not None else torch.promote_types(hidden.dtype, weight.dtype)
 
 
-def _ce_sum(logits: torch.Tensor, labels: torch.Tensor) -> torch.Tensor:
-    return F.cross_entropy(logits.float() if logits.dtype in (torch.float16, torch.bfloat16) else logits, labels,
-                           reduction="sum")
+def _logits(rows: torch.Tensor, weight: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """One chunk's logits in ``dtype`` (what the row kernel reads: bf16 or
+    fp32; other dtypes are widened to fp32 first)."""
+    z = F.linear(rows.to(dtype), weight.to(dtype))
+    return z if z.dtype in (torch.bfloat16, torch.float32) else z.float()
 
 
-class _ExactPartitionedLinearCrossEntropy(torch.autograd.Function):
-    """Chunked linear + CE, recomputing each chunk in the backward
-    (kernels/partitioned_loss.py:18-103)."""
+def _spans(count: int, chunk: int):
+    return ((start, min(start + chunk, count)) for start in range(0, count, chunk))
+
+
+class _ChunkedLinearCrossEntropy(torch.autograd.Function):
+    """Exact mean cross-entropy of ``hidden . weight^T`` with at most one
+    chunk of logits alive (kernels/partitioned_loss.py:18-103).
+
+    Forward: per chunk, hipBLASLt logits and the HIP row kernel's per-row
+    ``(lse - l_y) / count`` (no gradient pass). Backward: per chunk, the
+    logits again, the row kernel in gradient mode (logits overwritten in place
+    by ``(softmax - onehot) * g / count``, one rounding to the logits' dtype),
+    then ``dh = dlogits . W`` and, for a trainable head, ``dW += dlogits^T . h``.
+    The head's dtype decides the GEMM precision, as autocast does."""
 
     @staticmethod
     def forward(ctx: Any, hidden, weight, targets, chunk_size):
-        flat, labels = hidden.flatten(0, -2), targets.reshape(-1)
+        rows, labels = hidden.flatten(0, -2), targets.reshape(-1).contiguous()
         count = labels.numel()
-        total = torch.zeros((), device=hidden.device, dtype=torch.float32)
-        enabled = torch.is_autocast_enabled("cuda")
-        dtype = torch.get_autocast_dtype("cuda")
-        with _autocast(hidden.device.type, enabled, dtype):
-            for start in range(0, count, chunk_size):
-                end = min(start + chunk_size, count)
-                total = total + _ce_sum(F.linear(flat[start:end], weight), labels[start:end])
+        autocast = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else None
+        dtype = _compute_dtype(hidden, weight, autocast)
+        per_row = torch.empty(count, device=hidden.device, dtype=torch.float32)
+        for lo, hi in _spans(count, chunk_size):
+            per_row[lo:hi] = ops.direct.cross_entropy_rows(_logits(rows[lo:hi], weight, dtype), labels[lo:hi],
+                                                           float(count), False)
         ctx.save_for_backward(hidden, weight, targets)
-        ctx.chunk_size, ctx.enabled, ctx.dtype = chunk_size, enabled, dtype
-        return total / count
+        ctx.chunk_size, ctx.dtype = chunk_size, dtype
+        return per_row.sum()
 
     @staticmethod
+    @torch.autograd.function.once_differentiable
     def backward(ctx: Any, grad_output):
         hidden, weight, targets = ctx.saved_tensors
-        flat, labels = hidden.flatten(0, -2), targets.reshape(-1)
+        need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        rows, labels = hidden.flatten(0, -2), targets.reshape(-1).contiguous()
         count = labels.numel()
-        dh = torch.zeros_like(flat) if ctx.needs_input_grad[0] else None
-        dw = torch.zeros_like(weight) if ctx.needs_input_grad[1] else None
-        for start in range(0, count, ctx.chunk_size):
-            end = min(start + ctx.chunk_size, count)
-            with torch.enable_grad():
-                hc = flat[start:end].detach().requires_grad_(ctx.needs_input_grad[0])
-                wc = weight.detach().requires_grad_(ctx.needs_input_grad[1])
-                with _autocast(hidden.device.type, ctx.enabled, ctx.dtype):
-                    loss = _ce_sum(F.linear(hc, wc), labels[start:end])
-                inputs = [t for t, need in ((hc, ctx.needs_input_grad[0]), (wc, ctx.needs_input_grad[1])) if need]
-                grads = torch.autograd.grad(loss, inputs, grad_outputs=grad_output / count)
-            i = 0
-            if dh is not None:
-                dh[start:end].copy_(grads[0])
-                i = 1
-            if dw is not None:
-                dw.add_(grads[i])
-        return (dh.reshape_as(hidden) if dh is not None else None), dw, None, None
+        scale = float(grad_output)
+        if scale == 0.0:
+            return (torch.zeros_like(hidden) if need_h else None,
+                    torch.zeros_like(weight) if need_w else None, None, None)
+        divisor = float(count) / scale      # folds the incoming gradient into the one rounding
+        grad_rows = torch.empty_like(rows) if need_h else None
+        grad_w = torch.zeros(weight.shape, device=weight.device, dtype=torch.float32) if need_w else None
+        w = weight.detach().to(ctx.dtype)
+        for lo, hi in _spans(count, ctx.chunk_size):
+            part = rows[lo:hi].detach().to(ctx.dtype)
+            dlogits = _logits(part, w, ctx.dtype)
+            ops.direct.cross_entropy_rows(dlogits, labels[lo:hi], divisor, True)
+            dlogits = dlogits.to(ctx.dtype)
+            if need_h:
+                grad_rows[lo:hi].copy_(dlogits @ w)
+            if need_w:
+                grad_w.add_((dlogits.t() @ part).float())
+        grad_h = grad_rows.reshape_as(hidden) if need_h else None
+        return grad_h, (grad_w.to(weight.dtype) if need_w else None), None, None
 
 
-class _FrozenHeadCrossEntropy(torch.autograd.Function):
-    """One head projection per chunk, dL/dlogits formed with torch operations,
-    only the hidden gradient kept (kernels/partitioned_loss.py:106-157)."""
+class _AnalyticalHeadCrossEntropy(torch.autograd.Function):
+    """The "analytical" backend: per chunk, ``dL/dlogits`` from torch's
+    log-softmax (``exp(log_softmax) - onehot``, over ``count``) and the hidden
+    gradient ``dlogits . W`` kept from the forward; the head is frozen
+    (kernels/partitioned_loss.py:106-157)."""
 
     @staticmethod
     def forward(ctx: Any, hidden, weight, targets, chunk_size):
-        flat, labels = hidden.flatten(0, -2), targets.reshape(-1)
+        rows, labels = hidden.flatten(0, -2), targets.reshape(-1)
         count = labels.numel()
-        enabled = torch.is_autocast_enabled("cuda")
-        dtype = torch.get_autocast_dtype("cuda")
-        gradient = torch.empty_like(flat)
+        autocast = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else None
+        dtype = _compute_dtype(hidden, weight, autocast)
         total = torch.zeros((), device=hidden.device, dtype=torch.float32)
-        rows = torch.arange(min(chunk_size, count), device=hidden.device)
-        for start in range(0, count, chunk_size):
-            end = min(start + chunk_size, count)
-            with _autocast(hidden.device.type, enabled, dtype):
-                logits = F.linear(flat[start:end].detach(), weight)
-            red = logits.float() if logits.dtype in (torch.float16, torch.bfloat16) else logits
-            total.add_(F.cross_entropy(red, labels[start:end], reduction="sum").detach() / count)
-            prob = red.softmax(dim=-1)
-            prob[rows[: end - start], labels[start:end]] -= 1.0
-            prob /= count
-            with _autocast(hidden.device.type, enabled, dtype):
-                local = prob.to(weight.dtype) @ weight
-            gradient[start:end].copy_(local.to(gradient.dtype))
-        ctx.save_for_backward(gradient.reshape_as(hidden))
+        grad = torch.empty_like(rows)
+        w = weight.detach().to(dtype)
+        for lo, hi in _spans(count, chunk_size):
+            logp = torch.log_softmax(F.linear(rows[lo:hi].detach().to(dtype), w).float(), dim=-1)
+            picked = logp.gather(1, labels[lo:hi, None])
+            total -= picked.sum() / count
+            dlogits = logp.exp_().scatter_add_(1, labels[lo:hi, None], torch.full_like(picked, -1.0)).div_(count)
+            grad[lo:hi].copy_(dlogits.to(dtype) @ w)
+        ctx.save_for_backward(grad.reshape_as(hidden))
         return total
 
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx: Any, grad_output):
-        (gradient,) = ctx.saved_tensors
-        return gradient * grad_output, None, None, None
+        (grad,) = ctx.saved_tensors
+        return grad * grad_output, None, None, None
 
 
 def exact_partitioned_linear_cross_entropy(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
@@ -133,6 +145,8 @@ def exact_partitioned_linear_cross_entropy(hidden: torch.Tensor, weight: torch.T
     if hidden.device.type != "cuda":
         raise CapabilityError("exact partitioned linear cross-entropy is unavailable for CPU tensors "
                               "(it requires CUDA tensors on a ROCm GPU)")
+    if torch.float64 in (hidden.dtype, weight.dtype):
+        raise CapabilityError("exact partitioned linear cross-entropy reduces rows in fp32; float64 is unsupported")
     if precompute_frozen_gradient:
         if weight.requires_grad:
             raise ValueError("Gradient precomputation requires a frozen classifier")
@@ -142,10 +156,10 @@ def exact_partitioned_linear_cross_entropy(hidden: torch.Tensor, weight: torch.T
         if not torch.is_grad_enabled() or not hidden.requires_grad:
             if backend in {"auto", "triton"} and fused:
                 return frozen_linear_cross_entropy_loss_only(hidden, weight, targets, chunk_size)
-            return _ExactPartitionedLinearCrossEntropy.apply(hidden, weight, targets, chunk_size)
+            return _ChunkedLinearCrossEntropy.apply(hidden, weight, targets, chunk_size)
         if backend in {"auto", "triton"} and fused:
             return frozen_linear_cross_entropy(hidden, weight, targets, chunk_size)
         if backend == "analytical":
             _validate_inputs(hidden, weight, targets, chunk_size)
-            return _FrozenHeadCrossEntropy.apply(hidden, weight, targets, chunk_size)
-    return _ExactPartitionedLinearCrossEntropy.apply(hidden, weight, targets, chunk_size)
+            return _AnalyticalHeadCrossEntropy.apply(hidden, weight, targets, chunk_size)
+    return _ChunkedLinearCrossEntropy.apply(hidden, weight, targets, chunk_size)

@@ -19,7 +19,6 @@ contraction over 2I.
 from __future__ import annotations
 
 from dataclasses import dataclass
-from types import MethodType
 from typing import Any
 
 import torch
@@ -27,6 +26,7 @@ import torch
 from .. import ops
 from ..errors import CapabilityError
 from ..nf4 import _rows_cols, nibble_order, resolved_nf4_scales
+from ..patching import is_swapped, lora_operands, original_forward, refusal, swap_forward
 from .nf4_lora import nf4_lora_module_types
 
 
@@ -286,19 +286,20 @@ class _RMSNormReplayRecipe:
         return ops.direct.rmsnorm_forward(self.source, self.weight, float(self.eps), float(self.weight_offset))
 
 
-def _replayable_norm_forward(module: torch.nn.Module, hidden: torch.Tensor, *args: Any,
-                             **kwargs: Any) -> torch.Tensor:
-    """Norm forward that leaves a replay recipe on its target MLP when the
-    output is bf16 under grad mode (methods/gated_replay.py:33-47)."""
-    result = module._molt_original_forward(hidden, *args, **kwargs)
-    target_mlp = module._molt_target_mlp
-    if torch.is_grad_enabled() and result.dtype == torch.bfloat16:
-        target_mlp._molt_norm_replay_recipe = _RMSNormReplayRecipe(
-            source=hidden, weight=module.weight, eps=float(module.variance_epsilon),
-            weight_offset=float(module.weight_offset), target=result)
-    else:
-        target_mlp._molt_norm_replay_recipe = None
-    return result
+def _leave_replay_recipe(mlp: torch.nn.Module):
+    """Forward hook for a frozen RMSNorm: after each call it leaves on ``mlp``
+    the recipe that recomputes the norm's output from its input, or None when
+    the output will not be differentiated as bf16 (grad mode off, or another
+    dtype). The MLP's patched forward consumes the recipe when its input is
+    that very output (methods/gated_replay.py:13-47)."""
+
+    def hook(norm: torch.nn.Module, inputs: tuple, output: torch.Tensor) -> None:
+        keep = torch.is_grad_enabled() and output.dtype == torch.bfloat16
+        mlp._molt_norm_replay_recipe = _RMSNormReplayRecipe(
+            source=inputs[0], weight=norm.weight, eps=float(norm.variance_epsilon),
+            weight_offset=float(norm.weight_offset), target=output) if keep else None
+
+    return hook
 
 
 class _ResidualRecipeGatedNF4LoRA(torch.autograd.Function):
@@ -347,113 +348,84 @@ class _ResidualRecipeGatedNF4LoRA(torch.autograd.Function):
                 None, None, None, None, None, None, None, None, None)
 
 
+_REPLAY_HOOK = "_molt_replay_hook"
+_NORM_FIELDS = ("weight", "variance_epsilon", "weight_offset")
+
+
 def enable_rmsnorm_replay(model: torch.nn.Module) -> int:
-    """Wire each decoder layer's ``post_attention_layernorm`` to its ``mlp``
-    with :func:`_replayable_norm_forward`, so an MLP patched by
+    """Pair each decoder layer's ``post_attention_layernorm`` with its ``mlp``
+    through a forward hook (:func:`_leave_replay_recipe`), so an MLP routed by
     :func:`enable_fused_gated_nf4_lora` keeps the residual instead of the
     normalised input (``_ResidualRecipeGatedNF4LoRA``). The norm must carry
     ``weight``, ``variance_epsilon`` and ``weight_offset`` (FrozenRMSNormBF16).
-    The reference defines the recipe but wires no caller; this is that wiring."""
-    wired = 0
+    The reference defines the recipe but wires no caller; this is that wiring.
+    Returns the number of pairs; a norm already wired is skipped."""
+    pairs = []
     for layer in model.modules():
-        norm = getattr(layer, "post_attention_layernorm", None)
-        mlp = getattr(layer, "mlp", None)
-        if norm is None or mlp is None or hasattr(norm, "_molt_target_mlp"):
+        norm, mlp = getattr(layer, "post_attention_layernorm", None), getattr(layer, "mlp", None)
+        if norm is None or mlp is None or hasattr(norm, _REPLAY_HOOK):
             continue
-        if not all(hasattr(norm, a) for a in ("weight", "variance_epsilon", "weight_offset")):
-            continue
-        norm._molt_original_forward = norm.forward
-        norm._molt_target_mlp = mlp
-        norm.forward = MethodType(_replayable_norm_forward, norm)
-        mlp._molt_norm_replay_recipe = None
-        wired += 1
-    if not wired:
+        if all(hasattr(norm, f) for f in _NORM_FIELDS):
+            pairs.append((norm, mlp))
+    if not pairs:
         raise CapabilityError("No frozen RMSNorm -> MLP pairs were found (run enable_frozen_rmsnorm_bf16 first)")
-    return wired
+    for norm, mlp in pairs:
+        mlp._molt_norm_replay_recipe = None
+        setattr(norm, _REPLAY_HOOK, norm.register_forward_hook(_leave_replay_recipe(mlp)))
+    return len(pairs)
 
 
 # --------------------------------------------------------------------------
 # Patchers (methods/gated_replay.py:460-607)
 # --------------------------------------------------------------------------
-def _adapter_parts(module: torch.nn.Module) -> tuple[Any, ...] | None:
-    active = list(module.active_adapters)
-    if len(active) != 1:
-        return None
-    adapter = active[0]
-    if (
-        adapter not in module.lora_A
-        or adapter in module.lora_variant
-        or module.use_dora.get(adapter, False)
-        or not isinstance(module.lora_dropout[adapter], torch.nn.Identity)
-        or module.base_layer.bias is not None
-    ):
-        return None
-    return (
-        module.base_layer.weight,
-        module.lora_A[adapter].weight,
-        module.lora_B[adapter].weight,
-        module.base_layer.weight.quant_state,
-        float(module.scaling[adapter]),
-    )
+_PROJECTIONS = ("gate_proj", "up_proj", "down_proj")
+_SILU_NAMES = frozenset({"SiLU", "SiLUActivation"})
+
+
+def _gated_mlp(module: torch.nn.Module, kinds: tuple[type, ...], adapted: tuple[str, ...]) -> bool:
+    """A not yet patched SiLU-gated MLP whose three projections are NF4-LoRA
+    modules and whose ``adapted`` projections have a usable adapter."""
+    if is_swapped(module) or not all(hasattr(module, n) for n in _PROJECTIONS + ("act_fn",)):
+        return False
+    if type(module.act_fn).__name__ not in _SILU_NAMES:
+        return False
+    if not all(isinstance(getattr(module, n), kinds) for n in _PROJECTIONS):
+        return False
+    return all(not isinstance(lora_operands(getattr(module, n), check_state=False), str) for n in adapted)
+
+
+def _gated_mlps(model: torch.nn.Module, adapted: tuple[str, ...]) -> list[torch.nn.Module]:
+    kinds = nf4_lora_module_types()
+    return [m for m in model.modules() if _gated_mlp(m, kinds, adapted)]
+
+
+def _pinned_like(module: torch.nn.Module, slot: str, like: torch.Tensor, what: str) -> torch.Tensor:
+    """The pinned host buffer kept in ``module.<slot>``, (re)allocated to match
+    ``like``; allocation is refused while a CUDA graph is being captured."""
+    buf = getattr(module, slot, None)
+    if buf is None or buf.shape != like.shape or buf.dtype != like.dtype:
+        if torch.cuda.is_current_stream_capturing():
+            raise CapabilityError(f"gated activation {what} was not warmed up")
+        buf = torch.empty_like(like, device="cpu", pin_memory=True)
+        setattr(module, slot, buf)
+    return buf
 
 
 def _asymmetric_mlp_forward(module: torch.nn.Module, x: torch.Tensor, *args: Any, **kwargs: Any) -> torch.Tensor:
-    if (
-        args
-        or kwargs
-        or not torch.is_grad_enabled()
-        or x.dtype != torch.bfloat16
-        or not torch.is_autocast_enabled("cuda")
-        or torch.get_autocast_dtype("cuda") != torch.bfloat16
-    ):
-        return module._molt_original_forward(x, *args, **kwargs)
-    up_parts = _adapter_parts(module.up_proj)
-    down_parts = _adapter_parts(module.down_proj)
-    if up_parts is None or down_parts is None:
-        return module._molt_original_forward(x, *args, **kwargs)
+    why = refusal(x, args, kwargs, need_grad=True)
+    up_ops = lora_operands(module.up_proj) if why is None else why
+    down_ops = lora_operands(module.down_proj) if why is None else why
+    if isinstance(up_ops, str) or isinstance(down_ops, str):
+        return original_forward(module)(x, *args, **kwargs)
     gate = module.gate_proj(x)
     up = module.up_proj(x)
-    if module._molt_offload_up:
-        host_up = getattr(module, "_molt_host_up", None)
-        if host_up is None or host_up.shape != up.shape or host_up.dtype != up.dtype:
-            if torch.cuda.is_current_stream_capturing():
-                raise CapabilityError("gated activation host storage was not warmed up")
-            host_up = torch.empty_like(up, device="cpu", pin_memory=True)
-            module._molt_host_up = host_up
-    else:
-        host_up = None
-    if module._molt_offload_gate:
-        host_gate = getattr(module, "_molt_host_gate", None)
-        if host_gate is None or host_gate.shape != gate.shape or host_gate.dtype != gate.dtype:
-            if torch.cuda.is_current_stream_capturing():
-                raise CapabilityError("gated activation gate storage was not warmed up")
-            host_gate = torch.empty_like(gate, device="cpu", pin_memory=True)
-            module._molt_host_gate = host_gate
-    else:
-        host_gate = None
+    host_up = _pinned_like(module, "_molt_host_up", up, "host storage") if module._molt_offload_up else None
+    host_gate = (_pinned_like(module, "_molt_host_gate", gate, "gate storage")
+                 if module._molt_offload_gate else None)
     return asymmetric_gated_nf4_lora(
-        x, gate, up, up_parts[0], up_parts[1], up_parts[2], down_parts[0], down_parts[1], down_parts[2],
-        up_parts[3], down_parts[3], up_parts[4], down_parts[4], module._molt_rematerialize_up,
-        module._molt_offload_up, host_up, module._molt_offload_gate, host_gate,
-    )
-
-
-def _compatible_mlps(model: torch.nn.Module) -> list[torch.nn.Module]:
-    types = nf4_lora_module_types()
-    found = []
-    for module in model.modules():
-        if hasattr(module, "_molt_original_forward"):
-            continue
-        if not all(hasattr(module, name) for name in ("gate_proj", "up_proj", "down_proj", "act_fn")):
-            continue
-        if not all(isinstance(getattr(module, name), types) for name in ("gate_proj", "up_proj", "down_proj")):
-            continue
-        if type(module.act_fn).__name__ not in {"SiLU", "SiLUActivation"}:
-            continue
-        if _adapter_parts(module.up_proj) is None or _adapter_parts(module.down_proj) is None:
-            continue
-        found.append(module)
-    return found
+        x, gate, up, up_ops.packed, up_ops.lora_a, up_ops.lora_b, down_ops.packed, down_ops.lora_a,
+        down_ops.lora_b, up_ops.quant_state, down_ops.quant_state, up_ops.scaling, down_ops.scaling,
+        module._molt_rematerialize_up, module._molt_offload_up, host_up, module._molt_offload_gate, host_gate)
 
 
 def enable_asymmetric_gated_replay(
@@ -464,76 +436,56 @@ def enable_asymmetric_gated_replay(
     offload_blocks: int = 0,
     offload_gate_blocks: int = 0,
 ) -> int:
-    """Patch structurally compatible SiLU-gated NF4-LoRA MLP blocks
-    (methods/gated_replay.py:540-607)."""
-    if rematerialize_blocks is not None and rematerialize_blocks < 0:
-        raise ValueError("rematerialize_blocks cannot be negative")
-    if offload_blocks < 0:
-        raise ValueError("offload_blocks cannot be negative")
-    if offload_gate_blocks < 0:
-        raise ValueError("offload_gate_blocks cannot be negative")
+    """Route SiLU-gated NF4-LoRA MLP blocks through
+    :func:`asymmetric_gated_nf4_lora` (methods/gated_replay.py:540-607). The
+    first ``rematerialize_blocks`` blocks (all when None) replay the up
+    projection in the backward; the first ``offload_blocks`` /
+    ``offload_gate_blocks`` keep up / gate in pinned host memory instead.
+    Returns the number of blocks patched."""
+    limits = (("rematerialize_blocks", rematerialize_blocks, "replay"), ("offload_blocks", offload_blocks, "offload"),
+              ("offload_gate_blocks", offload_gate_blocks, "gate offload"))
+    for name, value, _ in limits:
+        if value is not None and value < 0:
+            raise ValueError(f"{name} cannot be negative")
     if rematerialize_up and (offload_blocks or offload_gate_blocks):
         raise ValueError("up projection replay and offload are mutually exclusive")
-    compatible = _compatible_mlps(model)
-    if not compatible:
+    blocks = _gated_mlps(model, ("up_proj", "down_proj"))
+    if not blocks:
         raise CapabilityError("No compatible SiLU-gated PEFT NF4 MLP blocks were found")
-    if rematerialize_blocks is not None and rematerialize_blocks > len(compatible):
-        raise CapabilityError(
-            f"requested {rematerialize_blocks} replay blocks but only "
-            f"{len(compatible)} compatible blocks were found"
-        )
-    if offload_blocks > len(compatible):
-        raise CapabilityError(
-            f"requested {offload_blocks} offload blocks but only "
-            f"{len(compatible)} compatible blocks were found"
-        )
-    if offload_gate_blocks > len(compatible):
-        raise CapabilityError(
-            f"requested {offload_gate_blocks} gate offload blocks but only "
-            f"{len(compatible)} compatible blocks were found"
-        )
-    selected = len(compatible) if rematerialize_blocks is None else rematerialize_blocks
-    patched = 0
-    for index, module in enumerate(compatible):
-        module._molt_original_forward = module.forward
-        module._molt_rematerialize_up = bool(rematerialize_up and index < selected)
-        module._molt_offload_up = bool(index < offload_blocks)
-        module._molt_offload_gate = bool(index < offload_gate_blocks)
-        module.forward = MethodType(_asymmetric_mlp_forward, module)
-        patched += 1
-    return patched
+    for _, value, label in limits:
+        if value is not None and value > len(blocks):
+            raise CapabilityError(f"requested {value} {label} blocks but only {len(blocks)} compatible blocks "
+                                  "were found")
+    replayed = len(blocks) if rematerialize_blocks is None else rematerialize_blocks
+    for index, block in enumerate(blocks):
+        swap_forward(block, _asymmetric_mlp_forward, _molt_rematerialize_up=bool(rematerialize_up and index < replayed),
+                     _molt_offload_up=index < offload_blocks, _molt_offload_gate=index < offload_gate_blocks)
+    return len(blocks)
 
 
 def _fused_mlp_forward(module: torch.nn.Module, x: torch.Tensor, *args: Any, **kwargs: Any) -> torch.Tensor:
-    if (
-        args
-        or kwargs
-        or x.dtype != torch.bfloat16
-        or not torch.is_autocast_enabled("cuda")
-        or torch.get_autocast_dtype("cuda") != torch.bfloat16
-    ):
-        return module._molt_original_forward(x, *args, **kwargs)
-    parts = [_adapter_parts(getattr(module, n)) for n in ("gate_proj", "up_proj", "down_proj")]
-    if any(p is None for p in parts):
-        return module._molt_original_forward(x, *args, **kwargs)
+    recipe, module._molt_norm_replay_recipe = getattr(module, "_molt_norm_replay_recipe", None), None
+    why = refusal(x, args, kwargs)
+    parts = [lora_operands(getattr(module, n)) if why is None else why for n in _PROJECTIONS]
+    if any(isinstance(p, str) for p in parts):
+        return original_forward(module)(x, *args, **kwargs)
     g, u, d = parts
-    recipe = getattr(module, "_molt_norm_replay_recipe", None)
-    module._molt_norm_replay_recipe = None
+    weights = (g.packed, g.lora_a, g.lora_b, u.packed, u.lora_a, u.lora_b, d.packed, d.lora_a, d.lora_b,
+               g.quant_state, u.quant_state, d.quant_state, g.scaling, u.scaling, d.scaling)
     if recipe is not None and recipe.target is x and recipe.source.shape == x.shape:
-        return _ResidualRecipeGatedNF4LoRA.apply(
-            recipe.source, x, g[0], g[1], g[2], u[0], u[1], u[2], d[0], d[1], d[2], g[3], u[3], d[3], g[4], u[4],
-            d[4], recipe.weight, recipe.eps, recipe.weight_offset)
-    return fused_gated_nf4_lora_mlp(x, g[0], g[1], g[2], u[0], u[1], u[2], d[0], d[1], d[2], g[3], u[3], d[3],
-                                    g[4], u[4], d[4])
+        return _ResidualRecipeGatedNF4LoRA.apply(recipe.source, x, *weights, recipe.weight, recipe.eps,
+                                                 recipe.weight_offset)
+    return fused_gated_nf4_lora_mlp(x, *weights)
 
 
 def enable_fused_gated_nf4_lora(model: torch.nn.Module) -> int:
     """Route every compatible SiLU-gated NF4-LoRA MLP through
-    :func:`fused_gated_nf4_lora_mlp` (gate and up adapters must be active)."""
-    compatible = [m for m in _compatible_mlps(model) if _adapter_parts(m.gate_proj) is not None]
-    if not compatible:
+    :func:`fused_gated_nf4_lora_mlp` (all three adapters must be usable); an
+    MLP paired with its norm by :func:`enable_rmsnorm_replay` runs the
+    residual-recipe node instead. Returns the number patched."""
+    blocks = _gated_mlps(model, _PROJECTIONS)
+    if not blocks:
         raise CapabilityError("No compatible SiLU-gated PEFT NF4 MLP blocks were found")
-    for module in compatible:
-        module._molt_original_forward = module.forward
-        module.forward = MethodType(_fused_mlp_forward, module)
-    return len(compatible)
+    for block in blocks:
+        swap_forward(block, _fused_mlp_forward)
+    return len(blocks)

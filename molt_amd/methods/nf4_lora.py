@@ -14,14 +14,14 @@ kernels (libmolt_amd.so):
 """
 from __future__ import annotations
 
-from types import MethodType
 from typing import Any
 
 import torch
 
 from .. import ops
 from ..errors import CapabilityError
-from ..nf4 import _rows_cols, nibble_order, resolved_nf4_scales
+from ..nf4 import _rows_cols, gemv_applies, nf4_gemv_linear, nibble_order, resolved_nf4_scales
+from ..patching import is_swapped, lora_operands, original_forward, refusal, swap_forward
 
 
 def _geometry(quant_state: Any) -> tuple[int, int]:
@@ -57,11 +57,14 @@ class _ScheduledNF4LoRA(torch.autograd.Function):
                 "device, and compute dtype"
             )
         flat_x = x.reshape(-1, k)
-        scales = resolved_nf4_scales(quant_state)
         low_rank = ops.direct.lora_project(flat_x, None, 0, 1.0, lora_a, 0)
-        result = ops.direct.nf4_lora_forward(flat_x, packed_weight.reshape(-1), scales, quant_state.code, n, k,
-                                      nibble_order(quant_state), int(quant_state.blocksize), low_rank,
-                                      lora_b, float(scaling))
+        if gemv_applies(flat_x, quant_state, lora_a.shape[0]):
+            # decode-sized batch: HBM-bound skinny-M GEMV instead of the MFMA GEMM
+            result = nf4_gemv_linear(flat_x, packed_weight, quant_state, low_rank, lora_b, scaling)
+        else:
+            result = ops.direct.nf4_lora_forward(
+                flat_x, packed_weight.reshape(-1), resolved_nf4_scales(quant_state), quant_state.code, n, k,
+                nibble_order(quant_state), int(quant_state.blocksize), low_rank, lora_b, float(scaling))
         ctx.quant_state = quant_state
         ctx.scaling = float(scaling)
         ctx.input_shape = x.shape
@@ -104,36 +107,15 @@ def scheduled_nf4_lora(
 
 
 def _scheduled_forward(module: torch.nn.Module, x: torch.Tensor, *args: Any, **kwargs: Any) -> torch.Tensor:
-    """PEFT Linear4bit adapter entry point with strict safe fallback
-    (methods/nf4_lora.py:136-165)."""
-    if (
-        args or kwargs or module.disable_adapters or module.merged
-        or x.dtype != torch.bfloat16
-        or not torch.is_autocast_enabled("cuda")
-        or torch.get_autocast_dtype("cuda") != torch.bfloat16
-    ):
-        return module._molt_original_forward(x, *args, **kwargs)
-    active = list(module.active_adapters)
-    if len(active) != 1:
-        return module._molt_original_forward(x, *args, **kwargs)
-    adapter = active[0]
-    if (
-        adapter not in module.lora_A
-        or adapter in module.lora_variant
-        or module.use_dora.get(adapter, False)
-        or not isinstance(module.lora_dropout[adapter], torch.nn.Identity)
-        or module.base_layer.bias is not None
-    ):
-        return module._molt_original_forward(x, *args, **kwargs)
-    return scheduled_nf4_lora(
-        x,
-        module.base_layer.weight,
-        module.lora_A[adapter].weight,
-        module.lora_B[adapter].weight,
-        module.base_layer.weight.quant_state,
-        float(module.scaling[adapter]),
-        getattr(module, "_molt_decoded_backward_weight", None),
-    )
+    """Forward of a patched NF4-LoRA projection: the HIP path when the call and
+    the adapter allow it, else the projection's own forward (the strict
+    fallback of methods/nf4_lora.py:136-165)."""
+    why = refusal(x, args, kwargs)
+    operands = lora_operands(module) if why is None else why
+    if isinstance(operands, str):
+        return original_forward(module)(x, *args, **kwargs)
+    return scheduled_nf4_lora(x, operands.packed, operands.lora_a, operands.lora_b, operands.quant_state,
+                              operands.scaling, getattr(module, "_molt_decoded_backward_weight", None))
 
 
 def nf4_lora_module_types() -> tuple[type, ...]:
@@ -150,6 +132,12 @@ def nf4_lora_module_types() -> tuple[type, ...]:
     return tuple(types)
 
 
+def _narrow(module: torch.nn.Module) -> bool:
+    """Grouped-query geometry: integer features with fewer outputs than inputs."""
+    width_in, width_out = getattr(module, "in_features", None), getattr(module, "out_features", None)
+    return isinstance(width_in, int) and isinstance(width_out, int) and width_out < width_in
+
+
 def enable_scheduled_nf4_lora(
     model: torch.nn.Module,
     *,
@@ -157,34 +145,36 @@ def enable_scheduled_nf4_lora(
     require_narrow_output: bool = False,
     cache_backward_weights: bool = False,
 ) -> int:
-    """Patch compatible NF4-LoRA modules (methods/nf4_lora.py:168-220)."""
-    types = nf4_lora_module_types()
-    patched = 0
-    for module_name, module in model.named_modules():
-        if not isinstance(module, types) or hasattr(module, "_molt_original_forward"):
-            continue
-        if module_suffixes is not None and not module_name.endswith(module_suffixes):
-            continue
-        if require_narrow_output and not (
-            isinstance(getattr(module, "in_features", None), int)
-            and isinstance(getattr(module, "out_features", None), int)
-            and module.out_features < module.in_features
-        ):
-            continue
-        module._molt_original_forward = module.forward
-        if cache_backward_weights:
-            from ..nf4 import dequantize_4bit
-
-            with torch.no_grad():
-                module._molt_decoded_backward_weight = dequantize_4bit(
-                    module.base_layer.weight.data, module.base_layer.weight.quant_state
-                ).to(dtype=torch.bfloat16)
-        module.forward = MethodType(_scheduled_forward, module)
-        patched += 1
-    if patched == 0:
-        requested = "all modules" if module_suffixes is None else ", ".join(module_suffixes)
+    """Route every selected NF4-LoRA projection of ``model`` through
+    :func:`scheduled_nf4_lora` (methods/nf4_lora.py:168-220). A projection is
+    selected when it is not yet patched, its qualified name ends with one of
+    ``module_suffixes`` (all when None) and, with ``require_narrow_output``, it
+    has fewer outputs than inputs. ``cache_backward_weights`` keeps a dense
+    bf16 decode of each selected weight (validated by the autograd node; the
+    HIP backward decodes bit-identical values in LDS). Returns the count and
+    raises CapabilityError when nothing is selected."""
+    kinds = nf4_lora_module_types()
+    suffixes = None if module_suffixes is None else tuple(module_suffixes)
+    selected = [
+        module for name, module in model.named_modules()
+        if isinstance(module, kinds) and not is_swapped(module)
+        and (suffixes is None or name.endswith(suffixes))
+        and (not require_narrow_output or _narrow(module))
+    ]
+    if not selected:
+        requested = "all modules" if suffixes is None else ", ".join(suffixes)
         raise CapabilityError(
             f"No compatible PEFT NF4-LoRA modules were found for {requested}"
             + (" with grouped-query geometry" if require_narrow_output else "")
         )
-    return patched
+    for module in selected:
+        state = {}
+        if cache_backward_weights:
+            from ..nf4 import dequantize_4bit
+
+            weight = module.base_layer.weight
+            with torch.no_grad():
+                state["_molt_decoded_backward_weight"] = dequantize_4bit(weight.data, weight.quant_state).to(
+                    torch.bfloat16)
+        swap_forward(module, _scheduled_forward, **state)
+    return len(selected)

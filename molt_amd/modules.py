@@ -19,7 +19,7 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
-from .nf4 import QuantState, dequantize_4bit, quantize_4bit
+from .nf4 import QuantState, dequantize_4bit, gemv_applies, nf4_gemv_linear, quantize_4bit
 
 
 class NF4Linear(nn.Module):
@@ -38,7 +38,13 @@ class NF4Linear(nn.Module):
         return cls(packed, qs)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        dense = dequantize_4bit(self.weight.data, self.weight.quant_state).to(x.dtype)
+        qs = self.weight.quant_state
+        if not (torch.is_grad_enabled() and x.requires_grad) and x.device.type == "cuda":
+            flat = x.reshape(-1, self.in_features)
+            if gemv_applies(flat, qs):
+                # decode (1..16 tokens, no autograd): stream the packed weight once
+                return nf4_gemv_linear(flat, self.weight, qs).reshape(*x.shape[:-1], self.out_features)
+        dense = dequantize_4bit(self.weight.data, qs).to(x.dtype)
         return F.linear(x, dense)
 
 

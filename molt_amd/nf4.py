@@ -186,6 +186,37 @@ def dequantize_4bit(A: torch.Tensor, quant_state: Any, out_dtype: torch.dtype | 
     return dense.reshape(quant_state.shape)
 
 
+GEMV_MAX_TOKENS = 16
+GEMV_MAX_RANK = 128
+
+
+def gemv_applies(flat_x: torch.Tensor, quant_state: Any, rank: int = 0) -> bool:
+    """True when ``flat_x`` [tokens, in_features] is a decode-sized batch the
+    skinny-M GEMV serves: 1..16 tokens, NF4 block 64, in_features a multiple of
+    64, LoRA rank <= 128 and 16-byte aligned contiguous bf16 rows."""
+    _, k = _rows_cols(quant_state.shape)
+    return (1 <= flat_x.shape[0] <= GEMV_MAX_TOKENS and flat_x.dtype == torch.bfloat16
+            and int(quant_state.blocksize) == 64 and k % 64 == 0 and rank <= GEMV_MAX_RANK
+            and flat_x.is_contiguous() and flat_x.data_ptr() % 16 == 0)
+
+
+def nf4_gemv_linear(flat_x: torch.Tensor, packed: torch.Tensor, quant_state: Any,
+                    low_rank: torch.Tensor | None = None, lora_b: torch.Tensor | None = None,
+                    scaling: float = 0.0) -> torch.Tensor:
+    """``Y = X deq(W)^T (+ T bf16(s B)^T)`` for 1..16 tokens through the
+    skinny-M NF4 GEMV (the decode step of training/qlora.py:1332-1358). Reads
+    nested statistics directly, so the weight needs no resolved scale cache."""
+    n, k = _rows_cols(quant_state.shape)
+    if quant_state.nested:
+        s2 = quant_state.state2
+        return ops.direct.nf4_gemv(flat_x, packed.reshape(-1), None, quant_state.absmax, s2.absmax, s2.code,
+                                   _offset(quant_state), int(s2.blocksize), quant_state.code, n, k,
+                                   nibble_order(quant_state), low_rank, lora_b, float(scaling))
+    return ops.direct.nf4_gemv(flat_x, packed.reshape(-1), quant_state.absmax.float(), None, None, None, 0.0, 256,
+                               quant_state.code, n, k, nibble_order(quant_state), low_rank, lora_b,
+                               float(scaling))
+
+
 def _rows_cols(shape) -> tuple[int, int]:
     shape = tuple(int(v) for v in shape)
     if len(shape) == 0:

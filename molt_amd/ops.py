@@ -140,6 +140,38 @@ def _check_packed(packed: Tensor, rows: int, cols: int, what: str) -> Tensor:
     return packed.contiguous()
 
 
+def _check_stats(what: str, rows: int, cols: int, block_size: int, code: Tensor,
+                 scales: Optional[Tensor] = None, absmax_q: Optional[Tensor] = None,
+                 absmax2: Optional[Tensor] = None, code2: Optional[Tensor] = None,
+                 dq_block: int = 256) -> None:
+    """Every block statistic the kernels read must exist: one scale (or one
+    nested code) per ``block_size`` elements of the flattened weight, one
+    absmax2 per ``dq_block`` codes, 16 NF4 levels and 256 nested levels."""
+    if block_size <= 0 or (absmax_q is not None and dq_block <= 0):
+        raise ValueError(f"{what}: block sizes must be positive")
+    nblocks = -(-rows * cols // block_size)
+    if code.numel() < 16:
+        raise ValueError(f"{what}: the NF4 code table needs 16 entries, got {code.numel()}")
+    if absmax_q is None:
+        if scales is None or scales.numel() < nblocks:
+            have = 0 if scales is None else scales.numel()
+            raise ValueError(f"{what}: {have} block scales for {nblocks} blocks of {rows}x{cols}")
+        return
+    if absmax_q.dtype != torch.uint8 or absmax_q.numel() < nblocks:
+        raise ValueError(f"{what}: nested absmax must be uint8 with {nblocks} entries "
+                         f"(got {absmax_q.dtype}, {absmax_q.numel()})")
+    if absmax2 is None or absmax2.numel() < -(-nblocks // dq_block):
+        raise ValueError(f"{what}: {0 if absmax2 is None else absmax2.numel()} second-level absmax "
+                         f"values for {-(-nblocks // dq_block)} blocks")
+    if code2 is None or code2.numel() < 256:
+        raise ValueError(f"{what}: the nested code table needs 256 entries")
+
+
+def _check_rows(what: str, name: str, t: Optional[Tensor], rows: int) -> None:
+    if t is not None and (t.dim() != 2 or t.shape[0] != rows):
+        raise ValueError(f"{what}: {name} must have {rows} rows, got {tuple(t.shape)}")
+
+
 # Optional per-launch event probe: name -> list of (start, end) torch.cuda.Event
 # pairs recorded on the launch stream around each call of that entry point.
 _probes: dict[str, list] = {}
@@ -182,6 +214,7 @@ def nf4_dequantize(packed: Tensor, scales: Tensor, code: Tensor, rows: int, cols
     what = "NF4 dequantize"
     dev = _require_gpu(packed, scales, code, what=what)
     packed = _check_packed(packed, rows, cols, what)
+    _check_stats(what, rows, cols, block_size, code, scales=scales)
     out = torch.empty((rows, cols), device=dev, dtype=out_dtype)
     w = _weight(packed, _f32(scales), _f32(code), rows, cols, block_size, order)
     dt = _lib.DTYPE_F32 if out_dtype == torch.float32 else _lib.DTYPE_BF16
@@ -205,6 +238,8 @@ def nf4_dequantize_nested(packed: Tensor, absmax_q: Tensor, absmax2: Tensor, cod
     what = "NF4 dequantize"
     dev = _require_gpu(packed, absmax_q, absmax2, code2, code, what=what)
     packed = _check_packed(packed, rows, cols, what)
+    _check_stats(what, rows, cols, block_size, code, absmax_q=absmax_q, absmax2=absmax2, code2=code2,
+                 dq_block=dq_block)
     if out_dtype not in (torch.float32, torch.bfloat16):
         raise CapabilityError(f"{what}: output dtype {out_dtype} unsupported (bf16, fp32)")
     out = torch.empty((rows, cols), device=dev, dtype=out_dtype)
@@ -225,6 +260,8 @@ def nf4_resolve_scales(absmax_q: Tensor, absmax2: Tensor, code2: Tensor, offset:
                        dq_block: int) -> Tensor:
     """fp32 block scales from nested statistics (methods/nf4_backward.py:145-164)."""
     dev = _require_gpu(absmax_q, absmax2, code2, what="NF4 scale resolution")
+    _check_stats("NF4 scale resolution", 1, absmax_q.numel(), 1, torch.empty(16, device="meta"),
+                 absmax_q=absmax_q, absmax2=absmax2, code2=code2, dq_block=dq_block)
     q = absmax_q.contiguous()
     out = torch.empty(q.numel(), device=dev, dtype=torch.float32)
     # rows*cols only matter through ceil(n / block_size); describe n = nblocks with block 1
@@ -247,6 +284,8 @@ def nf4_quantize(x: Tensor, block_size: int, order: int, code: Tensor) -> tuple[
     dev = _require_gpu(x, code, what=what)
     if x.numel() == 0 or block_size < 16 or block_size % 2:
         raise ValueError("invalid tensor or NF4 block size")
+    if code.numel() < 16:
+        raise ValueError(f"{what}: the NF4 code table needs 16 entries, got {code.numel()}")
     if x.dtype == torch.bfloat16:
         src, dt = x.contiguous(), _lib.DTYPE_BF16
     else:
@@ -271,6 +310,8 @@ def _(x, block_size, order, code):
 def nf4_double_quantize(absmax: Tensor, code2: Tensor, dq_block: int) -> tuple[Tensor, Tensor, Tensor]:
     """Nested statistics (bitsandbytes compress_statistics=True)."""
     dev = _require_gpu(absmax, code2, what="NF4 double quantize")
+    if code2.numel() < 256 or dq_block <= 0:
+        raise ValueError("NF4 double quantize: needs a 256-entry code table and a positive block size")
     a = _f32(absmax)
     n = a.numel()
     q = torch.empty(n, device=dev, dtype=torch.uint8)
@@ -300,8 +341,8 @@ def lora_project(z: Tensor, z2: Optional[Tensor], mode: int, zscale: float, lora
     dev = _require_gpu(z, z2, lora, what=what)
     z = _bf16(z, "activations", what)
     z2 = None if z2 is None else _bf16(z2, "activations", what)
-    if z.dim() != 2:
-        raise ValueError(f"{what}: expected a 2-D activation")
+    if z.dim() != 2 or (z2 is not None and z2.shape != z.shape):
+        raise ValueError(f"{what}: expected a 2-D activation (and a second operand of the same shape)")
     m, d = z.shape
     lw = _f32(lora)
     r = lw.shape[0] if layout == 0 else lw.shape[1]
@@ -332,12 +373,16 @@ def nf4_lora_forward(x: Tensor, packed: Tensor, scales: Tensor, code: Tensor, ro
     if x.dim() != 2 or x.shape[1] != cols:
         raise ValueError(f"{what}: input width {tuple(x.shape)} does not match in_features {cols}")
     packed = _check_packed(packed, rows, cols, what)
+    _check_stats(what, rows, cols, block_size, code, scales=scales)
     y = torch.empty((x.shape[0], rows), device=dev, dtype=torch.bfloat16)
     w = _weight(packed, _f32(scales), _f32(code), rows, cols, block_size, order)
     r = 0
     tt = bb = None
     if t is not None:
         tt = _bf16(t, "low-rank activations", what)
+        _check_rows(what, "the low-rank activation", tt, x.shape[0])
+        if lora_b is None:
+            raise ValueError(f"{what}: a low-rank activation needs LoRA B")
         bb = _f32(lora_b)
         r = tt.shape[1]
         if bb.shape != (rows, r):
@@ -360,12 +405,14 @@ def nf4_gateup_forward(x: Tensor, packed_g: Tensor, scales_g: Tensor, packed_u: 
     """gate, up and h = bf16(bf16(silu(gate)) up) in one launch
     (methods/gated_replay.py:78-94,290-291)."""
     what = "NF4-LoRA gate/up forward"
-    dev = _require_gpu(x, packed_g, scales_g, packed_u, scales_u, code, t, what=what)
+    dev = _require_gpu(x, packed_g, scales_g, packed_u, scales_u, code, t, lora_bg, lora_bu, what=what)
     x = _bf16(x, "activations", what)
     if x.dim() != 2 or x.shape[1] != cols:
         raise ValueError(f"{what}: input width {tuple(x.shape)} does not match in_features {cols}")
     pg = _check_packed(packed_g, rows, cols, what)
     pu = _check_packed(packed_u, rows, cols, what)
+    _check_stats(what, rows, cols, 64, code, scales=scales_g)
+    _check_stats(what, rows, cols, 64, code, scales=scales_u)
     cd = _f32(code)
     wg = _weight(pg, _f32(scales_g), cd, rows, cols, 64, order)
     wu = _weight(pu, _f32(scales_u), cd, rows, cols, 64, order)
@@ -375,6 +422,9 @@ def nf4_gateup_forward(x: Tensor, packed_g: Tensor, scales_g: Tensor, packed_u: 
     tt = bg = bu = None
     if t is not None:
         tt = _bf16(t, "low-rank activations", what)
+        _check_rows(what, "the low-rank activation", tt, m)
+        if lora_bg is None or lora_bu is None or tt.shape[1] % 2:
+            raise ValueError(f"{what}: a low-rank activation needs [T_gate | T_up] and both LoRA B")
         r = tt.shape[1] // 2
         bg, bu = _f32(lora_bg), _f32(lora_bu)
         if bg.shape != (rows, r) or bu.shape != (rows, r):
@@ -402,12 +452,15 @@ def nf4_lora_backward_input(dy: Tensor, packed: Tensor, scales: Tensor, code: Te
     if dy.dim() != 2 or dy.shape[1] != rows:
         raise ValueError("gradient width must match the NF4 output dimension")
     packed = _check_packed(packed, rows, cols, what)
+    _check_stats(what, rows, cols, block_size, code, scales=scales)
     dx = torch.empty((dy.shape[0], cols), device=dev, dtype=torch.bfloat16)
     w = _weight(packed, _f32(scales), _f32(code), rows, cols, block_size, order)
     r = 0
     uu = aa = None
     if u is not None:
         uu = _bf16(u, "LoRA gradients", what)
+        if lora_a is None:
+            raise ValueError(f"{what}: a LoRA gradient needs LoRA A")
         aa = _f32(lora_a)
         r = uu.shape[1]
         if uu.shape[0] != dy.shape[0]:
@@ -439,6 +492,8 @@ def nf4_lora_backward_input_pair(dy0: Tensor, dy1: Tensor, packed0: Tensor, scal
         raise ValueError("gradient width must match the NF4 output dimension")
     p0 = _check_packed(packed0, rows, cols, what)
     p1 = _check_packed(packed1, rows, cols, what)
+    _check_stats(what, rows, cols, 64, code, scales=scales0)
+    _check_stats(what, rows, cols, 64, code, scales=scales1)
     cd = _f32(code)
     w0 = _weight(p0, _f32(scales0), cd, rows, cols, 64, order)
     w1 = _weight(p1, _f32(scales1), cd, rows, cols, 64, order)
@@ -447,7 +502,10 @@ def nf4_lora_backward_input_pair(dy0: Tensor, dy1: Tensor, packed0: Tensor, scal
     r = 0
     uu0 = uu1 = aa0 = aa1 = None
     if u0 is not None:
+        if u1 is None or a0 is None or a1 is None:
+            raise ValueError(f"{what}: LoRA terms need both gradients and both A matrices")
         uu0, uu1 = _bf16(u0, "LoRA gradients", what), _bf16(u1, "LoRA gradients", what)
+        _check_rows(what, "the LoRA gradient", uu0, m)
         aa0, aa1 = _f32(a0), _f32(a1)
         r = uu0.shape[1]
         if uu1.shape != uu0.shape or aa0.shape != (r, cols) or aa1.shape != (r, cols):
@@ -479,13 +537,17 @@ def nf4_swiglu_backward(dy: Tensor, packed: Tensor, scales: Tensor, code: Tensor
     if gate.shape != (dy.shape[0], cols) or up.shape != gate.shape:
         raise ValueError(f"{what}: gate/up shape must be ({dy.shape[0]}, {cols})")
     packed = _check_packed(packed, rows, cols, what)
+    _check_stats(what, rows, cols, 64, code, scales=scales)
     w = _weight(packed, _f32(scales), _f32(code), rows, cols, 64, order)
     dg = torch.empty_like(gate)
     du = torch.empty_like(up)
     r = 0
     uu = aa = None
     if u is not None:
+        if lora_a is None:
+            raise ValueError(f"{what}: a LoRA gradient needs LoRA A")
         uu, aa = _bf16(u, "LoRA gradients", what), _f32(lora_a)
+        _check_rows(what, "the LoRA gradient", uu, dy.shape[0])
         r = uu.shape[1]
         if aa.shape != (r, cols):
             raise ValueError("LoRA gradient and A matrix dimensions are incompatible")
@@ -509,6 +571,8 @@ def lora_grad(l: Tensor, l2: Optional[Tensor], mode: int, rmat: Tensor, scale: f
     l = _bf16(l, "activations", what)
     l2 = None if l2 is None else _bf16(l2, "activations", what)
     rmat = _bf16(rmat, "low-rank operand", what)
+    if l2 is not None and l2.shape != l.shape:
+        raise ValueError(f"{what}: the second operand {tuple(l2.shape)} must match {tuple(l.shape)}")
     if l.dim() != 2 or rmat.dim() != 2 or l.shape[0] != rmat.shape[0]:
         raise ValueError(f"{what}: row counts differ ({tuple(l.shape)} vs {tuple(rmat.shape)})")
     m, p = l.shape
@@ -537,11 +601,13 @@ def nf4_gemv(x: Tensor, packed: Tensor, scales: Optional[Tensor], absmax_q: Opti
     """Skinny-M (<= 16 tokens) NF4 GEMV with the LoRA add-on (decode path of
     training/qlora.py:1332-1358)."""
     what = "NF4 GEMV"
-    dev = _require_gpu(x, packed, code, t, lora_b, what=what)
+    dev = _require_gpu(x, packed, scales, absmax_q, absmax2, code2, code, t, lora_b, what=what)
     x = _bf16(x, "activations", what)
     if x.dim() != 2 or x.shape[1] != cols or not 1 <= x.shape[0] <= 16:
         raise ValueError(f"{what}: needs 1..16 rows of width {cols}, got {tuple(x.shape)}")
     packed = _check_packed(packed, rows, cols, what)
+    _check_stats(what, rows, cols, 64, code, scales=scales, absmax_q=absmax_q, absmax2=absmax2, code2=code2,
+                 dq_block=dq_block)
     m = x.shape[0]
     nested = absmax_q is not None
     w = _weight(packed, None if nested else _f32(scales), _f32(code), rows, cols, 64, order,
@@ -551,7 +617,10 @@ def nf4_gemv(x: Tensor, packed: Tensor, scales: Optional[Tensor], absmax_q: Opti
     r = 0
     tt = bb = None
     if t is not None:
+        if lora_b is None:
+            raise ValueError(f"{what}: a low-rank activation needs LoRA B")
         tt, bb = _bf16(t, "low-rank activations", what), _f32(lora_b)
+        _check_rows(what, "the low-rank activation", tt, m)
         r = tt.shape[1]
         if bb.shape != (rows, r):
             raise ValueError(f"{what}: LoRA B shape {tuple(bb.shape)} != ({rows}, {r})")

@@ -128,3 +128,49 @@ def test_fake_impls_give_shapes_without_a_gpu():
         assert t.shape == (10, 4)
         g = ops.lora_grad(x, None, 0, t, 1.0, 1)
         assert g.shape == (4, 128) and g.dtype == torch.float32
+
+
+def test_statistics_and_row_checks_run_before_any_launch():
+    """The ops refuse short or missing block statistics and low-rank operands
+    with the wrong row count on the host, so no undersized pointer reaches a
+    kernel (the checks need no GPU)."""
+    from molt_amd.ops import _check_rows, _check_stats
+
+    code = torch.zeros(16)
+    _check_stats("t", 128, 64, 64, code, scales=torch.zeros(128))
+    with pytest.raises(ValueError, match="127 block scales for 128 blocks"):
+        _check_stats("t", 128, 64, 64, code, scales=torch.zeros(127))
+    with pytest.raises(ValueError, match="0 block scales"):
+        _check_stats("t", 128, 64, 64, code)
+    with pytest.raises(ValueError, match="16 entries"):
+        _check_stats("t", 128, 64, 64, torch.zeros(15), scales=torch.zeros(128))
+    q = torch.zeros(1000, dtype=torch.uint8)
+    _check_stats("t", 1000, 64, 64, code, absmax_q=q, absmax2=torch.zeros(4), code2=torch.zeros(256))
+    with pytest.raises(ValueError, match="nested absmax"):
+        _check_stats("t", 1001, 64, 64, code, absmax_q=q, absmax2=torch.zeros(4), code2=torch.zeros(256))
+    with pytest.raises(ValueError, match="nested absmax"):
+        _check_stats("t", 1000, 64, 64, code, absmax_q=q.float(), absmax2=torch.zeros(4), code2=torch.zeros(256))
+    with pytest.raises(ValueError, match="second-level"):
+        _check_stats("t", 1000, 64, 64, code, absmax_q=q, absmax2=torch.zeros(3), code2=torch.zeros(256))
+    with pytest.raises(ValueError, match="256 entries"):
+        _check_stats("t", 1000, 64, 64, code, absmax_q=q, absmax2=torch.zeros(4), code2=torch.zeros(255))
+    _check_rows("t", "T", torch.zeros(5, 3), 5)
+    with pytest.raises(ValueError, match="must have 6 rows"):
+        _check_rows("t", "T", torch.zeros(5, 3), 6)
+
+
+def test_tuning_settings_round_trip_without_a_gpu():
+    from molt_amd._lib import TUNING_KEYS, tuning
+
+    lib = _lib.load()
+    before = {k: int(lib.molt_amd_get_tuning(v)) for k, v in TUNING_KEYS.items()}
+    with tuning(big_tile_min=7, gemv_dot_m=2, lora_dma=0):
+        assert lib.molt_amd_get_tuning(TUNING_KEYS["big_tile_min"]) == 7
+        assert lib.molt_amd_get_tuning(TUNING_KEYS["gemv_dot_m"]) == 2
+        assert lib.molt_amd_get_tuning(TUNING_KEYS["lora_dma"]) == 0
+    assert {k: int(lib.molt_amd_get_tuning(v)) for k, v in TUNING_KEYS.items()} == before
+    assert lib.molt_amd_set_tuning(TUNING_KEYS["gemv_dot_m"], 9) == _lib.MOLT_EINVAL
+    assert lib.molt_amd_set_tuning(99, 1) == _lib.MOLT_EINVAL
+    assert lib.molt_amd_get_tuning(99) == -2
+    with pytest.raises(ValueError, match="unknown tuning"):
+        tuning(nope=1)

@@ -1,5 +1,5 @@
 """The 256 x 256-tile GEMM kernels (chosen for large problems) forced at small
-shapes with row/column tails via MOLT_AMD_BIG_TILE_MIN. They must match the
+shapes with row/column tails via the big_tile_min setting. They must match the
 fp64 oracle, and the 128 x 128-tile kernels bit for bit (both accumulate the
 same MFMA products in the same contraction order)."""
 from __future__ import annotations
@@ -24,11 +24,12 @@ def _weight(out_f, in_f, seed):
 
 
 def _both(monkeypatch, fn):
-    monkeypatch.setenv("MOLT_AMD_BIG_TILE_MIN", "1")
-    big = fn()
-    monkeypatch.setenv("MOLT_AMD_BIG_TILE_MIN", str(1 << 40))
-    small = fn()
-    monkeypatch.delenv("MOLT_AMD_BIG_TILE_MIN")
+    from molt_amd._lib import tuning
+
+    with tuning(big_tile_min=1):
+        big = fn()
+    with tuning(big_tile_min=1 << 40):
+        small = fn()
     return big, small
 
 

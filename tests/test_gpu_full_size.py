@@ -65,6 +65,125 @@ def test_cfg4_sampled_rows_match_oracle_and_runs_repeat_bitwise():
         assert torch.isfinite(g).all() and g.abs().sum() > 0
 
 
+def _fp64(t: torch.Tensor) -> torch.Tensor:
+    return t.detach().to(torch.float64)
+
+
+def _rel(actual: torch.Tensor, expected: torch.Tensor) -> float:
+    a, e = _fp64(actual), _fp64(expected)
+    return float(torch.linalg.vector_norm(a - e) / torch.linalg.vector_norm(e).clamp_min(1e-300))
+
+
+def test_cfg4_full_size_adapter_gradients_and_intermediates():
+    """All 8192 rows at cfg4: the six adapter gradients against fp64 GPU matmuls
+    of the node's own bf16 operands (dB = s dY^T T, dA = U^T Z; 1e-5), and the
+    intermediates g, u, h, dg, du, Y and dX against fp32 GEMMs over the
+    bit-exact dequantised weights (5e-3)."""
+    from molt_amd import ops
+    from molt_amd.methods.gated_replay import _fused_backward, _fused_forward
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    print("cfg4 full size: adapter gradients", flush=True)
+    s = 2.0
+    projs = [_proj(I, H, 110), _proj(I, H, 210), _proj(H, I, 310)]
+    (pg, qg, ag, bg), (pu, qu, au, bu), (pd, qd, ad, bd) = projs
+    x = seeded((M, H), 410)
+    dy = seeded((M, H), 411)
+    with torch.no_grad():
+        y, gate, up, h, t_gu, t_d, dims = _fused_forward(x, pg, ag, bg, pu, au, bu, pd, ad, bd, qg, qu, qd,
+                                                         s, s, s)
+        dx, dag, dbg, dau, dbu, dad, dbd = _fused_backward(dy, x, gate, up, h, t_gu, t_d, pg, ag, bg, pu, au, bu,
+                                                           pd, ad, bd, (qg, qu, qd), (s, s, s), dims)
+        sc = molt_amd.resolved_nf4_scales
+        u_d = ops.lora_project(dy, None, 2, s, bd, 1)
+        dg, du = ops.nf4_swiglu_backward(dy, pd.reshape(-1), sc(qd), qd.code, H, I, 1, u_d, ad, gate, up)
+        u_g = ops.lora_project(dg, None, 2, s, bg, 1)
+        u_u = ops.lora_project(du, None, 2, s, bu, 1)
+        r = R
+        checks = {
+            "dA_gate": (dag, _fp64(u_g).T @ _fp64(x)),
+            "dA_up": (dau, _fp64(u_u).T @ _fp64(x)),
+            "dA_down": (dad, _fp64(u_d).T @ _fp64(h)),
+            "dB_gate": (dbg, s * (_fp64(dg).T @ _fp64(t_gu[:, :r]))),
+            "dB_up": (dbu, s * (_fp64(du).T @ _fp64(t_gu[:, r:]))),
+            "dB_down": (dbd, s * (_fp64(dy).T @ _fp64(t_d))),
+        }
+        for name, (got, ref) in checks.items():
+            err = _rel(got, ref)
+            print(f"  {name}: rel {err:.2e}", flush=True)
+            assert err <= 1e-5, f"{name}: relative error {err:.3e} > 1e-5"
+        print("cfg4 full size: intermediates vs fp32 GEMMs", flush=True)
+        wg, wu, wd = (molt_amd.dequantize_4bit(p, q, torch.bfloat16).float() for p, q in ((pg, qg), (pu, qu), (pd, qd)))
+        xf, dyf = x.float(), dy.float()
+        bf = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
+
+        def lin(z, w, a, b):
+            return z @ w.T + s * (bf(z @ bf(a).T) @ bf(b).T)
+
+        g_ref = lin(xf, wg, ag, bg)
+        assert _rel(gate.float(), g_ref) <= 5e-3
+        u_ref = lin(xf, wu, au, bu)
+        assert _rel(up.float(), u_ref) <= 5e-3
+        del g_ref, u_ref
+        gf, uf = gate.float(), up.float()
+        h_ref = gf * torch.sigmoid(gf) * uf
+        assert _rel(h.float(), h_ref) <= 5e-3
+        del h_ref
+        assert _rel(y.float(), lin(h.float(), wd, ad, bd)) <= 5e-3
+        dh = dyf @ wd + bf(bf(s * dyf) @ bf(bd)) @ bf(ad)
+        sg = torch.sigmoid(gf)
+        assert _rel(dg.float(), dh * uf * sg * (1 + gf * (1 - sg))) <= 5e-3
+        assert _rel(du.float(), dh * gf * sg) <= 5e-3
+        del dh, sg
+        dgf, duf = dg.float(), du.float()
+        dx_ref = dgf @ wg + duf @ wu + bf(bf(s * dgf) @ bf(bg)) @ bf(ag) + bf(bf(s * duf) @ bf(bu)) @ bf(au)
+        err = _rel(dx.float(), dx_ref)
+        print(f"  dX all rows: rel {err:.2e}", flush=True)
+        assert err <= 5e-3
+
+
+def test_cfg2_full_size_forward_and_input_gradient():
+    """cfg2 at its own workload: W 8960x1536 and 1536x8960, M = 4096 tokens,
+    r = 16, forward Y and backward dX through scheduled_nf4_lora (the 256 x 256
+    tile kernels at this size). 64 sampled rows against the fp64 oracle, every
+    row against fp32 GEMMs over the bit-exact dequantised weight, and bitwise
+    repeatability (tests/kernels/test_nf4_lora.py:14-45 shapes)."""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    s, r, m = 2.0, 16, 4096
+    rows = np.sort(np.random.default_rng(7).choice(m, 64, replace=False))
+    for out_f, in_f in ((8960, 1536), (1536, 8960)):
+        print(f"cfg2 {in_f}->{out_f} M={m}", flush=True)
+        w = seeded((out_f, in_f), 600 + out_f, std=0.02, dtype=torch.float32)
+        packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True)
+        del w
+        a = uniform((r, in_f), 601, 1.0 / np.sqrt(in_f))
+        b = seeded((out_f, r), 602, std=0.01, dtype=torch.float32)
+        x = seeded((m, in_f), 603)
+        dy = seeded((m, out_f), 604)
+        outs = []
+        for _ in range(2):
+            xr = x.clone().requires_grad_()
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                y = scheduled_nf4_lora(xr, packed, a, b, qs, s)
+            y.backward(dy)
+            outs.append((y.detach(), xr.grad))
+        assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+        y, dx = outs[0]
+        wo = oracle_weight(packed, qs).dequant_bf16().astype(np.float64)
+        ao, bo = bf16_values(a), bf16_values(b)
+        xo, dyo = bf16_values(x)[rows], bf16_values(dy)[rows]
+        assert_close_fro(np_f32(y)[rows], O.lora_linear_forward(xo, wo, ao, bo, s), what="Y rows")
+        rdx, _, _ = O.lora_linear_backward(xo, wo, ao, bo, s, dyo)
+        assert_close_fro(np_f32(dx)[rows], rdx, what="dX rows")
+        wf = molt_amd.dequantize_4bit(packed, qs, torch.bfloat16).float()
+        bf = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
+        xf, dyf = x.float(), dy.float()
+        y_ref = xf @ wf.T + s * (bf(xf @ bf(a).T) @ bf(b).T)
+        dx_ref = dyf @ wf + bf(bf(s * dyf) @ bf(b)) @ bf(a)
+        assert _rel(y.float(), y_ref) <= 5e-3
+        assert _rel(dx.float(), dx_ref) <= 5e-3
+
+
 def test_empty_token_batches():
     s = 2.0
     projs = [_proj(256, 128, 10), _proj(256, 128, 20), _proj(128, 256, 30)]

@@ -164,3 +164,37 @@ def test_custom_ops_pass_opcheck():
     torch.library.opcheck(ops.lora_grad, (flat, None, 0, t, 1.0, 1))
     torch.library.opcheck(ops.nf4_dequantize, (packed.reshape(-1), scales, qs.code, 64, 128, 64, 1, torch.bfloat16))
     assert TOL == 5e-3
+
+
+def test_ops_refuse_host_statistics_and_short_operands():
+    """Host-side refusals before any launch: statistics on the CPU, too few
+    block scales, and low-rank operands whose rows do not match the tokens."""
+    from molt_amd import ops
+
+    x, packed, qs, a, b, dy = _problem(128, 64, 4, 16, 4, weight_std=0.02)
+    flat = x.reshape(-1, 128)
+    scales = molt_amd.resolved_nf4_scales(qs)
+    t = ops.lora_project(flat, None, 0, 1.0, a, 0)
+    p = packed.reshape(-1)
+    with pytest.raises(CapabilityError, match="CUDA"):
+        ops.nf4_lora_forward(flat, p, scales.cpu(), qs.code, 64, 128, 1, 64, t, b, 2.0)
+    with pytest.raises(ValueError, match="block scales"):
+        ops.nf4_lora_forward(flat, p, scales[:-1], qs.code, 64, 128, 1, 64, t, b, 2.0)
+    with pytest.raises(ValueError, match="rows"):
+        ops.nf4_lora_forward(flat, p, scales, qs.code, 64, 128, 1, 64, t[:-1], b, 2.0)
+    with pytest.raises(CapabilityError, match="CUDA"):
+        ops.nf4_gateup_forward(flat, p, scales, p, scales, qs.code, 64, 128, 1,
+                               torch.cat([t, t], 1), b.cpu(), b, 2.0, 2.0)
+    with pytest.raises(ValueError, match="rows"):
+        ops.nf4_lora_backward_input(dy.reshape(-1, 64), p, scales, qs.code, 64, 128, 1, 64,
+                                    t[:3], a, 1.0)
+    s2 = qs.state2
+    with pytest.raises(CapabilityError, match="CUDA"):
+        ops.nf4_gemv(flat[:1], p, None, qs.absmax.cpu(), s2.absmax, s2.code, float(qs.offset), 256, qs.code,
+                     64, 128, 1, None, None, 1.0)
+    with pytest.raises(ValueError, match="second-level"):
+        ops.nf4_gemv(flat[:1], p, None, qs.absmax, s2.absmax[:0], s2.code, float(qs.offset), 256, qs.code,
+                     64, 128, 1, None, None, 1.0)
+    with pytest.raises(ValueError, match="rows"):
+        ops.nf4_gemv(flat[:2], p, None, qs.absmax, s2.absmax, s2.code, float(qs.offset), 256, qs.code,
+                     64, 128, 1, t[:1], b, 1.0)

@@ -12,9 +12,10 @@ from oracle import nf4_oracle as O
 from tests._util import assert_close_fro, np_f32
 
 from molt_amd import ops
+from molt_amd.errors import CapabilityError
 from molt_amd.kernels.frozen_linear_cross_entropy import (_fused_frozen_head_forward, frozen_linear_cross_entropy,
                                                           frozen_linear_cross_entropy_loss_only)
-from molt_amd.kernels.partitioned_loss import _FrozenHeadCrossEntropy, exact_partitioned_linear_cross_entropy
+from molt_amd.kernels.partitioned_loss import _AnalyticalHeadCrossEntropy, exact_partitioned_linear_cross_entropy
 
 pytestmark = pytest.mark.gpu
 
@@ -53,7 +54,7 @@ def test_large_vocabulary_repeated_calls_are_reproducible():
     torch.testing.assert_close(reference_loss, expected, rtol=1e-5, atol=1e-5)
     with torch.enable_grad():
         h = hidden.detach().requires_grad_()
-        analytical = _FrozenHeadCrossEntropy.apply(h, weight, targets, 96)
+        analytical = _AnalyticalHeadCrossEntropy.apply(h, weight, targets, 96)
         analytical.backward()
     torch.testing.assert_close(reference_grad, h.grad, rtol=0, atol=2e-3)
     for _ in range(20):
@@ -171,3 +172,26 @@ def test_loss_only_path_is_bit_exact_to_training_loss():
                                                             precompute_frozen_gradient=True, backend="triton")
     assert torch.equal(evaluation, training.detach())
     assert torch.equal(frozen_linear_cross_entropy_loss_only(hidden.detach(), weight, targets, 8), evaluation)
+
+
+@pytest.mark.parametrize("chunk_size", [1, 3, 8, 32])
+def test_recomputing_backend_matches_unpartitioned_loss_and_both_gradients(chunk_size):
+    """tests/test_molt_stream_partitioned_loss.py:7-25 in fp32 on the GPU (the
+    row kernel reduces in fp32) against fp64 autograd on the CPU, with a
+    trainable head: loss, hidden gradient and head gradient."""
+    torch.manual_seed(17)
+    hidden64 = torch.randn(2, 4, 7, dtype=torch.float64, requires_grad=True)
+    weight64 = torch.randn(11, 7, dtype=torch.float64, requires_grad=True)
+    targets = torch.randint(0, 11, (2, 4))
+    reference = F.cross_entropy(F.linear(hidden64, weight64).flatten(0, 1), targets.flatten())
+    reference.backward()
+    hidden = hidden64.detach().float().cuda().requires_grad_()
+    weight = weight64.detach().float().cuda().requires_grad_()
+    loss = exact_partitioned_linear_cross_entropy(hidden, weight, targets.cuda(), chunk_size)
+    loss.backward()
+    torch.testing.assert_close(loss.double().cpu(), reference.detach(), rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(hidden.grad.double().cpu(), hidden64.grad, rtol=1e-4, atol=1e-6)
+    torch.testing.assert_close(weight.grad.double().cpu(), weight64.grad, rtol=1e-4, atol=1e-6)
+    with pytest.raises(CapabilityError, match="float64"):
+        exact_partitioned_linear_cross_entropy(hidden64.detach().cuda(), weight64.detach().cuda(), targets.cuda(),
+                                               chunk_size)
