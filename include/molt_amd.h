@@ -228,6 +228,20 @@ int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weig
                   float scaling, uint16_t* y, int64_t ldy, void* workspace,
                   size_t workspace_bytes, void* stream);
 
+/* molt_nf4_gemv without a workspace argument and without any allocation. No
+ * counterpart in the reference: it is for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The split-K partials live in a static device array of
+ * molt_nf4_gemv_noalloc_limit() bytes (8 MiB) per GPU, held until the process
+ * ends; a shape needing more (molt_nf4_gemv_workspace above the limit) returns
+ * MOLT_EUNSUPPORTED before any launch. Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (two streams, two threads) race. Same
+ * results as molt_nf4_gemv, bit for bit. */
+size_t molt_nf4_gemv_noalloc_limit(void);
+int molt_nf4_gemv_noalloc(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,
+                          const uint16_t* t, int64_t ldt, const float* lora_b, int32_t r,
+                          float scaling, uint16_t* y, int64_t ldy, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* SwiGLU elementwise                                                        */
 /* ------------------------------------------------------------------------ */

@@ -68,6 +68,8 @@ SIGNATURES: dict[str, tuple] = {
                                  _p]),
     "molt_nf4_gemv_workspace": (_sz, [_i64, _i64, _i64]),
     "molt_nf4_gemv": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _f32, _p, _i64, _p, _sz, _p]),
+    "molt_nf4_gemv_noalloc_limit": (_sz, []),
+    "molt_nf4_gemv_noalloc": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _f32, _p, _i64, _p]),
     "molt_silu_mul_forward": (C.c_int, [_p, _p, _p, _i64, _i32, _i32, _p]),
     "molt_silu_mul_backward": (C.c_int, [_p, _p, _p, _p, _p, _i64, _i32, _p]),
     "molt_rmsnorm_forward": (C.c_int, [_p, _i32, _i64, _i64, _i64, _p, _i32, _f32, _f32, _p, _i64, _p, _p]),

@@ -21,6 +21,7 @@
 // 32 ranks; its B rows are copied into LDS by direct global->LDS loads and T
 // is held in registers, both issued with the first weight chunk.
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 
@@ -867,4 +868,64 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
   if (q4) hipLaunchKernelGGL((nf4_gemv_kernel<true>), dim3((unsigned)groups), dim3(GV_NT), 0, st, p);
   else hipLaunchKernelGGL((nf4_gemv_kernel<false>), dim3((unsigned)groups), dim3(GV_NT), 0, st, p);
   return check_launch(who);
+}
+
+// ---------------------------------------------------------------------------
+// molt_nf4_gemv_noalloc: molt_nf4_gemv with its split-K partials in a static
+// device array instead of a caller workspace, for callers that cannot allocate.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t GEMV_SCRATCH_BYTES = size_t(8) << 20;   // 2 Mi fp32 partials
+constexpr int GEMV_SCRATCH_DEVICES = 64;
+
+// One copy per device, held until the process ends. Host code never uses this
+// name as an address: it is the host-side handle of the symbol, and only the
+// per-device address that hipGetSymbolAddress returns is passed to kernels.
+static __device__ __align__(256) unsigned char scratch[GEMV_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+void* g_scratch_addr[GEMV_SCRATCH_DEVICES];
+
+// The current device's address of `scratch`, looked up on the first call on
+// that device (with it current) and kept.
+int scratch_address(void** out, const char* who) {
+  int dev = -1;
+  const hipError_t de = hipGetDevice(&dev);
+  MOLT_REQUIRE(de == hipSuccess && dev >= 0 && dev < GEMV_SCRATCH_DEVICES, MOLT_ELAUNCH,
+               "%s: no current device (%s)", who, hipGetErrorString(de));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    MOLT_REQUIRE(e == hipSuccess && p != nullptr, MOLT_ELAUNCH, "%s: scratch symbol lookup failed on device %d: %s",
+                 who, dev, hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return MOLT_OK;
+}
+}  // namespace
+
+extern "C" size_t molt_nf4_gemv_noalloc_limit(void) { return GEMV_SCRATCH_BYTES; }
+
+extern "C" int molt_nf4_gemv_noalloc(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,
+                                     const uint16_t* t, int64_t ldt, const float* lora_b, int32_t r, float scaling,
+                                     uint16_t* y, int64_t ldy, void* stream) {
+  const char* who = "molt_nf4_gemv_noalloc";
+  MOLT_REQUIRE(w != nullptr, MOLT_EINVAL, "%s: null weight", who);
+  MOLT_REQUIRE(M >= 1 && M <= 16 && w->rows > 0 && w->cols > 0, MOLT_EUNSUPPORTED, "%s: M=%lld outside 1..16 or empty weight",
+               who, (long long)M);
+  const size_t need = molt_nf4_gemv_workspace(M, w->rows, w->cols);
+  MOLT_REQUIRE(need <= GEMV_SCRATCH_BYTES, MOLT_EUNSUPPORTED,
+               "%s: M=%lld, %lld x %lld needs %zu bytes of split-K partials, more than the %zu-byte static scratch "
+               "(use molt_nf4_gemv with a workspace)",
+               who, (long long)M, (long long)w->rows, (long long)w->cols, need, GEMV_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_address(&ws, who);
+    if (rc != MOLT_OK) return rc;
+  }
+  // Nothing in the scratch has to start at zero: every partial the reduction
+  // reads is written earlier in the same call.
+  return molt_nf4_gemv(x, ldx, M, w, t, ldt, lora_b, r, scaling, y, ldy, ws, need, stream);
 }

@@ -174,3 +174,18 @@ def test_tuning_settings_round_trip_without_a_gpu():
     assert lib.molt_amd_get_tuning(99) == -2
     with pytest.raises(ValueError, match="unknown tuning"):
         tuning(nope=1)
+
+
+def test_noalloc_gemv_refuses_oversized_partials_before_any_device_call():
+    """The size check of molt_nf4_gemv_noalloc runs before it touches the
+    device (this container has none), so an oversized request never launches."""
+    lib = _lib.load()
+    limit = int(lib.molt_nf4_gemv_noalloc_limit())
+    assert limit == 8 << 20
+    w = _lib.NF4Weight()
+    w.rows, w.cols, w.block_size, w.dq_block, w.nested = 40000, 14336, 64, 256, 1
+    need = int(lib.molt_nf4_gemv_workspace(16, w.rows, w.cols))
+    assert need > limit
+    rc = lib.molt_nf4_gemv_noalloc(None, 14336, 16, w, None, 1, None, 0, 0.0, None, 40000, None)
+    assert rc == _lib.MOLT_EUNSUPPORTED
+    assert b"static scratch" in lib.molt_amd_last_error()
