@@ -3,14 +3,16 @@
 Headline (value): tokens/s of one NF4-LoRA gated MLP forward+backward at the
 Llama-3-8B MLP shape (BASELINE cfg4: H=4096, I=14336, r=64, alpha=128,
 M=8192 tokens), including every adapter gradient. Inputs are synthetic, seeded
-and already resident in HBM. Also reported: the roofline of the dominant
-kernel (the fused gate/up NF4 GEMM) from HIP events recorded around its
-launches on its own stream during the timed steps, the frozen RMSNorm kernels
+and already resident in HBM. Also reported: every NF4 GEMM of the step with
+its algorithmic TFLOP/s from HIP events recorded around its launches on the
+launch stream during the timed steps, and the roofline of the longest of them;
+the standalone NF4 dequant (HBM GB/s); the frozen RMSNorm kernels
 and the RMSNorm-replay recipe step, every NF4-LoRA projection shape of the
 cfg3 decoder (attention and MLP, forward + backward), the frozen LM head with
-its chunked cross-entropy, the skinny-M NF4 GEMV sweep (cfg5, HBM
-GB/s), and the CPU baseline (the oracle's restatement of MOLT's
-eager CPU path, cfg1, numpy fp32 on the host cores).
+its chunked cross-entropy, the 28-layer cfg3 decoder stack, the skinny-M NF4
+GEMV sweep (cfg5, HBM GB/s), cfg1 on the GPU and, beside it, the CPU baseline
+(the oracle's restatement of MOLT's eager CPU path, cfg1, numpy fp32 on the
+host cores).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -137,6 +139,145 @@ def gemv_sweep(dev, reps: int = 20):
         del packs, qcopies, descs
         torch.cuda.empty_cache()
     return out
+
+
+def dequant_bench(dev, n: int = 14336, k: int = 4096, reps: int = 10):
+    """Standalone NF4 dequant (molt_nf4_dequantize, nested statistics, bf16
+    out) of an n x k weight: 2.515869 algorithmic bytes per element (read the
+    packed codes and the statistics, write bf16). Each launch reads a distinct
+    copy (>= 512 MiB in all) and writes one of four outputs (470 MB), so
+    neither side stays in the 256 MB Infinity Cache; launches are replayed from
+    a HIP graph."""
+    import ctypes
+    import torch
+    import molt_amd
+    from molt_amd import _lib, ops
+
+    lib = _lib.load()
+    g = torch.Generator(device="cpu").manual_seed(13)
+    w = (torch.randn(n, k, generator=g) * 0.02).to(dev)
+    packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True)
+    del w
+    per_copy = n * k // 2 + qs.absmax.numel()
+    copies = max(2, math.ceil(512 * 2**20 / per_copy))
+    packs = [packed.reshape(-1).clone() for _ in range(copies)]
+    qcopies = [qs.absmax.clone() for _ in range(copies)]
+    outs = [torch.empty(n, k, device=dev, dtype=torch.bfloat16) for _ in range(4)]
+    code, a2, c2 = qs.code.float().contiguous(), qs.state2.absmax.float().contiguous(), qs.state2.code.float().contiguous()
+    descs = [ops._weight(pk, None, code, n, k, 64, 1, qq, a2, c2, float(qs.offset), 256)
+             for pk, qq in zip(packs, qcopies)]
+
+    def launch_all():
+        st = torch.cuda.current_stream().cuda_stream
+        for i, d in enumerate(descs):
+            _lib.check(lib.molt_nf4_dequantize(ctypes.byref(d), outs[i % 4].data_ptr(), _lib.DTYPE_BF16, st))
+
+    launch_all()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch_all()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * copies)
+    alg = n * k * (NF4_BYTES_PER_ELEM + 2)
+    gbs = alg / (us * 1e-6) / 1e9
+    log(f"dequant {n}x{k}: {us:.2f} us, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM)")
+    return {"N": n, "K": k, "us": round(us, 3), "bytes": int(alg), "GB_s": round(gbs, 1),
+            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "copies": copies}
+
+
+def cfg1_gpu(dev, steps: int = 20):
+    """cfg1 (the CPU baseline's workload: H=896, I=4864, r=16, alpha=32,
+    M=1024) on the GPU through the same fused gated-MLP node as the headline."""
+    import torch
+
+    H, I, r, alpha, M = 896, 4864, 16, 32.0, 1024
+    projs, x, dy, s = make_mlp(H, I, r, alpha, M, 1337, dev)
+    for _ in range(3):
+        mlp_step(projs, x, dy, s)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        mlp_step(projs, x, dy, s)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    tf = (12 * H * I + 18 * r * (H + I)) * M / (ms * 1e-3) / 1e12
+    log(f"cfg1 on the GPU: {ms:.3f} ms/step, {M / (ms * 1e-3):.0f} tok/s, {tf:.1f} TFLOP/s")
+    return {"tokens_s": round(M / (ms * 1e-3), 1), "ms_per_step": round(ms, 4), "TFLOP_s": round(tf, 1),
+            "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+
+
+def cfg3_stack(dev, steps: int = 3):
+    """cfg3: the 28-layer Qwen2.5-1.5B-shaped decoder stack (hidden 1536,
+    12/2 heads of 128, intermediate 8960, RMSNorm; transformers' Llama decoder
+    with those shapes, bias-free projections), NF4 QLoRA r=16 alpha=32 on all
+    seven projections, fwd+bwd over bf16 embeddings N(0,1) at 4 x 1024 tokens,
+    with the gated MLP's RMSNorm replay. Attention is torch SDPA. FLOPs per token
+    and layer: the projections' forward GEMMs twice (forward and input
+    gradient; the frozen weights have none), 6 r (K + N) per LoRA adapter, and
+    causal attention 6 * seq * H (QK^T and PV, forward and twice that backward,
+    halved for causality)."""
+    import torch
+    from transformers import LlamaConfig, LlamaModel
+
+    from molt_amd.kernels import enable_frozen_rmsnorm_bf16
+    from molt_amd.loading import prepare_nf4_qlora
+    from molt_amd.methods import enable_fused_gated_nf4_lora, enable_rmsnorm_replay, enable_scheduled_nf4_lora
+
+    H, I, L, heads, kv, hd, r, B, S = 1536, 8960, 28, 12, 2, 128, 16, 4, 1024
+    cfg = LlamaConfig(hidden_size=H, intermediate_size=I, num_hidden_layers=L, num_attention_heads=heads,
+                      num_key_value_heads=kv, head_dim=hd, vocab_size=256, rms_norm_eps=1e-6,
+                      max_position_embeddings=S, attention_bias=False, mlp_bias=False)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(1337)
+    with torch.device(dev):
+        model = LlamaModel(cfg)
+    prepare_nf4_qlora(model, r, 32.0)
+    enable_frozen_rmsnorm_bf16(model)
+    enable_scheduled_nf4_lora(model, module_suffixes=("q_proj", "k_proj", "v_proj", "o_proj"))
+    enable_fused_gated_nf4_lora(model)
+    enable_rmsnorm_replay(model)
+    g = torch.Generator(device="cpu").manual_seed(3)
+    x = torch.randn(B, S, H, generator=g).to(dev, torch.bfloat16).requires_grad_()
+    dy = torch.randn(B, S, H, generator=g).to(dev, torch.bfloat16)
+    params = [p for p in model.parameters() if p.requires_grad]
+
+    def step():
+        x.grad = None
+        for p in params:
+            p.grad = None
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            out = model(inputs_embeds=x).last_hidden_state
+        out.backward(dy)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    proj = 2 * H * (H + 2 * kv * hd) + 2 * H * H + 3 * 2 * H * I       # forward GEMMs per token
+    lora = 6 * r * ((H + H) + 2 * (H + kv * hd) + (H + H) + 3 * (H + I))  # 6 r (K + N) per projection
+    attn = 6 * S * H                                                    # causal QK^T, PV: fwd + 2x bwd
+    flop_tok = L * (2 * proj + lora + attn)                             # fwd + dX, frozen weights
+    tok = B * S
+    tf = flop_tok * tok / (ms * 1e-3) / 1e12
+    log(f"cfg3 stack: {ms:.2f} ms/step, {tok / (ms * 1e-3):.0f} tok/s, {tf:.0f} TFLOP/s "
+        f"({100 * tf / PEAK_BF16_TFLOPS:.1f}% of bf16 peak)")
+    del model
+    torch.cuda.empty_cache()
+    return {"layers": L, "tokens": tok, "ms_per_step": round(ms, 3), "tokens_s": round(tok / (ms * 1e-3), 1),
+            "gflop_per_token": round(flop_tok / 1e9, 3), "TFLOP_s": round(tf, 1),
+            "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
 
 
 def rmsnorm_bench(dev, projs, dy, s, M, H, steps: int, reps: int = 5):
@@ -304,20 +445,47 @@ def lm_head_bench(dev, steps: int = 5):
             "row_kernel_frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "gateup_fwd_cfg4_hbm_traffic.txt"
+# (C entry point, kernel it launches, algorithmic FLOPs per launch at (M, H, I, r))
+GEMMS = (
+    ("molt_nf4_gateup_forward", "big::fwd_kernel<true> (gate/up forward)",
+     lambda M, H, I, r: 2 * (2 * M * H * I) + 2 * (2 * M * I * r)),
+    ("molt_nf4_lora_forward", "big::fwd_kernel<false> (down forward)",
+     lambda M, H, I, r: 2 * M * I * H + 2 * M * H * r),
+    ("molt_nf4_swiglu_backward", "big::bwd_kernel<2> (down dX + SwiGLU backward)",
+     lambda M, H, I, r: 2 * M * H * I + 2 * M * r * I),
+    ("molt_nf4_lora_backward_input_pair", "big::bwd_kernel<0> (paired gate/up dX)",
+     lambda M, H, I, r: 2 * (2 * M * I * H) + 2 * (2 * M * r * H)),
+)
+TRAFFIC_FILE = ROOT / "profiles" / "gemm_cfg4_hbm_traffic.txt"
+COUNTER_FILE = ROOT / "profiles" / "gemm_cfg4_counters.txt"
 
 
-def measured_traffic():
-    """HBM bytes per launch of the gate/up kernel, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE passes (each scaled by the same counter's reading
-    for a copy of known size); None when no such summary is present."""
+def _summary_rows(path: Path) -> dict:
+    """``kernel | key=value ...`` lines of a committed profile summary, by kernel."""
+    rows = {}
     try:
-        for line in TRAFFIC_FILE.read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(float(line.split(":", 1)[1]))
+        for line in path.read_text().splitlines():
+            if "|" not in line or line.startswith("#"):
+                continue
+            name, _, rest = line.partition("|")
+            rows[name.strip()] = dict(kv.split("=", 1) for kv in rest.split())
     except OSError:
         pass
-    return None
+    return rows
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (each scaled by the same counter's reading
+    for a copy of known size); None when no such summary is present."""
+    row = _summary_rows(TRAFFIC_FILE).get(kernel)
+    return int(float(row["traffic_bytes"])) if row and "traffic_bytes" in row else None
+
+
+def measured_counters() -> dict:
+    """MFMA busy fraction per GEMM kernel from the committed rocprofv3 counter
+    summary: SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x GRBM_GUI_ACTIVE per XCD)."""
+    return {k: float(v["mfma_busy"]) for k, v in _summary_rows(COUNTER_FILE).items() if "mfma_busy" in v}
 
 
 def profile_kernel(which: str, reps: int) -> int:
@@ -334,6 +502,10 @@ def profile_kernel(which: str, reps: int) -> int:
         dst = torch.empty_like(src)
         for _ in range(reps):
             dst.copy_(src)
+    elif which == "step":
+        projs, x, dy, s = make_mlp(4096, 14336, 64, 128.0, 8192, 1337, dev)
+        for _ in range(reps):
+            mlp_step(projs, x, dy, s)
     else:
         H, I, r, alpha, M = 4096, 14336, 64, 128.0, 8192
         projs, x, _dy, s = make_mlp(H, I, r, alpha, M, 1337, dev)
@@ -414,8 +586,10 @@ def main() -> int:
     ap.add_argument("--no-norm", action="store_true", help="skip the RMSNorm / norm-replay recipe measurement")
     ap.add_argument("--no-proj", action="store_true", help="skip the cfg3 projection sweep")
     ap.add_argument("--no-head", action="store_true", help="skip the LM head + cross-entropy measurement")
-    ap.add_argument("--profile-kernel", choices=("gateup", "copy"),
-                    help="only launch one kernel (for rocprofv3 --pmc passes) and exit")
+    ap.add_argument("--no-dequant", action="store_true", help="skip the standalone dequant measurement")
+    ap.add_argument("--no-stack", action="store_true", help="skip the cfg3 28-layer decoder stack")
+    ap.add_argument("--profile-kernel", choices=("gateup", "step", "copy"),
+                    help="only launch one kernel or one gated-MLP step (for rocprofv3 --pmc passes) and exit")
     ap.add_argument("--reps", type=int, default=3, help="launches for --profile-kernel")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -440,23 +614,32 @@ def main() -> int:
         mlp_step(projs, x, dy, s)
     torch.cuda.synchronize()
     log("warmup done")
-    pairs = ops.probe_events("molt_nf4_gateup_forward")
+    probes = {entry: ops.probe_events(entry) for entry, _, _ in GEMMS}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         mlp_step(projs, x, dy, s)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    ops.probe_events("molt_nf4_gateup_forward", enable=False)
+    for entry in probes:
+        ops.probe_events(entry, enable=False)
     ms_step = elapsed * 1e3 / args.steps
     tok_s = M * args.steps / elapsed
     flop_step = (12 * H * I + 18 * r * (H + I)) * M
     step_tflops = flop_step / (ms_step * 1e-3) / 1e12
-    k_ms = statistics.mean(a.elapsed_time(b) for a, b in pairs)
-    k_flop = 2 * (2 * M * H * I) + 2 * (2 * M * I * r)      # gate+up base GEMMs + their LoRA B GEMMs
-    k_tflops = k_flop / (k_ms * 1e-3) / 1e12
-    log(f"step {ms_step:.3f} ms, {tok_s:.0f} tok/s, {step_tflops:.1f} TFLOP/s ({100 * step_tflops / PEAK_BF16_TFLOPS:.1f}% of bf16 peak); "
-        f"gate/up kernel {k_ms:.3f} ms = {k_tflops:.1f} TFLOP/s")
+    counters = measured_counters()
+    gemms = []
+    for entry, kernel, flop_fn in GEMMS:
+        k_ms = statistics.mean(a.elapsed_time(b) for a, b in probes[entry])
+        k_flop = flop_fn(M, H, I, r)
+        k_tflops = k_flop / (k_ms * 1e-3) / 1e12
+        gemms.append({"entry": entry, "kernel": kernel, "avg_launch_ms": round(k_ms, 4),
+                      "launches": len(probes[entry]), "flop_per_launch": k_flop, "achieved": round(k_tflops, 1),
+                      "frac": round(k_tflops / PEAK_BF16_TFLOPS, 4), "mfma_busy": counters.get(kernel)})
+        log(f"{kernel}: {k_ms:.3f} ms = {k_tflops:.1f} TFLOP/s ({100 * k_tflops / PEAK_BF16_TFLOPS:.1f}%)")
+    dominant = max(gemms, key=lambda g: g["avg_launch_ms"])
+    log(f"step {ms_step:.3f} ms, {tok_s:.0f} tok/s, {step_tflops:.1f} TFLOP/s "
+        f"({100 * step_tflops / PEAK_BF16_TFLOPS:.1f}% of bf16 peak); dominant kernel {dominant['kernel']}")
 
     result = {
         "metric": METRIC, "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -465,28 +648,39 @@ def main() -> int:
         "config": {"workload": "cfg4: Llama-3-8B-shaped NF4-LoRA gated MLP fwd+bwd incl. dA/dB",
                    "hidden": H, "intermediate": I, "lora_rank": r, "lora_alpha": alpha, "tokens": M,
                    "nf4_block": 64, "double_quant": True, "parallelism": "single GPU"},
-        "mfma_util_pct": round(100 * step_tflops / PEAK_BF16_TFLOPS, 2),
+        "step_frac_of_bf16_peak": round(step_tflops / PEAK_BF16_TFLOPS, 4),
         "step_tflops": round(step_tflops, 1),
-        "roofline": {"kernel": "big::fwd_kernel<true> (fused gate/up NF4-LoRA GEMM)", "bound": "mfma",
-                     "achieved": round(k_tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(k_tflops / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(),
+        "roofline": {"kernel": dominant["kernel"], "bound": "mfma", "achieved": dominant["achieved"],
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": dominant["frac"],
+                     "traffic": measured_traffic(dominant["kernel"]),
                      "traffic_unit": "bytes/launch (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)",
-                     "avg_launch_ms": round(k_ms, 4), "launches": len(pairs),
-                     "flop_per_launch": k_flop},
+                     "avg_launch_ms": dominant["avg_launch_ms"], "launches": dominant["launches"],
+                     "flop_per_launch": dominant["flop_per_launch"], "mfma_busy": dominant["mfma_busy"]},
+        "gemm_kernels": gemms,
     }
+    del probes
+    if not args.no_dequant:
+        result["dequant"] = dequant_bench(dev)
     if not args.no_norm:
         result["rmsnorm"] = rmsnorm_bench(dev, projs, dy, s, M, H, args.steps)
     if not args.no_proj:
         result["cfg3_projections"] = projection_sweep(dev)
     if not args.no_head:
         result["lm_head"] = lm_head_bench(dev)
+    if not args.no_stack:
+        del projs, x, dy
+        torch.cuda.empty_cache()
+        result["cfg3_stack"] = cfg3_stack(dev)
     if not args.no_gemv:
         sweep = gemv_sweep(dev)
         result["gemv"] = sweep
         result["gemv_best_frac_hbm"] = max(e["frac_hbm"] for e in sweep)
     if not args.no_cpu:
+        result["cfg1_gpu"] = cfg1_gpu(dev)
         log("cpu baseline (cfg1, oracle restatement, numpy fp32)")
         result["cpu_baseline"] = cpu_baseline()
+        result["cpu_baseline"]["gpu_speedup_cfg1"] = round(result["cfg1_gpu"]["tokens_s"] /
+                                                           result["cpu_baseline"]["value"], 1)
     print(json.dumps(result), flush=True)
     return 0
 
