@@ -321,38 +321,51 @@ struct GdRound {
   float lb[RW][2];
 };
 
-// Loads of one round (rows n0 .. n0 + RW - 1, clamped to the matrix).
-template <int RW, int IPR>
-MOLT_DEV void gd_load(GdRound<RW, IPR>& R, const GemvParams& p, int64_t n0, int lane, int KB) {
+// Loads of one round (rows n0 .. n0 + RW - 1, clamped to the matrix). Every
+// load is unconditional (statistics layout and LoRA presence are template
+// parameters, out-of-range indices are clamped and their values masked), so
+// each round issues the same fixed number of loads and the compiler's vmcnt
+// wait before a round's arithmetic counts exactly the two later rounds as
+// still in flight; a load under a run-time branch made it wait for those too.
+// Rows past the matrix read row `fallback` instead (the wave's own first row,
+// already on its way to the cache; one shared row would be a hot spot).
+template <int RW, int IPR, bool NESTED, bool LORA>
+MOLT_DEV void gd_load(GdRound<RW, IPR>& R, const GemvParams& p, int64_t n0, int lane, int KB, int64_t fallback) {
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
-    const int64_t n = n0 + r < p.N ? n0 + r : p.N - 1;
+    const int64_t n = n0 + r < p.N ? n0 + r : fallback;
 #pragma unroll
     for (int i = 0; i < IPR; ++i) {
       const int j = r * IPR + i;
       R.w[j] = *reinterpret_cast<const u32x4_t*>(p.packed + (uint32_t)(n * (p.K >> 1) + 1024 * i + 16 * lane));
       const uint32_t blk = (uint32_t)(n * KB + 32 * i + (lane >> 1));
-      if (p.scales) {
-        R.q[j] = 0;
-        R.s[j] = p.scales[blk];
-      } else {
+      if constexpr (NESTED) {
         R.q[j] = p.q[blk];
         R.s[j] = p.absmax2[blk >> p.dq_shift];
+      } else {
+        R.q[j] = 0;
+        R.s[j] = p.scales[blk];
       }
     }
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int jr = lane + 64 * q;
-      R.lb[r][q] = jr < p.r ? p.lb[n * p.r + jr] : 0.0f;
+      if constexpr (LORA) {
+        const float v = p.lb[n * p.r + (jr < p.r ? jr : p.r - 1)];
+        R.lb[r][q] = jr < p.r ? v : 0.0f;
+      } else {
+        R.lb[r][q] = 0.0f;
+      }
     }
   }
 }
 
-// Dot products of one round and the stores of its rows. X row m sits at
+// Dot products of one round; returns the value lane r * MX + m stores (row r
+// of token m, see gd_store). X row m sits at
 // xs + m * xstride (elements); with XREG (one token) the lane's X chunks are
 // xg[4 i + h] in registers instead.
 template <int RW, int IPR, int MX, bool XREG>
-MOLT_DEV void gd_compute(const GdRound<RW, IPR>& R, const GemvParams& p, const uint32_t* tab, const uint16_t* xs,
+MOLT_DEV float gd_compute(const GdRound<RW, IPR>& R, const GemvParams& p, const uint32_t* tab, const uint16_t* xs,
                          int xstride, const u32x4_t* xg, const float* code2s, const float (&lt)[MX][2], int64_t n0,
                          int lane) {
   float acc[RW][MX];
@@ -413,12 +426,18 @@ MOLT_DEV void gd_compute(const GdRound<RW, IPR>& R, const GemvParams& p, const u
       acc[r][m] = v;
     }
   }
+  float v = acc[0][0];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int m = 0; m < MX; ++m) v = lane == r * MX + m ? acc[r][m] : v;
+  return v;
+}
+
+// Store of one round's results: lane r * MX + m holds row n0 + r of token m.
+template <int RW, int MX>
+MOLT_DEV void gd_store(const GemvParams& p, float v, int64_t n0, int lane) {
   if (lane < RW * MX) {
-    float v = acc[0][0];
-#pragma unroll
-    for (int r = 0; r < RW; ++r)
-#pragma unroll
-      for (int m = 0; m < MX; ++m) v = lane == r * MX + m ? acc[r][m] : v;
     const int rr = lane / MX, m = lane % MX;
     const int64_t n = n0 + rr;
     if (n < p.N && m < p.M) p.y[(int64_t)m * p.ldy + n] = bf16_bits(v);
@@ -427,7 +446,14 @@ MOLT_DEV void gd_compute(const GdRound<RW, IPR>& R, const GemvParams& p, const u
 
 // At K = 4096 with up to two X rows the kernel is held to 128 registers, so two
 // workgroups fit on a CU.
-template <int RW, int IPR, int MX>
+//
+// MAXR > 0: at most MAXR rounds per wave, all issued up front in straight-line
+// code (rounds past `rounds` load the clamped last row and are not computed),
+// each round's arithmetic starting as soon as its own loads have landed, and
+// every store after the last round: with no branch between a load and its use
+// the compiler's waits count exactly the later loads still in flight. MAXR = 0:
+// any number of rounds, loaded two ahead in three rotating register sets.
+template <int RW, int IPR, int MX, bool NESTED, bool LORA, int MAXR>
 __global__ __launch_bounds__(GD_NT) __attribute__((amdgpu_waves_per_eu(IPR == 2 && MX <= 2 ? 4 : 1)))
 void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
   __shared__ GdSmem sm;
@@ -463,19 +489,34 @@ void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
     const int m = c / XCH < p.M ? c / XCH : p.M - 1;
     xr[it] = *reinterpret_cast<const u32x4_t*>(p.x + m * p.ldx + 8 * (c % XCH));
   }
-  const float c2 = p.code2 ? p.code2[tid & 255] : 0.0f;
+  // unconditional loads here too (clamped, then masked): see gd_load
+  float c2 = 0.0f;
+  if constexpr (NESTED) c2 = p.code2[tid & 255];
   float lt[MX][2];
 #pragma unroll
   for (int m = 0; m < MX; ++m) {
     const int mm = m < p.M ? m : p.M - 1;
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
-      lt[m][q] = lane + 64 * q < p.r ? bf16_to_f32(p.t[mm * p.ldt + lane + 64 * q]) : 0.0f;
+    for (int q = 0; q < 2; ++q) {
+      const int jr = lane + 64 * q;
+      lt[m][q] = 0.0f;
+      if constexpr (LORA) {
+        const float v = bf16_to_f32(p.t[mm * p.ldt + (jr < p.r ? jr : p.r - 1)]);
+        lt[m][q] = jr < p.r ? v : 0.0f;
+      }
+    }
   }
 
-  GdRound<RW, IPR> b0, b1, b2;
-  gd_load(b0, p, nb, lane, KB);
-  if (rounds > 1) gd_load(b1, p, nb + stride, lane, KB);
+  // The small loads above (X, the nested code table, T) are issued before any
+  // weight load and must stay there: a wait for one of them placed after the
+  // weight loads would wait for the whole weight stream too.
+  __builtin_amdgcn_sched_barrier(0);
+  constexpr int NB = MAXR > 0 ? MAXR : 3;
+  const int64_t nf = nb < p.N ? nb : p.N - 1;
+  GdRound<RW, IPR> b[NB];
+  gd_load<RW, IPR, NESTED, LORA>(b[0], p, nb, lane, KB, nf);
+#pragma unroll
+  for (int j = 1; j < (MAXR > 0 ? MAXR : 2); ++j) gd_load<RW, IPR, NESTED, LORA>(b[j], p, nb + j * stride, lane, KB, nf);
 
   // X in LDS by (piece, dword, lane): 16-byte chunk c = 256 i + 4 l + h (elements
   // 2048 i + 32 l + 8 h ..) sits at 256 i + 64 h + l, so the reads of a piece's
@@ -506,20 +547,35 @@ void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
       const float first = p.order ? chi : clo, second = p.order ? clo : chi;
       sm.tab[(hi * 16 + lo) * GV_TABW + copy] = pack_bf16x2(first, second);
     }
-    if (tid < 256) sm.code2s[tid] = c2;
+    sm.code2s[tid & 255] = c2;                       // every thread: no branch around the load
   }
   __syncthreads();
 
   const uint32_t* tab = sm.tab + (lane & 31);
-  for (int j = 0; j < rounds; j += 3) {
-    if (j + 2 < rounds) gd_load(b2, p, nb + (j + 2) * stride, lane, KB);
-    gd_compute<RW, IPR, MX, XREG>(b0, p, tab, gd_xs, xstride, xg, sm.code2s, lt, nb + j * stride, lane);
-    if (j + 1 >= rounds) break;
-    if (j + 3 < rounds) gd_load(b0, p, nb + (j + 3) * stride, lane, KB);
-    gd_compute<RW, IPR, MX, XREG>(b1, p, tab, gd_xs, xstride, xg, sm.code2s, lt, nb + (j + 1) * stride, lane);
-    if (j + 2 >= rounds) break;
-    if (j + 4 < rounds) gd_load(b1, p, nb + (j + 4) * stride, lane, KB);
-    gd_compute<RW, IPR, MX, XREG>(b2, p, tab, gd_xs, xstride, xg, sm.code2s, lt, nb + (j + 2) * stride, lane);
+  if constexpr (MAXR > 0) {
+    float out[MAXR];
+#pragma unroll
+    for (int j = 0; j < MAXR; ++j)
+      out[j] = gd_compute<RW, IPR, MX, XREG>(b[j], p, tab, gd_xs, xstride, xg, sm.code2s, lt, nb + j * stride, lane);
+#pragma unroll
+    for (int j = 0; j < MAXR; ++j)
+      if (j < rounds) gd_store<RW, MX>(p, out[j], nb + j * stride, lane);
+  } else {
+    // Rounds past the last one load the (clamped) last row again and are never
+    // computed: unconditional loads keep the waits exact (see gd_load).
+    for (int j = 0; j < rounds; j += 3) {
+      gd_load<RW, IPR, NESTED, LORA>(b[2], p, nb + (j + 2) * stride, lane, KB, nf);
+      gd_store<RW, MX>(p, gd_compute<RW, IPR, MX, XREG>(b[0], p, tab, gd_xs, xstride, xg, sm.code2s, lt,
+                                                          nb + j * stride, lane), nb + j * stride, lane);
+      if (j + 1 >= rounds) break;
+      gd_load<RW, IPR, NESTED, LORA>(b[0], p, nb + (j + 3) * stride, lane, KB, nf);
+      gd_store<RW, MX>(p, gd_compute<RW, IPR, MX, XREG>(b[1], p, tab, gd_xs, xstride, xg, sm.code2s, lt,
+                                                          nb + (j + 1) * stride, lane), nb + (j + 1) * stride, lane);
+      if (j + 2 >= rounds) break;
+      gd_load<RW, IPR, NESTED, LORA>(b[1], p, nb + (j + 4) * stride, lane, KB, nf);
+      gd_store<RW, MX>(p, gd_compute<RW, IPR, MX, XREG>(b[2], p, tab, gd_xs, xstride, xg, sm.code2s, lt,
+                                                          nb + (j + 2) * stride, lane), nb + (j + 2) * stride, lane);
+    }
   }
 }
 
@@ -824,14 +880,29 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
     const int64_t wgs = ceil_div64(waves, GD_WAVES);
     const int rounds = (int)ceil_div64(w->rows, wgs * GD_WAVES * rw);
     const size_t dyn = ipr == 2 && mx == 1 ? 0 : (size_t)mx * (w->cols + GD_XPAD) * 2;   // X in registers
-#define MOLT_GD(IPRv, MXv) \
-  hipLaunchKernelGGL((nf4_gemv_dot_kernel<1, IPRv, MXv>), dim3((unsigned)wgs), dim3(GD_NT), dyn, st, p, rounds)
+#define MOLT_GDK(IPRv, MXv, NE, LO, MR) \
+  hipLaunchKernelGGL((nf4_gemv_dot_kernel<1, IPRv, MXv, NE, LO, MR>), dim3((unsigned)wgs), dim3(GD_NT), dyn, st, p, \
+                     rounds)
+    // nested statistics with at most 4 rounds per wave (every cfg5 decode shape): straight-line rounds
+#define MOLT_GDS(IPRv, MXv, LO)                                                   \
+  do {                                                                            \
+    if (rounds == 1) MOLT_GDK(IPRv, MXv, true, LO, 1);                                       \
+    else if (rounds == 2) MOLT_GDK(IPRv, MXv, true, LO, 2); else MOLT_GDK(IPRv, MXv, true, LO, 4); \
+  } while (0)
+#define MOLT_GD(IPRv, MXv)                                                                                  \
+  do {                                                                                                      \
+    if (nested && rounds <= 4) { if (r > 0) MOLT_GDS(IPRv, MXv, true); else MOLT_GDS(IPRv, MXv, false); } \
+    else if (nested) { if (r > 0) MOLT_GDK(IPRv, MXv, true, true, 0); else MOLT_GDK(IPRv, MXv, true, false, 0); } \
+    else { if (r > 0) MOLT_GDK(IPRv, MXv, false, true, 0); else MOLT_GDK(IPRv, MXv, false, false, 0); }     \
+  } while (0)
     if (ipr == 2) {
       if (mx == 1) MOLT_GD(2, 1); else if (mx == 2) MOLT_GD(2, 2); else MOLT_GD(2, 4);
     } else {
       if (mx == 1) MOLT_GD(7, 1); else if (mx == 2) MOLT_GD(7, 2); else MOLT_GD(7, 4);
     }
 #undef MOLT_GD
+#undef MOLT_GDS
+#undef MOLT_GDK
     return check_launch(who);
   }
   // 2 <= M <= 16, K of 8 (or a multiple of 7 or 8) 512-element chunks:
