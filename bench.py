@@ -489,9 +489,11 @@ def measured_counters() -> dict:
 
 
 def profile_kernel(which: str, reps: int) -> int:
-    """Run one kernel `reps` times at cfg4 shapes, for rocprofv3 counter passes:
-    'gateup' = the fused gate/up NF4-LoRA GEMM, 'copy' = a 1 GiB device copy
-    (1 GiB read + 1 GiB written) that calibrates FETCH_SIZE / WRITE_SIZE."""
+    """Run one kernel `reps` times at cfg4 shapes, for rocprofv3 passes:
+    'gateup' = the fused gate/up NF4-LoRA GEMM, 'step' = whole gated-MLP steps,
+    'stack' = cfg3 decoder-stack steps, 'hipblaslt' = plain bf16 GEMMs of the
+    step's four shapes (the vendor-library ceiling), 'copy' = a 1 GiB device
+    copy (1 GiB read + 1 GiB written) that calibrates FETCH_SIZE / WRITE_SIZE."""
     import torch
     from molt_amd import ops
 
@@ -506,6 +508,38 @@ def profile_kernel(which: str, reps: int) -> int:
         projs, x, dy, s = make_mlp(4096, 14336, 64, 128.0, 8192, 1337, dev)
         for _ in range(reps):
             mlp_step(projs, x, dy, s)
+    elif which == "stack":
+        cfg3_stack(dev, steps=reps)
+    elif which == "hipblaslt":
+        # plain bf16 GEMMs of the cfg4 step's four contractions (hipBLASLt through torch.mm):
+        # the vendor-library ceiling for these shapes, without NF4 decode or LoRA
+        M, H, I = 8192, 4096, 14336
+        g = torch.Generator(device="cpu").manual_seed(21)
+        x = torch.randn(M, H, generator=g).to(dev, torch.bfloat16)
+        w_gu = torch.randn(H, 2 * I, generator=g).to(dev, torch.bfloat16)      # [K, N] row-major
+        h = torch.randn(M, I, generator=g).to(dev, torch.bfloat16)
+        w_d = torch.randn(I, H, generator=g).to(dev, torch.bfloat16)
+        dy = torch.randn(M, H, generator=g).to(dev, torch.bfloat16)
+        w_dt = torch.randn(H, I, generator=g).to(dev, torch.bfloat16)
+        dgu = torch.randn(M, 2 * I, generator=g).to(dev, torch.bfloat16)
+        w_gut = torch.randn(2 * I, H, generator=g).to(dev, torch.bfloat16)
+        shapes = (("gate/up forward", x, w_gu), ("down forward", h, w_d), ("down dX", dy, w_dt),
+                  ("paired gate/up dX", dgu, w_gut))
+        for _ in range(reps):
+            for name, a, b in shapes:
+                torch.mm(a, b)
+        torch.cuda.synchronize()
+        for name, a, b in shapes:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                torch.mm(a, b)
+            e1.record()
+            e1.synchronize()
+            ms = e0.elapsed_time(e1) / reps
+            tf = 2 * a.shape[0] * a.shape[1] * b.shape[1] / (ms * 1e-3) / 1e12
+            log(f"hipBLASLt bf16 {name} [{a.shape[0]}x{a.shape[1]}]x[{b.shape[0]}x{b.shape[1]}]: {ms:.3f} ms, "
+                f"{tf:.0f} TFLOP/s ({100 * tf / PEAK_BF16_TFLOPS:.1f}% of bf16 peak)")
     else:
         H, I, r, alpha, M = 4096, 14336, 64, 128.0, 8192
         projs, x, _dy, s = make_mlp(H, I, r, alpha, M, 1337, dev)
@@ -588,7 +622,7 @@ def main() -> int:
     ap.add_argument("--no-head", action="store_true", help="skip the LM head + cross-entropy measurement")
     ap.add_argument("--no-dequant", action="store_true", help="skip the standalone dequant measurement")
     ap.add_argument("--no-stack", action="store_true", help="skip the cfg3 28-layer decoder stack")
-    ap.add_argument("--profile-kernel", choices=("gateup", "step", "copy"),
+    ap.add_argument("--profile-kernel", choices=("gateup", "step", "stack", "hipblaslt", "copy"),
                     help="only launch one kernel or one gated-MLP step (for rocprofv3 --pmc passes) and exit")
     ap.add_argument("--reps", type=int, default=3, help="launches for --profile-kernel")
     args = ap.parse_args()
