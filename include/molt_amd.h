@@ -78,11 +78,15 @@ const char* molt_amd_version(void);
  *       else 0..4): largest token count for the streaming dot-product GEMV.
  *   MOLT_TUNE_LORA_DMA      (0 when MOLT_AMD_PJ_NODMA is set, else 1): LDS DMA
  *       staging in the LoRA projection.
+ *   MOLT_TUNE_SPLIT_K       (0 when MOLT_AMD_NO_SPLIT_K is set, else 1): split
+ *       the contraction of a long-K GEMM with few output tiles over
+ *       workgroups (needs the caller's workspace, see below).
  * molt_amd_set_tuning returns MOLT_EINVAL for an unknown key or a value out of
  * range; molt_amd_get_tuning returns -2 for an unknown key. */
 #define MOLT_TUNE_BIG_TILE_MIN 0
 #define MOLT_TUNE_GEMV_DOT_M 1
 #define MOLT_TUNE_LORA_DMA 2
+#define MOLT_TUNE_SPLIT_K 3
 int molt_amd_set_tuning(int32_t key, int64_t value);
 int64_t molt_amd_get_tuning(int32_t key);
 
@@ -145,11 +149,18 @@ int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t ldz, int32_
 /* Y[M, N] = bf16( X . deq(W)^T + T . bf16(s * B)^T ), fp32 accumulation, with
  * X bf16 [M, K], T bf16 [M, r] = molt_lora_project(X, lora_a) and B fp32 [N, r]
  * (row stride r). `w->scales` must be resolved fp32 scales. r = 0 skips LoRA.
+ * When the output has too few 256 x 256 tiles to fill the GPU and K is long,
+ * the contraction is split over workgroups whose fp32 partials go to the
+ * caller's workspace (16-byte aligned, molt_nf4_lora_forward_workspace(M, N, K)
+ * bytes) and are summed in split order (deterministic); a NULL or smaller
+ * workspace runs without the split. Concurrent calls need separate workspaces.
  * Replaces bnb.matmul_4bit + the LoRA epilogue at methods/nf4_lora.py:43-50 and
  * methods/gated_replay.py:211-224. */
+size_t molt_nf4_lora_forward_workspace(int64_t M, int64_t N, int64_t K);
 int molt_nf4_lora_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,
                           const uint16_t* t, int64_t ldt, const float* lora_b, int32_t r,
-                          float scaling, uint16_t* y, int64_t ldy, void* stream);
+                          float scaling, uint16_t* y, int64_t ldy, void* workspace,
+                          size_t workspace_bytes, void* stream);
 
 /* Gate and up projections of a gated MLP in one launch, sharing X:
  *   gate = bf16(X . deq(Wg)^T + T[:, :r] . bf16(sg Bg)^T)
@@ -168,23 +179,27 @@ int molt_nf4_gateup_forward(const uint16_t* x, int64_t ldx, int64_t M, const mol
 /* dX[M, K] = bf16( dY . deq(W) + U . bf16(lora_scale * A) ), U bf16 [M, r] (for
  * the scheduled backward U = molt_lora_project(dY, lora_b, z_mode 2, s) and
  * lora_scale = 1), A fp32 [r, K] (row stride K). r = 0 skips LoRA.
+ * The workspace is that of the split contraction, as in molt_nf4_lora_forward:
+ * molt_nf4_lora_backward_workspace(M, N, K, 1) bytes (N = w->rows, K = w->cols).
  * Replaces the dX half of _ScheduledNF4LoRA.backward (methods/nf4_lora.py:86-101)
  * and packed_nf4_backward_input / packed_nf4_lora_backward_input
  * (methods/nf4_backward.py:167-284). */
+size_t molt_nf4_lora_backward_workspace(int64_t M, int64_t N, int64_t K, int32_t segments);
 int molt_nf4_lora_backward_input(const uint16_t* dy, int64_t lddy, int64_t M,
                                  const molt_nf4_weight* w, const uint16_t* u, int64_t ldu,
                                  const float* lora_a, int32_t r, float lora_scale, uint16_t* dx,
-                                 int64_t lddx, void* stream);
+                                 int64_t lddx, void* workspace, size_t workspace_bytes, void* stream);
 
 /* dX = dY0 . deq(W0) + dY1 . deq(W1) + U0 . bf16(A0) + U1 . bf16(A1): the input
  * gradient of the gate and up projections of a gated MLP in one contraction
- * (methods/gated_replay.py:167-186). */
+ * (methods/gated_replay.py:167-186). Workspace: molt_nf4_lora_backward_workspace(M,
+ * N, K, 2) bytes for the split contraction (see molt_nf4_lora_forward). */
 int molt_nf4_lora_backward_input_pair(const uint16_t* dy0, const uint16_t* dy1, int64_t lddy,
                                       int64_t M, const molt_nf4_weight* w0,
                                       const molt_nf4_weight* w1, const uint16_t* u0,
                                       const uint16_t* u1, int64_t ldu, const float* a0,
                                       const float* a1, int32_t r, uint16_t* dx, int64_t lddx,
-                                      void* stream);
+                                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* SwiGLU backward fused into the down projection's input gradient
  * (methods/gated_replay.py:376-387; kernels/gated_activation.py:44-51):

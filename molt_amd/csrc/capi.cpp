@@ -33,7 +33,7 @@ int check_launch(const char* what) {
 // relaxed atomic load per call.
 namespace {
 struct Tuning {
-  std::atomic<int64_t> v[3];
+  std::atomic<int64_t> v[4];
   Tuning() {
     const char* e = getenv("MOLT_AMD_BIG_TILE_MIN");
     v[MOLT_TUNE_BIG_TILE_MIN].store(e ? atoll(e) : 256);
@@ -41,6 +41,7 @@ struct Tuning {
     const int64_t m = e ? atoll(e) : -1;
     v[MOLT_TUNE_GEMV_DOT_M].store(m < -1 ? -1 : (m > 4 ? 4 : m));
     v[MOLT_TUNE_LORA_DMA].store(getenv("MOLT_AMD_PJ_NODMA") ? 0 : 1);
+    v[MOLT_TUNE_SPLIT_K].store(getenv("MOLT_AMD_NO_SPLIT_K") ? 0 : 1);
   }
 };
 Tuning& tuning() {
@@ -52,6 +53,7 @@ bool tuning_ok(int32_t key, int64_t value) {
     case MOLT_TUNE_BIG_TILE_MIN: return value >= 0;
     case MOLT_TUNE_GEMV_DOT_M: return value >= -1 && value <= 4;
     case MOLT_TUNE_LORA_DMA: return value == 0 || value == 1;
+    case MOLT_TUNE_SPLIT_K: return value == 0 || value == 1;
     default: return false;
   }
 }
@@ -77,13 +79,13 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
                                           const molt_nf4_weight* w1, const uint16_t* t, int64_t ldt, int lr,
                                           const float* b0, const float* b1, int64_t ldb, int r, float s0, float s1,
                                           uint16_t* y0, uint16_t* y1, uint16_t* y2, int64_t ldy,
-                                          hipStream_t stream);
+                                          void* workspace, size_t workspace_bytes, hipStream_t stream);
 extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* dy1, int64_t lddy, int64_t M,
                                            const molt_nf4_weight* w0, const molt_nf4_weight* w1,
                                            const uint16_t* u0, const uint16_t* u1, int64_t ldu, const float* a0,
                                            const float* a1, int64_t lda, int r, float lora_scale, uint16_t* dx,
                                            int64_t lddx, const uint16_t* gate, const uint16_t* up, uint16_t* dg, uint16_t* du,
-                                           int64_t ldg, hipStream_t stream);
+                                           int64_t ldg, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 extern "C" {
 
@@ -99,15 +101,15 @@ int molt_amd_set_tuning(int32_t key, int64_t value) {
 }
 
 int64_t molt_amd_get_tuning(int32_t key) {
-  return key >= 0 && key <= MOLT_TUNE_LORA_DMA ? molt::tuning_value(key) : -2;
+  return key >= 0 && key <= MOLT_TUNE_SPLIT_K ? molt::tuning_value(key) : -2;
 }
 
 int molt_nf4_lora_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,
                           const uint16_t* t, int64_t ldt, const float* lora_b, int32_t r, float scaling,
-                          uint16_t* y, int64_t ldy, void* stream) {
+                          uint16_t* y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
   if (!w) return molt::set_error(MOLT_EINVAL, "molt_nf4_lora_forward: null weight");
   return molt_nf4_lora_forward_impl(x, ldx, M, w, nullptr, t, ldt, r, lora_b, nullptr, r, r, scaling, scaling,
-                                    y, nullptr, nullptr, ldy, (hipStream_t)stream);
+                                    y, nullptr, nullptr, ldy, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int molt_nf4_gateup_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* wg,
@@ -116,25 +118,27 @@ int molt_nf4_gateup_forward(const uint16_t* x, int64_t ldx, int64_t M, const mol
                             uint16_t* h, int64_t ldo, void* stream) {
   if (!wg || !wu) return molt::set_error(MOLT_EINVAL, "molt_nf4_gateup_forward: null weight");
   return molt_nf4_lora_forward_impl(x, ldx, M, wg, wu, t, ldt, 2 * r, bg, bu, r, r, sg, su, gate, up, h, ldo,
-                                    (hipStream_t)stream);
+                                    nullptr, 0, (hipStream_t)stream);
 }
 
 int molt_nf4_lora_backward_input(const uint16_t* dy, int64_t lddy, int64_t M, const molt_nf4_weight* w,
                                  const uint16_t* u, int64_t ldu, const float* lora_a, int32_t r, float lora_scale,
-                                 uint16_t* dx, int64_t lddx, void* stream) {
+                                 uint16_t* dx, int64_t lddx, void* workspace, size_t workspace_bytes, void* stream) {
   if (!w) return molt::set_error(MOLT_EINVAL, "molt_nf4_lora_backward_input: null weight");
   return molt_nf4_lora_backward_impl(dy, nullptr, lddy, M, w, nullptr, u, nullptr, ldu, lora_a, nullptr, w->cols,
-                                     r, lora_scale, dx, lddx, nullptr, nullptr, nullptr, nullptr, 0,
-                                     (hipStream_t)stream);
+                                     r, lora_scale, dx, lddx, nullptr, nullptr, nullptr, nullptr, 0, workspace,
+                                     workspace_bytes, (hipStream_t)stream);
 }
 
 int molt_nf4_lora_backward_input_pair(const uint16_t* dy0, const uint16_t* dy1, int64_t lddy, int64_t M,
                                       const molt_nf4_weight* w0, const molt_nf4_weight* w1, const uint16_t* u0,
                                       const uint16_t* u1, int64_t ldu, const float* a0, const float* a1,
-                                      int32_t r, uint16_t* dx, int64_t lddx, void* stream) {
+                                      int32_t r, uint16_t* dx, int64_t lddx, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
   if (!w0 || !w1) return molt::set_error(MOLT_EINVAL, "molt_nf4_lora_backward_input_pair: null weight");
   return molt_nf4_lora_backward_impl(dy0, dy1, lddy, M, w0, w1, u0, u1, ldu, a0, a1, w0->cols, r, 1.0f, dx, lddx,
-                                     nullptr, nullptr, nullptr, nullptr, 0, (hipStream_t)stream);
+                                     nullptr, nullptr, nullptr, nullptr, 0, workspace, workspace_bytes,
+                                     (hipStream_t)stream);
 }
 
 int molt_nf4_swiglu_backward(const uint16_t* dy, int64_t lddy, int64_t M, const molt_nf4_weight* wd,
@@ -144,7 +148,7 @@ int molt_nf4_swiglu_backward(const uint16_t* dy, int64_t lddy, int64_t M, const 
   if (M == 0) return MOLT_OK;   // an empty token batch: the outputs are empty too (their pointers may be null)
   if (!dgate) return molt::set_error(MOLT_EINVAL, "molt_nf4_swiglu_backward: null dgate");
   return molt_nf4_lora_backward_impl(dy, nullptr, lddy, M, wd, nullptr, u, nullptr, ldu, lora_a, nullptr, wd->cols,
-                                     r, 1.0f, nullptr, 0, gate, up, dgate, dup, ldg, (hipStream_t)stream);
+                                     r, 1.0f, nullptr, 0, gate, up, dgate, dup, ldg, nullptr, 0, (hipStream_t)stream);
 }
 
 }  // extern "C"

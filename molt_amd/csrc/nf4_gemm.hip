@@ -23,6 +23,8 @@
 // same (m, i) and the epilogue writes g, u and h = bf16(bf16(silu(g)) u).
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "mfma_core.h"
 
 namespace molt {
@@ -48,6 +50,10 @@ struct FwdParams {
   const float* lb[2]; int64_t ldlb; int r; float s[2];
   uint16_t* y[3]; int64_t ldy;                 // single: y[0]; pair: g, u, h
   int vec_out;
+  // split-K (large-tile single-output kernel only): blockIdx.y = split, each
+  // split runs split_steps (even) 64-deep steps and writes an fp32 partial
+  // tile to part[split][M][N]; null part = no split
+  int split_steps; float* part;
 };
 
 struct BwdParams {
@@ -61,6 +67,7 @@ struct BwdParams {
   uint16_t* dx; int64_t lddx;
   const uint16_t* gate; const uint16_t* up; uint16_t* dg; uint16_t* du; int64_t ldg;
   int vec_out;
+  int split_steps; float* part;   // split-K of the plain-store large-tile kernel (see FwdParams)
 };
 
 struct Smem {
@@ -835,6 +842,25 @@ MOLT_DEV void gateup_store(const EpTile& ep, const FwdParams& p, int64_t m0, int
   }
 }
 
+// fp32 partial tile of a split-K launch: part[m][n0 ..] (row stride N, N a
+// multiple of 256 so every 4-element group is inside the row), rows past M skipped.
+MOLT_DEV void store_partial(float* part, int64_t M, int64_t N, const f32x16_t (&acc)[TM][TN], int64_t m0, int64_t n0,
+                            int wm, int wn, int lane) {
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t m = m0 + wm * WCOLS + j * 32 + (lane & 31);
+    if (m >= M) continue;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t n = n0 + wn * WROWS + i * 32 + 8 * g + 4 * (lane >> 5);
+        const f32x4_t v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        *reinterpret_cast<f32x4_t*>(part + m * N + n) = v;
+      }
+  }
+}
+
 // Forward NF4 GEMM, 256 x 256 tile, 8 waves of 128 (W rows) x 64 (X rows).
 //
 // Pipeline of step s (BK = 64 contraction elements), all from LDS buffer s&1:
@@ -901,17 +927,20 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
   };
   const int ks = (int)(p.K / BK);
   const int64_t klast = p.K - BK;
+  // this workgroup's steps: all of them, or split blockIdx.y's range (an even count)
+  const int sbeg = p.part ? (int)blockIdx.y * p.split_steps : 0;
+  const int send = p.part ? min(ks, sbeg + p.split_steps) : ks;
   WBytes r0, r1;
-  x_load(xb0, 0);
-  w_load(r0, 0);
+  x_load(xb0, (int64_t)sbeg * BK);
+  w_load(r0, (int64_t)sbeg * BK);
   wait_vm0();
-  __syncthreads();  // table, X(0)
+  __syncthreads();  // table, X(sbeg)
   {
     float2 c[4];
 #pragma unroll
     for (int d = 0; d < 4; ++d) { w_lookup(r0, tabc, d, c); w_finish(c, r0.sc, wb0, wR, wh, d); }
   }
-  w_load(r0, min((int64_t)BK, klast));
+  w_load(r0, min((int64_t)(sbeg + 1) * BK, klast));
   wait_vm0();
   __syncthreads();
 
@@ -946,12 +975,14 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
     step_barrier();
   };
   // W(s + 1) sits in r0 during even steps and in r1 during odd ones; the LDS buffers alternate likewise.
-  for (int s = 0; s < ks; s += 2) {
+  for (int s = sbeg; s < send; s += 2) {
     step(s, r0, r1, xb0, wb0, xb1, wb1);
     step(s + 1, r1, r0, xb1, wb1, xb0, wb0);
   }
   mfma_set(a[1], b[1], acc);
-  for (int64_t c0 = 0; c0 < p.lr; c0 += BK) {
+  // the LoRA steps belong to the last split (uniform per workgroup)
+  const int64_t lr = !p.part || blockIdx.y + 1 == gridDim.y ? p.lr : 0;
+  for (int64_t c0 = 0; c0 < lr; c0 += BK) {
     lora_a_stage(xb0, p.t, p.ldt, m0, p.M, c0, p.lr, tid);
     lora_wrow_stage(wb0, p, tn, PAIR, c0, tid);
     __syncthreads();
@@ -960,6 +991,10 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
   }
 
   if (!PAIR) {
+    if (p.part) {
+      store_partial(p.part + (int64_t)blockIdx.y * p.M * p.N, p.M, p.N, acc, m0, tn * BN, wm, wn, lane);
+      return;
+    }
     const bool vec = p.vec_out != 0;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
@@ -1247,13 +1282,16 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
     }
   };
 
+  // this workgroup's steps: all of them, or split blockIdx.y's range (an even count)
+  const int sbeg = p.part ? (int)blockIdx.y * p.split_steps : 0;
+  const int send = p.part ? min(ks, sbeg + p.split_steps) : ks;
   WPatch r0, r1;
-  x_load(xb0, 0);
-  w_load(r0, 0);
+  x_load(xb0, sbeg);
+  w_load(r0, sbeg);
   wait_vm0();
-  __syncthreads();  // table, X(0)
+  __syncthreads();  // table, X(sbeg)
   wp_commit(r0, tabc, wb0, cg, rg);
-  w_load(r0, 1);
+  w_load(r0, sbeg + 1);
   wait_vm0();
   __syncthreads();
 
@@ -1303,12 +1341,14 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
     wait_vm_at_most<WPatch::kLoads>();            // dY(s + 1) landed; only W(s + 2)'s loads may fly
     step_barrier();
   };
-  for (int s = 0; s < ks; s += 2) {
+  for (int s = sbeg; s < send; s += 2) {
     step(s, r0, r1, xb0, wb0, xb1, wb1);
     step(s + 1, r1, r0, xb1, wb1, xb0, wb0);
   }
   mfma_set(a[1], b[1], acc);
-  for (int seg = 0; seg < p.nseg && p.r > 0; ++seg) {
+  // the LoRA steps belong to the last split (uniform per workgroup)
+  const int lr = !p.part || blockIdx.y + 1 == gridDim.y ? p.r : 0;
+  for (int seg = 0; seg < p.nseg && lr > 0; ++seg) {
     for (int64_t c0 = 0; c0 < p.r; c0 += BK) {
       lora_a_stage(xb0, sel(p.u, seg), p.ldu, m0, p.M, c0, p.r, tid);
       lora_wcol_stage(wb0, p, seg, tn, c0, tid);
@@ -1318,6 +1358,10 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
     }
   }
 
+  if (EPI == EPI_STORE && p.part) {
+    store_partial(p.part + (int64_t)blockIdx.y * p.M * p.Kw, p.M, p.Kw, acc, m0, tn * BN, wm, wn, lane);
+    return;
+  }
   if (EPI == EPI_STORE) {
     const bool vec = p.vec_out != 0;
 #pragma unroll
@@ -1348,6 +1392,30 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
 
 }  // namespace big
 
+// y[m, n] = bf16(sum over splits s = 0, 1, .. of part[s][m][n]): the splits
+// are added in order, so the result does not depend on which workgroup of the
+// split-K launch finished first. Four consecutive n per thread (N % 4 == 0).
+__global__ void split_sum_kernel(const float* __restrict__ part, int splits, int64_t M, int64_t N,
+                                 uint16_t* __restrict__ y, int64_t ldy) {
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= M * (N / 4)) return;
+  const int64_t m = q / (N / 4), n = 4 * (q - m * (N / 4));
+  f32x4_t v = *reinterpret_cast<const f32x4_t*>(part + m * N + n);
+  for (int s = 1; s < splits; ++s) {
+    const f32x4_t w = *reinterpret_cast<const f32x4_t*>(part + (int64_t)s * M * N + m * N + n);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] += w[e];
+  }
+  uint16_t* dst = y + m * ldy + n;
+  if (((uintptr_t)dst & 7) == 0) {
+    const u32x2_t o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    *reinterpret_cast<u32x2_t*>(dst) = o;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[e] = bf16_bits(v[e]);
+  }
+}
+
 // ------------------------------------------------------------- host helpers
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
@@ -1355,6 +1423,22 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 // better. The MOLT_TUNE_BIG_TILE_MIN setting overrides the threshold (tests use
 // it to run the large-tile kernels at small shapes).
 int64_t big_tile_min() { return molt::tuning_value(MOLT_TUNE_BIG_TILE_MIN); }
+
+// Split-K plan of a plain-store large-tile GEMM whose output has fewer tiles
+// than big_tile_min() (too few to fill the GPU) but a long contraction: S
+// splits of an even number (>= 16) of 64-deep steps, S the largest with
+// tiles * S <= CUs (at most 8). Returns S (1 = no split) and the steps per split.
+int split_plan(int64_t tiles, int64_t steps, int& split_steps) {
+  split_steps = (int)steps;
+  if (molt::tuning_value(MOLT_TUNE_SPLIT_K) == 0 || tiles >= big_tile_min()) return 1;
+  int S = (int)std::min<int64_t>(8, molt::device_cus() / std::max<int64_t>(tiles, 1));
+  while (S > 1 && steps / S < 16) --S;
+  if (S <= 1) return 1;
+  split_steps = (int)(2 * ceil_div64(ceil_div64(steps, S), 2));
+  return (int)ceil_div64(steps, split_steps);
+}
+
+size_t split_bytes(int S, int64_t M, int64_t N) { return S > 1 ? (size_t)S * M * N * sizeof(float) : 0; }
 
 int check_weight_for_gemm(const molt_nf4_weight* w, const char* who) {
   MOLT_REQUIRE(w && w->packed && w->code, MOLT_EINVAL, "%s: weight, packed and code are required", who);
@@ -1380,7 +1464,8 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
                                           const uint16_t* t, int64_t ldt, int lr,
                                           const float* b0, const float* b1, int64_t ldb, int r,
                                           float s0, float s1, uint16_t* y0, uint16_t* y1,
-                                          uint16_t* y2, int64_t ldy, hipStream_t stream) {
+                                          uint16_t* y2, int64_t ldy, void* workspace, size_t workspace_bytes,
+                                          hipStream_t stream) {
   const char* who = "molt_nf4_lora_forward";
   int rc = check_weight_for_gemm(w0, who);
   if (rc) return rc;
@@ -1422,6 +1507,20 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
     else hipLaunchKernelGGL((big::fwd_kernel<false>), grid, block, 0, stream, p);
     return check_launch(who);
   }
+  if (big_ok && !pair && p.N % big::BN == 0) {
+    int split_steps = 0;
+    const int S = split_plan(big_tiles, p.K / BK, split_steps);
+    const size_t need = split_bytes(S, M, p.N);
+    if (S > 1 && workspace && workspace_bytes >= need && aligned(workspace, 16)) {
+      p.split_steps = split_steps;
+      p.part = static_cast<float*>(workspace);
+      hipLaunchKernelGGL((big::fwd_kernel<false>), dim3((unsigned)big_tiles, (unsigned)S), dim3(big::NT), 0, stream, p);
+      const int64_t q = M * (p.N / 4);
+      hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)ceil_div64(q, 256)), dim3(256), 0, stream, p.part, S, M, p.N,
+                         y0, ldy);
+      return check_launch(who);
+    }
+  }
   const int64_t cols_per_tile = pair ? BN / 2 : BN;
   const int64_t tiles = ceil_div64(M, BM) * ceil_div64(p.N, cols_per_tile);
   MOLT_REQUIRE(tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
@@ -1442,8 +1541,8 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
                                            const uint16_t* u1, int64_t ldu, const float* a0,
                                            const float* a1, int64_t lda, int r, float lora_scale,
                                            uint16_t* dx, int64_t lddx, const uint16_t* gate, const uint16_t* up,
-                                           uint16_t* dg, uint16_t* du, int64_t ldg,
-                                           hipStream_t stream) {
+                                           uint16_t* dg, uint16_t* du, int64_t ldg, void* workspace,
+                                           size_t workspace_bytes, hipStream_t stream) {
   const char* who = "molt_nf4_lora_backward_input";
   int rc = check_weight_for_gemm(w0, who);
   if (rc) return rc;
@@ -1499,6 +1598,21 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
     else hipLaunchKernelGGL((big::bwd_kernel<EPI_STORE>), grid, block, 0, stream, p);
     return check_launch(who);
   }
+  if (big_ok && !swiglu && p.Kw % big::BN == 0) {
+    int split_steps = 0;
+    const int S = split_plan(big_tiles, nseg * (p.Nw / BK), split_steps);
+    const size_t need = split_bytes(S, M, p.Kw);
+    if (S > 1 && workspace && workspace_bytes >= need && aligned(workspace, 16)) {
+      p.split_steps = split_steps;
+      p.part = static_cast<float*>(workspace);
+      hipLaunchKernelGGL((big::bwd_kernel<EPI_STORE>), dim3((unsigned)big_tiles, (unsigned)S), dim3(big::NT), 0, stream,
+                         p);
+      const int64_t q = M * (p.Kw / 4);
+      hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)ceil_div64(q, 256)), dim3(256), 0, stream, p.part, S, M, p.Kw,
+                         dx, lddx);
+      return check_launch(who);
+    }
+  }
   const int64_t tiles = ceil_div64(M, BM) * ceil_div64(p.Kw, BN);
   MOLT_REQUIRE(tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
   dim3 grid((unsigned)tiles), block(NT);
@@ -1510,4 +1624,20 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
     else hipLaunchKernelGGL((nf4_bwd_kernel<EPI_STORE, false>), grid, block, 0, stream, p);
   }
   return check_launch(who);
+}
+
+// Workspace of molt_nf4_lora_forward / molt_nf4_lora_backward_input(_pair): the
+// split-K partials when the plan splits (see split_plan), else 0.
+extern "C" size_t molt_nf4_lora_forward_workspace(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N % big::BN != 0 || K % 128 != 0) return 0;
+  const int64_t tiles = ceil_div64(M, big::BM) * (N / big::BN);
+  int split_steps = 0;
+  return split_bytes(split_plan(tiles, K / BK, split_steps), M, N);
+}
+
+extern "C" size_t molt_nf4_lora_backward_workspace(int64_t M, int64_t Nw, int64_t Kw, int32_t nseg) {
+  if (M <= 0 || Kw % big::BN != 0 || Nw % 64 != 0 || (nseg * (Nw / 64)) % 2 != 0) return 0;
+  const int64_t tiles = ceil_div64(M, big::BM) * (Kw / big::BN);
+  int split_steps = 0;
+  return split_bytes(split_plan(tiles, nseg * (Nw / BK), split_steps), M, Kw);
 }

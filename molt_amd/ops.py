@@ -387,8 +387,10 @@ def nf4_lora_forward(x: Tensor, packed: Tensor, scales: Tensor, code: Tensor, ro
         r = tt.shape[1]
         if bb.shape != (rows, r):
             raise ValueError(f"{what}: LoRA B shape {tuple(bb.shape)} != ({rows}, {r})")
+    ws_bytes = int(_lib.load().molt_nf4_lora_forward_workspace(x.shape[0], rows, cols))
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     _call("molt_nf4_lora_forward", x.data_ptr(), cols, x.shape[0], C.byref(w), _ptr(tt), max(r, 1),
-          _ptr(bb), r, float(scaling), y.data_ptr(), rows, _stream(dev))
+          _ptr(bb), r, float(scaling), y.data_ptr(), rows, _ptr(ws), ws_bytes, _stream(dev))
     return y
 
 
@@ -467,8 +469,10 @@ def nf4_lora_backward_input(dy: Tensor, packed: Tensor, scales: Tensor, code: Te
             raise ValueError("LoRA gradient rows must match the output gradient")
         if aa.dim() != 2 or aa.shape != (r, cols):
             raise ValueError("LoRA gradient and A matrix dimensions are incompatible")
+    ws_bytes = int(_lib.load().molt_nf4_lora_backward_workspace(dy.shape[0], rows, cols, 1))
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     _call("molt_nf4_lora_backward_input", dy.data_ptr(), rows, dy.shape[0], C.byref(w), _ptr(uu),
-          max(r, 1), _ptr(aa), r, float(lora_scale), dx.data_ptr(), cols, _stream(dev))
+          max(r, 1), _ptr(aa), r, float(lora_scale), dx.data_ptr(), cols, _ptr(ws), ws_bytes, _stream(dev))
     return dx
 
 
@@ -510,9 +514,11 @@ def nf4_lora_backward_input_pair(dy0: Tensor, dy1: Tensor, packed0: Tensor, scal
         r = uu0.shape[1]
         if uu1.shape != uu0.shape or aa0.shape != (r, cols) or aa1.shape != (r, cols):
             raise ValueError("LoRA gradient and A matrix dimensions are incompatible")
+    ws_bytes = int(_lib.load().molt_nf4_lora_backward_workspace(m, rows, cols, 2))
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     _call("molt_nf4_lora_backward_input_pair", dy0.data_ptr(), dy1.data_ptr(), rows, m, C.byref(w0),
           C.byref(w1), _ptr(uu0), _ptr(uu1), max(r, 1), _ptr(aa0), _ptr(aa1), r, dx.data_ptr(), cols,
-          _stream(dev))
+          _ptr(ws), ws_bytes, _stream(dev))
     return dx
 
 

@@ -189,3 +189,18 @@ def test_noalloc_gemv_refuses_oversized_partials_before_any_device_call():
     rc = lib.molt_nf4_gemv_noalloc(None, 14336, 16, w, None, 1, None, 0, 0.0, None, 40000, None)
     assert rc == _lib.MOLT_EUNSUPPORTED
     assert b"static scratch" in lib.molt_amd_last_error()
+
+
+def test_split_k_workspace_queries_need_no_gpu():
+    """The split plan: a long contraction with few 256 x 256 output tiles gets
+    fp32 partials for S splits; a problem that fills the GPU gets none."""
+    lib = _lib.load()
+    assert lib.molt_nf4_lora_forward_workspace(8192, 14336, 4096) == 0
+    assert lib.molt_nf4_lora_forward_workspace(4096, 1536, 8960) == 2 * 4096 * 1536 * 4
+    assert lib.molt_nf4_lora_backward_workspace(4096, 8960, 1536, 2) == 2 * 4096 * 1536 * 4
+    assert lib.molt_nf4_lora_backward_workspace(8192, 14336, 4096, 2) == 0
+    assert lib.molt_nf4_lora_forward_workspace(4096, 1000, 8960) == 0       # N not a multiple of 256
+    from molt_amd._lib import tuning
+
+    with tuning(split_k=0):
+        assert lib.molt_nf4_lora_forward_workspace(4096, 1536, 8960) == 0

@@ -28,7 +28,7 @@ def _both(monkeypatch, fn):
 
     with tuning(big_tile_min=1):
         big = fn()
-    with tuning(big_tile_min=1 << 40):
+    with tuning(big_tile_min=1 << 40, split_k=0):
         small = fn()
     return big, small
 
