@@ -286,6 +286,13 @@ class _RMSNormReplayRecipe:
         return ops.direct.rmsnorm_forward(self.source, self.weight, float(self.eps), float(self.weight_offset))
 
 
+def _leave_recipe(mlp: torch.nn.Module, norm: torch.nn.Module, source: torch.Tensor, output: torch.Tensor) -> None:
+    keep = torch.is_grad_enabled() and output.dtype == torch.bfloat16
+    mlp._molt_norm_replay_recipe = _RMSNormReplayRecipe(
+        source=source, weight=norm.weight, eps=float(norm.variance_epsilon),
+        weight_offset=float(norm.weight_offset), target=output) if keep else None
+
+
 def _leave_replay_recipe(mlp: torch.nn.Module):
     """Forward hook for a frozen RMSNorm: after each call it leaves on ``mlp``
     the recipe that recomputes the norm's output from its input, or None when
@@ -294,12 +301,19 @@ def _leave_replay_recipe(mlp: torch.nn.Module):
     that very output (methods/gated_replay.py:13-47)."""
 
     def hook(norm: torch.nn.Module, inputs: tuple, output: torch.Tensor) -> None:
-        keep = torch.is_grad_enabled() and output.dtype == torch.bfloat16
-        mlp._molt_norm_replay_recipe = _RMSNormReplayRecipe(
-            source=inputs[0], weight=norm.weight, eps=float(norm.variance_epsilon),
-            weight_offset=float(norm.weight_offset), target=output) if keep else None
+        _leave_recipe(mlp, norm, inputs[0], output)
 
     return hook
+
+
+def _replayable_norm_forward(module: torch.nn.Module, hidden: torch.Tensor, *args: Any, **kwargs: Any) -> torch.Tensor:
+    """The reference's forward replacement for a norm wired by hand
+    (methods/gated_replay.py:32-47): runs ``module._molt_original_forward`` and
+    leaves the recipe on ``module._molt_target_mlp``, as the hook of
+    :func:`enable_rmsnorm_replay` does."""
+    result = module._molt_original_forward(hidden, *args, **kwargs)
+    _leave_recipe(module._molt_target_mlp, module, hidden, result)
+    return result
 
 
 class _ResidualRecipeGatedNF4LoRA(torch.autograd.Function):
