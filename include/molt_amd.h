@@ -223,6 +223,24 @@ int molt_lora_grad(const uint16_t* l, const uint16_t* l2, int64_t ldl, int32_t l
                    float scale, float* out, int32_t out_layout, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* molt_lora_grad with the frozen RMSNorm's output as L, formed as it is
+ * staged: L(m, p) = bf16(fp32(x(m, p)) * inv_rms[m] * (fp32(w[p]) + offset)),
+ * the products and roundings of molt_rmsnorm_forward, so the result is
+ * bitwise that of molt_lora_grad over the materialised norm output when
+ * inv_rms comes from molt_rmsnorm_forward on the same x and weight. x bf16
+ * [M, P] (row stride ldx), inv_rms fp32 [M], w bf16 or fp32 [P] (w_dtype).
+ * Same workspace as molt_lora_grad (molt_lora_grad_workspace(M, P, Q)).
+ * Requires 16-byte aligned rows of x and rmat and P, Q multiples of 8, else
+ * MOLT_EUNSUPPORTED. Replaces the replay of the normalised input for the
+ * gate/up adapters' dA in _ResidualRecipeGatedNF4LoRA.backward
+ * (methods/gated_replay.py:146-151,167-184), which the reference
+ * materialises (_RMSNormReplayRecipe.materialize, :22-30). */
+int molt_lora_grad_rmsnorm(const uint16_t* x, int64_t ldx, const float* inv_rms,
+                           const void* norm_weight, int32_t w_dtype, float offset,
+                           const uint16_t* rmat, int64_t ldr, int64_t M, int64_t P, int64_t Q,
+                           float scale, float* out, int32_t out_layout, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Skinny-M NF4 GEMV (M <= 16)                                               */
 /* ------------------------------------------------------------------------ */
@@ -281,6 +299,9 @@ int molt_silu_mul_backward(const void* grad, const void* gate, const void* up, v
  * out = bf16(fp32(fp32(x) * inv) * (fp32(w) + offset)). x is bf16 or fp32
  * (x_dtype) with row stride ldx, weight bf16 or fp32 [H], out bf16 with row
  * stride ldo. inv_rms (fp32 [M], may be NULL) receives inv of every row.
+ * out may be NULL when inv_rms is not: then only inv is computed, bitwise as
+ * by a call whose out rows are 16-byte aligned (the norm-replay gradient,
+ * molt_lora_grad_rmsnorm, uses it).
  * Replaces _FrozenRMSNormFunction.forward (kernels/frozen_rmsnorm.py:10-23) and
  * _RMSNormReplayRecipe.materialize (methods/gated_replay.py:22-30). */
 int molt_rmsnorm_forward(const void* x, int32_t x_dtype, int64_t ldx, int64_t M, int64_t H,

@@ -69,6 +69,8 @@ SIGNATURES: dict[str, tuple] = {
     "molt_lora_grad_workspace": (_sz, [_i64, _i64, _i64]),
     "molt_lora_grad": (C.c_int, [_p, _p, _i64, _i32, _p, _i64, _i64, _i64, _i64, _f32, _p, _i32, _p, _sz,
                                  _p]),
+    "molt_lora_grad_rmsnorm": (C.c_int, [_p, _i64, _p, _p, _i32, _f32, _p, _i64, _i64, _i64, _i64, _f32, _p,
+                                         _i32, _p, _sz, _p]),
     "molt_nf4_gemv_workspace": (_sz, [_i64, _i64, _i64]),
     "molt_nf4_gemv": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _f32, _p, _i64, _p, _sz, _p]),
     "molt_nf4_gemv_noalloc_limit": (_sz, []),

@@ -376,15 +376,47 @@ __global__ void proj_reduce_kernel(const float* __restrict__ part, int ks, int64
 constexpr int GR_P = 128, GR_Q = 64, GR_NT = 256;
 constexpr int GR_WROWS = 64, GR_WCOLS = 32;   // waves 2 (p) x 2 (q)
 
+// L operand modes: 0 plain, 1 SwiGLU replay from (gate, up), 2 the frozen
+// RMSNorm output bf16(fp32(x) * inv[m] * (fp32(w) + offset)) replayed from
+// the norm's input x, its per-row inv and its weight.
+constexpr int L_PLAIN = 0, L_REPLAY = 1, L_NORM = 2;
+
 struct GradParams {
   const uint16_t* l; const uint16_t* l2; int64_t ldl; int mode;
   const uint16_t* rm; int64_t ldr;
   int64_t M, P, Q;
   int64_t slice;
   float* part;
+  const float* inv; const void* nw; int nw_f32; float noff;   // L_NORM only
 };
 
-struct Patch { Chunk v[8]; };
+struct Patch {
+  Chunk v[8];
+  float inv[8];   // L_NORM: inv of each patch row
+};
+
+// (fp32(w) + offset) of the 8 columns a thread stages; 1 past the matrix.
+MOLT_DEV void norm_weights(const GradParams& p, int64_t col, float (&wo)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int64_t c = col + e < p.P ? col + e : 0;
+    const float w = p.nw_f32 ? reinterpret_cast<const float*>(p.nw)[c]
+                             : bf16_to_f32(reinterpret_cast<const uint16_t*>(p.nw)[c]);
+    wo[e] = __fadd_rn(w, p.noff);
+  }
+}
+
+// The norm's bf16 output for one loaded chunk, with the products and their
+// order of the RMSNorm forward kernel: bf16((x * inv) * (w + offset)).
+MOLT_DEV u32x4_t norm_value(const Chunk& c, float inv, const float (&wo)[8]) {
+  u32x4_t o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    o[e] = pack_bf16x2(__fmul_rn(__fmul_rn(bf16_lo(c.a[e]), inv), wo[2 * e]),
+                       __fmul_rn(__fmul_rn(bf16_hi(c.a[e]), inv), wo[2 * e + 1]));
+  const uint32_t keep = c.ok ? 0xffffffffu : 0u;
+  return o & keep;
+}
 
 // Which operand and patch a thread stages: waves 0-1 stage the 8 x 16 L
 // patches of a 64 x 128 tile, wave 2 the 8 x 8 R patches of a 64 x 64 tile,
@@ -397,27 +429,38 @@ MOLT_DEV bool patch_role(int wave, int lane, bool& is_l, int& mg, int& cg) {
   return wave < 3;
 }
 
-template <bool VEC, bool REPLAY>
+template <bool VEC, int LM>
 MOLT_DEV void patch_load(Patch& pt, const GradParams& p, int wave, int lane, int64_t m0, int64_t mend,
                          int64_t p0, int64_t q0) {
+  constexpr bool REPLAY = LM == L_REPLAY;
   bool is_l; int mg, cg;
   if (!patch_role(wave, lane, is_l, mg, cg)) return;
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
     const int64_t m = m0 + 8 * mg + r;
-    if (is_l) chunk_load<VEC, REPLAY>(pt.v[r], p.l, p.l2, p.ldl, p.mode, 1.0f, m, mend, p0 + 8 * cg, p.P);
-    else chunk_load<VEC, false>(pt.v[r], p.rm, nullptr, p.ldr, 0, 1.0f, m, mend, q0 + 8 * cg, p.Q);
+    if (is_l) {
+      chunk_load<VEC, REPLAY>(pt.v[r], p.l, p.l2, p.ldl, p.mode, 1.0f, m, mend, p0 + 8 * cg, p.P);
+      if constexpr (LM == L_NORM) pt.inv[r] = p.inv[m < mend ? m : 0];
+    } else {
+      chunk_load<VEC, false>(pt.v[r], p.rm, nullptr, p.ldr, 0, 1.0f, m, mend, q0 + 8 * cg, p.Q);
+    }
   }
 }
 
-template <bool VEC, bool REPLAY>
-MOLT_DEV void patch_store(const Patch& pt, const GradParams& p, uint16_t* ls, uint16_t* rs, int wave, int lane) {
+template <bool VEC, int LM>
+MOLT_DEV void patch_store(const Patch& pt, const GradParams& p, const float (&wo)[8], uint16_t* ls, uint16_t* rs,
+                          int wave, int lane) {
+  constexpr bool REPLAY = LM == L_REPLAY;
   bool is_l; int mg, cg;
   if (!patch_role(wave, lane, is_l, mg, cg)) return;
   u32x4_t v[8];
 #pragma unroll
-  for (int r = 0; r < 8; ++r)
-    v[r] = is_l ? chunk_value<VEC, REPLAY>(pt.v[r], p.mode, 1.0f) : chunk_value<VEC, false>(pt.v[r], 0, 1.0f);
+  for (int r = 0; r < 8; ++r) {
+    if constexpr (LM == L_NORM)
+      v[r] = is_l ? norm_value(pt.v[r], pt.inv[r], wo) : chunk_value<VEC, false>(pt.v[r], 0, 1.0f);
+    else
+      v[r] = is_l ? chunk_value<VEC, REPLAY>(pt.v[r], p.mode, 1.0f) : chunk_value<VEC, false>(pt.v[r], 0, 1.0f);
+  }
   uint16_t* dst = is_l ? ls : rs;
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
@@ -429,12 +472,12 @@ MOLT_DEV void patch_store(const Patch& pt, const GradParams& p, uint16_t* ls, ui
   }
 }
 
-template <bool VEC, bool REPLAY>
+template <bool VEC, int LM>
 __global__ __launch_bounds__(GR_NT) void lora_grad_kernel(const GradParams p) {
   // One LDS tile (27 KB: three workgroups per CU) where the registers allow
-  // three; the SwiGLU-replay variant, held to two by its registers, double-
-  // buffers instead and saves a barrier per step.
-  constexpr int NB = REPLAY ? 2 : 1;
+  // three; the SwiGLU- and RMSNorm-replay variants, held to two by their
+  // registers, double-buffer instead and save a barrier per step.
+  constexpr int NB = LM == L_PLAIN ? 1 : 2;
   __shared__ __attribute__((aligned(16))) uint16_t ls[NB][GR_P * LDSW];
   __shared__ __attribute__((aligned(16))) uint16_t rs[NB][GR_Q * LDSW];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -446,27 +489,32 @@ __global__ __launch_bounds__(GR_NT) void lora_grad_kernel(const GradParams p) {
   const int64_t mend = mbeg + p.slice < p.M ? mbeg + p.slice : p.M;
   const int steps = (int)ceil_div64(mend - mbeg, BK);
 
+  float wo[8] = {};
+  if constexpr (LM == L_NORM) {
+    bool is_l; int mg, cg;
+    if (patch_role(wave, lane, is_l, mg, cg) && is_l) norm_weights(p, p0 + 8 * cg, wo);
+  }
   f32x16_t acc[2][1];
   zero_acc(acc);
   Patch pt;
-  patch_load<VEC, REPLAY>(pt, p, wave, lane, mbeg, mend, p0, q0);
-  patch_store<VEC, REPLAY>(pt, p, ls[0], rs[0], wave, lane);
+  patch_load<VEC, LM>(pt, p, wave, lane, mbeg, mend, p0, q0);
+  patch_store<VEC, LM>(pt, p, wo, ls[0], rs[0], wave, lane);
   __syncthreads();
   if constexpr (NB == 2) {
     for (int s = 0; s < steps; ++s) {
       const int cur = s & 1;
-      if (s + 1 < steps) patch_load<VEC, REPLAY>(pt, p, wave, lane, mbeg + (int64_t)(s + 1) * BK, mend, p0, q0);
+      if (s + 1 < steps) patch_load<VEC, LM>(pt, p, wave, lane, mbeg + (int64_t)(s + 1) * BK, mend, p0, q0);
       mfma_step<2, 1>(ls[cur], rs[cur], wp * GR_WROWS, wq * GR_WCOLS, acc, lane);
-      if (s + 1 < steps) patch_store<VEC, REPLAY>(pt, p, ls[cur ^ 1], rs[cur ^ 1], wave, lane);
+      if (s + 1 < steps) patch_store<VEC, LM>(pt, p, wo, ls[cur ^ 1], rs[cur ^ 1], wave, lane);
       __syncthreads();
     }
   } else {
     for (int s = 0; s < steps; ++s) {
-      if (s + 1 < steps) patch_load<VEC, REPLAY>(pt, p, wave, lane, mbeg + (int64_t)(s + 1) * BK, mend, p0, q0);
+      if (s + 1 < steps) patch_load<VEC, LM>(pt, p, wave, lane, mbeg + (int64_t)(s + 1) * BK, mend, p0, q0);
       mfma_step<2, 1>(ls[0], rs[0], wp * GR_WROWS, wq * GR_WCOLS, acc, lane);
       if (s + 1 >= steps) break;
       __syncthreads();                               // the single tile is consumed
-      patch_store<VEC, REPLAY>(pt, p, ls[0], rs[0], wave, lane);
+      patch_store<VEC, LM>(pt, p, wo, ls[0], rs[0], wave, lane);
       __syncthreads();
     }
   }
@@ -646,6 +694,42 @@ extern "C" size_t molt_lora_grad_workspace(int64_t M, int64_t P, int64_t Q) {
   return (size_t)grad_splits(M, P, Q) * (size_t)P * (size_t)Q * sizeof(float);
 }
 
+// Split over M, launch the gradient kernel and sum the splits (shared by
+// molt_lora_grad and molt_lora_grad_rmsnorm; p carries the operands).
+static int launch_grad(GradParams& p, bool vec, int lm, float scale, float* out, int32_t out_layout,
+                       void* workspace, size_t workspace_bytes, hipStream_t st, const char* who) {
+  const int64_t M = p.M, P = p.P, Q = p.Q;
+  const int S = grad_splits(M, P, Q);
+  const size_t need = (size_t)S * P * Q * sizeof(float);
+  MOLT_REQUIRE(workspace && workspace_bytes >= need, MOLT_EWORKSPACE, "%s: workspace %zu < %zu bytes", who,
+               workspace_bytes, need);
+  p.slice = ceil_div64(ceil_div64(M, S), BK) * BK;
+  p.part = (float*)workspace;
+  const int S_eff = (int)ceil_div64(M, p.slice);
+  dim3 grid((unsigned)ceil_div64(P, GR_P), (unsigned)ceil_div64(Q, GR_Q), (unsigned)S_eff);
+  if (!vec) hipLaunchKernelGGL((lora_grad_kernel<false, L_PLAIN>), grid, dim3(GR_NT), 0, st, p);
+  else if (lm == L_REPLAY) hipLaunchKernelGGL((lora_grad_kernel<true, L_REPLAY>), grid, dim3(GR_NT), 0, st, p);
+  else if (lm == L_NORM) hipLaunchKernelGGL((lora_grad_kernel<true, L_NORM>), grid, dim3(GR_NT), 0, st, p);
+  else hipLaunchKernelGGL((lora_grad_kernel<true, L_PLAIN>), grid, dim3(GR_NT), 0, st, p);
+  int rc = check_launch(who);
+  if (rc) return rc;
+  const int64_t n = P * Q;
+  unsigned blocks = (unsigned)((n + 255) / 256);
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(lora_grad_reduce_kernel, dim3(blocks), dim3(256), 0, st, p.part, S_eff, P, Q, scale, out,
+                     out_layout);
+  return check_launch(who);
+}
+
+// M == 0: the gradient is zero. A fill kernel rather than hipMemsetAsync, so
+// that the call stays correct when a caller captures it into a HIP graph.
+static int zero_grad(float* out, int64_t P, int64_t Q, hipStream_t st, const char* who) {
+  const int64_t n = P * Q;
+  const unsigned blocks = (unsigned)(n / 256 + 1 < 4096 ? n / 256 + 1 : 4096);
+  hipLaunchKernelGGL(zero_fill_kernel, dim3(blocks), dim3(256), 0, st, out, n);
+  return check_launch(who);
+}
+
 extern "C" int molt_lora_grad(const uint16_t* l, const uint16_t* l2, int64_t ldl, int32_t l_mode,
                               const uint16_t* rmat, int64_t ldr, int64_t M, int64_t P, int64_t Q, float scale,
                               float* out, int32_t out_layout, void* workspace, size_t workspace_bytes,
@@ -656,39 +740,35 @@ extern "C" int molt_lora_grad(const uint16_t* l, const uint16_t* l2, int64_t ldl
   MOLT_REQUIRE(M >= 0 && P > 0 && Q > 0, MOLT_EINVAL, "%s: bad shape", who);
   MOLT_REQUIRE(out && ldl >= P && ldr >= Q, MOLT_EINVAL, "%s: bad pointers/strides", who);
   hipStream_t st = (hipStream_t)stream;
-  if (M != 0) {
-    MOLT_REQUIRE(l && rmat, MOLT_EINVAL, "%s: null operand", who);
-    MOLT_REQUIRE(l_mode == 0 || l2, MOLT_EINVAL, "%s: SwiGLU replay needs the up tensor", who);
-  } else {
-    // A fill kernel rather than hipMemsetAsync, so that the call stays
-    // correct when a caller captures it into a HIP graph.
-    const int64_t n = P * Q;
-    const unsigned blocks = (unsigned)(n / 256 + 1 < 4096 ? n / 256 + 1 : 4096);
-    hipLaunchKernelGGL(zero_fill_kernel, dim3(blocks), dim3(256), 0, st, out, n);
-    return check_launch(who);
-  }
-  const int S = grad_splits(M, P, Q);
-  const size_t need = (size_t)S * P * Q * sizeof(float);
-  MOLT_REQUIRE(workspace && workspace_bytes >= need, MOLT_EWORKSPACE, "%s: workspace %zu < %zu bytes", who,
-               workspace_bytes, need);
+  if (M == 0) return zero_grad(out, P, Q, st, who);
+  MOLT_REQUIRE(l && rmat, MOLT_EINVAL, "%s: null operand", who);
+  MOLT_REQUIRE(l_mode == 0 || l2, MOLT_EINVAL, "%s: SwiGLU replay needs the up tensor", who);
   GradParams p{};
   p.l = l; p.l2 = l2; p.ldl = ldl; p.mode = l_mode; p.rm = rmat; p.ldr = ldr;
   p.M = M; p.P = P; p.Q = Q;
-  p.slice = ceil_div64(ceil_div64(M, S), BK) * BK;
-  p.part = (float*)workspace;
   const bool vec = P % 8 == 0 && Q % 8 == 0 && ldl % 8 == 0 && ldr % 8 == 0 && aligned(l, 16) &&
                    aligned(rmat, 16) && (l_mode == 0 || aligned(l2, 16));
-  const int S_eff = (int)ceil_div64(M, p.slice);
-  dim3 grid((unsigned)ceil_div64(P, GR_P), (unsigned)ceil_div64(Q, GR_Q), (unsigned)S_eff);
-  if (!vec) hipLaunchKernelGGL((lora_grad_kernel<false, false>), grid, dim3(GR_NT), 0, st, p);
-  else if (l_mode == 1) hipLaunchKernelGGL((lora_grad_kernel<true, true>), grid, dim3(GR_NT), 0, st, p);
-  else hipLaunchKernelGGL((lora_grad_kernel<true, false>), grid, dim3(GR_NT), 0, st, p);
-  int rc = check_launch(who);
-  if (rc) return rc;
-  const int64_t n = P * Q;
-  unsigned blocks = (unsigned)((n + 255) / 256);
-  if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(lora_grad_reduce_kernel, dim3(blocks), dim3(256), 0, st, p.part, S_eff, P, Q, scale, out,
-                     out_layout);
-  return check_launch(who);
+  return launch_grad(p, vec, l_mode, scale, out, out_layout, workspace, workspace_bytes, st, who);
+}
+
+extern "C" int molt_lora_grad_rmsnorm(const uint16_t* x, int64_t ldx, const float* inv_rms, const void* norm_weight,
+                                      int32_t w_dtype, float offset, const uint16_t* rmat, int64_t ldr, int64_t M,
+                                      int64_t P, int64_t Q, float scale, float* out, int32_t out_layout,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+  const char* who = "molt_lora_grad_rmsnorm";
+  MOLT_REQUIRE(w_dtype == MOLT_DTYPE_BF16 || w_dtype == MOLT_DTYPE_F32, MOLT_EINVAL,
+               "%s: norm weight dtype must be bf16 or fp32", who);
+  MOLT_REQUIRE(out_layout == 0 || out_layout == 1, MOLT_EINVAL, "%s: bad out_layout", who);
+  MOLT_REQUIRE(M >= 0 && P > 0 && Q > 0, MOLT_EINVAL, "%s: bad shape", who);
+  MOLT_REQUIRE(out && ldx >= P && ldr >= Q, MOLT_EINVAL, "%s: bad pointers/strides", who);
+  hipStream_t st = (hipStream_t)stream;
+  if (M == 0) return zero_grad(out, P, Q, st, who);
+  MOLT_REQUIRE(x && inv_rms && norm_weight && rmat, MOLT_EINVAL, "%s: null operand", who);
+  MOLT_REQUIRE(P % 8 == 0 && Q % 8 == 0 && ldx % 8 == 0 && ldr % 8 == 0 && aligned(x, 16) && aligned(rmat, 16),
+               MOLT_EUNSUPPORTED, "%s: needs 16-byte aligned rows and P, Q multiples of 8", who);
+  GradParams p{};
+  p.l = x; p.ldl = ldx; p.mode = L_NORM; p.rm = rmat; p.ldr = ldr;
+  p.M = M; p.P = P; p.Q = Q;
+  p.inv = inv_rms; p.nw = norm_weight; p.nw_f32 = w_dtype == MOLT_DTYPE_F32; p.noff = offset;
+  return launch_grad(p, true, L_NORM, scale, out, out_layout, workspace, workspace_bytes, st, who);
 }

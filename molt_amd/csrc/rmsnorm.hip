@@ -154,6 +154,7 @@ __global__ __launch_bounds__(RN_NT) void rmsnorm_fwd_kernel(const RmsParams p) {
         for (int e = 0; e < 8; ++e) s += __fmul_rn(xv[c][e], xv[c][e]);
       const float inv = rsqrtf(wave_sum(s) * inv_h + p.eps);
       if (p.inv_rms && lane == 0) p.inv_rms[row] = inv;
+      if (!p.out) continue;   // inv only
 #pragma unroll
       for (int c = 0; c < NV; ++c) {
         const int64_t i = 8 * lane + 512 * c;
@@ -168,6 +169,7 @@ __global__ __launch_bounds__(RN_NT) void rmsnorm_fwd_kernel(const RmsParams p) {
     } else {
       const float inv = rsqrtf(row_sumsq<XF32>(xr, p.H, lane) * inv_h + p.eps);
       if (p.inv_rms && lane == 0) p.inv_rms[row] = inv;
+      if (!p.out) continue;
       for (int64_t i = lane; i < p.H; i += 64) {
         const float v = __fmul_rn(__fmul_rn(ld1<XF32>(xr, i), inv), __fadd_rn(ld1<WF32>(p.w, i), p.offset));
         orow[i] = bf16_bits(v);
@@ -311,9 +313,11 @@ extern "C" int molt_rmsnorm_forward(const void* x, int32_t x_dtype, int64_t ldx,
   MOLT_REQUIRE(M >= 0 && H > 0 && ldx >= H && ldo >= H, MOLT_EINVAL, "%s: bad shape (M=%lld H=%lld ldx=%lld ldo=%lld)",
                who, (long long)M, (long long)H, (long long)ldx, (long long)ldo);
   if (M == 0) return MOLT_OK;
-  MOLT_REQUIRE(x && weight && out, MOLT_EINVAL, "%s: null pointer", who);
+  MOLT_REQUIRE(x && weight && (out || inv_rms), MOLT_EINVAL, "%s: null pointer", who);
   const bool xf = x_dtype == MOLT_DTYPE_F32, wf = w_dtype == MOLT_DTYPE_F32;
-  const int nv = pick_nv(H, vec_ok(x, ldx, xf ? 4 : 2) && a16(weight) && vec_ok(out, ldo, 2));
+  // Without out (inv only) the kernel choice is that of a call whose out rows
+  // are 16-byte aligned, so inv is bitwise that of such a call.
+  const int nv = pick_nv(H, vec_ok(x, ldx, xf ? 4 : 2) && a16(weight) && (!out || vec_ok(out, ldo, 2)));
   RmsParams p{x, nullptr, weight, out, inv_rms, ldx, 0, ldo, M, H, eps, offset};
   MOLT_RN_LAUNCH(rmsnorm_fwd_kernel, xf, wf, nv, dim3(rn_grid(M)), (hipStream_t)stream, p);
   return check_launch(who);

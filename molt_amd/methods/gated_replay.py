@@ -186,10 +186,13 @@ def _fused_forward(x, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_p
 
 
 def _fused_backward(grad_output, flat, gate, up, gated, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed,
-                    up_a, up_b, down_packed, down_a, down_b, qs, scaling, dims):
+                    up_a, up_b, down_packed, down_a, down_b, qs, scaling, dims, norm=None):
     """Backward of the fused gated MLP. ``flat`` is the projections' input
     [tokens, H]; ``gated`` is h when the forward kept it, else None (replayed
-    from gate and up). Returns (dX [tokens, H], dA_g, dB_g, dA_u, dB_u, dA_d, dB_d)."""
+    from gate and up). With ``norm = (source, inv_rms, weight, offset)`` and
+    ``flat`` None, the input is the frozen RMSNorm's output, replayed from its
+    bf16 source as the gate/up adapters' gradient stages it.
+    Returns (dX [tokens, H], dA_g, dB_g, dA_u, dB_u, dA_d, dB_d)."""
     gate_qs, up_qs, down_qs = qs
     s_g, s_u, s_d = scaling
     h_dim, i_dim, r = dims
@@ -209,7 +212,11 @@ def _fused_backward(grad_output, flat, gate, up, gated, t_gu, t_d, gate_packed, 
         d_down_a = ops.direct.lora_grad(gate, up, 1, u_d, 1.0, 1)
     d_down_b = ops.direct.lora_grad(dy, None, 0, t_d, s_d, 0)
     # dA_gate and dA_up both contract X: one pass over X with [U_g | U_u]
-    d_gu_a = ops.direct.lora_grad(flat, None, 0, torch.cat([u_g, u_u], 1), 1.0, 1)
+    u_gu = torch.cat([u_g, u_u], 1)
+    if norm is not None:
+        d_gu_a = ops.direct.lora_grad_rmsnorm(norm[0], norm[1], norm[2], norm[3], u_gu, 1.0, 1)
+    else:
+        d_gu_a = ops.direct.lora_grad(flat, None, 0, u_gu, 1.0, 1)
     d_gate_b = ops.direct.lora_grad(dg, None, 0, t_gu[:, :r], s_g, 0)
     d_up_b = ops.direct.lora_grad(du, None, 0, t_gu[:, r:], s_u, 0)
     return dx, d_gu_a[:r], d_gate_b, d_gu_a[r:], d_up_b, d_down_a, d_down_b
@@ -322,10 +329,13 @@ class _ResidualRecipeGatedNF4LoRA(torch.autograd.Function):
 
     Forward is the fused gated MLP on ``normalized``. It saves the residual
     ``source``, gate and up (h is replayed from them, as the reference does),
-    and the two rank-r projections. Backward re-materialises the normalised
-    input from the source with the RMSNorm kernel and runs the fused backward;
-    it returns the gradient of ``normalized`` (the norm's own node carries it
-    to the residual) and the six adapter gradients."""
+    and the two rank-r projections. Backward runs the fused backward, in which
+    only the gate/up adapters' gradient reads the normalised input: for a bf16
+    source that gradient applies the norm to the source as it stages it (one
+    pass for the per-row scale, nothing stored; bitwise the materialised
+    values), otherwise the RMSNorm kernel re-materialises the input first. It
+    returns the gradient of ``normalized`` (the norm's own node carries it to
+    the residual) and the six adapter gradients."""
 
     @staticmethod
     def forward(ctx: Any, source, normalized, gate_packed_weight, gate_lora_a, gate_lora_b, up_packed_weight,
@@ -354,10 +364,18 @@ class _ResidualRecipeGatedNF4LoRA(torch.autograd.Function):
     def backward(ctx: Any, grad_output: torch.Tensor):
         (source, gate, up, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_packed, down_a,
          down_b, norm_weight) = ctx.saved_tensors
-        normalized = _RMSNormReplayRecipe(source, norm_weight, ctx.norm_eps, ctx.norm_weight_offset).materialize()
+        flat_source = source.reshape(-1, ctx.dims[0])
+        if ops.norm_replay_fusable(flat_source):
+            # the normalised input is formed as the adapters' gradient stages
+            # it, from the source and the norm's per-row scale: never stored
+            inv = ops.direct.rmsnorm_inv(flat_source, norm_weight, ctx.norm_eps)
+            flat, norm = None, (flat_source, inv, norm_weight, ctx.norm_weight_offset)
+        else:
+            normalized = _RMSNormReplayRecipe(source, norm_weight, ctx.norm_eps, ctx.norm_weight_offset).materialize()
+            flat, norm = normalized.reshape(-1, ctx.dims[0]), None
         dx, dag, dbg, dau, dbu, dad, dbd = _fused_backward(
-            grad_output, normalized.reshape(-1, ctx.dims[0]), gate, up, None, t_gu, t_d, gate_packed, gate_a,
-            gate_b, up_packed, up_a, up_b, down_packed, down_a, down_b, ctx.qs, ctx.scaling, ctx.dims)
+            grad_output, flat, gate, up, None, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed, up_a, up_b,
+            down_packed, down_a, down_b, ctx.qs, ctx.scaling, ctx.dims, norm)
         return (None, dx.reshape(ctx.input_shape), None, dag, dbg, None, dau, dbu, None, dad, dbd,
                 None, None, None, None, None, None, None, None, None)
 

@@ -598,6 +598,50 @@ def _(l, l2, mode, rmat, scale, layout):
     return l.new_empty((p, q) if layout == 0 else (q, p), dtype=torch.float32)
 
 
+@_custom_op(f"{NS}::lora_grad_rmsnorm", mutates_args=())
+def lora_grad_rmsnorm(x: Tensor, inv_rms: Tensor, norm_weight: Tensor, offset: float, rmat: Tensor,
+                      scale: float, layout: int) -> Tensor:
+    """lora_grad with L = the frozen RMSNorm's bf16 output, formed from its
+    input x (bf16 [M, P]), per-row inv_rms (rmsnorm_inv) and weight as it is
+    staged, bitwise as over the materialised output
+    (methods/gated_replay.py:146-151,167-184)."""
+    what = "LoRA gradient over the RMSNorm replay"
+    dev = _require_gpu(x, inv_rms, norm_weight, rmat, what=what)
+    rmat = _bf16(rmat, "low-rank operand", what)
+    if x.dtype != torch.bfloat16 or x.dim() != 2 or not x.is_contiguous():
+        raise ValueError(f"{what}: x must be a contiguous bf16 matrix")
+    m, p = x.shape
+    q = rmat.shape[1] if rmat.dim() == 2 else -1
+    if rmat.dim() != 2 or rmat.shape[0] != m:
+        raise ValueError(f"{what}: row counts differ ({tuple(x.shape)} vs {tuple(rmat.shape)})")
+    if inv_rms.dtype != torch.float32 or inv_rms.shape != (m,):
+        raise ValueError(f"{what}: inv_rms must be fp32 [{m}]")
+    w = norm_weight.detach().contiguous()
+    if w.numel() != p:
+        raise ValueError(f"{what}: norm weight has {w.numel()} elements for {p} features")
+    out = torch.empty((p, q) if layout == 0 else (q, p), device=dev, dtype=torch.float32)
+    lib = _lib.load()
+    ws_bytes = int(lib.molt_lora_grad_workspace(m, p, q))
+    ws = torch.empty(max(ws_bytes, 4), device=dev, dtype=torch.uint8)
+    _call("molt_lora_grad_rmsnorm", x.data_ptr(), p, inv_rms.contiguous().data_ptr(), w.data_ptr(),
+          _rn_dtype(w, "weight"), float(offset), rmat.data_ptr(), q, m, p, q, float(scale), out.data_ptr(), layout,
+          ws.data_ptr(), ws_bytes, _stream(dev))
+    return out
+
+
+@lora_grad_rmsnorm.register_fake
+def _(x, inv_rms, norm_weight, offset, rmat, scale, layout):
+    p, q = x.shape[1], rmat.shape[1]
+    return x.new_empty((p, q) if layout == 0 else (q, p), dtype=torch.float32)
+
+
+def norm_replay_fusable(x: Tensor) -> bool:
+    """Whether lora_grad_rmsnorm takes x as it is: a bf16 matrix, contiguous,
+    16-byte aligned, a multiple of 8 features."""
+    return (x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous() and x.shape[1] % 8 == 0
+            and x.data_ptr() % 16 == 0)
+
+
 # ------------------------------------------------------------------ GEMV
 @_custom_op(f"{NS}::nf4_gemv", mutates_args=())
 def nf4_gemv(x: Tensor, packed: Tensor, scales: Optional[Tensor], absmax_q: Optional[Tensor],
@@ -721,6 +765,28 @@ def rmsnorm_forward(x: Tensor, weight: Tensor, eps: float, offset: float) -> Ten
 @rmsnorm_forward.register_fake
 def _(x, weight, eps, offset):
     return torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+
+
+@_custom_op(f"{NS}::rmsnorm_inv", mutates_args=())
+def rmsnorm_inv(x: Tensor, weight: Tensor, eps: float) -> Tensor:
+    """fp32 rsqrt(mean(fp32(x)^2) + eps) of every row, bitwise the value
+    rmsnorm_forward(x, weight, ...) scales the row by (same kernel, same
+    reduction)."""
+    dev = _require_gpu(x, weight, what="frozen RMSNorm")
+    h = _rn_check(x, weight)
+    xc, w = x.contiguous(), weight.detach().contiguous()
+    rows = xc.numel() // h
+    inv = torch.empty(rows, dtype=torch.float32, device=dev)
+    if rows == 0:
+        return inv
+    _call("molt_rmsnorm_forward", xc.data_ptr(), _rn_dtype(xc, "hidden"), h, rows, h, w.data_ptr(),
+          _rn_dtype(w, "weight"), float(eps), 0.0, None, h, inv.data_ptr(), _stream(dev))
+    return inv
+
+
+@rmsnorm_inv.register_fake
+def _(x, weight, eps):
+    return torch.empty(x.numel() // x.shape[-1], dtype=torch.float32, device=x.device)
 
 
 @_custom_op(f"{NS}::rmsnorm_backward", mutates_args=())

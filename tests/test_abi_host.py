@@ -128,6 +128,35 @@ def test_fake_impls_give_shapes_without_a_gpu():
         assert t.shape == (10, 4)
         g = ops.lora_grad(x, None, 0, t, 1.0, 1)
         assert g.shape == (4, 128) and g.dtype == torch.float32
+        inv = ops.rmsnorm_inv(x, torch.empty(128, device="cuda"), 1e-6)
+        assert inv.shape == (10,) and inv.dtype == torch.float32
+        gn = ops.lora_grad_rmsnorm(x, inv, torch.empty(128, device="cuda"), 0.0, t, 1.0, 1)
+        assert gn.shape == (4, 128) and gn.dtype == torch.float32
+
+
+def test_norm_replay_gradient_refuses_before_any_launch():
+    lib = _lib.load()
+    out = 0x1000
+    # weight dtype, null operands, then 16-byte alignment / multiples of 8
+    rc = lib.molt_lora_grad_rmsnorm(0x1000, 64, 0x1000, 0x1000, 7, 0.0, 0x1000, 8, 64, 64, 8, 1.0, out, 1, 0x1000,
+                                    1 << 20, None)
+    assert rc == _lib.MOLT_EINVAL and b"dtype" in lib.molt_amd_last_error()
+    rc = lib.molt_lora_grad_rmsnorm(0x1000, 64, None, 0x1000, 0, 0.0, 0x1000, 8, 64, 64, 8, 1.0, out, 1, 0x1000,
+                                    1 << 20, None)
+    assert rc == _lib.MOLT_EINVAL and b"null" in lib.molt_amd_last_error()
+    rc = lib.molt_lora_grad_rmsnorm(0x1002, 64, 0x1000, 0x1000, 0, 0.0, 0x1000, 8, 64, 64, 8, 1.0, out, 1, 0x1000,
+                                    1 << 20, None)
+    assert rc == _lib.MOLT_EUNSUPPORTED
+    rc = lib.molt_lora_grad_rmsnorm(0x1000, 60, 0x1000, 0x1000, 0, 0.0, 0x1000, 8, 64, 60, 8, 1.0, out, 1, 0x1000,
+                                    1 << 20, None)
+    assert rc == _lib.MOLT_EUNSUPPORTED
+    # too small a workspace is refused before the launch
+    rc = lib.molt_lora_grad_rmsnorm(0x1000, 64, 0x1000, 0x1000, 0, 0.0, 0x1000, 8, 64, 64, 8, 1.0, out, 1, 0x1000,
+                                    4, None)
+    assert rc == _lib.MOLT_EWORKSPACE
+    # inv-only RMSNorm needs an inv output
+    rc = lib.molt_rmsnorm_forward(0x1000, 0, 64, 4, 64, 0x1000, 0, 1e-6, 0.0, None, 64, None, None)
+    assert rc == _lib.MOLT_EINVAL
 
 
 def test_statistics_and_row_checks_run_before_any_launch():

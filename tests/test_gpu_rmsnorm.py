@@ -227,6 +227,66 @@ def test_residual_recipe_matches_fused_mlp_and_oracle(hidden, inter, r, m, offse
         assert_close_fro(np_f32(leaf.grad), ref, what=name)
 
 
+@pytest.mark.parametrize("m,h,q,w_dtype,offset", [
+    (200, 256, 32, torch.bfloat16, 0.0),
+    (77, 1536, 16, torch.float32, 1.0),
+    (1, 64, 8, torch.bfloat16, 0.0),
+    (8192, 4096, 128, torch.bfloat16, 0.0),   # cfg4: the gate/up adapters' dA
+])
+def test_norm_replay_gradient_is_bitwise_the_materialised_one(m, h, q, w_dtype, offset):
+    """The gate/up dA over the RMSNorm output formed as it is staged
+    (molt_lora_grad_rmsnorm) equals lora_grad over the materialised output,
+    and rmsnorm_inv is the scale the forward kernel applies."""
+    print(f"norm-replay dA m={m} h={h} q={q} w={w_dtype} off={offset}", flush=True)
+    eps = 1e-5
+    x = seeded((m, h), 81, std=1.3)
+    w = seeded((h,), 82, std=0.3).to(w_dtype)
+    u = seeded((m, q), 83)
+    inv = ops.rmsnorm_inv(x, w, eps)
+    n = ops.rmsnorm_forward(x, w, eps, offset)
+    assert torch.equal(n, ((x.float() * inv[:, None]) * (w.float() + offset)).to(torch.bfloat16))
+    for scale, layout in ((1.0, 1), (0.5, 0)):
+        got = ops.lora_grad_rmsnorm(x, inv, w, offset, u, scale, layout)
+        ref = ops.lora_grad(n, None, 0, u, scale, layout)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), f"layout {layout}: max |diff| {(got - ref).abs().max().item()}"
+
+
+def test_norm_replay_gradient_of_no_tokens_is_zero():
+    x = torch.empty(0, 64, dtype=torch.bfloat16, device="cuda")
+    u = torch.empty(0, 8, dtype=torch.bfloat16, device="cuda")
+    w = torch.ones(64, dtype=torch.bfloat16, device="cuda")
+    inv = ops.rmsnorm_inv(x, w, 1e-6)
+    assert inv.shape == (0,)
+    g = ops.lora_grad_rmsnorm(x, inv, w, 0.0, u, 1.0, 1)
+    assert torch.equal(g, torch.zeros(8, 64, device="cuda"))
+
+
+def test_residual_recipe_with_fp32_source_materialises_and_matches_fused_mlp():
+    """An fp32 residual takes the materialising replay; results stay bitwise
+    those of the fused node on the norm's output."""
+    hidden, inter, r, m, s, eps = 128, 256, 8, 96, 2.0, 1e-6
+    projs = [_proj(inter, hidden, r, 10), _proj(inter, hidden, r, 20), _proj(hidden, inter, r, 30)]
+    (pg, qg, ag, bg), (pu, qu, au, bu), (pd, qd, ad, bd) = projs
+    norm_w = seeded((hidden,), 50, std=0.2)
+    source = seeded((m, hidden), 51, std=1.5, dtype=torch.float32).requires_grad_()
+    dy = seeded((m, hidden), 52)
+    leaves = [t.clone().requires_grad_() for t in (ag, bg, au, bu, ad, bd)]
+    normalized = _FrozenRMSNormFunction.apply(source, norm_w, eps, 0.0)
+    y = _ResidualRecipeGatedNF4LoRA.apply(source, normalized, pg, leaves[0], leaves[1], pu, leaves[2], leaves[3],
+                                          pd, leaves[4], leaves[5], qg, qu, qd, s, s, s, norm_w, eps, 0.0)
+    y.backward(dy)
+    x2 = normalized.detach().clone().requires_grad_()
+    leaves2 = [t.clone().requires_grad_() for t in (ag, bg, au, bu, ad, bd)]
+    y2 = fused_gated_nf4_lora_mlp(x2, pg, leaves2[0], leaves2[1], pu, leaves2[2], leaves2[3], pd, leaves2[4],
+                                  leaves2[5], qg, qu, qd, s, s, s)
+    y2.backward(dy)
+    assert torch.equal(y, y2)
+    for a, b in zip(leaves, leaves2):
+        assert torch.equal(a.grad, b.grad)
+    assert source.grad.dtype == torch.float32 and torch.isfinite(source.grad).all()
+
+
 class _DecoderTail(nn.Module):
     """residual + mlp(post_attention_layernorm(residual)), as a decoder layer's second half."""
 
