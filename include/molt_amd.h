@@ -81,12 +81,16 @@ const char* molt_amd_version(void);
  *   MOLT_TUNE_SPLIT_K       (0 when MOLT_AMD_NO_SPLIT_K is set, else 1): split
  *       the contraction of a long-K GEMM with few output tiles over
  *       workgroups (needs the caller's workspace, see below).
+ *   MOLT_TUNE_SPLIT_MIN_STEPS (MOLT_AMD_SPLIT_MIN_STEPS, default 8, 2..4096):
+ *       fewest 64-deep contraction steps per split range of a 256 x 256 tile;
+ *       a 128 x 128 tile, a quarter of the work per step, takes a quarter.
  * molt_amd_set_tuning returns MOLT_EINVAL for an unknown key or a value out of
  * range; molt_amd_get_tuning returns -2 for an unknown key. */
 #define MOLT_TUNE_BIG_TILE_MIN 0
 #define MOLT_TUNE_GEMV_DOT_M 1
 #define MOLT_TUNE_LORA_DMA 2
 #define MOLT_TUNE_SPLIT_K 3
+#define MOLT_TUNE_SPLIT_MIN_STEPS 4
 int molt_amd_set_tuning(int32_t key, int64_t value);
 int64_t molt_amd_get_tuning(int32_t key);
 

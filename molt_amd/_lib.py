@@ -20,7 +20,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmolt_amd.so"
 
 MOLT_OK, MOLT_EINVAL, MOLT_EUNSUPPORTED, MOLT_ELAUNCH, MOLT_EWORKSPACE = 0, 1, 2, 3, 4
 DTYPE_BF16, DTYPE_F32 = 0, 1
-TUNING_KEYS = {"big_tile_min": 0, "gemv_dot_m": 1, "lora_dma": 2, "split_k": 3}   # MOLT_TUNE_* of include/molt_amd.h
+TUNING_KEYS = {"big_tile_min": 0, "gemv_dot_m": 1, "lora_dma": 2, "split_k": 3, "split_min_steps": 4}   # MOLT_TUNE_* of include/molt_amd.h
 
 _p = C.c_void_p
 _i64 = C.c_int64
@@ -125,7 +125,7 @@ class tuning:
         with tuning(big_tile_min=1):   # force the 256 x 256 tile GEMMs
             ...
 
-    Keys: ``big_tile_min``, ``gemv_dot_m``, ``lora_dma``, ``split_k``. Settings are process
+    Keys: ``big_tile_min``, ``gemv_dot_m``, ``lora_dma``, ``split_k``, ``split_min_steps``. Settings are process
     wide; callers that change them concurrently race."""
 
     def __init__(self, **values: int) -> None:

@@ -33,7 +33,7 @@ int check_launch(const char* what) {
 // relaxed atomic load per call.
 namespace {
 struct Tuning {
-  std::atomic<int64_t> v[4];
+  std::atomic<int64_t> v[5];
   Tuning() {
     const char* e = getenv("MOLT_AMD_BIG_TILE_MIN");
     v[MOLT_TUNE_BIG_TILE_MIN].store(e ? atoll(e) : 256);
@@ -42,6 +42,9 @@ struct Tuning {
     v[MOLT_TUNE_GEMV_DOT_M].store(m < -1 ? -1 : (m > 4 ? 4 : m));
     v[MOLT_TUNE_LORA_DMA].store(getenv("MOLT_AMD_PJ_NODMA") ? 0 : 1);
     v[MOLT_TUNE_SPLIT_K].store(getenv("MOLT_AMD_NO_SPLIT_K") ? 0 : 1);
+    e = getenv("MOLT_AMD_SPLIT_MIN_STEPS");
+    const int64_t ms = e ? atoll(e) : 8;
+    v[MOLT_TUNE_SPLIT_MIN_STEPS].store(ms < 2 ? 2 : ms);
   }
 };
 Tuning& tuning() {
@@ -54,6 +57,7 @@ bool tuning_ok(int32_t key, int64_t value) {
     case MOLT_TUNE_GEMV_DOT_M: return value >= -1 && value <= 4;
     case MOLT_TUNE_LORA_DMA: return value == 0 || value == 1;
     case MOLT_TUNE_SPLIT_K: return value == 0 || value == 1;
+    case MOLT_TUNE_SPLIT_MIN_STEPS: return value >= 2 && value <= 4096;
     default: return false;
   }
 }
@@ -101,7 +105,7 @@ int molt_amd_set_tuning(int32_t key, int64_t value) {
 }
 
 int64_t molt_amd_get_tuning(int32_t key) {
-  return key >= 0 && key <= MOLT_TUNE_SPLIT_K ? molt::tuning_value(key) : -2;
+  return key >= 0 && key <= MOLT_TUNE_SPLIT_MIN_STEPS ? molt::tuning_value(key) : -2;
 }
 
 int molt_nf4_lora_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,

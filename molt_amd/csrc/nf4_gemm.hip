@@ -128,6 +128,35 @@ MOLT_DEV void a_generic(uint16_t* xs, const uint16_t* __restrict__ a, int64_t ld
   }
 }
 
+// X side of a LoRA contraction step (T or U, [M, L] bf16): the thread's four
+// 8-element chunks as 32 element loads from clamped addresses, all issued
+// before the first use (a load behind a bounds branch would make the compiler
+// wait for every load issued before it), zeros outside the operand.
+MOLT_DEV void a_lora(uint16_t* xs, const uint16_t* __restrict__ a, int64_t lda, int64_t m0, int64_t M, int64_t k0,
+                     int64_t L, int tid) {
+  uint16_t e[A_PT][8];
+#pragma unroll
+  for (int c = 0; c < A_PT; ++c) {
+    const int idx = tid + c * NT;
+    const int64_t m = m0 + (idx >> 3), k = k0 + (idx & 7) * 8;
+    const int64_t mc = m < M ? m : M - 1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t kc = k + i < L ? k + i : L - 1;
+      e[c][i] = a[mc * lda + kc];
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < A_PT; ++c) {
+    const int idx = tid + c * NT;
+    const int64_t m = m0 + (idx >> 3), k = k0 + (idx & 7) * 8;
+    uint16_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = m < M && k + i < L ? e[c][i] : (uint16_t)0;
+    *reinterpret_cast<u32x4_t*>(xs + (idx >> 3) * LDSW + (idx & 7) * 8) = __builtin_bit_cast(u32x4_t, v);
+  }
+}
+
 // ------------------------------------------------ forward W-side (row-contract)
 // LDS row R of the W tile -> (weight index, weight row).
 MOLT_DEV void fwd_row(int R, int64_t tn, bool pair, int& which, int64_t& n) {
@@ -190,16 +219,34 @@ MOLT_DEV void wrow_generic(uint16_t* ws, const FwdParams& p, int64_t tn, bool pa
   }
 }
 
-// LoRA step (forward): W-side row R holds bf16(s * B[n, j - off]) for its window.
+// LoRA step (forward): W-side row R holds bf16(s * B[n, j - off]) for its
+// window. A thread owns 32 consecutive columns of one row (as wrow_issue);
+// its loads come from clamped addresses and are all issued before any use.
 MOLT_DEV void wrow_lora(uint16_t* ws, const FwdParams& p, int64_t tn, bool pair, int64_t k0, int tid) {
-  for (int e = tid; e < BN * BK; e += NT) {
-    const int R = e / BK, j = e % BK;
-    int which; int64_t n;
-    fwd_row(R, tn, pair, which, n);
-    const int64_t c = k0 + j - (int64_t)which * p.r;  // column inside this weight's adapter
-    uint16_t v = 0;
-    if (n < p.N && c >= 0 && c < p.r) v = bf16_bits((which ? p.s[1] : p.s[0]) * sel(p.lb, which)[n * p.ldlb + c]);
-    ws[R * LDSW + j] = v;
+  const int R = tid >> 1, half = tid & 1;
+  int which; int64_t n;
+  fwd_row(R, tn, pair, which, n);
+  const float s = which ? p.s[1] : p.s[0];
+  const float* brow = sel(p.lb, which) + (n < p.N ? n : p.N - 1) * p.ldlb;
+  const int64_t c0 = k0 + 32 * half - (int64_t)which * p.r;   // adapter column of the first element
+  float f[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const int64_t c = c0 + j;
+    f[j] = brow[c < 0 ? 0 : (c < p.r ? c : p.r - 1)];
+  }
+  uint16_t* dst = ws + R * LDSW + 32 * half;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    u32x4_t o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = 8 * d + 2 * i;
+      const bool ok0 = n < p.N && c0 + j >= 0 && c0 + j < p.r;
+      const bool ok1 = n < p.N && c0 + j + 1 >= 0 && c0 + j + 1 < p.r;
+      o[i] = pack_bf16x2(ok0 ? s * f[j] : 0.0f, ok1 ? s * f[j + 1] : 0.0f);
+    }
+    *reinterpret_cast<u32x4_t*>(dst + 8 * d) = o;
   }
 }
 
@@ -269,15 +316,111 @@ MOLT_DEV void wcol_generic(uint16_t* ws, const BwdParams& p, int seg, int64_t tn
   }
 }
 
+// LoRA step (backward): W-side row R (output column) holds bf16(la_scale *
+// A[c0 + j, col]). A thread owns the patch of wcol_commit (8 contraction rows
+// x 4 columns); its loads come from clamped addresses and are all issued
+// before any use.
 MOLT_DEV void wcol_lora(uint16_t* ws, const BwdParams& p, int seg, int64_t tn, int64_t c0, int tid) {
   const float* a = sel(p.la, seg);
-  for (int e = tid; e < BN * BK; e += NT) {
-    const int R = e % BN, j = e / BN;
-    const int64_t col = tn * BN + R, c = c0 + j;
-    uint16_t v = 0;
-    if (col < p.Kw && c < p.r) v = bf16_bits(p.la_scale * a[c * p.ldla + col]);
-    ws[R * LDSW + j] = v;
+  const int cg = tid % CG, rg = tid / CG;
+  const int64_t col = tn * BN + 4 * cg;
+  float f[8][4];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int64_t c = c0 + 8 * rg + r;
+    const int64_t cc = c < p.r ? c : p.r - 1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f[r][j] = a[cc * p.ldla + (col + j < p.Kw ? col + j : p.Kw - 1)];
   }
+  float v[8][4];
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[r][j] = c0 + 8 * rg + r < p.r && col + j < p.Kw ? p.la_scale * f[r][j] : 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    u32x4_t o;
+    o[0] = pack_bf16x2(v[0][j], v[1][j]);
+    o[1] = pack_bf16x2(v[2][j], v[3][j]);
+    o[2] = pack_bf16x2(v[4][j], v[5][j]);
+    o[3] = pack_bf16x2(v[6][j], v[7][j]);
+    *reinterpret_cast<u32x4_t*>(ws + (4 * cg + j) * LDSW + 8 * rg) = o;
+  }
+}
+
+// ------------------------------------------- pipelined main steps (aligned)
+// Workgroup barrier without __syncthreads()'s release fence (the fence makes
+// the compiler drain every outstanding vector-memory op, including register
+// loads that are only used steps later); this wave's LDS accesses are waited
+// for, and the empty asm statements keep the compiler from moving memory
+// accesses across the barrier.
+MOLT_DEV void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);              // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// The register loads of one forward main step (aligned operands): X rows and
+// W rows past the matrix re-read the last row, so every load is issued
+// unconditionally (a load behind a bounds branch makes the compiler wait for
+// all earlier loads at the join). Those rows only feed output rows and
+// columns that are never stored.
+struct FwdStage { AReg a; WRowReg w; };
+
+MOLT_DEV void fwd_issue(FwdStage& st, const FwdParams& p, int64_t m0, int64_t tn, bool pair, int s, int tid) {
+  const int64_t k0 = (int64_t)s * BK;
+#pragma unroll
+  for (int c = 0; c < A_PT; ++c) {
+    const int idx = tid + c * NT;
+    const int64_t m = m0 + (idx >> 3) < p.M ? m0 + (idx >> 3) : p.M - 1;
+    st.a.v[c] = *reinterpret_cast<const u32x4_t*>(p.x + m * p.ldx + k0 + (idx & 7) * 8);
+  }
+  const int R = tid >> 1, half = tid & 1;
+  int which; int64_t n;
+  fwd_row(R, tn, pair, which, n);
+  const int64_t flat = (n < p.N ? n : p.N - 1) * p.K + k0 + 32 * half;
+  st.w.q = *reinterpret_cast<const u32x4_t*>(sel(p.packed, which) + (flat >> 1));
+  st.w.sc = sel(p.scales, which)[flat >> 6];
+}
+
+// Main steps sbeg .. sbeg + n - 1 of the aligned forward kernels. Three
+// register sets rotate: while step i's MFMAs run from LDS buffer i % 2, step
+// i + 1 is committed from its set to the other buffer and that set is refilled
+// with step i + 4, so the loads of two to three steps are in flight at every
+// step boundary (one step of lookahead left the kernel waiting on memory
+// latency at these short contractions). Steps past the range re-load the
+// last one and are never committed.
+template <bool PAIR>
+MOLT_DEV void fwd_main(const FwdParams& p, Smem& sm, int64_t m0, int64_t tn, int sbeg, int n,
+                       f32x16_t (&acc)[TM][TN], int tid, int lane, int wm, int wn) {
+  const int last = n - 1;
+  auto S = [&](int i) { return sbeg + (i < last ? i : last); };
+  FwdStage s0, s1, s2;
+  fwd_issue(s0, p, m0, tn, PAIR, S(0), tid);
+  fwd_issue(s1, p, m0, tn, PAIR, S(1), tid);
+  fwd_issue(s2, p, m0, tn, PAIR, S(2), tid);
+  a_commit(s0.a, sm.xs[0], tid);
+  wrow_commit(s0.w, sm.ws[0], sm.tab, tid);
+  fwd_issue(s0, p, m0, tn, PAIR, S(3), tid);
+  lds_barrier();
+#define MOLT_FWD_ITER(K, SET)                                                        \
+  mfma_step<TM, TN>(sm.ws[(K) & 1], sm.xs[(K) & 1], wn * WROWS, wm * WCOLS, acc, lane); \
+  if (i + (K) + 1 >= n) break;                                                       \
+  a_commit(SET.a, sm.xs[((K) + 1) & 1], tid);                                        \
+  wrow_commit(SET.w, sm.ws[((K) + 1) & 1], sm.tab, tid);                             \
+  fwd_issue(SET, p, m0, tn, PAIR, S(i + (K) + 4), tid);                              \
+  lds_barrier();
+  for (int i = 0; i < n; i += 6) {
+    MOLT_FWD_ITER(0, s1)
+    MOLT_FWD_ITER(1, s2)
+    MOLT_FWD_ITER(2, s0)
+    MOLT_FWD_ITER(3, s1)
+    MOLT_FWD_ITER(4, s2)
+    MOLT_FWD_ITER(5, s0)
+  }
+#undef MOLT_FWD_ITER
+  __syncthreads();   // every wave is done with the LDS buffers
 }
 
 // --------------------------------------------------------------- epilogues
@@ -306,9 +449,30 @@ MOLT_DEV void load4(const uint16_t* __restrict__ src, int64_t ld, int64_t m, int
   }
 }
 
+// fp32 partial tile of a split-K launch of the 128 x 128 kernels:
+// part[m][n0 ..] (row stride N, N % 4 == 0), rows past M and columns past N
+// skipped.
+MOLT_DEV void store_partial128(float* part, int64_t M, int64_t N, const f32x16_t (&acc)[TM][TN], int64_t m0,
+                               int64_t n0, int wm, int wn, int lane) {
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t m = m0 + wm * WCOLS + j * 32 + (lane & 31);
+    if (m >= M) continue;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t n = n0 + wn * WROWS + i * 32 + 8 * g + 4 * (lane >> 5);
+        if (n >= N) continue;
+        const f32x4_t v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        *reinterpret_cast<f32x4_t*>(part + m * N + n) = v;
+      }
+  }
+}
+
 // ------------------------------------------------------------------ kernels
 template <bool PAIR, bool ALIGNED>
-__global__ __launch_bounds__(NT) void nf4_fwd_kernel(const FwdParams p) {
+__global__ __launch_bounds__(NT, 2) void nf4_fwd_kernel(const FwdParams p) {
   __shared__ Smem sm;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WAVES_M, wn = wave / WAVES_M;
@@ -323,8 +487,16 @@ __global__ __launch_bounds__(NT) void nf4_fwd_kernel(const FwdParams p) {
   if (tid < 16) sm.code16[tid] = p.code[tid];
 
   const int ks = (int)ceil_div64(p.K, BK);
-  const int ls = p.lr > 0 ? (int)ceil_div64(p.lr, BK) : 0;
-  const int total = ks + ls;
+  // split-K (single output only): this workgroup runs main steps
+  // [sbeg, send); the LoRA steps belong to the last split
+  const bool split = !PAIR && p.part != nullptr;
+  const int sbeg = split ? (int)blockIdx.y * p.split_steps : 0;
+  const int send = split ? min(ks, sbeg + p.split_steps) : ks;
+  const int ls = p.lr > 0 && (!split || blockIdx.y + 1 == gridDim.y) ? (int)ceil_div64(p.lr, BK) : 0;
+  const int nmain = send - sbeg;
+  const int total = nmain + ls;
+  // virtual step v -> main step sbeg + v, then LoRA step ks + (v - nmain)
+  auto step_of = [&](int v) { return v < nmain ? sbeg + v : ks + (v - nmain); };
 
   f32x16_t acc[TM][TN];
   zero_acc(acc);
@@ -350,23 +522,34 @@ __global__ __launch_bounds__(NT) void nf4_fwd_kernel(const FwdParams p) {
       }
     } else {
       const int64_t c0 = (int64_t)(s - ks) * BK;
-      a_generic(xs, p.t, p.ldt, m0, p.M, c0, p.lr, tid);
+      a_lora(xs, p.t, p.ldt, m0, p.M, c0, p.lr, tid);
       wrow_lora(ws, p, tn, PAIR, c0, tid);
     }
   };
 
   __syncthreads();  // pair table ready
-  issue(0);
-  commit(0, 0);
-  __syncthreads();
-  for (int s = 0; s < total; ++s) {
-    const int cur = s & 1;
-    if (s + 1 < total) issue(s + 1);
+  int v0 = 0;       // first virtual step of the loop below
+  if constexpr (ALIGNED) {
+    if (nmain > 0) fwd_main<PAIR>(p, sm, m0, tn, sbeg, nmain, acc, tid, lane, wm, wn);
+    v0 = nmain;     // the loop runs the LoRA steps only
+  }
+  if (v0 < total) {
+    issue(step_of(v0));
+    commit(step_of(v0), 0);
+    __syncthreads();
+  }
+  for (int v = v0; v < total; ++v) {
+    const int cur = (v - v0) & 1;
+    if (v + 1 < total) issue(step_of(v + 1));
     mfma_step<TM, TN>(sm.ws[cur], sm.xs[cur], wn * WROWS, wm * WCOLS, acc, lane);
-    if (s + 1 < total) commit(s + 1, cur ^ 1);
+    if (v + 1 < total) commit(step_of(v + 1), cur ^ 1);
     __syncthreads();
   }
 
+  if (split) {
+    store_partial128(p.part + (int64_t)blockIdx.y * p.M * p.N, p.M, p.N, acc, m0, tn * BN, wm, wn, lane);
+    return;
+  }
   const bool vec = p.vec_out != 0;
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
@@ -414,7 +597,15 @@ __global__ __launch_bounds__(NT) void nf4_bwd_kernel(const BwdParams p) {
 
   const int ks = (int)ceil_div64(p.Nw, BK);        // steps per NF4 segment
   const int lsteps = p.r > 0 ? (int)ceil_div64(p.r, BK) : 0;
-  const int total = p.nseg * ks + p.nseg * lsteps;
+  // split-K (plain store only): main steps [sbeg, send) of the nseg * ks,
+  // the LoRA steps in the last split
+  const bool split = EPI == EPI_STORE && p.part != nullptr;
+  const int sbeg = split ? (int)blockIdx.y * p.split_steps : 0;
+  const int send = split ? min(p.nseg * ks, sbeg + p.split_steps) : p.nseg * ks;
+  const int nmain = send - sbeg;
+  const int nl = !split || blockIdx.y + 1 == gridDim.y ? p.nseg * lsteps : 0;
+  const int total = nmain + nl;
+  auto step_of = [&](int v) { return v < nmain ? sbeg + v : p.nseg * ks + (v - nmain); };
 
   f32x16_t acc[TM][TN];
   zero_acc(acc);
@@ -446,23 +637,27 @@ __global__ __launch_bounds__(NT) void nf4_bwd_kernel(const BwdParams p) {
       const int ls = s - p.nseg * ks;
       const int seg = ls / lsteps;
       const int64_t c0 = (int64_t)(ls % lsteps) * BK;
-      a_generic(xs, sel(p.u, seg), p.ldu, m0, p.M, c0, p.r, tid);
+      a_lora(xs, sel(p.u, seg), p.ldu, m0, p.M, c0, p.r, tid);
       wcol_lora(ws, p, seg, tn, c0, tid);
     }
   };
 
   __syncthreads();
-  issue(0);
-  commit(0, 0);
+  issue(step_of(0));
+  commit(step_of(0), 0);
   __syncthreads();
-  for (int s = 0; s < total; ++s) {
-    const int cur = s & 1;
-    if (s + 1 < total) issue(s + 1);
+  for (int v = 0; v < total; ++v) {
+    const int cur = v & 1;
+    if (v + 1 < total) issue(step_of(v + 1));
     mfma_step<TM, TN>(sm.ws[cur], sm.xs[cur], wn * WROWS, wm * WCOLS, acc, lane);
-    if (s + 1 < total) commit(s + 1, cur ^ 1);
+    if (v + 1 < total) commit(step_of(v + 1), cur ^ 1);
     __syncthreads();
   }
 
+  if (split) {
+    store_partial128(p.part + (int64_t)blockIdx.y * p.M * p.Kw, p.M, p.Kw, acc, m0, tn * BN, wm, wn, lane);
+    return;
+  }
   const bool vec = p.vec_out != 0;
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
@@ -1424,18 +1619,81 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 // it to run the large-tile kernels at small shapes).
 int64_t big_tile_min() { return molt::tuning_value(MOLT_TUNE_BIG_TILE_MIN); }
 
-// Split-K plan of a plain-store large-tile GEMM whose output has fewer tiles
-// than big_tile_min() (too few to fill the GPU) but a long contraction: S
-// splits of an even number (>= 16) of 64-deep steps, S the largest with
-// tiles * S <= CUs (at most 8). Returns S (1 = no split) and the steps per split.
-int split_plan(int64_t tiles, int64_t steps, int& split_steps) {
+// Split-K: a plain-store GEMM whose output has too few tiles to fill the CUs
+// but a long contraction runs S workgroups per tile over contiguous ranges of
+// split_steps 64-deep steps, S the largest with tiles * S <= CUs (at most 8)
+// that leaves every range at least min_steps steps (an even count for the
+// large-tile kernel, which runs steps in pairs). Returns S (1 = no split).
+int plan_splits(int64_t tiles, int64_t steps, int64_t min_steps, bool even, int& split_steps) {
   split_steps = (int)steps;
-  if (molt::tuning_value(MOLT_TUNE_SPLIT_K) == 0 || tiles >= big_tile_min()) return 1;
+  if (molt::tuning_value(MOLT_TUNE_SPLIT_K) == 0) return 1;
   int S = (int)std::min<int64_t>(8, molt::device_cus() / std::max<int64_t>(tiles, 1));
-  while (S > 1 && steps / S < 16) --S;
+  while (S > 1 && steps / S < min_steps) --S;
   if (S <= 1) return 1;
-  split_steps = (int)(2 * ceil_div64(ceil_div64(steps, S), 2));
+  const int64_t per = ceil_div64(steps, S);
+  split_steps = (int)(even ? 2 * ceil_div64(per, 2) : per);
   return (int)ceil_div64(steps, split_steps);
+}
+
+// The fewest steps per range: MOLT_TUNE_SPLIT_MIN_STEPS for a 256 x 256 tile;
+// a 128 x 128 step is a quarter of the work, so a quarter of that for the
+// small kernels.
+int64_t split_min_big() { return molt::tuning_value(MOLT_TUNE_SPLIT_MIN_STEPS); }
+int64_t split_min_small() { return std::max<int64_t>(1, split_min_big() / 4); }
+
+// The 256 x 256 kernels run an even number of 64-deep steps and address X
+// (dY), the packed bytes and the scales through 32-bit buffer offsets.
+bool fwd_big_ok(int64_t M, int64_t ldx, int64_t N, int64_t K, bool al) {
+  const int64_t lim = 0x7fffffffll;
+  return al && K % 128 == 0 && ((M - 1) * ldx + K) * 2 <= lim && N * K / 2 <= lim && N * K / 16 <= lim;
+}
+bool bwd_big_ok(int64_t M, int64_t lddy, int64_t Nw, int64_t Kw, int nseg) {
+  const int64_t lim = 0x7fffffffll;
+  return (nseg * (Nw / 64)) % 2 == 0 && ((M - 1) * lddy + Nw) * 2 <= lim && Nw * Kw / 2 <= lim && Nw * Kw / 16 <= lim;
+}
+
+// A split large-tile launch is taken only when its workgroups occupy at least
+// half the CUs; a narrower output (the 1536 -> 256 grouped-query projections)
+// fills the GPU better as 128 x 128 tiles, split or not.
+bool fills_half(int64_t workgroups) { return 2 * workgroups >= molt::device_cus(); }
+
+// Kernel choice of one GEMM: the 256 x 256 kernels (unsplit or split-K), or
+// the 128 x 128 kernels (split-K or unsplit).
+enum { PLAN_BIG = 0, PLAN_BIG_SPLIT = 1, PLAN_SMALL_SPLIT = 2, PLAN_SMALL = 3 };
+struct GemmPlan { int kind, S, split_steps; };
+
+// Forward Y[M, N] over K: big_ok / al say whether the operands qualify for the
+// large-tile kernels / the 128 x 128 kernels' aligned path.
+GemmPlan fwd_plan(int64_t M, int64_t N, int64_t K, bool pair, bool big_ok, bool al) {
+  const int64_t big_tiles = ceil_div64(M, big::BM) * ceil_div64(N, pair ? big::BN / 2 : big::BN);
+  if (big_ok && big_tiles >= big_tile_min()) return {PLAN_BIG, 1, 0};
+  int ss = 0;
+  if (big_ok && !pair && N % big::BN == 0) {
+    const int S = plan_splits(big_tiles, K / BK, split_min_big(), true, ss);
+    if (S > 1 && fills_half(big_tiles * S)) return {PLAN_BIG_SPLIT, S, ss};
+  }
+  if (al && !pair && N % 4 == 0) {
+    const int S = plan_splits(ceil_div64(M, BM) * ceil_div64(N, BN), ceil_div64(K, BK), split_min_small(), false, ss);
+    if (S > 1) return {PLAN_SMALL_SPLIT, S, ss};
+  }
+  return {PLAN_SMALL, 1, 0};
+}
+
+// Input gradient dX[M, Kw] over nseg segments of Nw (EPI_SWIGLU_BWD never splits).
+GemmPlan bwd_plan(int64_t M, int64_t Nw, int64_t Kw, int nseg, bool swiglu, bool big_ok, bool al) {
+  const int64_t big_tiles = ceil_div64(M, big::BM) * ceil_div64(Kw, big::BN);
+  if (big_ok && big_tiles >= big_tile_min()) return {PLAN_BIG, 1, 0};
+  int ss = 0;
+  if (big_ok && !swiglu && Kw % big::BN == 0) {
+    const int S = plan_splits(big_tiles, nseg * (Nw / BK), split_min_big(), true, ss);
+    if (S > 1 && fills_half(big_tiles * S)) return {PLAN_BIG_SPLIT, S, ss};
+  }
+  if (al && !swiglu && Kw % 4 == 0) {
+    const int S = plan_splits(ceil_div64(M, BM) * ceil_div64(Kw, BN), nseg * ceil_div64(Nw, BK), split_min_small(),
+                              false, ss);
+    if (S > 1) return {PLAN_SMALL_SPLIT, S, ss};
+  }
+  return {PLAN_SMALL, 1, 0};
 }
 
 size_t split_bytes(int S, int64_t M, int64_t N) { return S > 1 ? (size_t)S * M * N * sizeof(float) : 0; }
@@ -1495,42 +1753,42 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
   const bool al = (p.K % 64 == 0) && p.block_size == 64 && ldx % 8 == 0 && aligned(x, 16) &&
                   aligned(w0->packed, 16) && (!pair || aligned(w1->packed, 16));
   const int64_t big_tiles = ceil_div64(M, big::BM) * ceil_div64(p.N, pair ? big::BN / 2 : big::BN);
-  // The 256 x 256 kernel runs an even number of 64-deep steps and addresses X,
-  // the packed bytes and the scales through 32-bit buffer offsets.
-  const int64_t lim = 0x7fffffffll;
-  const bool big_ok = al && p.K % 128 == 0 && ((M - 1) * ldx + p.K) * 2 <= lim && p.N * p.K / 2 <= lim &&
-                      p.N * p.K / 16 <= lim;
-  if (big_ok && big_tiles >= big_tile_min()) {
+  const GemmPlan plan = fwd_plan(M, p.N, p.K, pair, fwd_big_ok(M, ldx, p.N, p.K, al), al);
+  const size_t need = split_bytes(plan.S, M, p.N);
+  const bool split = plan.S > 1 && workspace && workspace_bytes >= need && aligned(workspace, 16);
+  if (plan.kind == PLAN_BIG || (plan.kind == PLAN_BIG_SPLIT && split)) {
     MOLT_REQUIRE(big_tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
-    dim3 grid((unsigned)big_tiles), block(big::NT);
+    if (plan.kind == PLAN_BIG_SPLIT) {
+      p.split_steps = plan.split_steps;
+      p.part = static_cast<float*>(workspace);
+    }
+    dim3 grid((unsigned)big_tiles, (unsigned)plan.S), block(big::NT);
     if (pair) hipLaunchKernelGGL((big::fwd_kernel<true>), grid, block, 0, stream, p);
     else hipLaunchKernelGGL((big::fwd_kernel<false>), grid, block, 0, stream, p);
-    return check_launch(who);
-  }
-  if (big_ok && !pair && p.N % big::BN == 0) {
-    int split_steps = 0;
-    const int S = split_plan(big_tiles, p.K / BK, split_steps);
-    const size_t need = split_bytes(S, M, p.N);
-    if (S > 1 && workspace && workspace_bytes >= need && aligned(workspace, 16)) {
-      p.split_steps = split_steps;
+  } else {
+    const int64_t cols_per_tile = pair ? BN / 2 : BN;
+    const int64_t tiles = ceil_div64(M, BM) * ceil_div64(p.N, cols_per_tile);
+    MOLT_REQUIRE(tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
+    const bool small_split = plan.kind == PLAN_SMALL_SPLIT && split;
+    if (small_split) {
+      p.split_steps = plan.split_steps;
       p.part = static_cast<float*>(workspace);
-      hipLaunchKernelGGL((big::fwd_kernel<false>), dim3((unsigned)big_tiles, (unsigned)S), dim3(big::NT), 0, stream, p);
-      const int64_t q = M * (p.N / 4);
-      hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)ceil_div64(q, 256)), dim3(256), 0, stream, p.part, S, M, p.N,
-                         y0, ldy);
-      return check_launch(who);
+    }
+    dim3 grid((unsigned)tiles, small_split ? (unsigned)plan.S : 1u), block(NT);
+    if (pair) {
+      if (al) hipLaunchKernelGGL((nf4_fwd_kernel<true, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((nf4_fwd_kernel<true, false>), grid, block, 0, stream, p);
+    } else {
+      if (al) hipLaunchKernelGGL((nf4_fwd_kernel<false, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((nf4_fwd_kernel<false, false>), grid, block, 0, stream, p);
     }
   }
-  const int64_t cols_per_tile = pair ? BN / 2 : BN;
-  const int64_t tiles = ceil_div64(M, BM) * ceil_div64(p.N, cols_per_tile);
-  MOLT_REQUIRE(tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
-  dim3 grid((unsigned)tiles), block(NT);
-  if (pair) {
-    if (al) hipLaunchKernelGGL((nf4_fwd_kernel<true, true>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((nf4_fwd_kernel<true, false>), grid, block, 0, stream, p);
-  } else {
-    if (al) hipLaunchKernelGGL((nf4_fwd_kernel<false, true>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((nf4_fwd_kernel<false, false>), grid, block, 0, stream, p);
+  if (p.part) {
+    rc = check_launch(who);
+    if (rc) return rc;
+    const int64_t q = M * (p.N / 4);
+    hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)ceil_div64(q, 256)), dim3(256), 0, stream, p.part, plan.S, M,
+                       p.N, y0, ldy);
   }
   return check_launch(who);
 }
@@ -1585,59 +1843,59 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
                   aligned(dy0, 16) && (nseg == 1 || aligned(dy1, 16)) && aligned(w0->packed, 2) &&
                   (nseg == 1 || aligned(w1->packed, 2));
   const int64_t big_tiles = ceil_div64(M, big::BM) * ceil_div64(p.Kw, big::BN);
-  // The 256 x 256 kernel runs an even number of 64-deep steps and addresses dY,
-  // the packed bytes and the scales through 32-bit buffer offsets.
-  const int64_t lim = 0x7fffffffll;
   const bool big_ok = al && aligned(w0->packed, 4) && (nseg == 1 || aligned(w1->packed, 4)) &&
-                      (nseg * (p.Nw / 64)) % 2 == 0 && ((M - 1) * lddy + p.Nw) * 2 <= lim &&
-                      p.Nw * p.Kw / 2 <= lim && p.Nw * p.Kw / 16 <= lim;
-  if (big_ok && big_tiles >= big_tile_min()) {
+                      bwd_big_ok(M, lddy, p.Nw, p.Kw, nseg);
+  const GemmPlan plan = bwd_plan(M, p.Nw, p.Kw, nseg, swiglu, big_ok, al);
+  const size_t need = split_bytes(plan.S, M, p.Kw);
+  const bool split = plan.S > 1 && workspace && workspace_bytes >= need && aligned(workspace, 16);
+  if (plan.kind == PLAN_BIG || (plan.kind == PLAN_BIG_SPLIT && split)) {
     MOLT_REQUIRE(big_tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
-    dim3 grid((unsigned)big_tiles), block(big::NT);
+    if (plan.kind == PLAN_BIG_SPLIT) {
+      p.split_steps = plan.split_steps;
+      p.part = static_cast<float*>(workspace);
+    }
+    dim3 grid((unsigned)big_tiles, (unsigned)plan.S), block(big::NT);
     if (swiglu) hipLaunchKernelGGL((big::bwd_kernel<EPI_SWIGLU_BWD>), grid, block, 0, stream, p);
     else hipLaunchKernelGGL((big::bwd_kernel<EPI_STORE>), grid, block, 0, stream, p);
-    return check_launch(who);
-  }
-  if (big_ok && !swiglu && p.Kw % big::BN == 0) {
-    int split_steps = 0;
-    const int S = split_plan(big_tiles, nseg * (p.Nw / BK), split_steps);
-    const size_t need = split_bytes(S, M, p.Kw);
-    if (S > 1 && workspace && workspace_bytes >= need && aligned(workspace, 16)) {
-      p.split_steps = split_steps;
+  } else {
+    const int64_t tiles = ceil_div64(M, BM) * ceil_div64(p.Kw, BN);
+    MOLT_REQUIRE(tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
+    const bool small_split = plan.kind == PLAN_SMALL_SPLIT && split;
+    if (small_split) {
+      p.split_steps = plan.split_steps;
       p.part = static_cast<float*>(workspace);
-      hipLaunchKernelGGL((big::bwd_kernel<EPI_STORE>), dim3((unsigned)big_tiles, (unsigned)S), dim3(big::NT), 0, stream,
-                         p);
-      const int64_t q = M * (p.Kw / 4);
-      hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)ceil_div64(q, 256)), dim3(256), 0, stream, p.part, S, M, p.Kw,
-                         dx, lddx);
-      return check_launch(who);
+    }
+    dim3 grid((unsigned)tiles, small_split ? (unsigned)plan.S : 1u), block(NT);
+    if (swiglu) {
+      if (al) hipLaunchKernelGGL((nf4_bwd_kernel<EPI_SWIGLU_BWD, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((nf4_bwd_kernel<EPI_SWIGLU_BWD, false>), grid, block, 0, stream, p);
+    } else {
+      if (al) hipLaunchKernelGGL((nf4_bwd_kernel<EPI_STORE, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((nf4_bwd_kernel<EPI_STORE, false>), grid, block, 0, stream, p);
     }
   }
-  const int64_t tiles = ceil_div64(M, BM) * ceil_div64(p.Kw, BN);
-  MOLT_REQUIRE(tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
-  dim3 grid((unsigned)tiles), block(NT);
-  if (swiglu) {
-    if (al) hipLaunchKernelGGL((nf4_bwd_kernel<EPI_SWIGLU_BWD, true>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((nf4_bwd_kernel<EPI_SWIGLU_BWD, false>), grid, block, 0, stream, p);
-  } else {
-    if (al) hipLaunchKernelGGL((nf4_bwd_kernel<EPI_STORE, true>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((nf4_bwd_kernel<EPI_STORE, false>), grid, block, 0, stream, p);
+  if (p.part) {
+    rc = check_launch(who);
+    if (rc) return rc;
+    const int64_t q = M * (p.Kw / 4);
+    hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)ceil_div64(q, 256)), dim3(256), 0, stream, p.part, plan.S, M,
+                       p.Kw, dx, lddx);
   }
   return check_launch(who);
 }
 
 // Workspace of molt_nf4_lora_forward / molt_nf4_lora_backward_input(_pair): the
-// split-K partials when the plan splits (see split_plan), else 0.
+// split-K partials when the plan for 16-byte aligned operands splits (see
+// plan_splits), else 0. Calls whose operands do not qualify, or whose
+// workspace is smaller, run unsplit.
 extern "C" size_t molt_nf4_lora_forward_workspace(int64_t M, int64_t N, int64_t K) {
-  if (M <= 0 || N % big::BN != 0 || K % 128 != 0) return 0;
-  const int64_t tiles = ceil_div64(M, big::BM) * (N / big::BN);
-  int split_steps = 0;
-  return split_bytes(split_plan(tiles, K / BK, split_steps), M, N);
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0) return 0;
+  const GemmPlan plan = fwd_plan(M, N, K, false, fwd_big_ok(M, K, N, K, true), true);
+  return split_bytes(plan.S, M, N);
 }
 
 extern "C" size_t molt_nf4_lora_backward_workspace(int64_t M, int64_t Nw, int64_t Kw, int32_t nseg) {
-  if (M <= 0 || Kw % big::BN != 0 || Nw % 64 != 0 || (nseg * (Nw / 64)) % 2 != 0) return 0;
-  const int64_t tiles = ceil_div64(M, big::BM) * (Kw / big::BN);
-  int split_steps = 0;
-  return split_bytes(split_plan(tiles, nseg * (Nw / BK), split_steps), M, Kw);
+  if (M <= 0 || Nw <= 0 || Kw <= 0 || Nw % 64 != 0 || Kw % 64 != 0 || nseg < 1 || nseg > 2) return 0;
+  const GemmPlan plan = bwd_plan(M, Nw, Kw, nseg, false, bwd_big_ok(M, Nw, Nw, Kw, nseg), true);
+  return split_bytes(plan.S, M, Kw);
 }

@@ -1,9 +1,10 @@
-"""Split-K large-tile GEMMs: a long contraction with too few 256 x 256 output
-tiles to fill the GPU (the cfg3 down projection and the paired gate/up input
-gradient at M = 4096, and small forced shapes) runs over several workgroups
-per tile whose fp32 partials are summed in split order. Checked against the
-fp64 oracle (5e-3), against the unsplit kernels (same values up to fp32
-summation order), and for bitwise repeatability."""
+"""Split-K GEMMs: a long contraction with too few output tiles to fill the GPU
+runs over several workgroups per tile whose fp32 partials are summed in split
+order. The 256 x 256 kernels split the cfg3 down projection and the paired
+gate/up input gradient at M = 4096; the 128 x 128 kernels split the narrow
+grouped-query k/v projection (1536 -> 256) and small ragged shapes. Checked
+against the fp64 oracle (5e-3), against the unsplit kernels (same values up to
+fp32 summation order), and for bitwise repeatability."""
 from __future__ import annotations
 
 import numpy as np
@@ -31,7 +32,8 @@ def _rel(a, b):
     return float((a - b).norm() / b.norm())
 
 
-@pytest.mark.parametrize("m,n,k,r", [(4096, 1536, 8960, 16), (512, 512, 4096, 8), (300, 256, 2048, 0)])
+@pytest.mark.parametrize("m,n,k,r", [(4096, 1536, 8960, 16), (512, 512, 4096, 8), (300, 256, 2048, 0),
+                                     (4096, 256, 1536, 16), (300, 384, 1024, 8), (77, 136, 512, 5)])
 def test_split_forward(m, n, k, r):
     print(f"split-K forward m={m} n={n} k={k} r={r}", flush=True)
     lib = _lib.load()
@@ -61,7 +63,8 @@ def test_split_forward(m, n, k, r):
 
 
 @pytest.mark.parametrize("m,nw,kw,pair,r", [(4096, 8960, 1536, True, 16), (4096, 8960, 1536, False, 16),
-                                            (512, 4096, 512, True, 8), (200, 2048, 256, False, 0)])
+                                            (512, 4096, 512, True, 8), (200, 2048, 256, False, 0),
+                                            (512, 1536, 1536, False, 16), (200, 1024, 384, True, 8)])
 def test_split_backward(m, nw, kw, pair, r):
     print(f"split-K backward m={m} nw={nw} kw={kw} pair={pair} r={r}", flush=True)
     lib = _lib.load()
