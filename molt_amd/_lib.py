@@ -118,6 +118,11 @@ def check(rc: int) -> None:
     raise RuntimeError(msg)
 
 
+# Bumped by every change made through `tuning`, so that cached workspace sizes
+# (which follow the kernel choice) are looked up again.
+tuning_generation = 0
+
+
 class tuning:
     """Kernel-choice settings of the library (``molt_amd_set_tuning``), as a
     context manager that restores the previous values on exit::
@@ -136,14 +141,18 @@ class tuning:
         self.saved: dict[str, int] = {}
 
     def __enter__(self) -> "tuning":
+        global tuning_generation
         lib = load()
         for name, value in self.values.items():
             key = TUNING_KEYS[name]
             self.saved[name] = int(lib.molt_amd_get_tuning(key))
             check(lib.molt_amd_set_tuning(key, int(value)))
+        tuning_generation += 1
         return self
 
     def __exit__(self, *exc) -> None:
+        global tuning_generation
         lib = load()
         for name, value in self.saved.items():
             check(lib.molt_amd_set_tuning(TUNING_KEYS[name], value))
+        tuning_generation += 1

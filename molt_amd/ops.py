@@ -105,13 +105,51 @@ def _bf16(t: Tensor, name: str, what: str) -> Tensor:
 
 
 def _f32(t: Tensor) -> Tensor:
+    if t.dtype == torch.float32 and t.is_contiguous():
+        return t           # only its address is passed on
     return t.detach().to(torch.float32).contiguous()
+
+
+# Workspace sizes by (query, arguments, tuning generation): a host lookup
+# instead of a library call per launch. The sizes follow the kernel choice,
+# which only the tuning settings change; a size gone stale through a change
+# made outside ``_lib.tuning`` only makes the GEMMs run unsplit.
+_WS: dict = {}
+
+
+def _workspace(query: str, *args: int) -> int:
+    key = (query, args, _lib.tuning_generation)
+    n = _WS.get(key)
+    if n is None:
+        if len(_WS) > 4096:
+            _WS.clear()
+        n = _WS[key] = int(getattr(_lib.load(), query)(*args))
+    return n
+
+
+# Weight descriptors by content: the pointers and geometry they hold. A hit
+# describes the very memory of the tensors passed in (they are alive for the
+# launch), so the cache holds no references to them.
+_DESC: dict = {}
 
 
 def _weight(packed: Tensor, scales: Optional[Tensor], code: Tensor, rows: int, cols: int,
             block_size: int, order: int, absmax_q: Optional[Tensor] = None,
             absmax2: Optional[Tensor] = None, code2: Optional[Tensor] = None,
             offset: float = 0.0, dq_block: int = 256) -> _lib.NF4Weight:
+    key = (packed.data_ptr(), _ptr(scales), code.data_ptr(), _ptr(absmax_q), _ptr(absmax2), _ptr(code2),
+           float(offset), int(block_size), int(dq_block), int(order), int(rows), int(cols))
+    w = _DESC.get(key)
+    if w is None:
+        if len(_DESC) > 4096:
+            _DESC.clear()
+        w = _DESC[key] = _descriptor(packed, scales, code, rows, cols, block_size, order, absmax_q, absmax2,
+                                     code2, offset, dq_block)
+    return w
+
+
+def _descriptor(packed, scales, code, rows, cols, block_size, order, absmax_q, absmax2, code2, offset,
+                dq_block) -> _lib.NF4Weight:
     w = _lib.NF4Weight()
     w.packed = packed.data_ptr()
     w.scales = _ptr(scales)
@@ -126,8 +164,6 @@ def _weight(packed: Tensor, scales: Optional[Tensor], code: Tensor, rows: int, c
     w.nibble_order = int(order)
     w.rows = int(rows)
     w.cols = int(cols)
-    # keep every tensor whose address the descriptor holds alive until the launch
-    w.keepalive = (packed, scales, code, absmax_q, absmax2, code2)
     return w
 
 
@@ -349,7 +385,7 @@ def lora_project(z: Tensor, z2: Optional[Tensor], mode: int, zscale: float, lora
     if (lw.shape[1] if layout == 0 else lw.shape[0]) != d:
         raise ValueError(f"{what}: adapter width {tuple(lw.shape)} does not match activation width {d}")
     out = torch.empty((m, r), device=dev, dtype=torch.bfloat16)
-    ws_bytes = int(_lib.load().molt_lora_project_workspace(m, d, r))
+    ws_bytes = _workspace("molt_lora_project_workspace", m, d, r)
     ws = torch.empty(max(ws_bytes, 16), device=dev, dtype=torch.uint8)
     _call("molt_lora_project", z.data_ptr(), _ptr(z2), d, mode, zscale, m, d, lw.data_ptr(), layout, r,
           out.data_ptr(), r, ws.data_ptr(), ws_bytes, _stream(dev))
@@ -387,7 +423,7 @@ def nf4_lora_forward(x: Tensor, packed: Tensor, scales: Tensor, code: Tensor, ro
         r = tt.shape[1]
         if bb.shape != (rows, r):
             raise ValueError(f"{what}: LoRA B shape {tuple(bb.shape)} != ({rows}, {r})")
-    ws_bytes = int(_lib.load().molt_nf4_lora_forward_workspace(x.shape[0], rows, cols))
+    ws_bytes = _workspace("molt_nf4_lora_forward_workspace", x.shape[0], rows, cols)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     _call("molt_nf4_lora_forward", x.data_ptr(), cols, x.shape[0], C.byref(w), _ptr(tt), max(r, 1),
           _ptr(bb), r, float(scaling), y.data_ptr(), rows, _ptr(ws), ws_bytes, _stream(dev))
@@ -469,7 +505,7 @@ def nf4_lora_backward_input(dy: Tensor, packed: Tensor, scales: Tensor, code: Te
             raise ValueError("LoRA gradient rows must match the output gradient")
         if aa.dim() != 2 or aa.shape != (r, cols):
             raise ValueError("LoRA gradient and A matrix dimensions are incompatible")
-    ws_bytes = int(_lib.load().molt_nf4_lora_backward_workspace(dy.shape[0], rows, cols, 1))
+    ws_bytes = _workspace("molt_nf4_lora_backward_workspace", dy.shape[0], rows, cols, 1)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     _call("molt_nf4_lora_backward_input", dy.data_ptr(), rows, dy.shape[0], C.byref(w), _ptr(uu),
           max(r, 1), _ptr(aa), r, float(lora_scale), dx.data_ptr(), cols, _ptr(ws), ws_bytes, _stream(dev))
@@ -514,7 +550,7 @@ def nf4_lora_backward_input_pair(dy0: Tensor, dy1: Tensor, packed0: Tensor, scal
         r = uu0.shape[1]
         if uu1.shape != uu0.shape or aa0.shape != (r, cols) or aa1.shape != (r, cols):
             raise ValueError("LoRA gradient and A matrix dimensions are incompatible")
-    ws_bytes = int(_lib.load().molt_nf4_lora_backward_workspace(m, rows, cols, 2))
+    ws_bytes = _workspace("molt_nf4_lora_backward_workspace", m, rows, cols, 2)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     _call("molt_nf4_lora_backward_input_pair", dy0.data_ptr(), dy1.data_ptr(), rows, m, C.byref(w0),
           C.byref(w1), _ptr(uu0), _ptr(uu1), max(r, 1), _ptr(aa0), _ptr(aa1), r, dx.data_ptr(), cols,
@@ -584,8 +620,7 @@ def lora_grad(l: Tensor, l2: Optional[Tensor], mode: int, rmat: Tensor, scale: f
     m, p = l.shape
     q = rmat.shape[1]
     out = torch.empty((p, q) if layout == 0 else (q, p), device=dev, dtype=torch.float32)
-    lib = _lib.load()
-    ws_bytes = int(lib.molt_lora_grad_workspace(m, p, q))
+    ws_bytes = _workspace("molt_lora_grad_workspace", m, p, q)
     ws = torch.empty(max(ws_bytes, 4), device=dev, dtype=torch.uint8)
     _call("molt_lora_grad", l.data_ptr(), _ptr(l2), p, mode, rmat.data_ptr(), q, m, p, q, float(scale),
           out.data_ptr(), layout, ws.data_ptr(), ws_bytes, _stream(dev))
@@ -620,8 +655,7 @@ def lora_grad_rmsnorm(x: Tensor, inv_rms: Tensor, norm_weight: Tensor, offset: f
     if w.numel() != p:
         raise ValueError(f"{what}: norm weight has {w.numel()} elements for {p} features")
     out = torch.empty((p, q) if layout == 0 else (q, p), device=dev, dtype=torch.float32)
-    lib = _lib.load()
-    ws_bytes = int(lib.molt_lora_grad_workspace(m, p, q))
+    ws_bytes = _workspace("molt_lora_grad_workspace", m, p, q)
     ws = torch.empty(max(ws_bytes, 4), device=dev, dtype=torch.uint8)
     _call("molt_lora_grad_rmsnorm", x.data_ptr(), p, inv_rms.contiguous().data_ptr(), w.data_ptr(),
           _rn_dtype(w, "weight"), float(offset), rmat.data_ptr(), q, m, p, q, float(scale), out.data_ptr(), layout,
