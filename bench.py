@@ -349,7 +349,9 @@ def projection_sweep(dev, reps: int = 10):
     """Every NF4-LoRA projection of the cfg3 decoder (Qwen2.5-1.5B shapes:
     H=1536, 12 q heads / 2 kv heads x 128, I=8960, r=16, M=4096 tokens)
     through scheduled_nf4_lora, forward + backward (dX, dA, dB), with the
-    algorithmic FLOPs 4*M*N*K + 6*M*r*(N+K) per projection."""
+    algorithmic FLOPs 4*M*N*K + 6*M*r*(N+K) per projection. Timed twice: eager
+    through autograd (host-inclusive; the small shapes are host-bound) and as
+    the GPU work alone (the same kernels replayed from a HIP graph)."""
     import torch
     import molt_amd
     from molt_amd.methods import scheduled_nf4_lora
@@ -382,12 +384,61 @@ def projection_sweep(dev, reps: int = 10):
             run()
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) * 1e3 / reps
+        gpu_ms = _graph_ms(lambda: _projection_ops(x, packed, qs, a, b, dy, s))
         flop = 4 * M * n * k + 6 * M * r * (n + k)
         tf = flop / (ms * 1e-3) / 1e12
+        gtf = flop / (gpu_ms * 1e-3) / 1e12
         out.append({"proj": name, "N": n, "K": k, "M": M, "r": r, "ms_fwd_bwd": round(ms, 4), "TFLOP_s": round(tf, 1),
-                    "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)})
-        log(f"cfg3 {name} N={n} K={k} M={M}: fwd+bwd {ms:.3f} ms, {tf:.0f} TFLOP/s ({100 * tf / PEAK_BF16_TFLOPS:.1f}%)")
+                    "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4), "gpu_ms_fwd_bwd": round(gpu_ms, 4),
+                    "gpu_TFLOP_s": round(gtf, 1), "gpu_frac_bf16_peak": round(gtf / PEAK_BF16_TFLOPS, 4)})
+        log(f"cfg3 {name} N={n} K={k} M={M}: fwd+bwd {ms:.3f} ms eager ({tf:.0f} TFLOP/s, "
+            f"{100 * tf / PEAK_BF16_TFLOPS:.1f}%), {gpu_ms:.3f} ms of GPU work ({gtf:.0f} TFLOP/s, "
+            f"{100 * gtf / PEAK_BF16_TFLOPS:.1f}%)")
     return out
+
+
+def _projection_ops(x, packed, qs, a, b, dy, s):
+    """The kernels of one scheduled NF4-LoRA projection, forward and backward,
+    as _ScheduledNF4LoRA issues them (methods/nf4_lora.py forward/backward)."""
+    from molt_amd import ops
+    from molt_amd.nf4 import nibble_order, resolved_nf4_scales
+
+    n, k = b.shape[0], x.shape[1]
+    sc, order = resolved_nf4_scales(qs), nibble_order(qs)
+    t = ops.direct.lora_project(x, None, 0, 1.0, a, 0)
+    ops.direct.nf4_lora_forward(x, packed.reshape(-1), sc, qs.code, n, k, order, 64, t, b, s)
+    u = ops.direct.lora_project(dy, None, 2, s, b, 1)
+    ops.direct.nf4_lora_backward_input(dy, packed.reshape(-1), sc, qs.code, n, k, order, 64, u, a, 1.0)
+    ops.direct.lora_grad(x, None, 0, u, 1.0, 1)
+    ops.direct.lora_grad(dy, None, 0, t, s, 0)
+
+
+def _graph_ms(fn, reps: int = 10, replays: int = 5) -> float:
+    """GPU time per call of `fn` with the host out of the way: `reps` calls
+    captured in one HIP graph, replayed `replays` times between HIP events."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for _ in range(reps):
+                fn()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (reps * replays)
+    del graph
+    return ms
 
 
 def lm_head_bench(dev, steps: int = 5):
