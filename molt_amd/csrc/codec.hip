@@ -26,9 +26,32 @@ MOLT_DEV float block_scale(const ScaleSrc& s, int64_t b) {
 }
 
 // ---------------------------------------------------------------- dequantise
-// One thread per 16 packed bytes (32 elements). Byte -> code pair from a
-// 256-entry LDS table, times the block scale, rounded once to the output dtype.
-template <int OUT_F32, bool BLK32>
+// Work unit: 4 packed bytes = 8 elements, one 16-byte bf16 (32-byte fp32)
+// output chunk. Unit u of a pass goes to lane u % 64 of the wave, so each
+// load instruction reads 256 contiguous bytes and each store instruction
+// writes 1 KB (2 KB fp32) contiguous. A thread takes DQ_UPT units per pass,
+// all loads (packed bytes, then block statistics) issued before any use;
+// loads past the last whole unit re-read it. The unit that holds the end of
+// an element count not divisible by 8 is decoded element by element.
+// Byte -> code pair from a 256-entry LDS table, times the block scale,
+// rounded once to the output dtype.
+constexpr int DQ_UPT = 4;
+
+template <int OUT_F32>
+MOLT_DEV void dq_store(void* out, int64_t e0, const float (&v)[8]) {
+  if (OUT_F32) {
+    float* o = reinterpret_cast<float*>(out) + e0;
+    *reinterpret_cast<f32x4_t*>(o) = f32x4_t{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4_t*>(o + 4) = f32x4_t{v[4], v[5], v[6], v[7]};
+  } else {
+    u32x4_t w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(v[2 * j], v[2 * j + 1]);
+    *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(out) + e0) = w;
+  }
+}
+
+template <int OUT_F32, bool BLK8>
 __global__ __launch_bounds__(CODEC_NT) void dequant_kernel(const uint8_t* __restrict__ packed,
                                                            ScaleSrc ss, const float* __restrict__ code,
                                                            int order, int64_t n, int block,
@@ -40,62 +63,54 @@ __global__ __launch_bounds__(CODEC_NT) void dequant_kernel(const uint8_t* __rest
     tab[b] = make_float2(code[order ? hi : lo], code[order ? lo : hi]);
   }
   __syncthreads();
-  const int64_t chunks = (n + 31) / 32;
-  for (int64_t c = (int64_t)blockIdx.x * CODEC_NT + threadIdx.x; c < chunks;
-       c += (int64_t)gridDim.x * CODEC_NT) {
-    const int64_t e0 = c * 32;
-    const bool full = e0 + 32 <= n;
-    u32x4_t q;
-    if (full) {
-      q = *reinterpret_cast<const u32x4_t*>(packed + c * 16);
-    } else {
-      uint8_t tmp[16];
-      const int64_t nbytes = (n - e0 + 1) / 2;
+  const int64_t whole = n / 8;                 // units with 8 elements
+  const int64_t units = (n + 7) / 8;
+  const int64_t step = (int64_t)gridDim.x * CODEC_NT * DQ_UPT;
+  for (int64_t base = (int64_t)blockIdx.x * CODEC_NT * DQ_UPT; base < units; base += step) {
+    uint32_t q[DQ_UPT];
+    float sc[DQ_UPT];
+    if (whole > 0) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) tmp[i] = i < nbytes ? packed[c * 16 + i] : 0;
-      q = __builtin_bit_cast(u32x4_t, tmp);
-    }
-    float v[32];
-    if (BLK32) {
-      const float sc = block_scale(ss, e0 / block);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float2 p = tab[(q[i >> 2] >> (8 * (i & 3))) & 0xffu];
-        v[2 * i] = p.x * sc;
-        v[2 * i + 1] = p.y * sc;
+      for (int i = 0; i < DQ_UPT; ++i) {
+        const int64_t u = base + i * CODEC_NT + threadIdx.x;
+        q[i] = *reinterpret_cast<const uint32_t*>(packed + 4 * (u < whole ? u : whole - 1));
       }
-    } else {
+      if (BLK8) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float2 p = tab[(q[i >> 2] >> (8 * (i & 3))) & 0xffu];
-        const int64_t ea = e0 + 2 * i, eb = ea + 1;
-        v[2 * i] = ea < n ? p.x * block_scale(ss, ea / block) : 0.0f;
-        v[2 * i + 1] = eb < n ? p.y * block_scale(ss, eb / block) : 0.0f;
-      }
-    }
-    if (OUT_F32) {
-      float* o = reinterpret_cast<float*>(out) + e0;
-      if (full) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          *reinterpret_cast<f32x4_t*>(o + 4 * i) = f32x4_t{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
-      } else {
-        for (int i = 0; i < 32; ++i)
-          if (e0 + i < n) o[i] = v[i];
-      }
-    } else {
-      uint16_t* o = reinterpret_cast<uint16_t*>(out) + e0;
-      if (full) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          u32x4_t w;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(v[8 * i + 2 * j], v[8 * i + 2 * j + 1]);
-          *reinterpret_cast<u32x4_t*>(o + 8 * i) = w;
+        for (int i = 0; i < DQ_UPT; ++i) {
+          const int64_t u = base + i * CODEC_NT + threadIdx.x;
+          sc[i] = block_scale(ss, 8 * (u < whole ? u : whole - 1) / block);
         }
-      } else {
-        for (int i = 0; i < 32; ++i)
-          if (e0 + i < n) o[i] = bf16_bits(v[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < DQ_UPT; ++i) {
+      const int64_t u = base + i * CODEC_NT + threadIdx.x;
+      const int64_t e0 = 8 * u;
+      float v[8];
+      if (u < whole) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float2 p = tab[(q[i] >> (8 * j)) & 0xffu];
+          if (BLK8) {
+            v[2 * j] = p.x * sc[i];
+            v[2 * j + 1] = p.y * sc[i];
+          } else {
+            v[2 * j] = p.x * block_scale(ss, (e0 + 2 * j) / block);
+            v[2 * j + 1] = p.y * block_scale(ss, (e0 + 2 * j + 1) / block);
+          }
+        }
+        dq_store<OUT_F32>(out, e0, v);
+      } else if (u < units) {
+        // the last, partial unit: its bytes and elements one by one
+        for (int k = 0; e0 + k < n; ++k) {
+          const int byte = packed[(e0 + k) >> 1];
+          const float2 p = tab[byte];
+          const float c = ((e0 + k) & 1) ? p.y : p.x;
+          const float vk = c * block_scale(ss, (e0 + k) / block);
+          if (OUT_F32) reinterpret_cast<float*>(out)[e0 + k] = vk;
+          else reinterpret_cast<uint16_t*>(out)[e0 + k] = bf16_bits(vk);
+        }
       }
     }
   }
@@ -271,16 +286,16 @@ extern "C" int molt_nf4_dequantize(const molt_nf4_weight* w, void* out, int32_t 
   if (n == 0) return MOLT_OK;
   MOLT_REQUIRE(aligned(w->packed, 16), MOLT_EINVAL, "%s: packed data must be 16-byte aligned", who);
   MOLT_REQUIRE(aligned(out, 16), MOLT_EINVAL, "%s: output must be 16-byte aligned", who);
-  const bool blk32 = w->block_size % 32 == 0;
-  const unsigned grid = grid_for((n + 31) / 32, CODEC_NT);
+  const bool blk8 = w->block_size % 8 == 0;
+  const unsigned grid = grid_for(ceil_div64((n + 7) / 8, DQ_UPT), CODEC_NT);
   hipStream_t st = (hipStream_t)stream;
 #define MOLT_DQ(F32, B32)                                                                        \
   hipLaunchKernelGGL((dequant_kernel<F32, B32>), dim3(grid), dim3(CODEC_NT), 0, st, w->packed, ss, \
                      w->code, w->nibble_order, n, w->block_size, out)
   if (out_dtype == MOLT_DTYPE_F32) {
-    if (blk32) MOLT_DQ(1, true); else MOLT_DQ(1, false);
+    if (blk8) MOLT_DQ(1, true); else MOLT_DQ(1, false);
   } else {
-    if (blk32) MOLT_DQ(0, true); else MOLT_DQ(0, false);
+    if (blk8) MOLT_DQ(0, true); else MOLT_DQ(0, false);
   }
 #undef MOLT_DQ
   return check_launch(who);
