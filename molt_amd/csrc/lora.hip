@@ -551,9 +551,15 @@ __global__ void lora_grad_reduce_kernel(const float* __restrict__ part, int S, i
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+// M slices of a gradient launch: as many as keep every workgroup of the
+// single-buffered kernel resident at once (three per CU), so no partial
+// second round of workgroups trails the first. The count must not depend on
+// the L operand's mode: the slices fix the fp32 summation order, and the
+// replayed and normalised operands must give bitwise the gradient of the
+// materialised one.
 int grad_splits(int64_t M, int64_t P, int64_t Q) {
   const int64_t tiles = ceil_div64(P, GR_P) * ceil_div64(Q, GR_Q);
-  int64_t s = (1024 + tiles - 1) / tiles;      // aim for ~1024 workgroups
+  int64_t s = 3 * (int64_t)molt::device_cus() / tiles;
   const int64_t max_s = ceil_div64(M, 256);    // keep >= 256 rows per split
   if (s > max_s) s = max_s;
   if (s < 1) s = 1;
