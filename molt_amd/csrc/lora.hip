@@ -579,7 +579,7 @@ using namespace molt;
 // registers). K split: the steps are split two or four ways (at least 16
 // steps per range) until there is a workgroup for every CU.
 int proj_mt(int64_t M, int tq, bool vec, int z_mode) {
-  return (vec && z_mode != 1 && M >= 64 * 64 && tq <= 2) ? 2 : 1;
+  return (vec && z_mode != 1 && M >= 256 * 64 && tq <= 2) ? 2 : 1;
 }
 
 int proj_ksplit(int64_t M, int64_t D, int mt) {
