@@ -9,11 +9,16 @@
 // fused kernel does (kernels/frozen_linear_cross_entropy.py:97-139).
 //
 // One workgroup owns a row. Pass 1 keeps a per-thread online (max, sum) and
-// combines them across the workgroup; pass 2 re-reads the row (from the
-// L2 / Infinity Cache: a row of Qwen's 151,936-entry vocabulary is 297 KB of
-// bf16) and writes the gradient, in place when `grad` aliases the logits:
-// every element is read by the thread that overwrites it, and the target
-// logit is read in pass 1.
+// combines them across the workgroup; pass 2 writes the gradient, in place
+// when `grad` aliases the logits: every element is read by the thread that
+// overwrites it, and the target logit is read in pass 1. bf16 rows of up to
+// 163,840 logits (Qwen's 151,936-entry vocabulary is 297 KB) stay in
+// registers between the passes (ce_reg_kernel); longer or fp32 rows are read
+// twice (ce_kernel, the second read from the L2 / Infinity Cache). The
+// exponentials use the hardware exp2 (__expf) and the two divisions of the
+// gradient are multiplications by reciprocals taken once per row, as the
+// reference's fused kernel computes them with the fast approximate forms
+// (tl.exp, fp32 `/`); the loss keeps the accurate logf and division.
 #include "common.h"
 
 namespace molt {
@@ -67,16 +72,16 @@ MOLT_DEV void ce_st(void* p, int64_t i, float v) {
 MOLT_DEV void ce_merge(float& m, float& d, float m2, float d2) {
   const float mn = fmaxf(m, m2);
   if (mn == -INFINITY) return;   // both empty
-  d = (d > 0.0f ? d * expf(m - mn) : 0.0f) + (d2 > 0.0f ? d2 * expf(m2 - mn) : 0.0f);
+  d = (d > 0.0f ? d * __expf(m - mn) : 0.0f) + (d2 > 0.0f ? d2 * __expf(m2 - mn) : 0.0f);
   m = mn;
 }
 
 MOLT_DEV void ce_add(float& m, float& d, float x) {
   if (x > m) {
-    d = (d > 0.0f ? d * expf(m - x) : 0.0f) + 1.0f;
+    d = (d > 0.0f ? d * __expf(m - x) : 0.0f) + 1.0f;
     m = x;
   } else {
-    d += expf(x - m);
+    d += __expf(x - m);
   }
 }
 
@@ -110,7 +115,7 @@ __global__ __launch_bounds__(CE_NT) void ce_kernel(const CeParams p) {
       for (int e = 1; e < 8; ++e) bm = fmaxf(bm, v[e]);
       float bs = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) bs += expf(v[e] - bm);
+      for (int e = 0; e < 8; ++e) bs += __expf(v[e] - bm);
       ce_merge(m, d, bm, bs);
     }
   } else {
@@ -132,7 +137,7 @@ __global__ __launch_bounds__(CE_NT) void ce_kernel(const CeParams p) {
   if constexpr (GRAD) {
     void* grow = F32 ? (void*)(reinterpret_cast<float*>(p.grad) + row * p.ldg)
                      : (void*)(reinterpret_cast<uint16_t*>(p.grad) + row * p.ldg);
-    const float inv_d = 1.0f / d;
+    const float inv_d = 1.0f / d, inv_total = 1.0f / p.total;
     if constexpr (VEC) {
       for (int64_t i = 8 * (int64_t)tid; i < p.V; i += 8 * CE_NT) {
         float v[8];
@@ -140,15 +145,93 @@ __global__ __launch_bounds__(CE_NT) void ce_kernel(const CeParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float t = (valid && i + e == y) ? 1.0f : 0.0f;
-          v[e] = (expf(v[e] - m) * inv_d - t) / p.total;
+          v[e] = (__expf(v[e] - m) * inv_d - t) * inv_total;
         }
         ce_st8<F32>(grow, i, v);
       }
     } else {
       for (int64_t i = tid; i < p.V; i += CE_NT) {
         const float t = (valid && i == y) ? 1.0f : 0.0f;
-        ce_st<F32>(grow, i, (expf(ce_ld<F32>(lrow, i) - m) * inv_d - t) / p.total);
+        ce_st<F32>(grow, i, (__expf(ce_ld<F32>(lrow, i) - m) * inv_d - t) * inv_total);
       }
+    }
+  }
+}
+
+// bf16 rows of at most 8 * CE_NT * CH elements, read once: every thread loads
+// its CH chunks of 8 logits (chunk c at element 8 (tid + c CE_NT), the chunks
+// the two-pass loop above visits, in the same order) into registers, all
+// loads issued at once; pass 1 and pass 2 then run from registers, so the
+// row is read from memory once instead of twice, and with the same
+// arithmetic in the same order the results equal the two-pass kernel's bit
+// for bit. Chunks past the row re-load the last chunk and are skipped.
+template <int CH, bool GRAD>
+__global__ __launch_bounds__(CE_NT) void ce_reg_kernel(const CeParams p) {
+  __shared__ float red_m[CE_NT / 64], red_d[CE_NT / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const uint16_t* lrow = reinterpret_cast<const uint16_t*>(p.logits) + row * p.ld;
+  const int64_t y = p.targets[row];
+  const bool valid = y >= 0 && y < p.V;
+  const float ly = bf16_to_f32(lrow[valid ? y : 0]);
+
+  u32x4_t q[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int64_t i = 8 * ((int64_t)tid + (int64_t)c * CE_NT);
+    q[c] = *reinterpret_cast<const u32x4_t*>(lrow + (i < p.V ? i : p.V - 8));
+  }
+  float m = -INFINITY, d = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int64_t i = 8 * ((int64_t)tid + (int64_t)c * CE_NT);
+    if (i >= p.V) continue;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { v[2 * e] = bf16_lo(q[c][e]); v[2 * e + 1] = bf16_hi(q[c][e]); }
+    float bm = v[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) bm = fmaxf(bm, v[e]);
+    float bs = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) bs += __expf(v[e] - bm);
+    ce_merge(m, d, bm, bs);
+    __builtin_amdgcn_sched_barrier(0);   // one chunk at a time: the row already fills the registers
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float m2 = __shfl_xor(m, o, 64), d2 = __shfl_xor(d, o, 64);
+    ce_merge(m, d, m2, d2);
+  }
+  if (lane == 0) { red_m[wave] = m; red_d[wave] = d; }
+  __syncthreads();
+  m = red_m[0];
+  d = red_d[0];
+#pragma unroll
+  for (int w = 1; w < CE_NT / 64; ++w) ce_merge(m, d, red_m[w], red_d[w]);
+
+  if (tid == 0) p.loss[row] = valid ? (m + logf(d) - ly) / p.total : 0.0f;
+  if constexpr (GRAD) {
+    uint16_t* grow = reinterpret_cast<uint16_t*>(p.grad) + row * p.ldg;
+    const float inv_d = 1.0f / d, inv_total = 1.0f / p.total;
+    // keep only the packed row alive across the reduction (unpacked, pass 1's
+    // fp32 copies would double its registers)
+#pragma unroll
+    for (int c = 0; c < CH; ++c) asm volatile("" : "+v"(q[c]));
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int64_t i = 8 * ((int64_t)tid + (int64_t)c * CE_NT);
+      if (i >= p.V) continue;
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { v[2 * e] = bf16_lo(q[c][e]); v[2 * e + 1] = bf16_hi(q[c][e]); }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float t = (valid && i + e == y) ? 1.0f : 0.0f;
+        v[e] = (__expf(v[e] - m) * inv_d - t) * inv_total;
+      }
+      ce_st8<false>(grow, i, v);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
@@ -179,6 +262,23 @@ extern "C" int molt_cross_entropy_rows(const void* logits, int32_t dtype, int64_
   CeParams p{logits, ld, rows, vocab, targets, total, loss, grad, ldg};
   const dim3 grid((unsigned)rows), block(CE_NT);
   hipStream_t st = (hipStream_t)stream;
+  // bf16 rows up to 8 * CE_NT * 20 = 163,840 logits: one read, from registers
+  const int64_t chunks = ceil_div64(vocab, 8 * CE_NT);
+  if (!f32 && vec && chunks <= 20) {
+#define MOLT_CE_REG(CH)                                                                    \
+  do {                                                                                     \
+    if (grad) hipLaunchKernelGGL((ce_reg_kernel<CH, true>), grid, block, 0, st, p);        \
+    else hipLaunchKernelGGL((ce_reg_kernel<CH, false>), grid, block, 0, st, p);            \
+  } while (0)
+    if (chunks <= 4) MOLT_CE_REG(4);
+    else if (chunks <= 8) MOLT_CE_REG(8);
+    else if (chunks <= 12) MOLT_CE_REG(12);
+    else if (chunks <= 16) MOLT_CE_REG(16);
+    else if (chunks <= 19) MOLT_CE_REG(19);   // Qwen's 151,936-entry vocabulary
+    else MOLT_CE_REG(20);
+#undef MOLT_CE_REG
+    return check_launch(who);
+  }
 #define MOLT_CE_LAUNCH(F, V, G) hipLaunchKernelGGL((ce_kernel<F, V, G>), grid, block, 0, st, p)
   if (grad) {
     if (f32) { if (vec) MOLT_CE_LAUNCH(true, true, true); else MOLT_CE_LAUNCH(true, false, true); }
