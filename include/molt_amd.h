@@ -84,6 +84,11 @@ const char* molt_amd_version(void);
  *   MOLT_TUNE_SPLIT_MIN_STEPS (MOLT_AMD_SPLIT_MIN_STEPS, default 8, 2..4096):
  *       fewest 64-deep contraction steps per split range of a 256 x 256 tile;
  *       a 128 x 128 tile, a quarter of the work per step, takes a quarter.
+ *   MOLT_TUNE_STAGE_MIN_MTILES (MOLT_AMD_STAGE_MIN_MTILES, default 16, 0 = never):
+ *       fewest 256-row blocks of X (dY) for which the 256 x 256 kernels read
+ *       the weight as a bf16 copy that one pass dequantises into the caller's
+ *       workspace (transposed for the input gradient), instead of dequantising
+ *       every weight tile again in each row block (see the workspace queries).
  * molt_amd_set_tuning returns MOLT_EINVAL for an unknown key or a value out of
  * range; molt_amd_get_tuning returns -2 for an unknown key. */
 #define MOLT_TUNE_BIG_TILE_MIN 0
@@ -91,8 +96,18 @@ const char* molt_amd_version(void);
 #define MOLT_TUNE_LORA_DMA 2
 #define MOLT_TUNE_SPLIT_K 3
 #define MOLT_TUNE_SPLIT_MIN_STEPS 4
+#define MOLT_TUNE_STAGE_MIN_MTILES 5
 int molt_amd_set_tuning(int32_t key, int64_t value);
 int64_t molt_amd_get_tuning(int32_t key);
+
+/* Kernel timing: record the HIP events start_event and end_event (hipEvent_t)
+ * on the call's stream immediately before and after the GEMM kernel launched
+ * by the next NF4 GEMM entry point this thread calls (molt_nf4_lora_forward,
+ * molt_nf4_gateup_forward, molt_nf4_lora_backward_input(_pair),
+ * molt_nf4_swiglu_backward): not around its weight staging or split-K sum, so
+ * hipEventElapsedTime gives that kernel's duration. No counterpart in the
+ * reference; used by the benchmark. */
+int molt_amd_time_next_gemm(void* start_event, void* end_event);
 
 /* ------------------------------------------------------------------------ */
 /* NF4 codec                                                                 */
@@ -153,11 +168,14 @@ int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t ldz, int32_
 /* Y[M, N] = bf16( X . deq(W)^T + T . bf16(s * B)^T ), fp32 accumulation, with
  * X bf16 [M, K], T bf16 [M, r] = molt_lora_project(X, lora_a) and B fp32 [N, r]
  * (row stride r). `w->scales` must be resolved fp32 scales. r = 0 skips LoRA.
- * When the output has too few 256 x 256 tiles to fill the GPU and K is long,
- * the contraction is split over workgroups whose fp32 partials go to the
- * caller's workspace (16-byte aligned, molt_nf4_lora_forward_workspace(M, N, K)
- * bytes) and are summed in split order (deterministic); a NULL or smaller
- * workspace runs without the split. Concurrent calls need separate workspaces.
+ * Workspace (256-byte aligned, molt_nf4_lora_forward_workspace(M, N, K) bytes):
+ * for many token rows the bf16 weight, written once by the dequant and read by
+ * the GEMM (MOLT_TUNE_STAGE_MIN_MTILES); and, when the output has too few
+ * 256 x 256 tiles to fill the GPU and K is long, the fp32 partials of a
+ * contraction split over workgroups, summed in split order (deterministic).
+ * The results do not depend on the workspace; a NULL or smaller workspace runs
+ * without staging and without the split. Concurrent calls need separate
+ * workspaces.
  * Replaces bnb.matmul_4bit + the LoRA epilogue at methods/nf4_lora.py:43-50 and
  * methods/gated_replay.py:211-224. */
 size_t molt_nf4_lora_forward_workspace(int64_t M, int64_t N, int64_t K);
@@ -172,19 +190,24 @@ int molt_nf4_lora_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_
  *   h    = bf16(bf16(silu(gate)) * up)
  * with T bf16 [M, 2r] = [X . Ag^T | X . Au^T]. A workgroup owns gate and up of
  * the same intermediate columns, so h is formed in registers from the two
- * accumulators. Outputs are bf16 [M, I] with row stride ldo.
+ * accumulators. Outputs are bf16 [M, I] with row stride ldo. Workspace: the
+ * two staged bf16 weights, molt_nf4_gateup_forward_workspace(M, I, K) bytes
+ * (see molt_nf4_lora_forward; NULL runs unstaged).
  * Replaces the gate_proj/up_proj calls and `F.silu(gate) * up` of
  * methods/gated_replay.py:78-94,290-291 (and benchmarks/qualified_path_measure.py:404-432). */
+size_t molt_nf4_gateup_forward_workspace(int64_t M, int64_t N, int64_t K);
 int molt_nf4_gateup_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* wg,
                             const molt_nf4_weight* wu, const uint16_t* t, int64_t ldt,
                             const float* bg, const float* bu, int32_t r, float sg, float su,
-                            uint16_t* gate, uint16_t* up, uint16_t* h, int64_t ldo, void* stream);
+                            uint16_t* gate, uint16_t* up, uint16_t* h, int64_t ldo, void* workspace,
+                            size_t workspace_bytes, void* stream);
 
 /* dX[M, K] = bf16( dY . deq(W) + U . bf16(lora_scale * A) ), U bf16 [M, r] (for
  * the scheduled backward U = molt_lora_project(dY, lora_b, z_mode 2, s) and
  * lora_scale = 1), A fp32 [r, K] (row stride K). r = 0 skips LoRA.
- * The workspace is that of the split contraction, as in molt_nf4_lora_forward:
- * molt_nf4_lora_backward_workspace(M, N, K, 1) bytes (N = w->rows, K = w->cols).
+ * Workspace as in molt_nf4_lora_forward, molt_nf4_lora_backward_workspace(M, N,
+ * K, 1) bytes (N = w->rows, K = w->cols): the staged weight is deq(W)^T
+ * [K, N] in bf16, then the split partials.
  * Replaces the dX half of _ScheduledNF4LoRA.backward (methods/nf4_lora.py:86-101)
  * and packed_nf4_backward_input / packed_nf4_lora_backward_input
  * (methods/nf4_backward.py:167-284). */
@@ -209,12 +232,13 @@ int molt_nf4_lora_backward_input_pair(const uint16_t* dy0, const uint16_t* dy1, 
  * (methods/gated_replay.py:376-387; kernels/gated_activation.py:44-51):
  * dh = bf16(dY . deq(Wd) + U . bf16(Ad)); dg = bf16(bf16(dh * up) * silu'(gate)),
  * du = bf16(dh * bf16(silu(gate))). gate, up, dg, du are bf16 [M, I] with row
- * stride ldg; dh is never stored. */
+ * stride ldg; dh is never stored. Workspace: the staged deq(Wd)^T,
+ * molt_nf4_lora_backward_workspace(M, H, I, 1) bytes (NULL runs unstaged). */
 int molt_nf4_swiglu_backward(const uint16_t* dy, int64_t lddy, int64_t M,
                              const molt_nf4_weight* wd, const uint16_t* u, int64_t ldu,
                              const float* lora_a, int32_t r, const uint16_t* gate,
                              const uint16_t* up, int64_t ldg, uint16_t* dgate, uint16_t* dup,
-                             void* stream);
+                             void* workspace, size_t workspace_bytes, void* stream);
 
 /* LoRA weight gradient out = scale * L^T . R over M rows, fp32:
  *  L bf16 [M, P] (l_mode 0) or SwiGLU replay of (L, L2) (l_mode 1); R bf16 [M, Q].

@@ -20,7 +20,8 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmolt_amd.so"
 
 MOLT_OK, MOLT_EINVAL, MOLT_EUNSUPPORTED, MOLT_ELAUNCH, MOLT_EWORKSPACE = 0, 1, 2, 3, 4
 DTYPE_BF16, DTYPE_F32 = 0, 1
-TUNING_KEYS = {"big_tile_min": 0, "gemv_dot_m": 1, "lora_dma": 2, "split_k": 3, "split_min_steps": 4}   # MOLT_TUNE_* of include/molt_amd.h
+TUNING_KEYS = {"big_tile_min": 0, "gemv_dot_m": 1, "lora_dma": 2, "split_k": 3, "split_min_steps": 4,
+               "stage_min_mtiles": 5}   # MOLT_TUNE_* of include/molt_amd.h
 
 _p = C.c_void_p
 _i64 = C.c_int64
@@ -55,17 +56,19 @@ SIGNATURES: dict[str, tuple] = {
     "molt_lora_project_workspace": (_sz, [_i64, _i64, _i32]),
     "molt_lora_project": (C.c_int, [_p, _p, _i64, _i32, _f32, _i64, _i64, _p, _i32, _i32, _p, _i64, _p, _sz,
                                     _p]),
+    "molt_amd_time_next_gemm": (C.c_int, [_p, _p]),
     "molt_nf4_lora_forward_workspace": (_sz, [_i64, _i64, _i64]),
     "molt_nf4_lora_forward": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _f32, _p, _i64, _p, _sz, _p]),
+    "molt_nf4_gateup_forward_workspace": (_sz, [_i64, _i64, _i64]),
     "molt_nf4_gateup_forward": (C.c_int, [_p, _i64, _i64, _W, _W, _p, _i64, _p, _p, _i32, _f32, _f32,
-                                          _p, _p, _p, _i64, _p]),
+                                          _p, _p, _p, _i64, _p, _sz, _p]),
     "molt_nf4_lora_backward_workspace": (_sz, [_i64, _i64, _i64, _i32]),
     "molt_nf4_lora_backward_input": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _f32, _p, _i64, _p, _sz,
                                                _p]),
     "molt_nf4_lora_backward_input_pair": (C.c_int, [_p, _p, _i64, _i64, _W, _W, _p, _p, _i64, _p, _p,
                                                     _i32, _p, _i64, _p, _sz, _p]),
     "molt_nf4_swiglu_backward": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _p, _p, _i64, _p, _p,
-                                           _p]),
+                                           _p, _sz, _p]),
     "molt_lora_grad_workspace": (_sz, [_i64, _i64, _i64]),
     "molt_lora_grad": (C.c_int, [_p, _p, _i64, _i32, _p, _i64, _i64, _i64, _i64, _f32, _p, _i32, _p, _sz,
                                  _p]),

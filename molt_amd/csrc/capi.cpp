@@ -12,6 +12,13 @@
 namespace molt {
 
 static thread_local char g_last_error[512] = "";
+static thread_local void* g_gemm_events[2] = {nullptr, nullptr};
+
+void take_gemm_events(void** start, void** end) {
+  *start = g_gemm_events[0];
+  *end = g_gemm_events[1];
+  g_gemm_events[0] = g_gemm_events[1] = nullptr;
+}
 
 int set_error(int code, const char* fmt, ...) {
   va_list ap;
@@ -33,7 +40,7 @@ int check_launch(const char* what) {
 // relaxed atomic load per call.
 namespace {
 struct Tuning {
-  std::atomic<int64_t> v[5];
+  std::atomic<int64_t> v[6];
   Tuning() {
     const char* e = getenv("MOLT_AMD_BIG_TILE_MIN");
     v[MOLT_TUNE_BIG_TILE_MIN].store(e ? atoll(e) : 256);
@@ -45,6 +52,9 @@ struct Tuning {
     e = getenv("MOLT_AMD_SPLIT_MIN_STEPS");
     const int64_t ms = e ? atoll(e) : 8;
     v[MOLT_TUNE_SPLIT_MIN_STEPS].store(ms < 2 ? 2 : ms);
+    e = getenv("MOLT_AMD_STAGE_MIN_MTILES");
+    const int64_t st = e ? atoll(e) : 16;
+    v[MOLT_TUNE_STAGE_MIN_MTILES].store(st < 0 ? 0 : st);
   }
 };
 Tuning& tuning() {
@@ -58,6 +68,7 @@ bool tuning_ok(int32_t key, int64_t value) {
     case MOLT_TUNE_LORA_DMA: return value == 0 || value == 1;
     case MOLT_TUNE_SPLIT_K: return value == 0 || value == 1;
     case MOLT_TUNE_SPLIT_MIN_STEPS: return value >= 2 && value <= 4096;
+    case MOLT_TUNE_STAGE_MIN_MTILES: return value >= 0;
     default: return false;
   }
 }
@@ -105,7 +116,13 @@ int molt_amd_set_tuning(int32_t key, int64_t value) {
 }
 
 int64_t molt_amd_get_tuning(int32_t key) {
-  return key >= 0 && key <= MOLT_TUNE_SPLIT_MIN_STEPS ? molt::tuning_value(key) : -2;
+  return key >= 0 && key <= MOLT_TUNE_STAGE_MIN_MTILES ? molt::tuning_value(key) : -2;
+}
+
+int molt_amd_time_next_gemm(void* start_event, void* end_event) {
+  molt::g_gemm_events[0] = start_event;
+  molt::g_gemm_events[1] = end_event;
+  return MOLT_OK;
 }
 
 int molt_nf4_lora_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,
@@ -119,10 +136,10 @@ int molt_nf4_lora_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_
 int molt_nf4_gateup_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* wg,
                             const molt_nf4_weight* wu, const uint16_t* t, int64_t ldt, const float* bg,
                             const float* bu, int32_t r, float sg, float su, uint16_t* gate, uint16_t* up,
-                            uint16_t* h, int64_t ldo, void* stream) {
+                            uint16_t* h, int64_t ldo, void* workspace, size_t workspace_bytes, void* stream) {
   if (!wg || !wu) return molt::set_error(MOLT_EINVAL, "molt_nf4_gateup_forward: null weight");
   return molt_nf4_lora_forward_impl(x, ldx, M, wg, wu, t, ldt, 2 * r, bg, bu, r, r, sg, su, gate, up, h, ldo,
-                                    nullptr, 0, (hipStream_t)stream);
+                                    workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int molt_nf4_lora_backward_input(const uint16_t* dy, int64_t lddy, int64_t M, const molt_nf4_weight* w,
@@ -147,12 +164,14 @@ int molt_nf4_lora_backward_input_pair(const uint16_t* dy0, const uint16_t* dy1, 
 
 int molt_nf4_swiglu_backward(const uint16_t* dy, int64_t lddy, int64_t M, const molt_nf4_weight* wd,
                              const uint16_t* u, int64_t ldu, const float* lora_a, int32_t r, const uint16_t* gate,
-                             const uint16_t* up, int64_t ldg, uint16_t* dgate, uint16_t* dup, void* stream) {
+                             const uint16_t* up, int64_t ldg, uint16_t* dgate, uint16_t* dup, void* workspace,
+                             size_t workspace_bytes, void* stream) {
   if (!wd) return molt::set_error(MOLT_EINVAL, "molt_nf4_swiglu_backward: null weight");
   if (M == 0) return MOLT_OK;   // an empty token batch: the outputs are empty too (their pointers may be null)
   if (!dgate) return molt::set_error(MOLT_EINVAL, "molt_nf4_swiglu_backward: null dgate");
   return molt_nf4_lora_backward_impl(dy, nullptr, lddy, M, wd, nullptr, u, nullptr, ldu, lora_a, nullptr, wd->cols,
-                                     r, 1.0f, nullptr, 0, gate, up, dgate, dup, ldg, nullptr, 0, (hipStream_t)stream);
+                                     r, 1.0f, nullptr, 0, gate, up, dgate, dup, ldg, workspace, workspace_bytes,
+                                     (hipStream_t)stream);
 }
 
 }  // extern "C"

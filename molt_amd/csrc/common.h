@@ -45,6 +45,9 @@ int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 int64_t tuning_value(int32_t key);   // a MOLT_TUNE_* setting (molt_amd_set_tuning)
 int device_cus();                    // compute units of the current device, cached per device
+// Events registered by molt_amd_time_next_gemm for this thread (null if none);
+// taking them clears the registration.
+void take_gemm_events(void** start, void** end);
 }  // namespace molt
 
 #define MOLT_REQUIRE(cond, code, ...)              \

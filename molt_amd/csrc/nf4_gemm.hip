@@ -54,6 +54,9 @@ struct FwdParams {
   // split runs split_steps (even) 64-deep steps and writes an fp32 partial
   // tile to part[split][M][N]; null part = no split
   int split_steps; float* part;
+  // staged weights (large-tile kernels): bf16 deq(W) [N, K] of each weight,
+  // row stride ldw, read by DMA instead of dequantising packed bytes
+  const uint16_t* wst[2]; int64_t ldw;
 };
 
 struct BwdParams {
@@ -68,6 +71,9 @@ struct BwdParams {
   const uint16_t* gate; const uint16_t* up; uint16_t* dg; uint16_t* du; int64_t ldg;
   int vec_out;
   int split_steps; float* part;   // split-K of the plain-store large-tile kernel (see FwdParams)
+  // staged weights (large-tile kernels): bf16 deq(W)^T [Kw, Nw] of each
+  // segment, row stride ldw: row k holds the contraction elements of output column k
+  const uint16_t* wst[2]; int64_t ldw;
 };
 
 struct Smem {
@@ -728,6 +734,10 @@ MOLT_DEV int loff(int R, int c) { return R * 64 + ((c ^ lswz(R)) << 3); }
 // (1 KB) of a buffer holds rows 8 blk .. 8 blk + 7, lane l filling position
 // l % 8 of row 8 blk + l / 8. Returns the tile row and first contraction
 // element the lane must fetch.
+// DMA instructions that fill one operand buffer (16 bytes per lane each).
+constexpr int kStageDma = BUF * 2 / (NT * 16);
+static_assert(kStageDma == 4, "x_load and the staged W DMA issue 4 instructions per buffer");
+
 MOLT_DEV void dma_slot(int blk, int lane, int& R, int& k) {
   R = 8 * blk + (lane >> 3);
   k = 8 * ((lane & 7) ^ lswz(R));
@@ -1071,10 +1081,14 @@ MOLT_DEV void store_partial(float* part, int64_t M, int64_t N, const f32x16_t (&
 // that buffer choice is static: the compiler can then tell the LDS reads of
 // one buffer from the DMA into the other and inserts no waits between them.
 // Requires K % 128 == 0 (an even number of steps) and block size 64.
-template <bool PAIR>
+// STAGED: W arrives as the bf16 copy p.wst (the values the dequant would
+// produce) by the same DMA as X, so a step is DMA, fragment reads and MFMAs
+// only and the code-pair table is not needed.
+template <bool PAIR, bool STAGED>
 __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t xb0[BUF], xb1[BUF], wb0[BUF], wb1[BUF];
-  __shared__ float2 tab[256 * TABC];
+  __shared__ float2 tab[STAGED ? 1 : 256 * TABC];
+  __shared__ __attribute__((aligned(16))) uint16_t xb2[STAGED ? BUF : 8];   // the table's space
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WAVES_M, wn = wave / WAVES_M;
   const int64_t cols_per_tile = PAIR ? BN / 2 : BN;
@@ -1082,7 +1096,7 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
   int64_t tm, tn;
   grouped_tile(xcd_tile(blockIdx.x, nt_m * nt_n), nt_m, nt_n, GROUP_M, tm, tn);
   const int64_t m0 = tm * BM;
-  build_tab(tab, p.code, p.order, tid);
+  if constexpr (!STAGED) build_tab(tab, p.code, p.order, tid);
   const float2* tabc = tab + (lane & (TABC - 1));
 
   FragOff fo;
@@ -1125,19 +1139,6 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
   // this workgroup's steps: all of them, or split blockIdx.y's range (an even count)
   const int sbeg = p.part ? (int)blockIdx.y * p.split_steps : 0;
   const int send = p.part ? min(ks, sbeg + p.split_steps) : ks;
-  WBytes r0, r1;
-  x_load(xb0, (int64_t)sbeg * BK);
-  w_load(r0, (int64_t)sbeg * BK);
-  wait_vm0();
-  __syncthreads();  // table, X(sbeg)
-  {
-    float2 c[4];
-#pragma unroll
-    for (int d = 0; d < 4; ++d) { w_lookup(r0, tabc, d, c); w_finish(c, r0.sc, wb0, wR, wh, d); }
-  }
-  w_load(r0, min((int64_t)(sbeg + 1) * BK, klast));
-  wait_vm0();
-  __syncthreads();
 
   bf16x8_t a[2][TM], b[2][TN];
 #pragma unroll
@@ -1145,34 +1146,116 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
 #pragma unroll
   for (int j = 0; j < TN; ++j) b[1][j] = bf16x8_t{};
 
-  auto step = [&](int s, const WBytes& cw, WBytes& nw, const uint16_t* xc, const uint16_t* wc, uint16_t* xn,
-                  uint16_t* wnx) {
-    const int64_t k1 = min((int64_t)(s + 1) * BK, klast), k2 = min((int64_t)(s + 2) * BK, klast);
-    float2 c[4];
-    load_frags(wc, xc, fo, 0, a[0], b[0]);
-    mfma_set(a[1], b[1], acc);
-    x_load(xn, k1);
-    dma_then_loads();
-    w_load(nw, k2);
-    w_lookup(cw, tabc, 0, c);
-    __builtin_amdgcn_sched_barrier(0);
+  if constexpr (STAGED) {
+    // W tile row R by DMA from row n of its weight's bf16 copy; a DMA block is
+    // 8 rows of one weight (gate and up alternate every 64 rows), so the
+    // buffer resource is uniform per instruction.
+    const __amdgpu_buffer_rsrc_t ws0 = make_rsrc(p.wst[0], p.N * p.ldw * 2);
+    const __amdgpu_buffer_rsrc_t ws1 = make_rsrc(p.wst[PAIR ? 1 : 0], p.N * p.ldw * 2);
+    uint32_t wdoff[4];
+    int wsel[4];
 #pragma unroll
-    for (int kk = 0; kk < 3; ++kk) {
-      load_frags(wc, xc, fo, kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
-      mfma_set(a[kk & 1], b[kk & 1], acc);
-      w_finish(c, cw.sc, wnx, wR, wh, kk);
-      w_lookup(cw, tabc, kk + 1, c);
-      interleave_substep();
-      __builtin_amdgcn_sched_barrier(0);
+    for (int c = 0; c < 4; ++c) {
+      int R, k, which;
+      int64_t nr;
+      dma_slot(wave * 4 + c, lane, R, k);
+      fwd_row(R, tn, PAIR, which, nr);
+      wsel[c] = __builtin_amdgcn_readfirstlane(which);
+      wdoff[c] = (uint32_t)((min(nr, p.N - 1) * p.ldw + k) * 2);
     }
-    w_finish(c, cw.sc, wnx, wR, wh, 3);
-    wait_vm_at_most<WBytes::kLoads>();            // X(s + 1) landed; only W(s + 2)'s loads may fly
+    auto w_dma = [&](uint16_t* dst, int64_t k0) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        buf_load_lds16(wsel[c] ? ws1 : ws0, dst + (wave * 4 + c) * 512, wdoff[c], (uint32_t)(k0 * 2));
+    };
+    // X in a ring of three buffers, loaded two steps ahead; W in two, one
+    // step ahead (its tiles are shared by every row block, mostly from L2).
+    x_load(xb0, (int64_t)sbeg * BK);
+    w_dma(wb0, (int64_t)sbeg * BK);
+    x_load(xb1, min((int64_t)(sbeg + 1) * BK, klast));
+    wait_vm_at_most<kStageDma>();                    // X(sbeg), W(sbeg) landed; X(sbeg + 1) may fly
     step_barrier();
-  };
-  // W(s + 1) sits in r0 during even steps and in r1 during odd ones; the LDS buffers alternate likewise.
-  for (int s = sbeg; s < send; s += 2) {
-    step(s, r0, r1, xb0, wb0, xb1, wb1);
-    step(s + 1, r1, r0, xb1, wb1, xb0, wb0);
+    auto step = [&](int s, const uint16_t* xc, const uint16_t* wc, uint16_t* x2, uint16_t* wnx) {
+      load_frags(wc, xc, fo, 0, a[0], b[0]);
+      mfma_set(a[1], b[1], acc);
+      w_dma(wnx, min((int64_t)(s + 1) * BK, klast));
+      dma_then_loads();                              // keep W(s + 1) issued before X(s + 2)
+      x_load(x2, min((int64_t)(s + 2) * BK, klast));
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int kk = 0; kk < 3; ++kk) {
+        load_frags(wc, xc, fo, kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
+        mfma_set(a[kk & 1], b[kk & 1], acc);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      wait_vm_at_most<kStageDma>();                  // W(s + 1), X(s + 1) landed; X(s + 2) may fly
+      step_barrier();
+    };
+    // buffers of step s: X s % 3, W s % 2, so the pattern repeats every 6 steps
+    int s = sbeg;
+    for (; s + 6 <= send; s += 6) {
+      step(s, xb0, wb0, xb2, wb1);
+      step(s + 1, xb1, wb1, xb0, wb0);
+      step(s + 2, xb2, wb0, xb1, wb1);
+      step(s + 3, xb0, wb1, xb2, wb0);
+      step(s + 4, xb1, wb0, xb0, wb1);
+      step(s + 5, xb2, wb1, xb1, wb0);
+    }
+    if (s + 2 <= send) {
+      step(s, xb0, wb0, xb2, wb1);
+      step(s + 1, xb1, wb1, xb0, wb0);
+      s += 2;
+    }
+    if (s + 2 <= send) {
+      step(s, xb2, wb0, xb1, wb1);
+      step(s + 1, xb0, wb1, xb2, wb0);
+    }
+    wait_vm0();                                      // the last step's X(s + 2), never read
+    __syncthreads();
+  } else {
+    WBytes r0, r1;
+    x_load(xb0, (int64_t)sbeg * BK);
+    w_load(r0, (int64_t)sbeg * BK);
+    wait_vm0();
+    __syncthreads();  // table, X(sbeg)
+    {
+      float2 c[4];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) { w_lookup(r0, tabc, d, c); w_finish(c, r0.sc, wb0, wR, wh, d); }
+    }
+    w_load(r0, min((int64_t)(sbeg + 1) * BK, klast));
+    wait_vm0();
+    __syncthreads();
+
+    auto step = [&](int s, const WBytes& cw, WBytes& nw, const uint16_t* xc, const uint16_t* wc, uint16_t* xn,
+                    uint16_t* wnx) {
+      const int64_t k1 = min((int64_t)(s + 1) * BK, klast), k2 = min((int64_t)(s + 2) * BK, klast);
+      float2 c[4];
+      load_frags(wc, xc, fo, 0, a[0], b[0]);
+      mfma_set(a[1], b[1], acc);
+      x_load(xn, k1);
+      dma_then_loads();
+      w_load(nw, k2);
+      w_lookup(cw, tabc, 0, c);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int kk = 0; kk < 3; ++kk) {
+        load_frags(wc, xc, fo, kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
+        mfma_set(a[kk & 1], b[kk & 1], acc);
+        w_finish(c, cw.sc, wnx, wR, wh, kk);
+        w_lookup(cw, tabc, kk + 1, c);
+        interleave_substep();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      w_finish(c, cw.sc, wnx, wR, wh, 3);
+      wait_vm_at_most<WBytes::kLoads>();            // X(s + 1) landed; only W(s + 2)'s loads may fly
+      step_barrier();
+    };
+    // W(s + 1) sits in r0 during even steps and in r1 during odd ones; the LDS buffers alternate likewise.
+    for (int s = sbeg; s < send; s += 2) {
+      step(s, r0, r1, xb0, wb0, xb1, wb1);
+      step(s + 1, r1, r0, xb1, wb1, xb0, wb0);
+    }
   }
   mfma_set(a[1], b[1], acc);
   // the LoRA steps belong to the last split (uniform per workgroup)
@@ -1230,6 +1313,12 @@ struct WPatch {
   uint32_t q[kRows];
   float sc[kRows];
 };
+
+// Column group of a lane's 4 x 8 patch (the row group is tid / 32, so lanes l
+// and l + 32 share a column group).
+MOLT_DEV int patch_cg(int lane) {
+  return (lane & 1) | (((lane >> 2) & 1) << 1) | (((lane >> 3) & 3) << 2) | (((lane >> 1) & 1) << 4);
+}
 
 // Lookups of byte b of the four patch rows: columns 2b, 2b + 1.
 MOLT_DEV void wp_lookup(const WPatch& w, const float2* tabc, int b, float2 (&c)[4]) {
@@ -1410,17 +1499,21 @@ MOLT_DEV void interleave_substep_bwd() {
 // in registers, dequantised (one patch row per sub-step) into the other W
 // buffer, last sub-step's MFMAs carried across the barrier. Requires
 // Nw % 64 == 0, Kw % 8 == 0, an even number of steps and block size 64.
-template <int EPI>
+// STAGED: the W tile arrives by DMA from the transposed bf16 copy p.wst of
+// each segment (row = output column, as the tile stores it), like the
+// forward's staged variant.
+template <int EPI, bool STAGED>
 __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t xb0[BUF], xb1[BUF], wb0[BUF], wb1[BUF];
-  __shared__ float2 tab[256 * TABC];
+  __shared__ float2 tab[STAGED ? 1 : 256 * TABC];
+  __shared__ __attribute__((aligned(16))) uint16_t xb2[STAGED ? BUF : 8];   // the table's space
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WAVES_M, wn = wave / WAVES_M;
   const int64_t nt_m = ceil_div64(p.M, BM), nt_n = ceil_div64(p.Kw, BN);
   int64_t tm, tn;
   grouped_tile(xcd_tile(blockIdx.x, nt_m * nt_n), nt_m, nt_n, GROUP_M, tm, tn);
   const int64_t m0 = tm * BM;
-  build_tab(tab, p.code, p.order, tid);
+  if constexpr (!STAGED) build_tab(tab, p.code, p.order, tid);
   const float2* tabc = tab + (lane & (TABC - 1));
 
   FragOff fo;
@@ -1446,8 +1539,7 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
   // 16-byte slot (chunk position) mod 8; for the transposed store of row
   // R = 8 cg + k (+4) the position is m ^ f(R) and f(R) varies with cg & 3
   // only, so lane bits 0 and 2 carry those (two lanes per slot).
-  const int cg = (lane & 1) | (((lane >> 2) & 1) << 1) | (((lane >> 3) & 3) << 2) | (((lane >> 1) & 1) << 4);
-  const int rg = tid >> 5;
+  const int cg = patch_cg(lane), rg = tid >> 5;
   const int64_t col = min(tn * BN + 8 * cg, p.Kw - 8);
   const int64_t wbytes = p.Nw * p.Kw / 2, sbytes = p.Nw * p.Kw / 16;
   const __amdgpu_buffer_rsrc_t wr0 = make_rsrc(p.packed[0], wbytes), wr1 = make_rsrc(p.packed[1], wbytes);
@@ -1480,15 +1572,6 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
   // this workgroup's steps: all of them, or split blockIdx.y's range (an even count)
   const int sbeg = p.part ? (int)blockIdx.y * p.split_steps : 0;
   const int send = p.part ? min(ks, sbeg + p.split_steps) : ks;
-  WPatch r0, r1;
-  x_load(xb0, sbeg);
-  w_load(r0, sbeg);
-  wait_vm0();
-  __syncthreads();  // table, X(sbeg)
-  wp_commit(r0, tabc, wb0, cg, rg);
-  w_load(r0, sbeg + 1);
-  wait_vm0();
-  __syncthreads();
 
   bf16x8_t a[2][TM], b[2][TN];
 #pragma unroll
@@ -1496,49 +1579,123 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
 #pragma unroll
   for (int j = 0; j < TN; ++j) b[1][j] = bf16x8_t{};
 
-  // Dequant of W(s+1) across the sub-steps: column pairs (0,1), (4,5) then
-  // (2,3), (6,7), each pair's lookups one sub-step ahead; columns k and k + 4
-  // are written together after the lane exchange.
-  auto step = [&](int s, const WPatch& cw, WPatch& nw, const uint16_t* xc, const uint16_t* wc, uint16_t* xn,
-                  uint16_t* wnx) {
-    float2 c[4];
-    u32x2_t c0, c1, c4, c5;
-    load_frags(wc, xc, fo, 0, a[0], b[0]);
-    mfma_set(a[1], b[1], acc);
-    x_load(xn, s + 1);
-    dma_then_loads();
-    w_load(nw, s + 2);
-    wp_lookup(cw, tabc, 0, c);
-    __builtin_amdgcn_sched_barrier(0);
-    load_frags(wc, xc, fo, 1, a[1], b[1]);
-    mfma_set(a[0], b[0], acc);
-    wp_finish(c, cw.sc, c0, c1);
-    wp_lookup(cw, tabc, 2, c);
-    interleave_substep_bwd<0>();
-    __builtin_amdgcn_sched_barrier(0);
-    load_frags(wc, xc, fo, 2, a[0], b[0]);
-    mfma_set(a[1], b[1], acc);
-    wp_finish(c, cw.sc, c4, c5);
-    wp_swap_write(c0, c4, wnx, cg, rg, 0);
-    wp_swap_write(c1, c5, wnx, cg, rg, 1);
-    wp_lookup(cw, tabc, 1, c);
-    interleave_substep_bwd<2>();
-    __builtin_amdgcn_sched_barrier(0);
-    load_frags(wc, xc, fo, 3, a[1], b[1]);
-    mfma_set(a[0], b[0], acc);
-    wp_finish(c, cw.sc, c0, c1);
-    wp_lookup(cw, tabc, 3, c);
-    interleave_substep_bwd<0>();
-    __builtin_amdgcn_sched_barrier(0);
-    wp_finish(c, cw.sc, c4, c5);
-    wp_swap_write(c0, c4, wnx, cg, rg, 2);
-    wp_swap_write(c1, c5, wnx, cg, rg, 3);
-    wait_vm_at_most<WPatch::kLoads>();            // dY(s + 1) landed; only W(s + 2)'s loads may fly
+  if constexpr (STAGED) {
+    // W tile row R = output column tn * BN + R, the row of the segment's
+    // transposed copy; the step's contraction rows are its columns c0 .. c0 + 63.
+    const int64_t wtbytes = p.Kw * p.ldw * 2;
+    const __amdgpu_buffer_rsrc_t ws0 = make_rsrc(p.wst[0], wtbytes), ws1 = make_rsrc(p.wst[1], wtbytes);
+    uint32_t wdoff[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      int R, k;
+      dma_slot(wave * 4 + c, lane, R, k);
+      wdoff[c] = (uint32_t)((min(tn * BN + R, p.Kw - 1) * p.ldw + k) * 2);
+    }
+    auto w_dma = [&](uint16_t* dst, int s) {
+      const __amdgpu_buffer_rsrc_t wr = seg_of(s) ? ws1 : ws0;
+      const uint32_t so = (uint32_t)(c0_of(s) * 2);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) buf_load_lds16(wr, dst + (wave * 4 + c) * 512, wdoff[c], so);
+    };
+    // dY in a ring of three buffers, loaded two steps ahead; W in two, one
+    // step ahead (as in the staged forward kernel).
+    x_load(xb0, sbeg);
+    w_dma(wb0, sbeg);
+    x_load(xb1, sbeg + 1);
+    wait_vm_at_most<kStageDma>();                    // dY(sbeg), W(sbeg) landed; dY(sbeg + 1) may fly
     step_barrier();
-  };
-  for (int s = sbeg; s < send; s += 2) {
-    step(s, r0, r1, xb0, wb0, xb1, wb1);
-    step(s + 1, r1, r0, xb1, wb1, xb0, wb0);
+    auto step = [&](int s, const uint16_t* xc, const uint16_t* wc, uint16_t* x2, uint16_t* wnx) {
+      load_frags(wc, xc, fo, 0, a[0], b[0]);
+      mfma_set(a[1], b[1], acc);
+      w_dma(wnx, s + 1);
+      dma_then_loads();                              // keep W(s + 1) issued before dY(s + 2)
+      x_load(x2, s + 2);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int kk = 0; kk < 3; ++kk) {
+        load_frags(wc, xc, fo, kk + 1, a[(kk + 1) & 1], b[(kk + 1) & 1]);
+        mfma_set(a[kk & 1], b[kk & 1], acc);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      wait_vm_at_most<kStageDma>();                  // W(s + 1), dY(s + 1) landed; dY(s + 2) may fly
+      step_barrier();
+    };
+    // buffers of step s: dY s % 3, W s % 2, so the pattern repeats every 6 steps
+    int s = sbeg;
+    for (; s + 6 <= send; s += 6) {
+      step(s, xb0, wb0, xb2, wb1);
+      step(s + 1, xb1, wb1, xb0, wb0);
+      step(s + 2, xb2, wb0, xb1, wb1);
+      step(s + 3, xb0, wb1, xb2, wb0);
+      step(s + 4, xb1, wb0, xb0, wb1);
+      step(s + 5, xb2, wb1, xb1, wb0);
+    }
+    if (s + 2 <= send) {
+      step(s, xb0, wb0, xb2, wb1);
+      step(s + 1, xb1, wb1, xb0, wb0);
+      s += 2;
+    }
+    if (s + 2 <= send) {
+      step(s, xb2, wb0, xb1, wb1);
+      step(s + 1, xb0, wb1, xb2, wb0);
+    }
+    wait_vm0();                                      // the last step's dY(s + 2), never read
+    __syncthreads();
+  } else {
+    WPatch r0, r1;
+    x_load(xb0, sbeg);
+    w_load(r0, sbeg);
+    wait_vm0();
+    __syncthreads();  // table, X(sbeg)
+    wp_commit(r0, tabc, wb0, cg, rg);
+    w_load(r0, sbeg + 1);
+    wait_vm0();
+    __syncthreads();
+
+    // Dequant of W(s+1) across the sub-steps: column pairs (0,1), (4,5) then
+    // (2,3), (6,7), each pair's lookups one sub-step ahead; columns k and k + 4
+    // are written together after the lane exchange.
+    auto step = [&](int s, const WPatch& cw, WPatch& nw, const uint16_t* xc, const uint16_t* wc, uint16_t* xn,
+                    uint16_t* wnx) {
+      float2 c[4];
+      u32x2_t c0, c1, c4, c5;
+      load_frags(wc, xc, fo, 0, a[0], b[0]);
+      mfma_set(a[1], b[1], acc);
+      x_load(xn, s + 1);
+      dma_then_loads();
+      w_load(nw, s + 2);
+      wp_lookup(cw, tabc, 0, c);
+      __builtin_amdgcn_sched_barrier(0);
+      load_frags(wc, xc, fo, 1, a[1], b[1]);
+      mfma_set(a[0], b[0], acc);
+      wp_finish(c, cw.sc, c0, c1);
+      wp_lookup(cw, tabc, 2, c);
+      interleave_substep_bwd<0>();
+      __builtin_amdgcn_sched_barrier(0);
+      load_frags(wc, xc, fo, 2, a[0], b[0]);
+      mfma_set(a[1], b[1], acc);
+      wp_finish(c, cw.sc, c4, c5);
+      wp_swap_write(c0, c4, wnx, cg, rg, 0);
+      wp_swap_write(c1, c5, wnx, cg, rg, 1);
+      wp_lookup(cw, tabc, 1, c);
+      interleave_substep_bwd<2>();
+      __builtin_amdgcn_sched_barrier(0);
+      load_frags(wc, xc, fo, 3, a[1], b[1]);
+      mfma_set(a[0], b[0], acc);
+      wp_finish(c, cw.sc, c0, c1);
+      wp_lookup(cw, tabc, 3, c);
+      interleave_substep_bwd<0>();
+      __builtin_amdgcn_sched_barrier(0);
+      wp_finish(c, cw.sc, c4, c5);
+      wp_swap_write(c0, c4, wnx, cg, rg, 2);
+      wp_swap_write(c1, c5, wnx, cg, rg, 3);
+      wait_vm_at_most<WPatch::kLoads>();            // dY(s + 1) landed; only W(s + 2)'s loads may fly
+      step_barrier();
+    };
+    for (int s = sbeg; s < send; s += 2) {
+      step(s, r0, r1, xb0, wb0, xb1, wb1);
+      step(s + 1, r1, r0, xb1, wb1, xb0, wb0);
+    }
   }
   mfma_set(a[1], b[1], acc);
   // the LoRA steps belong to the last split (uniform per workgroup)
@@ -1583,6 +1740,53 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
   swiglu_load(in, p, m0, tn, tid);
   __syncthreads();
   swiglu_bwd_store(ep, p, m0, tn, tid, in);
+}
+
+// Transposed bf16 copy of one or two weights for the staged input-gradient
+// kernels: wt[k][n] = bf16(code(W[n][k]) * scale(n, k / 64)), the values the
+// fused kernel dequantises into its W tile. A workgroup converts tiles of 64
+// weight rows x 256 columns with the fused kernel's 4 x 8 patches and lane
+// exchange into an LDS tile in the operand layout (row = column k of W), then
+// writes the tile's 256 rows of 128 bytes, 8 lanes per row, as whole-line
+// 16-byte stores. blockIdx.z selects the weight. Requires Nw % 64 == 0,
+// Kw % 256 == 0 and 4-byte aligned packed data.
+struct StageTParams {
+  const uint8_t* packed[2]; const float* scales[2]; uint16_t* wt[2];
+  const float* code; int order; int64_t Nw, Kw, ldw;
+};
+
+__global__ __launch_bounds__(NT) void stage_wt_kernel(const StageTParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[BUF];
+  __shared__ float2 tab[256 * TABC];
+  const int tid = threadIdx.x, lane = tid & 63;
+  build_tab(tab, p.code, p.order, tid);
+  const float2* tabc = tab + (lane & (TABC - 1));
+  const int seg = blockIdx.z;
+  const uint8_t* packed = sel(p.packed, seg);
+  const float* scales = sel(p.scales, seg);
+  uint16_t* wt = sel(p.wt, seg);
+  const int cg = patch_cg(lane), rg = tid >> 5;
+  const int64_t col = (int64_t)blockIdx.x * BN + 8 * cg;
+  const int64_t n_tiles = p.Nw / 64;
+  __syncthreads();  // table
+  for (int64_t nt = blockIdx.y; nt < n_tiles; nt += gridDim.y) {
+    WPatch w;
+#pragma unroll
+    for (int r = 0; r < WPatch::kRows; ++r) {
+      const int64_t n = nt * 64 + 4 * rg + r;
+      w.q[r] = *reinterpret_cast<const uint32_t*>(packed + n * (p.Kw / 2) + col / 2);
+      w.sc[r] = scales[n * (p.Kw / 64) + col / 64];
+    }
+    wp_commit(w, tabc, tile, cg, rg);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < BUF / 8 / NT; ++i) {
+      const int q = tid + NT * i, R = q >> 3, c = q & 7;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(tile + loff(R, c));
+      *reinterpret_cast<u32x4_t*>(wt + ((int64_t)blockIdx.x * BN + R) * p.ldw + nt * 64 + 8 * c) = v;
+    }
+    __syncthreads();
+  }
 }
 
 }  // namespace big
@@ -1698,6 +1902,49 @@ GemmPlan bwd_plan(int64_t M, int64_t Nw, int64_t Kw, int nseg, bool swiglu, bool
 
 size_t split_bytes(int S, int64_t M, int64_t N) { return S > 1 ? (size_t)S * M * N * sizeof(float) : 0; }
 
+// Staged weights: a 256 x 256 GEMM over many 256-row blocks of X (dY)
+// dequantises each weight tile once per row block. From
+// MOLT_TUNE_STAGE_MIN_MTILES row blocks on, one pass writes the bf16 weight
+// (transposed for the input gradient) to the caller's workspace and the
+// kernels read it by DMA; the weight tile values, and so the results, are the
+// same. The copy is addressed with 32-bit offsets.
+bool stage_wanted(int kind, int64_t M, int64_t rows, int64_t cols) {
+  const int64_t t = molt::tuning_value(MOLT_TUNE_STAGE_MIN_MTILES);
+  return (kind == PLAN_BIG || kind == PLAN_BIG_SPLIT) && t > 0 && ceil_div64(M, big::BM) >= t &&
+         rows * cols * 2 < 0x7fffffffll;
+}
+size_t stage_one(int64_t rows, int64_t cols) { return (size_t)(rows * cols * 2 + 255) / 256 * 256; }
+
+// molt_amd_time_next_gemm: its events are recorded right around the GEMM
+// kernel's launch (construct before, finish() after).
+struct KernelEvents {
+  void* start = nullptr;
+  void* end = nullptr;
+  hipStream_t stream;
+  explicit KernelEvents(hipStream_t s) : stream(s) {
+    molt::take_gemm_events(&start, &end);
+    if (start) (void)hipEventRecord(static_cast<hipEvent_t>(start), stream);
+  }
+  void finish() {
+    if (end) (void)hipEventRecord(static_cast<hipEvent_t>(end), stream);
+  }
+};
+
+// Workspace layout of the GEMM entry points: the staged weights (if any),
+// then the split-K partials (if any).
+struct GemmWorkspace { bool stage, split; size_t stage_bytes; };
+GemmWorkspace place_workspace(const GemmPlan& plan, bool want_stage, int weights, int64_t rows, int64_t cols,
+                              int64_t M, int64_t out_n, const void* ws, size_t ws_bytes) {
+  GemmWorkspace g{false, false, 0};
+  const size_t sb = want_stage ? weights * stage_one(rows, cols) : 0;
+  const size_t pb = split_bytes(plan.S, M, out_n);
+  const bool usable = ws && aligned(ws, 256);
+  g.stage = want_stage && usable && ws_bytes >= sb + pb;
+  g.stage_bytes = g.stage ? sb : 0;
+  g.split = plan.S > 1 && usable && ws_bytes >= g.stage_bytes + pb;
+  return g;
+}
+
 int check_weight_for_gemm(const molt_nf4_weight* w, const char* who) {
   MOLT_REQUIRE(w && w->packed && w->code, MOLT_EINVAL, "%s: weight, packed and code are required", who);
   MOLT_REQUIRE(w->scales, MOLT_EINVAL, "%s: resolved fp32 scales are required (molt_nf4_resolve_scales)", who);
@@ -1754,17 +2001,39 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
                   aligned(w0->packed, 16) && (!pair || aligned(w1->packed, 16));
   const int64_t big_tiles = ceil_div64(M, big::BM) * ceil_div64(p.N, pair ? big::BN / 2 : big::BN);
   const GemmPlan plan = fwd_plan(M, p.N, p.K, pair, fwd_big_ok(M, ldx, p.N, p.K, al), al);
-  const size_t need = split_bytes(plan.S, M, p.N);
-  const bool split = plan.S > 1 && workspace && workspace_bytes >= need && aligned(workspace, 16);
+  const GemmWorkspace gw = place_workspace(plan, stage_wanted(plan.kind, M, p.N, p.K), pair ? 2 : 1, p.N, p.K, M,
+                                           p.N, workspace, workspace_bytes);
+  char* wsb = static_cast<char*>(workspace);
+  const bool split = gw.split;
   if (plan.kind == PLAN_BIG || (plan.kind == PLAN_BIG_SPLIT && split)) {
     MOLT_REQUIRE(big_tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
     if (plan.kind == PLAN_BIG_SPLIT) {
       p.split_steps = plan.split_steps;
-      p.part = static_cast<float*>(workspace);
+      p.part = reinterpret_cast<float*>(wsb + gw.stage_bytes);
+    }
+    if (gw.stage) {
+      // the bf16 weight rows (resolved scales, so the flat-scale dequant)
+      for (int i = 0; i < (pair ? 2 : 1); ++i) {
+        molt_nf4_weight flat = *(i ? w1 : w0);
+        flat.nested = 0;
+        uint16_t* dst = reinterpret_cast<uint16_t*>(wsb + i * stage_one(p.N, p.K));
+        rc = molt_nf4_dequantize(&flat, dst, MOLT_DTYPE_BF16, stream);
+        if (rc) return rc;
+        p.wst[i] = dst;
+      }
+      if (!pair) p.wst[1] = p.wst[0];
+      p.ldw = p.K;
     }
     dim3 grid((unsigned)big_tiles, (unsigned)plan.S), block(big::NT);
-    if (pair) hipLaunchKernelGGL((big::fwd_kernel<true>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((big::fwd_kernel<false>), grid, block, 0, stream, p);
+    KernelEvents kev(stream);
+    if (gw.stage) {
+      if (pair) hipLaunchKernelGGL((big::fwd_kernel<true, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((big::fwd_kernel<false, true>), grid, block, 0, stream, p);
+    } else {
+      if (pair) hipLaunchKernelGGL((big::fwd_kernel<true, false>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((big::fwd_kernel<false, false>), grid, block, 0, stream, p);
+    }
+    kev.finish();
   } else {
     const int64_t cols_per_tile = pair ? BN / 2 : BN;
     const int64_t tiles = ceil_div64(M, BM) * ceil_div64(p.N, cols_per_tile);
@@ -1775,6 +2044,7 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
       p.part = static_cast<float*>(workspace);
     }
     dim3 grid((unsigned)tiles, small_split ? (unsigned)plan.S : 1u), block(NT);
+    KernelEvents kev(stream);
     if (pair) {
       if (al) hipLaunchKernelGGL((nf4_fwd_kernel<true, true>), grid, block, 0, stream, p);
       else hipLaunchKernelGGL((nf4_fwd_kernel<true, false>), grid, block, 0, stream, p);
@@ -1782,6 +2052,7 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
       if (al) hipLaunchKernelGGL((nf4_fwd_kernel<false, true>), grid, block, 0, stream, p);
       else hipLaunchKernelGGL((nf4_fwd_kernel<false, false>), grid, block, 0, stream, p);
     }
+    kev.finish();
   }
   if (p.part) {
     rc = check_launch(who);
@@ -1846,17 +2117,45 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
   const bool big_ok = al && aligned(w0->packed, 4) && (nseg == 1 || aligned(w1->packed, 4)) &&
                       bwd_big_ok(M, lddy, p.Nw, p.Kw, nseg);
   const GemmPlan plan = bwd_plan(M, p.Nw, p.Kw, nseg, swiglu, big_ok, al);
-  const size_t need = split_bytes(plan.S, M, p.Kw);
-  const bool split = plan.S > 1 && workspace && workspace_bytes >= need && aligned(workspace, 16);
+  const bool want_stage = stage_wanted(plan.kind, M, p.Nw, p.Kw) && p.Kw % big::BN == 0;
+  const GemmWorkspace gw = place_workspace(plan, want_stage, nseg, p.Nw, p.Kw, M, p.Kw, workspace, workspace_bytes);
+  char* wsb = static_cast<char*>(workspace);
+  const bool split = gw.split;
   if (plan.kind == PLAN_BIG || (plan.kind == PLAN_BIG_SPLIT && split)) {
     MOLT_REQUIRE(big_tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
     if (plan.kind == PLAN_BIG_SPLIT) {
       p.split_steps = plan.split_steps;
-      p.part = static_cast<float*>(workspace);
+      p.part = reinterpret_cast<float*>(wsb + gw.stage_bytes);
+    }
+    if (gw.stage) {
+      big::StageTParams sp{};
+      for (int i = 0; i < 2; ++i) {
+        const molt_nf4_weight* w = (i && w1) ? w1 : w0;
+        sp.packed[i] = w->packed;
+        sp.scales[i] = w->scales;
+        sp.wt[i] = reinterpret_cast<uint16_t*>(wsb + (i < nseg ? i : 0) * stage_one(p.Nw, p.Kw));
+        p.wst[i] = sp.wt[i];
+      }
+      sp.code = w0->code; sp.order = w0->nibble_order;
+      sp.Nw = p.Nw; sp.Kw = p.Kw; sp.ldw = p.ldw = p.Nw;
+      const int64_t col_tiles = p.Kw / big::BN, row_tiles = p.Nw / 64;
+      const int64_t per_col = std::max<int64_t>(1, std::min<int64_t>(row_tiles, ceil_div64(4 * molt::device_cus(),
+                                                                                        col_tiles * nseg)));
+      hipLaunchKernelGGL(big::stage_wt_kernel, dim3((unsigned)col_tiles, (unsigned)per_col, (unsigned)nseg),
+                         dim3(big::NT), 0, stream, sp);
+      rc = check_launch(who);
+      if (rc) return rc;
     }
     dim3 grid((unsigned)big_tiles, (unsigned)plan.S), block(big::NT);
-    if (swiglu) hipLaunchKernelGGL((big::bwd_kernel<EPI_SWIGLU_BWD>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((big::bwd_kernel<EPI_STORE>), grid, block, 0, stream, p);
+    KernelEvents kev(stream);
+    if (gw.stage) {
+      if (swiglu) hipLaunchKernelGGL((big::bwd_kernel<EPI_SWIGLU_BWD, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((big::bwd_kernel<EPI_STORE, true>), grid, block, 0, stream, p);
+    } else {
+      if (swiglu) hipLaunchKernelGGL((big::bwd_kernel<EPI_SWIGLU_BWD, false>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((big::bwd_kernel<EPI_STORE, false>), grid, block, 0, stream, p);
+    }
+    kev.finish();
   } else {
     const int64_t tiles = ceil_div64(M, BM) * ceil_div64(p.Kw, BN);
     MOLT_REQUIRE(tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
@@ -1866,6 +2165,7 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
       p.part = static_cast<float*>(workspace);
     }
     dim3 grid((unsigned)tiles, small_split ? (unsigned)plan.S : 1u), block(NT);
+    KernelEvents kev(stream);
     if (swiglu) {
       if (al) hipLaunchKernelGGL((nf4_bwd_kernel<EPI_SWIGLU_BWD, true>), grid, block, 0, stream, p);
       else hipLaunchKernelGGL((nf4_bwd_kernel<EPI_SWIGLU_BWD, false>), grid, block, 0, stream, p);
@@ -1873,6 +2173,7 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
       if (al) hipLaunchKernelGGL((nf4_bwd_kernel<EPI_STORE, true>), grid, block, 0, stream, p);
       else hipLaunchKernelGGL((nf4_bwd_kernel<EPI_STORE, false>), grid, block, 0, stream, p);
     }
+    kev.finish();
   }
   if (p.part) {
     rc = check_launch(who);
@@ -1891,11 +2192,18 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
 extern "C" size_t molt_nf4_lora_forward_workspace(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0) return 0;
   const GemmPlan plan = fwd_plan(M, N, K, false, fwd_big_ok(M, K, N, K, true), true);
-  return split_bytes(plan.S, M, N);
+  return (stage_wanted(plan.kind, M, N, K) ? stage_one(N, K) : 0) + split_bytes(plan.S, M, N);
+}
+
+extern "C" size_t molt_nf4_gateup_forward_workspace(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0) return 0;
+  const GemmPlan plan = fwd_plan(M, N, K, true, fwd_big_ok(M, K, N, K, true), true);
+  return stage_wanted(plan.kind, M, N, K) ? 2 * stage_one(N, K) : 0;
 }
 
 extern "C" size_t molt_nf4_lora_backward_workspace(int64_t M, int64_t Nw, int64_t Kw, int32_t nseg) {
   if (M <= 0 || Nw <= 0 || Kw <= 0 || Nw % 64 != 0 || Kw % 64 != 0 || nseg < 1 || nseg > 2) return 0;
   const GemmPlan plan = bwd_plan(M, Nw, Kw, nseg, false, bwd_big_ok(M, Nw, Nw, Kw, nseg), true);
-  return split_bytes(plan.S, M, Kw);
+  const bool stage = stage_wanted(plan.kind, M, Nw, Kw) && Kw % big::BN == 0;
+  return (stage ? nseg * stage_one(Nw, Kw) : 0) + split_bytes(plan.S, M, Kw);
 }

@@ -214,8 +214,11 @@ _probes: dict[str, list] = {}
 
 
 def probe_events(name: str, enable: bool = True) -> list:
-    """Start (or stop) recording HIP events around every launch of the C entry
-    point ``name``; returns the list that collects (start, end) pairs."""
+    """Start (or stop) recording HIP events around every call of the C entry
+    point ``name``; returns the list that collects (start, end) pairs. For the
+    NF4 GEMM entry points the library records them around the GEMM kernel
+    itself (``molt_amd_time_next_gemm``), leaving out weight staging and
+    split-K sums."""
     if enable:
         return _probes.setdefault(name, [])
     return _probes.pop(name, [])
@@ -237,9 +240,17 @@ def _call(fn_name: str, *args) -> None:
     lib = _lib.load()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
+    if fn_name in _GEMM_ENTRIES:
+        end.record()   # creates the event; the library records both again around the kernel
+        _lib.check(lib.molt_amd_time_next_gemm(C.c_void_p(start.cuda_event), C.c_void_p(end.cuda_event)))
     _lib.check(getattr(lib, fn_name)(*args))
-    end.record()
+    if fn_name not in _GEMM_ENTRIES:
+        end.record()
     pairs.append((start, end))
+
+
+_GEMM_ENTRIES = frozenset(("molt_nf4_lora_forward", "molt_nf4_gateup_forward", "molt_nf4_lora_backward_input",
+                           "molt_nf4_lora_backward_input_pair", "molt_nf4_swiglu_backward"))
 
 
 # ----------------------------------------------------------------- codec
@@ -467,9 +478,11 @@ def nf4_gateup_forward(x: Tensor, packed_g: Tensor, scales_g: Tensor, packed_u: 
         bg, bu = _f32(lora_bg), _f32(lora_bu)
         if bg.shape != (rows, r) or bu.shape != (rows, r):
             raise ValueError(f"{what}: LoRA B shapes {tuple(bg.shape)}, {tuple(bu.shape)} != ({rows}, {r})")
+    ws_bytes = _workspace("molt_nf4_gateup_forward_workspace", m, rows, cols)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     _call("molt_nf4_gateup_forward", x.data_ptr(), cols, m, C.byref(wg), C.byref(wu), _ptr(tt),
           max(2 * r, 1), _ptr(bg), _ptr(bu), r, float(sg), float(su), outs[0].data_ptr(),
-          outs[1].data_ptr(), outs[2].data_ptr(), rows, _stream(dev))
+          outs[1].data_ptr(), outs[2].data_ptr(), rows, _ptr(ws), ws_bytes, _stream(dev))
     return outs[0], outs[1], outs[2]
 
 
@@ -593,8 +606,11 @@ def nf4_swiglu_backward(dy: Tensor, packed: Tensor, scales: Tensor, code: Tensor
         r = uu.shape[1]
         if aa.shape != (r, cols):
             raise ValueError("LoRA gradient and A matrix dimensions are incompatible")
+    ws_bytes = _workspace("molt_nf4_lora_backward_workspace", dy.shape[0], rows, cols, 1)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     _call("molt_nf4_swiglu_backward", dy.data_ptr(), rows, dy.shape[0], C.byref(w), _ptr(uu), max(r, 1),
-          _ptr(aa), r, gate.data_ptr(), up.data_ptr(), cols, dg.data_ptr(), du.data_ptr(), _stream(dev))
+          _ptr(aa), r, gate.data_ptr(), up.data_ptr(), cols, dg.data_ptr(), du.data_ptr(), _ptr(ws), ws_bytes,
+          _stream(dev))
     return dg, du
 
 

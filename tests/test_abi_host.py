@@ -223,13 +223,41 @@ def test_noalloc_gemv_refuses_oversized_partials_before_any_device_call():
 def test_split_k_workspace_queries_need_no_gpu():
     """The split plan: a long contraction with few 256 x 256 output tiles gets
     fp32 partials for S splits; a problem that fills the GPU gets none."""
-    lib = _lib.load()
-    assert lib.molt_nf4_lora_forward_workspace(8192, 14336, 4096) == 0
-    assert lib.molt_nf4_lora_forward_workspace(4096, 1536, 8960) == 2 * 4096 * 1536 * 4
-    assert lib.molt_nf4_lora_backward_workspace(4096, 8960, 1536, 2) == 2 * 4096 * 1536 * 4
-    assert lib.molt_nf4_lora_backward_workspace(8192, 14336, 4096, 2) == 0
-    assert lib.molt_nf4_lora_forward_workspace(4096, 1000, 8960) == 0       # N not a multiple of 256
     from molt_amd._lib import tuning
 
-    with tuning(split_k=0):
-        assert lib.molt_nf4_lora_forward_workspace(4096, 1536, 8960) == 0
+    lib = _lib.load()
+    with tuning(stage_min_mtiles=0):
+        assert lib.molt_nf4_lora_forward_workspace(8192, 14336, 4096) == 0
+        assert lib.molt_nf4_lora_forward_workspace(4096, 1536, 8960) == 2 * 4096 * 1536 * 4
+        assert lib.molt_nf4_lora_backward_workspace(4096, 8960, 1536, 2) == 2 * 4096 * 1536 * 4
+        assert lib.molt_nf4_lora_backward_workspace(8192, 14336, 4096, 2) == 0
+        assert lib.molt_nf4_lora_forward_workspace(4096, 1000, 8960) == 0       # N not a multiple of 256
+        with tuning(split_k=0):
+            assert lib.molt_nf4_lora_forward_workspace(4096, 1536, 8960) == 0
+
+
+def _stage(rows, cols):
+    return (rows * cols * 2 + 255) // 256 * 256
+
+
+def test_staged_weight_workspace_queries_need_no_gpu():
+    """From stage_min_mtiles 256-row blocks of X (default 16) the large-tile
+    GEMMs take a bf16 copy of each weight first in the workspace, then any
+    split-K partials; fewer rows, or a setting of 0, stage nothing."""
+    from molt_amd._lib import tuning
+
+    lib = _lib.load()
+    assert lib.molt_amd_get_tuning(_lib.TUNING_KEYS["stage_min_mtiles"]) == 16
+    assert lib.molt_nf4_lora_forward_workspace(8192, 14336, 4096) == _stage(14336, 4096)
+    assert lib.molt_nf4_gateup_forward_workspace(8192, 14336, 4096) == 2 * _stage(14336, 4096)
+    assert lib.molt_nf4_lora_backward_workspace(8192, 14336, 4096, 2) == 2 * _stage(14336, 4096)
+    assert lib.molt_nf4_lora_backward_workspace(8192, 4096, 14336, 1) == _stage(4096, 14336)
+    assert lib.molt_nf4_lora_forward_workspace(4096, 1536, 8960) == _stage(1536, 8960) + 2 * 4096 * 1536 * 4
+    assert lib.molt_nf4_lora_backward_workspace(4096, 8960, 1536, 2) == 2 * _stage(8960, 1536) + 2 * 4096 * 1536 * 4
+    assert lib.molt_nf4_lora_forward_workspace(2048, 14336, 4096) == 0          # 8 row blocks
+    assert lib.molt_nf4_gateup_forward_workspace(256, 14336, 4096) == 0
+    assert lib.molt_nf4_lora_backward_workspace(8192, 1024, 4160, 1) == 0       # Kw not a multiple of 256
+    with tuning(stage_min_mtiles=0):
+        assert lib.molt_nf4_gateup_forward_workspace(8192, 14336, 4096) == 0
+    with tuning(stage_min_mtiles=8):
+        assert lib.molt_nf4_lora_forward_workspace(2048, 14336, 4096) == _stage(14336, 4096)
