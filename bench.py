@@ -496,15 +496,16 @@ def lm_head_bench(dev, steps: int = 5):
             "row_kernel_frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
 
 
-# (C entry point, kernel it launches, algorithmic FLOPs per launch at (M, H, I, r))
+# (C entry point, the GEMM kernel it launches at cfg4 (the staged-weight variants), algorithmic FLOPs
+# per launch at (M, H, I, r))
 GEMMS = (
-    ("molt_nf4_gateup_forward", "big::fwd_kernel<true> (gate/up forward)",
+    ("molt_nf4_gateup_forward", "big::fwd_kernel<true, true> (gate/up forward)",
      lambda M, H, I, r: 2 * (2 * M * H * I) + 2 * (2 * M * I * r)),
-    ("molt_nf4_lora_forward", "big::fwd_kernel<false> (down forward)",
+    ("molt_nf4_lora_forward", "big::fwd_kernel<false, true> (down forward)",
      lambda M, H, I, r: 2 * M * I * H + 2 * M * H * r),
-    ("molt_nf4_swiglu_backward", "big::bwd_kernel<2> (down dX + SwiGLU backward)",
+    ("molt_nf4_swiglu_backward", "big::bwd_kernel<2, true> (down dX + SwiGLU backward)",
      lambda M, H, I, r: 2 * M * H * I + 2 * M * r * I),
-    ("molt_nf4_lora_backward_input_pair", "big::bwd_kernel<0> (paired gate/up dX)",
+    ("molt_nf4_lora_backward_input_pair", "big::bwd_kernel<0, true> (paired gate/up dX)",
      lambda M, H, I, r: 2 * (2 * M * I * H) + 2 * (2 * M * r * H)),
 )
 TRAFFIC_FILE = ROOT / "profiles" / "gemm_cfg4_hbm_traffic.txt"
