@@ -106,7 +106,7 @@ extern "C" {
 
 const char* molt_amd_last_error(void) { return molt::g_last_error; }
 
-const char* molt_amd_version(void) { return "molt_amd 0.2.0 gfx950"; }
+const char* molt_amd_version(void) { return "molt_amd 0.3.0 gfx950"; }
 
 int molt_amd_set_tuning(int32_t key, int64_t value) {
   if (!molt::tuning_ok(key, value))
