@@ -168,9 +168,10 @@ int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t ldz, int32_
 /* Y[M, N] = bf16( X . deq(W)^T + T . bf16(s * B)^T ), fp32 accumulation, with
  * X bf16 [M, K], T bf16 [M, r] = molt_lora_project(X, lora_a) and B fp32 [N, r]
  * (row stride r). `w->scales` must be resolved fp32 scales. r = 0 skips LoRA.
- * Workspace (256-byte aligned, molt_nf4_lora_forward_workspace(M, N, K) bytes):
+ * Workspace (256-byte aligned, molt_nf4_lora_forward_workspace(M, N, K, r) bytes):
  * for many token rows the bf16 weight, written once by the dequant and read by
- * the GEMM (MOLT_TUNE_STAGE_MIN_MTILES); and, when the output has too few
+ * the GEMM (MOLT_TUNE_STAGE_MIN_MTILES), and for r % 64 == 0 the bf16(s B)
+ * rows its LoRA steps then stream the same way; and, when the output has too few
  * 256 x 256 tiles to fill the GPU and K is long, the fp32 partials of a
  * contraction split over workgroups, summed in split order (deterministic).
  * The results do not depend on the workspace; a NULL or smaller workspace runs
@@ -178,7 +179,7 @@ int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t ldz, int32_
  * workspaces.
  * Replaces bnb.matmul_4bit + the LoRA epilogue at methods/nf4_lora.py:43-50 and
  * methods/gated_replay.py:211-224. */
-size_t molt_nf4_lora_forward_workspace(int64_t M, int64_t N, int64_t K);
+size_t molt_nf4_lora_forward_workspace(int64_t M, int64_t N, int64_t K, int32_t r);
 int molt_nf4_lora_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,
                           const uint16_t* t, int64_t ldt, const float* lora_b, int32_t r,
                           float scaling, uint16_t* y, int64_t ldy, void* workspace,
@@ -191,11 +192,11 @@ int molt_nf4_lora_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_
  * with T bf16 [M, 2r] = [X . Ag^T | X . Au^T]. A workgroup owns gate and up of
  * the same intermediate columns, so h is formed in registers from the two
  * accumulators. Outputs are bf16 [M, I] with row stride ldo. Workspace: the
- * two staged bf16 weights, molt_nf4_gateup_forward_workspace(M, I, K) bytes
+ * two staged bf16 weights, molt_nf4_gateup_forward_workspace(M, I, K, r) bytes
  * (see molt_nf4_lora_forward; NULL runs unstaged).
  * Replaces the gate_proj/up_proj calls and `F.silu(gate) * up` of
  * methods/gated_replay.py:78-94,290-291 (and benchmarks/qualified_path_measure.py:404-432). */
-size_t molt_nf4_gateup_forward_workspace(int64_t M, int64_t N, int64_t K);
+size_t molt_nf4_gateup_forward_workspace(int64_t M, int64_t N, int64_t K, int32_t r);
 int molt_nf4_gateup_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* wg,
                             const molt_nf4_weight* wu, const uint16_t* t, int64_t ldt,
                             const float* bg, const float* bu, int32_t r, float sg, float su,
@@ -220,7 +221,7 @@ int molt_nf4_lora_backward_input(const uint16_t* dy, int64_t lddy, int64_t M,
 /* dX = dY0 . deq(W0) + dY1 . deq(W1) + U0 . bf16(A0) + U1 . bf16(A1): the input
  * gradient of the gate and up projections of a gated MLP in one contraction
  * (methods/gated_replay.py:167-186). Workspace: molt_nf4_lora_backward_workspace(M,
- * N, K, 2) bytes for the split contraction (see molt_nf4_lora_forward). */
+ * N, K, 2) bytes (see molt_nf4_lora_backward_input). */
 int molt_nf4_lora_backward_input_pair(const uint16_t* dy0, const uint16_t* dy1, int64_t lddy,
                                       int64_t M, const molt_nf4_weight* w0,
                                       const molt_nf4_weight* w1, const uint16_t* u0,

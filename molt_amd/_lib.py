@@ -57,9 +57,9 @@ SIGNATURES: dict[str, tuple] = {
     "molt_lora_project": (C.c_int, [_p, _p, _i64, _i32, _f32, _i64, _i64, _p, _i32, _i32, _p, _i64, _p, _sz,
                                     _p]),
     "molt_amd_time_next_gemm": (C.c_int, [_p, _p]),
-    "molt_nf4_lora_forward_workspace": (_sz, [_i64, _i64, _i64]),
+    "molt_nf4_lora_forward_workspace": (_sz, [_i64, _i64, _i64, _i32]),
     "molt_nf4_lora_forward": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _f32, _p, _i64, _p, _sz, _p]),
-    "molt_nf4_gateup_forward_workspace": (_sz, [_i64, _i64, _i64]),
+    "molt_nf4_gateup_forward_workspace": (_sz, [_i64, _i64, _i64, _i32]),
     "molt_nf4_gateup_forward": (C.c_int, [_p, _i64, _i64, _W, _W, _p, _i64, _p, _p, _i32, _f32, _f32,
                                           _p, _p, _p, _i64, _p, _sz, _p]),
     "molt_nf4_lora_backward_workspace": (_sz, [_i64, _i64, _i64, _i32]),

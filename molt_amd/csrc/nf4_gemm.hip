@@ -57,6 +57,9 @@ struct FwdParams {
   // staged weights (large-tile kernels): bf16 deq(W) [N, K] of each weight,
   // row stride ldw, read by DMA instead of dequantising packed bytes
   const uint16_t* wst[2]; int64_t ldw;
+  // LoRA steps through the staged kernel's DMA ring (lr % 64 == 0): bf16(s B)
+  // rows of each weight [N, lr], the pair's block-diagonal layout
+  const uint16_t* lbst[2]; int lora_ring;
 };
 
 struct BwdParams {
@@ -738,6 +741,36 @@ MOLT_DEV int loff(int R, int c) { return R * 64 + ((c ^ lswz(R)) << 3); }
 constexpr int kStageDma = BUF * 2 / (NT * 16);
 static_assert(kStageDma == 4, "x_load and the staged W DMA issue 4 instructions per buffer");
 
+// Value selects for the staged kernels' per-step sources. A conditional
+// expression over two lvalues (captured variables, array elements) selects an
+// address and loads through it, from scratch memory, which also makes the
+// result look divergent; by-value parameters keep it a register select.
+template <typename T>
+MOLT_DEV T pick(bool c, T a, T b) { return c ? a : b; }
+
+// Steps 0 .. n - 1 of a staged kernel: step j reads X buffer j % 3 and W
+// buffer j % 2 and loads X(j + 2), W(j + 1) into the buffers read at step
+// j - 1. The pattern repeats every 6 steps; every call names its buffers
+// statically (the compiler then tells the LDS reads of one buffer from the
+// DMA into another and inserts no waits between them).
+template <typename Step>
+MOLT_DEV void ring_steps(int n, Step& step, uint16_t* x0, uint16_t* x1, uint16_t* x2, uint16_t* w0, uint16_t* w1) {
+  int j = 0;
+  for (; j + 6 <= n; j += 6) {
+    step(j, x0, w0, x2, w1);
+    step(j + 1, x1, w1, x0, w0);
+    step(j + 2, x2, w0, x1, w1);
+    step(j + 3, x0, w1, x2, w0);
+    step(j + 4, x1, w0, x0, w1);
+    step(j + 5, x2, w1, x1, w0);
+  }
+  if (j < n) step(j, x0, w0, x2, w1);
+  if (j + 1 < n) step(j + 1, x1, w1, x0, w0);
+  if (j + 2 < n) step(j + 2, x2, w0, x1, w1);
+  if (j + 3 < n) step(j + 3, x0, w1, x2, w0);
+  if (j + 4 < n) step(j + 4, x1, w0, x0, w1);
+}
+
 MOLT_DEV void dma_slot(int blk, int lane, int& R, int& k) {
   R = 8 * blk + (lane >> 3);
   k = 8 * ((lane & 7) ^ lswz(R));
@@ -1149,10 +1182,14 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
   if constexpr (STAGED) {
     // W tile row R by DMA from row n of its weight's bf16 copy; a DMA block is
     // 8 rows of one weight (gate and up alternate every 64 rows), so the
-    // buffer resource is uniform per instruction.
-    const __amdgpu_buffer_rsrc_t ws0 = make_rsrc(p.wst[0], p.N * p.ldw * 2);
-    const __amdgpu_buffer_rsrc_t ws1 = make_rsrc(p.wst[PAIR ? 1 : 0], p.N * p.ldw * 2);
-    uint32_t wdoff[4];
+    // buffer resource is uniform per instruction. With p.lora_ring the LoRA
+    // contraction follows as extra steps of the same ring: X from T (rank
+    // columns), W from the weight's staged bf16(s B) rows [N, lr].
+    const bool ring = p.lora_ring && (!p.part || blockIdx.y + 1 == gridDim.y);
+    const int64_t lrs = ring ? p.lr : 0;
+    const int64_t xbytes = ((p.M - 1) * p.ldx + p.K) * 2, tbytes = ring ? ((p.M - 1) * p.ldt + p.lr) * 2 : 0;
+    const int64_t wbytes = p.N * p.ldw * 2, bbytes = p.N * lrs * 2;
+    uint32_t wdoff[4], toff[4], bdoff[4];
     int wsel[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -1162,25 +1199,49 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
       fwd_row(R, tn, PAIR, which, nr);
       wsel[c] = __builtin_amdgcn_readfirstlane(which);
       wdoff[c] = (uint32_t)((min(nr, p.N - 1) * p.ldw + k) * 2);
+      bdoff[c] = (uint32_t)((min(nr, p.N - 1) * lrs + k) * 2);
+      toff[c] = (uint32_t)((min(m0 + R, p.M - 1) * p.ldt + k) * 2);
     }
-    auto w_dma = [&](uint16_t* dst, int64_t k0) {
+    // step j of this workgroup: the contraction step sbeg + j, then the LoRA
+    // steps; indices past the end repeat the last step (loads never read).
+    const int n_main = send - sbeg, n_all = n_main + (int)(lrs / BK);
+    // (buffer resources built from selected base pointers: a select of two
+    // resources is lowered through memory)
+    auto x_src = [&](uint16_t* dst, int j) {
+      j = __builtin_amdgcn_readfirstlane(min(j, n_all - 1));
+      const bool lo = j >= n_main;
+      const __amdgpu_buffer_rsrc_t r = make_rsrc(pick<const void*>(lo, p.t, p.x), pick<int64_t>(lo, tbytes, xbytes));
+      const uint32_t so = __builtin_amdgcn_readfirstlane(
+          (uint32_t)((lo ? (int64_t)(j - n_main) * BK : (int64_t)(sbeg + j) * BK) * 2));
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        buf_load_lds16(wsel[c] ? ws1 : ws0, dst + (wave * 4 + c) * 512, wdoff[c], (uint32_t)(k0 * 2));
+      for (int c = 0; c < 4; ++c) buf_load_lds16(r, dst + (wave * 4 + c) * 512, pick(lo, toff[c], xoff[c]), so);
+    };
+    auto w_src = [&](uint16_t* dst, int j) {
+      j = __builtin_amdgcn_readfirstlane(min(j, n_all - 1));
+      const bool lo = j >= n_main;
+      const uint32_t so = __builtin_amdgcn_readfirstlane(
+          (uint32_t)((lo ? (int64_t)(j - n_main) * BK : (int64_t)(sbeg + j) * BK) * 2));
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int w = PAIR ? wsel[c] : 0;
+        const void* base = pick<const void*>(lo, sel(p.lbst, w), sel(p.wst, w));
+        buf_load_lds16(make_rsrc(base, pick<int64_t>(lo, bbytes, wbytes)), dst + (wave * 4 + c) * 512,
+                       pick(lo, bdoff[c], wdoff[c]), so);
+      }
     };
     // X in a ring of three buffers, loaded two steps ahead; W in two, one
     // step ahead (its tiles are shared by every row block, mostly from L2).
-    x_load(xb0, (int64_t)sbeg * BK);
-    w_dma(wb0, (int64_t)sbeg * BK);
-    x_load(xb1, min((int64_t)(sbeg + 1) * BK, klast));
-    wait_vm_at_most<kStageDma>();                    // X(sbeg), W(sbeg) landed; X(sbeg + 1) may fly
+    x_src(xb0, 0);
+    w_src(wb0, 0);
+    x_src(xb1, 1);
+    wait_vm_at_most<kStageDma>();                    // X(0), W(0) landed; X(1) may fly
     step_barrier();
-    auto step = [&](int s, const uint16_t* xc, const uint16_t* wc, uint16_t* x2, uint16_t* wnx) {
+    auto step = [&](int j, const uint16_t* xc, const uint16_t* wc, uint16_t* x2, uint16_t* wnx) {
       load_frags(wc, xc, fo, 0, a[0], b[0]);
       mfma_set(a[1], b[1], acc);
-      w_dma(wnx, min((int64_t)(s + 1) * BK, klast));
-      dma_then_loads();                              // keep W(s + 1) issued before X(s + 2)
-      x_load(x2, min((int64_t)(s + 2) * BK, klast));
+      w_src(wnx, j + 1);
+      dma_then_loads();                              // keep W(j + 1) issued before X(j + 2)
+      x_src(x2, j + 2);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int kk = 0; kk < 3; ++kk) {
@@ -1188,29 +1249,11 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
         mfma_set(a[kk & 1], b[kk & 1], acc);
         __builtin_amdgcn_sched_barrier(0);
       }
-      wait_vm_at_most<kStageDma>();                  // W(s + 1), X(s + 1) landed; X(s + 2) may fly
+      wait_vm_at_most<kStageDma>();                  // W(j + 1), X(j + 1) landed; X(j + 2) may fly
       step_barrier();
     };
-    // buffers of step s: X s % 3, W s % 2, so the pattern repeats every 6 steps
-    int s = sbeg;
-    for (; s + 6 <= send; s += 6) {
-      step(s, xb0, wb0, xb2, wb1);
-      step(s + 1, xb1, wb1, xb0, wb0);
-      step(s + 2, xb2, wb0, xb1, wb1);
-      step(s + 3, xb0, wb1, xb2, wb0);
-      step(s + 4, xb1, wb0, xb0, wb1);
-      step(s + 5, xb2, wb1, xb1, wb0);
-    }
-    if (s + 2 <= send) {
-      step(s, xb0, wb0, xb2, wb1);
-      step(s + 1, xb1, wb1, xb0, wb0);
-      s += 2;
-    }
-    if (s + 2 <= send) {
-      step(s, xb2, wb0, xb1, wb1);
-      step(s + 1, xb0, wb1, xb2, wb0);
-    }
-    wait_vm0();                                      // the last step's X(s + 2), never read
+    ring_steps(n_all, step, xb0, xb1, xb2, wb0, wb1);
+    wait_vm0();                                      // the last step's X(j + 2), never read
     __syncthreads();
   } else {
     WBytes r0, r1;
@@ -1259,7 +1302,7 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
   }
   mfma_set(a[1], b[1], acc);
   // the LoRA steps belong to the last split (uniform per workgroup)
-  const int64_t lr = !p.part || blockIdx.y + 1 == gridDim.y ? p.lr : 0;
+  const int64_t lr = (!p.part || blockIdx.y + 1 == gridDim.y) && !(STAGED && p.lora_ring) ? p.lr : 0;
   for (int64_t c0 = 0; c0 < lr; c0 += BK) {
     lora_a_stage(xb0, p.t, p.ldt, m0, p.M, c0, p.lr, tid);
     lora_wrow_stage(wb0, p, tn, PAIR, c0, tid);
@@ -1549,9 +1592,10 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
 
   const int kseg = (int)(p.Nw / BK);
   const int ks = p.nseg * kseg;
-  // step -> (segment, first contraction row), clamped to the last step
-  auto seg_of = [&](int s) { return min(s, ks - 1) / kseg; };
-  auto c0_of = [&](int s) { const int t = min(s, ks - 1); return (int64_t)(t - (t / kseg) * kseg) * BK; };
+  // step -> (segment, first contraction row), clamped to the last step; at
+  // most two segments, so a compare instead of a scalar division
+  auto seg_of = [&](int s) { return min(s, ks - 1) >= kseg ? 1 : 0; };
+  auto c0_of = [&](int s) { const int t = min(s, ks - 1); return (int64_t)(t - (t >= kseg ? kseg : 0)) * BK; };
   auto x_load = [&](uint16_t* dst, int s) {
     const __amdgpu_buffer_rsrc_t xr = seg_of(s) ? xr1 : xr0;
     const uint32_t so = (uint32_t)(c0_of(s) * 2);
@@ -1789,6 +1833,31 @@ __global__ __launch_bounds__(NT) void stage_wt_kernel(const StageTParams p) {
   }
 }
 
+// bf16 LoRA operand for the LoRA steps of the staged forward kernel's ring,
+// the values the fused kernel stages into LDS. W side: o_w[n][c] for
+// c < lr = bf16(s_w B_w[n][c - w r]) where 0 <= c - w r < r, else bf16(s_w 0)
+// (weight w = blockIdx.y: one weight has lr = r; the gate/up pair lr = 2r,
+// gate ranks first). One thread per 8 consecutive columns.
+__global__ void stage_lora_b_kernel(const float* b0, const float* b1, int64_t ldb, int r, float s0, float s1,
+                                    int64_t N, int lr, uint16_t* o0, uint16_t* o1) {
+  const int w = blockIdx.y;
+  const float* b = w ? b1 : b0;
+  const float s = w ? s1 : s0;
+  uint16_t* o = w ? o1 : o0;
+  const int chunks = lr / 8;
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= N * chunks) return;
+  const int64_t n = q / chunks;
+  const int c0 = (int)(q - n * chunks) * 8 - w * r;
+  float f[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = (c0 + i >= 0 && c0 + i < r) ? b[n * ldb + c0 + i] : 0.0f;
+  u32x4_t v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(s * f[2 * i], s * f[2 * i + 1]);
+  *reinterpret_cast<u32x4_t*>(o + n * lr + (q - n * chunks) * 8) = v;
+}
+
 }  // namespace big
 
 // y[m, n] = bf16(sum over splits s = 0, 1, .. of part[s][m][n]): the splits
@@ -1931,17 +2000,24 @@ struct KernelEvents {
 };
 
 // Workspace layout of the GEMM entry points: the staged weights (if any),
-// then the split-K partials (if any).
-struct GemmWorkspace { bool stage, split; size_t stage_bytes; };
+// their bf16 LoRA operands for the ring (if any: lora_rows x lora_cols per
+// weight, lora_cols a multiple of 64), then the split-K partials (if any). A
+// workspace too small for the LoRA copies stages the weights alone.
+struct GemmWorkspace { bool stage, ring, split; size_t stage_bytes, lora_bytes; };
 GemmWorkspace place_workspace(const GemmPlan& plan, bool want_stage, int weights, int64_t rows, int64_t cols,
-                              int64_t M, int64_t out_n, const void* ws, size_t ws_bytes) {
-  GemmWorkspace g{false, false, 0};
+                              int64_t lora_rows, int64_t lora_cols, int64_t M, int64_t out_n, const void* ws,
+                              size_t ws_bytes) {
+  GemmWorkspace g{false, false, false, 0, 0};
   const size_t sb = want_stage ? weights * stage_one(rows, cols) : 0;
+  const bool want_ring = want_stage && lora_cols > 0 && lora_cols % BK == 0;
+  const size_t lb = want_ring ? weights * stage_one(lora_rows, lora_cols) : 0;
   const size_t pb = split_bytes(plan.S, M, out_n);
   const bool usable = ws && aligned(ws, 256);
   g.stage = want_stage && usable && ws_bytes >= sb + pb;
+  g.ring = g.stage && want_ring && ws_bytes >= sb + lb + pb;
   g.stage_bytes = g.stage ? sb : 0;
-  g.split = plan.S > 1 && usable && ws_bytes >= g.stage_bytes + pb;
+  g.lora_bytes = g.ring ? lb : 0;
+  g.split = plan.S > 1 && usable && ws_bytes >= g.stage_bytes + g.lora_bytes + pb;
   return g;
 }
 
@@ -2001,15 +2077,29 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
                   aligned(w0->packed, 16) && (!pair || aligned(w1->packed, 16));
   const int64_t big_tiles = ceil_div64(M, big::BM) * ceil_div64(p.N, pair ? big::BN / 2 : big::BN);
   const GemmPlan plan = fwd_plan(M, p.N, p.K, pair, fwd_big_ok(M, ldx, p.N, p.K, al), al);
-  const GemmWorkspace gw = place_workspace(plan, stage_wanted(plan.kind, M, p.N, p.K), pair ? 2 : 1, p.N, p.K, M,
-                                           p.N, workspace, workspace_bytes);
+  // the LoRA ring reads T by DMA: 16-byte aligned rows
+  const bool t_dma = lr > 0 && t && aligned(t, 16) && ldt % 8 == 0;
+  const GemmWorkspace gw = place_workspace(plan, stage_wanted(plan.kind, M, p.N, p.K), pair ? 2 : 1, p.N, p.K, p.N,
+                                           t_dma ? lr : 0, M, p.N, workspace, workspace_bytes);
   char* wsb = static_cast<char*>(workspace);
   const bool split = gw.split;
   if (plan.kind == PLAN_BIG || (plan.kind == PLAN_BIG_SPLIT && split)) {
     MOLT_REQUIRE(big_tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
     if (plan.kind == PLAN_BIG_SPLIT) {
       p.split_steps = plan.split_steps;
-      p.part = reinterpret_cast<float*>(wsb + gw.stage_bytes);
+      p.part = reinterpret_cast<float*>(wsb + gw.stage_bytes + gw.lora_bytes);
+    }
+    if (gw.ring) {
+      const int nw = pair ? 2 : 1;
+      for (int i = 0; i < 2; ++i) p.lbst[i] = reinterpret_cast<uint16_t*>(wsb + gw.stage_bytes + (i < nw ? i : 0) *
+                                                                           stage_one(p.N, lr));
+      const int64_t q = p.N * (lr / 8);
+      hipLaunchKernelGGL(big::stage_lora_b_kernel, dim3((unsigned)ceil_div64(q, 256), (unsigned)nw), dim3(256), 0,
+                         stream, b0, pair ? b1 : b0, ldb, r, s0, s1, p.N, lr, const_cast<uint16_t*>(p.lbst[0]),
+                         const_cast<uint16_t*>(p.lbst[1]));
+      rc = check_launch(who);
+      if (rc) return rc;
+      p.lora_ring = 1;
     }
     if (gw.stage) {
       // the bf16 weight rows (resolved scales, so the flat-scale dequant)
@@ -2118,14 +2208,15 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
                       bwd_big_ok(M, lddy, p.Nw, p.Kw, nseg);
   const GemmPlan plan = bwd_plan(M, p.Nw, p.Kw, nseg, swiglu, big_ok, al);
   const bool want_stage = stage_wanted(plan.kind, M, p.Nw, p.Kw) && p.Kw % big::BN == 0;
-  const GemmWorkspace gw = place_workspace(plan, want_stage, nseg, p.Nw, p.Kw, M, p.Kw, workspace, workspace_bytes);
+  const GemmWorkspace gw = place_workspace(plan, want_stage, nseg, p.Nw, p.Kw, 0, 0, M, p.Kw, workspace,
+                                           workspace_bytes);
   char* wsb = static_cast<char*>(workspace);
   const bool split = gw.split;
   if (plan.kind == PLAN_BIG || (plan.kind == PLAN_BIG_SPLIT && split)) {
     MOLT_REQUIRE(big_tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
     if (plan.kind == PLAN_BIG_SPLIT) {
       p.split_steps = plan.split_steps;
-      p.part = reinterpret_cast<float*>(wsb + gw.stage_bytes);
+      p.part = reinterpret_cast<float*>(wsb + gw.stage_bytes + gw.lora_bytes);
     }
     if (gw.stage) {
       big::StageTParams sp{};
@@ -2189,21 +2280,32 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
 // split-K partials when the plan for 16-byte aligned operands splits (see
 // plan_splits), else 0. Calls whose operands do not qualify, or whose
 // workspace is smaller, run unsplit.
-extern "C" size_t molt_nf4_lora_forward_workspace(int64_t M, int64_t N, int64_t K) {
-  if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0) return 0;
-  const GemmPlan plan = fwd_plan(M, N, K, false, fwd_big_ok(M, K, N, K, true), true);
-  return (stage_wanted(plan.kind, M, N, K) ? stage_one(N, K) : 0) + split_bytes(plan.S, M, N);
+// Staged weights, their LoRA copies (rank a multiple of 64) and split partials.
+size_t gemm_workspace(const GemmPlan& plan, bool stage, int weights, int64_t rows, int64_t cols, int64_t lora_rows,
+                      int64_t lora_cols, int64_t M, int64_t out_n) {
+  size_t b = split_bytes(plan.S, M, out_n);
+  if (stage) {
+    b += weights * stage_one(rows, cols);
+    if (lora_cols > 0 && lora_cols % BK == 0) b += weights * stage_one(lora_rows, lora_cols);
+  }
+  return b;
 }
 
-extern "C" size_t molt_nf4_gateup_forward_workspace(int64_t M, int64_t N, int64_t K) {
-  if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0) return 0;
+extern "C" size_t molt_nf4_lora_forward_workspace(int64_t M, int64_t N, int64_t K, int32_t r) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0 || r < 0) return 0;
+  const GemmPlan plan = fwd_plan(M, N, K, false, fwd_big_ok(M, K, N, K, true), true);
+  return gemm_workspace(plan, stage_wanted(plan.kind, M, N, K), 1, N, K, N, r, M, N);
+}
+
+extern "C" size_t molt_nf4_gateup_forward_workspace(int64_t M, int64_t N, int64_t K, int32_t r) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0 || r < 0) return 0;
   const GemmPlan plan = fwd_plan(M, N, K, true, fwd_big_ok(M, K, N, K, true), true);
-  return stage_wanted(plan.kind, M, N, K) ? 2 * stage_one(N, K) : 0;
+  return gemm_workspace(plan, stage_wanted(plan.kind, M, N, K), 2, N, K, N, 2 * (int64_t)r, M, N);
 }
 
 extern "C" size_t molt_nf4_lora_backward_workspace(int64_t M, int64_t Nw, int64_t Kw, int32_t nseg) {
   if (M <= 0 || Nw <= 0 || Kw <= 0 || Nw % 64 != 0 || Kw % 64 != 0 || nseg < 1 || nseg > 2) return 0;
   const GemmPlan plan = bwd_plan(M, Nw, Kw, nseg, false, bwd_big_ok(M, Nw, Nw, Kw, nseg), true);
   const bool stage = stage_wanted(plan.kind, M, Nw, Kw) && Kw % big::BN == 0;
-  return (stage ? nseg * stage_one(Nw, Kw) : 0) + split_bytes(plan.S, M, Kw);
+  return gemm_workspace(plan, stage, nseg, Nw, Kw, 0, 0, M, Kw);
 }

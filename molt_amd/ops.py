@@ -434,7 +434,7 @@ def nf4_lora_forward(x: Tensor, packed: Tensor, scales: Tensor, code: Tensor, ro
         r = tt.shape[1]
         if bb.shape != (rows, r):
             raise ValueError(f"{what}: LoRA B shape {tuple(bb.shape)} != ({rows}, {r})")
-    ws_bytes = _workspace("molt_nf4_lora_forward_workspace", x.shape[0], rows, cols)
+    ws_bytes = _workspace("molt_nf4_lora_forward_workspace", x.shape[0], rows, cols, r)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     _call("molt_nf4_lora_forward", x.data_ptr(), cols, x.shape[0], C.byref(w), _ptr(tt), max(r, 1),
           _ptr(bb), r, float(scaling), y.data_ptr(), rows, _ptr(ws), ws_bytes, _stream(dev))
@@ -478,7 +478,7 @@ def nf4_gateup_forward(x: Tensor, packed_g: Tensor, scales_g: Tensor, packed_u: 
         bg, bu = _f32(lora_bg), _f32(lora_bu)
         if bg.shape != (rows, r) or bu.shape != (rows, r):
             raise ValueError(f"{what}: LoRA B shapes {tuple(bg.shape)}, {tuple(bu.shape)} != ({rows}, {r})")
-    ws_bytes = _workspace("molt_nf4_gateup_forward_workspace", m, rows, cols)
+    ws_bytes = _workspace("molt_nf4_gateup_forward_workspace", m, rows, cols, r)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     _call("molt_nf4_gateup_forward", x.data_ptr(), cols, m, C.byref(wg), C.byref(wu), _ptr(tt),
           max(2 * r, 1), _ptr(bg), _ptr(bu), r, float(sg), float(su), outs[0].data_ptr(),

@@ -227,13 +227,13 @@ def test_split_k_workspace_queries_need_no_gpu():
 
     lib = _lib.load()
     with tuning(stage_min_mtiles=0):
-        assert lib.molt_nf4_lora_forward_workspace(8192, 14336, 4096) == 0
-        assert lib.molt_nf4_lora_forward_workspace(4096, 1536, 8960) == 2 * 4096 * 1536 * 4
+        assert lib.molt_nf4_lora_forward_workspace(8192, 14336, 4096, 0) == 0
+        assert lib.molt_nf4_lora_forward_workspace(4096, 1536, 8960, 0) == 2 * 4096 * 1536 * 4
         assert lib.molt_nf4_lora_backward_workspace(4096, 8960, 1536, 2) == 2 * 4096 * 1536 * 4
         assert lib.molt_nf4_lora_backward_workspace(8192, 14336, 4096, 2) == 0
-        assert lib.molt_nf4_lora_forward_workspace(4096, 1000, 8960) == 0       # N not a multiple of 256
+        assert lib.molt_nf4_lora_forward_workspace(4096, 1000, 8960, 0) == 0       # N not a multiple of 256
         with tuning(split_k=0):
-            assert lib.molt_nf4_lora_forward_workspace(4096, 1536, 8960) == 0
+            assert lib.molt_nf4_lora_forward_workspace(4096, 1536, 8960, 0) == 0
 
 
 def _stage(rows, cols):
@@ -248,16 +248,23 @@ def test_staged_weight_workspace_queries_need_no_gpu():
 
     lib = _lib.load()
     assert lib.molt_amd_get_tuning(_lib.TUNING_KEYS["stage_min_mtiles"]) == 16
-    assert lib.molt_nf4_lora_forward_workspace(8192, 14336, 4096) == _stage(14336, 4096)
-    assert lib.molt_nf4_gateup_forward_workspace(8192, 14336, 4096) == 2 * _stage(14336, 4096)
+    assert lib.molt_nf4_lora_forward_workspace(8192, 14336, 4096, 0) == _stage(14336, 4096)
+    assert lib.molt_nf4_gateup_forward_workspace(8192, 14336, 4096, 0) == 2 * _stage(14336, 4096)
     assert lib.molt_nf4_lora_backward_workspace(8192, 14336, 4096, 2) == 2 * _stage(14336, 4096)
     assert lib.molt_nf4_lora_backward_workspace(8192, 4096, 14336, 1) == _stage(4096, 14336)
-    assert lib.molt_nf4_lora_forward_workspace(4096, 1536, 8960) == _stage(1536, 8960) + 2 * 4096 * 1536 * 4
+    assert lib.molt_nf4_lora_forward_workspace(4096, 1536, 8960, 0) == _stage(1536, 8960) + 2 * 4096 * 1536 * 4
     assert lib.molt_nf4_lora_backward_workspace(4096, 8960, 1536, 2) == 2 * _stage(8960, 1536) + 2 * 4096 * 1536 * 4
-    assert lib.molt_nf4_lora_forward_workspace(2048, 14336, 4096) == 0          # 8 row blocks
-    assert lib.molt_nf4_gateup_forward_workspace(256, 14336, 4096) == 0
+    assert lib.molt_nf4_lora_forward_workspace(2048, 14336, 4096, 0) == 0          # 8 row blocks
+    assert lib.molt_nf4_gateup_forward_workspace(256, 14336, 4096, 0) == 0
     assert lib.molt_nf4_lora_backward_workspace(8192, 1024, 4160, 1) == 0       # Kw not a multiple of 256
     with tuning(stage_min_mtiles=0):
-        assert lib.molt_nf4_gateup_forward_workspace(8192, 14336, 4096) == 0
+        assert lib.molt_nf4_gateup_forward_workspace(8192, 14336, 4096, 0) == 0
     with tuning(stage_min_mtiles=8):
-        assert lib.molt_nf4_lora_forward_workspace(2048, 14336, 4096) == _stage(14336, 4096)
+        assert lib.molt_nf4_lora_forward_workspace(2048, 14336, 4096, 0) == _stage(14336, 4096)
+    # in the forward, a rank that is a multiple of 64 adds the bf16(s B) rows the ring streams
+    assert lib.molt_nf4_lora_forward_workspace(8192, 4096, 14336, 64) == _stage(4096, 14336) + _stage(4096, 64)
+    assert lib.molt_nf4_gateup_forward_workspace(8192, 14336, 4096, 64) == 2 * (_stage(14336, 4096)
+                                                                                 + _stage(14336, 128))
+    assert lib.molt_nf4_gateup_forward_workspace(8192, 14336, 4096, 16) == 2 * _stage(14336, 4096)   # 2r = 32
+    assert lib.molt_nf4_lora_forward_workspace(4096, 1536, 8960, 64) == (_stage(1536, 8960) + _stage(1536, 64)
+                                                                         + 2 * 4096 * 1536 * 4)

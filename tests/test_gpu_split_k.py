@@ -37,7 +37,7 @@ def _rel(a, b):
 def test_split_forward(m, n, k, r):
     print(f"split-K forward m={m} n={n} k={k} r={r}", flush=True)
     lib = _lib.load()
-    assert lib.molt_nf4_lora_forward_workspace(m, n, k) > 0, "the shape must take the split path"
+    assert lib.molt_nf4_lora_forward_workspace(m, n, k, r) > 0, "the shape must take the split path"
     packed, qs, scales = _weight(n, k, 11)
     x = seeded((m, k), 12)
     a = uniform((max(r, 1), k), 13, 1 / np.sqrt(k))

@@ -5,7 +5,9 @@ dequantising every weight tile again in each 256-row block. The tile values, the
 contraction order and so every output must equal the fused kernels' bit for bit:
 each case runs staged (stage_min_mtiles=1) and fused (0) and compares, with
 ragged row/column tails, LoRA terms, the gate/up pair, the paired and SwiGLU
-backward, and split-K (the partials then sit after the staged copy)."""
+backward, and split-K (the partials then sit after the staged copy). In the
+forward, ranks that are a multiple of 64 (of 32 for the gate/up pair) also
+stage bf16(s B) and stream the LoRA steps through the same ring."""
 from __future__ import annotations
 
 import numpy as np
@@ -44,12 +46,13 @@ def _equal(staged, fused):
 
 
 @pytest.mark.parametrize("m,n,k,r,btm", [(300, 320, 256, 16, 1), (4173, 512, 1024, 16, 1),
-                                         (4096, 1536, 8960, 16, 256)])
+                                         (4096, 1536, 8960, 16, 256), (300, 320, 256, 64, 1),
+                                         (4173, 512, 1024, 128, 1), (4096, 1536, 8960, 64, 256)])
 def test_forward_staged(m, n, k, r, btm):
     print(f"staged forward m={m} n={n} k={k} r={r} big_tile_min={btm}", flush=True)
     lib = _lib.load()
     with tuning(big_tile_min=btm, stage_min_mtiles=1):
-        assert lib.molt_nf4_lora_forward_workspace(m, n, k) >= n * k * 2, "the call must stage the weight"
+        assert lib.molt_nf4_lora_forward_workspace(m, n, k, r) >= n * k * 2, "the call must stage the weight"
     packed, qs, scales = _weight(n, k, 31)
     x = seeded((m, k), 32)
     a = uniform((r, k), 33, 1 / np.sqrt(k))
@@ -64,11 +67,12 @@ def test_forward_staged(m, n, k, r, btm):
     assert_close_fro(np_f32(staged)[rows], ref, what="staged Y rows")
 
 
-@pytest.mark.parametrize("m,i,h,r", [(300, 192, 256, 16), (4100, 512, 512, 8)])
+@pytest.mark.parametrize("m,i,h,r", [(300, 192, 256, 16), (4100, 512, 512, 8), (300, 192, 256, 32),
+                                     (4100, 512, 512, 64)])
 def test_gateup_staged(m, i, h, r):
     print(f"staged gate/up m={m} I={i} H={h} r={r}", flush=True)
     with tuning(big_tile_min=1, stage_min_mtiles=1):
-        assert _lib.load().molt_nf4_gateup_forward_workspace(m, i, h) >= 2 * i * h * 2
+        assert _lib.load().molt_nf4_gateup_forward_workspace(m, i, h, r) >= 2 * i * h * 2
     pg, qg, sg = _weight(i, h, 35)
     pu, qu, su = _weight(i, h, 36)
     x = seeded((m, h), 37)
@@ -80,7 +84,8 @@ def test_gateup_staged(m, i, h, r):
     _equal(staged, fused)
 
 
-@pytest.mark.parametrize("m,n,k,r", [(300, 256, 512, 16), (4173, 1024, 768, 0)])
+@pytest.mark.parametrize("m,n,k,r", [(300, 256, 512, 16), (4173, 1024, 768, 0), (300, 256, 512, 64),
+                                     (4173, 1024, 768, 128)])
 def test_backward_staged(m, n, k, r):
     print(f"staged backward m={m} n={n} k={k} r={r}", flush=True)
     with tuning(big_tile_min=1, stage_min_mtiles=1):
@@ -100,7 +105,8 @@ def test_backward_staged(m, n, k, r):
     assert_close_fro(np_f32(staged)[rows], ref, what="staged dX rows")
 
 
-@pytest.mark.parametrize("m,i,h,r,btm", [(300, 256, 512, 16, 1), (4096, 8960, 1536, 16, 256)])
+@pytest.mark.parametrize("m,i,h,r,btm", [(300, 256, 512, 16, 1), (4096, 8960, 1536, 16, 256),
+                                         (300, 256, 512, 64, 1), (4096, 8960, 1536, 64, 256)])
 def test_paired_backward_staged(m, i, h, r, btm):
     print(f"staged paired backward m={m} I={i} H={h} r={r} big_tile_min={btm}", flush=True)
     with tuning(big_tile_min=btm, stage_min_mtiles=1):
@@ -115,8 +121,9 @@ def test_paired_backward_staged(m, i, h, r, btm):
     _equal(staged, fused)
 
 
-def test_swiglu_backward_staged():
-    m, h, i, r = 300, 256, 512, 16
+@pytest.mark.parametrize("r", [16, 64])
+def test_swiglu_backward_staged(r):
+    m, h, i = 300, 256, 512
     print(f"staged SwiGLU backward m={m} H={h} I={i} r={r}", flush=True)
     pd, qd, sd = _weight(h, i, 54)
     dy = seeded((m, h), 55)
@@ -139,11 +146,39 @@ def test_staging_needs_the_workspace():
     for ws_bytes in (0, None):
         y = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
         with tuning(big_tile_min=1, stage_min_mtiles=1):
-            nbytes = lib.molt_nf4_lora_forward_workspace(m, n, k) if ws_bytes is None else 0
+            nbytes = lib.molt_nf4_lora_forward_workspace(m, n, k, 0) if ws_bytes is None else 0
             ws = torch.empty(nbytes, device=x.device, dtype=torch.uint8) if nbytes else None
             _lib.check(lib.molt_nf4_lora_forward(x.data_ptr(), k, m, ops.C.byref(w), None, 1, None, 0, 1.0,
                                                  y.data_ptr(), n, None if ws is None else ws.data_ptr(), nbytes,
                                                  ops._stream(x.device)))
         outs.append(y)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+
+
+def test_lora_ring_needs_its_workspace():
+    """A workspace sized without the rank (room for the staged weight only)
+    stages the weight and runs the LoRA steps outside the ring: same result."""
+    m, n, k, r = 300, 256, 512, 64
+    print(f"staged forward, LoRA ring with and without its workspace m={m} n={n} k={k} r={r}", flush=True)
+    packed, qs, scales = _weight(n, k, 62)
+    x = seeded((m, k), 63)
+    a = uniform((r, k), 64, 1 / np.sqrt(k))
+    b = seeded((n, r), 65, std=0.01, dtype=torch.float32)
+    t = ops.lora_project(x, None, 0, 1.0, a, 0)
+    w = ops._weight(packed, scales, qs.code.float(), n, k, 64, 1)
+    bb = b.contiguous()
+    lib = _lib.load()
+    outs = []
+    with tuning(big_tile_min=1, stage_min_mtiles=1):
+        for rank in (0, r):
+            nbytes = lib.molt_nf4_lora_forward_workspace(m, n, k, rank)
+            ws = torch.empty(nbytes, device=x.device, dtype=torch.uint8)
+            y = torch.empty((m, n), device=x.device, dtype=torch.bfloat16)
+            _lib.check(lib.molt_nf4_lora_forward(x.data_ptr(), k, m, ops.C.byref(w), t.data_ptr(), r, bb.data_ptr(),
+                                                 r, 2.0, y.data_ptr(), n, ws.data_ptr(), nbytes,
+                                                 ops._stream(x.device)))
+            outs.append(y)
+        assert lib.molt_nf4_lora_forward_workspace(m, n, k, r) > lib.molt_nf4_lora_forward_workspace(m, n, k, 0)
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1])
