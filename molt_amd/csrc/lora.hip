@@ -245,13 +245,14 @@ MOLT_DEV void pj_dma16(__amdgpu_buffer_rsrc_t r, uint16_t* dst, uint32_t off, ui
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (pj_lds_t)dst, 16, off, soff, 0, 0);
 }
 
-// Wait until at most n vector-memory ops are outstanding (n = 4 or 8), with
-// compiler barriers so no LDS read moves above the wait.
-MOLT_DEV void pj_wait_vm(int n) {
+// Wait until at most N vector-memory ops are outstanding (vmcnt N, other
+// counters untouched), with compiler barriers so no LDS read moves above the
+// wait. gfx9 splits vmcnt over bits 3:0 and 15:14.
+template <int N>
+MOLT_DEV void pj_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
   asm volatile("" ::: "memory");
-  if (n == 8) __builtin_amdgcn_s_waitcnt(0x0F78);
-  else if (n == 4) __builtin_amdgcn_s_waitcnt(0x0F74);
-  else __builtin_amdgcn_s_waitcnt(0x0F70);
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
   asm volatile("" ::: "memory");
 }
 
@@ -296,16 +297,19 @@ __global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_dma_kernel(const P
 #pragma unroll
       for (int c = 0; c < 4 * MT; ++c) pj_dma16(zr, dst + c * 512, zoff[c], (uint32_t)(s * BK * 2));
     };
-    u32x4_t w[TQ][4];
+    // z by DMA and the adapter fragments by register loads, both one step
+    // ahead (two register sets, alternating), so a step waits for nothing it
+    // issued itself
+    u32x4_t w0[TQ][4], w1[TQ][4];
     int64_t s = s_begin + wave;
     int b = 0;
     dma(s, zs[wave][0]);
-    for (;;) {
-      proj_load_w<TQ>(w, p, s, lane);
+    proj_load_w<TQ>(w0, p, s, lane);
+    auto step = [&](const u32x4_t (&wc)[TQ][4], u32x4_t (&wn)[TQ][4]) {
       const int64_t sn = s + PJ_WAVES < s_end ? s + PJ_WAVES : s_end - 1;
       dma(sn, zs[wave][b ^ 1]);
-      // this step's DMA (issued before the adapter loads) has landed; the next one may fly
-      pj_wait_vm(4 * MT);
+      proj_load_w<TQ>(wn, p, sn, lane);
+      pj_wait_vm<4 * MT + 4 * TQ>();                // this step's z and adapter landed; the next step's may fly
       const uint16_t* zc = zs[wave][b];
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
@@ -320,14 +324,16 @@ __global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_dma_kernel(const P
           const bf16x8_t zb = __builtin_bit_cast(bf16x8_t, zv);
 #pragma unroll
           for (int t = 0; t < TQ; ++t)
-            acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, w[t][kk]), zb,
+            acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, wc[t][kk]), zb,
                                                                 acc[i][t], 0, 0, 0);
         }
       s += PJ_WAVES;
-      if (s >= s_end) break;
       b ^= 1;
+      return s < s_end;
+    };
+    while (step(w0, w1) && step(w1, w0)) {
     }
-    pj_wait_vm(0);   // the last (repeated) DMA before the kernel ends
+    pj_wait_vm<0>();   // the last (repeated) loads before the kernel ends
   }
 
 #pragma unroll
