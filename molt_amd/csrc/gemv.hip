@@ -306,10 +306,20 @@ constexpr int GD_WAVES = 8;
 constexpr int GD_NT = 64 * GD_WAVES;
 constexpr int GD_XPAD = 8;                // bf16 elements of X row padding
 
+// Code-pair table of the dot kernel: entry (byte b, copy c) at b * TS + c.
+// With TS = 64 (256 bytes per entry, copies in the first 128) a lane's
+// lookup address is one v_perm_b32 of the packed dword: the byte lands in
+// bits 8-15 beside the lane's copy offset (lane % 32) * 4 in bits 0-7, where
+// the 32-dword stride takes a bit-field extract and a shift-add per byte.
+// It doubles the table's footprint (64 KB), so it is used where the LDS
+// allows (see gd_perm).
+template <int TS>
 struct GdSmem {
-  uint32_t tab[256 * GV_TABW];
+  uint32_t tab[256 * TS];
   float code2s[256];
 };
+template <int IPR, int MX>
+constexpr bool gd_perm() { return IPR == 2 ? MX == 1 : MX <= 2; }
 
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 
@@ -364,10 +374,11 @@ MOLT_DEV void gd_load(GdRound<RW, IPR>& R, const GemvParams& p, int64_t n0, int 
 // of token m, see gd_store). X row m sits at
 // xs + m * xstride (elements); with XREG (one token) the lane's X chunks are
 // xg[4 i + h] in registers instead.
-template <int RW, int IPR, int MX, bool XREG>
+template <int RW, int IPR, int MX, bool XREG, bool PERM = false>
 MOLT_DEV float gd_compute(const GdRound<RW, IPR>& R, const GemvParams& p, const uint32_t* tab, const uint16_t* xs,
                          int xstride, const u32x4_t* xg, const float* code2s, const float (&lt)[MX][2], int64_t n0,
                          int lane) {
+  const uint32_t lb = (uint32_t)(lane & 31) * 4;     // PERM: byte offset of the lane's copy
   float acc[RW][MX];
 #pragma unroll
   for (int r = 0; r < RW; ++r)
@@ -390,7 +401,14 @@ MOLT_DEV float gd_compute(const GdRound<RW, IPR>& R, const GemvParams& p, const 
       for (int b = 0; b < 4; ++b) {
 #pragma unroll
         for (int r = 0; r < RW; ++r) {
-          const uint32_t pair = tab[((R.w[r * IPR + i][h] >> (8 * b)) & 0xffu) * GV_TABW];
+          uint32_t pair;
+          if constexpr (PERM) {
+            // bits 15:8 = byte b of the dword, bits 7:0 = lb: selectors 4 + b (S0), 0 (S1), 12 (zero)
+            const uint32_t off = __builtin_amdgcn_perm(R.w[r * IPR + i][h], lb, 0x0C0C0400u | ((uint32_t)b << 8));
+            pair = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(tab) + off);
+          } else {
+            pair = tab[((R.w[r * IPR + i][h] >> (8 * b)) & 0xffu) * GV_TABW];
+          }
 #pragma unroll
           for (int m = 0; m < MX; ++m) {
             // copy the element out first: __builtin_bit_cast of a vector-element
@@ -456,7 +474,9 @@ MOLT_DEV void gd_store(const GemvParams& p, float v, int64_t n0, int lane) {
 template <int RW, int IPR, int MX, bool NESTED, bool LORA, int MAXR>
 __global__ __launch_bounds__(GD_NT) __attribute__((amdgpu_waves_per_eu(IPR == 2 && MX <= 2 ? 4 : 1)))
 void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
-  __shared__ GdSmem sm;
+  constexpr bool PERM = gd_perm<IPR, MX>();
+  constexpr int TS = PERM ? 64 : GV_TABW;
+  __shared__ GdSmem<TS> sm;
   extern __shared__ __attribute__((aligned(16))) uint16_t gd_xs[];      // X, MX rows of K + GD_XPAD elements
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -545,18 +565,18 @@ void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
 #pragma unroll
       for (int i = 1; i < 16; ++i) chi = hi == i ? cv[i] : chi;
       const float first = p.order ? chi : clo, second = p.order ? clo : chi;
-      sm.tab[(hi * 16 + lo) * GV_TABW + copy] = pack_bf16x2(first, second);
+      sm.tab[(hi * 16 + lo) * TS + copy] = pack_bf16x2(first, second);
     }
     sm.code2s[tid & 255] = c2;                       // every thread: no branch around the load
   }
   __syncthreads();
 
-  const uint32_t* tab = sm.tab + (lane & 31);
+  const uint32_t* tab = PERM ? sm.tab : sm.tab + (lane & 31);
   if constexpr (MAXR > 0) {
     float out[MAXR];
 #pragma unroll
     for (int j = 0; j < MAXR; ++j)
-      out[j] = gd_compute<RW, IPR, MX, XREG>(b[j], p, tab, gd_xs, xstride, xg, sm.code2s, lt, nb + j * stride, lane);
+      out[j] = gd_compute<RW, IPR, MX, XREG, PERM>(b[j], p, tab, gd_xs, xstride, xg, sm.code2s, lt, nb + j * stride, lane);
 #pragma unroll
     for (int j = 0; j < MAXR; ++j)
       if (j < rounds) gd_store<RW, MX>(p, out[j], nb + j * stride, lane);
@@ -565,15 +585,15 @@ void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
     // computed: unconditional loads keep the waits exact (see gd_load).
     for (int j = 0; j < rounds; j += 3) {
       gd_load<RW, IPR, NESTED, LORA>(b[2], p, nb + (j + 2) * stride, lane, KB, nf);
-      gd_store<RW, MX>(p, gd_compute<RW, IPR, MX, XREG>(b[0], p, tab, gd_xs, xstride, xg, sm.code2s, lt,
+      gd_store<RW, MX>(p, gd_compute<RW, IPR, MX, XREG, PERM>(b[0], p, tab, gd_xs, xstride, xg, sm.code2s, lt,
                                                           nb + j * stride, lane), nb + j * stride, lane);
       if (j + 1 >= rounds) break;
       gd_load<RW, IPR, NESTED, LORA>(b[0], p, nb + (j + 3) * stride, lane, KB, nf);
-      gd_store<RW, MX>(p, gd_compute<RW, IPR, MX, XREG>(b[1], p, tab, gd_xs, xstride, xg, sm.code2s, lt,
+      gd_store<RW, MX>(p, gd_compute<RW, IPR, MX, XREG, PERM>(b[1], p, tab, gd_xs, xstride, xg, sm.code2s, lt,
                                                           nb + (j + 1) * stride, lane), nb + (j + 1) * stride, lane);
       if (j + 2 >= rounds) break;
       gd_load<RW, IPR, NESTED, LORA>(b[1], p, nb + (j + 4) * stride, lane, KB, nf);
-      gd_store<RW, MX>(p, gd_compute<RW, IPR, MX, XREG>(b[2], p, tab, gd_xs, xstride, xg, sm.code2s, lt,
+      gd_store<RW, MX>(p, gd_compute<RW, IPR, MX, XREG, PERM>(b[2], p, tab, gd_xs, xstride, xg, sm.code2s, lt,
                                                           nb + (j + 2) * stride, lane), nb + (j + 2) * stride, lane);
     }
   }
