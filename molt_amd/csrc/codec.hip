@@ -15,6 +15,7 @@ struct ScaleSrc {
   const float* scales;
   const uint8_t* q; const float* absmax2; const float* code2; float offset; int dq_block;
   int nested;
+  int dq_shift;    // log2(dq_block) when it is a power of two, else -1
 };
 
 // scale = fp32(fp32(code2[q] * absmax2[b / dq]) + offset), or the fp32 scale itself.
@@ -51,18 +52,26 @@ MOLT_DEV void dq_store(void* out, int64_t e0, const float (&v)[8]) {
   }
 }
 
+// BLK8 with a power-of-two block (blk_shift >= 0): the 8-element unit u lies
+// in block (8 u) >> blk_shift, the nested statistics' code table sits in LDS
+// and every statistics load of the pass is issued before the first is used
+// (no 64-bit division, no dependent global load per unit).
 template <int OUT_F32, bool BLK8>
 __global__ __launch_bounds__(CODEC_NT) void dequant_kernel(const uint8_t* __restrict__ packed,
                                                            ScaleSrc ss, const float* __restrict__ code,
-                                                           int order, int64_t n, int block,
+                                                           int order, int64_t n, int block, int blk_shift,
                                                            void* __restrict__ out) {
+  static_assert(CODEC_NT == 256, "one table entry per thread");
   __shared__ float2 tab[256];
+  __shared__ float c2s[256];
   {
     const int b = threadIdx.x;
     const int hi = b >> 4, lo = b & 15;
     tab[b] = make_float2(code[order ? hi : lo], code[order ? lo : hi]);
+    c2s[b] = ss.nested ? ss.code2[b] : 0.0f;
   }
   __syncthreads();
+  const bool fast = BLK8 && blk_shift >= 0 && (!ss.nested || ss.dq_shift >= 0);
   const int64_t whole = n / 8;                 // units with 8 elements
   const int64_t units = (n + 7) / 8;
   const int64_t step = (int64_t)gridDim.x * CODEC_NT * DQ_UPT;
@@ -75,7 +84,32 @@ __global__ __launch_bounds__(CODEC_NT) void dequant_kernel(const uint8_t* __rest
         const int64_t u = base + i * CODEC_NT + threadIdx.x;
         q[i] = *reinterpret_cast<const uint32_t*>(packed + 4 * (u < whole ? u : whole - 1));
       }
-      if (BLK8) {
+      if (BLK8 && fast) {
+        int64_t blk[DQ_UPT];
+#pragma unroll
+        for (int i = 0; i < DQ_UPT; ++i) {
+          const int64_t u = base + i * CODEC_NT + threadIdx.x;
+          blk[i] = (8 * (u < whole ? u : whole - 1)) >> blk_shift;
+        }
+        if (ss.nested) {
+          uint32_t qb[DQ_UPT];
+          float a2[DQ_UPT];
+#pragma unroll
+          for (int i = 0; i < DQ_UPT; ++i) {
+            qb[i] = ss.q[blk[i]];
+            a2[i] = ss.absmax2[blk[i] >> ss.dq_shift];
+          }
+#pragma unroll
+          for (int i = 0; i < DQ_UPT; ++i) {
+#pragma clang fp contract(off)
+            const float prod = c2s[qb[i]] * a2[i];   // block_scale's order: fp32(code2[q] * absmax2) + offset
+            sc[i] = prod + ss.offset;
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < DQ_UPT; ++i) sc[i] = ss.scales[blk[i]];
+        }
+      } else if (BLK8) {
 #pragma unroll
         for (int i = 0; i < DQ_UPT; ++i) {
           const int64_t u = base + i * CODEC_NT + threadIdx.x;
@@ -246,6 +280,14 @@ __global__ __launch_bounds__(CODEC_NT) void dq_quant_kernel(const float* __restr
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+// log2(v) for a power of two, else -1.
+int pow2_shift(int64_t v) {
+  if (v <= 0 || (v & (v - 1)) != 0) return -1;
+  int s = 0;
+  while ((int64_t{1} << s) < v) ++s;
+  return s;
+}
+
 int make_scale_src(const molt_nf4_weight* w, ScaleSrc& s, const char* who) {
   s = ScaleSrc{};
   s.nested = w->nested != 0;
@@ -254,6 +296,7 @@ int make_scale_src(const molt_nf4_weight* w, ScaleSrc& s, const char* who) {
                  "%s: nested statistics incomplete", who);
     s.q = w->absmax_q; s.absmax2 = w->absmax2; s.code2 = w->code2; s.offset = w->offset;
     s.dq_block = w->dq_block;
+    s.dq_shift = pow2_shift(w->dq_block);
   } else {
     MOLT_REQUIRE(w->scales, MOLT_EINVAL, "%s: scales missing", who);
     s.scales = w->scales;
@@ -291,7 +334,7 @@ extern "C" int molt_nf4_dequantize(const molt_nf4_weight* w, void* out, int32_t 
   hipStream_t st = (hipStream_t)stream;
 #define MOLT_DQ(F32, B32)                                                                        \
   hipLaunchKernelGGL((dequant_kernel<F32, B32>), dim3(grid), dim3(CODEC_NT), 0, st, w->packed, ss, \
-                     w->code, w->nibble_order, n, w->block_size, out)
+                     w->code, w->nibble_order, n, w->block_size, pow2_shift(w->block_size), out)
   if (out_dtype == MOLT_DTYPE_F32) {
     if (blk8) MOLT_DQ(1, true); else MOLT_DQ(1, false);
   } else {
