@@ -133,8 +133,8 @@ class tuning:
         with tuning(big_tile_min=1):   # force the 256 x 256 tile GEMMs
             ...
 
-    Keys: ``big_tile_min``, ``gemv_dot_m``, ``lora_dma``, ``split_k``, ``split_min_steps``. Settings are process
-    wide; callers that change them concurrently race."""
+    Keys: ``big_tile_min``, ``gemv_dot_m``, ``lora_dma``, ``split_k``, ``split_min_steps``,
+    ``stage_min_mtiles``. Settings are process wide; callers that change them concurrently race."""
 
     def __init__(self, **values: int) -> None:
         unknown = set(values) - set(TUNING_KEYS)
