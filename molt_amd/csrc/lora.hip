@@ -256,10 +256,31 @@ MOLT_DEV void pj_wait_vm() {
   asm volatile("" ::: "memory");
 }
 
+// The adapter fragments of step s by buffer loads: the lane offset is fixed
+// and the step's offset scalar, so a step needs no address registers (the
+// compiler would otherwise reuse ones that a load in flight still writes).
+template <int TQ>
+MOLT_DEV void pj_load_w(u32x4_t (&w)[TQ][4], __amdgpu_buffer_rsrc_t wr, int64_t s, int lane) {
+#pragma unroll
+  for (int t = 0; t < TQ; ++t) {
+    const uint32_t so = __builtin_amdgcn_readfirstlane((uint32_t)((s * TQ + t) * 4 * 64 * 16));
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) w[t][kk] = __builtin_amdgcn_raw_buffer_load_b128(wr, lane * 16 + kk * 1024, so, 0);
+  }
+}
+
 template <int TQ, int MT, int KS>
 __global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_dma_kernel(const ProjParams p) {
+  // z buffers per wave: a ring of three (z two of the wave's steps ahead)
+  // where the LDS allows it, else two (one step ahead). One array per ring
+  // slot, selected statically: the compiler waits for every DMA that may
+  // write the LDS a fragment read touches, and only distinct arrays tell it
+  // that the DMA in flight does not.
+  constexpr int NB = MT == 1 ? 3 : 2;
+  constexpr int ZB = 32 * MT * BK;
   __shared__ f32x16_t red[PJ_WAVES - 1][64];
-  __shared__ __attribute__((aligned(16))) uint16_t zs[PJ_WAVES][2][32 * MT * BK];
+  __shared__ __attribute__((aligned(16))) uint16_t zs0[PJ_WAVES][ZB], zs1[PJ_WAVES][ZB];
+  __shared__ __attribute__((aligned(16))) uint16_t zs2[NB == 3 ? PJ_WAVES : 1][NB == 3 ? ZB : 8];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5;
@@ -278,6 +299,7 @@ __global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_dma_kernel(const P
 
   if (s_begin + wave < s_end) {
     const __amdgpu_buffer_rsrc_t zr = pj_rsrc(p.z, ((p.M - 1) * p.ldz + p.D) * 2);
+    const __amdgpu_buffer_rsrc_t wr = pj_rsrc(p.wp, all_steps * TQ * 4 * 64 * 16);
     uint32_t zoff[4 * MT];
 #pragma unroll
     for (int c = 0; c < 4 * MT; ++c) {
@@ -297,20 +319,32 @@ __global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_dma_kernel(const P
 #pragma unroll
       for (int c = 0; c < 4 * MT; ++c) pj_dma16(zr, dst + c * 512, zoff[c], (uint32_t)(s * BK * 2));
     };
-    // z by DMA and the adapter fragments by register loads, both one step
-    // ahead (two register sets, alternating), so a step waits for nothing it
-    // issued itself
+    // The adapter fragments by register loads one step ahead (two register
+    // sets, alternating; they come from L2). z by DMA NB - 1 steps ahead: with
+    // three buffers a step issues the next step's adapter loads before the
+    // z two steps on, so its wait (loads complete in issue order) leaves
+    // both of those and the z issued a step earlier in flight.
     u32x4_t w0[TQ][4], w1[TQ][4];
     int64_t s = s_begin + wave;
-    int b = 0;
-    dma(s, zs[wave][0]);
-    proj_load_w<TQ>(w0, p, s, lane);
-    auto step = [&](const u32x4_t (&wc)[TQ][4], u32x4_t (&wn)[TQ][4]) {
-      const int64_t sn = s + PJ_WAVES < s_end ? s + PJ_WAVES : s_end - 1;
-      dma(sn, zs[wave][b ^ 1]);
-      proj_load_w<TQ>(wn, p, sn, lane);
-      pj_wait_vm<4 * MT + 4 * TQ>();                // this step's z and adapter landed; the next step's may fly
-      const uint16_t* zc = zs[wave][b];
+    auto clamp = [&](int64_t t) { return t < s_end ? t : s_end - 1; };
+    uint16_t* z0 = zs0[wave];
+    uint16_t* z1 = zs1[wave];
+    uint16_t* z2 = zs2[NB == 3 ? wave : 0];
+    dma(s, z0);
+    pj_load_w<TQ>(w0, wr, s, lane);
+    if constexpr (NB == 3) dma(clamp(s + PJ_WAVES), z1);
+    // step with z(s) in zc and the adapter in wc; zn receives the z load it issues
+    auto step = [&](const u32x4_t (&wc)[TQ][4], u32x4_t (&wn)[TQ][4], const uint16_t* zc, uint16_t* zn) {
+      const int64_t sn = clamp(s + PJ_WAVES);
+      if constexpr (NB == 3) {
+        pj_load_w<TQ>(wn, wr, sn, lane);
+        dma(clamp(s + 2 * PJ_WAVES), zn);
+        pj_wait_vm<8 * MT + 4 * TQ>();              // this step's z and adapter landed
+      } else {
+        dma(sn, zn);
+        pj_load_w<TQ>(wn, wr, sn, lane);
+        pj_wait_vm<4 * MT + 4 * TQ>();              // this step's z and adapter landed; the next step's may fly
+      }
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
@@ -328,10 +362,16 @@ __global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_dma_kernel(const P
                                                                 acc[i][t], 0, 0, 0);
         }
       s += PJ_WAVES;
-      b ^= 1;
       return s < s_end;
     };
-    while (step(w0, w1) && step(w1, w0)) {
+    if constexpr (NB == 3) {
+      // z of the wave's step j in buffer j % 3, the adapter in set j % 2: the pattern repeats every 6 steps
+      while (step(w0, w1, z0, z2) && step(w1, w0, z1, z0) && step(w0, w1, z2, z1) && step(w1, w0, z0, z2) &&
+             step(w0, w1, z1, z0) && step(w1, w0, z2, z1)) {
+      }
+    } else {
+      while (step(w0, w1, z0, z1) && step(w1, w0, z1, z0)) {
+      }
     }
     pj_wait_vm<0>();   // the last (repeated) loads before the kernel ends
   }

@@ -433,12 +433,23 @@ MOLT_DEV void fwd_main(const FwdParams& p, Smem& sm, int64_t m0, int64_t tn, int
 }
 
 // --------------------------------------------------------------- epilogues
+// Vector stores of output tiles. NT: non-temporal (used by the 256 x 256
+// kernels, whose outputs are hundreds of MB): the tiles stream to HBM while
+// the GEMM runs instead of staying dirty in the last-level cache, where the
+// next, memory-bound kernel would pay for writing them back.
+template <bool NT, typename V>
+MOLT_DEV void st_vec(uint16_t* dst, const V& v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<V*>(dst));
+  else *reinterpret_cast<V*>(dst) = v;
+}
+
+template <bool NT = false>
 MOLT_DEV void store4(uint16_t* __restrict__ out, int64_t ld, int64_t m, int64_t n, int64_t N,
                      const float* v, bool vec) {
   uint16_t* dst = out + m * ld + n;
   if (vec && n + 3 < N) {
     u32x2_t o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-    *reinterpret_cast<u32x2_t*>(dst) = o;
+    st_vec<NT>(dst, o);
   } else {
 #pragma unroll
     for (int e = 0; e < 4; ++e)
@@ -712,6 +723,9 @@ __global__ __launch_bounds__(NT) void nf4_bwd_kernel(const BwdParams p) {
 // backward's transposed patch stores are all bank-conflict free.
 // ======================================================================
 namespace big {
+
+// outputs by non-temporal stores (st_vec)
+constexpr bool kStreamOut = true;
 
 constexpr int BM = 256, BN = 256, NT = 512, WAVES_M = 4;
 constexpr int WROWS = 128, WCOLS = 64, TM = 4, TN = 2, LD = 64;
@@ -1066,9 +1080,9 @@ MOLT_DEV void gateup_store(const EpTile& ep, const FwdParams& p, int64_t m0, int
     }
     const int64_t off = m * p.ldy + n;
     if (p.vec_out && n + 8 <= p.N) {
-      *reinterpret_cast<u32x4_t*>(p.y[0] + off) = gw;
-      *reinterpret_cast<u32x4_t*>(p.y[1] + off) = uw;
-      *reinterpret_cast<u32x4_t*>(p.y[2] + off) = hw;
+      st_vec<kStreamOut>(p.y[0] + off, gw);
+      st_vec<kStreamOut>(p.y[1] + off, uw);
+      st_vec<kStreamOut>(p.y[2] + off, hw);
     } else {
       for (int e = 0; e < 8 && n + e < p.N; ++e) {
         const int w = e >> 1, sh = (e & 1) * 16;
@@ -1511,8 +1525,8 @@ MOLT_DEV void swiglu_bwd_store(const EpTile& ep, const BwdParams& p, int64_t m0,
       duw[e] = pack_bf16x2(duo[0], duo[1]);
     }
     if (p.vec_out && n + 8 <= p.Kw) {
-      *reinterpret_cast<u32x4_t*>(p.dg + off) = dgw;
-      *reinterpret_cast<u32x4_t*>(p.du + off) = duw;
+      st_vec<kStreamOut>(p.dg + off, dgw);
+      st_vec<kStreamOut>(p.du + off, duw);
     } else {
       for (int e = 0; e < 8 && n + e < p.Kw; ++e) {
         const int w = e >> 1, sh = (e & 1) * 16;
