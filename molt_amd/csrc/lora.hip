@@ -432,7 +432,8 @@ struct GradParams {
   const uint16_t* rm; int64_t ldr;
   int64_t M, P, Q;
   int64_t slice;
-  float* part;
+  float* part;          // split partials [S][P][Q] (layout 0) or [S][Q][P] (layout 1)
+  int layout;
   const float* inv; const void* nw; int nw_f32; float noff;   // L_NORM only
 };
 
@@ -566,15 +567,29 @@ __global__ __launch_bounds__(GR_NT) void lora_grad_kernel(const GradParams p) {
   }
 
   // acc[i][0] is C[p][q]: column q = lane % 32, rows p = 8(e/4) + 4(lane/32) + e%4.
+  // The partial is stored in the output's layout, so that the split sum is
+  // element-wise; in layout 1 a lane's four consecutive p are one 16-byte store.
   float* out = p.part + (int64_t)blockIdx.z * p.P * p.Q;
   const int64_t q = q0 + wq * GR_WCOLS + (lane & 31);
   if (q >= p.Q) return;
+  const bool v4 = p.P % 4 == 0 && ((uintptr_t)out & 15) == 0;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int64_t pp = p0 + wp * GR_WROWS + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-      if (pp < p.P) out[pp * p.Q + q] = acc[i][0][e];
+    for (int g = 0; g < 4; ++g) {
+      const int64_t pp = p0 + wp * GR_WROWS + i * 32 + 8 * g + 4 * (lane >> 5);
+      if (p.layout == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (pp + e < p.P) out[(pp + e) * p.Q + q] = acc[i][0][4 * g + e];
+      } else if (v4 && pp < p.P) {
+        const f32x4_t v = {acc[i][0][4 * g], acc[i][0][4 * g + 1], acc[i][0][4 * g + 2], acc[i][0][4 * g + 3]};
+        *reinterpret_cast<f32x4_t*>(out + q * p.P + pp) = v;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (pp + e < p.P) out[q * p.P + pp + e] = acc[i][0][4 * g + e];
+      }
     }
 }
 
@@ -583,15 +598,34 @@ __global__ void zero_fill_kernel(float* __restrict__ out, int64_t n) {
     out[i] = 0.0f;
 }
 
-__global__ void lora_grad_reduce_kernel(const float* __restrict__ part, int S, int64_t P, int64_t Q,
-                                        float scale, float* __restrict__ out, int layout) {
-  const int64_t n = P * Q;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x) {
+// Sum of the S split partials (stored in the output's layout) in split order,
+// times scale: element-wise, four floats per thread with vec4 (n % 4 == 0,
+// 16-byte aligned partials and output). The loads of up to 8 partials are
+// issued before their in-order sum, so a thread waits once per 8 partials.
+__global__ void lora_grad_reduce_kernel(const float* __restrict__ part, int S, int64_t n, float scale,
+                                        float* __restrict__ out, int vec4) {
+  if (vec4) {
+    const int64_t n4 = n / 4;
+    const f32x4_t* p4 = reinterpret_cast<const f32x4_t*>(part);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
+      f32x4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
+      int k = 0;
+      for (; k + 8 <= S; k += 8) {
+        f32x4_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = p4[(int64_t)(k + u) * n4 + i];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+      }
+      for (; k < S; ++k) s += p4[(int64_t)k * n4 + i];
+      reinterpret_cast<f32x4_t*>(out)[i] = s * scale;
+    }
+    return;
+  }
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     float s = 0.0f;
     for (int k = 0; k < S; ++k) s += part[(int64_t)k * n + i];
-    const int64_t pp = i / Q, q = i % Q;
-    out[layout == 0 ? i : q * P + pp] = s * scale;
+    out[i] = s * scale;
   }
 }
 
@@ -757,6 +791,7 @@ static int launch_grad(GradParams& p, bool vec, int lm, float scale, float* out,
                workspace_bytes, need);
   p.slice = ceil_div64(ceil_div64(M, S), BK) * BK;
   p.part = (float*)workspace;
+  p.layout = out_layout;
   const int S_eff = (int)ceil_div64(M, p.slice);
   dim3 grid((unsigned)ceil_div64(P, GR_P), (unsigned)ceil_div64(Q, GR_Q), (unsigned)S_eff);
   if (!vec) hipLaunchKernelGGL((lora_grad_kernel<false, L_PLAIN>), grid, dim3(GR_NT), 0, st, p);
@@ -766,10 +801,11 @@ static int launch_grad(GradParams& p, bool vec, int lm, float scale, float* out,
   int rc = check_launch(who);
   if (rc) return rc;
   const int64_t n = P * Q;
-  unsigned blocks = (unsigned)((n + 255) / 256);
+  const int vec4 = n % 4 == 0 && aligned(p.part, 16) && aligned(out, 16);
+  const int64_t items = vec4 ? n / 4 : n;
+  unsigned blocks = (unsigned)((items + 255) / 256);
   if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(lora_grad_reduce_kernel, dim3(blocks), dim3(256), 0, st, p.part, S_eff, P, Q, scale, out,
-                     out_layout);
+  hipLaunchKernelGGL(lora_grad_reduce_kernel, dim3(blocks), dim3(256), 0, st, p.part, S_eff, n, scale, out, vec4);
   return check_launch(who);
 }
 

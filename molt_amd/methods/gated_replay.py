@@ -200,8 +200,10 @@ def _fused_backward(grad_output, flat, gate, up, gated, t_gu, t_d, gate_packed, 
     u_d = ops.direct.lora_project(dy, None, 2, s_d, down_b, 1)
     dg, du = ops.direct.nf4_swiglu_backward(dy, down_packed.reshape(-1), resolved_nf4_scales(down_qs), down_qs.code,
                                      h_dim, i_dim, nibble_order(down_qs), u_d, down_a, gate, up)
-    u_g = ops.direct.lora_project(dg, None, 2, s_g, gate_b, 1)
-    u_u = ops.direct.lora_project(du, None, 2, s_u, up_b, 1)
+    # U_g and U_u as the column halves of one [tokens, 2r] matrix: the paired
+    # input gradient reads the halves in place and dA_gate/dA_up share one pass
+    u_gu = ops.direct.lora_project_pair(dg, du, s_g, s_u, gate_b, up_b)
+    u_g, u_u = u_gu[:, :r], u_gu[:, r:]
     dx = ops.direct.nf4_lora_backward_input_pair(
         dg, du, gate_packed.reshape(-1), resolved_nf4_scales(gate_qs), up_packed.reshape(-1),
         resolved_nf4_scales(up_qs), gate_qs.code, i_dim, h_dim, nibble_order(gate_qs), u_g, u_u, gate_a,
@@ -212,7 +214,6 @@ def _fused_backward(grad_output, flat, gate, up, gated, t_gu, t_d, gate_packed, 
         d_down_a = ops.direct.lora_grad(gate, up, 1, u_d, 1.0, 1)
     d_down_b = ops.direct.lora_grad(dy, None, 0, t_d, s_d, 0)
     # dA_gate and dA_up both contract X: one pass over X with [U_g | U_u]
-    u_gu = torch.cat([u_g, u_u], 1)
     if norm is not None:
         d_gu_a = ops.direct.lora_grad_rmsnorm(norm[0], norm[1], norm[2], norm[3], u_gu, 1.0, 1)
     else:

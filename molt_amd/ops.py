@@ -104,6 +104,17 @@ def _bf16(t: Tensor, name: str, what: str) -> Tensor:
     return t.contiguous()
 
 
+def _bf16_rows(t: Tensor, name: str, what: str) -> Tensor:
+    """A BF16 matrix whose rows may be strided (a column slice of a wider
+    matrix): passed as is with its row stride when the elements of a row are
+    contiguous, else made contiguous."""
+    if t.dtype != torch.bfloat16:
+        raise CapabilityError(f"{what} requires BF16 {name} (got {t.dtype})")
+    if t.dim() == 2 and t.stride(1) == 1 and t.stride(0) >= t.shape[1]:
+        return t
+    return t.contiguous()
+
+
 def _f32(t: Tensor) -> Tensor:
     if t.dtype == torch.float32 and t.is_contiguous():
         return t           # only its address is passed on
@@ -409,6 +420,38 @@ def _(z, z2, mode, zscale, lora, layout):
     return z.new_empty((z.shape[0], r), dtype=torch.bfloat16)
 
 
+@_custom_op(f"{NS}::lora_project_pair", mutates_args=())
+def lora_project_pair(z0: Tensor, z1: Tensor, zscale0: float, zscale1: float, lora0: Tensor,
+                      lora1: Tensor) -> Tensor:
+    """[bf16(bf16(s0 z0) . bf16(B0)) | bf16(bf16(s1 z1) . bf16(B1))], [M, 2 r]: the
+    gate and up U of the gated MLP's backward (methods/nf4_lora.py:87-90, mode
+    2, adapters [D, r]) written as the two column halves of one matrix, so that
+    the gate/up input gradient and the shared dA pass read them in place."""
+    what = "LoRA projection pair"
+    dev = _require_gpu(z0, z1, lora0, lora1, what=what)
+    z0 = _bf16(z0, "activations", what)
+    z1 = _bf16(z1, "activations", what)
+    if z0.dim() != 2 or z1.shape != z0.shape:
+        raise ValueError(f"{what}: expected two 2-D activations of one shape")
+    m, d = z0.shape
+    l0, l1 = _f32(lora0), _f32(lora1)
+    if l0.dim() != 2 or l0.shape[0] != d or l1.shape != l0.shape:
+        raise ValueError(f"{what}: adapters {tuple(l0.shape)}, {tuple(l1.shape)} must both be [{d}, r]")
+    r = l0.shape[1]
+    out = torch.empty((m, 2 * r), device=dev, dtype=torch.bfloat16)
+    ws_bytes = _workspace("molt_lora_project_workspace", m, d, r)
+    ws = torch.empty(max(ws_bytes, 16), device=dev, dtype=torch.uint8)
+    for half, (z, zs, lw) in enumerate(((z0, zscale0, l0), (z1, zscale1, l1))):
+        _call("molt_lora_project", z.data_ptr(), None, d, 2, zs, m, d, lw.data_ptr(), 1, r,
+              out.data_ptr() + half * r * out.element_size(), 2 * r, ws.data_ptr(), ws_bytes, _stream(dev))
+    return out
+
+
+@lora_project_pair.register_fake
+def _(z0, z1, zscale0, zscale1, lora0, lora1):
+    return z0.new_empty((z0.shape[0], 2 * lora0.shape[1]), dtype=torch.bfloat16)
+
+
 @_custom_op(f"{NS}::nf4_lora_forward", mutates_args=())
 def nf4_lora_forward(x: Tensor, packed: Tensor, scales: Tensor, code: Tensor, rows: int, cols: int,
                      order: int, block_size: int, t: Optional[Tensor], lora_b: Optional[Tensor],
@@ -557,7 +600,9 @@ def nf4_lora_backward_input_pair(dy0: Tensor, dy1: Tensor, packed0: Tensor, scal
     if u0 is not None:
         if u1 is None or a0 is None or a1 is None:
             raise ValueError(f"{what}: LoRA terms need both gradients and both A matrices")
-        uu0, uu1 = _bf16(u0, "LoRA gradients", what), _bf16(u1, "LoRA gradients", what)
+        uu0, uu1 = _bf16_rows(u0, "LoRA gradients", what), _bf16_rows(u1, "LoRA gradients", what)
+        if uu0.stride(0) != uu1.stride(0):   # one row stride for both (e.g. column halves of one matrix)
+            uu0, uu1 = uu0.contiguous(), uu1.contiguous()
         _check_rows(what, "the LoRA gradient", uu0, m)
         aa0, aa1 = _f32(a0), _f32(a1)
         r = uu0.shape[1]
@@ -566,7 +611,8 @@ def nf4_lora_backward_input_pair(dy0: Tensor, dy1: Tensor, packed0: Tensor, scal
     ws_bytes = _workspace("molt_nf4_lora_backward_workspace", m, rows, cols, 2)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     _call("molt_nf4_lora_backward_input_pair", dy0.data_ptr(), dy1.data_ptr(), rows, m, C.byref(w0),
-          C.byref(w1), _ptr(uu0), _ptr(uu1), max(r, 1), _ptr(aa0), _ptr(aa1), r, dx.data_ptr(), cols,
+          C.byref(w1), _ptr(uu0), _ptr(uu1), max(uu0.stride(0) if r else 1, 1), _ptr(aa0), _ptr(aa1), r,
+          dx.data_ptr(), cols,
           _ptr(ws), ws_bytes, _stream(dev))
     return dx
 
@@ -628,7 +674,7 @@ def lora_grad(l: Tensor, l2: Optional[Tensor], mode: int, rmat: Tensor, scale: f
     dev = _require_gpu(l, l2, rmat, what=what)
     l = _bf16(l, "activations", what)
     l2 = None if l2 is None else _bf16(l2, "activations", what)
-    rmat = _bf16(rmat, "low-rank operand", what)
+    rmat = _bf16_rows(rmat, "low-rank operand", what)
     if l2 is not None and l2.shape != l.shape:
         raise ValueError(f"{what}: the second operand {tuple(l2.shape)} must match {tuple(l.shape)}")
     if l.dim() != 2 or rmat.dim() != 2 or l.shape[0] != rmat.shape[0]:
@@ -638,8 +684,8 @@ def lora_grad(l: Tensor, l2: Optional[Tensor], mode: int, rmat: Tensor, scale: f
     out = torch.empty((p, q) if layout == 0 else (q, p), device=dev, dtype=torch.float32)
     ws_bytes = _workspace("molt_lora_grad_workspace", m, p, q)
     ws = torch.empty(max(ws_bytes, 4), device=dev, dtype=torch.uint8)
-    _call("molt_lora_grad", l.data_ptr(), _ptr(l2), p, mode, rmat.data_ptr(), q, m, p, q, float(scale),
-          out.data_ptr(), layout, ws.data_ptr(), ws_bytes, _stream(dev))
+    _call("molt_lora_grad", l.data_ptr(), _ptr(l2), p, mode, rmat.data_ptr(), max(rmat.stride(0), q), m, p, q,
+          float(scale), out.data_ptr(), layout, ws.data_ptr(), ws_bytes, _stream(dev))
     return out
 
 

@@ -92,3 +92,30 @@ def test_lora_grad_empty_rows_gives_zeros():
     out = ops.lora_grad(l, None, 0, rmat, 1.0, 1)
     assert out.shape == (16, 64)
     assert torch.count_nonzero(out).item() == 0
+
+
+@pytest.mark.parametrize("m,d,r", [(300, 4096, 64), (8192, 1024, 16), (70, 200, 8)])
+def test_lora_project_pair_is_the_two_projections_side_by_side(m, d, r):
+    """The gate/up U pair written as column halves of one matrix equals the two
+    separate pre-scaled projections bit for bit."""
+    print(f"lora_project_pair m={m} d={d} r={r}", flush=True)
+    z0, z1 = seeded((m, d), 11), seeded((m, d), 12)
+    b0, b1 = uniform((d, r), 13, 1 / np.sqrt(d)), uniform((d, r), 14, 1 / np.sqrt(d))
+    pair = ops.lora_project_pair(z0, z1, 0.5, 2.0, b0, b1)
+    u0 = ops.lora_project(z0, None, 2, 0.5, b0, 1)
+    u1 = ops.lora_project(z1, None, 2, 2.0, b1, 1)
+    assert pair.shape == (m, 2 * r)
+    assert torch.equal(pair[:, :r], u0) and torch.equal(pair[:, r:], u1)
+
+
+@pytest.mark.parametrize("m,p,q,layout", [(4099, 512, 64, 0), (2048, 384, 64, 1), (300, 200, 16, 0)])
+def test_lora_grad_reads_a_column_slice_in_place(m, p, q, layout):
+    """R given as the column half of a wider matrix (row stride 2q, passed as
+    ldr) gives the gradient of the same values made contiguous, bit for bit."""
+    print(f"lora_grad strided R m={m} p={p} q={q} layout={layout}", flush=True)
+    l = seeded((m, p), 15)
+    wide = seeded((m, 2 * q), 16)
+    for half in (wide[:, :q], wide[:, q:]):
+        assert not half.is_contiguous()
+        assert torch.equal(ops.lora_grad(l, None, 0, half, 1.5, layout),
+                           ops.lora_grad(l, None, 0, half.contiguous(), 1.5, layout))

@@ -182,3 +182,19 @@ def test_lora_ring_needs_its_workspace():
         assert lib.molt_nf4_lora_forward_workspace(m, n, k, r) > lib.molt_nf4_lora_forward_workspace(m, n, k, 0)
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1])
+
+
+def test_paired_backward_reads_u_halves_in_place():
+    """U_g and U_u as the column halves of one matrix (one row stride, as the
+    fused MLP's backward passes them) give the result of contiguous copies."""
+    m, i, h, r = 300, 256, 512, 16
+    print(f"paired backward, strided U m={m} I={i} H={h} r={r}", flush=True)
+    p0, q0, s0 = _weight(i, h, 66)
+    p1, q1, s1 = _weight(i, h, 67)
+    d0, d1 = seeded((m, i), 68), seeded((m, i), 69)
+    u = seeded((m, 2 * r), 70)
+    a0, a1 = uniform((r, h), 71, 0.05), uniform((r, h), 72, 0.05)
+    outs = [ops.nf4_lora_backward_input_pair(d0, d1, p0, s0, p1, s1, q0.code, i, h, 1, ug, uu, a0, a1)
+            for ug, uu in ((u[:, :r], u[:, r:]), (u[:, :r].contiguous(), u[:, r:].contiguous()))]
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
