@@ -256,6 +256,17 @@ MOLT_DEV void pj_wait_vm() {
   asm volatile("" ::: "memory");
 }
 
+// Workgroup barrier without __syncthreads()'s release fence, which would make
+// every wave drain its DMA in flight (stages that are only read later); the
+// caller waits (vmcnt) for the stage the other waves read next, and this
+// wave's own LDS accesses are waited for here.
+MOLT_DEV void pj_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // The adapter fragments of step s by buffer loads: the lane offset is fixed
 // and the step's offset scalar, so a step needs no address registers (the
 // compiler would otherwise reuse ones that a load in flight still writes).
@@ -519,6 +530,35 @@ MOLT_DEV void patch_store(const Patch& pt, const GradParams& p, const float (&wo
   }
 }
 
+// acc[i][0] is C[p][q]: column q = lane % 32, rows p = 8(e/4) + 4(lane/32) + e%4.
+// The partial is stored in the output's layout, so that the split sum is
+// element-wise; in layout 1 a lane's four consecutive p are one 16-byte store.
+MOLT_DEV void grad_store_partial(const GradParams& p, const f32x16_t (&acc)[2][1], int64_t p0, int64_t q0, int wp,
+                                 int wq, int lane) {
+  float* out = p.part + (int64_t)blockIdx.z * p.P * p.Q;
+  const int64_t q = q0 + wq * GR_WCOLS + (lane & 31);
+  if (q >= p.Q) return;
+  const bool v4 = p.P % 4 == 0 && ((uintptr_t)out & 15) == 0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int64_t pp = p0 + wp * GR_WROWS + i * 32 + 8 * g + 4 * (lane >> 5);
+      if (p.layout == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (pp + e < p.P) out[(pp + e) * p.Q + q] = acc[i][0][4 * g + e];
+      } else if (v4 && pp < p.P) {
+        const f32x4_t v = {acc[i][0][4 * g], acc[i][0][4 * g + 1], acc[i][0][4 * g + 2], acc[i][0][4 * g + 3]};
+        *reinterpret_cast<f32x4_t*>(out + q * p.P + pp) = v;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (pp + e < p.P) out[q * p.P + pp + e] = acc[i][0][4 * g + e];
+      }
+    }
+}
+
 template <bool VEC, int LM>
 __global__ __launch_bounds__(GR_NT) void lora_grad_kernel(const GradParams p) {
   // One LDS tile (27 KB: three workgroups per CU) where the registers allow
@@ -566,31 +606,115 @@ __global__ __launch_bounds__(GR_NT) void lora_grad_kernel(const GradParams p) {
     }
   }
 
-  // acc[i][0] is C[p][q]: column q = lane % 32, rows p = 8(e/4) + 4(lane/32) + e%4.
-  // The partial is stored in the output's layout, so that the split sum is
-  // element-wise; in layout 1 a lane's four consecutive p are one 16-byte store.
-  float* out = p.part + (int64_t)blockIdx.z * p.P * p.Q;
-  const int64_t q = q0 + wq * GR_WCOLS + (lane & 31);
-  if (q >= p.Q) return;
-  const bool v4 = p.P % 4 == 0 && ((uintptr_t)out & 15) == 0;
+  grad_store_partial(p, acc, p0, q0, wp, wq, lane);
+}
+
+// ------------------------------------------------------------------------
+// DMA-staged gradient (plain L, 16-byte aligned rows, P and Q multiples of 8):
+// the L and R tiles of a 64-row step arrive by buffer-load DMA in their
+// natural row layout, in a ring of three stages (two steps ahead), and the
+// MFMA fragments, which need M contiguous per lane, are gathered from LDS by
+// 16-bit reads (eight per fragment, into the halves of four registers). In a
+// row with bit 3 of its index set, 16-byte chunk j sits at position j ^ 4, so
+// that the two lane halves of a fragment read (rows 8 apart) fall on
+// different banks. Rows past M lie outside the buffer resource and read as
+// zero; columns past P or Q only feed outputs that are not stored. Same tiles,
+// slices and MFMA operands as lora_grad_kernel: the result is bitwise its.
+// ------------------------------------------------------------------------
+constexpr int GD_LT = BK * GR_P, GD_RT = BK * GR_Q;   // elements of one stage's L and R tile
+
+MOLT_DEV bf16x8_t gd_frag(const uint16_t* __restrict__ s, int base, int stride) {
+  typedef unsigned short us2_t __attribute__((ext_vector_type(2)));
+  u32x4_t v;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int e = 0; e < 4; ++e) {
+    us2_t t;
+    t.x = s[base + 2 * e * stride];
+    t.y = s[base + (2 * e + 1) * stride];
+    v[e] = __builtin_bit_cast(uint32_t, t);
+  }
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+__global__ __launch_bounds__(GR_NT, 2) void lora_grad_dma_kernel(const GradParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t la[GD_LT], lb[GD_LT], lc[GD_LT];
+  __shared__ __attribute__((aligned(16))) uint16_t ra[GD_RT], rb[GD_RT], rc[GD_RT];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wp = wave & 1, wq = wave >> 1, h = lane >> 5;
+  const int64_t p0 = (int64_t)blockIdx.x * GR_P;
+  const int64_t q0 = (int64_t)blockIdx.y * GR_Q;
+  const int64_t mbeg = (int64_t)blockIdx.z * p.slice;
+  const int64_t mend = mbeg + p.slice < p.M ? mbeg + p.slice : p.M;
+  const int steps = (int)ceil_div64(mend - mbeg, BK);
+  const __amdgpu_buffer_rsrc_t lr = pj_rsrc(p.l, ((p.M - 1) * p.ldl + p.P) * 2);
+  const __amdgpu_buffer_rsrc_t rr = pj_rsrc(p.rm, ((p.M - 1) * p.ldr + p.Q) * 2);
+  // DMA instruction c of L covers rows 4c .. 4c + 3 (16 lanes per 256-byte
+  // row), of R rows 8c .. 8c + 7 (8 lanes per 128-byte row); a wave issues
+  // L instructions 4 wave .. + 3 and R instructions 2 wave, 2 wave + 1.
+  uint32_t loff[4], roff[2];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int64_t pp = p0 + wp * GR_WROWS + i * 32 + 8 * g + 4 * (lane >> 5);
-      if (p.layout == 0) {
+  for (int j = 0; j < 4; ++j) {
+    const int r = 4 * (4 * wave + j) + (lane >> 4);
+    const int ch = (lane & 15) ^ (4 * ((r >> 3) & 1));
+    loff[j] = (uint32_t)((r * p.ldl + p0 + 8 * ch) * 2);
+  }
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (pp + e < p.P) out[(pp + e) * p.Q + q] = acc[i][0][4 * g + e];
-      } else if (v4 && pp < p.P) {
-        const f32x4_t v = {acc[i][0][4 * g], acc[i][0][4 * g + 1], acc[i][0][4 * g + 2], acc[i][0][4 * g + 3]};
-        *reinterpret_cast<f32x4_t*>(out + q * p.P + pp) = v;
-      } else {
+  for (int j = 0; j < 2; ++j) {
+    const int r = 8 * (2 * wave + j) + (lane >> 3);
+    const int ch = (lane & 7) ^ (4 * ((r >> 3) & 1));
+    roff[j] = (uint32_t)((r * p.ldr + q0 + 8 * ch) * 2);
+  }
+  auto dma = [&](int s, uint16_t* ld, uint16_t* rd) {
+    s = s < steps ? s : steps - 1;   // past the end: the last stage again, never read
+    const int64_t m = mbeg + (int64_t)s * BK;
+    const uint32_t ls = __builtin_amdgcn_readfirstlane((uint32_t)(m * p.ldl * 2));
+    const uint32_t rs = __builtin_amdgcn_readfirstlane((uint32_t)(m * p.ldr * 2));
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (pp + e < p.P) out[q * p.P + pp + e] = acc[i][0][4 * g + e];
-      }
+    for (int j = 0; j < 4; ++j) pj_dma16(lr, ld + (4 * wave + j) * 512, loff[j], ls);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) pj_dma16(rr, rd + (2 * wave + j) * 512, roff[j], rs);
+  };
+  // fragment bases (row 8 h of the step; sub-step kk adds 16 rows, element e one row)
+  int abase[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int pl = wp * GR_WROWS + 32 * i + (lane & 31);
+    abase[i] = 8 * h * GR_P + (((pl >> 3) ^ (4 * h)) << 3) + (pl & 7);
+  }
+  const int ql = wq * GR_WCOLS + (lane & 31);
+  const int bbase = 8 * h * GR_Q + (((ql >> 3) ^ (4 * h)) << 3) + (ql & 7);
+
+  f32x16_t acc[2][1];
+  zero_acc(acc);
+  dma(0, la, ra);
+  dma(1, lb, rb);
+  pj_wait_vm<6>();                   // stage 0 landed; stage 1 may fly
+  pj_barrier();
+  int s = 0;
+  // step s: stage s from (lcur, rcur); the DMA of stage s + 2 goes to the
+  // buffers stage s - 1 used, which every wave left at the last barrier
+  auto step = [&](const uint16_t* lcur, const uint16_t* rcur, uint16_t* lnn, uint16_t* rnn) {
+    dma(s + 2, lnn, rnn);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const bf16x8_t a0 = gd_frag(lcur, abase[0] + 16 * kk * GR_P, GR_P);
+      const bf16x8_t a1 = gd_frag(lcur, abase[1] + 16 * kk * GR_P, GR_P);
+      const bf16x8_t b0 = gd_frag(rcur, bbase + 16 * kk * GR_Q, GR_Q);
+      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[0][0], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
     }
+    pj_wait_vm<6>();                 // stage s + 1 landed; stage s + 2 may fly
+    pj_barrier();
+    return ++s < steps;
+  };
+  // (two rounds of the ring per iteration: the compiler adds a wait for the
+  // DMA in flight at the loop head, which this makes one step in six)
+  while (step(la, ra, lc, rc) && step(lb, rb, la, ra) && step(lc, rc, lb, rb) && step(la, ra, lc, rc) &&
+         step(lb, rb, la, ra) && step(lc, rc, lb, rb)) {
+  }
+  pj_wait_vm<0>();                   // the repeated stages past the end
+  grad_store_partial(p, acc, p0, q0, wp, wq, lane);
 }
 
 __global__ void zero_fill_kernel(float* __restrict__ out, int64_t n) {
@@ -631,15 +755,16 @@ __global__ void lora_grad_reduce_kernel(const float* __restrict__ part, int S, i
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
-// M slices of a gradient launch: as many as keep every workgroup of the
-// single-buffered kernel resident at once (three per CU), so no partial
-// second round of workgroups trails the first. The count must not depend on
+// M slices of a gradient launch: as many as keep every workgroup resident at
+// once (two per CU: the DMA kernel's LDS ring, the replay variants'
+// registers), so no partial second round of workgroups trails the first
+// (measured: 50 -> 46 us for the dB over dg at cfg4). The count must not depend on
 // the L operand's mode: the slices fix the fp32 summation order, and the
 // replayed and normalised operands must give bitwise the gradient of the
 // materialised one.
 int grad_splits(int64_t M, int64_t P, int64_t Q) {
   const int64_t tiles = ceil_div64(P, GR_P) * ceil_div64(Q, GR_Q);
-  int64_t s = 3 * (int64_t)molt::device_cus() / tiles;
+  int64_t s = 2 * (int64_t)molt::device_cus() / tiles;
   const int64_t max_s = ceil_div64(M, 256);    // keep >= 256 rows per split
   if (s > max_s) s = max_s;
   if (s < 1) s = 1;
@@ -794,7 +919,11 @@ static int launch_grad(GradParams& p, bool vec, int lm, float scale, float* out,
   p.layout = out_layout;
   const int S_eff = (int)ceil_div64(M, p.slice);
   dim3 grid((unsigned)ceil_div64(P, GR_P), (unsigned)ceil_div64(Q, GR_Q), (unsigned)S_eff);
-  if (!vec) hipLaunchKernelGGL((lora_grad_kernel<false, L_PLAIN>), grid, dim3(GR_NT), 0, st, p);
+  // the DMA-staged kernel for plain aligned operands whose byte offsets fit the buffer resources
+  const bool dma = vec && lm == L_PLAIN && molt::tuning_value(MOLT_TUNE_LORA_DMA) != 0 &&
+                   ((M - 1) * p.ldl + P) * 2 < ((int64_t)1 << 31) && ((M - 1) * p.ldr + Q) * 2 < ((int64_t)1 << 31);
+  if (dma) hipLaunchKernelGGL(lora_grad_dma_kernel, grid, dim3(GR_NT), 0, st, p);
+  else if (!vec) hipLaunchKernelGGL((lora_grad_kernel<false, L_PLAIN>), grid, dim3(GR_NT), 0, st, p);
   else if (lm == L_REPLAY) hipLaunchKernelGGL((lora_grad_kernel<true, L_REPLAY>), grid, dim3(GR_NT), 0, st, p);
   else if (lm == L_NORM) hipLaunchKernelGGL((lora_grad_kernel<true, L_NORM>), grid, dim3(GR_NT), 0, st, p);
   else hipLaunchKernelGGL((lora_grad_kernel<true, L_PLAIN>), grid, dim3(GR_NT), 0, st, p);

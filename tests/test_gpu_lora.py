@@ -119,3 +119,26 @@ def test_lora_grad_reads_a_column_slice_in_place(m, p, q, layout):
         assert not half.is_contiguous()
         assert torch.equal(ops.lora_grad(l, None, 0, half, 1.5, layout),
                            ops.lora_grad(l, None, 0, half.contiguous(), 1.5, layout))
+
+
+@pytest.mark.parametrize("m,p,q,layout,strided", [
+    (300, 200, 16, 1, False),     # one step, tails in P and Q
+    (4099, 512, 64, 0, False),    # row tail in the last slice, several slices
+    (1000, 136, 24, 0, True),     # P past one 128 tile, R a column slice (row stride 2q)
+    (2048, 384, 128, 1, False),   # two rank tiles
+    (8192, 4096, 128, 1, True),   # cfg4's paired dA over X, U halves of one matrix
+    (5000, 14336, 64, 0, False),  # long rows (dB over dg)
+])
+def test_lora_grad_dma_kernel_equals_the_register_kernel(m, p, q, layout, strided):
+    """The DMA-staged gradient kernel (plain aligned operands) has the same
+    tiles, slices and MFMA operands as the register-staged one: bitwise equal."""
+    print(f"lora_grad DMA vs register m={m} p={p} q={q} layout={layout} strided={strided}", flush=True)
+    l = seeded((m, p), 17)
+    wide = seeded((m, 2 * q), 18)
+    rmat = wide[:, q:] if strided else wide[:, :q].contiguous()
+    with molt_amd._lib.tuning(lora_dma=1):
+        dma = ops.lora_grad(l, None, 0, rmat, 0.5, layout)
+    with molt_amd._lib.tuning(lora_dma=0):
+        reg = ops.lora_grad(l, None, 0, rmat, 0.5, layout)
+    torch.cuda.synchronize()
+    assert torch.equal(dma, reg)
