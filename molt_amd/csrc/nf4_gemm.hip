@@ -1475,9 +1475,10 @@ MOLT_DEV void stage_acc(const EpTile& ep, const f32x16_t (&acc)[TM][TN], int wm,
 constexpr int SW_IT = BM * 32 / NT;
 struct SwigluIn { u32x4_t g[SW_IT], u[SW_IT]; };
 
+template <int IT0 = 0, int NIT = SW_IT>
 MOLT_DEV void swiglu_load(SwigluIn& in, const BwdParams& p, int64_t m0, int64_t tn, int tid) {
 #pragma unroll
-  for (int it = 0; it < SW_IT; ++it) {
+  for (int it = IT0; it < IT0 + NIT; ++it) {
     const int q = tid + it * NT;
     const int64_t m = m0 + (q >> 5), n = tn * BN + 8 * (q & 31);
     const int64_t off = m * p.ldg + n;
@@ -1497,10 +1498,28 @@ MOLT_DEV void swiglu_load(SwigluIn& in, const BwdParams& p, int64_t m0, int64_t 
   }
 }
 
+// gate/up loads of iterations IT0 .. IT0 + NIT - 1 for full 16-byte chunks
+// (Kw and ldg multiples of 8, 16-byte aligned gate/up): every load is issued,
+// chunks past M or Kw reading the first chunk instead (their results are not
+// stored), so the loads are straight-line code and a later wait can leave the
+// other batch in flight.
+template <int IT0, int NIT>
+MOLT_DEV void swiglu_load16(SwigluIn& in, const BwdParams& p, int64_t m0, int64_t tn, int tid) {
+#pragma unroll
+  for (int it = IT0; it < IT0 + NIT; ++it) {
+    const int q = tid + it * NT;
+    const int64_t m = m0 + (q >> 5), n = tn * BN + 8 * (q & 31);
+    const int64_t off = m < p.M && n < p.Kw ? m * p.ldg + n : 0;
+    in.g[it] = *reinterpret_cast<const u32x4_t*>(p.gate + off);
+    in.u[it] = *reinterpret_cast<const u32x4_t*>(p.up + off);
+  }
+}
+
+template <int IT0 = 0, int NIT = SW_IT>
 MOLT_DEV void swiglu_bwd_store(const EpTile& ep, const BwdParams& p, int64_t m0, int64_t tn, int tid,
                                const SwigluIn& in) {
 #pragma unroll
-  for (int it = 0; it < SW_IT; ++it) {
+  for (int it = IT0; it < IT0 + NIT; ++it) {
     const int q = tid + it * NT;
     const int row = q >> 5, ch = q & 31;
     const int64_t m = m0 + row, n = tn * BN + 8 * ch;
@@ -1534,6 +1553,47 @@ MOLT_DEV void swiglu_bwd_store(const EpTile& ep, const BwdParams& p, int64_t m0,
         p.du[off + e] = (uint16_t)(duw[w] >> sh);
       }
     }
+  }
+}
+
+// dg/du of iterations IT0 .. IT0 + NIT - 1 in the full-chunk case, as
+// straight-line code: every lane issues its two 16-byte buffer stores
+// (non-temporal), those of chunks past M or Kw with an offset past the end of
+// the buffer, where the hardware drops them. With per-lane branches around
+// the stores the compiler cannot count the stores in flight and waits for all
+// of them before the next iteration's gate/up values, which serialises the
+// epilogue on store latency.
+template <int IT0, int NIT>
+MOLT_DEV void swiglu_bwd_store16(const EpTile& ep, const BwdParams& p, int64_t m0, int64_t tn, int tid,
+                                 const SwigluIn& in) {
+  const int64_t bytes = ((p.M - 1) * p.ldg + p.Kw) * 2;
+  const __amdgpu_buffer_rsrc_t rg = make_rsrc(p.dg, bytes), ru = make_rsrc(p.du, bytes);
+#pragma unroll
+  for (int it = IT0; it < IT0 + NIT; ++it) {
+    const int q = tid + it * NT;
+    const int row = q >> 5, ch = q & 31;
+    const int64_t m = m0 + row, n = tn * BN + 8 * ch;
+    const uint32_t off = m < p.M && n < p.Kw ? (uint32_t)((m * p.ldg + n) * 2) : 0x80000000u;
+    const u32x4_t dh = *reinterpret_cast<const u32x4_t*>(ep_at(ep, row, 8 * ch));
+    const u32x4_t gw = in.g[it], uw = in.u[it];
+    u32x4_t dgw, duw;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float dgo[2], duo[2];
+      const float dhv[2] = {bf16_lo(dh[e]), bf16_hi(dh[e])};
+      const float gv[2] = {bf16_lo(gw[e]), bf16_hi(gw[e])};
+      const float uv[2] = {bf16_lo(uw[e]), bf16_hi(uw[e])};
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-gv[t]));
+        duo[t] = dhv[t] * round_bf16(gv[t] * sg);
+        dgo[t] = round_bf16(dhv[t] * uv[t]) * (sg * (1.0f + gv[t] * (1.0f - sg)));
+      }
+      dgw[e] = pack_bf16x2(dgo[0], dgo[1]);
+      duw[e] = pack_bf16x2(duo[0], duo[1]);
+    }
+    __builtin_amdgcn_raw_buffer_store_b128(dgw, rg, off, 0, kStreamOut ? 2 : 0);
+    __builtin_amdgcn_raw_buffer_store_b128(duw, ru, off, 0, kStreamOut ? 2 : 0);
   }
 }
 
@@ -1793,11 +1853,34 @@ __global__ __launch_bounds__(NT) void bwd_kernel(const BwdParams p) {
   // SwiGLU backward: stage dh = bf16(acc) of the tile, then compute dgate/dup
   // cooperatively with 16-byte loads of gate/up and 16-byte stores.
   const EpTile ep{xb0, xb1, wb0, wb1};
-  stage_acc(ep, acc, wm, wn, lane);
   SwigluIn in;
-  swiglu_load(in, p, m0, tn, tid);
+  if constexpr (!STAGED) {   // (the fused kernel's registers leave no room for the batches below)
+    stage_acc(ep, acc, wm, wn, lane);
+    swiglu_load(in, p, m0, tn, tid);
+    __syncthreads();
+    swiglu_bwd_store(ep, p, m0, tn, tid, in);
+    return;
+  }
+  // full 16-byte chunks (and byte offsets that fit the buffer resources):
+  // gate/up in two batches, the first in flight while dh is staged, the
+  // second while the first half's outputs are formed and stored
+  const bool full16 = p.vec_out && p.ldg % 8 == 0 && p.Kw % 8 == 0 &&
+                      ((((uintptr_t)p.gate | (uintptr_t)p.up | (uintptr_t)p.dg | (uintptr_t)p.du) & 15) == 0) &&
+                      ((p.M - 1) * p.ldg + p.Kw) * 2 < ((int64_t)1 << 31);
+  constexpr int H = SW_IT / 2;
+  if (full16) swiglu_load16<0, H>(in, p, m0, tn, tid);
+  else swiglu_load<0, H>(in, p, m0, tn, tid);
+  stage_acc(ep, acc, wm, wn, lane);
   __syncthreads();
-  swiglu_bwd_store(ep, p, m0, tn, tid, in);
+  if (full16) {
+    swiglu_load16<H, H>(in, p, m0, tn, tid);
+    swiglu_bwd_store16<0, H>(ep, p, m0, tn, tid, in);
+    swiglu_bwd_store16<H, H>(ep, p, m0, tn, tid, in);
+  } else {
+    swiglu_load<H, H>(in, p, m0, tn, tid);
+    swiglu_bwd_store<0, H>(ep, p, m0, tn, tid, in);
+    swiglu_bwd_store<H, H>(ep, p, m0, tn, tid, in);
+  }
 }
 
 // Transposed bf16 copy of one or two weights for the staged input-gradient
