@@ -77,7 +77,8 @@ const char* molt_amd_version(void);
  *   MOLT_TUNE_GEMV_DOT_M    (MOLT_AMD_GEMV_DOT_M, default -1 = per-shape rule,
  *       else 0..4): largest token count for the streaming dot-product GEMV.
  *   MOLT_TUNE_LORA_DMA      (0 when MOLT_AMD_PJ_NODMA is set, else 1): LDS DMA
- *       staging in the LoRA projection.
+ *       staging in the LoRA projection and in the (plain-operand) LoRA
+ *       gradient; 0 selects the register-staged kernels (same results).
  *   MOLT_TUNE_SPLIT_K       (0 when MOLT_AMD_NO_SPLIT_K is set, else 1): split
  *       the contraction of a long-K GEMM with few output tiles over
  *       workgroups (needs the caller's workspace, see below).
