@@ -717,6 +717,103 @@ __global__ __launch_bounds__(GR_NT, 2) void lora_grad_dma_kernel(const GradParam
   grad_store_partial(p, acc, p0, q0, wp, wq, lane);
 }
 
+// SwiGLU-replay L = bf16(bf16(silu(g)) u) (ztrans mode 1, the forward's h)
+// gathered from the g and u tiles: the fragment of gd_frag, formed per element.
+MOLT_DEV bf16x8_t gd_frag_replay(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u, int base,
+                                 int stride) {
+  u32x4_t v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int o0 = base + 2 * e * stride, o1 = o0 + stride;
+    const float h0 = ztrans(bf16_to_f32(g[o0]), bf16_to_f32(u[o0]), 1, 1.0f);
+    const float h1 = ztrans(bf16_to_f32(g[o1]), bf16_to_f32(u[o1]), 1, 1.0f);
+    v[e] = pack_bf16x2(h0, h1);
+  }
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// The DMA-staged gradient with the SwiGLU-replayed L: g and u tiles arrive
+// like the plain kernel's L tile (same slots and chunk order), in a ring of
+// two stages (one step ahead: three stages of g, u and R would leave room for
+// one workgroup per CU), and each fragment element is replayed as it is
+// gathered. Same tiles, slices and MFMA operands as the other gradient
+// kernels: bitwise the gradient of the materialised h.
+__global__ __launch_bounds__(GR_NT, 2) void lora_grad_dma_replay_kernel(const GradParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t ga[GD_LT], gb[GD_LT], ua[GD_LT], ub[GD_LT];
+  __shared__ __attribute__((aligned(16))) uint16_t ra[GD_RT], rb[GD_RT];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wp = wave & 1, wq = wave >> 1, h = lane >> 5;
+  const int64_t p0 = (int64_t)blockIdx.x * GR_P;
+  const int64_t q0 = (int64_t)blockIdx.y * GR_Q;
+  const int64_t mbeg = (int64_t)blockIdx.z * p.slice;
+  const int64_t mend = mbeg + p.slice < p.M ? mbeg + p.slice : p.M;
+  const int steps = (int)ceil_div64(mend - mbeg, BK);
+  const int64_t lbytes = ((p.M - 1) * p.ldl + p.P) * 2;
+  const __amdgpu_buffer_rsrc_t gr = pj_rsrc(p.l, lbytes), ur = pj_rsrc(p.l2, lbytes);
+  const __amdgpu_buffer_rsrc_t rr = pj_rsrc(p.rm, ((p.M - 1) * p.ldr + p.Q) * 2);
+  uint32_t loff[4], roff[2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 4 * (4 * wave + j) + (lane >> 4);
+    const int ch = (lane & 15) ^ (4 * ((r >> 3) & 1));
+    loff[j] = (uint32_t)((r * p.ldl + p0 + 8 * ch) * 2);
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = 8 * (2 * wave + j) + (lane >> 3);
+    const int ch = (lane & 7) ^ (4 * ((r >> 3) & 1));
+    roff[j] = (uint32_t)((r * p.ldr + q0 + 8 * ch) * 2);
+  }
+  auto dma = [&](int s, uint16_t* gd, uint16_t* ud, uint16_t* rd) {
+    s = s < steps ? s : steps - 1;   // past the end: the last stage again, never read
+    const int64_t m = mbeg + (int64_t)s * BK;
+    const uint32_t ls = __builtin_amdgcn_readfirstlane((uint32_t)(m * p.ldl * 2));
+    const uint32_t rs = __builtin_amdgcn_readfirstlane((uint32_t)(m * p.ldr * 2));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pj_dma16(gr, gd + (4 * wave + j) * 512, loff[j], ls);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pj_dma16(ur, ud + (4 * wave + j) * 512, loff[j], ls);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) pj_dma16(rr, rd + (2 * wave + j) * 512, roff[j], rs);
+  };
+  int abase[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int pl = wp * GR_WROWS + 32 * i + (lane & 31);
+    abase[i] = 8 * h * GR_P + (((pl >> 3) ^ (4 * h)) << 3) + (pl & 7);
+  }
+  const int ql = wq * GR_WCOLS + (lane & 31);
+  const int bbase = 8 * h * GR_Q + (((ql >> 3) ^ (4 * h)) << 3) + (ql & 7);
+
+  f32x16_t acc[2][1];
+  zero_acc(acc);
+  dma(0, ga, ua, ra);
+  pj_wait_vm<0>();
+  pj_barrier();
+  int s = 0;
+  // step s: stage s from the current buffers; stage s + 1 goes to the others,
+  // which every wave left at the last barrier
+  auto step = [&](const uint16_t* gc, const uint16_t* uc, const uint16_t* rc, uint16_t* gn, uint16_t* un,
+                  uint16_t* rn) {
+    dma(s + 1, gn, un, rn);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const bf16x8_t a0 = gd_frag_replay(gc, uc, abase[0] + 16 * kk * GR_P, GR_P);
+      const bf16x8_t a1 = gd_frag_replay(gc, uc, abase[1] + 16 * kk * GR_P, GR_P);
+      const bf16x8_t b0 = gd_frag(rc, bbase + 16 * kk * GR_Q, GR_Q);
+      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[0][0], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
+    }
+    pj_wait_vm<0>();                 // stage s + 1 landed
+    pj_barrier();
+    return ++s < steps;
+  };
+  while (step(ga, ua, ra, gb, ub, rb) && step(gb, ub, rb, ga, ua, ra)) {
+  }
+  grad_store_partial(p, acc, p0, q0, wp, wq, lane);
+}
+
 __global__ void zero_fill_kernel(float* __restrict__ out, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
     out[i] = 0.0f;
@@ -922,7 +1019,11 @@ static int launch_grad(GradParams& p, bool vec, int lm, float scale, float* out,
   // the DMA-staged kernel for plain aligned operands whose byte offsets fit the buffer resources
   const bool dma = vec && lm == L_PLAIN && molt::tuning_value(MOLT_TUNE_LORA_DMA) != 0 &&
                    ((M - 1) * p.ldl + P) * 2 < ((int64_t)1 << 31) && ((M - 1) * p.ldr + Q) * 2 < ((int64_t)1 << 31);
+  const bool dma_replay = vec && lm == L_REPLAY && molt::tuning_value(MOLT_TUNE_LORA_DMA) != 0 &&
+                          ((M - 1) * p.ldl + P) * 2 < ((int64_t)1 << 31) &&
+                          ((M - 1) * p.ldr + Q) * 2 < ((int64_t)1 << 31);
   if (dma) hipLaunchKernelGGL(lora_grad_dma_kernel, grid, dim3(GR_NT), 0, st, p);
+  else if (dma_replay) hipLaunchKernelGGL(lora_grad_dma_replay_kernel, grid, dim3(GR_NT), 0, st, p);
   else if (!vec) hipLaunchKernelGGL((lora_grad_kernel<false, L_PLAIN>), grid, dim3(GR_NT), 0, st, p);
   else if (lm == L_REPLAY) hipLaunchKernelGGL((lora_grad_kernel<true, L_REPLAY>), grid, dim3(GR_NT), 0, st, p);
   else if (lm == L_NORM) hipLaunchKernelGGL((lora_grad_kernel<true, L_NORM>), grid, dim3(GR_NT), 0, st, p);

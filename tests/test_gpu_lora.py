@@ -142,3 +142,22 @@ def test_lora_grad_dma_kernel_equals_the_register_kernel(m, p, q, layout, stride
         reg = ops.lora_grad(l, None, 0, rmat, 0.5, layout)
     torch.cuda.synchronize()
     assert torch.equal(dma, reg)
+
+
+@pytest.mark.parametrize("m,p,q,layout", [(300, 200, 16, 1), (4099, 512, 64, 1), (8192, 14336, 64, 1),
+                                          (2048, 384, 128, 0)])
+def test_lora_grad_dma_replay_equals_register_and_materialised(m, p, q, layout):
+    """The DMA-staged SwiGLU-replay gradient equals the register-staged replay
+    and the gradient over the materialised h = bf16(bf16(silu(g)) u), bit for bit."""
+    print(f"lora_grad replay DMA m={m} p={p} q={q} layout={layout}", flush=True)
+    g, u = seeded((m, p), 19), seeded((m, p), 20)
+    rmat = seeded((m, q), 21)
+    h = ops.silu_mul_forward(g, u, True)
+    with molt_amd._lib.tuning(lora_dma=1):
+        dma = ops.lora_grad(g, u, 1, rmat, 1.0, layout)
+        mat = ops.lora_grad(h, None, 0, rmat, 1.0, layout)
+    with molt_amd._lib.tuning(lora_dma=0):
+        reg = ops.lora_grad(g, u, 1, rmat, 1.0, layout)
+    torch.cuda.synchronize()
+    assert torch.equal(dma, reg)
+    assert torch.equal(dma, mat)
