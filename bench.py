@@ -703,11 +703,12 @@ def main() -> int:
     torch.cuda.synchronize()
     log("warmup done")
     # Events around a launch cost a few µs of GPU idle each (≈ 12 µs a step per
-    # timed GEMM), so the timed steps carry them only for the gate/up forward,
+    # timed GEMM with four markers, half that with the two of pre-made event
+    # pairs), so the timed steps carry them only for the gate/up forward,
     # the step's longest kernel (twice the FLOPs of any other); the other
     # GEMMs are timed over as many steps again after the timed region.
     lead = GEMMS[0][0]
-    probes = {lead: ops.probe_events(lead)}
+    probes = {lead: ops.probe_events(lead, reserve=args.steps)}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -715,7 +716,7 @@ def main() -> int:
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ops.probe_events(lead, enable=False)
-    rest = {entry: ops.probe_events(entry) for entry, _, _ in GEMMS[1:]}
+    rest = {entry: ops.probe_events(entry, reserve=args.steps) for entry, _, _ in GEMMS[1:]}
     for i in range(args.steps):
         mlp_step(projs, x, dy, s)
     torch.cuda.synchronize()

@@ -222,16 +222,29 @@ def _check_rows(what: str, name: str, t: Optional[Tensor], rows: int) -> None:
 # Optional per-launch event probe: name -> list of (start, end) torch.cuda.Event
 # pairs recorded on the launch stream around each call of that entry point.
 _probes: dict[str, list] = {}
+# Event pairs made ahead of the calls they will time (GEMM entry points only).
+_probe_pool: dict[str, list] = {}
 
 
-def probe_events(name: str, enable: bool = True) -> list:
+def probe_events(name: str, enable: bool = True, reserve: int = 0) -> list:
     """Start (or stop) recording HIP events around every call of the C entry
     point ``name``; returns the list that collects (start, end) pairs. For the
     NF4 GEMM entry points the library records them around the GEMM kernel
     itself (``molt_amd_time_next_gemm``), leaving out weight staging and
-    split-K sums."""
+    split-K sums. ``reserve`` makes that many event pairs now (each recorded
+    once, which is what creates a HIP event), so that the first ``reserve``
+    GEMM calls put only the library's two timing markers in the stream
+    instead of four (each marker leaves the GPU idle for a few µs)."""
     if enable:
+        if reserve and name in _GEMM_ENTRIES:
+            pool = _probe_pool.setdefault(name, [])
+            for _ in range(reserve):
+                pair = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                pair[0].record()
+                pair[1].record()
+                pool.append(pair)
         return _probes.setdefault(name, [])
+    _probe_pool.pop(name, None)
     return _probes.pop(name, [])
 
 
@@ -249,10 +262,15 @@ def _call(fn_name: str, *args) -> None:
             _lib.check(rc)
         return
     lib = _lib.load()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
+    pool = _probe_pool.get(fn_name)
+    if pool:
+        start, end = pool.pop()
+    else:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        if fn_name in _GEMM_ENTRIES:
+            end.record()   # creates the event; the library records both again around the kernel
     if fn_name in _GEMM_ENTRIES:
-        end.record()   # creates the event; the library records both again around the kernel
         _lib.check(lib.molt_amd_time_next_gemm(C.c_void_p(start.cuda_event), C.c_void_p(end.cuda_event)))
     _lib.check(getattr(lib, fn_name)(*args))
     if fn_name not in _GEMM_ENTRIES:
