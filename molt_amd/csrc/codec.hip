@@ -48,7 +48,7 @@ MOLT_DEV void dq_store(void* out, int64_t e0, const float (&v)[8]) {
     u32x4_t w;
 #pragma unroll
     for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(v[2 * j], v[2 * j + 1]);
-    *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(out) + e0) = w;
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(out) + e0));
   }
 }
 
