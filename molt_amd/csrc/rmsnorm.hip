@@ -81,7 +81,9 @@ struct Raw8<true> {
   MOLT_DEV float operator[](int e) const { return e < 4 ? a[e] : b[e - 4]; }
 };
 
-template <bool F32>
+// NT: non-temporal bf16 stores (whole 16-byte runs of consecutive lanes);
+// faster for the forward's output, slower for the backward's dx.
+template <bool F32, bool NT = false>
 MOLT_DEV void st8(void* p, int64_t i, const float (&v)[8]) {
   if constexpr (F32) {
     f32x4_t a, b;
@@ -93,7 +95,8 @@ MOLT_DEV void st8(void* p, int64_t i, const float (&v)[8]) {
     u32x4_t q;
 #pragma unroll
     for (int e = 0; e < 4; ++e) q[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
-    *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(p) + i) = q;
+    if constexpr (NT) __builtin_nontemporal_store(q, reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(p) + i));
+    else *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(p) + i) = q;
   }
 }
 
@@ -163,7 +166,7 @@ __global__ __launch_bounds__(RN_NT) void rmsnorm_fwd_kernel(const RmsParams p) {
           ld8<WF32>(p.w, i, w);
 #pragma unroll
           for (int e = 0; e < 8; ++e) o8[e] = __fmul_rn(__fmul_rn(xv[c][e], inv), __fadd_rn(w[e], p.offset));
-          st8<false>(orow, i, o8);
+          st8<false, true>(orow, i, o8);
         }
       }
     } else {
