@@ -46,7 +46,7 @@ MOLT_DEV void ce_ld8(const void* p, int64_t i, float (&v)[8]) {
   }
 }
 
-template <bool F32>
+template <bool F32, bool NT = false>
 MOLT_DEV void ce_st8(void* p, int64_t i, const float (&v)[8]) {
   if constexpr (F32) {
     f32x4_t a, b;
@@ -58,7 +58,8 @@ MOLT_DEV void ce_st8(void* p, int64_t i, const float (&v)[8]) {
     u32x4_t q;
 #pragma unroll
     for (int e = 0; e < 4; ++e) q[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
-    *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(p) + i) = q;
+    if constexpr (NT) __builtin_nontemporal_store(q, reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(p) + i));
+    else *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(p) + i) = q;
   }
 }
 
@@ -230,7 +231,7 @@ __global__ __launch_bounds__(CE_NT) void ce_reg_kernel(const CeParams p) {
         const float t = (valid && i + e == y) ? 1.0f : 0.0f;
         v[e] = (__expf(v[e] - m) * inv_d - t) * inv_total;
       }
-      ce_st8<false>(grow, i, v);
+      ce_st8<false, true>(grow, i, v);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
