@@ -158,7 +158,8 @@ __global__ void resolve_kernel(ScaleSrc ss, int64_t nblocks, float* __restrict__
 
 // ------------------------------------------------------------------ quantise
 // One wave per block: absmax by wave reduction (max is order independent),
-// then each element's code is the first index of the minimum |x/absmax - code|.
+// then each element's code is the first index of the minimum |x/absmax - code|
+// (the running minimum's strict `<` keeps the first index on ties).
 MOLT_DEV float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
@@ -182,6 +183,42 @@ __global__ __launch_bounds__(CODEC_NT) void quantize_kernel(const void* __restri
     if (IN_BF16) return bf16_to_f32(reinterpret_cast<const uint16_t*>(x)[i]);
     return reinterpret_cast<const float*>(x)[i];
   };
+  auto nearest = [&](float nv) -> uint32_t {
+    float best = fabsf(nv - cb[0]);
+    uint32_t bi = 0;
+#pragma unroll
+    for (int c = 1; c < 16; ++c) {
+      const float d = fabsf(nv - cb[c]);
+      if (d < best) { best = d; bi = (uint32_t)c; }
+    }
+    return bi;
+  };
+  if (block == 64) {
+    // one element per lane, loaded once; QB blocks per pass with every load
+    // issued before the first is used; the odd lane's code joins its even
+    // neighbour's by a lane shift and the even lanes store the bytes
+    constexpr int QB = 4;
+    for (int64_t b0 = (int64_t)blockIdx.x * (CODEC_NT / 64) + (threadIdx.x >> 6); b0 < nblocks; b0 += QB * waves) {
+      float v[QB];
+#pragma unroll
+      for (int k = 0; k < QB; ++k) {
+        const int64_t b = b0 + k * waves;
+        v[k] = b < nblocks ? load(b * 64 + lane) : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < QB; ++k) {
+        const int64_t b = b0 + k * waves;
+        if (b >= nblocks) break;   // uniform across the wave
+        const float am = fmaxf(wave_max(fmaxf(0.0f, fabsf(v[k]))), 1.17549435e-38f);
+        if (lane == 0) absmax[b] = am;
+        const uint32_t bi = nearest(v[k] / am);
+        const uint32_t odd = (uint32_t)__shfl_down((int)bi, 1, 64);
+        if ((lane & 1) == 0)
+          packed[b * 32 + (lane >> 1)] = (uint8_t)(order ? ((bi << 4) | odd) : (bi | (odd << 4)));
+      }
+    }
+    return;
+  }
   for (int64_t b = (int64_t)blockIdx.x * (CODEC_NT / 64) + (threadIdx.x >> 6); b < nblocks; b += waves) {
     const int64_t base = b * block;
     float m = 0.0f;
@@ -193,17 +230,7 @@ __global__ __launch_bounds__(CODEC_NT) void quantize_kernel(const void* __restri
     for (int j = lane; j < block / 2; j += 64) {
       uint32_t idx[2];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const float nv = load(base + 2 * j + t) / am;
-        float best = fabsf(nv - cb[0]);
-        uint32_t bi = 0;
-#pragma unroll
-        for (int c = 1; c < 16; ++c) {
-          const float d = fabsf(nv - cb[c]);
-          if (d < best) { best = d; bi = (uint32_t)c; }
-        }
-        idx[t] = bi;
-      }
+      for (int t = 0; t < 2; ++t) idx[t] = nearest(load(base + 2 * j + t) / am);
       packed[(base >> 1) + j] = (uint8_t)(order ? ((idx[0] << 4) | idx[1]) : (idx[0] | (idx[1] << 4)));
     }
   }
