@@ -28,16 +28,31 @@ def test_quantize_codes_and_absmax_bit_exact(shape, block, order, dtype):
     assert np.array_equal(packed.cpu().numpy(), O.pack_nibbles(idx, order))
 
 
-def test_quantize_special_values():
-    """Zero blocks (absmax clamped to FLT_MIN), exact codes, ties."""
+@pytest.mark.parametrize("block", [32, 64])
+def test_quantize_special_values(block):
+    """Zero blocks (absmax clamped to FLT_MIN), exact codes, ties; block 64
+    takes the one-element-per-lane path, block 32 the pair-per-lane one."""
     code = O.NF4_CODE
     lo, hi = code[9], code[10]
     mid = np.float32((np.float64(lo) + np.float64(hi)) / 2)
     x = np.concatenate([np.zeros(64, np.float32), code * np.float32(3.0), code * np.float32(-0.25),
                         np.array([1.0, mid, -mid] + [0.0] * 29, np.float32)]).astype(np.float32)
     xt = torch.from_numpy(x).cuda()
-    packed, absmax = ops.nf4_quantize(xt, 32, 1, molt_amd.NF4_CODEBOOK.cuda())
-    idx, am = O.quantize_blocks(x, 32)
+    for order in (0, 1):
+        packed, absmax = ops.nf4_quantize(xt, block, order, molt_amd.NF4_CODEBOOK.cuda())
+        idx, am = O.quantize_blocks(x, block)
+        assert np.array_equal(np_f32(absmax).view(np.uint32), am.view(np.uint32))
+        assert np.array_equal(packed.cpu().numpy(), O.pack_nibbles(idx, order))
+
+
+def test_quantize_block64_more_blocks_than_one_pass():
+    """135,168 blocks of 64: more than one pass of the block-64 path's grid
+    (8192 workgroups x 4 waves x 4 blocks), the second pass partial."""
+    shape = (4096, 2112)
+    print(f"quantize block64 multi-pass shape={shape}", flush=True)
+    x = seeded(shape, 7, std=0.02, dtype=torch.bfloat16)
+    packed, absmax = ops.nf4_quantize(x, 64, 1, molt_amd.NF4_CODEBOOK.cuda())
+    idx, am = O.quantize_blocks(np_f32(x), 64)
     assert np.array_equal(np_f32(absmax).view(np.uint32), am.view(np.uint32))
     assert np.array_equal(packed.cpu().numpy(), O.pack_nibbles(idx, 1))
 
