@@ -260,12 +260,24 @@ __global__ __launch_bounds__(CODEC_NT) void dq_chunk_sum_kernel(const float* __r
   if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
 }
 
+// One wave: the chunk sums are fetched 64 at a time into LDS (so the loads
+// overlap), then lane 0 adds them left to right, the order the sum is defined by.
 __global__ void dq_offset_kernel(const double* __restrict__ partial, int64_t chunks, int64_t n,
                                  float* __restrict__ offset) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  __shared__ double stage[64];
+  const int lane = threadIdx.x;
   double s = 0.0;
-  for (int64_t i = 0; i < chunks; ++i) s += partial[i];
-  *offset = (float)(s / (double)n);
+  for (int64_t base = 0; base < chunks; base += 64) {
+    const int64_t i = base + lane;
+    stage[lane] = i < chunks ? partial[i] : 0.0;
+    __syncthreads();
+    if (lane == 0) {
+      const int64_t cnt = chunks - base < 64 ? chunks - base : 64;
+      for (int64_t k = 0; k < cnt; ++k) s += stage[k];
+    }
+    __syncthreads();
+  }
+  if (lane == 0) *offset = (float)(s / (double)n);
 }
 
 // One workgroup per dq block (<= 256 values): absmax2 over |absmax - offset|,

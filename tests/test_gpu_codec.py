@@ -57,7 +57,7 @@ def test_quantize_block64_more_blocks_than_one_pass():
     assert np.array_equal(packed.cpu().numpy(), O.pack_nibbles(idx, 1))
 
 
-@pytest.mark.parametrize("n", [1, 255, 256, 4096, 4097, 70000])
+@pytest.mark.parametrize("n", [1, 255, 256, 4096, 4097, 70000, 300000])
 def test_double_quantize_bit_exact(n):
     print(f"double quantize n={n}", flush=True)
     g = torch.Generator().manual_seed(n)
