@@ -362,6 +362,17 @@ int molt_cross_entropy_rows(const void* logits, int32_t dtype, int64_t ld, int64
                             const int64_t* targets, float total, float* loss, void* grad, int64_t ldg,
                             void* stream);
 
+/* The same rows under F.cross_entropy's rule for the exact chunked loss
+ * (kernels/partitioned_loss.py:18-103, which sums F.cross_entropy over chunks
+ * and divides by the token count): a row whose target lies outside [0, vocab)
+ * (the ignored index -100; the caller rejects any other) gets a zero loss and a
+ * zero gradient, and the gradient is multiplied by *grad_scale (device fp32
+ * scalar, the upstream gradient; NULL for 1), so no host read of it is needed:
+ * grad[i, j] = (softmax_ij - [j == y_i]) / total * (*grad_scale). */
+int molt_cross_entropy_rows_exact(const void* logits, int32_t dtype, int64_t ld, int64_t rows, int64_t vocab,
+                                  const int64_t* targets, float total, const float* grad_scale, float* loss,
+                                  void* grad, int64_t ldg, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

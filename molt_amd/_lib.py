@@ -84,6 +84,7 @@ SIGNATURES: dict[str, tuple] = {
     "molt_rmsnorm_backward": (C.c_int, [_p, _i64, _p, _i32, _i64, _i64, _i64, _p, _i32, _f32, _f32, _p, _i64,
                                         _p]),
     "molt_cross_entropy_rows": (C.c_int, [_p, _i32, _i64, _i64, _i64, _p, _f32, _p, _p, _i64, _p]),
+    "molt_cross_entropy_rows_exact": (C.c_int, [_p, _i32, _i64, _i64, _i64, _p, _f32, _p, _p, _p, _i64, _p]),
 }
 
 _lock = threading.Lock()

@@ -20,6 +20,13 @@ void take_gemm_events(void** start, void** end) {
   g_gemm_events[0] = g_gemm_events[1] = nullptr;
 }
 
+// A GEMM entry point that returns before reaching its implementation still
+// consumes the events armed for it.
+static int drop_gemm_events(int rc) {
+  g_gemm_events[0] = g_gemm_events[1] = nullptr;
+  return rc;
+}
+
 int set_error(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -128,7 +135,8 @@ int molt_amd_time_next_gemm(void* start_event, void* end_event) {
 int molt_nf4_lora_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,
                           const uint16_t* t, int64_t ldt, const float* lora_b, int32_t r, float scaling,
                           uint16_t* y, int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
-  if (!w) return molt::set_error(MOLT_EINVAL, "molt_nf4_lora_forward: null weight");
+  if (!w)
+    return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "molt_nf4_lora_forward: null weight"));
   return molt_nf4_lora_forward_impl(x, ldx, M, w, nullptr, t, ldt, r, lora_b, nullptr, r, r, scaling, scaling,
                                     y, nullptr, nullptr, ldy, workspace, workspace_bytes, (hipStream_t)stream);
 }
@@ -137,7 +145,8 @@ int molt_nf4_gateup_forward(const uint16_t* x, int64_t ldx, int64_t M, const mol
                             const molt_nf4_weight* wu, const uint16_t* t, int64_t ldt, const float* bg,
                             const float* bu, int32_t r, float sg, float su, uint16_t* gate, uint16_t* up,
                             uint16_t* h, int64_t ldo, void* workspace, size_t workspace_bytes, void* stream) {
-  if (!wg || !wu) return molt::set_error(MOLT_EINVAL, "molt_nf4_gateup_forward: null weight");
+  if (!wg || !wu)
+    return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "molt_nf4_gateup_forward: null weight"));
   return molt_nf4_lora_forward_impl(x, ldx, M, wg, wu, t, ldt, 2 * r, bg, bu, r, r, sg, su, gate, up, h, ldo,
                                     workspace, workspace_bytes, (hipStream_t)stream);
 }
@@ -145,7 +154,8 @@ int molt_nf4_gateup_forward(const uint16_t* x, int64_t ldx, int64_t M, const mol
 int molt_nf4_lora_backward_input(const uint16_t* dy, int64_t lddy, int64_t M, const molt_nf4_weight* w,
                                  const uint16_t* u, int64_t ldu, const float* lora_a, int32_t r, float lora_scale,
                                  uint16_t* dx, int64_t lddx, void* workspace, size_t workspace_bytes, void* stream) {
-  if (!w) return molt::set_error(MOLT_EINVAL, "molt_nf4_lora_backward_input: null weight");
+  if (!w)
+    return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "molt_nf4_lora_backward_input: null weight"));
   return molt_nf4_lora_backward_impl(dy, nullptr, lddy, M, w, nullptr, u, nullptr, ldu, lora_a, nullptr, w->cols,
                                      r, lora_scale, dx, lddx, nullptr, nullptr, nullptr, nullptr, 0, workspace,
                                      workspace_bytes, (hipStream_t)stream);
@@ -156,7 +166,8 @@ int molt_nf4_lora_backward_input_pair(const uint16_t* dy0, const uint16_t* dy1, 
                                       const uint16_t* u1, int64_t ldu, const float* a0, const float* a1,
                                       int32_t r, uint16_t* dx, int64_t lddx, void* workspace,
                                       size_t workspace_bytes, void* stream) {
-  if (!w0 || !w1) return molt::set_error(MOLT_EINVAL, "molt_nf4_lora_backward_input_pair: null weight");
+  if (!w0 || !w1)
+    return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "molt_nf4_lora_backward_input_pair: null weight"));
   return molt_nf4_lora_backward_impl(dy0, dy1, lddy, M, w0, w1, u0, u1, ldu, a0, a1, w0->cols, r, 1.0f, dx, lddx,
                                      nullptr, nullptr, nullptr, nullptr, 0, workspace, workspace_bytes,
                                      (hipStream_t)stream);
@@ -166,9 +177,11 @@ int molt_nf4_swiglu_backward(const uint16_t* dy, int64_t lddy, int64_t M, const 
                              const uint16_t* u, int64_t ldu, const float* lora_a, int32_t r, const uint16_t* gate,
                              const uint16_t* up, int64_t ldg, uint16_t* dgate, uint16_t* dup, void* workspace,
                              size_t workspace_bytes, void* stream) {
-  if (!wd) return molt::set_error(MOLT_EINVAL, "molt_nf4_swiglu_backward: null weight");
-  if (M == 0) return MOLT_OK;   // an empty token batch: the outputs are empty too (their pointers may be null)
-  if (!dgate) return molt::set_error(MOLT_EINVAL, "molt_nf4_swiglu_backward: null dgate");
+  if (!wd)
+    return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "molt_nf4_swiglu_backward: null weight"));
+  if (M == 0) return molt::drop_gemm_events(MOLT_OK);   // an empty token batch: the outputs are empty too
+  if (!dgate)
+    return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "molt_nf4_swiglu_backward: null dgate"));
   return molt_nf4_lora_backward_impl(dy, nullptr, lddy, M, wd, nullptr, u, nullptr, ldu, lora_a, nullptr, wd->cols,
                                      r, 1.0f, nullptr, 0, gate, up, dgate, dup, ldg, workspace, workspace_bytes,
                                      (hipStream_t)stream);

@@ -6,7 +6,11 @@
 //   loss_i  = valid ? (lse - l_y) / total : 0
 //   grad_ij = (exp(l_j - m) / d - [valid && j == y]) / total   (stored in the logits' dtype)
 // Invalid targets give a zero loss and a softmax gradient, as the reference's
-// fused kernel does (kernels/frozen_linear_cross_entropy.py:97-139).
+// fused kernel does (kernels/frozen_linear_cross_entropy.py:97-139). The exact
+// entry point (molt_cross_entropy_rows_exact) follows F.cross_entropy's rule
+// for ignored rows instead: zero loss and a zero gradient (the caller rejects
+// targets that are neither valid nor ignored), and multiplies the gradient by
+// an upstream scale read from device memory (kernels/partitioned_loss.py:56-98).
 //
 // One workgroup owns a row. Pass 1 keeps a per-thread online (max, sum) and
 // combines them across the workgroup; pass 2 writes the gradient, in place
@@ -93,7 +97,18 @@ struct CeParams {
   float total;
   float* loss;
   void* grad; int64_t ldg;
+  const float* gscale;   // upstream gradient (exact rule), or null
+  int zero_invalid;      // exact rule: rows without a valid target get a zero gradient
 };
+
+// Gradient of one element from its fp32 softmax-minus-target term: / total,
+// then the upstream scale when there is one; zero on ignored rows (also for a
+// NaN upstream scale, as F.cross_entropy leaves ignored rows untouched).
+MOLT_DEV float ce_grad(float diff, float inv_total, const CeParams& p, bool zero_row, float gs) {
+  float g = diff * inv_total;
+  if (p.gscale) g *= gs;
+  return zero_row ? 0.0f : g;
+}
 
 template <bool F32, bool VEC, bool GRAD>
 __global__ __launch_bounds__(CE_NT) void ce_kernel(const CeParams p) {
@@ -139,6 +154,8 @@ __global__ __launch_bounds__(CE_NT) void ce_kernel(const CeParams p) {
     void* grow = F32 ? (void*)(reinterpret_cast<float*>(p.grad) + row * p.ldg)
                      : (void*)(reinterpret_cast<uint16_t*>(p.grad) + row * p.ldg);
     const float inv_d = 1.0f / d, inv_total = 1.0f / p.total;
+    const bool zero_row = p.zero_invalid && !valid;
+    const float gs = p.gscale ? *p.gscale : 1.0f;
     if constexpr (VEC) {
       for (int64_t i = 8 * (int64_t)tid; i < p.V; i += 8 * CE_NT) {
         float v[8];
@@ -146,14 +163,14 @@ __global__ __launch_bounds__(CE_NT) void ce_kernel(const CeParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float t = (valid && i + e == y) ? 1.0f : 0.0f;
-          v[e] = (__expf(v[e] - m) * inv_d - t) * inv_total;
+          v[e] = ce_grad(__expf(v[e] - m) * inv_d - t, inv_total, p, zero_row, gs);
         }
         ce_st8<F32>(grow, i, v);
       }
     } else {
       for (int64_t i = tid; i < p.V; i += CE_NT) {
         const float t = (valid && i == y) ? 1.0f : 0.0f;
-        ce_st<F32>(grow, i, (__expf(ce_ld<F32>(lrow, i) - m) * inv_d - t) * inv_total);
+        ce_st<F32>(grow, i, ce_grad(__expf(ce_ld<F32>(lrow, i) - m) * inv_d - t, inv_total, p, zero_row, gs));
       }
     }
   }
@@ -215,6 +232,8 @@ __global__ __launch_bounds__(CE_NT) void ce_reg_kernel(const CeParams p) {
   if constexpr (GRAD) {
     uint16_t* grow = reinterpret_cast<uint16_t*>(p.grad) + row * p.ldg;
     const float inv_d = 1.0f / d, inv_total = 1.0f / p.total;
+    const bool zero_row = p.zero_invalid && !valid;
+    const float gs = p.gscale ? *p.gscale : 1.0f;
     // keep only the packed row alive across the reduction (unpacked, pass 1's
     // fp32 copies would double its registers)
 #pragma unroll
@@ -229,7 +248,7 @@ __global__ __launch_bounds__(CE_NT) void ce_reg_kernel(const CeParams p) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float t = (valid && i + e == y) ? 1.0f : 0.0f;
-        v[e] = (__expf(v[e] - m) * inv_d - t) * inv_total;
+        v[e] = ce_grad(__expf(v[e] - m) * inv_d - t, inv_total, p, zero_row, gs);
       }
       ce_st8<false, true>(grow, i, v);
       __builtin_amdgcn_sched_barrier(0);
@@ -244,10 +263,11 @@ bool ce_a16(const void* q) { return ((uintptr_t)q & 15) == 0; }
 
 using namespace molt;
 
-extern "C" int molt_cross_entropy_rows(const void* logits, int32_t dtype, int64_t ld, int64_t rows, int64_t vocab,
-                                       const int64_t* targets, float total, float* loss, void* grad, int64_t ldg,
-                                       void* stream) {
-  const char* who = "molt_cross_entropy_rows";
+namespace {
+
+int ce_rows(const char* who, const void* logits, int32_t dtype, int64_t ld, int64_t rows, int64_t vocab,
+            const int64_t* targets, float total, const float* grad_scale, int zero_invalid, float* loss, void* grad,
+            int64_t ldg, void* stream) {
   MOLT_REQUIRE(dtype == MOLT_DTYPE_BF16 || dtype == MOLT_DTYPE_F32, MOLT_EINVAL, "%s: dtype must be bf16 or fp32",
                who);
   MOLT_REQUIRE(rows >= 0 && vocab > 0 && ld >= vocab && (!grad || ldg >= vocab), MOLT_EINVAL,
@@ -260,7 +280,7 @@ extern "C" int molt_cross_entropy_rows(const void* logits, int32_t dtype, int64_
   const int es = f32 ? 4 : 2;
   const bool vec = vocab % 8 == 0 && ce_a16(logits) && (ld * es) % 16 == 0 &&
                    (!grad || (ce_a16(grad) && (ldg * es) % 16 == 0));
-  CeParams p{logits, ld, rows, vocab, targets, total, loss, grad, ldg};
+  CeParams p{logits, ld, rows, vocab, targets, total, loss, grad, ldg, grad_scale, zero_invalid};
   const dim3 grid((unsigned)rows), block(CE_NT);
   hipStream_t st = (hipStream_t)stream;
   // bf16 rows up to 8 * CE_NT * 20 = 163,840 logits: one read, from registers
@@ -290,4 +310,21 @@ extern "C" int molt_cross_entropy_rows(const void* logits, int32_t dtype, int64_
   }
 #undef MOLT_CE_LAUNCH
   return check_launch(who);
+}
+
+}  // namespace
+
+extern "C" int molt_cross_entropy_rows(const void* logits, int32_t dtype, int64_t ld, int64_t rows, int64_t vocab,
+                                       const int64_t* targets, float total, float* loss, void* grad, int64_t ldg,
+                                       void* stream) {
+  return ce_rows("molt_cross_entropy_rows", logits, dtype, ld, rows, vocab, targets, total, nullptr, 0, loss, grad,
+                 ldg, stream);
+}
+
+extern "C" int molt_cross_entropy_rows_exact(const void* logits, int32_t dtype, int64_t ld, int64_t rows,
+                                             int64_t vocab, const int64_t* targets, float total,
+                                             const float* grad_scale, float* loss, void* grad, int64_t ldg,
+                                             void* stream) {
+  return ce_rows("molt_cross_entropy_rows_exact", logits, dtype, ld, rows, vocab, targets, total, grad_scale, 1, loss,
+                 grad, ldg, stream);
 }

@@ -2081,18 +2081,25 @@ bool stage_wanted(int kind, int64_t M, int64_t rows, int64_t cols) {
 }
 size_t stage_one(int64_t rows, int64_t cols) { return (size_t)(rows * cols * 2 + 255) / 256 * 256; }
 
-// molt_amd_time_next_gemm: its events are recorded right around the GEMM
-// kernel's launch (construct before, finish() after).
-struct KernelEvents {
+// molt_amd_time_next_gemm: a GEMM entry point takes (and so disarms) the
+// events as it starts, whatever it then does; a call that returns early leaves
+// them unrecorded instead of passing them on to a later, unrelated GEMM.
+struct GemmEvents {
   void* start = nullptr;
   void* end = nullptr;
+  GemmEvents() { molt::take_gemm_events(&start, &end); }
+};
+
+// The taken events are recorded right around the GEMM kernel's launch
+// (construct before, finish() after).
+struct KernelEvents {
+  const GemmEvents& ev;
   hipStream_t stream;
-  explicit KernelEvents(hipStream_t s) : stream(s) {
-    molt::take_gemm_events(&start, &end);
-    if (start) (void)hipEventRecord(static_cast<hipEvent_t>(start), stream);
+  KernelEvents(const GemmEvents& e, hipStream_t s) : ev(e), stream(s) {
+    if (ev.start) (void)hipEventRecord(static_cast<hipEvent_t>(ev.start), stream);
   }
   void finish() {
-    if (end) (void)hipEventRecord(static_cast<hipEvent_t>(end), stream);
+    if (ev.end) (void)hipEventRecord(static_cast<hipEvent_t>(ev.end), stream);
   }
 };
 
@@ -2145,6 +2152,7 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
                                           uint16_t* y2, int64_t ldy, void* workspace, size_t workspace_bytes,
                                           hipStream_t stream) {
   const char* who = "molt_nf4_lora_forward";
+  const GemmEvents armed;
   int rc = check_weight_for_gemm(w0, who);
   if (rc) return rc;
   const bool pair = w1 != nullptr;
@@ -2212,7 +2220,7 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
       p.ldw = p.K;
     }
     dim3 grid((unsigned)big_tiles, (unsigned)plan.S), block(big::NT);
-    KernelEvents kev(stream);
+    KernelEvents kev(armed, stream);
     if (gw.stage) {
       if (pair) hipLaunchKernelGGL((big::fwd_kernel<true, true>), grid, block, 0, stream, p);
       else hipLaunchKernelGGL((big::fwd_kernel<false, true>), grid, block, 0, stream, p);
@@ -2231,7 +2239,7 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
       p.part = static_cast<float*>(workspace);
     }
     dim3 grid((unsigned)tiles, small_split ? (unsigned)plan.S : 1u), block(NT);
-    KernelEvents kev(stream);
+    KernelEvents kev(armed, stream);
     if (pair) {
       if (al) hipLaunchKernelGGL((nf4_fwd_kernel<true, true>), grid, block, 0, stream, p);
       else hipLaunchKernelGGL((nf4_fwd_kernel<true, false>), grid, block, 0, stream, p);
@@ -2260,6 +2268,7 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
                                            uint16_t* dg, uint16_t* du, int64_t ldg, void* workspace,
                                            size_t workspace_bytes, hipStream_t stream) {
   const char* who = "molt_nf4_lora_backward_input";
+  const GemmEvents armed;
   int rc = check_weight_for_gemm(w0, who);
   if (rc) return rc;
   const int nseg = w1 ? 2 : 1;
@@ -2335,7 +2344,7 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
       if (rc) return rc;
     }
     dim3 grid((unsigned)big_tiles, (unsigned)plan.S), block(big::NT);
-    KernelEvents kev(stream);
+    KernelEvents kev(armed, stream);
     if (gw.stage) {
       if (swiglu) hipLaunchKernelGGL((big::bwd_kernel<EPI_SWIGLU_BWD, true>), grid, block, 0, stream, p);
       else hipLaunchKernelGGL((big::bwd_kernel<EPI_STORE, true>), grid, block, 0, stream, p);
@@ -2353,7 +2362,7 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
       p.part = static_cast<float*>(workspace);
     }
     dim3 grid((unsigned)tiles, small_split ? (unsigned)plan.S : 1u), block(NT);
-    KernelEvents kev(stream);
+    KernelEvents kev(armed, stream);
     if (swiglu) {
       if (al) hipLaunchKernelGGL((nf4_bwd_kernel<EPI_SWIGLU_BWD, true>), grid, block, 0, stream, p);
       else hipLaunchKernelGGL((nf4_bwd_kernel<EPI_SWIGLU_BWD, false>), grid, block, 0, stream, p);

@@ -39,6 +39,19 @@ def _spans(count: int, chunk: int):
     return ((start, min(start + chunk, count)) for start in range(0, count, chunk))
 
 
+IGNORE_INDEX = -100   # F.cross_entropy's default ignore_index, which the reference's exact path uses
+
+
+def _check_targets(labels: torch.Tensor, vocab: int) -> None:
+    """F.cross_entropy's target rule: a target is a class in [0, vocab) or the
+    ignored index; anything else is an error (one device reduction and one
+    host read per forward)."""
+    bad = ((labels < 0) | (labels >= vocab)) & (labels != IGNORE_INDEX)
+    if bool(bad.any()):
+        first = int(labels[bad][0])
+        raise IndexError(f"Target {first} is out of bounds for {vocab} classes (ignore_index is {IGNORE_INDEX})")
+
+
 class _ChunkedLinearCrossEntropy(torch.autograd.Function):
     """Exact mean cross-entropy of ``hidden . weight^T`` with at most one
     chunk of logits alive (kernels/partitioned_loss.py:18-103).
@@ -46,20 +59,26 @@ class _ChunkedLinearCrossEntropy(torch.autograd.Function):
     Forward: per chunk, hipBLASLt logits and the HIP row kernel's per-row
     ``(lse - l_y) / count`` (no gradient pass). Backward: per chunk, the
     logits again, the row kernel in gradient mode (logits overwritten in place
-    by ``(softmax - onehot) * g / count``, one rounding to the logits' dtype),
-    then ``dh = dlogits . W`` and, for a trainable head, ``dW += dlogits^T . h``.
-    The head's dtype decides the GEMM precision, as autocast does."""
+    by ``(softmax - onehot) / count * g``, one rounding to the logits' dtype,
+    with the upstream gradient ``g`` read on the device), then
+    ``dh = dlogits . W`` and, for a trainable head, ``dW += dlogits^T . h``.
+    Targets follow F.cross_entropy: rows with the ignored index -100 add
+    nothing to the loss and get a zero gradient (the mean still divides by
+    every token, as the reference's sum over chunks / token count does); any
+    other target outside the vocabulary raises. The head's dtype decides the
+    GEMM precision, as autocast does."""
 
     @staticmethod
     def forward(ctx: Any, hidden, weight, targets, chunk_size):
         rows, labels = hidden.flatten(0, -2), targets.reshape(-1).contiguous()
         count = labels.numel()
+        _check_targets(labels, weight.shape[0])
         autocast = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else None
         dtype = _compute_dtype(hidden, weight, autocast)
         per_row = torch.empty(count, device=hidden.device, dtype=torch.float32)
         for lo, hi in _spans(count, chunk_size):
-            per_row[lo:hi] = ops.direct.cross_entropy_rows(_logits(rows[lo:hi], weight, dtype), labels[lo:hi],
-                                                           float(count), False)
+            per_row[lo:hi] = ops.direct.cross_entropy_rows_exact(_logits(rows[lo:hi], weight, dtype), labels[lo:hi],
+                                                                 float(count), None, False)
         ctx.save_for_backward(hidden, weight, targets)
         ctx.chunk_size, ctx.dtype = chunk_size, dtype
         return per_row.sum()
@@ -71,18 +90,14 @@ class _ChunkedLinearCrossEntropy(torch.autograd.Function):
         need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         rows, labels = hidden.flatten(0, -2), targets.reshape(-1).contiguous()
         count = labels.numel()
-        scale = float(grad_output)
-        if scale == 0.0:
-            return (torch.zeros_like(hidden) if need_h else None,
-                    torch.zeros_like(weight) if need_w else None, None, None)
-        divisor = float(count) / scale      # folds the incoming gradient into the one rounding
+        scale = grad_output.detach().to(torch.float32).reshape(1)
         grad_rows = torch.empty_like(rows) if need_h else None
         grad_w = torch.zeros(weight.shape, device=weight.device, dtype=torch.float32) if need_w else None
         w = weight.detach().to(ctx.dtype)
         for lo, hi in _spans(count, ctx.chunk_size):
             part = rows[lo:hi].detach().to(ctx.dtype)
             dlogits = _logits(part, w, ctx.dtype)
-            ops.direct.cross_entropy_rows(dlogits, labels[lo:hi], divisor, True)
+            ops.direct.cross_entropy_rows_exact(dlogits, labels[lo:hi], float(count), scale, True)
             dlogits = dlogits.to(ctx.dtype)
             if need_h:
                 grad_rows[lo:hi].copy_(dlogits @ w)

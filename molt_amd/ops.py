@@ -139,8 +139,12 @@ def _workspace(query: str, *args: int) -> int:
 
 
 # Weight descriptors by content: the pointers and geometry they hold. A hit
-# describes the very memory of the tensors passed in (they are alive for the
-# launch), so the cache holds no references to them.
+# describes the very memory of the tensors passed in, so the cache holds no
+# references to them. Callers bind every tensor they pass (including fp32 or
+# contiguous copies made for the call) to a local that lives until the launch
+# has been enqueued: a temporary freed earlier could be handed to a workspace
+# or output allocated before the launch and overwritten by a staging kernel
+# ahead of the GEMM that reads it.
 _DESC: dict = {}
 
 
@@ -292,7 +296,8 @@ def nf4_dequantize(packed: Tensor, scales: Tensor, code: Tensor, rows: int, cols
     packed = _check_packed(packed, rows, cols, what)
     _check_stats(what, rows, cols, block_size, code, scales=scales)
     out = torch.empty((rows, cols), device=dev, dtype=out_dtype)
-    w = _weight(packed, _f32(scales), _f32(code), rows, cols, block_size, order)
+    sc, cd = _f32(scales), _f32(code)
+    w = _weight(packed, sc, cd, rows, cols, block_size, order)
     dt = _lib.DTYPE_F32 if out_dtype == torch.float32 else _lib.DTYPE_BF16
     if out_dtype not in (torch.float32, torch.bfloat16):
         raise CapabilityError(f"{what}: output dtype {out_dtype} unsupported (bf16, fp32)")
@@ -319,8 +324,8 @@ def nf4_dequantize_nested(packed: Tensor, absmax_q: Tensor, absmax2: Tensor, cod
     if out_dtype not in (torch.float32, torch.bfloat16):
         raise CapabilityError(f"{what}: output dtype {out_dtype} unsupported (bf16, fp32)")
     out = torch.empty((rows, cols), device=dev, dtype=out_dtype)
-    w = _weight(packed, None, _f32(code), rows, cols, block_size, order, absmax_q.contiguous(),
-                _f32(absmax2), _f32(code2), offset, dq_block)
+    cd, q, a2, c2 = _f32(code), absmax_q.contiguous(), _f32(absmax2), _f32(code2)
+    w = _weight(packed, None, cd, rows, cols, block_size, order, q, a2, c2, offset, dq_block)
     dt = _lib.DTYPE_F32 if out_dtype == torch.float32 else _lib.DTYPE_BF16
     _call("molt_nf4_dequantize", C.byref(w), out.data_ptr(), dt, _stream(dev))
     return out
@@ -341,9 +346,9 @@ def nf4_resolve_scales(absmax_q: Tensor, absmax2: Tensor, code2: Tensor, offset:
     q = absmax_q.contiguous()
     out = torch.empty(q.numel(), device=dev, dtype=torch.float32)
     # rows*cols only matter through ceil(n / block_size); describe n = nblocks with block 1
-    w = _weight(torch.empty(1, dtype=torch.uint8, device=dev), None,
-                torch.empty(16, device=dev), 1, q.numel(), 1, 1, q, _f32(absmax2), _f32(code2),
-                offset, dq_block)
+    dummy_packed, dummy_code = torch.empty(1, dtype=torch.uint8, device=dev), torch.empty(16, device=dev)
+    a2, c2 = _f32(absmax2), _f32(code2)
+    w = _weight(dummy_packed, None, dummy_code, 1, q.numel(), 1, 1, q, a2, c2, offset, dq_block)
     _call("molt_nf4_resolve_scales", C.byref(w), out.data_ptr(), _stream(dev))
     return out
 
@@ -483,7 +488,8 @@ def nf4_lora_forward(x: Tensor, packed: Tensor, scales: Tensor, code: Tensor, ro
     packed = _check_packed(packed, rows, cols, what)
     _check_stats(what, rows, cols, block_size, code, scales=scales)
     y = torch.empty((x.shape[0], rows), device=dev, dtype=torch.bfloat16)
-    w = _weight(packed, _f32(scales), _f32(code), rows, cols, block_size, order)
+    sc, cd = _f32(scales), _f32(code)
+    w = _weight(packed, sc, cd, rows, cols, block_size, order)
     r = 0
     tt = bb = None
     if t is not None:
@@ -523,9 +529,9 @@ def nf4_gateup_forward(x: Tensor, packed_g: Tensor, scales_g: Tensor, packed_u: 
     pu = _check_packed(packed_u, rows, cols, what)
     _check_stats(what, rows, cols, 64, code, scales=scales_g)
     _check_stats(what, rows, cols, 64, code, scales=scales_u)
-    cd = _f32(code)
-    wg = _weight(pg, _f32(scales_g), cd, rows, cols, 64, order)
-    wu = _weight(pu, _f32(scales_u), cd, rows, cols, 64, order)
+    cd, sc_g, sc_u = _f32(code), _f32(scales_g), _f32(scales_u)
+    wg = _weight(pg, sc_g, cd, rows, cols, 64, order)
+    wu = _weight(pu, sc_u, cd, rows, cols, 64, order)
     m = x.shape[0]
     outs = [torch.empty((m, rows), device=dev, dtype=torch.bfloat16) for _ in range(3)]
     r = 0
@@ -566,7 +572,8 @@ def nf4_lora_backward_input(dy: Tensor, packed: Tensor, scales: Tensor, code: Te
     packed = _check_packed(packed, rows, cols, what)
     _check_stats(what, rows, cols, block_size, code, scales=scales)
     dx = torch.empty((dy.shape[0], cols), device=dev, dtype=torch.bfloat16)
-    w = _weight(packed, _f32(scales), _f32(code), rows, cols, block_size, order)
+    sc, cd = _f32(scales), _f32(code)
+    w = _weight(packed, sc, cd, rows, cols, block_size, order)
     r = 0
     uu = aa = None
     if u is not None:
@@ -608,9 +615,9 @@ def nf4_lora_backward_input_pair(dy0: Tensor, dy1: Tensor, packed0: Tensor, scal
     p1 = _check_packed(packed1, rows, cols, what)
     _check_stats(what, rows, cols, 64, code, scales=scales0)
     _check_stats(what, rows, cols, 64, code, scales=scales1)
-    cd = _f32(code)
-    w0 = _weight(p0, _f32(scales0), cd, rows, cols, 64, order)
-    w1 = _weight(p1, _f32(scales1), cd, rows, cols, 64, order)
+    cd, sc0, sc1 = _f32(code), _f32(scales0), _f32(scales1)
+    w0 = _weight(p0, sc0, cd, rows, cols, 64, order)
+    w1 = _weight(p1, sc1, cd, rows, cols, 64, order)
     m = dy0.shape[0]
     dx = torch.empty((m, cols), device=dev, dtype=torch.bfloat16)
     r = 0
@@ -657,7 +664,8 @@ def nf4_swiglu_backward(dy: Tensor, packed: Tensor, scales: Tensor, code: Tensor
         raise ValueError(f"{what}: gate/up shape must be ({dy.shape[0]}, {cols})")
     packed = _check_packed(packed, rows, cols, what)
     _check_stats(what, rows, cols, 64, code, scales=scales)
-    w = _weight(packed, _f32(scales), _f32(code), rows, cols, 64, order)
+    sc, cd = _f32(scales), _f32(code)
+    w = _weight(packed, sc, cd, rows, cols, 64, order)
     dg = torch.empty_like(gate)
     du = torch.empty_like(up)
     r = 0
@@ -774,9 +782,9 @@ def nf4_gemv(x: Tensor, packed: Tensor, scales: Optional[Tensor], absmax_q: Opti
                  dq_block=dq_block)
     m = x.shape[0]
     nested = absmax_q is not None
-    w = _weight(packed, None if nested else _f32(scales), _f32(code), rows, cols, 64, order,
-                absmax_q.contiguous() if nested else None, _f32(absmax2) if nested else None,
-                _f32(code2) if nested else None, offset, dq_block)
+    sc, cd = None if nested else _f32(scales), _f32(code)
+    q, a2, c2 = (absmax_q.contiguous(), _f32(absmax2), _f32(code2)) if nested else (None, None, None)
+    w = _weight(packed, sc, cd, rows, cols, 64, order, q, a2, c2, offset, dq_block)
     y = torch.empty((m, rows), device=dev, dtype=torch.bfloat16)
     r = 0
     tt = bb = None
@@ -952,4 +960,35 @@ def cross_entropy_rows(logits: Tensor, targets: Tensor, total: float, with_grad:
 
 @cross_entropy_rows.register_fake
 def _(logits, targets, total, with_grad):
+    return logits.new_empty((logits.shape[0],), dtype=torch.float32)
+
+
+@_custom_op(f"{NS}::cross_entropy_rows_exact", mutates_args=("logits",))
+def cross_entropy_rows_exact(logits: Tensor, targets: Tensor, total: float, grad_scale: Optional[Tensor],
+                             with_grad: bool) -> Tensor:
+    """Per-row loss and (with ``with_grad``, in place) gradient under
+    F.cross_entropy's rule: rows whose target lies outside [0, vocab) (the
+    ignored index -100) get a zero loss and a zero gradient, and the gradient
+    is scaled by the device scalar ``grad_scale`` (kernels/partitioned_loss.py:18-103).
+    Targets that are neither valid nor ignored are the caller's to reject."""
+    dev = _require_gpu(logits, targets, grad_scale, what="cross-entropy")
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("cross-entropy: logits must be a row-major [rows, vocab] matrix")
+    if targets.dtype != torch.long or targets.shape != (logits.shape[0],):
+        raise ValueError("cross-entropy: targets must be int64 [rows]")
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise CapabilityError(f"cross-entropy supports bf16 and fp32 logits (got {logits.dtype})")
+    dt = _lib.DTYPE_BF16 if logits.dtype == torch.bfloat16 else _lib.DTYPE_F32
+    gs = None if grad_scale is None else grad_scale.detach().reshape(-1)[:1].to(torch.float32).contiguous()
+    rows, vocab = logits.shape
+    loss = torch.empty(rows, device=dev, dtype=torch.float32)
+    tg = targets.contiguous()
+    _call("molt_cross_entropy_rows_exact", logits.data_ptr(), dt, logits.stride(0), rows, vocab, tg.data_ptr(),
+          float(total), _ptr(gs), loss.data_ptr(), logits.data_ptr() if with_grad else None, logits.stride(0),
+          _stream(dev))
+    return loss
+
+
+@cross_entropy_rows_exact.register_fake
+def _(logits, targets, total, grad_scale, with_grad):
     return logits.new_empty((logits.shape[0],), dtype=torch.float32)

@@ -32,17 +32,22 @@ Pinning (what independently checks each function; see ``tests/test_oracle.py``):
   rounds differently.
 * ``linspace_f32`` / ``dynamic_map`` - bitsandbytes' ``create_dynamic_map``
   (bitsandbytes 0.50.2, a dependency absent from the reference tree and from
-  this image). Pinned against torch's fp32 ``linspace``, the closed form of
-  each entry (2 ulp) and the entry count per decade. Whether bitsandbytes'
-  linspace is fp32 (as restated) or fp64 rounded to fp32 changes 22 entries
-  by 1 ulp: that choice is PARITY UNPINNED. The kernels read the table as
-  data, so it only decides which table the build's quantiser writes.
+  this image). Pinned bit for bit against the published construction run as
+  torch fp32 ops (``torch.linspace`` without a dtype is fp32; the Python-float
+  decade scale multiplies in fp32), with the fp64-scale variant shown to
+  differ; also against torch's fp32 ``linspace``, the closed form of each
+  entry (2 ulp) and the entry count per decade.
 * ``lora_linear_*``, ``swiglu_*``, ``gated_mlp_*`` - fp64 textbook algebra;
   the backward formulas are pinned against torch autograd of the forward
   expression in fp64, and SwiGLU against ``F.silu(g) * u``
   (``tests/kernels/test_gated_activation.py:10-26``).
 * ``lora_linear_forward_bf16_points`` - the reference's autocast rounding
   points, pinned against the same forward run as torch CPU bf16 ops.
+* ``lora_linear_backward_bf16_points`` / ``gated_mlp_reference_bf16`` - the
+  reference's own bf16 step (rounding points of methods/nf4_lora.py:83-109 and
+  methods/gated_replay.py:290-299,372-388), pinned against torch autograd under
+  CPU bf16 autocast of the same graph (>= 99.9 % of elements equal). Used only
+  to report how far the reference path itself lands from the fp64 oracle.
 * ``rmsnorm_forward`` / ``rmsnorm_backward`` - fp64 algebra. The forward is
   pinned by closed forms (a constant row maps to ``sign * (w + offset)`` at
   eps = 0, scale invariance, unit RMS of the normalised row); the backward by
@@ -188,13 +193,14 @@ def dynamic_map(signed: bool = True, max_exponent_bits: int = 7, total_bits: int
     decade i the midpoints of an fp32 ``linspace(0.1, 1, 2**i + 1)``, scaled by
     ``fl32(10**(i - 6))`` in fp32, with both signs, plus 0 and 1, sorted.
 
-    Pinned (tests/test_oracle.py) against torch's own fp32 linspace, the closed
+    Pinned (tests/test_oracle.py) bit for bit against the published
+    construction run as torch fp32 ops (fp32 ``torch.linspace``, fp32
+    midpoints, the Python-float decade scale applied in fp32); an fp64-scale
+    variant differs from it. Also against torch's own fp32 linspace, the closed
     form ``10**(i-6) * (b_j + b_{j+1}) / 2`` with ``b_j = 0.1 + 0.9 j / 2**i``
-    to 2 ulp per entry, and the entry count per decade. Whether bitsandbytes'
-    linspace runs in fp32 (restated here) or in fp64 then rounded changes 22
-    of the 256 entries by 1 ulp; that choice is PARITY UNPINNED (the library
-    is absent). The kernels read the table as data, so it only decides which
-    table this build's quantiser writes."""
+    to 2 ulp per entry, and the entry count per decade. The kernels read the
+    table as data, so it only decides which table this build's quantiser
+    writes."""
     data: list[float] = []
     non_sign_bits = total_bits - 1
     additional = 2 ** (non_sign_bits - max_exponent_bits) - 1
@@ -382,6 +388,50 @@ def lora_linear_forward_bf16_points(x, w, a, b, s):
     lora = bf16_round(low @ b16.T)
     term = bf16_round(lora.astype(np.float32) * np.float32(s))
     return bf16_round(base.astype(np.float32) + term.astype(np.float32))
+
+
+def lora_linear_backward_bf16_points(x, w, a, b, s, dy):
+    """Backward with MOLT's bf16 rounding points under autocast
+    (methods/nf4_lora.py:83-109, the same equations as
+    methods/gated_replay.py:236-253): ``low = bf16(X A^T)``,
+    ``scaled = bf16(dY s)`` (scale before the product), ``through = bf16(scaled B)``,
+    ``base = bf16(dY W)``, ``dX = bf16(base + bf16(through A))``,
+    ``dB = bf16(scaled^T low)``, ``dA = bf16(through^T X)``; dA and dB are then
+    widened to fp32 (``.to(lora_a.dtype)``), so they carry a bf16 rounding.
+    Inner products are fp64 (the library GEMMs accumulate in fp32)."""
+    x, w, dy = _f64(x), _f64(w), _f64(dy)
+    a16, b16 = bf16_round(a).astype(np.float64), bf16_round(b).astype(np.float64)
+    low = bf16_round(x @ a16.T).astype(np.float64)
+    scaled = bf16_round(dy * s).astype(np.float64)
+    through = bf16_round(scaled @ b16).astype(np.float64)
+    base = bf16_round(dy @ w)
+    dx = bf16_round(base + bf16_round(through @ a16))
+    return dx.astype(np.float64), bf16_round(through.T @ x).astype(np.float64), \
+        bf16_round(scaled.T @ low).astype(np.float64)
+
+
+def gated_mlp_reference_bf16(x, wg, wu, wd, ag, bg, au, bu, ad, bd, s, dy):
+    """The reference's own bf16 gated-MLP step, every autocast rounding point
+    kept, for reporting how far MOLT's path itself lands from the fp64 oracle.
+    gate and up come from NF4-LoRA nodes (methods/nf4_lora.py:43-50); the
+    replay node forms ``bf16(bf16(silu(g)) * u)`` (methods/gated_replay.py:290-291,
+    372-374), runs the down projection's bf16 backward, then
+    ``du = bf16(dh * bf16(silu(g)))`` and ``dg = silu_backward(bf16(dh * u), g)``
+    rounded to bf16 (:385-387); autograd adds the gate and up input gradients in
+    bf16. Returns (Y, dX, (dAg, dBg, dAu, dBu, dAd, dBd))."""
+    rnd = lambda v: bf16_round(v).astype(np.float64)  # noqa: E731
+    g = rnd(lora_linear_forward_bf16_points(x, wg, ag, bg, s))
+    u = rnd(lora_linear_forward_bf16_points(x, wu, au, bu, s))
+    act = rnd(g * _sigmoid(g))
+    h = rnd(act * u)
+    y = rnd(lora_linear_forward_bf16_points(h, wd, ad, bd, s))
+    dh, dad, dbd = lora_linear_backward_bf16_points(h, wd, ad, bd, s, dy)
+    du = rnd(dh * act)
+    sg = _sigmoid(g)
+    dg = rnd(rnd(dh * u) * sg * (1.0 + g * (1.0 - sg)))
+    dxg, dag, dbg = lora_linear_backward_bf16_points(x, wg, ag, bg, s, dg)
+    dxu, dau, dbu = lora_linear_backward_bf16_points(x, wu, au, bu, s, du)
+    return y, rnd(dxg + dxu), (dag, dbg, dau, dbu, dad, dbd)
 
 
 # --------------------------------------------------------------------------

@@ -59,8 +59,16 @@ def test_cfg4_sampled_rows_match_oracle_and_runs_repeat_bitwise():
     dyo = bf16_values(dy)[rows]
     ry, saved = O.gated_mlp_forward(xo, ws[0], ws[1], ws[2], *av, s)
     rdx, _ = O.gated_mlp_backward(xo, ws[0], ws[1], ws[2], *av, s, dyo, saved)
-    assert_close_fro(np_f32(first[0])[rows], ry, what="Y rows")
-    assert_close_fro(np_f32(first[1])[rows], rdx, what="dX rows")
+    ey_hip = assert_close_fro(np_f32(first[0])[rows], ry, what="Y rows")
+    edx_hip = assert_close_fro(np_f32(first[1])[rows], rdx, what="dX rows")
+    # the reference's own bf16 step on the same rows (a row of Y and dX depends
+    # only on its own rows of X and dY), reported beside the HIP error
+    masters = [np_f32(t).astype(np.float64) for _, _, a, b in projs for t in (a, b)]
+    ey, edx, _ = O.gated_mlp_reference_bf16(xo, ws[0], ws[1], ws[2], *masters, s, dyo)
+    ey_ref, edx_ref = O.rel_fro(ey, ry), O.rel_fro(edx, rdx)
+    print(f"cfg4 sampled rows, relative Frobenius error vs fp64: Y HIP {ey_hip:.3e} reference-bf16 {ey_ref:.3e}; "
+          f"dX HIP {edx_hip:.3e} reference-bf16 {edx_ref:.3e}", flush=True)
+    assert ey_hip <= 1.5 * ey_ref and edx_hip <= 1.5 * edx_ref
     for g in first[2:]:
         assert torch.isfinite(g).all() and g.abs().sum() > 0
 

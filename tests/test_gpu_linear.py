@@ -76,6 +76,31 @@ def test_scheduled_nf4_lora_tails_and_ranks(width, out_width, rank, tokens):
     assert_close_fro(np_f32(db), rdb, what="dB")
 
 
+@pytest.mark.parametrize("width,out_width", [(1536, 256), (1536, 8960), (8960, 1536)])
+def test_scheduled_error_beside_the_reference_bf16_path(width, out_width):
+    """The HIP linear's relative Frobenius error against the fp64 oracle, printed
+    beside the error of the reference's own autocast step on the same operands
+    (``lora_linear_forward_bf16_points`` / ``lora_linear_backward_bf16_points``,
+    methods/nf4_lora.py:43-50,83-109). The HIP path may not be worse than 1.5x
+    the reference's error on Y, dX, dA or dB."""
+    s = 2.0
+    x, packed, qs, a, b, dy = _problem(width, out_width, 16, 512, 946, weight_std=0.02)
+    got = _run(x, packed, qs, a, b, dy, s)
+    ref = _oracle(x, packed, qs, a, b, dy, s)
+    w = oracle_weight(packed, qs).dequant_bf16().astype(np.float64)
+    xo = bf16_values(x).reshape(-1, width)
+    dyo = bf16_values(dy).reshape(-1, out_width)
+    ao, bo = np_f32(a).astype(np.float64), np_f32(b).astype(np.float64)
+    emul = (O.lora_linear_forward_bf16_points(xo, w, ao, bo, s),) + O.lora_linear_backward_bf16_points(
+        xo, w, ao, bo, s, dyo)
+    print(f"scheduled {width}->{out_width} r=16 M=512: relative Frobenius error vs fp64 (HIP / reference bf16)",
+          flush=True)
+    for name, g, e, o in zip(("Y", "dX", "dA", "dB"), got, emul, ref):
+        eh, ee = O.rel_fro(np_f32(g).reshape(o.shape), o), O.rel_fro(e, o)
+        print(f"  {name:3s} {eh:10.3e} {ee:10.3e}", flush=True)
+        assert eh <= TOL and eh <= 1.5 * ee, f"{name}: HIP {eh:.3e}, reference bf16 {ee:.3e}"
+
+
 def test_cached_backward_weight_is_bitwise_equal_to_per_call_decode():
     """tests/kernels/test_nf4_lora.py:48-79."""
     x, packed, qs, a, b, dy = _problem(1536, 1536, 8, 256, 944)

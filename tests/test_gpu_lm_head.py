@@ -195,3 +195,38 @@ def test_recomputing_backend_matches_unpartitioned_loss_and_both_gradients(chunk
     with pytest.raises(CapabilityError, match="float64"):
         exact_partitioned_linear_cross_entropy(hidden64.detach().cuda(), weight64.detach().cuda(), targets.cuda(),
                                                chunk_size)
+
+
+@pytest.mark.parametrize("grad_scale", [1.0, -0.5])
+def test_recomputing_backend_ignored_targets_and_signed_upstream_gradient(grad_scale):
+    """The exact path follows F.cross_entropy as the reference's exact path
+    calls it (kernels/partitioned_loss.py:43-101: summed over chunks, divided by
+    every token): targets of -100 add nothing to the loss and get a zero
+    gradient, and the upstream gradient may be negative. Against fp64 autograd
+    of that formulation on the CPU, with a trainable head."""
+    torch.manual_seed(19)
+    hidden64 = torch.randn(3, 5, 9, dtype=torch.float64, requires_grad=True)
+    weight64 = torch.randn(13, 9, dtype=torch.float64, requires_grad=True)
+    targets = torch.randint(0, 13, (3, 5))
+    targets[0, 1] = targets[2, 4] = targets[1, 0] = -100
+    ref = F.cross_entropy(F.linear(hidden64, weight64).flatten(0, 1), targets.flatten(), reduction="sum")
+    ref = ref / targets.numel()
+    (ref * grad_scale).backward()
+    hidden = hidden64.detach().float().cuda().requires_grad_()
+    weight = weight64.detach().float().cuda().requires_grad_()
+    loss = exact_partitioned_linear_cross_entropy(hidden, weight, targets.cuda(), 4)
+    (loss * grad_scale).backward()
+    torch.testing.assert_close(loss.double().cpu(), ref.detach(), rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(hidden.grad.double().cpu(), hidden64.grad, rtol=1e-4, atol=1e-6)
+    torch.testing.assert_close(weight.grad.double().cpu(), weight64.grad, rtol=1e-4, atol=1e-6)
+    assert torch.count_nonzero(hidden.grad[0, 1]) == 0 and torch.count_nonzero(hidden.grad[2, 4]) == 0
+
+
+def test_recomputing_backend_rejects_out_of_range_targets():
+    hidden = torch.randn(2, 3, 8, device="cuda", requires_grad=True)
+    weight = torch.randn(5, 8, device="cuda")
+    for bad in (5, -1, -7):
+        targets = torch.zeros(2, 3, dtype=torch.long, device="cuda")
+        targets[1, 2] = bad
+        with pytest.raises(IndexError, match="out of bounds"):
+            exact_partitioned_linear_cross_entropy(hidden, weight, targets, 2)

@@ -61,6 +61,42 @@ def test_fused_gated_mlp_matches_oracle(hidden, inter, r, m):
         assert_close_fro(np_f32(leaf.grad), ref, what=name)
 
 
+@pytest.mark.parametrize("hidden,inter,r,m", [(896, 4864, 16, 1024), (256, 448, 64, 200)])
+def test_fused_gated_mlp_error_beside_the_reference_bf16_path(hidden, inter, r, m):
+    """The HIP path's relative Frobenius error against the fp64 oracle, printed
+    beside the error of the reference's own bf16 step on the same operands
+    (``gated_mlp_reference_bf16``: every autocast rounding point of
+    methods/nf4_lora.py:43-50,83-109 and methods/gated_replay.py:290-299,372-388).
+    The HIP path keeps fp32 through each contraction and its epilogue, so it may
+    not be worse than 1.5x the reference's error on any output or gradient."""
+    s = 2.0
+    projs = [_proj(inter, hidden, r, 90), _proj(inter, hidden, r, 91), _proj(hidden, inter, r, 92)]
+    x = seeded((m, hidden), 93).requires_grad_()
+    dy = seeded((m, hidden), 94)
+    leaves = []
+    for _, _, a, b in projs:
+        leaves += [a.clone().requires_grad_(), b.clone().requires_grad_()]
+    (pg, qg, _, _), (pu, qu, _, _), (pd, qd, _, _) = projs
+    y = fused_gated_nf4_lora_mlp(x, pg, leaves[0], leaves[1], pu, leaves[2], leaves[3], pd, leaves[4], leaves[5],
+                                 qg, qu, qd, s, s, s)
+    y.backward(dy)
+    ry, rdx, rgrads = _oracle_mlp(x, projs, s, dy)
+    ws = [oracle_weight(p, q).dequant_bf16().astype(np.float64) for p, q, _, _ in projs]
+    ab = [np_f32(t).astype(np.float64) for _, _, a, b in projs for t in (a, b)]
+    ey, edx, egrads = O.gated_mlp_reference_bf16(bf16_values(x), *ws, *ab, s, bf16_values(dy))
+    names = ("Y", "dX", "dA_gate", "dB_gate", "dA_up", "dB_up", "dA_down", "dB_down")
+    hip = [np_f32(y), np_f32(x.grad)] + [np_f32(leaf.grad) for leaf in leaves]
+    emul = [ey, edx] + list(egrads)
+    ref = [ry, rdx] + list(rgrads)
+    print(f"gated MLP H={hidden} I={inter} r={r} M={m}: relative Frobenius error vs fp64 oracle", flush=True)
+    print(f"  {'':8s} {'HIP':>10s} {'reference bf16':>15s}", flush=True)
+    for name, h, e, o in zip(names, hip, emul, ref):
+        eh, ee = O.rel_fro(h, o), O.rel_fro(e, o)
+        print(f"  {name:8s} {eh:10.3e} {ee:15.3e}", flush=True)
+        assert eh <= 5e-3, f"{name}: HIP error {eh:.3e} > 5e-3"
+        assert eh <= 1.5 * ee, f"{name}: HIP error {eh:.3e} > 1.5 x the reference path's {ee:.3e}"
+
+
 @pytest.mark.parametrize("hidden,inter,r,m", [(128, 256, 8, 32), (256, 448, 64, 200)])
 def test_fused_gated_mlp_saved_h_equals_replay(hidden, inter, r, m):
     # Keeping h from the forward must give bit-identical gradients to replaying it.

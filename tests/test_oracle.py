@@ -242,6 +242,40 @@ def test_dynamic_map_closed_form():
     assert m[-1] == 1.0 and np.count_nonzero(m == 0.0) == 1 and np.all(np.diff(m) > 0)
 
 
+def _dynamic_map_torch(scale_in_fp64: bool = False) -> np.ndarray:
+    """The published ``create_dynamic_map`` construction (bitsandbytes 0.50.2,
+    signed, 7 exponent bits, 8 bits) written as torch ops on fp32 tensors: per
+    decade an fp32 ``torch.linspace(0.1, 1, 2**i + 1)``, fp32 midpoints, then the
+    decade scale ``10**(i-6)`` as a Python float times the fp32 tensor (torch
+    rounds the scalar to fp32 and multiplies in fp32), both signs, 0 and 1,
+    sorted. ``scale_in_fp64`` is the plausible mistake of scaling in fp64 and
+    rounding once afterwards."""
+    data = []
+    for i in range(7):
+        bounds = torch.linspace(0.1, 1, 2 ** i + 1)
+        assert bounds.dtype == torch.float32
+        means = (bounds[:-1] + bounds[1:]) / 2.0
+        if scale_in_fp64:
+            vals = (10 ** (i - 6) * means.double()).float()
+        else:
+            vals = 10 ** (i - 6) * means
+        assert vals.dtype == torch.float32
+        data += vals.tolist() + (-vals).tolist()
+    data += [0.0, 1.0]
+    return torch.tensor(data, dtype=torch.float32).sort().values.numpy()
+
+
+def test_dynamic_map_bitwise_equals_torch_fp32_construction():
+    """Bit-for-bit pin of the nested statistics' code table (``state2.code``,
+    read by methods/nf4_backward.py:157-160): the oracle's numpy restatement
+    (its own linspace, fp32 scalar scale) equals the construction run as torch
+    fp32 ops, and the fp64-scale variant, which moves entries by an ulp, does not."""
+    ours = O.dynamic_map()
+    assert np.array_equal(ours.view(np.uint32), _dynamic_map_torch().view(np.uint32))
+    variant = _dynamic_map_torch(scale_in_fp64=True)
+    assert np.count_nonzero(variant.view(np.uint32) != ours.view(np.uint32)) > 0
+
+
 def test_product_dynamic_map_is_the_oracle_table():
     import molt_amd
 
@@ -340,6 +374,68 @@ def test_bf16_points_forward_matches_torch_bf16_ops():
     assert np.all(np.abs(ours - ref) <= 2 * ulp)
     no_round = O.lora_linear_forward(x.float().numpy(), w.float().numpy(), a.numpy(), b.numpy(), s)
     assert np.mean(O.bf16_round(no_round) == ref) < 0.9
+
+
+def _autocast_gated_mlp(x, wg, wu, wd, ag, bg, au, bu, ad, bd, s, dy):
+    """The reference's gated-MLP step as a torch autograd graph on the CPU under
+    bf16 autocast: gate and up as ``F.linear(x, W) + F.linear(F.linear(x, A), B) * s``
+    (methods/nf4_lora.py:43-50; the NF4 base as the bf16 dequantised weight),
+    ``h = F.silu(g) * u`` and the down projection likewise
+    (methods/gated_replay.py:290-299). Autograd's own backward (Mul, SiLU, Linear
+    and the autocast casts of the fp32 masters) supplies the rounding points the
+    reference's manual backward reproduces (:341-388); the gate and up input
+    gradients are summed in bf16, as autograd sums the two nodes' outputs."""
+    from torch.nn import functional as F
+
+    leaves = [t.clone().requires_grad_() for t in (ag, bg, au, bu, ad, bd)]
+    xg, xu = x.clone().requires_grad_(), x.clone().requires_grad_()
+
+    def proj(z, w, a, b):
+        return F.linear(z, w) + F.linear(F.linear(z, a), b) * s
+
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        g = proj(xg, wg, leaves[0], leaves[1])
+        u = proj(xu, wu, leaves[2], leaves[3])
+        gd, ud = g.detach().requires_grad_(), u.detach().requires_grad_()
+        y = proj(F.silu(gd) * ud, wd, leaves[4], leaves[5])
+    assert y.dtype == torch.bfloat16
+    y.backward(dy)
+    g.backward(gd.grad)
+    u.backward(ud.grad)
+    return y, xg.grad + xu.grad, [leaf.grad for leaf in leaves]
+
+
+def test_reference_bf16_gated_mlp_matches_torch_autocast_autograd():
+    """``lora_linear_backward_bf16_points`` and ``gated_mlp_reference_bf16`` (the
+    reference's own bf16 rounding points, used by the GPU tests to report the
+    reference path's error beside the HIP path's) against torch's autocast +
+    autograd on the CPU: at least 99.9 % of every output's elements equal (the
+    restatement's inner products are fp64, torch's fp32). Dropping the bf16
+    rounding of dA/dB (the reference widens bf16 products to fp32) fails it."""
+    g = torch.Generator().manual_seed(5)
+    m, hid, inter, r, s = 64, 128, 256, 16, 2.0
+    x = torch.randn(m, hid, generator=g).bfloat16()
+    dy = torch.randn(m, hid, generator=g).bfloat16()
+    wg, wu = ((torch.randn(inter, hid, generator=g) * 0.05).bfloat16() for _ in range(2))
+    wd = (torch.randn(hid, inter, generator=g) * 0.05).bfloat16()
+    ag, au = (torch.randn(r, hid, generator=g) / hid ** 0.5 for _ in range(2))
+    ad = torch.randn(r, inter, generator=g) / inter ** 0.5
+    bg, bu = (torch.randn(inter, r, generator=g) * 0.05 for _ in range(2))
+    bd = torch.randn(hid, r, generator=g) * 0.05
+    ty, tdx, tgrads = _autocast_gated_mlp(x, wg, wu, wd, ag, bg, au, bu, ad, bd, s, dy)
+    f = lambda t: t.detach().float().numpy().astype(np.float64)  # noqa: E731
+    args = [f(t) for t in (x, wg, wu, wd, ag, bg, au, bu, ad, bd)]
+    oy, odx, ograds = O.gated_mlp_reference_bf16(*args, s, f(dy))
+    for name, ours, ref in [("Y", oy, ty), ("dX", odx, tdx)] + list(
+            zip(("dAg", "dBg", "dAu", "dBu", "dAd", "dBd"), ograds, tgrads)):
+        assert np.mean(ours == f(ref)) >= 0.999, name
+    # dA of the down projection without the reference's bf16 rounding
+    xo, wdo, ado, bdo = args[0], args[3], args[8], args[9]
+    gg = O.bf16_round(O.lora_linear_forward_bf16_points(xo, args[1], args[4], args[5], s)).astype(np.float64)
+    uu = O.bf16_round(O.lora_linear_forward_bf16_points(xo, args[2], args[6], args[7], s)).astype(np.float64)
+    hh = O.bf16_round(O.bf16_round(gg / (1 + np.exp(-gg))) * uu).astype(np.float64)
+    _, dad_unrounded, _ = O.lora_linear_backward(hh, wdo, O.bf16_round(ado), O.bf16_round(bdo), s, f(dy))
+    assert np.mean(dad_unrounded == f(tgrads[4])) < 0.5
 
 
 # --------------------------------------------------------------- RMSNorm
