@@ -67,17 +67,21 @@ def _targets(model: nn.Module, target_modules: str | Iterable[str]) -> list[tupl
 
 def quantize_linears_nf4(model: nn.Module, target_modules: str | Iterable[str] = "all-linear", *,
                          device: torch.device | str = "cuda", blocksize: int = 64,
-                         compress_statistics: bool = True) -> int:
-    """Replace each selected bias-free ``nn.Linear`` with a frozen
-    :class:`NF4Linear` quantised on ``device``, one module at a time so that
-    only one dense weight is on the GPU at once. Returns the number replaced."""
+                         compress_statistics: bool = True, bias_dtype: torch.dtype | None = None) -> int:
+    """Replace each selected ``nn.Linear`` with a frozen :class:`NF4Linear`
+    quantised on ``device``, one module at a time so that only one dense weight
+    is on the GPU at once. A bias stays unquantised and frozen, on ``device`` in
+    ``bias_dtype`` (the linear's own dtype when None), as bitsandbytes'
+    ``Linear4bit`` keeps it (Qwen2's q/k/v projections carry one). Returns the
+    number replaced."""
     count = 0
     for parent, attr, lin, name in _targets(model, target_modules):
-        if lin.bias is not None:
-            raise CapabilityError(f"{name}: NF4 QLoRA projections must be bias-free")
         dense = lin.weight.detach().to(device=device, dtype=torch.float32)
+        bias = None
+        if lin.bias is not None:
+            bias = lin.bias.detach().to(device=device, dtype=bias_dtype or lin.bias.dtype)
         setattr(parent, attr, NF4Linear.from_dense(dense, blocksize=blocksize,
-                                                   compress_statistics=compress_statistics))
+                                                   compress_statistics=compress_statistics, bias=bias))
         del dense
         count += 1
     if not count:
@@ -109,7 +113,7 @@ def prepare_nf4_qlora(model: nn.Module, r: int, lora_alpha: float,
     output head) and add LoRA adapters with fp32 masters. Returns the model."""
     for p in model.parameters():
         p.requires_grad_(False)
-    quantize_linears_nf4(model, target_modules, device=device)
+    quantize_linears_nf4(model, target_modules, device=device, bias_dtype=dtype)
     for module in model.modules():
         if isinstance(module, (NF4Linear, NF4LoRALinear)):
             continue
@@ -186,8 +190,11 @@ def load_prequantized_nf4(model: nn.Module, state: dict[str, torch.Tensor], *,
                           device: torch.device | str = "cuda") -> int:
     """Replace each ``nn.Linear`` whose ``<prefix>.weight`` carries a
     bitsandbytes NF4 quant state in ``state`` with an :class:`NF4Linear` holding
-    those bytes and statistics on ``device``. Returns the number replaced;
-    the other entries are left for ``model.load_state_dict(strict=False)``."""
+    those bytes and statistics on ``device``, and its bias: ``<prefix>.bias``
+    from ``state`` when present, else the module's own (a module with a bias
+    keeps one; a checkpoint bias for a bias-free module is an error). Returns
+    the number replaced; the other entries are left for
+    ``model.load_state_dict(strict=False)``."""
     count = 0
     for parent_name, parent in list(model.named_modules()):
         for attr, child in list(parent.named_children()):
@@ -202,6 +209,15 @@ def load_prequantized_nf4(model: nn.Module, state: dict[str, torch.Tensor], *,
             packed = state[key].to(device=device, dtype=torch.uint8).reshape(-1, 1)
             if packed.numel() != (out_f * in_f + 1) // 2:
                 raise ValueError(f"{key}: {packed.numel()} packed bytes for a {out_f}x{in_f} weight")
-            setattr(parent, attr, NF4Linear(packed, qs))
+            bias_key = key[:-len("weight")] + "bias"
+            own_bias = child.bias
+            if bias_key in state:
+                if own_bias is None and isinstance(child, nn.Linear):
+                    raise ValueError(f"{bias_key}: the checkpoint has a bias but the module is bias-free")
+                dtype = own_bias.dtype if own_bias is not None else state[bias_key].dtype
+                bias = state[bias_key].to(device=device, dtype=dtype)
+            else:
+                bias = None if own_bias is None else own_bias.detach().to(device)
+            setattr(parent, attr, NF4Linear(packed, qs, bias))
             count += 1
     return count

@@ -11,6 +11,11 @@ kernels (libmolt_amd.so):
   methods/nf4_lora.py:87-90), ``dX = dY deq(W) + U bf16(A)`` in one NF4-fused
   GEMM, and the adapter gradients ``dA = U^T X``, ``dB = s dY^T T`` as
   deterministic split-M reductions returned in fp32.
+
+A biased base (Qwen2's q/k/v) adds its bias to the bf16 GEMM output, as the
+base linear's own ``F.linear(x, W, bias)`` would before the LoRA term; the
+reference's patcher instead falls back to PEFT's forward for such a base
+(methods/nf4_lora.py:154). A trainable bias gets ``dY`` summed over tokens.
 """
 from __future__ import annotations
 
@@ -35,7 +40,7 @@ class _ScheduledNF4LoRA(torch.autograd.Function):
     @staticmethod
     def forward(ctx: Any, x: torch.Tensor, packed_weight: torch.Tensor, lora_a: torch.Tensor,
                 lora_b: torch.Tensor, quant_state: Any, scaling: float,
-                decoded_backward_weight: torch.Tensor | None) -> torch.Tensor:
+                decoded_backward_weight: torch.Tensor | None, bias: torch.Tensor | None = None) -> torch.Tensor:
         if x.device.type != "cuda" or packed_weight.device.type != "cuda":
             raise CapabilityError("scheduled NF4-LoRA requires CUDA tensors")
         if packed_weight.requires_grad:
@@ -47,6 +52,8 @@ class _ScheduledNF4LoRA(torch.autograd.Function):
         n, k = _geometry(quant_state)
         if x.shape[-1] != k:
             raise ValueError(f"input width {x.shape[-1]} does not match in_features {k}")
+        if bias is not None and (bias.shape != (n,) or bias.device != x.device):
+            raise ValueError(f"bias must be a ({n},) tensor on {x.device}, got {tuple(bias.shape)} on {bias.device}")
         if decoded_backward_weight is not None and (
             decoded_backward_weight.shape != (lora_b.shape[0], x.shape[-1])
             or decoded_backward_weight.device != x.device
@@ -65,6 +72,8 @@ class _ScheduledNF4LoRA(torch.autograd.Function):
             result = ops.direct.nf4_lora_forward(
                 flat_x, packed_weight.reshape(-1), resolved_nf4_scales(quant_state), quant_state.code, n, k,
                 nibble_order(quant_state), int(quant_state.blocksize), low_rank, lora_b, float(scaling))
+        if bias is not None:
+            result.add_(bias.to(result.dtype))
         ctx.quant_state = quant_state
         ctx.scaling = float(scaling)
         ctx.input_shape = x.shape
@@ -88,8 +97,9 @@ class _ScheduledNF4LoRA(torch.autograd.Function):
                                              nibble_order(qs), int(qs.blocksize), grad_through_b, lora_a, 1.0)
         grad_a = ops.direct.lora_grad(flat_x, None, 0, grad_through_b, 1.0, 1)
         grad_b = ops.direct.lora_grad(flat_grad, None, 0, low_rank, ctx.scaling, 0)
+        grad_bias = flat_grad.float().sum(0) if ctx.needs_input_grad[7] else None
         return (grad_x.reshape(ctx.input_shape), None, grad_a.to(lora_a.dtype), grad_b.to(lora_b.dtype),
-                None, None, None)
+                None, None, None, grad_bias)
 
 
 def scheduled_nf4_lora(
@@ -100,10 +110,13 @@ def scheduled_nf4_lora(
     quant_state: Any,
     scaling: float,
     decoded_backward_weight: torch.Tensor | None = None,
+    *,
+    bias: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """methods/nf4_lora.py:116-133."""
+    """methods/nf4_lora.py:116-133, plus an optional base ``bias`` (keyword
+    only, so the reference's positional signature is unchanged)."""
     return _ScheduledNF4LoRA.apply(x, packed_weight, lora_a, lora_b, quant_state, scaling,
-                                   decoded_backward_weight)
+                                   decoded_backward_weight, bias)
 
 
 def _scheduled_forward(module: torch.nn.Module, x: torch.Tensor, *args: Any, **kwargs: Any) -> torch.Tensor:
@@ -111,11 +124,12 @@ def _scheduled_forward(module: torch.nn.Module, x: torch.Tensor, *args: Any, **k
     the adapter allow it, else the projection's own forward (the strict
     fallback of methods/nf4_lora.py:136-165)."""
     why = refusal(x, args, kwargs)
-    operands = lora_operands(module) if why is None else why
+    operands = lora_operands(module, allow_bias=True) if why is None else why
     if isinstance(operands, str):
         return original_forward(module)(x, *args, **kwargs)
     return scheduled_nf4_lora(x, operands.packed, operands.lora_a, operands.lora_b, operands.quant_state,
-                              operands.scaling, getattr(module, "_molt_decoded_backward_weight", None))
+                              operands.scaling, getattr(module, "_molt_decoded_backward_weight", None),
+                              bias=operands.bias)
 
 
 def nf4_lora_module_types() -> tuple[type, ...]:

@@ -23,29 +23,38 @@ from .nf4 import QuantState, dequantize_4bit, gemv_applies, nf4_gemv_linear, qua
 
 
 class NF4Linear(nn.Module):
-    """Frozen NF4 base projection (the ``base_layer`` of a LoRA adapter)."""
+    """Frozen NF4 base projection (the ``base_layer`` of a LoRA adapter), with
+    an optional frozen bias (bitsandbytes' ``Linear4bit`` keeps the linear's
+    bias unquantised; Qwen2's q/k/v projections carry one)."""
 
-    def __init__(self, packed: torch.Tensor, quant_state: QuantState) -> None:
+    def __init__(self, packed: torch.Tensor, quant_state: QuantState, bias: torch.Tensor | None = None) -> None:
         super().__init__()
         self.weight = nn.Parameter(packed, requires_grad=False)
         self.weight.quant_state = quant_state
-        self.bias = None
         self.out_features, self.in_features = int(quant_state.shape[0]), int(quant_state.shape[1])
+        if bias is not None and tuple(bias.shape) != (self.out_features,):
+            raise ValueError(f"bias shape {tuple(bias.shape)} does not match out_features {self.out_features}")
+        self.bias = None if bias is None else nn.Parameter(bias.detach(), requires_grad=False)
 
     @classmethod
-    def from_dense(cls, dense: torch.Tensor, blocksize: int = 64, compress_statistics: bool = True) -> "NF4Linear":
+    def from_dense(cls, dense: torch.Tensor, blocksize: int = 64, compress_statistics: bool = True,
+                   bias: torch.Tensor | None = None) -> "NF4Linear":
         packed, qs = quantize_4bit(dense, blocksize=blocksize, compress_statistics=compress_statistics)
-        return cls(packed, qs)
+        return cls(packed, qs, bias)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         qs = self.weight.quant_state
-        if not (torch.is_grad_enabled() and x.requires_grad) and x.device.type == "cuda":
+        bias_grad = self.bias is not None and self.bias.requires_grad
+        if not (torch.is_grad_enabled() and (x.requires_grad or bias_grad)) and x.device.type == "cuda":
             flat = x.reshape(-1, self.in_features)
             if gemv_applies(flat, qs):
                 # decode (1..16 tokens, no autograd): stream the packed weight once
-                return nf4_gemv_linear(flat, self.weight, qs).reshape(*x.shape[:-1], self.out_features)
+                y = nf4_gemv_linear(flat, self.weight, qs)
+                if self.bias is not None:
+                    y = y + self.bias.to(y.dtype)
+                return y.reshape(*x.shape[:-1], self.out_features)
         dense = dequantize_4bit(self.weight.data, qs).to(x.dtype)
-        return F.linear(x, dense)
+        return F.linear(x, dense, None if self.bias is None else self.bias.to(x.dtype))
 
 
 class NF4LoRALinear(nn.Module):

@@ -9,14 +9,16 @@ patched module from an unpatched one. :func:`swap_forward` and
 
 Whether a patched NF4-LoRA projection may run the HIP kernels on a given call
 is decided by two ordered rule tables: :data:`ADAPTER_STRUCTURE` (what the
-module is: one LoRA adapter without DoRA, dropout or a variant, over a
-bias-free NF4 base) and :data:`ADAPTER_STATE` plus :data:`CALL_RULES` (what
-the call is: adapters enabled and unmerged, a bf16 input under bf16 CUDA
-autocast, no extra arguments). The first rule that fails names the reason the
-original forward runs instead, and :func:`refusal` returns it, so a caller can
-see why a module stayed on the original path. The conditions are those the
-reference's patchers check (methods/nf4_lora.py:136-165;
-methods/gated_replay.py:460-520).
+module is: one LoRA adapter without DoRA, dropout or a variant, over an NF4
+base that, for the gated-MLP nodes, has no bias) and :data:`ADAPTER_STATE`
+plus :data:`CALL_RULES` (what the call is: adapters enabled and unmerged, a
+bf16 input under bf16 CUDA autocast, no extra arguments). The first rule that
+fails names the reason the original forward runs instead, and :func:`refusal`
+returns it, so a caller can see why a module stayed on the original path. The
+conditions are those the reference's patchers check (methods/nf4_lora.py:136-165;
+methods/gated_replay.py:460-520), except that the scheduled projection also
+runs a biased base (Qwen2's q/k/v): its autograd node adds the bias after the
+NF4 GEMM, where the reference falls back to PEFT's forward.
 """
 from __future__ import annotations
 
@@ -53,12 +55,13 @@ def original_forward(module: nn.Module, key: str = ORIGINAL_FORWARD) -> Callable
 class LoraOperands:
     """What the kernels read from one NF4 projection with a single active
     LoRA adapter: the packed base weight and its quant state, the fp32 LoRA
-    masters and the adapter's scale."""
+    masters, the adapter's scale and the base's bias (None for most)."""
     packed: torch.Tensor
     lora_a: torch.Tensor
     lora_b: torch.Tensor
     quant_state: Any
     scaling: float
+    bias: torch.Tensor | None = None
 
 
 def _single_adapter(module: nn.Module) -> str | None:
@@ -74,8 +77,10 @@ ADAPTER_STRUCTURE: tuple[tuple[str, Callable[[nn.Module, Any], bool]], ...] = (
     ("the adapter is a LoRA variant", lambda m, a: a not in m.lora_variant),
     ("the adapter uses DoRA", lambda m, a: not m.use_dora.get(a, False)),
     ("the adapter applies dropout", lambda m, a: isinstance(m.lora_dropout[a], nn.Identity)),
-    ("the NF4 base projection has a bias", lambda m, a: m.base_layer.bias is None),
 )
+
+# The gated-MLP nodes have no bias term; only the scheduled projection takes one.
+BIAS_RULE = ("the NF4 base projection has a bias", lambda m, a: getattr(m.base_layer, "bias", None) is None)
 
 ADAPTER_STATE: tuple[tuple[str, Callable[[nn.Module, Any], bool]], ...] = (
     ("adapters are disabled", lambda m, a: not m.disable_adapters),
@@ -97,18 +102,19 @@ CALL_RULES: tuple[tuple[str, Callable[[torch.Tensor, tuple, dict], bool]], ...] 
 GRAD_RULE = ("autograd is disabled", lambda x, args, kwargs: torch.is_grad_enabled())
 
 
-def lora_operands(module: nn.Module, *, check_state: bool = True) -> LoraOperands | str:
+def lora_operands(module: nn.Module, *, check_state: bool = True, allow_bias: bool = False) -> LoraOperands | str:
     """The operands of ``module``'s active adapter, or the reason it has none
     the kernels can use. ``check_state=False`` applies only the structural
-    rules (what a patcher checks once, at patch time)."""
+    rules (what a patcher checks once, at patch time); ``allow_bias`` accepts a
+    biased base (the scheduled projection adds it)."""
     name = _single_adapter(module)
-    rules = ADAPTER_STRUCTURE + (ADAPTER_STATE if check_state else ())
+    rules = ADAPTER_STRUCTURE + (() if allow_bias else (BIAS_RULE,)) + (ADAPTER_STATE if check_state else ())
     for reason, ok in rules:
         if not ok(module, name):
             return reason
     base = module.base_layer
     return LoraOperands(base.weight, module.lora_A[name].weight, module.lora_B[name].weight,
-                        base.weight.quant_state, float(module.scaling[name]))
+                        base.weight.quant_state, float(module.scaling[name]), getattr(base, "bias", None))
 
 
 def refusal(x: torch.Tensor, args: tuple = (), kwargs: dict | None = None, *, need_grad: bool = False) -> str | None:
