@@ -73,11 +73,18 @@ def mlp_step(projs, x, dy, s):
     y.backward(dy)
 
 
-def gemv_sweep(dev, reps: int = 20):
+GEMV_CFG5 = ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336))
+# Qwen2.5-1.5B decode shapes (the reference's generate_qlora, training/qlora.py:1332-1358):
+# q/o 1536 x 1536, k/v 256 x 1536, gate/up 8960 x 1536, down 1536 x 8960
+GEMV_QWEN = ((1536, 1536), (256, 1536), (8960, 1536), (1536, 8960))
+
+
+def gemv_sweep(dev, reps: int = 20, shapes=GEMV_CFG5 + GEMV_QWEN):
     """cfg5: NF4 GEMV at Llama-3-8B projection shapes, M in {1..16}, r=16 LoRA
-    add-on. Each launch reads a different copy of the weight (>= 512 MiB of
-    distinct copies per shape, beyond the 256 MB Infinity Cache); launches
-    are captured in a HIP graph so host launch cost is not timed."""
+    add-on, plus the Qwen2.5-1.5B decode shapes as extra rows. Each launch
+    reads a different copy of the weight (>= 512 MiB of distinct copies per
+    shape, beyond the 256 MB Infinity Cache); launches are captured in a HIP
+    graph so host launch cost is not timed."""
     import ctypes
     import torch
     import molt_amd
@@ -86,7 +93,7 @@ def gemv_sweep(dev, reps: int = 20):
     lib = _lib.load()
     out = []
     g = torch.Generator(device="cpu").manual_seed(5)
-    for n, k in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)):
+    for n, k in shapes:
         w = (torch.randn(n, k, generator=g) * 0.02).to(dev)
         packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True)
         del w
@@ -135,7 +142,8 @@ def gemv_sweep(dev, reps: int = 20):
             alg = n * k * NF4_BYTES_PER_ELEM + m * k * 2 + m * n * 2 + r * (k + n) * 2
             gbs = alg / (us * 1e-6) / 1e9
             out.append({"N": n, "K": k, "M": m, "us": round(us, 3), "GB_s": round(gbs, 1),
-                        "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)})
+                        "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                        "set": "cfg5" if (n, k) in GEMV_CFG5 else "qwen2.5-1.5b"})
             log(f"gemv N={n} K={k} M={m}: {us:.2f} us/launch, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}%)")
             del graph
         del packs, qcopies, descs
@@ -774,7 +782,7 @@ def main() -> int:
     if not args.no_gemv:
         sweep = gemv_sweep(dev)
         result["gemv"] = sweep
-        result["gemv_best_frac_hbm"] = max(e["frac_hbm"] for e in sweep)
+        result["gemv_best_frac_hbm"] = max(e["frac_hbm"] for e in sweep if e["set"] == "cfg5")
     if not args.no_cpu:
         result["cfg1_gpu"] = cfg1_gpu(dev)
         log("cpu baseline (cfg1, oracle restatement, numpy fp32)")

@@ -299,9 +299,10 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(4))) void
 // the replicated LDS table of bf16 code pairs and meet X (staged once per
 // workgroup in LDS) through v_dot2_f32_bf16; the block scale multiplies each
 // lane's half-block sum, lane j < r adds T[j] bf16(s B[n, j]), and the 64
-// lanes of a row are summed by butterfly shuffles. MX rows of X (the tokens,
+// lanes of a row are summed by DPP row reductions and scalar reads. MX rows of X (the tokens,
 // M <= MX; rows past M repeat row M - 1 and are not stored) share each code
-// lookup, one dot2 per token. Requires K % 2048 == 0.
+// lookup, one dot2 per token. K is any multiple of 64 up to 7 x 2048: the last
+// piece of a row may be partial (its lanes past the row end are masked).
 constexpr int GD_WAVES = 8;
 constexpr int GD_NT = 64 * GD_WAVES;
 constexpr int GD_XPAD = 8;                // bf16 elements of X row padding
@@ -347,8 +348,12 @@ MOLT_DEV void gd_load(GdRound<RW, IPR>& R, const GemvParams& p, int64_t n0, int 
 #pragma unroll
     for (int i = 0; i < IPR; ++i) {
       const int j = r * IPR + i;
-      R.w[j] = *reinterpret_cast<const u32x4_t*>(p.packed + (uint32_t)(n * (p.K >> 1) + 1024 * i + 16 * lane));
-      const uint32_t blk = (uint32_t)(n * KB + 32 * i + (lane >> 1));
+      // the last piece may end inside the row: its lanes past the end re-read
+      // the row's last 16 bytes and block (their products are dropped)
+      const int wo = i + 1 < IPR ? 1024 * i + 16 * lane : min(1024 * i + 16 * lane, (p.K >> 1) - 16);
+      const int bo = i + 1 < IPR ? 32 * i + (lane >> 1) : min(32 * i + (lane >> 1), KB - 1);
+      R.w[j] = *reinterpret_cast<const u32x4_t*>(p.packed + (uint32_t)(n * (p.K >> 1) + wo));
+      const uint32_t blk = (uint32_t)(n * KB + bo);
       if constexpr (NESTED) {
         R.q[j] = p.q[blk];
         R.s[j] = p.absmax2[blk >> p.dq_shift];
@@ -368,6 +373,23 @@ MOLT_DEV void gd_load(GdRound<RW, IPR>& R, const GemvParams& p, int64_t n0, int 
       }
     }
   }
+}
+
+// Sum over the 64 lanes of a wave with no LDS traffic (a shuffle becomes an
+// LDS permute whose wait also drains the round's outstanding table lookups):
+// DPP within each row of 16 lanes (swap neighbours, swap pairs, half-row
+// mirror, row mirror), then the four row sums read into scalars and added in
+// row order. The result is wave-uniform.
+MOLT_DEV float gd_wave_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  const int iv = __builtin_bit_cast(int, v);
+  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16))) +
+         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48)));
 }
 
 // Dot products of one round; returns the value lane r * MX + m stores (row r
@@ -420,29 +442,26 @@ MOLT_DEV float gd_compute(const GdRound<RW, IPR>& R, const GemvParams& p, const 
         }
       }
     }
+    // lanes past the end of a row in its last piece contribute nothing
+    const bool live = i + 1 < IPR || 1024 * i + 16 * lane < (p.K >> 1);
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
       const float sc = gv_scale(p, code2s, R.q[r * IPR + i], R.s[r * IPR + i]);
 #pragma unroll
       for (int m = 0; m < MX; ++m) {
-        acc[r][m] += sc * bs[r][m];
+        acc[r][m] += live ? sc * bs[r][m] : 0.0f;
         asm volatile("" : "+v"(acc[r][m]));                           // keeps each piece's lookups short-lived
       }
     }
     __builtin_amdgcn_sched_barrier(0);
   }
-  // LoRA partials join the row sums; butterfly sum over the wave; lane
+  // LoRA partials join the row sums; sum over the wave (gd_wave_sum); lane
   // r * MX + m stores row r of token m
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
     const float b0 = round_bf16(p.s * R.lb[r][0]), b1 = round_bf16(p.s * R.lb[r][1]);
 #pragma unroll
-    for (int m = 0; m < MX; ++m) {
-      float v = acc[r][m] + (lt[m][0] * b0 + lt[m][1] * b1);
-#pragma unroll
-      for (int sh = 32; sh >= 1; sh >>= 1) v += __shfl_xor(v, sh);
-      acc[r][m] = v;
-    }
+    for (int m = 0; m < MX; ++m) acc[r][m] = gd_wave_sum(acc[r][m] + (lt[m][0] * b0 + lt[m][1] * b1));
   }
   float v = acc[0][0];
 #pragma unroll
@@ -472,7 +491,7 @@ MOLT_DEV void gd_store(const GemvParams& p, float v, int64_t n0, int lane) {
 // the compiler's waits count exactly the later loads still in flight. MAXR = 0:
 // any number of rounds, loaded two ahead in three rotating register sets.
 template <int RW, int IPR, int MX, bool NESTED, bool LORA, int MAXR>
-__global__ __launch_bounds__(GD_NT) __attribute__((amdgpu_waves_per_eu(IPR == 2 && MX <= 2 ? 4 : 1)))
+__global__ __launch_bounds__(GD_NT) __attribute__((amdgpu_waves_per_eu(IPR <= 2 && MX <= 2 ? 4 : 1)))
 void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
   constexpr bool PERM = gd_perm<IPR, MX>();
   constexpr int TS = PERM ? 64 : GV_TABW;
@@ -495,19 +514,23 @@ void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
   // registers, read straight from memory; otherwise X is staged in LDS.
   constexpr bool XREG = IPR == 2 && MX == 1;
   constexpr int XCH = IPR * 256, XIT = XREG ? 0 : (MX * XCH + GD_NT - 1) / GD_NT;   // 16-byte chunks of X
-  const int xstride = p.K + GD_XPAD;
+  // X rows in LDS take whole pieces (IPR x 2048 elements); chunks past the end
+  // of a row (a partial last piece) re-read its last chunk, whose products
+  // the compute drops
+  const int xstride = IPR * 2048 + GD_XPAD;
+  const int xlast = (p.K >> 3) - 1;                                   // last 16-byte chunk of a row
   u32x4_t xr[XIT > 0 ? XIT : 1];
   u32x4_t xg[XREG ? 4 * IPR : 1];
   if constexpr (XREG) {
 #pragma unroll
     for (int c = 0; c < 4 * IPR; ++c)
-      xg[c] = *reinterpret_cast<const u32x4_t*>(p.x + 8 * (256 * (c >> 2) + 4 * lane + (c & 3)));
+      xg[c] = *reinterpret_cast<const u32x4_t*>(p.x + 8 * min(256 * (c >> 2) + 4 * lane + (c & 3), xlast));
   }
 #pragma unroll
   for (int it = 0; it < XIT; ++it) {
     const int c = tid + it * GD_NT < MX * XCH ? tid + it * GD_NT : MX * XCH - 1;
     const int m = c / XCH < p.M ? c / XCH : p.M - 1;
-    xr[it] = *reinterpret_cast<const u32x4_t*>(p.x + m * p.ldx + 8 * (c % XCH));
+    xr[it] = *reinterpret_cast<const u32x4_t*>(p.x + m * p.ldx + 8 * min(c % XCH, xlast));
   }
   // unconditional loads here too (clamped, then masked): see gd_load
   float c2 = 0.0f;
@@ -887,19 +910,28 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
   // and 4 with four. It serves M <= 2, and M = 3, 4 where it measured faster
   // than the MFMA kernel (K = 14336, or at most 2048 rows); the
   // MOLT_TUNE_GEMV_DOT_M setting (0..4) replaces that rule by a plain bound on M.
+  // Any K (a multiple of 64, at most 7 pieces of 2048): a row is IPR pieces of
+  // 1 KB, the last possibly partial; IPR is rounded up to an instantiated
+  // value (a wholly idle piece re-reads the row's last bytes and is dropped).
+  // Where the MFMA kernel does not take K (not 8, or a multiple of 7 or 8,
+  // chunks of 512), the dot kernel also serves M = 3, 4.
+  int gm_nw_probe = 8;
+  const bool gm_takes_k = gm_slices(4, w->cols, gm_nw_probe) > 0;
   const int dot_max_m = (int)molt::tuning_value(MOLT_TUNE_GEMV_DOT_M);
-  const bool dot_m = dot_max_m >= 0 ? M <= dot_max_m : (M <= 2 || (M <= 4 && (w->cols == 14336 || w->rows <= 2048)));
-  if (dot_m && (w->cols == 4096 || w->cols == 14336) && aligned(w->packed, 16)) {
-    const int ipr = (int)(w->cols / 2048);
+  const bool dot_m = dot_max_m >= 0 ? M <= dot_max_m
+                                    : (M <= 2 || (M <= 4 && (w->cols == 14336 || w->rows <= 2048 || !gm_takes_k)));
+  const int ipr_need = (int)ceil_div64(w->cols, 2048);
+  if (dot_m && ipr_need <= 7 && aligned(w->packed, 16)) {
+    const int ipr = ipr_need <= 3 ? ipr_need : (ipr_need <= 5 ? 5 : 7);
     const int cus = molt::device_cus();
     const int rw = 1;                                         // rows per wave per round
     const int mx = M == 1 ? 1 : (M == 2 ? 2 : 4);             // X rows held by the kernel
     // two workgroups per CU only where the kernel fits in 128 registers
-    const int per_cu = ipr == 2 && mx <= 2 ? 2 : 1;
+    const int per_cu = ipr <= 2 && mx <= 2 ? 2 : 1;
     const int64_t waves = std::min<int64_t>(ceil_div64(w->rows, rw), (int64_t)cus * GD_WAVES * per_cu);
     const int64_t wgs = ceil_div64(waves, GD_WAVES);
     const int rounds = (int)ceil_div64(w->rows, wgs * GD_WAVES * rw);
-    const size_t dyn = ipr == 2 && mx == 1 ? 0 : (size_t)mx * (w->cols + GD_XPAD) * 2;   // X in registers
+    const size_t dyn = ipr == 2 && mx == 1 ? 0 : (size_t)mx * (ipr * 2048 + GD_XPAD) * 2;   // X in registers
 #define MOLT_GDK(IPRv, MXv, NE, LO, MR) \
   hipLaunchKernelGGL((nf4_gemv_dot_kernel<1, IPRv, MXv, NE, LO, MR>), dim3((unsigned)wgs), dim3(GD_NT), dyn, st, p, \
                      rounds)
@@ -915,11 +947,16 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
     else if (nested) { if (r > 0) MOLT_GDK(IPRv, MXv, true, true, 0); else MOLT_GDK(IPRv, MXv, true, false, 0); } \
     else { if (r > 0) MOLT_GDK(IPRv, MXv, false, true, 0); else MOLT_GDK(IPRv, MXv, false, false, 0); }     \
   } while (0)
-    if (ipr == 2) {
-      if (mx == 1) MOLT_GD(2, 1); else if (mx == 2) MOLT_GD(2, 2); else MOLT_GD(2, 4);
-    } else {
-      if (mx == 1) MOLT_GD(7, 1); else if (mx == 2) MOLT_GD(7, 2); else MOLT_GD(7, 4);
+#define MOLT_GDI(IPRv) \
+  do { if (mx == 1) MOLT_GD(IPRv, 1); else if (mx == 2) MOLT_GD(IPRv, 2); else MOLT_GD(IPRv, 4); } while (0)
+    switch (ipr) {
+      case 1: MOLT_GDI(1); break;
+      case 2: MOLT_GDI(2); break;
+      case 3: MOLT_GDI(3); break;
+      case 5: MOLT_GDI(5); break;
+      default: MOLT_GDI(7); break;
     }
+#undef MOLT_GDI
 #undef MOLT_GD
 #undef MOLT_GDS
 #undef MOLT_GDK

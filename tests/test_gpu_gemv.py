@@ -225,3 +225,28 @@ def test_patched_module_decode_runs_the_gemv(m):
     finally:
         ops.probe_events("molt_nf4_gemv", False)
     assert_close_fro(np_f32(base).reshape(m, -1), bf16_values(x).reshape(m, -1) @ wo.T, what="base decode")
+
+
+@pytest.mark.parametrize("n,k", [(1536, 1536), (256, 1536), (8960, 1536), (1536, 8960), (4864, 896), (896, 4864),
+                                 (520, 2112), (300, 8192), (130, 6144), (70, 10240)])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+def test_gemv_any_k_matches_oracle_and_repeats(n, k, m):
+    """K outside {4096, 14336}: the Qwen2.5-1.5B decode shapes of the reference's
+    generate_qlora (training/qlora.py:1332-1358) and pieces that end inside a
+    row (2112, 896), an instantiated piece count above the row's (8192 -> 5
+    pieces, 10240 -> 5), with the r = 16 LoRA add-on and both nibble orders:
+    against the fp64 oracle, and two calls bitwise equal."""
+    print(f"gemv any-k n={n} k={k} m={m}", flush=True)
+    r, s, order = 16, 2.0, (n + m) % 2
+    w = seeded((n, k), 900 + n + k, std=0.02, dtype=torch.float32)
+    packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True, nibble_order=order)
+    x = seeded((m, k), 901 + m)
+    a = uniform((r, k), 902, 1.0 / np.sqrt(k))
+    b = seeded((n, r), 903, std=0.01, dtype=torch.float32)
+    t = ops.lora_project(x, None, 0, 1.0, a, 0)
+    y1, y2 = _gemv(x, packed, qs, t, b, s), _gemv(x, packed, qs, t, b, s)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    wo = oracle_weight(packed, qs).dequant_bf16().astype(np.float64)
+    ref = O.lora_linear_forward(bf16_values(x), wo, bf16_values(a), bf16_values(b), s)
+    assert_close_fro(np_f32(y1), ref, what="Y")
