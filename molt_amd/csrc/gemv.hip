@@ -340,7 +340,7 @@ struct GdRound {
 // still in flight; a load under a run-time branch made it wait for those too.
 // Rows past the matrix read row `fallback` instead (the wave's own first row,
 // already on its way to the cache; one shared row would be a hot spot).
-template <int RW, int IPR, bool NESTED, bool LORA>
+template <int RW, int IPR, bool NESTED, bool LORA, bool FULL>
 MOLT_DEV void gd_load(GdRound<RW, IPR>& R, const GemvParams& p, int64_t n0, int lane, int KB, int64_t fallback) {
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
@@ -350,8 +350,8 @@ MOLT_DEV void gd_load(GdRound<RW, IPR>& R, const GemvParams& p, int64_t n0, int 
       const int j = r * IPR + i;
       // the last piece may end inside the row: its lanes past the end re-read
       // the row's last 16 bytes and block (their products are dropped)
-      const int wo = i + 1 < IPR ? 1024 * i + 16 * lane : min(1024 * i + 16 * lane, (p.K >> 1) - 16);
-      const int bo = i + 1 < IPR ? 32 * i + (lane >> 1) : min(32 * i + (lane >> 1), KB - 1);
+      const int wo = FULL || i + 1 < IPR ? 1024 * i + 16 * lane : min(1024 * i + 16 * lane, (p.K >> 1) - 16);
+      const int bo = FULL || i + 1 < IPR ? 32 * i + (lane >> 1) : min(32 * i + (lane >> 1), KB - 1);
       R.w[j] = *reinterpret_cast<const u32x4_t*>(p.packed + (uint32_t)(n * (p.K >> 1) + wo));
       const uint32_t blk = (uint32_t)(n * KB + bo);
       if constexpr (NESTED) {
@@ -396,7 +396,7 @@ MOLT_DEV float gd_wave_sum(float v) {
 // of token m, see gd_store). X row m sits at
 // xs + m * xstride (elements); with XREG (one token) the lane's X chunks are
 // xg[4 i + h] in registers instead.
-template <int RW, int IPR, int MX, bool XREG, bool PERM = false>
+template <int RW, int IPR, int MX, bool XREG, bool PERM, bool FULL>
 MOLT_DEV float gd_compute(const GdRound<RW, IPR>& R, const GemvParams& p, const uint32_t* tab, const uint16_t* xs,
                          int xstride, const u32x4_t* xg, const float* code2s, const float (&lt)[MX][2], int64_t n0,
                          int lane) {
@@ -443,7 +443,7 @@ MOLT_DEV float gd_compute(const GdRound<RW, IPR>& R, const GemvParams& p, const 
       }
     }
     // lanes past the end of a row in its last piece contribute nothing
-    const bool live = i + 1 < IPR || 1024 * i + 16 * lane < (p.K >> 1);
+    const bool live = FULL || i + 1 < IPR || 1024 * i + 16 * lane < (p.K >> 1);
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
       const float sc = gv_scale(p, code2s, R.q[r * IPR + i], R.s[r * IPR + i]);
@@ -490,7 +490,7 @@ MOLT_DEV void gd_store(const GemvParams& p, float v, int64_t n0, int lane) {
 // every store after the last round: with no branch between a load and its use
 // the compiler's waits count exactly the later loads still in flight. MAXR = 0:
 // any number of rounds, loaded two ahead in three rotating register sets.
-template <int RW, int IPR, int MX, bool NESTED, bool LORA, int MAXR>
+template <int RW, int IPR, int MX, bool NESTED, bool LORA, int MAXR, bool FULL>
 __global__ __launch_bounds__(GD_NT) __attribute__((amdgpu_waves_per_eu(IPR <= 2 && MX <= 2 ? 4 : 1)))
 void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
   constexpr bool PERM = gd_perm<IPR, MX>();
@@ -557,9 +557,9 @@ void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
   constexpr int NB = MAXR > 0 ? MAXR : 3;
   const int64_t nf = nb < p.N ? nb : p.N - 1;
   GdRound<RW, IPR> b[NB];
-  gd_load<RW, IPR, NESTED, LORA>(b[0], p, nb, lane, KB, nf);
+  gd_load<RW, IPR, NESTED, LORA, FULL>(b[0], p, nb, lane, KB, nf);
 #pragma unroll
-  for (int j = 1; j < (MAXR > 0 ? MAXR : 2); ++j) gd_load<RW, IPR, NESTED, LORA>(b[j], p, nb + j * stride, lane, KB, nf);
+  for (int j = 1; j < (MAXR > 0 ? MAXR : 2); ++j) gd_load<RW, IPR, NESTED, LORA, FULL>(b[j], p, nb + j * stride, lane, KB, nf);
 
   // X in LDS by (piece, dword, lane): 16-byte chunk c = 256 i + 4 l + h (elements
   // 2048 i + 32 l + 8 h ..) sits at 256 i + 64 h + l, so the reads of a piece's
@@ -599,7 +599,7 @@ void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
     float out[MAXR];
 #pragma unroll
     for (int j = 0; j < MAXR; ++j)
-      out[j] = gd_compute<RW, IPR, MX, XREG, PERM>(b[j], p, tab, gd_xs, xstride, xg, sm.code2s, lt, nb + j * stride, lane);
+      out[j] = gd_compute<RW, IPR, MX, XREG, PERM, FULL>(b[j], p, tab, gd_xs, xstride, xg, sm.code2s, lt, nb + j * stride, lane);
 #pragma unroll
     for (int j = 0; j < MAXR; ++j)
       if (j < rounds) gd_store<RW, MX>(p, out[j], nb + j * stride, lane);
@@ -607,16 +607,16 @@ void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
     // Rounds past the last one load the (clamped) last row again and are never
     // computed: unconditional loads keep the waits exact (see gd_load).
     for (int j = 0; j < rounds; j += 3) {
-      gd_load<RW, IPR, NESTED, LORA>(b[2], p, nb + (j + 2) * stride, lane, KB, nf);
-      gd_store<RW, MX>(p, gd_compute<RW, IPR, MX, XREG, PERM>(b[0], p, tab, gd_xs, xstride, xg, sm.code2s, lt,
+      gd_load<RW, IPR, NESTED, LORA, FULL>(b[2], p, nb + (j + 2) * stride, lane, KB, nf);
+      gd_store<RW, MX>(p, gd_compute<RW, IPR, MX, XREG, PERM, FULL>(b[0], p, tab, gd_xs, xstride, xg, sm.code2s, lt,
                                                           nb + j * stride, lane), nb + j * stride, lane);
       if (j + 1 >= rounds) break;
-      gd_load<RW, IPR, NESTED, LORA>(b[0], p, nb + (j + 3) * stride, lane, KB, nf);
-      gd_store<RW, MX>(p, gd_compute<RW, IPR, MX, XREG, PERM>(b[1], p, tab, gd_xs, xstride, xg, sm.code2s, lt,
+      gd_load<RW, IPR, NESTED, LORA, FULL>(b[0], p, nb + (j + 3) * stride, lane, KB, nf);
+      gd_store<RW, MX>(p, gd_compute<RW, IPR, MX, XREG, PERM, FULL>(b[1], p, tab, gd_xs, xstride, xg, sm.code2s, lt,
                                                           nb + (j + 1) * stride, lane), nb + (j + 1) * stride, lane);
       if (j + 2 >= rounds) break;
-      gd_load<RW, IPR, NESTED, LORA>(b[1], p, nb + (j + 4) * stride, lane, KB, nf);
-      gd_store<RW, MX>(p, gd_compute<RW, IPR, MX, XREG, PERM>(b[2], p, tab, gd_xs, xstride, xg, sm.code2s, lt,
+      gd_load<RW, IPR, NESTED, LORA, FULL>(b[1], p, nb + (j + 4) * stride, lane, KB, nf);
+      gd_store<RW, MX>(p, gd_compute<RW, IPR, MX, XREG, PERM, FULL>(b[2], p, tab, gd_xs, xstride, xg, sm.code2s, lt,
                                                           nb + (j + 2) * stride, lane), nb + (j + 2) * stride, lane);
     }
   }
@@ -932,9 +932,17 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
     const int64_t wgs = ceil_div64(waves, GD_WAVES);
     const int rounds = (int)ceil_div64(w->rows, wgs * GD_WAVES * rw);
     const size_t dyn = ipr == 2 && mx == 1 ? 0 : (size_t)mx * (ipr * 2048 + GD_XPAD) * 2;   // X in registers
-#define MOLT_GDK(IPRv, MXv, NE, LO, MR) \
-  hipLaunchKernelGGL((nf4_gemv_dot_kernel<1, IPRv, MXv, NE, LO, MR>), dim3((unsigned)wgs), dim3(GD_NT), dyn, st, p, \
-                     rounds)
+    // rows of whole pieces (K = 4096, 14336) skip the partial-piece clamps and masks
+    const bool full = w->cols == (int64_t)ipr * 2048;
+#define MOLT_GDK(IPRv, MXv, NE, LO, MR)                                                                        \
+  do {                                                                                                          \
+    if ((IPRv == 2 || IPRv == 7) && full)                                                                       \
+      hipLaunchKernelGGL((nf4_gemv_dot_kernel<1, IPRv, MXv, NE, LO, MR, (IPRv == 2 || IPRv == 7)>),             \
+                         dim3((unsigned)wgs), dim3(GD_NT), dyn, st, p, rounds);                                 \
+    else                                                                                                        \
+      hipLaunchKernelGGL((nf4_gemv_dot_kernel<1, IPRv, MXv, NE, LO, MR, false>), dim3((unsigned)wgs), dim3(GD_NT), \
+                         dyn, st, p, rounds);                                                                   \
+  } while (0)
     // nested statistics with at most 4 rounds per wave (every cfg5 decode shape): straight-line rounds
 #define MOLT_GDS(IPRv, MXv, LO)                                                   \
   do {                                                                            \
