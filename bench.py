@@ -550,9 +550,66 @@ def measured_counters() -> dict:
     return {k: float(v["mfma_busy"]) for k, v in _summary_rows(COUNTER_FILE).items() if "mfma_busy" in v}
 
 
+PROFILE_DECODE = tuple((n, k, m) for n, k in GEMV_CFG5 for m in (1, 16))
+
+
+def profile_decode(dev, reps: int) -> None:
+    """Decode kernels for counter passes: the NF4 GEMV (r=16 LoRA add-on) at
+    each cfg5 shape with M in (1, 16), then the standalone 14336 x 4096
+    dequant, `reps` launches each, in that order, one synchronised launch at a
+    time. Every launch reads its own copy of the packed weight and absmax
+    (copies totalling >= 512 MiB per shape, beyond the 256 MB Infinity Cache),
+    so no launch finds another's operands in a cache. Prints one line per
+    launch, in dispatch order, naming the case."""
+    import ctypes
+    import torch
+    import molt_amd
+    from molt_amd import _lib, ops
+
+    lib = _lib.load()
+    g = torch.Generator(device="cpu").manual_seed(5)
+    r = 16
+    cases = [("gemv", n, k, m) for n, k, m in PROFILE_DECODE] + [("dequant", 14336, 4096, 0)]
+    for kind, n, k, m in cases:
+        w = (torch.randn(n, k, generator=g) * 0.02).to(dev)
+        packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True)
+        del w
+        copies = max(reps, math.ceil(512 * 2**20 / (n * k // 2)))
+        packs = [packed.reshape(-1).clone() for _ in range(copies)]
+        qcopies = [qs.absmax.clone() for _ in range(copies)]
+        code, a2, c2 = (qs.code.float().contiguous(), qs.state2.absmax.float().contiguous(),
+                        qs.state2.code.float().contiguous())
+        descs = [ops._weight(pk, None, code, n, k, 64, 1, qq, a2, c2, float(qs.offset), 256)
+                 for pk, qq in zip(packs, qcopies)]
+        st = torch.cuda.current_stream().cuda_stream
+        if kind == "gemv":
+            x = torch.randn(m, k, generator=g).to(dev, torch.bfloat16)
+            a = ((torch.rand(r, k, generator=g) * 2 - 1) / math.sqrt(k)).to(dev)
+            b = (torch.randn(n, r, generator=g) * 0.01).to(dev)
+            t = ops.lora_project(x, None, 0, 1.0, a, 0)
+            y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+            ws_bytes = int(lib.molt_nf4_gemv_workspace(m, n, k))
+            ws = torch.zeros(max(ws_bytes, 256), device=dev, dtype=torch.uint8)
+        else:
+            out = torch.empty(n, k, device=dev, dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        for i in range(reps):
+            d = descs[(i * (copies // reps)) % copies]   # spread over the copies
+            if kind == "gemv":
+                _lib.check(lib.molt_nf4_gemv(x.data_ptr(), k, m, ctypes.byref(d), t.data_ptr(), r, b.data_ptr(),
+                                             r, 2.0, y.data_ptr(), n, ws.data_ptr(), ws_bytes, st))
+            else:
+                _lib.check(lib.molt_nf4_dequantize(ctypes.byref(d), out.data_ptr(), _lib.DTYPE_BF16, st))
+            torch.cuda.synchronize()
+            log(f"decode-case {kind} N={n} K={k} M={m} launch {i}")
+        del packs, qcopies, descs
+        torch.cuda.empty_cache()
+
+
 def profile_kernel(which: str, reps: int) -> int:
     """Run one kernel `reps` times at cfg4 shapes, for rocprofv3 passes:
     'gateup' = the fused gate/up NF4-LoRA GEMM, 'step' = whole gated-MLP steps,
+    'decode' = the NF4 GEMV at the cfg5 shapes and the standalone dequant,
     'stack' = cfg3 decoder-stack steps, 'hipblaslt' = plain bf16 GEMMs of the
     step's four shapes (the vendor-library ceiling), 'copy' = a 1 GiB device
     copy (1 GiB read + 1 GiB written) that calibrates FETCH_SIZE / WRITE_SIZE."""
@@ -572,6 +629,8 @@ def profile_kernel(which: str, reps: int) -> int:
             mlp_step(projs, x, dy, s)
     elif which == "stack":
         cfg3_stack(dev, steps=reps)
+    elif which == "decode":
+        profile_decode(dev, reps)
     elif which == "hipblaslt":
         # plain bf16 GEMMs of the cfg4 step's four contractions (hipBLASLt through torch.mm):
         # the vendor-library ceiling for these shapes, without NF4 decode or LoRA
@@ -684,7 +743,7 @@ def main() -> int:
     ap.add_argument("--no-head", action="store_true", help="skip the LM head + cross-entropy measurement")
     ap.add_argument("--no-dequant", action="store_true", help="skip the standalone dequant measurement")
     ap.add_argument("--no-stack", action="store_true", help="skip the cfg3 28-layer decoder stack")
-    ap.add_argument("--profile-kernel", choices=("gateup", "step", "stack", "hipblaslt", "copy"),
+    ap.add_argument("--profile-kernel", choices=("gateup", "step", "decode", "stack", "hipblaslt", "copy"),
                     help="only launch one kernel or one gated-MLP step (for rocprofv3 --pmc passes) and exit")
     ap.add_argument("--reps", type=int, default=3, help="launches for --profile-kernel")
     args = ap.parse_args()
