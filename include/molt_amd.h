@@ -242,6 +242,55 @@ int molt_nf4_swiglu_backward(const uint16_t* dy, int64_t lddy, int64_t M,
                              const uint16_t* up, int64_t ldg, uint16_t* dgate, uint16_t* dup,
                              void* workspace, size_t workspace_bytes, void* stream);
 
+/* Weight transposes handed from the forward to the input gradient (no
+ * counterpart in the reference, whose backward re-dequantises the NF4 weight
+ * for dX, methods/nf4_backward.py:167-284; methods/gated_replay.py:376-387).
+ * For many token rows both GEMMs of a weight stage it in bf16, the input
+ * gradient transposed. A *_keep_wt forward also writes deq(W)^T, bf16 [K, N]
+ * with row stride N (16-byte aligned, N * K elements per weight), from the W
+ * tiles its own staged GEMM already holds: a tile of each contraction step is
+ * written by one row block, so the copy costs the GEMM little. It sets
+ * *wt_written to 1 when it did (its plan staged the weights, N % 8 == 0), else
+ * 0, and its outputs are those of the plain entry point. A *_wt input gradient
+ * given that copy (the same weight; NULL = none) reads it instead of
+ * dequantising and transposing the weight itself, with a workspace of
+ * molt_nf4_lora_backward_workspace_wt(M, N, K, segments) bytes; its results
+ * are bitwise those of the plain entry point. molt_nf4_keeps_wt(M, N, K,
+ * weights) is 1 when a forward and input gradient over M rows both stage
+ * (for 16-byte aligned operands): then keeping the copy (N * K * 2 bytes per
+ * weight, held from the forward to the backward) replaces the backward's
+ * staging pass. */
+int32_t molt_nf4_keeps_wt(int64_t M, int64_t N, int64_t K, int32_t weights);
+int molt_nf4_lora_forward_keep_wt(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,
+                                  const uint16_t* t, int64_t ldt, const float* lora_b, int32_t r,
+                                  float scaling, uint16_t* y, int64_t ldy, uint16_t* wt,
+                                  int32_t* wt_written, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+int molt_nf4_gateup_forward_keep_wt(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* wg,
+                                    const molt_nf4_weight* wu, const uint16_t* t, int64_t ldt,
+                                    const float* bg, const float* bu, int32_t r, float sg, float su,
+                                    uint16_t* gate, uint16_t* up, uint16_t* h, int64_t ldo,
+                                    uint16_t* wgt, uint16_t* wut, int32_t* wt_written, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+size_t molt_nf4_lora_backward_workspace_wt(int64_t M, int64_t N, int64_t K, int32_t segments);
+int molt_nf4_lora_backward_input_wt(const uint16_t* dy, int64_t lddy, int64_t M,
+                                    const molt_nf4_weight* w, const uint16_t* wt, const uint16_t* u,
+                                    int64_t ldu, const float* lora_a, int32_t r, float lora_scale,
+                                    uint16_t* dx, int64_t lddx, void* workspace, size_t workspace_bytes,
+                                    void* stream);
+int molt_nf4_lora_backward_input_pair_wt(const uint16_t* dy0, const uint16_t* dy1, int64_t lddy,
+                                         int64_t M, const molt_nf4_weight* w0,
+                                         const molt_nf4_weight* w1, const uint16_t* wt0,
+                                         const uint16_t* wt1, const uint16_t* u0, const uint16_t* u1,
+                                         int64_t ldu, const float* a0, const float* a1, int32_t r,
+                                         uint16_t* dx, int64_t lddx, void* workspace,
+                                         size_t workspace_bytes, void* stream);
+int molt_nf4_swiglu_backward_wt(const uint16_t* dy, int64_t lddy, int64_t M,
+                                const molt_nf4_weight* wd, const uint16_t* wdt, const uint16_t* u,
+                                int64_t ldu, const float* lora_a, int32_t r, const uint16_t* gate,
+                                const uint16_t* up, int64_t ldg, uint16_t* dgate, uint16_t* dup,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
 /* LoRA weight gradient out = scale * L^T . R over M rows, fp32:
  *  L bf16 [M, P] (l_mode 0) or SwiGLU replay of (L, L2) (l_mode 1); R bf16 [M, Q].
  *  out_layout 0: out[P, Q] (dB = s dY^T T, methods/nf4_lora.py:102);

@@ -69,6 +69,18 @@ SIGNATURES: dict[str, tuple] = {
                                                     _i32, _p, _i64, _p, _sz, _p]),
     "molt_nf4_swiglu_backward": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _p, _p, _i64, _p, _p,
                                            _p, _sz, _p]),
+    "molt_nf4_keeps_wt": (_i32, [_i64, _i64, _i64, _i32]),
+    "molt_nf4_lora_forward_keep_wt": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _f32, _p, _i64, _p, _p,
+                                                _p, _sz, _p]),
+    "molt_nf4_gateup_forward_keep_wt": (C.c_int, [_p, _i64, _i64, _W, _W, _p, _i64, _p, _p, _i32, _f32, _f32,
+                                                  _p, _p, _p, _i64, _p, _p, _p, _p, _sz, _p]),
+    "molt_nf4_lora_backward_workspace_wt": (_sz, [_i64, _i64, _i64, _i32]),
+    "molt_nf4_lora_backward_input_wt": (C.c_int, [_p, _i64, _i64, _W, _p, _p, _i64, _p, _i32, _f32, _p, _i64,
+                                                  _p, _sz, _p]),
+    "molt_nf4_lora_backward_input_pair_wt": (C.c_int, [_p, _p, _i64, _i64, _W, _W, _p, _p, _p, _p, _i64, _p,
+                                                       _p, _i32, _p, _i64, _p, _sz, _p]),
+    "molt_nf4_swiglu_backward_wt": (C.c_int, [_p, _i64, _i64, _W, _p, _p, _i64, _p, _i32, _p, _p, _i64, _p,
+                                              _p, _p, _sz, _p]),
     "molt_lora_grad_workspace": (_sz, [_i64, _i64, _i64]),
     "molt_lora_grad": (C.c_int, [_p, _p, _i64, _i32, _p, _i64, _i64, _i64, _i64, _f32, _p, _i32, _p, _sz,
                                  _p]),

@@ -8,6 +8,7 @@
 #include <atomic>
 
 #include "../../include/molt_amd.h"
+#include "common.h"
 
 namespace molt {
 
@@ -101,13 +102,15 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
                                           const molt_nf4_weight* w1, const uint16_t* t, int64_t ldt, int lr,
                                           const float* b0, const float* b1, int64_t ldb, int r, float s0, float s1,
                                           uint16_t* y0, uint16_t* y1, uint16_t* y2, int64_t ldy,
-                                          void* workspace, size_t workspace_bytes, hipStream_t stream);
+                                          const molt::WtHandoff* wt, void* workspace, size_t workspace_bytes,
+                                          hipStream_t stream);
 extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* dy1, int64_t lddy, int64_t M,
                                            const molt_nf4_weight* w0, const molt_nf4_weight* w1,
                                            const uint16_t* u0, const uint16_t* u1, int64_t ldu, const float* a0,
                                            const float* a1, int64_t lda, int r, float lora_scale, uint16_t* dx,
                                            int64_t lddx, const uint16_t* gate, const uint16_t* up, uint16_t* dg, uint16_t* du,
-                                           int64_t ldg, void* workspace, size_t workspace_bytes, hipStream_t stream);
+                                           int64_t ldg, const molt::WtHandoff* wt, void* workspace,
+                                           size_t workspace_bytes, hipStream_t stream);
 
 extern "C" {
 
@@ -138,7 +141,8 @@ int molt_nf4_lora_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_
   if (!w)
     return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "molt_nf4_lora_forward: null weight"));
   return molt_nf4_lora_forward_impl(x, ldx, M, w, nullptr, t, ldt, r, lora_b, nullptr, r, r, scaling, scaling,
-                                    y, nullptr, nullptr, ldy, workspace, workspace_bytes, (hipStream_t)stream);
+                                    y, nullptr, nullptr, ldy, nullptr, workspace, workspace_bytes,
+                                    (hipStream_t)stream);
 }
 
 int molt_nf4_gateup_forward(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* wg,
@@ -148,7 +152,7 @@ int molt_nf4_gateup_forward(const uint16_t* x, int64_t ldx, int64_t M, const mol
   if (!wg || !wu)
     return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "molt_nf4_gateup_forward: null weight"));
   return molt_nf4_lora_forward_impl(x, ldx, M, wg, wu, t, ldt, 2 * r, bg, bu, r, r, sg, su, gate, up, h, ldo,
-                                    workspace, workspace_bytes, (hipStream_t)stream);
+                                    nullptr, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int molt_nf4_lora_backward_input(const uint16_t* dy, int64_t lddy, int64_t M, const molt_nf4_weight* w,
@@ -157,8 +161,8 @@ int molt_nf4_lora_backward_input(const uint16_t* dy, int64_t lddy, int64_t M, co
   if (!w)
     return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "molt_nf4_lora_backward_input: null weight"));
   return molt_nf4_lora_backward_impl(dy, nullptr, lddy, M, w, nullptr, u, nullptr, ldu, lora_a, nullptr, w->cols,
-                                     r, lora_scale, dx, lddx, nullptr, nullptr, nullptr, nullptr, 0, workspace,
-                                     workspace_bytes, (hipStream_t)stream);
+                                     r, lora_scale, dx, lddx, nullptr, nullptr, nullptr, nullptr, 0, nullptr,
+                                     workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 int molt_nf4_lora_backward_input_pair(const uint16_t* dy0, const uint16_t* dy1, int64_t lddy, int64_t M,
@@ -169,7 +173,7 @@ int molt_nf4_lora_backward_input_pair(const uint16_t* dy0, const uint16_t* dy1, 
   if (!w0 || !w1)
     return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "molt_nf4_lora_backward_input_pair: null weight"));
   return molt_nf4_lora_backward_impl(dy0, dy1, lddy, M, w0, w1, u0, u1, ldu, a0, a1, w0->cols, r, 1.0f, dx, lddx,
-                                     nullptr, nullptr, nullptr, nullptr, 0, workspace, workspace_bytes,
+                                     nullptr, nullptr, nullptr, nullptr, 0, nullptr, workspace, workspace_bytes,
                                      (hipStream_t)stream);
 }
 
@@ -183,8 +187,74 @@ int molt_nf4_swiglu_backward(const uint16_t* dy, int64_t lddy, int64_t M, const 
   if (!dgate)
     return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "molt_nf4_swiglu_backward: null dgate"));
   return molt_nf4_lora_backward_impl(dy, nullptr, lddy, M, wd, nullptr, u, nullptr, ldu, lora_a, nullptr, wd->cols,
-                                     r, 1.0f, nullptr, 0, gate, up, dgate, dup, ldg, workspace, workspace_bytes,
+                                     r, 1.0f, nullptr, 0, gate, up, dgate, dup, ldg, nullptr, workspace,
+                                     workspace_bytes, (hipStream_t)stream);
+}
+
+int molt_nf4_lora_forward_keep_wt(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,
+                                  const uint16_t* t, int64_t ldt, const float* lora_b, int32_t r, float scaling,
+                                  uint16_t* y, int64_t ldy, uint16_t* wt, int32_t* wt_written, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  if (wt_written) *wt_written = 0;
+  if (!w)
+    return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "molt_nf4_lora_forward_keep_wt: null weight"));
+  const molt::WtHandoff h{{wt, wt}, wt_written, {nullptr, nullptr}};
+  return molt_nf4_lora_forward_impl(x, ldx, M, w, nullptr, t, ldt, r, lora_b, nullptr, r, r, scaling, scaling,
+                                    y, nullptr, nullptr, ldy, &h, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int molt_nf4_gateup_forward_keep_wt(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* wg,
+                                    const molt_nf4_weight* wu, const uint16_t* t, int64_t ldt, const float* bg,
+                                    const float* bu, int32_t r, float sg, float su, uint16_t* gate, uint16_t* up,
+                                    uint16_t* h, int64_t ldo, uint16_t* wgt, uint16_t* wut, int32_t* wt_written,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  if (wt_written) *wt_written = 0;
+  if (!wg || !wu)
+    return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "molt_nf4_gateup_forward_keep_wt: null weight"));
+  const molt::WtHandoff ho{{wgt, wut}, wt_written, {nullptr, nullptr}};
+  return molt_nf4_lora_forward_impl(x, ldx, M, wg, wu, t, ldt, 2 * r, bg, bu, r, r, sg, su, gate, up, h, ldo,
+                                    &ho, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int molt_nf4_lora_backward_input_wt(const uint16_t* dy, int64_t lddy, int64_t M, const molt_nf4_weight* w,
+                                    const uint16_t* wt, const uint16_t* u, int64_t ldu, const float* lora_a,
+                                    int32_t r, float lora_scale, uint16_t* dx, int64_t lddx, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  if (!w)
+    return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "molt_nf4_lora_backward_input_wt: null weight"));
+  const molt::WtHandoff h{{nullptr, nullptr}, nullptr, {wt, wt}};
+  return molt_nf4_lora_backward_impl(dy, nullptr, lddy, M, w, nullptr, u, nullptr, ldu, lora_a, nullptr, w->cols,
+                                     r, lora_scale, dx, lddx, nullptr, nullptr, nullptr, nullptr, 0, &h,
+                                     workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int molt_nf4_lora_backward_input_pair_wt(const uint16_t* dy0, const uint16_t* dy1, int64_t lddy, int64_t M,
+                                         const molt_nf4_weight* w0, const molt_nf4_weight* w1, const uint16_t* wt0,
+                                         const uint16_t* wt1, const uint16_t* u0, const uint16_t* u1, int64_t ldu,
+                                         const float* a0, const float* a1, int32_t r, uint16_t* dx, int64_t lddx,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (!w0 || !w1)
+    return molt::drop_gemm_events(
+        molt::set_error(MOLT_EINVAL, "molt_nf4_lora_backward_input_pair_wt: null weight"));
+  const molt::WtHandoff h{{nullptr, nullptr}, nullptr, {wt0, wt1}};
+  return molt_nf4_lora_backward_impl(dy0, dy1, lddy, M, w0, w1, u0, u1, ldu, a0, a1, w0->cols, r, 1.0f, dx, lddx,
+                                     nullptr, nullptr, nullptr, nullptr, 0, &h, workspace, workspace_bytes,
                                      (hipStream_t)stream);
+}
+
+int molt_nf4_swiglu_backward_wt(const uint16_t* dy, int64_t lddy, int64_t M, const molt_nf4_weight* wd,
+                                const uint16_t* wdt, const uint16_t* u, int64_t ldu, const float* lora_a, int32_t r,
+                                const uint16_t* gate, const uint16_t* up, int64_t ldg, uint16_t* dgate,
+                                uint16_t* dup, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!wd)
+    return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "molt_nf4_swiglu_backward_wt: null weight"));
+  if (M == 0) return molt::drop_gemm_events(MOLT_OK);
+  if (!dgate)
+    return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "molt_nf4_swiglu_backward_wt: null dgate"));
+  const molt::WtHandoff h{{nullptr, nullptr}, nullptr, {wdt, wdt}};
+  return molt_nf4_lora_backward_impl(dy, nullptr, lddy, M, wd, nullptr, u, nullptr, ldu, lora_a, nullptr, wd->cols,
+                                     r, 1.0f, nullptr, 0, gate, up, dgate, dup, ldg, &h, workspace,
+                                     workspace_bytes, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -48,6 +48,15 @@ int device_cus();                    // compute units of the current device, cac
 // Events registered by molt_amd_time_next_gemm for this thread (null if none);
 // taking them clears the registration.
 void take_gemm_events(void** start, void** end);
+// deq(W)^T copies handed from a forward GEMM to the input gradient of the same
+// weights (bf16 [K, N], row stride N, one per weight): `out` asks a forward to
+// write them, `written` (host memory) tells whether it did, `in` gives them to
+// an input-gradient GEMM, which then does not stage the weights itself.
+struct WtHandoff {
+  uint16_t* out[2];
+  int32_t* written;
+  const uint16_t* in[2];
+};
 }  // namespace molt
 
 #define MOLT_REQUIRE(cond, code, ...)              \

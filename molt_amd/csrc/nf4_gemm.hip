@@ -60,6 +60,9 @@ struct FwdParams {
   // LoRA steps through the staged kernel's DMA ring (lr % 64 == 0): bf16(s B)
   // rows of each weight [N, lr], the pair's block-diagonal layout
   const uint16_t* lbst[2]; int lora_ring;
+  // staged kernels: also write deq(W)^T [K, N] of each weight (row stride N,
+  // N % 8 == 0) for the input gradient of the same weights; null = do not
+  uint16_t* wt_out[2];
 };
 
 struct BwdParams {
@@ -928,6 +931,37 @@ MOLT_DEV void fwd_row(int R, int64_t tn, bool pair, int& which, int64_t& n) {
   }
 }
 
+// deq(W)^T from the W tile of a staged forward step (FwdParams::wt_out).
+// Thread q owns tile rows 4 (q % 64) .. + 3, four consecutive rows n of one
+// weight, and the 8 contraction elements of chunk q / 64 of the step; per half
+// chunk: four 8-byte LDS reads, a half-word exchange (v_perm) into 4 rows of
+// W^T (one per contraction element, 4 consecutive n each) and four 8-byte
+// non-temporal stores. The 64 lanes of a wave write one contraction element of
+// all 256 tile rows per store: whole 256-byte runs of W^T rows. (Fewer live
+// registers than 16-byte rows of 8 n, which the GEMM's budget does not leave.)
+MOLT_DEV void wt_tile_write(const FwdParams& p, const uint16_t* __restrict__ wc, int64_t tn, int64_t k0, bool pair,
+                            int tid) {
+  const int g = tid & 63, c = tid >> 6;
+  int which;
+  int64_t n0;
+  fwd_row(4 * g, tn, pair, which, n0);
+  if (n0 >= p.N) return;   // rows past the weight (clamped copies of its last row)
+  uint16_t* dst = sel(p.wt_out, which) + (k0 + 8 * c) * p.N + n0;
+#pragma unroll
+  for (int hk = 0; hk < 2; ++hk) {
+    u32x2_t v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = *reinterpret_cast<const u32x2_t*>(wc + loff(4 * g + i, c) + 4 * hk);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t pick_half = (e & 1) ? 0x07060302u : 0x05040100u;
+      const u32x2_t o = {__builtin_amdgcn_perm(v[1][e >> 1], v[0][e >> 1], pick_half),
+                         __builtin_amdgcn_perm(v[3][e >> 1], v[2][e >> 1], pick_half)};
+      st_vec<kStreamOut>(dst + (4 * hk + e) * p.N, o);
+    }
+  }
+}
+
 // One thread's packed W bytes and block scale for one forward step. w_load
 // fetches them with exactly kLoads vector-memory instructions, issued after the
 // step's X DMA (dma_then_loads); the step's closing wait leaves exactly these in
@@ -1250,7 +1284,21 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
     x_src(xb1, 1);
     wait_vm_at_most<kStageDma>();                    // X(0), W(0) landed; X(1) may fly
     step_barrier();
+    // deq(W)^T for the input gradient: main step s of column tile tn is
+    // written by the row block tm = s % nt_m, so each step's tile is written
+    // once and the work is spread evenly over the row blocks. The stores are
+    // issued before the step's DMA, so the closing wait (which leaves only
+    // X(j + 2) in flight) also covers them and every step ends in the same
+    // state. (Issuing them after the DMA and leaving them in flight into the
+    // next step needs a different wait in those steps; the compiler then
+    // waits more in the steps that follow, and it measured no faster.)
+    const bool keep_t = p.wt_out[0] != nullptr;
+    const int ntm = (int)nt_m, tm32 = (int)tm;
     auto step = [&](int j, const uint16_t* xc, const uint16_t* wc, uint16_t* x2, uint16_t* wnx) {
+      if (keep_t && j < n_main && (sbeg + j) % ntm == tm32) {
+        wt_tile_write(p, wc, tn, (int64_t)(sbeg + j) * BK, PAIR, tid);
+        __builtin_amdgcn_sched_barrier(0);           // the stores stay ahead of the step's DMA
+      }
       load_frags(wc, xc, fo, 0, a[0], b[0]);
       mfma_set(a[1], b[1], acc);
       w_src(wnx, j + 1);
@@ -2149,8 +2197,8 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
                                           const uint16_t* t, int64_t ldt, int lr,
                                           const float* b0, const float* b1, int64_t ldb, int r,
                                           float s0, float s1, uint16_t* y0, uint16_t* y1,
-                                          uint16_t* y2, int64_t ldy, void* workspace, size_t workspace_bytes,
-                                          hipStream_t stream) {
+                                          uint16_t* y2, int64_t ldy, const molt::WtHandoff* wt,
+                                          void* workspace, size_t workspace_bytes, hipStream_t stream) {
   const char* who = "molt_nf4_lora_forward";
   const GemmEvents armed;
   int rc = check_weight_for_gemm(w0, who);
@@ -2218,6 +2266,12 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
       }
       if (!pair) p.wst[1] = p.wst[0];
       p.ldw = p.K;
+      // deq(W)^T for the input gradient, written by the GEMM from its W tiles
+      if (wt && wt->out[0] && (!pair || wt->out[1]) && p.N % 8 == 0 && aligned(wt->out[0], 16) &&
+          (!pair || aligned(wt->out[1], 16))) {
+        p.wt_out[0] = wt->out[0];
+        p.wt_out[1] = pair ? wt->out[1] : wt->out[0];
+      }
     }
     dim3 grid((unsigned)big_tiles, (unsigned)plan.S), block(big::NT);
     KernelEvents kev(armed, stream);
@@ -2256,7 +2310,9 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
     hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)ceil_div64(q, 256)), dim3(256), 0, stream, p.part, plan.S, M,
                        p.N, y0, ldy);
   }
-  return check_launch(who);
+  rc = check_launch(who);
+  if (rc == MOLT_OK && p.wt_out[0] && wt->written) *wt->written = 1;
+  return rc;
 }
 
 extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* dy1, int64_t lddy,
@@ -2265,8 +2321,8 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
                                            const uint16_t* u1, int64_t ldu, const float* a0,
                                            const float* a1, int64_t lda, int r, float lora_scale,
                                            uint16_t* dx, int64_t lddx, const uint16_t* gate, const uint16_t* up,
-                                           uint16_t* dg, uint16_t* du, int64_t ldg, void* workspace,
-                                           size_t workspace_bytes, hipStream_t stream) {
+                                           uint16_t* dg, uint16_t* du, int64_t ldg, const molt::WtHandoff* wt,
+                                           void* workspace, size_t workspace_bytes, hipStream_t stream) {
   const char* who = "molt_nf4_lora_backward_input";
   const GemmEvents armed;
   int rc = check_weight_for_gemm(w0, who);
@@ -2314,8 +2370,12 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
                       bwd_big_ok(M, lddy, p.Nw, p.Kw, nseg);
   const GemmPlan plan = bwd_plan(M, p.Nw, p.Kw, nseg, swiglu, big_ok, al);
   const bool want_stage = stage_wanted(plan.kind, M, p.Nw, p.Kw) && p.Kw % big::BN == 0;
-  const GemmWorkspace gw = place_workspace(plan, want_stage, nseg, p.Nw, p.Kw, 0, 0, M, p.Kw, workspace,
+  // deq(W)^T of each segment handed over by the forward: read instead of staged
+  const bool use_wt = want_stage && wt && wt->in[0] && (nseg == 1 || wt->in[1]) && aligned(wt->in[0], 16) &&
+                      (nseg == 1 || aligned(wt->in[1], 16));
+  const GemmWorkspace gw = place_workspace(plan, want_stage && !use_wt, nseg, p.Nw, p.Kw, 0, 0, M, p.Kw, workspace,
                                            workspace_bytes);
+  const bool staged = gw.stage || use_wt;
   char* wsb = static_cast<char*>(workspace);
   const bool split = gw.split;
   if (plan.kind == PLAN_BIG || (plan.kind == PLAN_BIG_SPLIT && split)) {
@@ -2324,7 +2384,11 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
       p.split_steps = plan.split_steps;
       p.part = reinterpret_cast<float*>(wsb + gw.stage_bytes + gw.lora_bytes);
     }
-    if (gw.stage) {
+    if (use_wt) {
+      p.wst[0] = wt->in[0];
+      p.wst[1] = nseg == 2 ? wt->in[1] : wt->in[0];
+      p.ldw = p.Nw;
+    } else if (gw.stage) {
       big::StageTParams sp{};
       for (int i = 0; i < 2; ++i) {
         const molt_nf4_weight* w = (i && w1) ? w1 : w0;
@@ -2345,7 +2409,7 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
     }
     dim3 grid((unsigned)big_tiles, (unsigned)plan.S), block(big::NT);
     KernelEvents kev(armed, stream);
-    if (gw.stage) {
+    if (staged) {
       if (swiglu) hipLaunchKernelGGL((big::bwd_kernel<EPI_SWIGLU_BWD, true>), grid, block, 0, stream, p);
       else hipLaunchKernelGGL((big::bwd_kernel<EPI_STORE, true>), grid, block, 0, stream, p);
     } else {
@@ -2414,4 +2478,23 @@ extern "C" size_t molt_nf4_lora_backward_workspace(int64_t M, int64_t Nw, int64_
   const GemmPlan plan = bwd_plan(M, Nw, Kw, nseg, false, bwd_big_ok(M, Nw, Nw, Kw, nseg), true);
   const bool stage = stage_wanted(plan.kind, M, Nw, Kw) && Kw % big::BN == 0;
   return gemm_workspace(plan, stage, nseg, Nw, Kw, 0, 0, M, Kw);
+}
+
+// Workspace of the input-gradient entry points given deq(W)^T (the *_wt
+// variants): only the split partials, the weights are not staged.
+extern "C" size_t molt_nf4_lora_backward_workspace_wt(int64_t M, int64_t Nw, int64_t Kw, int32_t nseg) {
+  if (M <= 0 || Nw <= 0 || Kw <= 0 || Nw % 64 != 0 || Kw % 64 != 0 || nseg < 1 || nseg > 2) return 0;
+  const GemmPlan plan = bwd_plan(M, Nw, Kw, nseg, false, bwd_big_ok(M, Nw, Nw, Kw, nseg), true);
+  return gemm_workspace(plan, false, nseg, Nw, Kw, 0, 0, M, Kw);
+}
+
+// 1 when a *_keep_wt forward of M token rows over N x K weights (16-byte
+// aligned X with row stride K) writes deq(W)^T: its plan stages the weights
+// and N % 8 == 0; and when the input gradient of the same weights over the
+// same rows would read it (its plan stages them too).
+extern "C" int32_t molt_nf4_keeps_wt(int64_t M, int64_t N, int64_t K, int32_t weights) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64 != 0 || N % 64 != 0 || weights < 1 || weights > 2) return 0;
+  const GemmPlan fp = fwd_plan(M, N, K, weights == 2, fwd_big_ok(M, K, N, K, true), true);
+  const GemmPlan bp = bwd_plan(M, N, K, weights, false, bwd_big_ok(M, N, N, K, weights), true);
+  return stage_wanted(fp.kind, M, N, K) && stage_wanted(bp.kind, M, N, K) && K % big::BN == 0 ? 1 : 0;
 }

@@ -12,6 +12,7 @@ There is no CPU path: a CPU tensor raises CapabilityError.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from typing import Optional
 
 import torch
@@ -259,31 +260,39 @@ def _call(fn_name: str, *args) -> None:
     fn = _FNS.get(fn_name)
     if fn is None:
         fn = _FNS[fn_name] = getattr(_lib.load(), fn_name)
-    pairs = _probes.get(fn_name) if _probes else None
+    key = _PROBE_AS.get(fn_name, fn_name)
+    pairs = _probes.get(key) if _probes else None
     if pairs is None:
         rc = fn(*args)
         if rc:
             _lib.check(rc)
         return
     lib = _lib.load()
-    pool = _probe_pool.get(fn_name)
+    pool = _probe_pool.get(key)
     if pool:
         start, end = pool.pop()
     else:
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
-        if fn_name in _GEMM_ENTRIES:
+        if key in _GEMM_ENTRIES:
             end.record()   # creates the event; the library records both again around the kernel
-    if fn_name in _GEMM_ENTRIES:
+    if key in _GEMM_ENTRIES:
         _lib.check(lib.molt_amd_time_next_gemm(C.c_void_p(start.cuda_event), C.c_void_p(end.cuda_event)))
     _lib.check(getattr(lib, fn_name)(*args))
-    if fn_name not in _GEMM_ENTRIES:
+    if key not in _GEMM_ENTRIES:
         end.record()
     pairs.append((start, end))
 
 
 _GEMM_ENTRIES = frozenset(("molt_nf4_lora_forward", "molt_nf4_gateup_forward", "molt_nf4_lora_backward_input",
                            "molt_nf4_lora_backward_input_pair", "molt_nf4_swiglu_backward"))
+# the variants that hand the staged weights over run the same GEMM kernels:
+# probes of a GEMM entry point also time them
+_PROBE_AS = {"molt_nf4_lora_forward_keep_wt": "molt_nf4_lora_forward",
+             "molt_nf4_gateup_forward_keep_wt": "molt_nf4_gateup_forward",
+             "molt_nf4_lora_backward_input_wt": "molt_nf4_lora_backward_input",
+             "molt_nf4_lora_backward_input_pair_wt": "molt_nf4_lora_backward_input_pair",
+             "molt_nf4_swiglu_backward_wt": "molt_nf4_swiglu_backward"}
 
 
 # ----------------------------------------------------------------- codec
@@ -475,11 +484,53 @@ def _(z0, z1, zscale0, zscale1, lora0, lora1):
     return z0.new_empty((z0.shape[0], 2 * lora0.shape[1]), dtype=torch.bfloat16)
 
 
+_KEEP_WT = [os.environ.get("MOLT_KEEP_WEIGHT_TRANSPOSES", "1") != "0"]
+
+
+def keep_weight_transposes(enabled: Optional[bool] = None) -> bool:
+    """Policy of the fused gated MLP for large token batches: its forward GEMMs
+    leave the bf16 transposed weights (N * K * 2 bytes per weight, held until
+    the backward of the same call) for the input gradients, which then skip
+    their own dequantise-and-transpose pass. On by default; the environment
+    variable MOLT_KEEP_WEIGHT_TRANSPOSES=0 or ``keep_weight_transposes(False)``
+    trades that time back for the memory. Returns the setting in force (after
+    the change, if ``enabled`` is given)."""
+    if enabled is not None:
+        _KEEP_WT[0] = bool(enabled)
+    return _KEEP_WT[0]
+
+
+def _keeps_wt(m: int, rows: int, cols: int, weights: int) -> bool:
+    """Whether a forward over m rows would hand deq(W)^T to the input gradient
+    (molt_nf4_keeps_wt): both GEMMs stage the weights."""
+    return bool(_workspace("molt_nf4_keeps_wt", m, rows, cols, weights))
+
+
+def _empty_wt(dev) -> Tensor:
+    return torch.empty(0, device=dev, dtype=torch.bfloat16)
+
+
 @_custom_op(f"{NS}::nf4_lora_forward", mutates_args=())
 def nf4_lora_forward(x: Tensor, packed: Tensor, scales: Tensor, code: Tensor, rows: int, cols: int,
                      order: int, block_size: int, t: Optional[Tensor], lora_b: Optional[Tensor],
                      scaling: float) -> Tensor:
     """Y = X deq(W)^T + T bf16(s B)^T (methods/nf4_lora.py:43-50)."""
+    return _lora_forward(x, packed, scales, code, rows, cols, order, block_size, t, lora_b, scaling, False)[0]
+
+
+@_custom_op(f"{NS}::nf4_lora_forward_keep_wt", mutates_args=())
+def nf4_lora_forward_keep_wt(x: Tensor, packed: Tensor, scales: Tensor, code: Tensor, rows: int, cols: int,
+                             order: int, block_size: int, t: Optional[Tensor], lora_b: Optional[Tensor],
+                             scaling: float) -> tuple[Tensor, Tensor]:
+    """(Y, deq(W)^T): nf4_lora_forward that also leaves the bf16 transposed
+    weight [cols, rows] for the input gradient of the same weight
+    (nf4_lora_backward_input(..., wt=)) when both GEMMs stage the weight, else
+    an empty tensor in its place."""
+    y, wt = _lora_forward(x, packed, scales, code, rows, cols, order, block_size, t, lora_b, scaling, True)
+    return y, wt
+
+
+def _lora_forward(x, packed, scales, code, rows, cols, order, block_size, t, lora_b, scaling, keep):
     what = "NF4-LoRA forward"
     dev = _require_gpu(x, packed, scales, code, t, lora_b, what=what)
     x = _bf16(x, "activations", what)
@@ -503,14 +554,28 @@ def nf4_lora_forward(x: Tensor, packed: Tensor, scales: Tensor, code: Tensor, ro
             raise ValueError(f"{what}: LoRA B shape {tuple(bb.shape)} != ({rows}, {r})")
     ws_bytes = _workspace("molt_nf4_lora_forward_workspace", x.shape[0], rows, cols, r)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
+    if keep and _keeps_wt(x.shape[0], rows, cols, 1):
+        wt = torch.empty((cols, rows), device=dev, dtype=torch.bfloat16)
+        written = C.c_int32(0)
+        _call("molt_nf4_lora_forward_keep_wt", x.data_ptr(), cols, x.shape[0], C.byref(w), _ptr(tt), max(r, 1),
+              _ptr(bb), r, float(scaling), y.data_ptr(), rows, wt.data_ptr(), C.byref(written), _ptr(ws),
+              ws_bytes, _stream(dev))
+        return y, (wt if written.value else _empty_wt(dev))
     _call("molt_nf4_lora_forward", x.data_ptr(), cols, x.shape[0], C.byref(w), _ptr(tt), max(r, 1),
           _ptr(bb), r, float(scaling), y.data_ptr(), rows, _ptr(ws), ws_bytes, _stream(dev))
-    return y
+    return y, (_empty_wt(dev) if keep else None)
 
 
 @nf4_lora_forward.register_fake
 def _(x, packed, scales, code, rows, cols, order, block_size, t, lora_b, scaling):
     return x.new_empty((x.shape[0], rows), dtype=torch.bfloat16)
+
+
+@nf4_lora_forward_keep_wt.register_fake
+def _(x, packed, scales, code, rows, cols, order, block_size, t, lora_b, scaling):
+    keep = _keeps_wt(x.shape[0], rows, cols, 1)
+    return (x.new_empty((x.shape[0], rows), dtype=torch.bfloat16),
+            x.new_empty((cols, rows) if keep else (0,), dtype=torch.bfloat16))
 
 
 @_custom_op(f"{NS}::nf4_gateup_forward", mutates_args=())
@@ -520,6 +585,25 @@ def nf4_gateup_forward(x: Tensor, packed_g: Tensor, scales_g: Tensor, packed_u: 
                        sg: float, su: float) -> tuple[Tensor, Tensor, Tensor]:
     """gate, up and h = bf16(bf16(silu(gate)) up) in one launch
     (methods/gated_replay.py:78-94,290-291)."""
+    return _gateup_forward(x, packed_g, scales_g, packed_u, scales_u, code, rows, cols, order, t, lora_bg,
+                           lora_bu, sg, su, False)[:3]
+
+
+@_custom_op(f"{NS}::nf4_gateup_forward_keep_wt", mutates_args=())
+def nf4_gateup_forward_keep_wt(x: Tensor, packed_g: Tensor, scales_g: Tensor, packed_u: Tensor,
+                               scales_u: Tensor, code: Tensor, rows: int, cols: int, order: int,
+                               t: Optional[Tensor], lora_bg: Optional[Tensor], lora_bu: Optional[Tensor],
+                               sg: float, su: float) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(gate, up, h, deq(Wg)^T, deq(Wu)^T): nf4_gateup_forward that also
+    leaves the bf16 transposed weights [cols, rows] for the paired input
+    gradient (nf4_lora_backward_input_pair(..., wt0=, wt1=)) when both GEMMs
+    stage the weights, else empty tensors in their place."""
+    return _gateup_forward(x, packed_g, scales_g, packed_u, scales_u, code, rows, cols, order, t, lora_bg,
+                           lora_bu, sg, su, True)
+
+
+def _gateup_forward(x, packed_g, scales_g, packed_u, scales_u, code, rows, cols, order, t, lora_bg, lora_bu,
+                    sg, su, keep):
     what = "NF4-LoRA gate/up forward"
     dev = _require_gpu(x, packed_g, scales_g, packed_u, scales_u, code, t, lora_bg, lora_bu, what=what)
     x = _bf16(x, "activations", what)
@@ -547,9 +631,21 @@ def nf4_gateup_forward(x: Tensor, packed_g: Tensor, scales_g: Tensor, packed_u: 
             raise ValueError(f"{what}: LoRA B shapes {tuple(bg.shape)}, {tuple(bu.shape)} != ({rows}, {r})")
     ws_bytes = _workspace("molt_nf4_gateup_forward_workspace", m, rows, cols, r)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
+    if keep and _keeps_wt(m, rows, cols, 2):
+        wts = [torch.empty((cols, rows), device=dev, dtype=torch.bfloat16) for _ in range(2)]
+        written = C.c_int32(0)
+        _call("molt_nf4_gateup_forward_keep_wt", x.data_ptr(), cols, m, C.byref(wg), C.byref(wu), _ptr(tt),
+              max(2 * r, 1), _ptr(bg), _ptr(bu), r, float(sg), float(su), outs[0].data_ptr(),
+              outs[1].data_ptr(), outs[2].data_ptr(), rows, wts[0].data_ptr(), wts[1].data_ptr(),
+              C.byref(written), _ptr(ws), ws_bytes, _stream(dev))
+        if not written.value:
+            wts = [_empty_wt(dev), _empty_wt(dev)]
+        return outs[0], outs[1], outs[2], wts[0], wts[1]
     _call("molt_nf4_gateup_forward", x.data_ptr(), cols, m, C.byref(wg), C.byref(wu), _ptr(tt),
           max(2 * r, 1), _ptr(bg), _ptr(bu), r, float(sg), float(su), outs[0].data_ptr(),
           outs[1].data_ptr(), outs[2].data_ptr(), rows, _ptr(ws), ws_bytes, _stream(dev))
+    if keep:
+        return outs[0], outs[1], outs[2], _empty_wt(dev), _empty_wt(dev)
     return outs[0], outs[1], outs[2]
 
 
@@ -558,12 +654,21 @@ def _(x, packed_g, scales_g, packed_u, scales_u, code, rows, cols, order, t, lor
     return tuple(x.new_empty((x.shape[0], rows), dtype=torch.bfloat16) for _ in range(3))
 
 
+@nf4_gateup_forward_keep_wt.register_fake
+def _(x, packed_g, scales_g, packed_u, scales_u, code, rows, cols, order, t, lora_bg, lora_bu, sg, su):
+    shape = (cols, rows) if _keeps_wt(x.shape[0], rows, cols, 2) else (0,)
+    return tuple([x.new_empty((x.shape[0], rows), dtype=torch.bfloat16) for _ in range(3)] +
+                 [x.new_empty(shape, dtype=torch.bfloat16) for _ in range(2)])
+
+
 @_custom_op(f"{NS}::nf4_lora_backward_input", mutates_args=())
 def nf4_lora_backward_input(dy: Tensor, packed: Tensor, scales: Tensor, code: Tensor, rows: int,
                             cols: int, order: int, block_size: int, u: Optional[Tensor],
-                            lora_a: Optional[Tensor], lora_scale: float) -> Tensor:
+                            lora_a: Optional[Tensor], lora_scale: float, wt: Optional[Tensor] = None) -> Tensor:
     """dX = dY deq(W) + U bf16(lora_scale A) (methods/nf4_lora.py:86-101;
-    methods/nf4_backward.py:167-284)."""
+    methods/nf4_backward.py:167-284). ``wt``: deq(W)^T from
+    nf4_lora_forward_keep_wt of the same weight (an empty tensor or None =
+    none); the result is bitwise the same."""
     what = "NF4-LoRA backward"
     dev = _require_gpu(dy, packed, scales, code, u, lora_a, what=what)
     dy = _bf16(dy, "gradients", what)
@@ -586,6 +691,14 @@ def nf4_lora_backward_input(dy: Tensor, packed: Tensor, scales: Tensor, code: Te
             raise ValueError("LoRA gradient rows must match the output gradient")
         if aa.dim() != 2 or aa.shape != (r, cols):
             raise ValueError("LoRA gradient and A matrix dimensions are incompatible")
+    wt = _wt_given(wt, rows, cols, what)
+    if wt is not None:
+        ws_bytes = _workspace("molt_nf4_lora_backward_workspace_wt", dy.shape[0], rows, cols, 1)
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
+        _call("molt_nf4_lora_backward_input_wt", dy.data_ptr(), rows, dy.shape[0], C.byref(w), wt.data_ptr(),
+              _ptr(uu), max(r, 1), _ptr(aa), r, float(lora_scale), dx.data_ptr(), cols, _ptr(ws), ws_bytes,
+              _stream(dev))
+        return dx
     ws_bytes = _workspace("molt_nf4_lora_backward_workspace", dy.shape[0], rows, cols, 1)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     _call("molt_nf4_lora_backward_input", dy.data_ptr(), rows, dy.shape[0], C.byref(w), _ptr(uu),
@@ -593,8 +706,18 @@ def nf4_lora_backward_input(dy: Tensor, packed: Tensor, scales: Tensor, code: Te
     return dx
 
 
+def _wt_given(wt: Optional[Tensor], rows: int, cols: int, what: str) -> Optional[Tensor]:
+    """A deq(W)^T handed over by a keep_wt forward, or None (None or empty)."""
+    if wt is None or wt.numel() == 0:
+        return None
+    if wt.dtype != torch.bfloat16 or tuple(wt.shape) != (cols, rows) or not wt.is_contiguous():
+        raise ValueError(f"{what}: the transposed weight must be contiguous BF16 ({cols}, {rows}), "
+                         f"got {tuple(wt.shape)} {wt.dtype}")
+    return wt
+
+
 @nf4_lora_backward_input.register_fake
-def _(dy, packed, scales, code, rows, cols, order, block_size, u, lora_a, lora_scale):
+def _(dy, packed, scales, code, rows, cols, order, block_size, u, lora_a, lora_scale, wt=None):
     return dy.new_empty((dy.shape[0], cols), dtype=torch.bfloat16)
 
 
@@ -602,9 +725,12 @@ def _(dy, packed, scales, code, rows, cols, order, block_size, u, lora_a, lora_s
 def nf4_lora_backward_input_pair(dy0: Tensor, dy1: Tensor, packed0: Tensor, scales0: Tensor,
                                  packed1: Tensor, scales1: Tensor, code: Tensor, rows: int, cols: int,
                                  order: int, u0: Optional[Tensor], u1: Optional[Tensor],
-                                 a0: Optional[Tensor], a1: Optional[Tensor]) -> Tensor:
+                                 a0: Optional[Tensor], a1: Optional[Tensor], wt0: Optional[Tensor] = None,
+                                 wt1: Optional[Tensor] = None) -> Tensor:
     """dX of the gate and up projections in one contraction
-    (methods/gated_replay.py:167-186)."""
+    (methods/gated_replay.py:167-186). ``wt0``/``wt1``: deq(W0)^T and
+    deq(W1)^T from nf4_gateup_forward_keep_wt (empty or None = none; both or
+    neither); the result is bitwise the same."""
     what = "NF4-LoRA paired backward"
     dev = _require_gpu(dy0, dy1, packed0, scales0, packed1, scales1, code, u0, u1, a0, a1, what=what)
     dy0 = _bf16(dy0, "gradients", what)
@@ -633,6 +759,17 @@ def nf4_lora_backward_input_pair(dy0: Tensor, dy1: Tensor, packed0: Tensor, scal
         r = uu0.shape[1]
         if uu1.shape != uu0.shape or aa0.shape != (r, cols) or aa1.shape != (r, cols):
             raise ValueError("LoRA gradient and A matrix dimensions are incompatible")
+    wt0, wt1 = _wt_given(wt0, rows, cols, what), _wt_given(wt1, rows, cols, what)
+    if (wt0 is None) != (wt1 is None):
+        raise ValueError(f"{what}: give both transposed weights or neither")
+    if wt0 is not None:
+        ws_bytes = _workspace("molt_nf4_lora_backward_workspace_wt", m, rows, cols, 2)
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
+        _call("molt_nf4_lora_backward_input_pair_wt", dy0.data_ptr(), dy1.data_ptr(), rows, m, C.byref(w0),
+              C.byref(w1), wt0.data_ptr(), wt1.data_ptr(), _ptr(uu0), _ptr(uu1),
+              max(uu0.stride(0) if r else 1, 1), _ptr(aa0), _ptr(aa1), r, dx.data_ptr(), cols, _ptr(ws), ws_bytes,
+              _stream(dev))
+        return dx
     ws_bytes = _workspace("molt_nf4_lora_backward_workspace", m, rows, cols, 2)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     _call("molt_nf4_lora_backward_input_pair", dy0.data_ptr(), dy1.data_ptr(), rows, m, C.byref(w0),
@@ -643,16 +780,18 @@ def nf4_lora_backward_input_pair(dy0: Tensor, dy1: Tensor, packed0: Tensor, scal
 
 
 @nf4_lora_backward_input_pair.register_fake
-def _(dy0, dy1, packed0, scales0, packed1, scales1, code, rows, cols, order, u0, u1, a0, a1):
+def _(dy0, dy1, packed0, scales0, packed1, scales1, code, rows, cols, order, u0, u1, a0, a1, wt0=None, wt1=None):
     return dy0.new_empty((dy0.shape[0], cols), dtype=torch.bfloat16)
 
 
 @_custom_op(f"{NS}::nf4_swiglu_backward", mutates_args=())
 def nf4_swiglu_backward(dy: Tensor, packed: Tensor, scales: Tensor, code: Tensor, rows: int, cols: int,
                         order: int, u: Optional[Tensor], lora_a: Optional[Tensor], gate: Tensor,
-                        up: Tensor) -> tuple[Tensor, Tensor]:
+                        up: Tensor, wt: Optional[Tensor] = None) -> tuple[Tensor, Tensor]:
     """(dgate, dup) from dY through the down projection and SwiGLU
-    (methods/gated_replay.py:376-387); dh is never stored."""
+    (methods/gated_replay.py:376-387); dh is never stored. ``wt``: deq(Wd)^T
+    from nf4_lora_forward_keep_wt of the down weight (empty or None = none);
+    the result is bitwise the same."""
     what = "NF4-LoRA SwiGLU backward"
     dev = _require_gpu(dy, packed, scales, code, u, lora_a, gate, up, what=what)
     dy = _bf16(dy, "gradients", what)
@@ -678,6 +817,14 @@ def nf4_swiglu_backward(dy: Tensor, packed: Tensor, scales: Tensor, code: Tensor
         r = uu.shape[1]
         if aa.shape != (r, cols):
             raise ValueError("LoRA gradient and A matrix dimensions are incompatible")
+    wt = _wt_given(wt, rows, cols, what)
+    if wt is not None:
+        ws_bytes = _workspace("molt_nf4_lora_backward_workspace_wt", dy.shape[0], rows, cols, 1)
+        ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
+        _call("molt_nf4_swiglu_backward_wt", dy.data_ptr(), rows, dy.shape[0], C.byref(w), wt.data_ptr(),
+              _ptr(uu), max(r, 1), _ptr(aa), r, gate.data_ptr(), up.data_ptr(), cols, dg.data_ptr(),
+              du.data_ptr(), _ptr(ws), ws_bytes, _stream(dev))
+        return dg, du
     ws_bytes = _workspace("molt_nf4_lora_backward_workspace", dy.shape[0], rows, cols, 1)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
     _call("molt_nf4_swiglu_backward", dy.data_ptr(), rows, dy.shape[0], C.byref(w), _ptr(uu), max(r, 1),
@@ -687,7 +834,7 @@ def nf4_swiglu_backward(dy: Tensor, packed: Tensor, scales: Tensor, code: Tensor
 
 
 @nf4_swiglu_backward.register_fake
-def _(dy, packed, scales, code, rows, cols, order, u, lora_a, gate, up):
+def _(dy, packed, scales, code, rows, cols, order, u, lora_a, gate, up, wt=None):
     return torch.empty_like(gate), torch.empty_like(up)
 
 
