@@ -302,6 +302,34 @@ int molt_lora_grad(const uint16_t* l, const uint16_t* l2, int64_t ldl, int32_t l
                    float scale, float* out, int32_t out_layout, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* Several LoRA weight gradients in one launch, plus one launch that sums
+ * their splits (a molt_lora_grad call takes two launches per gradient). Each
+ * descriptor holds the arguments of one molt_lora_grad call, and its output is
+ * bitwise what that call gives: same tiles, M slices, partials and summation
+ * order. It is one launch pair when every gradient has plain operands
+ * (l_mode 0), 16-byte aligned rows, and P and Q multiples of 8. Otherwise the
+ * gradients run one after another. 1..8 descriptors. Workspace (256-byte
+ * aligned): molt_lora_grad_many_workspace(n, d) bytes. No counterpart in the
+ * reference, which computes each adapter gradient as its own matmul
+ * (methods/nf4_lora.py:102-103, methods/gated_replay.py:392-405); the
+ * gated-MLP backward runs its five gradients, and a scheduled projection its
+ * two, as one call. */
+typedef struct molt_lora_grad_desc {
+  const uint16_t* l;
+  const uint16_t* l2;
+  int64_t ldl;
+  int32_t l_mode;
+  const uint16_t* rmat;
+  int64_t ldr;
+  int64_t M, P, Q;
+  float scale;
+  float* out;
+  int32_t out_layout;
+} molt_lora_grad_desc;
+size_t molt_lora_grad_many_workspace(int32_t n, const molt_lora_grad_desc* d);
+int molt_lora_grad_many(int32_t n, const molt_lora_grad_desc* d, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
 /* molt_lora_grad with the frozen RMSNorm's output as L, formed as it is
  * staged: L(m, p) = bf16(fp32(x(m, p)) * inv_rms[m] * (fp32(w[p]) + offset)),
  * the products and roundings of molt_rmsnorm_forward, so the result is

@@ -42,6 +42,20 @@ class NF4Weight(C.Structure):
 
 _W = C.POINTER(NF4Weight)
 
+
+class LoraGradDesc(C.Structure):
+    """``molt_lora_grad_desc`` of include/molt_amd.h (one gradient of
+    ``molt_lora_grad_many``)."""
+    _fields_ = [
+        ("l", C.c_void_p), ("l2", C.c_void_p), ("ldl", C.c_int64), ("l_mode", C.c_int32),
+        ("rmat", C.c_void_p), ("ldr", C.c_int64),
+        ("M", C.c_int64), ("P", C.c_int64), ("Q", C.c_int64),
+        ("scale", C.c_float), ("out", C.c_void_p), ("out_layout", C.c_int32),
+    ]
+
+
+_GD = C.POINTER(LoraGradDesc)
+
 # name -> (restype, argtypes); the exact list of include/molt_amd.h.
 SIGNATURES: dict[str, tuple] = {
     "molt_amd_last_error": (C.c_char_p, []),
@@ -84,6 +98,8 @@ SIGNATURES: dict[str, tuple] = {
     "molt_lora_grad_workspace": (_sz, [_i64, _i64, _i64]),
     "molt_lora_grad": (C.c_int, [_p, _p, _i64, _i32, _p, _i64, _i64, _i64, _i64, _f32, _p, _i32, _p, _sz,
                                  _p]),
+    "molt_lora_grad_many_workspace": (_sz, [_i32, _GD]),
+    "molt_lora_grad_many": (C.c_int, [_i32, _GD, _p, _sz, _p]),
     "molt_lora_grad_rmsnorm": (C.c_int, [_p, _i64, _p, _p, _i32, _f32, _p, _i64, _i64, _i64, _i64, _f32, _p,
                                          _i32, _p, _sz, _p]),
     "molt_nf4_gemv_workspace": (_sz, [_i64, _i64, _i64]),

@@ -534,8 +534,8 @@ MOLT_DEV void patch_store(const Patch& pt, const GradParams& p, const float (&wo
 // The partial is stored in the output's layout, so that the split sum is
 // element-wise; in layout 1 a lane's four consecutive p are one 16-byte store.
 MOLT_DEV void grad_store_partial(const GradParams& p, const f32x16_t (&acc)[2][1], int64_t p0, int64_t q0, int wp,
-                                 int wq, int lane) {
-  float* out = p.part + (int64_t)blockIdx.z * p.P * p.Q;
+                                 int wq, int lane, int64_t slice) {
+  float* out = p.part + slice * p.P * p.Q;
   const int64_t q = q0 + wq * GR_WCOLS + (lane & 31);
   if (q >= p.Q) return;
   const bool v4 = p.P % 4 == 0 && ((uintptr_t)out & 15) == 0;
@@ -606,7 +606,7 @@ __global__ __launch_bounds__(GR_NT) void lora_grad_kernel(const GradParams p) {
     }
   }
 
-  grad_store_partial(p, acc, p0, q0, wp, wq, lane);
+  grad_store_partial(p, acc, p0, q0, wp, wq, lane, blockIdx.z);
 }
 
 // ------------------------------------------------------------------------
@@ -636,15 +636,16 @@ MOLT_DEV bf16x8_t gd_frag(const uint16_t* __restrict__ s, int base, int stride) 
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
-__global__ __launch_bounds__(GR_NT, 2) void lora_grad_dma_kernel(const GradParams p) {
+// One workgroup of the DMA-staged gradient: P tile bx, Q tile by, M slice bz.
+MOLT_DEV void grad_dma_tile(const GradParams& p, int bx, int by, int bz) {
   __shared__ __attribute__((aligned(16))) uint16_t la[GD_LT], lb[GD_LT], lc[GD_LT];
   __shared__ __attribute__((aligned(16))) uint16_t ra[GD_RT], rb[GD_RT], rc[GD_RT];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wp = wave & 1, wq = wave >> 1, h = lane >> 5;
-  const int64_t p0 = (int64_t)blockIdx.x * GR_P;
-  const int64_t q0 = (int64_t)blockIdx.y * GR_Q;
-  const int64_t mbeg = (int64_t)blockIdx.z * p.slice;
+  const int64_t p0 = (int64_t)bx * GR_P;
+  const int64_t q0 = (int64_t)by * GR_Q;
+  const int64_t mbeg = (int64_t)bz * p.slice;
   const int64_t mend = mbeg + p.slice < p.M ? mbeg + p.slice : p.M;
   const int steps = (int)ceil_div64(mend - mbeg, BK);
   const __amdgpu_buffer_rsrc_t lr = pj_rsrc(p.l, ((p.M - 1) * p.ldl + p.P) * 2);
@@ -714,7 +715,34 @@ __global__ __launch_bounds__(GR_NT, 2) void lora_grad_dma_kernel(const GradParam
          step(lb, rb, la, ra) && step(lc, rc, lb, rb)) {
   }
   pj_wait_vm<0>();                   // the repeated stages past the end
-  grad_store_partial(p, acc, p0, q0, wp, wq, lane);
+  grad_store_partial(p, acc, p0, q0, wp, wq, lane, bz);
+}
+
+__global__ __launch_bounds__(GR_NT, 2) void lora_grad_dma_kernel(const GradParams p) {
+  grad_dma_tile(p, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z);
+}
+
+// Several DMA-staged gradients in one launch (molt_lora_grad_many): the
+// workgroups of gradient d are the flat range [first[d], first[d + 1]),
+// ordered as its own launch's grid (P tiles fastest, then Q tiles, then M
+// slices), so each gradient's tiles, slices and partials are those of its
+// own launch.
+constexpr int kGradMany = 8;
+struct GradMany {
+  GradParams g[kGradMany];
+  int first[kGradMany + 1];
+  int gx[kGradMany], gy[kGradMany];
+  int n;
+};
+
+__global__ __launch_bounds__(GR_NT, 2) void lora_grad_dma_many_kernel(const GradMany m) {
+  const int b = (int)blockIdx.x;
+  int d = 0;
+#pragma unroll
+  for (int i = 1; i < kGradMany; ++i) d += (i < m.n && b >= m.first[i]) ? 1 : 0;
+  d = __builtin_amdgcn_readfirstlane(d);
+  const int local = b - m.first[d], gx = m.gx[d], gy = m.gy[d];
+  grad_dma_tile(m.g[d], local % gx, (local / gx) % gy, local / (gx * gy));
 }
 
 // SwiGLU-replay L = bf16(bf16(silu(g)) u) (ztrans mode 1, the forward's h)
@@ -811,7 +839,7 @@ __global__ __launch_bounds__(GR_NT, 2) void lora_grad_dma_replay_kernel(const Gr
   };
   while (step(ga, ua, ra, gb, ub, rb) && step(gb, ub, rb, ga, ua, ra)) {
   }
-  grad_store_partial(p, acc, p0, q0, wp, wq, lane);
+  grad_store_partial(p, acc, p0, q0, wp, wq, lane, blockIdx.z);
 }
 
 __global__ void zero_fill_kernel(float* __restrict__ out, int64_t n) {
@@ -847,6 +875,50 @@ __global__ void lora_grad_reduce_kernel(const float* __restrict__ part, int S, i
     float s = 0.0f;
     for (int k = 0; k < S; ++k) s += part[(int64_t)k * n + i];
     out[i] = s * scale;
+  }
+}
+
+// The split sums of several gradients in one launch: items of gradient d
+// (elements, or 4-element groups with vec4) are the flat range
+// [first[d], first[d + 1]); each is summed as lora_grad_reduce_kernel does.
+struct ReduceMany {
+  const float* part[kGradMany];
+  float* out[kGradMany];
+  int64_t n[kGradMany];
+  int64_t first[kGradMany + 1];
+  float scale[kGradMany];
+  int S[kGradMany], vec4[kGradMany];
+  int cnt;
+};
+
+__global__ void lora_grad_reduce_many_kernel(const ReduceMany r) {
+  const int64_t total = r.first[r.cnt];
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    int d = 0;
+#pragma unroll
+    for (int k = 1; k < kGradMany; ++k) d += (k < r.cnt && i >= r.first[k]) ? 1 : 0;
+    const int64_t j = i - r.first[d];
+    const float* part = r.part[d];
+    const int S = r.S[d];
+    if (r.vec4[d]) {
+      const int64_t n4 = r.n[d] / 4;
+      const f32x4_t* p4 = reinterpret_cast<const f32x4_t*>(part);
+      f32x4_t s4 = {0.0f, 0.0f, 0.0f, 0.0f};
+      int k = 0;
+      for (; k + 8 <= S; k += 8) {
+        f32x4_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = p4[(int64_t)(k + u) * n4 + j];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s4 += v[u];
+      }
+      for (; k < S; ++k) s4 += p4[(int64_t)k * n4 + j];
+      reinterpret_cast<f32x4_t*>(r.out[d])[j] = s4 * r.scale[d];
+    } else {
+      float a = 0.0f;
+      for (int k = 0; k < S; ++k) a += part[(int64_t)k * r.n[d] + j];
+      r.out[d][j] = a * r.scale[d];
+    }
   }
 }
 
@@ -1067,6 +1139,101 @@ extern "C" int molt_lora_grad(const uint16_t* l, const uint16_t* l2, int64_t ldl
   const bool vec = P % 8 == 0 && Q % 8 == 0 && ldl % 8 == 0 && ldr % 8 == 0 && aligned(l, 16) &&
                    aligned(rmat, 16) && (l_mode == 0 || aligned(l2, 16));
   return launch_grad(p, vec, l_mode, scale, out, out_layout, workspace, workspace_bytes, st, who);
+}
+
+// Several gradients in one launch (and their split sums in a second): each
+// output is bitwise that of its own molt_lora_grad call (same tiles, slices,
+// partials and summation order). All operands plain (l_mode 0) and eligible
+// for the DMA-staged kernel, else the gradients run one after another.
+static size_t grad_ws_bytes(int64_t M, int64_t P, int64_t Q) {
+  return M > 0 ? ((size_t)grad_splits(M, P, Q) * (size_t)P * (size_t)Q * sizeof(float) + 255) / 256 * 256 : 0;
+}
+
+extern "C" size_t molt_lora_grad_many_workspace(int32_t n, const molt_lora_grad_desc* d) {
+  if (n < 1 || n > kGradMany || !d) return 0;
+  size_t b = 0;
+  for (int i = 0; i < n; ++i)
+    if (d[i].P > 0 && d[i].Q > 0) b += grad_ws_bytes(d[i].M, d[i].P, d[i].Q);
+  return b;
+}
+
+extern "C" int molt_lora_grad_many(int32_t n, const molt_lora_grad_desc* d, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  const char* who = "molt_lora_grad_many";
+  MOLT_REQUIRE(d && n >= 1 && n <= kGradMany, MOLT_EINVAL, "%s: 1..%d gradients", who, kGradMany);
+  hipStream_t st = (hipStream_t)stream;
+  GradMany gm{};
+  ReduceMany rm{};
+  bool all_dma = true;
+  size_t off = 0;
+  GradParams ps[kGradMany];
+  for (int i = 0; i < n; ++i) {
+    const molt_lora_grad_desc& g = d[i];
+    MOLT_REQUIRE(g.l_mode == 0 || g.l_mode == 1, MOLT_EINVAL, "%s: bad l_mode (gradient %d)", who, i);
+    MOLT_REQUIRE(g.out_layout == 0 || g.out_layout == 1, MOLT_EINVAL, "%s: bad out_layout (gradient %d)", who, i);
+    MOLT_REQUIRE(g.M >= 0 && g.P > 0 && g.Q > 0, MOLT_EINVAL, "%s: bad shape (gradient %d)", who, i);
+    MOLT_REQUIRE(g.out && g.ldl >= g.P && g.ldr >= g.Q, MOLT_EINVAL, "%s: bad pointers/strides (gradient %d)", who, i);
+    MOLT_REQUIRE(g.M == 0 || (g.l && g.rmat && (g.l_mode == 0 || g.l2)), MOLT_EINVAL, "%s: null operand (gradient %d)",
+                 who, i);
+    GradParams& p = ps[i];
+    p = GradParams{};
+    p.l = g.l; p.l2 = g.l2; p.ldl = g.ldl; p.mode = g.l_mode; p.rm = g.rmat; p.ldr = g.ldr;
+    p.M = g.M; p.P = g.P; p.Q = g.Q; p.layout = g.out_layout;
+    p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + off);
+    off += grad_ws_bytes(g.M, g.P, g.Q);
+    const bool vec = g.P % 8 == 0 && g.Q % 8 == 0 && g.ldl % 8 == 0 && g.ldr % 8 == 0 && aligned(g.l, 16) &&
+                     aligned(g.rmat, 16);
+    all_dma = all_dma && g.M > 0 && vec && g.l_mode == 0 && molt::tuning_value(MOLT_TUNE_LORA_DMA) != 0 &&
+              ((g.M - 1) * g.ldl + g.P) * 2 < ((int64_t)1 << 31) && ((g.M - 1) * g.ldr + g.Q) * 2 < ((int64_t)1 << 31);
+  }
+  MOLT_REQUIRE(workspace ? workspace_bytes >= off && aligned(workspace, 256) : off == 0, MOLT_EWORKSPACE,
+               "%s: workspace %zu < %zu bytes (or not 256-byte aligned)", who, workspace_bytes, off);
+  if (!all_dma) {   // one launch pair per gradient
+    for (int i = 0; i < n; ++i) {
+      int rc;
+      if (d[i].M == 0) {
+        rc = zero_grad(d[i].out, d[i].P, d[i].Q, st, who);
+      } else {
+        const bool vec = d[i].P % 8 == 0 && d[i].Q % 8 == 0 && d[i].ldl % 8 == 0 && d[i].ldr % 8 == 0 &&
+                         aligned(d[i].l, 16) && aligned(d[i].rmat, 16) && (d[i].l_mode == 0 || aligned(d[i].l2, 16));
+        rc = launch_grad(ps[i], vec, d[i].l_mode, d[i].scale, d[i].out, d[i].out_layout, ps[i].part,
+                         grad_ws_bytes(d[i].M, d[i].P, d[i].Q), st, who);
+      }
+      if (rc) return rc;
+    }
+    return MOLT_OK;
+  }
+  int blocks = 0;
+  int64_t items = 0;
+  for (int i = 0; i < n; ++i) {
+    GradParams& p = ps[i];
+    const int S = grad_splits(p.M, p.P, p.Q);
+    p.slice = ceil_div64(ceil_div64(p.M, S), BK) * BK;
+    const int S_eff = (int)ceil_div64(p.M, p.slice);
+    gm.g[i] = p;
+    gm.gx[i] = (int)ceil_div64(p.P, GR_P);
+    gm.gy[i] = (int)ceil_div64(p.Q, GR_Q);
+    gm.first[i] = blocks;
+    MOLT_REQUIRE((int64_t)blocks + (int64_t)gm.gx[i] * gm.gy[i] * S_eff < (1ll << 31), MOLT_EINVAL,
+                 "%s: problem too large", who);
+    blocks += gm.gx[i] * gm.gy[i] * S_eff;
+    const int64_t nel = p.P * p.Q;
+    rm.part[i] = p.part; rm.out[i] = d[i].out; rm.n[i] = nel; rm.scale[i] = d[i].scale; rm.S[i] = S_eff;
+    rm.vec4[i] = nel % 4 == 0 && aligned(p.part, 16) && aligned(d[i].out, 16);
+    rm.first[i] = items;
+    items += rm.vec4[i] ? nel / 4 : nel;
+  }
+  gm.first[n] = blocks;
+  gm.n = n;
+  rm.first[n] = items;
+  rm.cnt = n;
+  hipLaunchKernelGGL(lora_grad_dma_many_kernel, dim3((unsigned)blocks), dim3(GR_NT), 0, st, gm);
+  int rc = check_launch(who);
+  if (rc) return rc;
+  int64_t rb = ceil_div64(items, 256);
+  if (rb > 4096) rb = 4096;
+  hipLaunchKernelGGL(lora_grad_reduce_many_kernel, dim3((unsigned)rb), dim3(256), 0, st, rm);
+  return check_launch(who);
 }
 
 extern "C" int molt_lora_grad_rmsnorm(const uint16_t* x, int64_t ldx, const float* inv_rms, const void* norm_weight,

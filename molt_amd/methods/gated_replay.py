@@ -240,18 +240,23 @@ def _fused_backward(grad_output, flat, gate, up, gated, t_gu, t_d, gate_packed, 
         resolved_nf4_scales(up_qs), gate_qs.code, i_dim, h_dim, nibble_order(gate_qs), u_g, u_u, gate_a,
         up_a, wgt, wut)
     del wgt, wut
+    # The adapter gradients with plain operands run as one launch (and one
+    # split-sum launch), bitwise as separate calls: dB_d over dY, dB_g over dg,
+    # dB_u over du, dA_d over h when the forward kept it, and dA_gate / dA_up
+    # as one pass over X with [U_g | U_u] when X is materialised.
+    plain = [(dy, t_d, s_d, 0), (dg, t_gu[:, :r], s_g, 0), (du, t_gu[:, r:], s_u, 0)]
     if gated is not None:   # h kept from the forward: bitwise the replayed value
-        d_down_a = ops.direct.lora_grad(gated, None, 0, u_d, 1.0, 1)
-    else:
-        d_down_a = ops.direct.lora_grad(gate, up, 1, u_d, 1.0, 1)
-    d_down_b = ops.direct.lora_grad(dy, None, 0, t_d, s_d, 0)
-    # dA_gate and dA_up both contract X: one pass over X with [U_g | U_u]
+        plain.append((gated, u_d, 1.0, 1))
+    if norm is None:
+        plain.append((flat, u_gu, 1.0, 1))
+    grads = ops.direct.lora_grad_many([g[0] for g in plain], [None] * len(plain), [0] * len(plain),
+                                      [g[1] for g in plain], [float(g[2]) for g in plain], [g[3] for g in plain])
+    d_down_b, d_gate_b, d_up_b = grads[0], grads[1], grads[2]
+    d_down_a = grads[3] if gated is not None else ops.direct.lora_grad(gate, up, 1, u_d, 1.0, 1)
     if norm is not None:
         d_gu_a = ops.direct.lora_grad_rmsnorm(norm[0], norm[1], norm[2], norm[3], u_gu, 1.0, 1)
     else:
-        d_gu_a = ops.direct.lora_grad(flat, None, 0, u_gu, 1.0, 1)
-    d_gate_b = ops.direct.lora_grad(dg, None, 0, t_gu[:, :r], s_g, 0)
-    d_up_b = ops.direct.lora_grad(du, None, 0, t_gu[:, r:], s_u, 0)
+        d_gu_a = grads[-1]
     return dx, d_gu_a[:r], d_gate_b, d_gu_a[r:], d_up_b, d_down_a, d_down_b
 
 

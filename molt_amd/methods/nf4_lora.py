@@ -65,13 +65,19 @@ class _ScheduledNF4LoRA(torch.autograd.Function):
             )
         flat_x = x.reshape(-1, k)
         low_rank = ops.direct.lora_project(flat_x, None, 0, 1.0, lora_a, 0)
+        ctx.wt = None
         if gemv_applies(flat_x, quant_state, lora_a.shape[0]):
             # decode-sized batch: HBM-bound skinny-M GEMV instead of the MFMA GEMM
             result = nf4_gemv_linear(flat_x, packed_weight, quant_state, low_rank, lora_b, scaling)
         else:
-            result = ops.direct.nf4_lora_forward(
-                flat_x, packed_weight.reshape(-1), resolved_nf4_scales(quant_state), quant_state.code, n, k,
-                nibble_order(quant_state), int(quant_state.blocksize), low_rank, lora_b, float(scaling))
+            args = (flat_x, packed_weight.reshape(-1), resolved_nf4_scales(quant_state), quant_state.code, n, k,
+                    nibble_order(quant_state), int(quant_state.blocksize), low_rank, lora_b, float(scaling))
+            if ops.keep_weight_transposes() and any(ctx.needs_input_grad):
+                # the GEMM also leaves deq(W)^T for the input gradient when it stages the weight
+                result, wt = ops.direct.nf4_lora_forward_keep_wt(*args)
+                ctx.wt = wt if wt.numel() else None
+            else:
+                result = ops.direct.nf4_lora_forward(*args)
         if bias is not None:
             result.add_(bias.to(result.dtype))
         ctx.quant_state = quant_state
@@ -93,10 +99,13 @@ class _ScheduledNF4LoRA(torch.autograd.Function):
         flat_grad = grad_output.reshape(-1, n).to(torch.bfloat16)
         scales = resolved_nf4_scales(qs)
         grad_through_b = ops.direct.lora_project(flat_grad, None, 2, ctx.scaling, lora_b, 1)
+        wt, ctx.wt = ctx.wt, None
         grad_x = ops.direct.nf4_lora_backward_input(flat_grad, packed_weight.reshape(-1), scales, qs.code, n, k,
-                                             nibble_order(qs), int(qs.blocksize), grad_through_b, lora_a, 1.0)
-        grad_a = ops.direct.lora_grad(flat_x, None, 0, grad_through_b, 1.0, 1)
-        grad_b = ops.direct.lora_grad(flat_grad, None, 0, low_rank, ctx.scaling, 0)
+                                             nibble_order(qs), int(qs.blocksize), grad_through_b, lora_a, 1.0, wt)
+        del wt
+        # dA = U^T X and dB = s dY^T T in one launch pair (bitwise as two calls)
+        grad_a, grad_b = ops.direct.lora_grad_many([flat_x, flat_grad], [None, None], [0, 0],
+                                                   [grad_through_b, low_rank], [1.0, ctx.scaling], [1, 0])
         grad_bias = flat_grad.float().sum(0) if ctx.needs_input_grad[7] else None
         return (grad_x.reshape(ctx.input_shape), None, grad_a.to(lora_a.dtype), grad_b.to(lora_b.dtype),
                 None, None, None, grad_bias)

@@ -868,6 +868,48 @@ def _(l, l2, mode, rmat, scale, layout):
     return l.new_empty((p, q) if layout == 0 else (q, p), dtype=torch.float32)
 
 
+@_custom_op(f"{NS}::lora_grad_many", mutates_args=())
+def lora_grad_many(ls: list[Tensor], l2s: list[Optional[Tensor]], modes: list[int], rmats: list[Tensor],
+                   scales: list[float], layouts: list[int]) -> list[Tensor]:
+    """Several ``lora_grad`` results (1..8) from one launch and one split-sum
+    launch (molt_lora_grad_many); each output is bitwise that of its own
+    ``lora_grad`` call."""
+    what = "LoRA gradients"
+    n = len(ls)
+    if not (1 <= n <= 8) or not (len(l2s) == len(modes) == len(rmats) == len(scales) == len(layouts) == n):
+        raise ValueError(f"{what}: 1..8 gradients with one entry per argument list")
+    dev = _require_gpu(*ls, *[t for t in l2s if t is not None], *rmats, what=what)
+    keep, outs = [], []
+    descs = (_lib.LoraGradDesc * n)()
+    for i in range(n):
+        l = _bf16(ls[i], "activations", what)
+        l2 = None if l2s[i] is None else _bf16(l2s[i], "activations", what)
+        rmat = _bf16_rows(rmats[i], "low-rank operand", what)
+        if l2 is not None and l2.shape != l.shape:
+            raise ValueError(f"{what}: the second operand {tuple(l2.shape)} must match {tuple(l.shape)}")
+        if l.dim() != 2 or rmat.dim() != 2 or l.shape[0] != rmat.shape[0]:
+            raise ValueError(f"{what}: row counts differ ({tuple(l.shape)} vs {tuple(rmat.shape)})")
+        m, p = l.shape
+        q = rmat.shape[1]
+        out = torch.empty((p, q) if layouts[i] == 0 else (q, p), device=dev, dtype=torch.float32)
+        keep += [l, l2, rmat]
+        outs.append(out)
+        descs[i] = _lib.LoraGradDesc(l.data_ptr(), _ptr(l2), p, int(modes[i]), rmat.data_ptr(),
+                                     max(rmat.stride(0), q), m, p, q, float(scales[i]), out.data_ptr(),
+                                     int(layouts[i]))
+    ws_bytes = int(_lib.load().molt_lora_grad_many_workspace(n, descs))
+    ws = torch.empty(max(ws_bytes, 256), device=dev, dtype=torch.uint8)
+    _call("molt_lora_grad_many", n, descs, ws.data_ptr(), ws_bytes, _stream(dev))
+    del keep
+    return outs
+
+
+@lora_grad_many.register_fake
+def _(ls, l2s, modes, rmats, scales, layouts):
+    return [l.new_empty((l.shape[1], r.shape[1]) if lay == 0 else (r.shape[1], l.shape[1]), dtype=torch.float32)
+            for l, r, lay in zip(ls, rmats, layouts)]
+
+
 @_custom_op(f"{NS}::lora_grad_rmsnorm", mutates_args=())
 def lora_grad_rmsnorm(x: Tensor, inv_rms: Tensor, norm_weight: Tensor, offset: float, rmat: Tensor,
                       scale: float, layout: int) -> Tensor:

@@ -161,3 +161,41 @@ def test_lora_grad_dma_replay_equals_register_and_materialised(m, p, q, layout):
     torch.cuda.synchronize()
     assert torch.equal(dma, reg)
     assert torch.equal(dma, mat)
+
+
+@pytest.mark.parametrize("case", ["cfg4_mlp", "projection_pair", "mixed_fallback"])
+def test_lora_grad_many_equals_separate_calls(case):
+    """Several gradients from one launch pair (molt_lora_grad_many) equal the
+    separate lora_grad calls bit for bit: the cfg4 gated-MLP backward's five
+    (dB over dY, dg, du with the column halves of T, dA over h, the paired dA
+    over X), a scheduled projection's dA/dB pair, and a set with an unaligned
+    and an empty gradient (run one after another)."""
+    print(f"lora_grad_many {case}", flush=True)
+    if case == "cfg4_mlp":
+        m, h, i, r = 8192, 4096, 14336, 64
+        dy, dg, du, hh, x = seeded((m, h), 30), seeded((m, i), 31), seeded((m, i), 32), seeded((m, i), 33), \
+            seeded((m, h), 34)
+        t_d, t_gu, u_d, u_gu = seeded((m, r), 35), seeded((m, 2 * r), 36), seeded((m, r), 37), seeded((m, 2 * r), 38)
+        sets = [(dy, None, 0, t_d, 2.0, 0), (dg, None, 0, t_gu[:, :r], 2.0, 0), (du, None, 0, t_gu[:, r:], 2.0, 0),
+                (hh, None, 0, u_d, 1.0, 1), (x, None, 0, u_gu, 1.0, 1)]
+    elif case == "projection_pair":
+        m, k, n, r = 4096, 1536, 256, 16
+        x, g = seeded((m, k), 40), seeded((m, n), 41)
+        u, t = seeded((m, r), 42), seeded((m, r), 43)
+        sets = [(x, None, 0, u, 1.0, 1), (g, None, 0, t, 0.5, 0)]
+    else:
+        sets = [(seeded((300, 200), 50), None, 0, seeded((300, 16), 51), 1.0, 1),
+                (seeded((1000, 203), 52), None, 0, seeded((1000, 13), 53), 0.5, 0),   # unaligned widths
+                (torch.empty((0, 64), device="cuda", dtype=torch.bfloat16), None, 0,
+                 torch.empty((0, 16), device="cuda", dtype=torch.bfloat16), 1.0, 1),
+                (seeded((4099, 512), 54), seeded((4099, 512), 55), 1, seeded((4099, 64), 56), 1.0, 1)]
+    sep = [ops.lora_grad(*s_) for s_ in sets]
+    many = ops.lora_grad_many([s_[0] for s_ in sets], [s_[1] for s_ in sets], [s_[2] for s_ in sets],
+                              [s_[3] for s_ in sets], [s_[4] for s_ in sets], [s_[5] for s_ in sets])
+    again = ops.lora_grad_many([s_[0] for s_ in sets], [s_[1] for s_ in sets], [s_[2] for s_ in sets],
+                               [s_[3] for s_ in sets], [s_[4] for s_ in sets], [s_[5] for s_ in sets])
+    torch.cuda.synchronize()
+    assert len(many) == len(sets)
+    for a_, b_, c_ in zip(sep, many, again):
+        assert a_.shape == b_.shape
+        assert torch.equal(a_, b_) and torch.equal(b_, c_)
