@@ -166,6 +166,35 @@ int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t ldz, int32_
                       int32_t lora_layout, int32_t r, uint16_t* out, int64_t ldo,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* The projection's adapter operand prepared ahead, for callers that project
+ * with the same adapter more than once or prepare several adapters at once
+ * (no counterpart in the reference, which casts each adapter under autocast
+ * per matmul). molt_lora_pack_many converts 1..8 fp32 adapters to the
+ * projection's bf16 fragment order in one launch: rows q < split from lora,
+ * the rest from lora2 (two stacked matrices of one layout without a copy;
+ * lora2 NULL and split = r for one). Each packed operand takes
+ * molt_lora_packed_bytes(D, r) bytes (16-byte aligned). molt_lora_project_packed
+ * is molt_lora_project over such an operand: no pack launch, and a workspace
+ * of molt_lora_project_packed_workspace(M, D, r) bytes (the split partials;
+ * often 0). Outputs are bitwise those of molt_lora_project on the same
+ * adapter. */
+typedef struct molt_lora_pack_desc {
+  const float* lora;
+  const float* lora2;
+  int32_t split;
+  int32_t layout;
+  int32_t r;
+  int64_t D;
+  uint16_t* packed;
+} molt_lora_pack_desc;
+size_t molt_lora_packed_bytes(int64_t D, int32_t r);
+int molt_lora_pack_many(int32_t n, const molt_lora_pack_desc* d, void* stream);
+size_t molt_lora_project_packed_workspace(int64_t M, int64_t D, int32_t r);
+int molt_lora_project_packed(const uint16_t* z, const uint16_t* z2, int64_t ldz, int32_t z_mode,
+                             float z_scale, int64_t M, int64_t D, const uint16_t* packed, int32_t r,
+                             uint16_t* out, int64_t ldo, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
 /* Y[M, N] = bf16( X . deq(W)^T + T . bf16(s * B)^T ), fp32 accumulation, with
  * X bf16 [M, K], T bf16 [M, r] = molt_lora_project(X, lora_a) and B fp32 [N, r]
  * (row stride r). `w->scales` must be resolved fp32 scales. r = 0 skips LoRA.

@@ -56,6 +56,18 @@ class LoraGradDesc(C.Structure):
 
 _GD = C.POINTER(LoraGradDesc)
 
+
+class LoraPackDesc(C.Structure):
+    """``molt_lora_pack_desc`` of include/molt_amd.h (one adapter of
+    ``molt_lora_pack_many``)."""
+    _fields_ = [
+        ("lora", C.c_void_p), ("lora2", C.c_void_p), ("split", C.c_int32), ("layout", C.c_int32),
+        ("r", C.c_int32), ("D", C.c_int64), ("packed", C.c_void_p),
+    ]
+
+
+_PD = C.POINTER(LoraPackDesc)
+
 # name -> (restype, argtypes); the exact list of include/molt_amd.h.
 SIGNATURES: dict[str, tuple] = {
     "molt_amd_last_error": (C.c_char_p, []),
@@ -70,6 +82,10 @@ SIGNATURES: dict[str, tuple] = {
     "molt_lora_project_workspace": (_sz, [_i64, _i64, _i32]),
     "molt_lora_project": (C.c_int, [_p, _p, _i64, _i32, _f32, _i64, _i64, _p, _i32, _i32, _p, _i64, _p, _sz,
                                     _p]),
+    "molt_lora_packed_bytes": (_sz, [_i64, _i32]),
+    "molt_lora_pack_many": (C.c_int, [_i32, _PD, _p]),
+    "molt_lora_project_packed_workspace": (_sz, [_i64, _i64, _i32]),
+    "molt_lora_project_packed": (C.c_int, [_p, _p, _i64, _i32, _f32, _i64, _i64, _p, _i32, _p, _i64, _p, _sz, _p]),
     "molt_amd_time_next_gemm": (C.c_int, [_p, _p]),
     "molt_nf4_lora_forward_workspace": (_sz, [_i64, _i64, _i64, _i32]),
     "molt_nf4_lora_forward": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _f32, _p, _i64, _p, _sz, _p]),

@@ -110,6 +110,54 @@ __global__ void lora_pack_kernel(const float* __restrict__ w, int layout, int R,
   }
 }
 
+// Several adapters packed in one launch (molt_lora_pack_many): fragment f of
+// adapter d is flat index first[d] + f, packed exactly as lora_pack_kernel
+// does; rows q < split[d] come from w0[d], the rest from w1[d] (the gate and
+// up A matrices stacked as one [2r, D] operand without a copy).
+constexpr int kPackMany = 8;
+struct PackMany {
+  const float* w0[kPackMany];
+  const float* w1[kPackMany];
+  uint16_t* wp[kPackMany];
+  int64_t D[kPackMany], steps[kPackMany];
+  int64_t first[kPackMany + 1];
+  int split[kPackMany], R[kPackMany], tq[kPackMany], layout[kPackMany];
+  int n;
+};
+
+__global__ void lora_pack_many_kernel(const PackMany m) {
+  const int64_t total = m.first[m.n];
+  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < total; g += (int64_t)gridDim.x * blockDim.x) {
+    int d = 0;
+#pragma unroll
+    for (int k = 1; k < kPackMany; ++k) d += (k < m.n && g >= m.first[k]) ? 1 : 0;
+    const int64_t f = g - m.first[d];
+    const int lane = (int)(f & 63);
+    const int64_t rest = f >> 6;
+    const int kk = (int)(rest & 3);
+    const int64_t st = rest >> 2;
+    const int tq = m.tq[d];
+    const int t = (int)(st % tq);
+    const int64_t step = st / tq;
+    const int q = 32 * t + (lane & 31);
+    const int64_t D = m.D[d], d0 = 64 * step + 32 * (lane >> 5) + 8 * kk;
+    const int R = m.R[d], split = m.split[d];
+    const bool first_src = q < split;
+    const float* w = first_src ? m.w0[d] : m.w1[d];
+    const int qs = first_src ? q : q - split, Rs = first_src ? split : R - split;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t dd = d0 + e;
+      v[e] = (q < R && dd < D) ? (m.layout[d] == 0 ? w[(int64_t)qs * D + dd] : w[dd * Rs + qs]) : 0.0f;
+    }
+    u32x4_t o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+    *reinterpret_cast<u32x4_t*>(m.wp[d] + f * 8) = o;
+  }
+}
+
 struct ProjParams {
   const uint16_t* z; const uint16_t* z2; int64_t ldz; int mode; float zs;
   int64_t M, D; int R;
@@ -974,6 +1022,10 @@ extern "C" size_t molt_lora_project_workspace(int64_t M, int64_t D, int32_t r) {
   return proj_packed_bytes(D, r) + part;
 }
 
+static int launch_projection(const uint16_t* z, const uint16_t* z2, int64_t ldz, int32_t z_mode, float z_scale,
+                             int64_t M, int64_t D, const uint16_t* wp, int32_t r, uint16_t* out, int64_t ldo,
+                             void* part, hipStream_t st, const char* who);
+
 extern "C" int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t ldz, int32_t z_mode, float z_scale,
                                  int64_t M, int64_t D, const float* lora, int32_t lora_layout, int32_t r,
                                  uint16_t* out, int64_t ldo, void* workspace, size_t workspace_bytes,
@@ -1000,10 +1052,78 @@ extern "C" int molt_lora_project(const uint16_t* z, const uint16_t* z2, int64_t 
   hipLaunchKernelGGL(lora_pack_kernel, dim3(pblocks), dim3(256), 0, st, lora, lora_layout, r, D, tq, steps, wp);
   int rc = check_launch(who);
   if (rc) return rc;
+  return launch_projection(z, z2, ldz, z_mode, z_scale, M, D, wp, r, out, ldo,
+                           (char*)workspace + proj_packed_bytes(D, r), st, who);
+}
+
+extern "C" size_t molt_lora_packed_bytes(int64_t D, int32_t r) {
+  return D > 0 && r > 0 ? proj_packed_bytes(D, r) : 0;
+}
+
+extern "C" int molt_lora_pack_many(int32_t n, const molt_lora_pack_desc* d, void* stream) {
+  const char* who = "molt_lora_pack_many";
+  MOLT_REQUIRE(d && n >= 1 && n <= kPackMany, MOLT_EINVAL, "%s: 1..%d adapters", who, kPackMany);
+  PackMany m{};
+  int64_t total = 0;
+  for (int i = 0; i < n; ++i) {
+    const molt_lora_pack_desc& a = d[i];
+    MOLT_REQUIRE(a.D > 0 && a.r > 0 && a.r <= 32 * PJ_TQ_MAX, MOLT_EINVAL, "%s: bad shape (adapter %d)", who, i);
+    MOLT_REQUIRE(a.layout == 0 || a.layout == 1, MOLT_EINVAL, "%s: bad layout (adapter %d)", who, i);
+    MOLT_REQUIRE(a.lora && a.packed && aligned(a.packed, 16), MOLT_EINVAL, "%s: null or unaligned (adapter %d)",
+                 who, i);
+    MOLT_REQUIRE(a.lora2 ? (a.split > 0 && a.split < a.r) : a.split == a.r, MOLT_EINVAL,
+                 "%s: bad split (adapter %d)", who, i);
+    m.w0[i] = a.lora; m.w1[i] = a.lora2 ? a.lora2 : a.lora; m.wp[i] = a.packed;
+    m.D[i] = a.D; m.steps[i] = ceil_div64(a.D, BK); m.split[i] = a.split; m.R[i] = a.r;
+    m.tq[i] = (int)proj_tq(a.r); m.layout[i] = a.layout;
+    m.first[i] = total;
+    total += m.steps[i] * m.tq[i] * 4 * 64;
+  }
+  m.first[n] = total;
+  m.n = n;
+  unsigned blocks = (unsigned)((total + 255) / 256);
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(lora_pack_many_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, m);
+  return check_launch(who);
+}
+
+extern "C" size_t molt_lora_project_packed_workspace(int64_t M, int64_t D, int32_t r) {
+  if (D <= 0 || r <= 0 || M < 0) return 0;
+  return molt_lora_project_workspace(M, D, r) - proj_packed_bytes(D, r);
+}
+
+extern "C" int molt_lora_project_packed(const uint16_t* z, const uint16_t* z2, int64_t ldz, int32_t z_mode,
+                                        float z_scale, int64_t M, int64_t D, const uint16_t* packed, int32_t r,
+                                        uint16_t* out, int64_t ldo, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
+  const char* who = "molt_lora_project_packed";
+  MOLT_REQUIRE(z_mode >= 0 && z_mode <= 2, MOLT_EINVAL, "%s: bad z_mode %d", who, z_mode);
+  MOLT_REQUIRE(M >= 0 && D > 0 && r > 0, MOLT_EINVAL, "%s: bad shape M=%lld D=%lld r=%d", who, (long long)M,
+               (long long)D, r);
+  MOLT_REQUIRE(r <= 32 * PJ_TQ_MAX, MOLT_EUNSUPPORTED, "%s: rank %d > %d", who, r, 32 * PJ_TQ_MAX);
+  if (M == 0) return MOLT_OK;
+  MOLT_REQUIRE(z && packed && aligned(packed, 16) && out && ldz >= D && ldo >= r, MOLT_EINVAL,
+               "%s: bad pointers/strides", who);
+  MOLT_REQUIRE(z_mode != 1 || z2, MOLT_EINVAL, "%s: SwiGLU replay needs the up tensor", who);
+  const size_t need = molt_lora_project_packed_workspace(M, D, r);
+  MOLT_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)), MOLT_EWORKSPACE,
+               "%s: workspace %zu < %zu bytes (or not 16-byte aligned)", who, workspace_bytes, need);
+  return launch_projection(z, z2, ldz, z_mode, z_scale, M, D, packed, r, out, ldo, workspace, (hipStream_t)stream,
+                           who);
+}
+
+// The projection kernel(s) over an adapter already packed at wp (split
+// partials, if any, at part); shared by molt_lora_project and
+// molt_lora_project_packed.
+static int launch_projection(const uint16_t* z, const uint16_t* z2, int64_t ldz, int32_t z_mode, float z_scale,
+                             int64_t M, int64_t D, const uint16_t* wp, int32_t r, uint16_t* out, int64_t ldo,
+                             void* part, hipStream_t st, const char* who) {
+  int rc = MOLT_OK;
+  const int tq = (int)proj_tq(r);
   ProjParams p{};
   p.z = z; p.z2 = z2; p.ldz = ldz; p.mode = z_mode; p.zs = z_scale;
   p.M = M; p.D = D; p.R = r; p.wp = wp; p.out = out; p.ldo = ldo;
-  p.part = (float*)((char*)workspace + proj_packed_bytes(D, r));
+  p.part = (float*)part;
   const bool vec = D % 8 == 0 && ldz % 8 == 0 && aligned(z, 16) && (z_mode != 1 || aligned(z2, 16));
   const int mt = proj_mt(M, tq, vec, z_mode);
   const int ks = vec ? proj_ksplit(M, D, mt) : 1;

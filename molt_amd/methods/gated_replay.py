@@ -169,13 +169,15 @@ def _take_wts(ctx):
 
 
 def _fused_forward(x, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_packed, down_a, down_b,
-                   gate_qs, up_qs, down_qs, gate_scaling, up_scaling, down_scaling, keep_wt=False):
+                   gate_qs, up_qs, down_qs, gate_scaling, up_scaling, down_scaling, keep_wt=False, grad=False):
     """Forward of the fused gated MLP on ``x`` [..., H]: gate/up as one
     dual-accumulator GEMM that also emits h, then the down projection.
-    Returns (y [tokens, H], gate, up, h, T_gu, T_d, (H, I, r), wts) with wts
-    the bf16 transposed weights (deq(Wg)^T, deq(Wu)^T, deq(Wd)^T) the GEMMs
-    wrote for the backward when ``keep_wt`` (each an empty tensor where they
-    did not stage the weight), else None."""
+    Returns (y [tokens, H], gate, up, h, T_gu, T_d, (H, I, r), wts, bpacks)
+    with wts the bf16 transposed weights (deq(Wg)^T, deq(Wu)^T, deq(Wd)^T) the
+    GEMMs wrote for the backward when ``keep_wt`` (each an empty tensor where
+    they did not stage the weight), else None, and bpacks the backward
+    projections' packed B_d, B_g, B_u when ``grad`` (packed in the same launch
+    as the forward's adapters), else None."""
     if x.device.type != "cuda" or x.dtype != torch.bfloat16:
         raise CapabilityError("fused gated NF4-LoRA MLP requires CUDA BF16 tensors")
     for t in (gate_a, gate_b, up_a, up_b, down_a, down_b):
@@ -191,7 +193,16 @@ def _fused_forward(x, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_p
     if up_a.shape[0] != r:
         raise ValueError("gate and up adapters must share a rank")
     flat = x.reshape(-1, h_dim)
-    t_gu = ops.direct.lora_project(flat, None, 0, 1.0, torch.cat([gate_a, up_a], 0), 0)
+    # every adapter operand of the step in one launch: [A_gate; A_up] and A_down
+    # for the forward's projections, B_down, B_gate, B_up for the backward's
+    if grad:
+        packs = ops.direct.lora_pack_many([gate_a, down_a, down_b, gate_b, up_b], [up_a, None, None, None, None],
+                                          [0, 0, 1, 1, 1])
+        bpacks = tuple(packs[2:])
+    else:
+        packs = ops.direct.lora_pack_many([gate_a, down_a], [up_a, None], [0, 0])
+        bpacks = None
+    t_gu = ops.direct.lora_project_packed(flat, None, 0, 1.0, packs[0], 2 * r)
     gu_args = (flat, gate_packed.reshape(-1), resolved_nf4_scales(gate_qs), up_packed.reshape(-1),
                resolved_nf4_scales(up_qs), gate_qs.code, i_dim, h_dim, nibble_order(gate_qs), t_gu, gate_b, up_b,
                float(gate_scaling), float(up_scaling))
@@ -200,7 +211,7 @@ def _fused_forward(x, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_p
         gate, up, gated, wgt, wut = ops.direct.nf4_gateup_forward_keep_wt(*gu_args)
     else:
         gate, up, gated = ops.direct.nf4_gateup_forward(*gu_args)
-    t_d = ops.direct.lora_project(gated, None, 0, 1.0, down_a, 0)
+    t_d = ops.direct.lora_project_packed(gated, None, 0, 1.0, packs[1], r)
     d_args = (gated, down_packed.reshape(-1), resolved_nf4_scales(down_qs), down_qs.code, h_dim, i_dim,
               nibble_order(down_qs), 64, t_d, down_b, float(down_scaling))
     if keep_wt:
@@ -208,11 +219,11 @@ def _fused_forward(x, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_p
         wts = (wgt, wut, wdt)
     else:
         y = ops.direct.nf4_lora_forward(*d_args)
-    return y, gate, up, gated, t_gu, t_d, (h_dim, i_dim, r), wts
+    return y, gate, up, gated, t_gu, t_d, (h_dim, i_dim, r), wts, bpacks
 
 
 def _fused_backward(grad_output, flat, gate, up, gated, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed,
-                    up_a, up_b, down_packed, down_a, down_b, qs, scaling, dims, norm=None, wts=None):
+                    up_a, up_b, down_packed, down_a, down_b, qs, scaling, dims, norm=None, wts=None, bpacks=None):
     """Backward of the fused gated MLP. ``flat`` is the projections' input
     [tokens, H]; ``gated`` is h when the forward kept it, else None (replayed
     from gate and up). With ``norm = (source, inv_rms, weight, offset)`` and
@@ -220,6 +231,8 @@ def _fused_backward(grad_output, flat, gate, up, gated, t_gu, t_d, gate_packed, 
     bf16 source as the gate/up adapters' gradient stages it. ``wts``: the
     transposed weights a keep_wt forward wrote (or None); the input gradients
     read them instead of staging the weights again (bitwise the same).
+    ``bpacks``: the packed B_d, B_g, B_u the forward made (or None: packed
+    here); the projections give bitwise the same U either way.
     Returns (dX [tokens, H], dA_g, dB_g, dA_u, dB_u, dA_d, dB_d)."""
     wgt, wut, wdt = wts if wts is not None else (None, None, None)
     del wts   # each copy is released as soon as its input gradient has run
@@ -227,13 +240,19 @@ def _fused_backward(grad_output, flat, gate, up, gated, t_gu, t_d, gate_packed, 
     s_g, s_u, s_d = scaling
     h_dim, i_dim, r = dims
     dy = grad_output.reshape(-1, h_dim).to(torch.bfloat16)
-    u_d = ops.direct.lora_project(dy, None, 2, s_d, down_b, 1)
+    if bpacks is not None:
+        u_d = ops.direct.lora_project_packed(dy, None, 2, s_d, bpacks[0], r)
+    else:
+        u_d = ops.direct.lora_project(dy, None, 2, s_d, down_b, 1)
     dg, du = ops.direct.nf4_swiglu_backward(dy, down_packed.reshape(-1), resolved_nf4_scales(down_qs), down_qs.code,
                                      h_dim, i_dim, nibble_order(down_qs), u_d, down_a, gate, up, wdt)
     del wdt
     # U_g and U_u as the column halves of one [tokens, 2r] matrix: the paired
     # input gradient reads the halves in place and dA_gate/dA_up share one pass
-    u_gu = ops.direct.lora_project_pair(dg, du, s_g, s_u, gate_b, up_b)
+    if bpacks is not None:
+        u_gu = ops.direct.lora_project_pair_packed(dg, du, s_g, s_u, bpacks[1], bpacks[2], r)
+    else:
+        u_gu = ops.direct.lora_project_pair(dg, du, s_g, s_u, gate_b, up_b)
     u_g, u_u = u_gu[:, :r], u_gu[:, r:]
     dx = ops.direct.nf4_lora_backward_input_pair(
         dg, du, gate_packed.reshape(-1), resolved_nf4_scales(gate_qs), up_packed.reshape(-1),
@@ -267,9 +286,10 @@ class _FusedGatedNF4LoRA(torch.autograd.Function):
     @staticmethod
     def forward(ctx: Any, x, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_packed, down_a,
                 down_b, gate_qs, up_qs, down_qs, gate_scaling, up_scaling, down_scaling, save_gated):
-        y, gate, up, gated, t_gu, t_d, dims, wts = _fused_forward(
+        y, gate, up, gated, t_gu, t_d, dims, wts, bpacks = _fused_forward(
             x, gate_packed, gate_a, gate_b, up_packed, up_a, up_b, down_packed, down_a, down_b, gate_qs,
-            up_qs, down_qs, gate_scaling, up_scaling, down_scaling, keep_wt=_keep_wt(ctx))
+            up_qs, down_qs, gate_scaling, up_scaling, down_scaling, keep_wt=_keep_wt(ctx),
+            grad=any(ctx.needs_input_grad))
         if not save_gated:
             gated = None  # replayed in backward from (gate, up)
         ctx.qs = (gate_qs, up_qs, down_qs)
@@ -278,7 +298,7 @@ class _FusedGatedNF4LoRA(torch.autograd.Function):
         ctx.input_shape = x.shape
         ctx.save_for_backward(x.reshape(-1, dims[0]), gate, up, gated, t_gu, t_d, gate_packed, gate_a, gate_b,
                               up_packed, up_a, up_b, down_packed, down_a, down_b)
-        ctx.wts = wts
+        ctx.wts, ctx.bpacks = wts, bpacks
         return y.reshape(*x.shape[:-1], dims[0])
 
     @staticmethod
@@ -288,7 +308,8 @@ class _FusedGatedNF4LoRA(torch.autograd.Function):
          down_a, down_b) = ctx.saved_tensors
         dx, dag, dbg, dau, dbu, dad, dbd = _fused_backward(
             grad_output, flat, gate, up, gated, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed, up_a, up_b,
-            down_packed, down_a, down_b, ctx.qs, ctx.scaling, ctx.dims, wts=_take_wts(ctx))
+            down_packed, down_a, down_b, ctx.qs, ctx.scaling, ctx.dims, wts=_take_wts(ctx),
+            bpacks=ctx.bpacks)
         return (dx.reshape(ctx.input_shape), None, dag, dbg, None, dau, dbu, None, dad, dbd,
                 None, None, None, None, None, None, None)
 
@@ -383,11 +404,11 @@ class _ResidualRecipeGatedNF4LoRA(torch.autograd.Function):
                 norm_eps, norm_weight_offset):
         if source.shape != normalized.shape:
             raise ValueError("the residual source and the normalised input must have the same shape")
-        y, gate, up, _, t_gu, t_d, dims, wts = _fused_forward(
+        y, gate, up, _, t_gu, t_d, dims, wts, bpacks = _fused_forward(
             normalized, gate_packed_weight, gate_lora_a, gate_lora_b, up_packed_weight, up_lora_a, up_lora_b,
             down_packed_weight, down_lora_a, down_lora_b, gate_quant_state, up_quant_state, down_quant_state,
-            gate_scaling, up_scaling, down_scaling, keep_wt=_keep_wt(ctx))
-        ctx.wts = wts
+            gate_scaling, up_scaling, down_scaling, keep_wt=_keep_wt(ctx), grad=any(ctx.needs_input_grad))
+        ctx.wts, ctx.bpacks = wts, bpacks
         ctx.qs = (gate_quant_state, up_quant_state, down_quant_state)
         ctx.scaling = (float(gate_scaling), float(up_scaling), float(down_scaling))
         ctx.dims = dims
@@ -415,7 +436,8 @@ class _ResidualRecipeGatedNF4LoRA(torch.autograd.Function):
             flat, norm = normalized.reshape(-1, ctx.dims[0]), None
         dx, dag, dbg, dau, dbu, dad, dbd = _fused_backward(
             grad_output, flat, gate, up, None, t_gu, t_d, gate_packed, gate_a, gate_b, up_packed, up_a, up_b,
-            down_packed, down_a, down_b, ctx.qs, ctx.scaling, ctx.dims, norm, wts=_take_wts(ctx))
+            down_packed, down_a, down_b, ctx.qs, ctx.scaling, ctx.dims, norm, wts=_take_wts(ctx),
+            bpacks=ctx.bpacks)
         return (None, dx.reshape(ctx.input_shape), None, dag, dbg, None, dau, dbu, None, dad, dbd,
                 None, None, None, None, None, None, None, None, None)
 

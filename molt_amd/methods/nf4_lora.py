@@ -64,7 +64,14 @@ class _ScheduledNF4LoRA(torch.autograd.Function):
                 "device, and compute dtype"
             )
         flat_x = x.reshape(-1, k)
-        low_rank = ops.direct.lora_project(flat_x, None, 0, 1.0, lora_a, 0)
+        # A (for this projection) and, when a gradient will flow, B (for the
+        # backward's) packed in one launch
+        ctx.b_packed = None
+        if any(ctx.needs_input_grad):
+            a_packed, ctx.b_packed = ops.direct.lora_pack_many([lora_a, lora_b], [None, None], [0, 1])
+        else:
+            a_packed = ops.direct.lora_pack_many([lora_a], [None], [0])[0]
+        low_rank = ops.direct.lora_project_packed(flat_x, None, 0, 1.0, a_packed, lora_a.shape[0])
         ctx.wt = None
         if gemv_applies(flat_x, quant_state, lora_a.shape[0]):
             # decode-sized batch: HBM-bound skinny-M GEMV instead of the MFMA GEMM
@@ -98,7 +105,12 @@ class _ScheduledNF4LoRA(torch.autograd.Function):
         flat_x = x.reshape(-1, k)
         flat_grad = grad_output.reshape(-1, n).to(torch.bfloat16)
         scales = resolved_nf4_scales(qs)
-        grad_through_b = ops.direct.lora_project(flat_grad, None, 2, ctx.scaling, lora_b, 1)
+        b_packed, ctx.b_packed = ctx.b_packed, None
+        if b_packed is not None:
+            grad_through_b = ops.direct.lora_project_packed(flat_grad, None, 2, ctx.scaling, b_packed,
+                                                            lora_b.shape[1])
+        else:
+            grad_through_b = ops.direct.lora_project(flat_grad, None, 2, ctx.scaling, lora_b, 1)
         wt, ctx.wt = ctx.wt, None
         grad_x = ops.direct.nf4_lora_backward_input(flat_grad, packed_weight.reshape(-1), scales, qs.code, n, k,
                                              nibble_order(qs), int(qs.blocksize), grad_through_b, lora_a, 1.0, wt)

@@ -484,6 +484,108 @@ def _(z0, z1, zscale0, zscale1, lora0, lora1):
     return z0.new_empty((z0.shape[0], 2 * lora0.shape[1]), dtype=torch.bfloat16)
 
 
+@_custom_op(f"{NS}::lora_pack_many", mutates_args=())
+def lora_pack_many(loras: list[Tensor], loras2: list[Optional[Tensor]], layouts: list[int]) -> list[Tensor]:
+    """The projection's bf16 fragment-order operands of 1..8 fp32 adapters in
+    one launch (molt_lora_pack_many), as uint8 tensors for
+    ``lora_project_packed``. ``loras2[i]`` (or None) is stacked after
+    ``loras[i]`` (rows for layout 0 = A [r, D], columns for layout 1 = B
+    [D, r]), so [A_gate; A_up] needs no copy."""
+    what = "LoRA pack"
+    n = len(loras)
+    if not (1 <= n <= 8) or len(loras2) != n or len(layouts) != n:
+        raise ValueError(f"{what}: 1..8 adapters with one entry per argument list")
+    dev = _require_gpu(*loras, *[t for t in loras2 if t is not None], what=what)
+    descs = (_lib.LoraPackDesc * n)()
+    keep, outs = [], []
+    lib = _lib.load()
+    for i in range(n):
+        a = _f32(loras[i])
+        b = None if loras2[i] is None else _f32(loras2[i])
+        lay = int(layouts[i])
+        if a.dim() != 2 or (b is not None and (b.dim() != 2 or (b.shape[1] if lay == 0 else b.shape[0]) !=
+                                               (a.shape[1] if lay == 0 else a.shape[0]))):
+            raise ValueError(f"{what}: adapters {tuple(a.shape)} and {None if b is None else tuple(b.shape)} "
+                             f"do not stack in layout {lay}")
+        d = a.shape[1] if lay == 0 else a.shape[0]
+        split = a.shape[0] if lay == 0 else a.shape[1]
+        r = split + (0 if b is None else (b.shape[0] if lay == 0 else b.shape[1]))
+        out = torch.empty(int(lib.molt_lora_packed_bytes(d, r)), device=dev, dtype=torch.uint8)
+        keep += [a, b]
+        outs.append(out)
+        descs[i] = _lib.LoraPackDesc(a.data_ptr(), _ptr(b), split, lay, r, d, out.data_ptr())
+    _call("molt_lora_pack_many", n, descs, _stream(dev))
+    del keep
+    return outs
+
+
+@lora_pack_many.register_fake
+def _(loras, loras2, layouts):
+    lib = _lib.load()
+    outs = []
+    for a, b, lay in zip(loras, loras2, layouts):
+        d = a.shape[1] if lay == 0 else a.shape[0]
+        r = (a.shape[0] if lay == 0 else a.shape[1]) + (0 if b is None else (b.shape[0] if lay == 0 else b.shape[1]))
+        outs.append(a.new_empty((int(lib.molt_lora_packed_bytes(d, r)),), dtype=torch.uint8))
+    return outs
+
+
+@_custom_op(f"{NS}::lora_project_packed", mutates_args=())
+def lora_project_packed(z: Tensor, z2: Optional[Tensor], mode: int, zscale: float, packed: Tensor,
+                        r: int) -> Tensor:
+    """``lora_project`` over an adapter packed by ``lora_pack_many`` (rank r,
+    width z.shape[1]): no pack launch; bitwise the same output."""
+    what = "LoRA projection"
+    dev = _require_gpu(z, z2, packed, what=what)
+    z = _bf16(z, "activations", what)
+    z2 = None if z2 is None else _bf16(z2, "activations", what)
+    if z.dim() != 2 or (z2 is not None and z2.shape != z.shape):
+        raise ValueError(f"{what}: expected a 2-D activation (and a second operand of the same shape)")
+    m, d = z.shape
+    if packed.dtype != torch.uint8 or packed.numel() != int(_lib.load().molt_lora_packed_bytes(d, r)):
+        raise ValueError(f"{what}: the packed adapter does not match width {d} and rank {r}")
+    out = torch.empty((m, r), device=dev, dtype=torch.bfloat16)
+    ws_bytes = _workspace("molt_lora_project_packed_workspace", m, d, r)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
+    _call("molt_lora_project_packed", z.data_ptr(), _ptr(z2), d, mode, zscale, m, d, packed.data_ptr(), r,
+          out.data_ptr(), r, _ptr(ws), ws_bytes, _stream(dev))
+    return out
+
+
+@lora_project_packed.register_fake
+def _(z, z2, mode, zscale, packed, r):
+    return z.new_empty((z.shape[0], r), dtype=torch.bfloat16)
+
+
+@_custom_op(f"{NS}::lora_project_pair_packed", mutates_args=())
+def lora_project_pair_packed(z0: Tensor, z1: Tensor, zscale0: float, zscale1: float, packed0: Tensor,
+                             packed1: Tensor, r: int) -> Tensor:
+    """``lora_project_pair`` over adapters packed by ``lora_pack_many`` (layout
+    1, rank r each): no pack launches; bitwise the same output."""
+    what = "LoRA projection pair"
+    dev = _require_gpu(z0, z1, packed0, packed1, what=what)
+    z0 = _bf16(z0, "activations", what)
+    z1 = _bf16(z1, "activations", what)
+    if z0.dim() != 2 or z1.shape != z0.shape:
+        raise ValueError(f"{what}: expected two 2-D activations of one shape")
+    m, d = z0.shape
+    nbytes = int(_lib.load().molt_lora_packed_bytes(d, r))
+    if packed0.numel() != nbytes or packed1.numel() != nbytes:
+        raise ValueError(f"{what}: the packed adapters do not match width {d} and rank {r}")
+    out = torch.empty((m, 2 * r), device=dev, dtype=torch.bfloat16)
+    ws_bytes = _workspace("molt_lora_project_packed_workspace", m, d, r)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
+    for half, (z, zs, pk) in enumerate(((z0, zscale0, packed0), (z1, zscale1, packed1))):
+        _call("molt_lora_project_packed", z.data_ptr(), None, d, 2, zs, m, d, pk.data_ptr(), r,
+              out.data_ptr() + half * r * out.element_size(), 2 * r, _ptr(ws), ws_bytes, _stream(dev))
+    return out
+
+
+@lora_project_pair_packed.register_fake
+def _(z0, z1, zscale0, zscale1, packed0, packed1, r):
+    return z0.new_empty((z0.shape[0], 2 * r), dtype=torch.bfloat16)
+
+
 _KEEP_WT = [os.environ.get("MOLT_KEEP_WEIGHT_TRANSPOSES", "1") != "0"]
 
 

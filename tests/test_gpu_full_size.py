@@ -98,10 +98,14 @@ def test_cfg4_full_size_adapter_gradients_and_intermediates():
     x = seeded((M, H), 410)
     dy = seeded((M, H), 411)
     with torch.no_grad():
-        y, gate, up, h, t_gu, t_d, dims = _fused_forward(x, pg, ag, bg, pu, au, bu, pd, ad, bd, qg, qu, qd,
-                                                         s, s, s)
+        # the training path: transposed weights and packed B handed from the forward to the backward
+        y, gate, up, h, t_gu, t_d, dims, wts, bpacks = _fused_forward(x, pg, ag, bg, pu, au, bu, pd, ad, bd, qg,
+                                                                      qu, qd, s, s, s, keep_wt=True, grad=True)
+        assert wts is not None and all(w.numel() > 0 for w in wts), "cfg4 stages and keeps every weight"
         dx, dag, dbg, dau, dbu, dad, dbd = _fused_backward(dy, x, gate, up, h, t_gu, t_d, pg, ag, bg, pu, au, bu,
-                                                           pd, ad, bd, (qg, qu, qd), (s, s, s), dims)
+                                                           pd, ad, bd, (qg, qu, qd), (s, s, s), dims, wts=wts,
+                                                           bpacks=bpacks)
+        del wts, bpacks
         sc = molt_amd.resolved_nf4_scales
         u_d = ops.lora_project(dy, None, 2, s, bd, 1)
         dg, du = ops.nf4_swiglu_backward(dy, pd.reshape(-1), sc(qd), qd.code, H, I, 1, u_d, ad, gate, up)

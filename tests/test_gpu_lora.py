@@ -199,3 +199,36 @@ def test_lora_grad_many_equals_separate_calls(case):
     for a_, b_, c_ in zip(sep, many, again):
         assert a_.shape == b_.shape
         assert torch.equal(a_, b_) and torch.equal(b_, c_)
+
+
+@pytest.mark.parametrize("m,d,r,mode,layout,stacked", [
+    (8192, 4096, 64, 0, 0, True),     # [A_gate; A_up] stacked without a copy (rank 128)
+    (8192, 14336, 64, 0, 0, False),   # A_down over h
+    (8192, 4096, 64, 2, 1, False),    # B_down over s dY
+    (300, 4096, 16, 2, 1, True),      # small M: the K split and its partials; stacked B columns
+    (70, 200, 8, 0, 0, False),        # tails (the register kernel)
+])
+def test_lora_pack_many_and_packed_projection_equal_lora_project(m, d, r, mode, layout, stacked):
+    """Adapters packed several to a launch (molt_lora_pack_many) and projected
+    without a pack launch give bitwise the output of lora_project on the same
+    (stacked) adapter."""
+    print(f"lora_pack_many + project_packed m={m} d={d} r={r} mode={mode} layout={layout} stacked={stacked}",
+          flush=True)
+    z = seeded((m, d), 60)
+    shape = (r, d) if layout == 0 else (d, r)
+    a0, a1 = uniform(shape, 61, 1 / np.sqrt(d)), uniform(shape, 62, 1 / np.sqrt(d))
+    other = uniform((16, 96), 63, 0.1)   # a second adapter packed in the same launch
+    packs = ops.lora_pack_many([other, a0], [None, a1 if stacked else None], [0, layout])
+    full = torch.cat([a0, a1], 0 if layout == 0 else 1) if stacked else a0
+    rr = 2 * r if stacked else r
+    ref = ops.lora_project(z, None, mode, 0.5, full, layout)
+    got = ops.lora_project_packed(z, None, mode, 0.5, packs[1], rr)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    assert torch.equal(ops.lora_project_packed(seeded((5, 96), 64), None, 0, 1.0, packs[0], 16),
+                       ops.lora_project(seeded((5, 96), 64), None, 0, 1.0, other, 0))
+    if layout == 1 and not stacked:
+        z1 = seeded((m, d), 65)
+        p2 = ops.lora_pack_many([a0, a1], [None, None], [1, 1])
+        pair = ops.lora_project_pair_packed(z, z1, 0.5, 2.0, p2[0], p2[1], r)
+        assert torch.equal(pair, ops.lora_project_pair(z, z1, 0.5, 2.0, a0, a1))
