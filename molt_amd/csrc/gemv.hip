@@ -511,7 +511,9 @@ void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
   // stores, and the barrier after them, do not wait for the weight stream.
   // One token at K = 4096: the lane's 64 elements of X (16-byte chunks
   // 256 i + 4 lane + h, the elements its weight bytes multiply) stay in
-  // registers, read straight from memory; otherwise X is staged in LDS.
+  // registers, read straight from memory; otherwise X is staged in LDS. (At
+  // K = 14336 with two rounds per wave the 112 registers fit, but the decode
+  // measured slower: 11.3 -> 12.5 us at 4096 x 14336.)
   constexpr bool XREG = IPR == 2 && MX == 1;
   constexpr int XCH = IPR * 256, XIT = XREG ? 0 : (MX * XCH + GD_NT - 1) / GD_NT;   // 16-byte chunks of X
   // X rows in LDS take whole pieces (IPR x 2048 elements); chunks past the end
@@ -630,9 +632,11 @@ void nf4_gemv_dot_kernel(const GemvParams p, int rounds) {
 // slice in every row, so each wave's X fragments (16 rows of X, 128 bytes
 // per lane) are loaded once and stay in registers. With one slice the
 // outputs are stored as bf16; with several (K = 14336: four slices of 3584)
-// each slice writes fp32 partials that gm_reduce_kernel sums in slice order. A round's loads (8 bytes per lane per block, the block
-// statistics, and for waves w < r / 32 the LoRA B rows of rank chunk w) are
-// issued two rounds ahead into three rotating register sets. Per block, two
+// each slice writes fp32 partials that gm_reduce_kernel sums in slice order.
+// A round's loads (16 bytes per lane per pair of blocks, the block
+// statistics, the LoRA B entries of the wave's rank chunk) are issued two
+// rounds ahead into three rotating register sets (with one round per
+// workgroup, ONE, only that round is loaded). Per block, two
 // v_mfma_f32_16x16x32_bf16 over bf16 code pairs from the replicated LDS table
 // give the block's partial products, scaled by the block scale in fp32 (as in
 // nf4_gemv_kernel); the 8 waves' 16 x 16 partials are summed through a
@@ -642,30 +646,44 @@ constexpr int GM_NT = 64 * GM_WAVES;
 
 // mode 0: resolved fp32 scales; 1: nested, one u8 code per block; 2: nested,
 // the codes of 4 blocks in one 4-byte load sharing one absmax2 entry.
-template <int SM>
+// LV: 0 no LoRA; 1 LoRA B rows read as 16-byte vectors (r % 4 == 0, 16-byte
+// aligned); 2 LoRA B rows read one float at a time.
+template <int SM, int LV>
 struct GmRound {
   static constexpr int NS = SM == 2 ? 2 : 8;
-  u32x2_t w[8];
+  static constexpr int NL = LV == 0 ? 1 : 8;
+  u32x4_t w[4];                                           // blocks 2i, 2i + 1: see gm_load
   uint32_t q[NS];
   float s[NS];
-  f32x4_t lb[2];
+  float lb[NL];
 };
 
+// Code-pair table at a 256-byte entry stride (see GdSmem): a lookup address is
+// one v_perm_b32 of the packed dword.
 struct GmSmem {
-  uint32_t tab[256 * GV_TABW];                            // bf16 code pair of byte b at [b * 32 + copy]
+  uint32_t tab[256 * 64];
   float code2s[256];
   f32x4_t red[2][GM_WAVES][64];
 };
 
-template <int SM>
-MOLT_DEV void gm_load(GmRound<SM>& R, const GemvParams& p, int64_t grp, int kw, int col, int g, bool lora) {
-  // kw: first element of the wave's 512-element K range
+// Loads of one round: 16-row group `grp` (clamped to the last group by the
+// caller, so every address is in bounds) over the wave's 512 elements at kw.
+// Every load is unconditional, so each round issues the same fixed number of
+// loads and the compiler's vmcnt wait before a round's arithmetic counts the
+// two later rounds as still in flight (a load under a branch made it wait for
+// them too). The LoRA B entries of rank chunk jc (8 ranks per lane group g)
+// are clamped into the row; the T fragment is zero for the ranks past r.
+template <int SM, int LV>
+MOLT_DEV void gm_load(GmRound<SM, LV>& R, const GemvParams& p, int64_t grp, int kw, int col, int g, int jc) {
   const int64_t n = 16 * grp + col < p.N ? 16 * grp + col : p.N - 1;
   const uint32_t blk0 = (uint32_t)(n * (p.K >> 6) + (kw >> 6));
-  const uint32_t wofs = (uint32_t)(n * (p.K >> 1) + (kw >> 1) + 8 * g);
+  // 16 bytes per lane: lane groups g = 0, 1 read bytes 16 g .. 16 g + 15 of
+  // block 2i, groups 2, 3 bytes 16 (g - 2) .. of block 2i + 1, so one load
+  // instruction covers 64 contiguous bytes of each of its 16 rows
+  const uint32_t wofs = (uint32_t)(n * (p.K >> 1) + (kw >> 1) + 16 * g);
 #pragma unroll
-  for (int b = 0; b < 8; ++b) R.w[b] = *reinterpret_cast<const u32x2_t*>(p.packed + wofs + 32u * b);
-  if (SM == 2) {
+  for (int i = 0; i < 4; ++i) R.w[i] = *reinterpret_cast<const u32x4_t*>(p.packed + wofs + 64u * i);
+  if constexpr (SM == 2) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       R.q[u] = *reinterpret_cast<const uint32_t*>(p.q + blk0 + 4 * u);
@@ -674,7 +692,7 @@ MOLT_DEV void gm_load(GmRound<SM>& R, const GemvParams& p, int64_t grp, int kw, 
   } else {
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
-      if (SM == 0) {
+      if constexpr (SM == 0) {
         R.q[b] = 0;
         R.s[b] = p.scales[blk0 + b];
       } else {
@@ -683,57 +701,108 @@ MOLT_DEV void gm_load(GmRound<SM>& R, const GemvParams& p, int64_t grp, int kw, 
       }
     }
   }
-  if (lora) {
-    const int j = 32 * ((kw >> 9) & 7) + 8 * g;                        // rank chunk = wave index
-    const float* br = p.lb + n * p.r + j;
-    const bool full = j + 8 <= p.r && (((uintptr_t)br) & 15) == 0;
-    if (full) {
-      R.lb[0] = *reinterpret_cast<const f32x4_t*>(br);
-      R.lb[1] = *reinterpret_cast<const f32x4_t*>(br + 4);
-    } else {
+  const int j = jc + 8 * g;                                            // first rank of the lane's 8
+  if constexpr (LV == 1) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float v = j + e < p.r ? p.lb[n * p.r + j + e] : 0.0f;
-        R.lb[e >> 2][e & 3] = v;
-      }
+    for (int h = 0; h < 2; ++h) {
+      const int jj = j + 4 * h;
+      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(p.lb + n * p.r + (jj < p.r ? jj : p.r - 4));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) R.lb[4 * h + e] = v[e];
     }
+  } else if constexpr (LV == 2) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) R.lb[e] = p.lb[n * p.r + (j + e < p.r ? j + e : p.r - 1)];
   }
 }
 
+// Block scale: the resolved fp32 scale, or code2[u8 code] * absmax2 + offset
+// (the nested statistics, as gv_scale computes them).
 template <int SM>
-MOLT_DEV f32x4_t gm_compute(const GmRound<SM>& R, const GemvParams& p, const uint32_t* tab, const float* code2s,
-                            const u32x4_t (&xf)[8][2], const u32x4_t& tf, bool lora) {
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+MOLT_DEV float gm_scale(const GemvParams& p, const float* code2s, uint32_t q, float s) {
+#pragma clang fp contract(off)
+  if constexpr (SM == 0) {
+    return s;
+  } else {
+    const float prod = code2s[q & 0xffu] * s;
+    return prod + p.offset;
+  }
+}
+
+// One round of one wave: 8 blocks of 64 elements of 16 rows. Each block's two
+// MFMAs go to an accumulator of their own and the block scales are applied
+// after all 16 MFMAs, so no MFMA result is waited for inside the loop; the sum
+// over blocks runs in block order (acc += scale * block partial).
+template <int SM, int LV>
+MOLT_DEV f32x4_t gm_compute(const GmRound<SM, LV>& R, const GemvParams& p, const char* tab, uint32_t lb,
+                            const float* code2s, const u32x4_t (&xf)[8][2], const u32x4_t& tf) {
+  float sc[8];
 #pragma unroll
-  for (int b = 0; b < 8; ++b) {
-    u32x4_t w0, w1;
+  for (int b = 0; b < 8; ++b)
+    sc[b] = SM == 2 ? gm_scale<SM>(p, code2s, R.q[b / 4] >> (8 * (b % 4)), R.s[b / 4])
+                    : gm_scale<SM>(p, code2s, R.q[b % GmRound<SM, LV>::NS], R.s[b % GmRound<SM, LV>::NS]);
+  // Each lane holds 16 bytes of block 2i (lane groups 0, 1) or 2i + 1 (groups
+  // 2, 3). Swapping dwords 2, 3 of the lower 32 lanes with dwords 0, 1 of the
+  // upper 32 (v_permlane32_swap) leaves every lane two dwords of each block:
+  // dword t of block 2i + e sits in wd[i][2 e + t], and in lane group g it holds
+  // the block's elements 16 gk(g) + 8 t .. + 7, gk = {0, 2, 1, 3}[g] (the X
+  // fragments follow the same order), so both MFMAs of a block sum only that
+  // block.
+  u32x4_t wd[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const auto s02 = __builtin_amdgcn_permlane32_swap(R.w[i][0], R.w[i][2], false, false);
+    const auto s13 = __builtin_amdgcn_permlane32_swap(R.w[i][1], R.w[i][3], false, false);
+    wd[i][0] = s02[0]; wd[i][2] = s02[1]; wd[i][1] = s13[0]; wd[i][3] = s13[1];
+  }
+  // The lookups of block b + 1 are issued before the MFMAs of block b (the
+  // scheduling barriers keep that order), so each block's LDS latency hides
+  // behind the previous block's MFMAs.
+  u32x4_t wl[2][2];
+  auto look = [&](int b, u32x4_t (&w)[2]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      w0[j] = tab[((R.w[b][0] >> (8 * j)) & 0xffu) * GV_TABW];
-      w1[j] = tab[((R.w[b][1] >> (8 * j)) & 0xffu) * GV_TABW];
+      // bits 15:8 = byte j of the dword, bits 7:0 = the lane's copy offset
+      const uint32_t sel = 0x0C0C0400u | ((uint32_t)j << 8);
+      w[0][j] = *reinterpret_cast<const uint32_t*>(tab + __builtin_amdgcn_perm(wd[b >> 1][2 * (b & 1)], lb, sel));
+      w[1][j] = *reinterpret_cast<const uint32_t*>(tab + __builtin_amdgcn_perm(wd[b >> 1][2 * (b & 1) + 1], lb, sel));
     }
-    f32x4_t tmp = {0.f, 0.f, 0.f, 0.f};
-    tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, xf[b][0]),
-                                                  __builtin_bit_cast(bf16x8v, w0), tmp, 0, 0, 0);
-    tmp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, xf[b][1]),
-                                                  __builtin_bit_cast(bf16x8v, w1), tmp, 0, 0, 0);
-    const float sc = SM == 2 ? gv_scale(p, code2s, R.q[b / 4] >> (8 * (b % 4)), R.s[b / 4])
-                             : gv_scale(p, code2s, R.q[b], R.s[b]);
+  };
+  f32x4_t tmp[8];
+  look(0, wl[0]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] += sc * tmp[e];
+  for (int b = 0; b < 8; ++b) {
+    if (b + 1 < 8) look(b + 1, wl[(b + 1) & 1]);
+    __builtin_amdgcn_sched_barrier(0);
+    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+    tmp[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, xf[b][0]),
+                                                     __builtin_bit_cast(bf16x8v, wl[b & 1][0]), zero, 0, 0, 0);
+    tmp[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, xf[b][1]),
+                                                     __builtin_bit_cast(bf16x8v, wl[b & 1][1]), tmp[b], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
   }
-  if (lora) {
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int b = 0; b < 8; ++b)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += sc[b] * tmp[b][e];
+  if constexpr (LV != 0) {
+    // every wave runs the LoRA step, so each round consumes its B loads (a
+    // load whose value one path never reads made the compiler wait for the
+    // whole stream at the loop head). T is zero for the ranks past r and on
+    // waves holding no rank of slice 0, so the clamped B entries there (finite
+    // entries of the same row) add nothing; B itself is not masked, which would
+    // place a wait right after its load.
     u32x4_t bw;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      bw[e] = pack_bf16x2(p.s * R.lb[e >> 1][2 * (e & 1)], p.s * R.lb[e >> 1][2 * (e & 1) + 1]);
+    for (int e = 0; e < 4; ++e) bw[e] = pack_bf16x2(p.s * R.lb[2 * e], p.s * R.lb[2 * e + 1]);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v, tf), __builtin_bit_cast(bf16x8v, bw),
                                                   acc, 0, 0, 0);
   }
   return acc;
 }
 
-template <int SM, int NW>
+template <int SM, int NW, int LV, bool ONE>
 __global__ __launch_bounds__(GM_NT) void nf4_gemv_ms_kernel(const GemvParams p, int rounds, float* part) {
   static_assert(NW >= 4 && NW <= GM_WAVES, "K slice of NW x 512 elements");
   __shared__ GmSmem sm;
@@ -741,46 +810,53 @@ __global__ __launch_bounds__(GM_NT) void nf4_gemv_ms_kernel(const GemvParams p, 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, g = lane >> 4;
   const bool active = NW == GM_WAVES || wave < NW;                     // waves >= NW only help reduce
-  const int kw = (int)blockIdx.y * NW * 512 + 512 * wave;              // the wave's K range
-  const bool lora = active && blockIdx.y == 0 && 32 * wave < p.r;      // rank chunk `wave`, slice 0 only
+  // the wave's K range (a wave past NW loads wave 0's range and discards it)
+  const int kw = (int)blockIdx.y * NW * 512 + 512 * (active ? wave : 0);
+  const int jc = 32 * (active ? wave : 0);                             // the wave's LoRA rank chunk
+  const bool lora = LV != 0 && active && blockIdx.y == 0 && jc < p.r;  // slice 0 only
 
   typedef __attribute__((address_space(4))) const f32x4_t* cptr_t;
   const cptr_t cbp = (cptr_t)p.code;
   const f32x4_t cb0 = cbp[0], cb1 = cbp[1], cb2 = cbp[2], cb3 = cbp[3];
-  const float c2 = p.code2 ? p.code2[tid & 255] : 0.0f;
+  float c2 = 0.0f;
+  if constexpr (SM != 0) c2 = p.code2[tid & 255];
 
   // X fragments of the wave's K slice (rows >= M repeat row M - 1; their
-  // outputs are never stored) and the wave's T fragment.
+  // outputs are never stored) and the wave's T fragment (ranks past r: 0).
+  const int mc = col < p.M ? col : p.M - 1;
   u32x4_t xf[8][2];
-  if (active) {
-    const int mc = col < p.M ? col : p.M - 1;
-    const uint16_t* xr = p.x + (int64_t)mc * p.ldx + kw + 16 * g;
+  {
+    const uint16_t* xr = p.x + (int64_t)mc * p.ldx + kw + 32 * (g & 1) + 16 * (g >> 1);
 #pragma unroll
     for (int b = 0; b < 8; ++b)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) xf[b][h] = *reinterpret_cast<const u32x4_t*>(xr + 64 * b + 8 * h);
+      for (int h = 0; h < 2; ++h) xf[b][h] = *reinterpret_cast<const u32x4_t*>(xr + 64 * b + 8 * h);   // see gm_compute
   }
   u32x4_t tf = {0u, 0u, 0u, 0u};
-  if (lora) {
-    const int mc = col < p.M ? col : p.M - 1;
+  if constexpr (LV != 0) {
     uint16_t e[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int j = 32 * wave + 8 * g + i;
-      e[i] = j < p.r ? p.t[(int64_t)mc * p.ldt + j] : (uint16_t)0;
+      const int j = jc + 8 * g + i;
+      const uint16_t v = p.t[(int64_t)mc * p.ldt + (j < p.r ? j : p.r - 1)];
+      e[i] = lora && j < p.r ? v : (uint16_t)0;
     }
     tf = __builtin_bit_cast(u32x4_t, e);
   }
+  // the small loads above stay ahead of the weight stream (a wait for one of
+  // them placed after the weight loads would wait for the stream too)
+  __builtin_amdgcn_sched_barrier(0);
 
-  GmRound<SM> b0, b1, b2;
-  const int64_t g0 = blockIdx.x, gs = gridDim.x;
-  if (active) gm_load(b0, p, g0, kw, col, g, lora);
-  if (active && rounds > 1) gm_load(b1, p, g0 + gs, kw, col, g, lora);
+  GmRound<SM, LV> b0, b1, b2;
+  const int64_t g0 = blockIdx.x, gs = gridDim.x, glast = (p.N - 1) >> 4;
+  auto grp = [&](int j) { const int64_t v = g0 + (int64_t)j * gs; return v < glast ? v : glast; };
+  gm_load(b0, p, grp(0), kw, col, g, jc);
+  if constexpr (!ONE) gm_load(b1, p, grp(1), kw, col, g, jc);
 
   {
     const float cv[16] = {cb0[0], cb0[1], cb0[2], cb0[3], cb1[0], cb1[1], cb1[2], cb1[3],
                           cb2[0], cb2[1], cb2[2], cb2[3], cb3[0], cb3[1], cb3[2], cb3[3]};
-    static_assert(GV_TABW == 32 && GM_NT == 512, "table build covers 256 x 32 entries");
+    static_assert(GM_NT == 512, "table build covers 256 x 32 entries");
     const int lo = (tid >> 5) & 15, copy = tid & 31;
     float clo = cv[0];
 #pragma unroll
@@ -788,18 +864,24 @@ __global__ __launch_bounds__(GM_NT) void nf4_gemv_ms_kernel(const GemvParams p, 
 #pragma unroll
     for (int hi = 0; hi < 16; ++hi) {
       const float first = p.order ? cv[hi] : clo, second = p.order ? clo : cv[hi];
-      sm.tab[(hi * 16 + lo) * GV_TABW + copy] = pack_bf16x2(first, second);
+      sm.tab[(hi * 16 + lo) * 64 + copy] = pack_bf16x2(first, second);
     }
-    if (tid < 256) sm.code2s[tid] = c2;
+    sm.code2s[tid & 255] = c2;                       // every thread: no branch around the load
   }
   __syncthreads();
-  const uint32_t* tab = sm.tab + (lane & 31);
+  const char* tab = reinterpret_cast<const char*>(sm.tab);
+  const uint32_t lb = (uint32_t)(lane & 31) * 4;
 
   // Round j: partials into red[j & 1], barrier, threads 0..255 sum (in wave
-  // order) and store bf16, or an fp32 partial of this K slice.
+  // order) and store bf16, or an fp32 partial of this K slice. The barrier
+  // waits for the LDS stores only (no fence), so the weight loads of the next
+  // two rounds stay in flight across it. red[j & 1] is written again in round
+  // j + 2, after every thread has passed round j + 1's barrier, which each
+  // reaches only after its reads of round j have completed.
   auto finish = [&](const f32x4_t& acc, int j) {
-    if (active) sm.red[j & 1][wave][lane] = acc;
-    __syncthreads();
+    sm.red[j & 1][wave][lane] = acc;
+    __builtin_amdgcn_s_waitcnt(0xC07F);              // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
     if (tid < 256) {
       const int ln = tid >> 2, e = tid & 3;
       float v = 0.0f;
@@ -814,16 +896,26 @@ __global__ __launch_bounds__(GM_NT) void nf4_gemv_ms_kernel(const GemvParams p, 
     }
   };
   const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < rounds; j += 3) {
-    if (active && j + 2 < rounds) gm_load(b2, p, g0 + (j + 2) * gs, kw, col, g, lora);
-    finish(active ? gm_compute(b0, p, tab, sm.code2s, xf, tf, lora) : zero, j);
-    if (j + 1 >= rounds) break;
-    if (active && j + 3 < rounds) gm_load(b0, p, g0 + (j + 3) * gs, kw, col, g, lora);
-    finish(active ? gm_compute(b1, p, tab, sm.code2s, xf, tf, lora) : zero, j + 1);
-    if (j + 2 >= rounds) break;
-    if (active && j + 4 < rounds) gm_load(b1, p, g0 + (j + 4) * gs, kw, col, g, lora);
-    finish(active ? gm_compute(b2, p, tab, sm.code2s, xf, tf, lora) : zero, j + 2);
+  // Rounds past the last one load the (clamped) last group again and are never
+  // computed: unconditional loads keep the waits exact. Whole groups of three
+  // rounds run in the loop (no exit inside it, which made the compiler drain
+  // the stream at the loop head); the last one or two after it, from the
+  // rounds the loop has already loaded into b0 and b1.
+  if constexpr (ONE) {
+    finish(active ? gm_compute(b0, p, tab, lb, sm.code2s, xf, tf) : zero, 0);
+    return;
   }
+  int j = 0;
+  for (; j + 3 <= rounds; j += 3) {
+    gm_load(b2, p, grp(j + 2), kw, col, g, jc);
+    finish(active ? gm_compute(b0, p, tab, lb, sm.code2s, xf, tf) : zero, j);
+    gm_load(b0, p, grp(j + 3), kw, col, g, jc);
+    finish(active ? gm_compute(b1, p, tab, lb, sm.code2s, xf, tf) : zero, j + 1);
+    gm_load(b1, p, grp(j + 4), kw, col, g, jc);
+    finish(active ? gm_compute(b2, p, tab, lb, sm.code2s, xf, tf) : zero, j + 2);
+  }
+  if (j < rounds) finish(active ? gm_compute(b0, p, tab, lb, sm.code2s, xf, tf) : zero, j);
+  if (j + 1 < rounds) finish(active ? gm_compute(b1, p, tab, lb, sm.code2s, xf, tf) : zero, j + 1);
 }
 
 // Y[m, n] = bf16(sum over K slices of the fp32 partials), slices in order.
@@ -986,13 +1078,24 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
     const bool q4u = nested && w->dq_block >= 4 && aligned(w->absmax_q, 4);
     float* part = gm_ks > 1 ? static_cast<float*>(workspace) : nullptr;
     const dim3 grid((unsigned)wgs, (unsigned)gm_ks);
-#define MOLT_GM(SMv, NWv) hipLaunchKernelGGL((nf4_gemv_ms_kernel<SMv, NWv>), grid, dim3(GM_NT), 0, st, p, rounds, part)
+    // LoRA B rows as 16-byte vectors where every 4-rank group is aligned
+    const int lv = r == 0 ? 0 : (r % 4 == 0 && aligned(lora_b, 16) ? 1 : 2);
+#define MOLT_GM3(SMv, NWv, LVv)                                                                        \
+  do {                                                                                                  \
+    if (rounds == 1)                                                                                    \
+      hipLaunchKernelGGL((nf4_gemv_ms_kernel<SMv, NWv, LVv, true>), grid, dim3(GM_NT), 0, st, p, rounds, part);  \
+    else                                                                                                \
+      hipLaunchKernelGGL((nf4_gemv_ms_kernel<SMv, NWv, LVv, false>), grid, dim3(GM_NT), 0, st, p, rounds, part); \
+  } while (0)
+#define MOLT_GM(SMv, NWv) \
+  do { if (lv == 0) MOLT_GM3(SMv, NWv, 0); else if (lv == 1) MOLT_GM3(SMv, NWv, 1); else MOLT_GM3(SMv, NWv, 2); } while (0)
     if (gm_nw == 8) {
       if (!nested) MOLT_GM(0, 8); else if (q4u) MOLT_GM(2, 8); else MOLT_GM(1, 8);
     } else {
       if (!nested) MOLT_GM(0, 7); else if (q4u) MOLT_GM(2, 7); else MOLT_GM(1, 7);
     }
 #undef MOLT_GM
+#undef MOLT_GM3
     if (gm_ks > 1) {
       const int64_t n = M * w->rows;
       hipLaunchKernelGGL(gm_reduce_kernel, dim3((unsigned)ceil_div64(n, 256)), dim3(256), 0, st, part, gm_ks,

@@ -38,7 +38,10 @@ def test_gemv_matches_oracle(n, k, m):
 
 @pytest.mark.parametrize("m,n,r", [(1, 1024, 16), (1, 1000, 96), (1, 4100, 128), (5, 1024, 16), (16, 1024, 16),
                                    (3, 1000, 64),
-                                   (16, 520, 96), (2, 256, 128)])
+                                   (16, 520, 96), (2, 256, 128),
+                                   # ranks that are not a multiple of 4 (B read one float at a time),
+                                   # one ending inside a lane group's 8
+                                   (8, 1024, 5), (12, 3000, 70), (3, 4100, 30)])
 def test_gemv_with_lora_matches_oracle(m, n, r):
     print(f"gemv lora m={m} n={n} r={r}", flush=True)
     k, s = 4096, 2.0
@@ -60,7 +63,11 @@ def test_gemv_with_lora_matches_oracle(m, n, r):
                                                  (1, 14344, 4096, True, 1), (3, 520, 4096, False, 0),
                                                  (2, 776, 14336, True, 1), (4, 2056, 4096, True, 1),
                                                  (2, 4104, 4096, False, 0), (3, 264, 14336, True, 0),
-                                                 (4, 4100, 14336, False, 1), (4, 2048, 4096, True, 1)])
+                                                 (4, 4100, 14336, False, 1), (4, 2048, 4096, True, 1),
+                                                 # the MFMA kernel with resolved scales, one and four K slices
+                                                 (8, 1000, 4096, False, 0), (16, 776, 14336, False, 1),
+                                                 # one round per workgroup (4096 rows: 256 groups of 16)
+                                                 (5, 4096, 4096, True, 1)])
 def test_gemv_decode_shapes_match_oracle(m, n, k, nested, order):
     # K = 4096 / 14336 take the streaming dot-product decode kernel at M <= 2,
     # and at M = 3, 4 when K = 14336 or N <= 2048 (two or four X rows; M = 3
@@ -118,7 +125,7 @@ def test_gemv_nested_codes_at_odd_address(m, n):
     assert_close_fro(np_f32(y), ref, what="Y")
 
 
-@pytest.mark.parametrize("m,n,r", [(16, 1000, 64), (2, 4100, 16), (7, 520, 128)])
+@pytest.mark.parametrize("m,n,r", [(16, 1000, 64), (2, 4100, 16), (7, 520, 128), (9, 1000, 70)])
 def test_gemv_split_k_with_lora_matches_oracle(m, n, r):
     # K = 14336 with M >= 2: four K slices of fp32 partials summed by a second kernel.
     print(f"gemv split-K m={m} n={n} r={r}", flush=True)
