@@ -239,7 +239,8 @@ def cfg3_stack(dev, steps: int = 3):
 
     from molt_amd.kernels import enable_frozen_rmsnorm_bf16
     from molt_amd.loading import prepare_nf4_qlora
-    from molt_amd.methods import enable_fused_gated_nf4_lora, enable_rmsnorm_replay, enable_scheduled_nf4_lora
+    from molt_amd.methods import (enable_fused_gated_nf4_lora, enable_rmsnorm_replay, enable_scheduled_nf4_lora,
+                                  enable_stacked_nf4_lora)
 
     H, I, L, heads, kv, hd, r, B, S = 1536, 8960, 28, 12, 2, 128, 16, 4, 1024
     cfg = LlamaConfig(hidden_size=H, intermediate_size=I, num_hidden_layers=L, num_attention_heads=heads,
@@ -252,6 +253,7 @@ def cfg3_stack(dev, steps: int = 3):
     prepare_nf4_qlora(model, r, 32.0)
     enable_frozen_rmsnorm_bf16(model)
     enable_scheduled_nf4_lora(model, module_suffixes=("q_proj", "k_proj", "v_proj", "o_proj"))
+    enable_stacked_nf4_lora(model)          # q, k and v of each layer as one node
     enable_fused_gated_nf4_lora(model)
     enable_rmsnorm_replay(model)
     g = torch.Generator(device="cpu").manual_seed(3)
@@ -404,7 +406,63 @@ def projection_sweep(dev, reps: int = 10):
         log(f"cfg3 {name} N={n} K={k} M={M}: fwd+bwd {ms:.3f} ms eager ({tf:.0f} TFLOP/s, "
             f"{100 * tf / PEAK_BF16_TFLOPS:.1f}%), {gpu_ms:.3f} ms of GPU work ({gtf:.0f} TFLOP/s, "
             f"{100 * gtf / PEAK_BF16_TFLOPS:.1f}%)")
+    out.append(_stacked_qkv(dev, M, r, s, reps, g))
     return out
+
+
+def _stacked_qkv(dev, M, r, s, reps, g):
+    """cfg3's q, k and v projections (1536, 256 and 256 outputs of 1536) as one
+    stacked node (methods.stacked_lora) against the three scheduled nodes:
+    forward + backward, eager and as GPU work alone."""
+    import torch
+    import molt_amd
+    from molt_amd.methods import scheduled_nf4_lora
+    from molt_amd.methods.stacked_lora import stacked_nf4_lora
+
+    k, rows = 1536, (1536, 256, 256)
+    projs = []
+    for n in rows:
+        w = (torch.randn(n, k, generator=g) * 0.02).to(dev)
+        packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True)
+        a = ((torch.rand(r, k, generator=g) * 2 - 1) / math.sqrt(k)).to(dev).requires_grad_()
+        b = (torch.randn(n, r, generator=g) * 0.01).to(dev).requires_grad_()
+        projs.append((packed, qs, a, b))
+    x = torch.randn(M, k, generator=g).to(dev, torch.bfloat16).requires_grad_()
+    dys = [torch.randn(M, n, generator=g).to(dev, torch.bfloat16) for n in rows]
+    leaves = [x] + [t for p in projs for t in p[2:]]
+
+    def stacked():
+        for t in leaves:
+            t.grad = None
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            ys = stacked_nf4_lora(x, [p[0] for p in projs], [p[2] for p in projs], [p[3] for p in projs],
+                                  [p[1] for p in projs], s)
+        torch.autograd.backward(ys, dys)
+
+    def separate():
+        for t in leaves:
+            t.grad = None
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            ys = [scheduled_nf4_lora(x, p[0], p[2], p[3], p[1], s) for p in projs]
+        torch.autograd.backward(ys, dys)
+
+    res = {"proj": "q/k/v stacked", "N": sum(rows), "K": k, "M": M, "r": r}
+    flop = sum(4 * M * n * k + 6 * M * r * (n + k) for n in rows)
+    for name, fn in (("separate", separate), ("stacked", stacked)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / reps
+        gpu_ms = _graph_ms(fn)
+        res[f"{name}_ms_fwd_bwd"] = round(ms, 4)
+        res[f"{name}_gpu_ms_fwd_bwd"] = round(gpu_ms, 4)
+        log(f"cfg3 q/k/v {name} (N=1536+256+256 K={k} M={M}): fwd+bwd {ms:.3f} ms eager, {gpu_ms:.3f} ms of GPU "
+            f"work ({flop / (gpu_ms * 1e-3) / 1e12:.0f} TFLOP/s)")
+    return res
 
 
 def _projection_ops(x, packed, qs, a, b, dy, s):

@@ -320,6 +320,41 @@ int molt_nf4_swiglu_backward_wt(const uint16_t* dy, int64_t lddy, int64_t M,
                                 const uint16_t* up, int64_t ldg, uint16_t* dgate, uint16_t* dup,
                                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* Several NF4-LoRA projections that share one input as one node: their
+ * weights stacked along the output rows, W = [W_0; W_1; ..] (1..8 weights of
+ * the same columns, block size, nibble order and code table; N = sum of their
+ * rows), e.g. a decoder layer's q, k and v projections. No counterpart in the
+ * reference, which runs each projection as its own node
+ * (methods/nf4_lora.py:12-113 per projection); each output column is the
+ * product that projection's own node computes (its LoRA term through its own
+ * adapter), with fp32 sums in another order.
+ *  molt_lora_stack_adapters: A_stack fp32 [lr, K] = [A_0; A_1; ..; zero rows]
+ *   and B_blocks fp32 [N, lr], block-diagonal (B_i [rows_i, r] in columns
+ *   i r .. i r + r - 1 of its rows, zeros elsewhere); r and lr multiples of
+ *   4, n r <= lr; one launch.
+ *  molt_nf4_stacked_forward: Y[M, N] = bf16(X deq(W)^T + T bf16(s B_blocks)^T)
+ *   with T = molt_lora_project(X, A_stack) [M, lr], lr 0 or a multiple of 64;
+ *   it dequantises each weight into its rows of the staged copy and runs one
+ *   GEMM. Workspace: molt_nf4_lora_forward_workspace(M, N, K, lr). With wt
+ *   (bf16 [K, N], 16-byte aligned) it also writes deq(W)^T for the input
+ *   gradient (*wt_written = 1). Only the staged plan applies
+ *   (molt_nf4_keeps_wt(M, N, K, 1) = 1 for 16-byte aligned operands); other
+ *   shapes are refused with MOLT_EUNSUPPORTED before any launch.
+ *  molt_nf4_stacked_backward_input: dX = dY deq(W) + U bf16(lora_scale A_stack)
+ *   from that deq(W)^T (required), dY bf16 [M, N]; workspace
+ *   molt_nf4_lora_backward_workspace_wt(M, N, K, 1); refused like the forward
+ *   where the plan would not read wt. */
+int molt_lora_stack_adapters(int32_t n, const float* const* a, const float* const* b, const int64_t* rows,
+                             int32_t r, int64_t K, int32_t lr, float* a_stack, float* b_blocks, void* stream);
+int molt_nf4_stacked_forward(const uint16_t* x, int64_t ldx, int64_t M, int32_t nw, const molt_nf4_weight* w,
+                             const uint16_t* t, int64_t ldt, int32_t lr, const float* b_blocks, int64_t ldb,
+                             float scaling, uint16_t* y, int64_t ldy, uint16_t* wt, int32_t* wt_written,
+                             void* workspace, size_t workspace_bytes, void* stream);
+int molt_nf4_stacked_backward_input(const uint16_t* dy, int64_t lddy, int64_t M, int32_t nw,
+                                    const molt_nf4_weight* w, const uint16_t* wt, const uint16_t* u, int64_t ldu,
+                                    const float* a_stack, int32_t r, float lora_scale, uint16_t* dx, int64_t lddx,
+                                    void* workspace, size_t workspace_bytes, void* stream);
+
 /* LoRA weight gradient out = scale * L^T . R over M rows, fp32:
  *  L bf16 [M, P] (l_mode 0) or SwiGLU replay of (L, L2) (l_mode 1); R bf16 [M, Q].
  *  out_layout 0: out[P, Q] (dB = s dY^T T, methods/nf4_lora.py:102);

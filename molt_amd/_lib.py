@@ -116,6 +116,12 @@ SIGNATURES: dict[str, tuple] = {
                                  _p]),
     "molt_lora_grad_many_workspace": (_sz, [_i32, _GD]),
     "molt_lora_grad_many": (C.c_int, [_i32, _GD, _p, _sz, _p]),
+    "molt_lora_stack_adapters": (C.c_int, [_i32, C.POINTER(_p), C.POINTER(_p), C.POINTER(_i64), _i32, _i64, _i32,
+                                           _p, _p, _p]),
+    "molt_nf4_stacked_forward": (C.c_int, [_p, _i64, _i64, _i32, _W, _p, _i64, _i32, _p, _i64, _f32, _p, _i64,
+                                           _p, _p, _p, _sz, _p]),
+    "molt_nf4_stacked_backward_input": (C.c_int, [_p, _i64, _i64, _i32, _W, _p, _p, _i64, _p, _i32, _f32, _p,
+                                                  _i64, _p, _sz, _p]),
     "molt_lora_grad_rmsnorm": (C.c_int, [_p, _i64, _p, _p, _i32, _f32, _p, _i64, _i64, _i64, _i64, _f32, _p,
                                          _i32, _p, _sz, _p]),
     "molt_nf4_gemv_workspace": (_sz, [_i64, _i64, _i64]),

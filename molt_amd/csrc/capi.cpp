@@ -112,6 +112,12 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
                                            int64_t ldg, const molt::WtHandoff* wt, void* workspace,
                                            size_t workspace_bytes, hipStream_t stream);
 
+extern "C" int molt_nf4_stacked_forward_impl(const uint16_t* x, int64_t ldx, int64_t M, int32_t nw,
+                                             const molt_nf4_weight* w, const uint16_t* t, int64_t ldt, int32_t lr,
+                                             const float* b, int64_t ldb, float s, uint16_t* y, int64_t ldy,
+                                             uint16_t* wt_out, int32_t* wt_written, void* workspace,
+                                             size_t workspace_bytes, hipStream_t stream);
+
 extern "C" {
 
 const char* molt_amd_last_error(void) { return molt::g_last_error; }
@@ -255,6 +261,40 @@ int molt_nf4_swiglu_backward_wt(const uint16_t* dy, int64_t lddy, int64_t M, con
   return molt_nf4_lora_backward_impl(dy, nullptr, lddy, M, wd, nullptr, u, nullptr, ldu, lora_a, nullptr, wd->cols,
                                      r, 1.0f, nullptr, 0, gate, up, dgate, dup, ldg, &h, workspace,
                                      workspace_bytes, (hipStream_t)stream);
+}
+
+int molt_nf4_stacked_forward(const uint16_t* x, int64_t ldx, int64_t M, int32_t nw, const molt_nf4_weight* w,
+                             const uint16_t* t, int64_t ldt, int32_t lr, const float* b_blocks, int64_t ldb,
+                             float scaling, uint16_t* y, int64_t ldy, uint16_t* wt, int32_t* wt_written,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  return molt_nf4_stacked_forward_impl(x, ldx, M, nw, w, t, ldt, lr, b_blocks, ldb, scaling, y, ldy, wt, wt_written,
+                                       workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int molt_nf4_stacked_backward_input(const uint16_t* dy, int64_t lddy, int64_t M, int32_t nw,
+                                    const molt_nf4_weight* w, const uint16_t* wt, const uint16_t* u, int64_t ldu,
+                                    const float* a_stack, int32_t r, float lora_scale, uint16_t* dx, int64_t lddx,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  const char* who = "molt_nf4_stacked_backward_input";
+  if (!w || nw < 1 || nw > 8)
+    return molt::drop_gemm_events(molt::set_error(MOLT_EINVAL, "%s: 1..8 weights", who));
+  if (!wt)
+    return molt::drop_gemm_events(
+        molt::set_error(MOLT_EINVAL, "%s: the forward's transposed weight is required", who));
+  // the stack's shape and format in one descriptor: the GEMM reads wt, not the packed data
+  molt_nf4_weight stack = w[0];
+  stack.rows = 0;
+  for (int i = 0; i < nw; ++i) {
+    if (w[i].cols != w[0].cols || w[i].block_size != w[0].block_size || w[i].nibble_order != w[0].nibble_order ||
+        w[i].code != w[0].code)
+      return molt::drop_gemm_events(molt::set_error(
+          MOLT_EINVAL, "%s: stacked weights must share columns, block size, nibble order and code table", who));
+    stack.rows += w[i].rows;
+  }
+  const molt::WtHandoff h{{nullptr, nullptr}, nullptr, {wt, wt}, 1};
+  return molt_nf4_lora_backward_impl(dy, nullptr, lddy, M, &stack, nullptr, u, nullptr, ldu, a_stack, nullptr,
+                                     stack.cols, r, lora_scale, dx, lddx, nullptr, nullptr, nullptr, nullptr, 0, &h,
+                                     workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 }  // extern "C"

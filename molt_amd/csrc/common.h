@@ -52,10 +52,14 @@ void take_gemm_events(void** start, void** end);
 // weights (bf16 [K, N], row stride N, one per weight): `out` asks a forward to
 // write them, `written` (host memory) tells whether it did, `in` gives them to
 // an input-gradient GEMM, which then does not stage the weights itself.
+// `required`: the input gradient must read `in` (the weight descriptor then
+// only carries the shape and format); a plan that would not is refused before
+// any launch.
 struct WtHandoff {
   uint16_t* out[2];
   int32_t* written;
   const uint16_t* in[2];
+  int32_t required;
 };
 }  // namespace molt
 

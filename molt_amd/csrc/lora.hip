@@ -1087,6 +1087,75 @@ extern "C" int molt_lora_pack_many(int32_t n, const molt_lora_pack_desc* d, void
   return check_launch(who);
 }
 
+// ---------------------------------------------------------------------------
+// Adapters of several projections that share one input, stacked for one
+// projection node over their stacked weights: A_stack [lr, K] = [A_0; A_1; ..;
+// zero rows] and B_blocks [N, lr] block-diagonal (rows of B_i in columns
+// i r .. i r + r - 1, zeros elsewhere), both fp32. Four consecutive elements
+// per thread: K and lr are multiples of 4, so the four never cross a row of
+// A_stack nor a block of B_blocks.
+constexpr int kStackMax = 8;
+struct StackAdapters {
+  const float* a[kStackMax];
+  const float* b[kStackMax];
+  int64_t n0[kStackMax + 1];                          // first row of each B block; n0[n] = N
+  int n, r, lr;
+  int64_t K;
+  float* a_stack;
+  float* b_blocks;
+};
+
+__global__ __launch_bounds__(256) void lora_stack_adapters_kernel(const StackAdapters p) {
+  const int64_t na = (int64_t)p.lr * p.K, nb = p.n0[p.n] * p.lr;
+  const int64_t e = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+  if (e >= na + nb) return;
+  f32x4_t v = {0.f, 0.f, 0.f, 0.f};
+  if (e < na) {
+    const int64_t j = e / p.K, k = e - j * p.K;
+    const int i = (int)(j / p.r);
+    if (i < p.n) {
+      const float* src = p.a[i] + (j - (int64_t)i * p.r) * p.K + k;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = src[q];
+    }
+    *reinterpret_cast<f32x4_t*>(p.a_stack + e) = v;
+  } else {
+    const int64_t f = e - na, row = f / p.lr;
+    const int c = (int)(f - row * p.lr), i = c / p.r;
+    if (i < p.n && row >= p.n0[i] && row < p.n0[i + 1]) {
+      const float* src = p.b[i] + (row - p.n0[i]) * p.r + (c - i * p.r);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = src[q];
+    }
+    *reinterpret_cast<f32x4_t*>(p.b_blocks + f) = v;
+  }
+}
+
+extern "C" int molt_lora_stack_adapters(int32_t n, const float* const* a, const float* const* b,
+                                        const int64_t* rows, int32_t r, int64_t K, int32_t lr, float* a_stack,
+                                        float* b_blocks, void* stream) {
+  const char* who = "molt_lora_stack_adapters";
+  MOLT_REQUIRE(n >= 1 && n <= kStackMax && a && b && rows, MOLT_EINVAL, "%s: 1..%d adapters", who, kStackMax);
+  MOLT_REQUIRE(r > 0 && r % 4 == 0 && lr % 4 == 0 && (int64_t)n * r <= lr && K > 0 && K % 4 == 0, MOLT_EINVAL,
+               "%s: needs r and lr multiples of 4, n r <= lr and K a multiple of 4 (n=%d r=%d lr=%d K=%lld)", who,
+               n, r, lr, (long long)K);
+  MOLT_REQUIRE(a_stack && b_blocks && aligned(a_stack, 16) && aligned(b_blocks, 16), MOLT_EINVAL,
+               "%s: outputs must be 16-byte aligned", who);
+  StackAdapters p{};
+  p.n = n; p.r = r; p.lr = lr; p.K = K; p.a_stack = a_stack; p.b_blocks = b_blocks;
+  int64_t n0 = 0;
+  for (int i = 0; i < n; ++i) {
+    MOLT_REQUIRE(a[i] && b[i] && rows[i] > 0, MOLT_EINVAL, "%s: adapter %d missing or empty", who, i);
+    p.a[i] = a[i]; p.b[i] = b[i]; p.n0[i] = n0;
+    n0 += rows[i];
+  }
+  p.n0[n] = n0;
+  const int64_t quads = ((int64_t)lr * K + n0 * lr) / 4;
+  hipLaunchKernelGGL(lora_stack_adapters_kernel, dim3((unsigned)ceil_div64(quads, 256)), dim3(256), 0,
+                     (hipStream_t)stream, p);
+  return check_launch(who);
+}
+
 extern "C" size_t molt_lora_project_packed_workspace(int64_t M, int64_t D, int32_t r) {
   if (D <= 0 || r <= 0 || M < 0) return 0;
   return molt_lora_project_workspace(M, D, r) - proj_packed_bytes(D, r);

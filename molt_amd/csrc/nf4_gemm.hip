@@ -2315,6 +2315,104 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
   return rc;
 }
 
+// Y[M, N] = bf16(X . deq(W)^T + T . bf16(s B)^T) over a weight stacked from
+// nw NF4 weights along the output rows, W = [W_0; W_1; ..] (N the sum of their
+// rows): each is dequantised into its rows of the staged bf16 copy and one
+// staged big-tile GEMM runs over the whole, so projections that share an input
+// take one GEMM launch. B fp32 [N, lr] (row stride ldb) and T bf16 [M, lr] with
+// lr 0 or a multiple of 64 (the LoRA steps of the DMA ring). Only the staged
+// plan applies: any other is refused before a launch (MOLT_EUNSUPPORTED).
+extern "C" int molt_nf4_stacked_forward_impl(const uint16_t* x, int64_t ldx, int64_t M, int32_t nw,
+                                             const molt_nf4_weight* w, const uint16_t* t, int64_t ldt, int32_t lr,
+                                             const float* b, int64_t ldb, float s, uint16_t* y, int64_t ldy,
+                                             uint16_t* wt_out, int32_t* wt_written, void* workspace,
+                                             size_t workspace_bytes, hipStream_t stream) {
+  const char* who = "molt_nf4_stacked_forward";
+  const GemmEvents armed;
+  if (wt_written) *wt_written = 0;
+  MOLT_REQUIRE(w && nw >= 1 && nw <= 8, MOLT_EINVAL, "%s: 1..8 weights", who);
+  int64_t N = 0;
+  for (int i = 0; i < nw; ++i) {
+    const int rc = check_weight_for_gemm(&w[i], who);
+    if (rc) return rc;
+    MOLT_REQUIRE(w[i].cols == w[0].cols && w[i].block_size == w[0].block_size &&
+                 w[i].nibble_order == w[0].nibble_order && w[i].code == w[0].code, MOLT_EINVAL,
+                 "%s: stacked weights must share columns, block size, nibble order and code table", who);
+    N += w[i].rows;
+  }
+  const int64_t K = w[0].cols;
+  MOLT_REQUIRE(M >= 0 && ldx >= K && ldy >= N, MOLT_EINVAL, "%s: bad X or Y stride", who);
+  MOLT_REQUIRE(lr == 0 || (lr % BK == 0 && t && b && ldt >= lr && ldb >= lr), MOLT_EINVAL,
+               "%s: bad LoRA operands (lr=%d must be a multiple of %d)", who, lr, BK);
+  if (M == 0) return MOLT_OK;
+  MOLT_REQUIRE(x && y, MOLT_EINVAL, "%s: null X or Y", who);
+  bool al = K % 64 == 0 && w[0].block_size == 64 && ldx % 8 == 0 && aligned(x, 16);
+  for (int i = 0; i < nw; ++i) al = al && aligned(w[i].packed, 16);
+  const GemmPlan plan = fwd_plan(M, N, K, false, fwd_big_ok(M, ldx, N, K, al), al);
+  const bool t_dma = lr > 0 && aligned(t, 16) && ldt % 8 == 0;
+  MOLT_REQUIRE(stage_wanted(plan.kind, M, N, K) && (lr == 0 || t_dma), MOLT_EUNSUPPORTED,
+               "%s: needs the staged big-tile plan (M=%lld, N=%lld, K=%lld) and 16-byte aligned T rows", who,
+               (long long)M, (long long)N, (long long)K);
+  const GemmWorkspace gw = place_workspace(plan, true, 1, N, K, N, lr, M, N, workspace, workspace_bytes);
+  MOLT_REQUIRE(gw.stage && (lr == 0 || gw.ring) && (plan.kind != PLAN_BIG_SPLIT || gw.split), MOLT_EWORKSPACE,
+               "%s: workspace of %zu bytes (256-byte aligned) needed, got %zu", who,
+               molt_nf4_lora_forward_workspace(M, N, K, lr), workspace_bytes);
+
+  FwdParams p{};
+  p.x = x; p.ldx = ldx; p.M = M; p.K = K; p.N = N;
+  p.packed[0] = p.packed[1] = w[0].packed; p.scales[0] = p.scales[1] = w[0].scales;
+  p.code = w[0].code; p.order = w[0].nibble_order; p.block_size = w[0].block_size;
+  p.t = t; p.ldt = ldt; p.lr = lr;
+  p.lb[0] = p.lb[1] = b; p.ldlb = ldb; p.r = lr; p.s[0] = p.s[1] = s;
+  p.y[0] = y; p.ldy = ldy;
+  p.vec_out = (ldy % 4 == 0) && aligned(y, 8);
+  char* wsb = static_cast<char*>(workspace);
+  if (plan.kind == PLAN_BIG_SPLIT) {
+    p.split_steps = plan.split_steps;
+    p.part = reinterpret_cast<float*>(wsb + gw.stage_bytes + gw.lora_bytes);
+  }
+  int rc;
+  if (lr > 0) {
+    p.lbst[0] = p.lbst[1] = reinterpret_cast<uint16_t*>(wsb + gw.stage_bytes);
+    const int64_t q = N * (lr / 8);
+    hipLaunchKernelGGL(big::stage_lora_b_kernel, dim3((unsigned)ceil_div64(q, 256), 1u), dim3(256), 0, stream, b, b,
+                       ldb, lr, s, s, N, lr, const_cast<uint16_t*>(p.lbst[0]), const_cast<uint16_t*>(p.lbst[0]));
+    rc = check_launch(who);
+    if (rc) return rc;
+    p.lora_ring = 1;
+  }
+  // each weight's bf16 rows at its place in the stack (resolved scales: the flat-scale dequant)
+  int64_t row0 = 0;
+  for (int i = 0; i < nw; ++i) {
+    molt_nf4_weight flat = w[i];
+    flat.nested = 0;
+    rc = molt_nf4_dequantize(&flat, reinterpret_cast<uint16_t*>(wsb) + row0 * K, MOLT_DTYPE_BF16, stream);
+    if (rc) return rc;
+    row0 += w[i].rows;
+  }
+  p.wst[0] = p.wst[1] = reinterpret_cast<const uint16_t*>(wsb);
+  p.ldw = K;
+  if (wt_out && N % 8 == 0 && aligned(wt_out, 16)) p.wt_out[0] = p.wt_out[1] = wt_out;
+  const int64_t big_tiles = ceil_div64(M, big::BM) * ceil_div64(N, big::BN);
+  MOLT_REQUIRE(big_tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
+  {
+    KernelEvents kev(armed, stream);
+    hipLaunchKernelGGL((big::fwd_kernel<false, true>), dim3((unsigned)big_tiles, (unsigned)plan.S), dim3(big::NT), 0,
+                       stream, p);
+    kev.finish();
+  }
+  if (p.part) {
+    rc = check_launch(who);
+    if (rc) return rc;
+    const int64_t q = M * (N / 4);
+    hipLaunchKernelGGL(split_sum_kernel, dim3((unsigned)ceil_div64(q, 256)), dim3(256), 0, stream, p.part, plan.S, M,
+                       N, y, ldy);
+  }
+  rc = check_launch(who);
+  if (rc == MOLT_OK && p.wt_out[0] && wt_written) *wt_written = 1;
+  return rc;
+}
+
 extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* dy1, int64_t lddy,
                                            int64_t M, const molt_nf4_weight* w0,
                                            const molt_nf4_weight* w1, const uint16_t* u0,
@@ -2378,6 +2476,11 @@ extern "C" int molt_nf4_lora_backward_impl(const uint16_t* dy0, const uint16_t* 
   const bool staged = gw.stage || use_wt;
   char* wsb = static_cast<char*>(workspace);
   const bool split = gw.split;
+  if (wt && wt->required)
+    MOLT_REQUIRE(use_wt && (plan.kind == PLAN_BIG || (plan.kind == PLAN_BIG_SPLIT && split)), MOLT_EUNSUPPORTED,
+                 "%s: this input gradient reads the forward's transposed weight, which needs the staged big-tile "
+                 "plan (M=%lld, N=%lld, K=%lld) and a workspace for its split", who, (long long)M,
+                 (long long)p.Nw, (long long)p.Kw);
   if (plan.kind == PLAN_BIG || (plan.kind == PLAN_BIG_SPLIT && split)) {
     MOLT_REQUIRE(big_tiles < (1ll << 31), MOLT_EINVAL, "%s: problem too large", who);
     if (plan.kind == PLAN_BIG_SPLIT) {

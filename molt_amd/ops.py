@@ -680,6 +680,126 @@ def _(x, packed, scales, code, rows, cols, order, block_size, t, lora_b, scaling
             x.new_empty((cols, rows) if keep else (0,), dtype=torch.bfloat16))
 
 
+# ----------------------------------------------------------- stacked weights
+def stack_adapters(loras_a: list[Tensor], loras_b: list[Tensor], lr: int) -> tuple[Tensor, Tensor]:
+    """(A_stack fp32 [lr, K], B_blocks fp32 [N, lr]) for projections that
+    share one input (molt_lora_stack_adapters): A_stack = [A_0; A_1; ..; zero
+    rows], B_blocks block-diagonal with B_i [rows_i, r] in columns i r ..
+    i r + r - 1 of its rows. One launch."""
+    what = "adapter stack"
+    n = len(loras_a)
+    if not (1 <= n <= 8) or len(loras_b) != n:
+        raise ValueError(f"{what}: 1..8 adapter pairs")
+    dev = _require_gpu(*loras_a, *loras_b, what=what)
+    a = [_f32(t) for t in loras_a]
+    b = [_f32(t) for t in loras_b]
+    r, k = a[0].shape
+    for ai, bi in zip(a, b):
+        if ai.shape != (r, k) or bi.dim() != 2 or bi.shape[1] != r:
+            raise ValueError(f"{what}: adapters of one rank and width expected, got A {tuple(ai.shape)}, "
+                             f"B {tuple(bi.shape)}")
+    rows = [int(bi.shape[0]) for bi in b]
+    a_stack = torch.empty((lr, k), device=dev, dtype=torch.float32)
+    b_blocks = torch.empty((sum(rows), lr), device=dev, dtype=torch.float32)
+    pa = (C.c_void_p * n)(*[t.data_ptr() for t in a])
+    pb = (C.c_void_p * n)(*[t.data_ptr() for t in b])
+    pr = (C.c_int64 * n)(*rows)
+    _call("molt_lora_stack_adapters", n, pa, pb, pr, r, k, lr, a_stack.data_ptr(), b_blocks.data_ptr(),
+          _stream(dev))
+    del a, b
+    return a_stack, b_blocks
+
+
+def _stacked_weights(weights: list[tuple[Tensor, Tensor, int]], code: Tensor, cols: int, order: int,
+                     block_size: int, what: str):
+    """ctypes array of the stacked weights' descriptors (packed, resolved
+    scales, rows each), and their total rows."""
+    n = len(weights)
+    if not (1 <= n <= 8):
+        raise ValueError(f"{what}: 1..8 weights")
+    descs = (_lib.NF4Weight * n)()
+    keep = []
+    cd = _f32(code)
+    for i, (packed, scales, rows) in enumerate(weights):
+        packed = _check_packed(packed, rows, cols, what)
+        _check_stats(what, rows, cols, block_size, code, scales=scales)
+        sc = _f32(scales)
+        keep += [packed, sc]
+        descs[i] = _weight(packed, sc, cd, rows, cols, block_size, order)
+    keep.append(cd)
+    return descs, sum(int(w[2]) for w in weights), keep
+
+
+def nf4_stacked_forward(x: Tensor, weights: list[tuple[Tensor, Tensor, int]], code: Tensor, cols: int,
+                        order: int, block_size: int, t: Optional[Tensor], b_blocks: Optional[Tensor],
+                        scaling: float, keep_wt: bool) -> tuple[Tensor, Optional[Tensor]]:
+    """(Y [M, N], deq(W)^T [cols, N] or None) over the weights stacked along
+    their output rows, W = [W_0; W_1; ..] (molt_nf4_stacked_forward): one GEMM
+    for projections that share X. T [M, lr] = X A_stack^T and B_blocks [N, lr]
+    from ``stack_adapters`` (lr a multiple of 64), or None for no LoRA. Raises
+    CapabilityError for a batch the staged GEMM does not take."""
+    what = "stacked NF4-LoRA forward"
+    dev = _require_gpu(x, code, t, b_blocks, *[w[0] for w in weights], what=what)
+    x = _bf16(x, "activations", what)
+    if x.dim() != 2 or x.shape[1] != cols:
+        raise ValueError(f"{what}: input width {tuple(x.shape)} does not match in_features {cols}")
+    descs, n, keep = _stacked_weights(weights, code, cols, order, block_size, what)
+    m = x.shape[0]
+    lr = 0
+    if t is not None:
+        t = _bf16(t, "low-rank activations", what)
+        lr = t.shape[1]
+        if t.shape[0] != m or b_blocks is None or tuple(b_blocks.shape) != (n, lr):
+            raise ValueError(f"{what}: T {tuple(t.shape)} and B_blocks "
+                             f"{None if b_blocks is None else tuple(b_blocks.shape)} do not match ({m}, {n})")
+        b_blocks = _f32(b_blocks)
+    y = torch.empty((m, n), device=dev, dtype=torch.bfloat16)
+    ws_bytes = _workspace("molt_nf4_lora_forward_workspace", m, n, cols, lr)
+    ws = torch.empty(max(ws_bytes, 256), device=dev, dtype=torch.uint8)
+    wt = torch.empty((cols, n), device=dev, dtype=torch.bfloat16) if keep_wt else None
+    written = C.c_int32(0)
+    lib = _lib.load()
+    rc = lib.molt_nf4_stacked_forward(x.data_ptr(), cols, m, len(weights), descs, _ptr(t), max(lr, 1), lr,
+                                      _ptr(b_blocks), max(lr, 1), float(scaling), y.data_ptr(), n, _ptr(wt),
+                                      C.byref(written), ws.data_ptr(), ws_bytes, _stream(dev))
+    _lib.check(rc)     # a batch the staged GEMM does not take: CapabilityError
+    del keep
+    return y, (wt if keep_wt and written.value else None)
+
+
+def nf4_stacked_backward_input(dy: Tensor, weights: list[tuple[Tensor, Tensor, int]], code: Tensor, cols: int,
+                               order: int, block_size: int, wt: Tensor, u: Optional[Tensor],
+                               a_stack: Optional[Tensor], lora_scale: float) -> Tensor:
+    """dX = dY deq(W) + U bf16(lora_scale A_stack) for the stacked weights,
+    from the deq(W)^T their forward left (molt_nf4_stacked_backward_input)."""
+    what = "stacked NF4-LoRA backward"
+    dev = _require_gpu(dy, wt, u, a_stack, *[w[0] for w in weights], what=what)
+    dy = _bf16(dy, "gradients", what)
+    descs, n, keep = _stacked_weights(weights, code, cols, order, block_size, what)
+    if dy.dim() != 2 or dy.shape[1] != n:
+        raise ValueError(f"{what}: gradient width {tuple(dy.shape)} does not match the stacked outputs {n}")
+    if wt is None or wt.dtype != torch.bfloat16 or tuple(wt.shape) != (cols, n) or not wt.is_contiguous():
+        raise ValueError(f"{what}: the forward's contiguous BF16 ({cols}, {n}) transposed weight is required")
+    m = dy.shape[0]
+    r = 0
+    if u is not None:
+        u = _bf16(u, "LoRA gradients", what)
+        r = u.shape[1]
+        if u.shape[0] != m or a_stack is None or tuple(a_stack.shape) != (r, cols):
+            raise ValueError(f"{what}: U {tuple(u.shape)} and A_stack do not match ({m}, {cols})")
+        a_stack = _f32(a_stack)
+    dx = torch.empty((m, cols), device=dev, dtype=torch.bfloat16)
+    ws_bytes = _workspace("molt_nf4_lora_backward_workspace_wt", m, n, cols, 1)
+    ws = torch.empty(max(ws_bytes, 256), device=dev, dtype=torch.uint8)
+    lib = _lib.load()
+    rc = lib.molt_nf4_stacked_backward_input(dy.data_ptr(), n, m, len(weights), descs, wt.data_ptr(), _ptr(u),
+                                             max(r, 1), _ptr(a_stack), r, float(lora_scale), dx.data_ptr(), cols,
+                                             ws.data_ptr(), ws_bytes, _stream(dev))
+    _lib.check(rc)     # a batch the staged GEMM does not take: CapabilityError
+    del keep
+    return dx
+
+
 @_custom_op(f"{NS}::nf4_gateup_forward", mutates_args=())
 def nf4_gateup_forward(x: Tensor, packed_g: Tensor, scales_g: Tensor, packed_u: Tensor,
                        scales_u: Tensor, code: Tensor, rows: int, cols: int, order: int,
@@ -984,7 +1104,8 @@ def lora_grad_many(ls: list[Tensor], l2s: list[Optional[Tensor]], modes: list[in
     keep, outs = [], []
     descs = (_lib.LoraGradDesc * n)()
     for i in range(n):
-        l = _bf16(ls[i], "activations", what)
+        # a plain left operand may be a column slice of a wider matrix (its row stride is passed)
+        l = _bf16_rows(ls[i], "activations", what) if l2s[i] is None else _bf16(ls[i], "activations", what)
         l2 = None if l2s[i] is None else _bf16(l2s[i], "activations", what)
         rmat = _bf16_rows(rmats[i], "low-rank operand", what)
         if l2 is not None and l2.shape != l.shape:
@@ -996,7 +1117,7 @@ def lora_grad_many(ls: list[Tensor], l2s: list[Optional[Tensor]], modes: list[in
         out = torch.empty((p, q) if layouts[i] == 0 else (q, p), device=dev, dtype=torch.float32)
         keep += [l, l2, rmat]
         outs.append(out)
-        descs[i] = _lib.LoraGradDesc(l.data_ptr(), _ptr(l2), p, int(modes[i]), rmat.data_ptr(),
+        descs[i] = _lib.LoraGradDesc(l.data_ptr(), _ptr(l2), max(l.stride(0), p), int(modes[i]), rmat.data_ptr(),
                                      max(rmat.stride(0), q), m, p, q, float(scales[i]), out.data_ptr(),
                                      int(layouts[i]))
     ws_bytes = int(_lib.load().molt_lora_grad_many_workspace(n, descs))
