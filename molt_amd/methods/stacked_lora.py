@@ -181,6 +181,12 @@ def _stacked_forward(module: torch.nn.Module, x: torch.Tensor, *args: Any, **kwa
     return outs[0]
 
 
+def _clear_stacked_outputs(parent: torch.nn.Module, args: Any) -> None:
+    for group in parent._molt_stack_groups:
+        for mod in group:
+            mod._molt_stacked_out = None
+
+
 def enable_stacked_nf4_lora(
     model: torch.nn.Module,
     *,
@@ -207,6 +213,12 @@ def enable_stacked_nf4_lora(
             group = tuple(members)
             for mod in group:
                 swap_forward(mod, _stacked_forward, key=_UNSTACKED, _molt_stack_group=group, _molt_stacked_out=None)
+            if parent.__dict__.get("_molt_stack_groups") is None:
+                # outputs left for a later sibling live only within one call of the parent, so a
+                # sibling called before the first projection never takes an earlier call's output
+                parent._molt_stack_groups = []
+                parent.register_forward_pre_hook(_clear_stacked_outputs)
+            parent._molt_stack_groups.append(group)
             count += 1
     if not count:
         raise CapabilityError("No compatible PEFT NF4-LoRA projection groups were found for "

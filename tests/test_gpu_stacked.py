@@ -159,3 +159,38 @@ def test_patched_decoder_stack_runs_qkv_as_one_node():
     assert p0.keys() == p1.keys() and any("q_proj" in n for n in p1)
     for name in p0:
         assert_close_fro(np_f32(p1[name]), np_f32(p0[name]).astype(np.float64), tol=2e-2, what=name)
+
+
+
+def test_siblings_called_before_the_first_projection_run_their_own_node():
+    """A parent whose forward calls k_proj before q_proj, twice on the same
+    input tensor, with k's adapter changed between the calls: k must never
+    get an output the stacked node left in an earlier call (the parent's
+    pre-hook clears them), and every output matches that projection's own
+    node."""
+    from torch import nn
+
+    attn = _llama(5).layers[0].self_attn
+
+    class KFirst(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.q_proj, self.k_proj, self.v_proj = attn.q_proj, attn.k_proj, attn.v_proj
+
+        def forward(self, x):
+            return self.k_proj(x), self.q_proj(x), self.v_proj(x)
+
+    parent = KFirst()
+    assert enable_scheduled_nf4_lora(parent) == 3
+    assert enable_stacked_nf4_lora(parent) == 1
+    x = seeded((2, 256, 256), 41)
+    with tuning(big_tile_min=1, stage_min_mtiles=1), torch.autocast("cuda", dtype=torch.bfloat16):
+        for i in range(3):
+            with torch.no_grad():
+                parent.k_proj.lora_B["default"].weight.add_(0.05)
+            k, q, v = parent(x)
+            for mod, out in ((parent.k_proj, k), (parent.q_proj, q), (parent.v_proj, v)):
+                ref = mod._molt_unstacked_forward(x)
+                assert_close_fro(np_f32(out), np_f32(ref).astype(np.float64), tol=2e-3,
+                                 what=f"call {i} {type(mod).__name__}")
+    torch.cuda.synchronize()
