@@ -804,7 +804,7 @@ MOLT_DEV f32x4_t gm_compute(const GmRound<SM, LV>& R, const GemvParams& p, const
 
 template <int SM, int NW, int LV, bool ONE>
 __global__ __launch_bounds__(GM_NT) void nf4_gemv_ms_kernel(const GemvParams p, int rounds, float* part) {
-  static_assert(NW >= 4 && NW <= GM_WAVES, "K slice of NW x 512 elements");
+  static_assert(NW >= 3 && NW <= GM_WAVES, "K slice of NW x 512 elements");
   __shared__ GmSmem sm;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1066,7 +1066,19 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
   // streaming MFMA kernel over 16-row groups, one workgroup per CU, K split
   // over the waves (and, past 4096, over workgroups with fp32 partials).
   int gm_nw = 8;
-  const int gm_ks = gm_slices(M, w->cols, gm_nw);
+  int gm_ks = gm_slices(M, w->cols, gm_nw);
+  // K of 3, 4 or 6 chunks (1536, 2048, 3072: the hidden widths of the smaller
+  // Qwen2.5 / Llama-3.2 models) with at least one 16-row group per CU: the
+  // same kernel with 3, 4 or 6 waves owning a chunk each (the others only help
+  // the reduction), so the code table is built once per CU instead of once per
+  // 16 rows. Every LoRA rank chunk of 32 needs a wave of its own.
+  if (gm_ks == 0 && M >= 2 && w->cols % 512 == 0 && ceil_div64(w->rows, 16) >= molt::device_cus()) {
+    const int chunks = (int)(w->cols / 512);
+    if ((chunks == 3 || chunks == 4 || chunks == 6) && r <= 32 * chunks) {
+      gm_nw = chunks;
+      gm_ks = 1;
+    }
+  }
   if (gm_ks > 0 && aligned(w->packed, 8) && aligned(x, 16) && ldx % 8 == 0) {
     const size_t need = molt_nf4_gemv_workspace(M, w->rows, w->cols);
     MOLT_REQUIRE(workspace_bytes >= need && (need == 0 || aligned(workspace, 16)), MOLT_EWORKSPACE,
@@ -1089,11 +1101,16 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
   } while (0)
 #define MOLT_GM(SMv, NWv) \
   do { if (lv == 0) MOLT_GM3(SMv, NWv, 0); else if (lv == 1) MOLT_GM3(SMv, NWv, 1); else MOLT_GM3(SMv, NWv, 2); } while (0)
-    if (gm_nw == 8) {
-      if (!nested) MOLT_GM(0, 8); else if (q4u) MOLT_GM(2, 8); else MOLT_GM(1, 8);
-    } else {
-      if (!nested) MOLT_GM(0, 7); else if (q4u) MOLT_GM(2, 7); else MOLT_GM(1, 7);
+#define MOLT_GMN(NWv) \
+  do { if (!nested) MOLT_GM(0, NWv); else if (q4u) MOLT_GM(2, NWv); else MOLT_GM(1, NWv); } while (0)
+    switch (gm_nw) {
+      case 8: MOLT_GMN(8); break;
+      case 7: MOLT_GMN(7); break;
+      case 6: MOLT_GMN(6); break;
+      case 4: MOLT_GMN(4); break;
+      default: MOLT_GMN(3); break;
     }
+#undef MOLT_GMN
 #undef MOLT_GM
 #undef MOLT_GM3
     if (gm_ks > 1) {

@@ -257,3 +257,26 @@ def test_gemv_any_k_matches_oracle_and_repeats(n, k, m):
     wo = oracle_weight(packed, qs).dequant_bf16().astype(np.float64)
     ref = O.lora_linear_forward(bf16_values(x), wo, bf16_values(a), bf16_values(b), s)
     assert_close_fro(np_f32(y1), ref, what="Y")
+
+
+@pytest.mark.parametrize("m,n,k,r", [(8, 8960, 1536, 16), (16, 4100, 1536, 96), (5, 4104, 2048, 32),
+                                     (12, 4096, 3072, 64), (16, 8960, 1536, 128), (9, 1536, 1536, 16)])
+def test_gemv_small_k_token_batches_match_oracle(m, n, k, r):
+    """M = 5-16 at K = 1536, 2048, 3072 with at least one 16-row group per CU:
+    the MFMA kernel with 3, 4 or 6 active waves; ranks above 32 per active
+    wave (r = 128 at K = 1536) and fewer rows (1536) take the other kernel.
+    Against the fp64 oracle, two calls bitwise equal."""
+    print(f"gemv small-k batch m={m} n={n} k={k} r={r}", flush=True)
+    s = 2.0
+    w = seeded((n, k), 940 + n + k, std=0.02, dtype=torch.float32)
+    packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=True)
+    x = seeded((m, k), 941 + m)
+    a = uniform((r, k), 942, 1.0 / np.sqrt(k))
+    b = seeded((n, r), 943, std=0.01, dtype=torch.float32)
+    t = ops.lora_project(x, None, 0, 1.0, a, 0)
+    y1, y2 = _gemv(x, packed, qs, t, b, s), _gemv(x, packed, qs, t, b, s)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    wo = oracle_weight(packed, qs).dequant_bf16().astype(np.float64)
+    ref = O.lora_linear_forward(bf16_values(x), wo, bf16_values(a), bf16_values(b), s)
+    assert_close_fro(np_f32(y1), ref, what="Y")
