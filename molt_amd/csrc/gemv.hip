@@ -118,18 +118,25 @@ struct GvSmem {
   uint16_t lt[16 * GV_RMAX];                              // T rows 0..15, row stride r
 };
 
+// With gridDim.y > 1 (narrow outputs: few 16-row groups) K is split over
+// gridDim.y workgroups per group, contiguous ranges of whole units; each writes
+// its fp32 partial to `part` (slice-major) and gm_reduce_kernel sums them in
+// slice order. The LoRA term belongs to slice 0.
 template <bool Q4>
-__global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(4))) void nf4_gemv_kernel(const GemvParams p) {
+__global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(4)))
+void nf4_gemv_kernel(const GemvParams p, float* part) {
   __shared__ GvSmem sm;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t n0 = (int64_t)blockIdx.x * GV_ROWS;
   const int col = lane & 15, g = lane >> 4;
   const int KB = p.K >> 6;
-  // Waves take contiguous slices of whole units (4 blocks under Q4).
+  // Waves take contiguous slices of whole units (4 blocks under Q4) of this
+  // workgroup's K range.
   constexpr int unit = Q4 ? 4 : 1;
-  const int units = KB / unit;
-  const int b0 = unit * (wave * units / GV_WAVES), b1 = unit * ((wave + 1) * units / GV_WAVES);
+  const int all_units = KB / unit, ns = (int)gridDim.y, sl = (int)blockIdx.y;
+  const int u0 = sl * all_units / ns, units = (sl + 1) * all_units / ns - u0;
+  const int b0 = unit * (u0 + wave * units / GV_WAVES), b1 = unit * (u0 + (wave + 1) * units / GV_WAVES);
   const int mc = col < p.M ? col : p.M - 1;
   const uint32_t xofs = (uint32_t)(mc * p.ldx + 16 * g);
   uint32_t wofs[GV_TILES], blk0[GV_TILES];
@@ -152,7 +159,7 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(4))) void
   const float c2 = (p.code2 ? p.code2 : p.code)[p.code2 ? (tid & 255) : 0];
   GvChunk<Q4> c;
   if (b0 < b1) gv_load<Q4>(c, p, wofs, blk0, xofs, b0, b1);
-  const bool lora = p.r > 0;
+  const bool lora = p.r > 0 && sl == 0;
   if (lora) {
     // B rows n0 .. n0+63 are contiguous (row stride r): 4-byte copies.
     const int nb = GV_ROWS * p.r;
@@ -281,7 +288,8 @@ __global__ __launch_bounds__(GV_NT) __attribute__((amdgpu_waves_per_eu(4))) void
     for (int e = 0; e < 4; ++e) {
       const int m = 4 * g + e;
       if (m >= p.M) continue;
-      p.y[(int64_t)m * p.ldy + n] = bf16_bits(acc[t][e]);
+      if (ns == 1) p.y[(int64_t)m * p.ldy + n] = bf16_bits(acc[t][e]);
+      else part[((int64_t)sl * p.M + m) * p.N + n] = acc[t][e];
     }
   }
 }
@@ -949,14 +957,27 @@ int gm_slices(int64_t M, int64_t K, int& nw) {
   if (chunks % 8 == 0 && chunks / 8 <= 8) return (int)(chunks / 8);
   return 0;
 }
+// K slices of the fallback MFMA kernel (nf4_gemv_kernel): narrow outputs (at
+// most 128 groups of 16 rows) split K over up to 8 workgroups per group, as
+// many as keep two workgroups per CU and whole 4-block units for every wave.
+int gv_slices(int64_t N, int64_t K) {
+  const int64_t groups = ceil_div64(N, GV_ROWS);
+  if (groups > 128 || K % 256 != 0) return 1;
+  const int64_t units = K / 256;                        // 4-block units
+  const int64_t s = std::min<int64_t>(std::min<int64_t>(8, units / GV_WAVES), 2 * molt::device_cus() / groups);
+  return s < 2 ? 1 : (int)s;
+}
 }  // namespace
 }  // namespace molt
 
 extern "C" size_t molt_nf4_gemv_workspace(int64_t M, int64_t N, int64_t K) {
-  // fp32 partials of the K slices when the streaming MFMA kernel splits K
+  // fp32 partials of the K slices when the streaming MFMA kernel, or the
+  // fallback kernel of a narrow output, splits K
   int nw = 8;
   const int ks = gm_slices(M, K, nw);
-  return ks > 1 ? (size_t)ks * (size_t)M * (size_t)N * sizeof(float) : 0;
+  const int vs = gv_slices(N, K);
+  const int s = std::max(ks, vs);
+  return s > 1 ? (size_t)s * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
 extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,
@@ -1121,8 +1142,23 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
     return check_launch(who);
   }
   const bool q4 = nested && (w->cols / 64) % 4 == 0 && w->dq_block >= 4 && aligned(w->absmax_q, 4);
-  if (q4) hipLaunchKernelGGL((nf4_gemv_kernel<true>), dim3((unsigned)groups), dim3(GV_NT), 0, st, p);
-  else hipLaunchKernelGGL((nf4_gemv_kernel<false>), dim3((unsigned)groups), dim3(GV_NT), 0, st, p);
+  // narrow outputs split K over workgroups (fp32 partials summed in slice order)
+  int vs = gv_slices(w->rows, w->cols);
+  if (vs > 1) {
+    const size_t need = (size_t)vs * (size_t)M * (size_t)w->rows * sizeof(float);
+    if (!(workspace && aligned(workspace, 16) && workspace_bytes >= need)) vs = 1;   // a smaller workspace: unsplit
+  }
+  float* part = vs > 1 ? static_cast<float*>(workspace) : nullptr;
+  const dim3 grid((unsigned)groups, (unsigned)vs);
+  if (q4) hipLaunchKernelGGL((nf4_gemv_kernel<true>), grid, dim3(GV_NT), 0, st, p, part);
+  else hipLaunchKernelGGL((nf4_gemv_kernel<false>), grid, dim3(GV_NT), 0, st, p, part);
+  if (vs > 1) {
+    const int rc = check_launch(who);
+    if (rc) return rc;
+    const int64_t n = M * w->rows;
+    hipLaunchKernelGGL(gm_reduce_kernel, dim3((unsigned)ceil_div64(n, 256)), dim3(256), 0, st, part, vs, (int)M,
+                       w->rows, y, ldy);
+  }
   return check_launch(who);
 }
 

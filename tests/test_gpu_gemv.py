@@ -280,3 +280,26 @@ def test_gemv_small_k_token_batches_match_oracle(m, n, k, r):
     wo = oracle_weight(packed, qs).dequant_bf16().astype(np.float64)
     ref = O.lora_linear_forward(bf16_values(x), wo, bf16_values(a), bf16_values(b), s)
     assert_close_fro(np_f32(y1), ref, what="Y")
+
+
+@pytest.mark.parametrize("m,n,k,nested", [(8, 1536, 8960, True), (16, 256, 8960, True), (5, 520, 4864, True),
+                                          (12, 1000, 6144, False), (16, 1536, 8960, False)])
+def test_gemv_narrow_outputs_split_k_match_oracle(m, n, k, nested):
+    """The fallback kernel for narrow outputs (at most 128 groups of 16 rows)
+    with K split over workgroups and the fp32 partials summed in slice order:
+    the Qwen2.5-1.5B down projection at M = 8 and 16, a K with an odd unit
+    count and resolved scales; against the fp64 oracle, repeat bitwise."""
+    print(f"gemv narrow split-k m={m} n={n} k={k} nested={nested}", flush=True)
+    r, s = 16, 2.0
+    w = seeded((n, k), 960 + n + k, std=0.02, dtype=torch.float32)
+    packed, qs = molt_amd.quantize_4bit(w, blocksize=64, compress_statistics=nested)
+    x = seeded((m, k), 961 + m)
+    a = uniform((r, k), 962, 1.0 / np.sqrt(k))
+    b = seeded((n, r), 963, std=0.01, dtype=torch.float32)
+    t = ops.lora_project(x, None, 0, 1.0, a, 0)
+    y1, y2 = _gemv(x, packed, qs, t, b, s, nested=nested), _gemv(x, packed, qs, t, b, s, nested=nested)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    wo = oracle_weight(packed, qs).dequant_bf16().astype(np.float64)
+    ref = O.lora_linear_forward(bf16_values(x), wo, bf16_values(a), bf16_values(b), s)
+    assert_close_fro(np_f32(y1), ref, what="Y")
