@@ -1039,8 +1039,13 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
     const int cus = molt::device_cus();
     const int rw = 1;                                         // rows per wave per round
     const int mx = M == 1 ? 1 : (M == 2 ? 2 : 4);             // X rows held by the kernel
-    // two workgroups per CU only where the kernel fits in 128 registers
-    const int per_cu = ipr <= 2 && mx <= 2 ? 2 : 1;
+    // One workgroup per CU, so that each wave has more rounds over the same
+    // set-up work (code table, X, LoRA operands): one token 4096^2 5.2 -> 4.95
+    // us, 14336 x 4096 10.5-11.2 -> 10.1-10.2 us, 8960 x 1536 6.4 -> 5.4 us;
+    // two tokens 14336 x 4096 12.8-13.1 -> 12.1-12.5 us, 8960 x 1536 7.6 ->
+    // 6.4 us. Two (the kernel then fits in 128 registers) for two tokens over
+    // at most 4096 rows, where one measured slower (4096^2: 5.35 -> 5.6 us).
+    const int per_cu = ipr <= 2 && mx == 2 && w->rows <= 4096 ? 2 : 1;
     const int64_t waves = std::min<int64_t>(ceil_div64(w->rows, rw), (int64_t)cus * GD_WAVES * per_cu);
     const int64_t wgs = ceil_div64(waves, GD_WAVES);
     const int rounds = (int)ceil_div64(w->rows, wgs * GD_WAVES * rw);
