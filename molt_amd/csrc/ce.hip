@@ -102,15 +102,22 @@ struct CeParams {
 };
 
 // Gradient of one element from its fp32 softmax-minus-target term: / total,
-// then the upstream scale when there is one; zero on ignored rows (also for a
-// NaN upstream scale, as F.cross_entropy leaves ignored rows untouched).
-MOLT_DEV float ce_grad(float diff, float inv_total, const CeParams& p, bool zero_row, float gs) {
+// then (EXACT) the upstream scale; zero on ignored rows under the exact rule
+// (also for a NaN upstream scale, as F.cross_entropy leaves ignored rows
+// untouched). The rule is a template parameter, so the fused rule's loop
+// carries no per-element select or scale.
+template <bool EXACT>
+MOLT_DEV float ce_grad(float diff, float inv_total, bool zero_row, float gs) {
   float g = diff * inv_total;
-  if (p.gscale) g *= gs;
-  return zero_row ? 0.0f : g;
+  if constexpr (EXACT) {
+    g *= gs;
+    return zero_row ? 0.0f : g;
+  } else {
+    return g;
+  }
 }
 
-template <bool F32, bool VEC, bool GRAD>
+template <bool F32, bool VEC, bool GRAD, bool EXACT>
 __global__ __launch_bounds__(CE_NT) void ce_kernel(const CeParams p) {
   __shared__ float red_m[CE_NT / 64], red_d[CE_NT / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -154,8 +161,8 @@ __global__ __launch_bounds__(CE_NT) void ce_kernel(const CeParams p) {
     void* grow = F32 ? (void*)(reinterpret_cast<float*>(p.grad) + row * p.ldg)
                      : (void*)(reinterpret_cast<uint16_t*>(p.grad) + row * p.ldg);
     const float inv_d = 1.0f / d, inv_total = 1.0f / p.total;
-    const bool zero_row = p.zero_invalid && !valid;
-    const float gs = p.gscale ? *p.gscale : 1.0f;
+    const bool zero_row = EXACT && p.zero_invalid && !valid;
+    const float gs = EXACT && p.gscale ? *p.gscale : 1.0f;
     if constexpr (VEC) {
       for (int64_t i = 8 * (int64_t)tid; i < p.V; i += 8 * CE_NT) {
         float v[8];
@@ -163,14 +170,14 @@ __global__ __launch_bounds__(CE_NT) void ce_kernel(const CeParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float t = (valid && i + e == y) ? 1.0f : 0.0f;
-          v[e] = ce_grad(__expf(v[e] - m) * inv_d - t, inv_total, p, zero_row, gs);
+          v[e] = ce_grad<EXACT>(__expf(v[e] - m) * inv_d - t, inv_total, zero_row, gs);
         }
         ce_st8<F32>(grow, i, v);
       }
     } else {
       for (int64_t i = tid; i < p.V; i += CE_NT) {
         const float t = (valid && i == y) ? 1.0f : 0.0f;
-        ce_st<F32>(grow, i, ce_grad(__expf(ce_ld<F32>(lrow, i) - m) * inv_d - t, inv_total, p, zero_row, gs));
+        ce_st<F32>(grow, i, ce_grad<EXACT>(__expf(ce_ld<F32>(lrow, i) - m) * inv_d - t, inv_total, zero_row, gs));
       }
     }
   }
@@ -183,7 +190,7 @@ __global__ __launch_bounds__(CE_NT) void ce_kernel(const CeParams p) {
 // row is read from memory once instead of twice, and with the same
 // arithmetic in the same order the results equal the two-pass kernel's bit
 // for bit. Chunks past the row re-load the last chunk and are skipped.
-template <int CH, bool GRAD>
+template <int CH, bool GRAD, bool EXACT>
 __global__ __launch_bounds__(CE_NT) void ce_reg_kernel(const CeParams p) {
   __shared__ float red_m[CE_NT / 64], red_d[CE_NT / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -232,8 +239,8 @@ __global__ __launch_bounds__(CE_NT) void ce_reg_kernel(const CeParams p) {
   if constexpr (GRAD) {
     uint16_t* grow = reinterpret_cast<uint16_t*>(p.grad) + row * p.ldg;
     const float inv_d = 1.0f / d, inv_total = 1.0f / p.total;
-    const bool zero_row = p.zero_invalid && !valid;
-    const float gs = p.gscale ? *p.gscale : 1.0f;
+    const bool zero_row = EXACT && p.zero_invalid && !valid;
+    const float gs = EXACT && p.gscale ? *p.gscale : 1.0f;
     // keep only the packed row alive across the reduction (unpacked, pass 1's
     // fp32 copies would double its registers)
 #pragma unroll
@@ -248,7 +255,7 @@ __global__ __launch_bounds__(CE_NT) void ce_reg_kernel(const CeParams p) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float t = (valid && i + e == y) ? 1.0f : 0.0f;
-        v[e] = ce_grad(__expf(v[e] - m) * inv_d - t, inv_total, p, zero_row, gs);
+        v[e] = ce_grad<EXACT>(__expf(v[e] - m) * inv_d - t, inv_total, zero_row, gs);
       }
       ce_st8<false, true>(grow, i, v);
       __builtin_amdgcn_sched_barrier(0);
@@ -283,13 +290,15 @@ int ce_rows(const char* who, const void* logits, int32_t dtype, int64_t ld, int6
   CeParams p{logits, ld, rows, vocab, targets, total, loss, grad, ldg, grad_scale, zero_invalid};
   const dim3 grid((unsigned)rows), block(CE_NT);
   hipStream_t st = (hipStream_t)stream;
+  const bool exact = grad_scale != nullptr || zero_invalid != 0;
   // bf16 rows up to 8 * CE_NT * 20 = 163,840 logits: one read, from registers
   const int64_t chunks = ceil_div64(vocab, 8 * CE_NT);
   if (!f32 && vec && chunks <= 20) {
 #define MOLT_CE_REG(CH)                                                                    \
   do {                                                                                     \
-    if (grad) hipLaunchKernelGGL((ce_reg_kernel<CH, true>), grid, block, 0, st, p);        \
-    else hipLaunchKernelGGL((ce_reg_kernel<CH, false>), grid, block, 0, st, p);            \
+    if (grad && exact) hipLaunchKernelGGL((ce_reg_kernel<CH, true, true>), grid, block, 0, st, p); \
+    else if (grad) hipLaunchKernelGGL((ce_reg_kernel<CH, true, false>), grid, block, 0, st, p);    \
+    else hipLaunchKernelGGL((ce_reg_kernel<CH, false, false>), grid, block, 0, st, p);             \
   } while (0)
     if (chunks <= 4) MOLT_CE_REG(4);
     else if (chunks <= 8) MOLT_CE_REG(8);
@@ -300,7 +309,11 @@ int ce_rows(const char* who, const void* logits, int32_t dtype, int64_t ld, int6
 #undef MOLT_CE_REG
     return check_launch(who);
   }
-#define MOLT_CE_LAUNCH(F, V, G) hipLaunchKernelGGL((ce_kernel<F, V, G>), grid, block, 0, st, p)
+#define MOLT_CE_LAUNCH(F, V, G)                                                              \
+  do {                                                                                       \
+    if (G && exact) hipLaunchKernelGGL((ce_kernel<F, V, G, true>), grid, block, 0, st, p);   \
+    else hipLaunchKernelGGL((ce_kernel<F, V, G, false>), grid, block, 0, st, p);             \
+  } while (0)
   if (grad) {
     if (f32) { if (vec) MOLT_CE_LAUNCH(true, true, true); else MOLT_CE_LAUNCH(true, false, true); }
     else { if (vec) MOLT_CE_LAUNCH(false, true, true); else MOLT_CE_LAUNCH(false, false, true); }
