@@ -57,8 +57,9 @@ struct FwdParams {
   // staged weights (large-tile kernels): bf16 deq(W) [N, K] of each weight,
   // row stride ldw, read by DMA instead of dequantising packed bytes
   const uint16_t* wst[2]; int64_t ldw;
-  // LoRA steps through the staged kernel's DMA ring (lr % 64 == 0): bf16(s B)
-  // rows of each weight [N, lr], the pair's block-diagonal layout
+  // LoRA steps through the staged kernel's DMA ring: bf16(s B) rows of each
+  // weight [N, lora_ring] (lr rounded up to 64, zeros past the adapter's
+  // ranks), the pair's block-diagonal layout; 0 = no ring
   const uint16_t* lbst[2]; int lora_ring;
   // staged kernels: also write deq(W)^T [K, N] of each weight (row stride N,
   // N % 8 == 0) for the input gradient of the same weights; null = do not
@@ -1232,9 +1233,15 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
     // 8 rows of one weight (gate and up alternate every 64 rows), so the
     // buffer resource is uniform per instruction. With p.lora_ring the LoRA
     // contraction follows as extra steps of the same ring: X from T (rank
-    // columns), W from the weight's staged bf16(s B) rows [N, lr].
+    // columns), W from the weight's staged bf16(s B) rows [N, lrs], lrs = lr
+    // rounded up to 64. A shorter lr is one step whose chunks past lr re-read
+    // the row's own T columns (k mod lr): the staged rows are zero there, so
+    // they add exact zeros, and a non-finite T value meets only its own row,
+    // whose output it already makes non-finite. (A lane select of an
+    // out-of-range offset instead made the compiler rebuild every step's DMA
+    // offsets: +167 instructions.)
     const bool ring = p.lora_ring && (!p.part || blockIdx.y + 1 == gridDim.y);
-    const int64_t lrs = ring ? p.lr : 0;
+    const int64_t lrs = ring ? p.lora_ring : 0;
     const int64_t xbytes = ((p.M - 1) * p.ldx + p.K) * 2, tbytes = ring ? ((p.M - 1) * p.ldt + p.lr) * 2 : 0;
     const int64_t wbytes = p.N * p.ldw * 2, bbytes = p.N * lrs * 2;
     uint32_t wdoff[4], toff[4], bdoff[4];
@@ -1248,7 +1255,7 @@ __global__ __launch_bounds__(NT) void fwd_kernel(const FwdParams p) {
       wsel[c] = __builtin_amdgcn_readfirstlane(which);
       wdoff[c] = (uint32_t)((min(nr, p.N - 1) * p.ldw + k) * 2);
       bdoff[c] = (uint32_t)((min(nr, p.N - 1) * lrs + k) * 2);
-      toff[c] = (uint32_t)((min(m0 + R, p.M - 1) * p.ldt + k) * 2);
+      toff[c] = (uint32_t)((min(m0 + R, p.M - 1) * p.ldt + k % max(p.lr, 1)) * 2);
     }
     // step j of this workgroup: the contraction step sbeg + j, then the LoRA
     // steps; indices past the end repeat the last step (loads never read).
@@ -1978,30 +1985,121 @@ __global__ __launch_bounds__(NT) void stage_wt_kernel(const StageTParams p) {
   }
 }
 
-// bf16 LoRA operand for the LoRA steps of the staged forward kernel's ring,
-// the values the fused kernel stages into LDS. W side: o_w[n][c] for
-// c < lr = bf16(s_w B_w[n][c - w r]) where 0 <= c - w r < r, else bf16(s_w 0)
-// (weight w = blockIdx.y: one weight has lr = r; the gate/up pair lr = 2r,
-// gate ranks first). One thread per 8 consecutive columns.
-__global__ void stage_lora_b_kernel(const float* b0, const float* b1, int64_t ldb, int r, float s0, float s1,
-                                    int64_t N, int lr, uint16_t* o0, uint16_t* o1) {
-  const int w = blockIdx.y;
-  const float* b = w ? b1 : b0;
-  const float s = w ? s1 : s0;
-  uint16_t* o = w ? o1 : o0;
-  const int chunks = lr / 8;
-  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (q >= N * chunks) return;
-  const int64_t n = q / chunks;
-  const int c0 = (int)(q - n * chunks) * 8 - w * r;
-  float f[8];
+// Everything a staged forward GEMM reads besides X and T, in one launch: the
+// bf16 rows of each weight and the ring's bf16(s B) rows. Job j takes blocks
+// first[j] .. first[j + 1] - 1 (uniform per block).
+//  * kind 0, a weight of `units` 8-element units with block size 64 and
+//    resolved fp32 scales: bf16(code * scale) per element, the values (and
+//    the code-pair table, arithmetic and rounding) of molt_nf4_dequantize's
+//    flat-scale path, so the staged copy is bitwise that call's output. A
+//    thread takes 4 units, all loads issued before any use, and 16-byte
+//    non-temporal stores.
+//  * kind 1, the bf16 LoRA operand of one weight for the ring's LoRA steps
+//    (the values the fused kernel stages into LDS): o[n][c] for c < lr is
+//    bf16(s B[n][c - woff]) where 0 <= c - woff < r, else bf16(s 0). One
+//    weight has woff = 0; in the gate/up pair the up rows have woff = r (gate
+//    ranks first); lr is r, 2r, or 64 when that is shorter. One thread per 8
+//    consecutive columns.
+constexpr int kStageJobs = 10;
+constexpr int kStageUnits = 4;
+struct StageJobs {
+  const void* src[kStageJobs];      // packed bytes (kind 0) or fp32 B (kind 1)
+  const float* scales[kStageJobs];  // kind 0: resolved scales
+  const float* code[kStageJobs];    // kind 0: the 16 codes
+  uint16_t* out[kStageJobs];
+  int64_t count[kStageJobs];        // kind 0: units; kind 1: B rows
+  int64_t ldb[kStageJobs];
+  float s[kStageJobs];
+  int kind[kStageJobs], order[kStageJobs], r[kStageJobs], woff[kStageJobs], lr[kStageJobs];
+  int first[kStageJobs + 1];
+  int n;
+};
+
+__global__ __launch_bounds__(256) void stage_kernel(const StageJobs J) {
+  __shared__ float2 tab[256];
+  int j = 0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) f[i] = (c0 + i >= 0 && c0 + i < r) ? b[n * ldb + c0 + i] : 0.0f;
-  u32x4_t v;
+  for (int k = 1; k < kStageJobs; ++k) j += (k < J.n && (int)blockIdx.x >= J.first[k]) ? 1 : 0;
+  const int64_t blk = (int64_t)blockIdx.x - J.first[j];
+  if (J.kind[j] == 0) {
+    {
+      const float* code = J.code[j];
+      const int b = threadIdx.x, hi = b >> 4, lo = b & 15, order = J.order[j];
+      tab[b] = make_float2(code[order ? hi : lo], code[order ? lo : hi]);
+    }
+    __syncthreads();
+    const uint8_t* packed = static_cast<const uint8_t*>(J.src[j]);
+    const float* scales = J.scales[j];
+    const int64_t units = J.count[j];
+    uint32_t q[kStageUnits];
+    float sc[kStageUnits];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(s * f[2 * i], s * f[2 * i + 1]);
-  *reinterpret_cast<u32x4_t*>(o + n * lr + (q - n * chunks) * 8) = v;
+    for (int i = 0; i < kStageUnits; ++i) {
+      const int64_t u = min(blk * 256 * kStageUnits + i * 256 + threadIdx.x, units - 1);
+      q[i] = *reinterpret_cast<const uint32_t*>(packed + 4 * u);
+    }
+#pragma unroll
+    for (int i = 0; i < kStageUnits; ++i) {
+      const int64_t u = min(blk * 256 * kStageUnits + i * 256 + threadIdx.x, units - 1);
+      sc[i] = scales[(8 * u) >> 6];
+    }
+#pragma unroll
+    for (int i = 0; i < kStageUnits; ++i) {
+      const int64_t u = blk * 256 * kStageUnits + i * 256 + threadIdx.x;
+      if (u >= units) continue;
+      u32x4_t w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float2 pr = tab[(q[i] >> (8 * e)) & 0xffu];
+        w[e] = pack_bf16x2(pr.x * sc[i], pr.y * sc[i]);
+      }
+      __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t*>(J.out[j] + 8 * u));
+    }
+  } else {
+    const int lr = J.lr[j], chunks = lr / 8, r = J.r[j];
+    const int64_t q = blk * 256 + threadIdx.x;
+    if (q >= J.count[j] * chunks) return;
+    const int64_t n = q / chunks;
+    const int c0 = (int)(q - n * chunks) * 8 - J.woff[j];
+    const float* b = static_cast<const float*>(J.src[j]);
+    const float s = J.s[j];
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = (c0 + i >= 0 && c0 + i < r) ? b[n * J.ldb[j] + c0 + i] : 0.0f;
+    u32x4_t v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(s * f[2 * i], s * f[2 * i + 1]);
+    *reinterpret_cast<u32x4_t*>(J.out[j] + n * lr + (q - n * chunks) * 8) = v;
+  }
 }
+
+// Host-side list of stage_kernel jobs, launched once.
+struct Stager {
+  StageJobs J{};
+  int blocks = 0;
+  void add(int kind, int64_t count, int64_t nblocks) {
+    J.kind[J.n] = kind;
+    J.count[J.n] = count;
+    J.first[J.n] = blocks;
+    blocks += (int)nblocks;
+    J.first[++J.n] = blocks;
+  }
+  // a weight with resolved scales, block size 64 and rows * cols % 8 == 0
+  void weight(const molt_nf4_weight& w, uint16_t* out) {
+    const int i = J.n;
+    J.src[i] = w.packed; J.scales[i] = w.scales; J.code[i] = w.code; J.order[i] = w.nibble_order; J.out[i] = out;
+    const int64_t units = w.rows * w.cols / 8;
+    add(0, units, ceil_div64(units, 256 * kStageUnits));
+  }
+  void lora_b(const float* b, int64_t ldb, int r, int woff, float s, int64_t rows, int lr, uint16_t* out) {
+    const int i = J.n;
+    J.src[i] = b; J.ldb[i] = ldb; J.r[i] = r; J.woff[i] = woff; J.s[i] = s; J.lr[i] = lr; J.out[i] = out;
+    add(1, rows, ceil_div64(rows * (lr / 8), 256));
+  }
+  void launch(hipStream_t stream) const {
+    if (J.n) hipLaunchKernelGGL(stage_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, J);
+  }
+};
 
 }  // namespace big
 
@@ -2129,6 +2227,16 @@ bool stage_wanted(int kind, int64_t M, int64_t rows, int64_t cols) {
 }
 size_t stage_one(int64_t rows, int64_t cols) { return (size_t)(rows * cols * 2 + 255) / 256 * 256; }
 
+// Columns of the staged bf16(s B) rows the forward ring streams for a LoRA
+// contraction of length lr, or 0 when the ring does not take it: a multiple of
+// 64 runs as lr / 64 ring steps; a shorter one (a multiple of 8: 16 for one
+// rank-16 adapter, 32 for the gate/up pair) as one step over rows padded with
+// zeros to 64, its T columns past lr read as zeros.
+int64_t ring_cols(int64_t lr) {
+  if (lr > 0 && lr % BK == 0) return lr;
+  return lr > 0 && lr < BK && lr % 8 == 0 ? BK : 0;
+}
+
 // molt_amd_time_next_gemm: a GEMM entry point takes (and so disarms) the
 // events as it starts, whatever it then does; a call that returns early leaves
 // them unrecorded instead of passing them on to a later, unrelated GEMM.
@@ -2152,8 +2260,8 @@ struct KernelEvents {
 };
 
 // Workspace layout of the GEMM entry points: the staged weights (if any),
-// their bf16 LoRA operands for the ring (if any: lora_rows x lora_cols per
-// weight, lora_cols a multiple of 64), then the split-K partials (if any). A
+// their bf16 LoRA operands for the ring (if any: lora_rows x
+// ring_cols(lora_cols) per weight), then the split-K partials (if any). A
 // workspace too small for the LoRA copies stages the weights alone.
 struct GemmWorkspace { bool stage, ring, split; size_t stage_bytes, lora_bytes; };
 GemmWorkspace place_workspace(const GemmPlan& plan, bool want_stage, int weights, int64_t rows, int64_t cols,
@@ -2161,8 +2269,8 @@ GemmWorkspace place_workspace(const GemmPlan& plan, bool want_stage, int weights
                               size_t ws_bytes) {
   GemmWorkspace g{false, false, false, 0, 0};
   const size_t sb = want_stage ? weights * stage_one(rows, cols) : 0;
-  const bool want_ring = want_stage && lora_cols > 0 && lora_cols % BK == 0;
-  const size_t lb = want_ring ? weights * stage_one(lora_rows, lora_cols) : 0;
+  const bool want_ring = want_stage && ring_cols(lora_cols) > 0;
+  const size_t lb = want_ring ? weights * stage_one(lora_rows, ring_cols(lora_cols)) : 0;
   const size_t pb = split_bytes(plan.S, M, out_n);
   const bool usable = ws && aligned(ws, 256);
   g.stage = want_stage && usable && ws_bytes >= sb + pb;
@@ -2242,26 +2350,22 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
       p.split_steps = plan.split_steps;
       p.part = reinterpret_cast<float*>(wsb + gw.stage_bytes + gw.lora_bytes);
     }
+    // the staged operands in one launch: the bf16 weight rows (resolved
+    // scales, the flat-scale dequant) and the ring's bf16(s B) rows
+    big::Stager stager;
     if (gw.ring) {
       const int nw = pair ? 2 : 1;
+      const int lrc = (int)ring_cols(lr);   // staged row length (lr, or 64 for a shorter lr)
       for (int i = 0; i < 2; ++i) p.lbst[i] = reinterpret_cast<uint16_t*>(wsb + gw.stage_bytes + (i < nw ? i : 0) *
-                                                                           stage_one(p.N, lr));
-      const int64_t q = p.N * (lr / 8);
-      hipLaunchKernelGGL(big::stage_lora_b_kernel, dim3((unsigned)ceil_div64(q, 256), (unsigned)nw), dim3(256), 0,
-                         stream, b0, pair ? b1 : b0, ldb, r, s0, s1, p.N, lr, const_cast<uint16_t*>(p.lbst[0]),
-                         const_cast<uint16_t*>(p.lbst[1]));
-      rc = check_launch(who);
-      if (rc) return rc;
-      p.lora_ring = 1;
+                                                                           stage_one(p.N, lrc));
+      for (int i = 0; i < nw; ++i)
+        stager.lora_b(i ? b1 : b0, ldb, r, i * r, i ? s1 : s0, p.N, lrc, const_cast<uint16_t*>(p.lbst[i]));
+      p.lora_ring = lrc;
     }
     if (gw.stage) {
-      // the bf16 weight rows (resolved scales, so the flat-scale dequant)
       for (int i = 0; i < (pair ? 2 : 1); ++i) {
-        molt_nf4_weight flat = *(i ? w1 : w0);
-        flat.nested = 0;
         uint16_t* dst = reinterpret_cast<uint16_t*>(wsb + i * stage_one(p.N, p.K));
-        rc = molt_nf4_dequantize(&flat, dst, MOLT_DTYPE_BF16, stream);
-        if (rc) return rc;
+        stager.weight(*(i ? w1 : w0), dst);
         p.wst[i] = dst;
       }
       if (!pair) p.wst[1] = p.wst[0];
@@ -2273,6 +2377,9 @@ extern "C" int molt_nf4_lora_forward_impl(const uint16_t* x, int64_t ldx, int64_
         p.wt_out[1] = pair ? wt->out[1] : wt->out[0];
       }
     }
+    stager.launch(stream);
+    rc = check_launch(who);
+    if (rc) return rc;
     dim3 grid((unsigned)big_tiles, (unsigned)plan.S), block(big::NT);
     KernelEvents kev(armed, stream);
     if (gw.stage) {
@@ -2371,25 +2478,22 @@ extern "C" int molt_nf4_stacked_forward_impl(const uint16_t* x, int64_t ldx, int
     p.split_steps = plan.split_steps;
     p.part = reinterpret_cast<float*>(wsb + gw.stage_bytes + gw.lora_bytes);
   }
-  int rc;
+  // one staging launch: each weight's bf16 rows at its place in the stack
+  // (resolved scales: the flat-scale dequant) and the ring's bf16(s B) rows
+  big::Stager stager;
   if (lr > 0) {
     p.lbst[0] = p.lbst[1] = reinterpret_cast<uint16_t*>(wsb + gw.stage_bytes);
-    const int64_t q = N * (lr / 8);
-    hipLaunchKernelGGL(big::stage_lora_b_kernel, dim3((unsigned)ceil_div64(q, 256), 1u), dim3(256), 0, stream, b, b,
-                       ldb, lr, s, s, N, lr, const_cast<uint16_t*>(p.lbst[0]), const_cast<uint16_t*>(p.lbst[0]));
-    rc = check_launch(who);
-    if (rc) return rc;
-    p.lora_ring = 1;
+    stager.lora_b(b, ldb, lr, 0, s, N, lr, const_cast<uint16_t*>(p.lbst[0]));
+    p.lora_ring = lr;
   }
-  // each weight's bf16 rows at its place in the stack (resolved scales: the flat-scale dequant)
   int64_t row0 = 0;
   for (int i = 0; i < nw; ++i) {
-    molt_nf4_weight flat = w[i];
-    flat.nested = 0;
-    rc = molt_nf4_dequantize(&flat, reinterpret_cast<uint16_t*>(wsb) + row0 * K, MOLT_DTYPE_BF16, stream);
-    if (rc) return rc;
+    stager.weight(w[i], reinterpret_cast<uint16_t*>(wsb) + row0 * K);
     row0 += w[i].rows;
   }
+  stager.launch(stream);
+  int rc = check_launch(who);
+  if (rc) return rc;
   p.wst[0] = p.wst[1] = reinterpret_cast<const uint16_t*>(wsb);
   p.ldw = K;
   if (wt_out && N % 8 == 0 && aligned(wt_out, 16)) p.wt_out[0] = p.wt_out[1] = wt_out;
@@ -2559,7 +2663,7 @@ size_t gemm_workspace(const GemmPlan& plan, bool stage, int weights, int64_t row
   size_t b = split_bytes(plan.S, M, out_n);
   if (stage) {
     b += weights * stage_one(rows, cols);
-    if (lora_cols > 0 && lora_cols % BK == 0) b += weights * stage_one(lora_rows, lora_cols);
+    if (ring_cols(lora_cols) > 0) b += weights * stage_one(lora_rows, ring_cols(lora_cols));
   }
   return b;
 }

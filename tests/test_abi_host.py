@@ -261,10 +261,14 @@ def test_staged_weight_workspace_queries_need_no_gpu():
         assert lib.molt_nf4_gateup_forward_workspace(8192, 14336, 4096, 0) == 0
     with tuning(stage_min_mtiles=8):
         assert lib.molt_nf4_lora_forward_workspace(2048, 14336, 4096, 0) == _stage(14336, 4096)
-    # in the forward, a rank that is a multiple of 64 adds the bf16(s B) rows the ring streams
+    # in the forward, a LoRA length that is a multiple of 64 adds the bf16(s B) rows the ring streams;
+    # a shorter one (a multiple of 8) adds them padded to 64 columns
     assert lib.molt_nf4_lora_forward_workspace(8192, 4096, 14336, 64) == _stage(4096, 14336) + _stage(4096, 64)
     assert lib.molt_nf4_gateup_forward_workspace(8192, 14336, 4096, 64) == 2 * (_stage(14336, 4096)
                                                                                  + _stage(14336, 128))
-    assert lib.molt_nf4_gateup_forward_workspace(8192, 14336, 4096, 16) == 2 * _stage(14336, 4096)   # 2r = 32
+    assert lib.molt_nf4_gateup_forward_workspace(8192, 14336, 4096, 16) == 2 * (_stage(14336, 4096)
+                                                                                 + _stage(14336, 64))  # 2r = 32
+    assert lib.molt_nf4_lora_forward_workspace(8192, 4096, 14336, 16) == _stage(4096, 14336) + _stage(4096, 64)
+    assert lib.molt_nf4_lora_forward_workspace(8192, 4096, 14336, 12) == _stage(4096, 14336)   # not a multiple of 8
     assert lib.molt_nf4_lora_forward_workspace(4096, 1536, 8960, 64) == (_stage(1536, 8960) + _stage(1536, 64)
                                                                          + 2 * 4096 * 1536 * 4)

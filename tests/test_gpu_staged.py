@@ -6,7 +6,8 @@ contraction order and so every output must equal the fused kernels' bit for bit:
 each case runs staged (stage_min_mtiles=1) and fused (0) and compares, with
 ragged row/column tails, LoRA terms, the gate/up pair, the paired and SwiGLU
 backward, and split-K (the partials then sit after the staged copy). In the
-forward, ranks that are a multiple of 64 (of 32 for the gate/up pair) also
+forward, LoRA lengths (r, or 2r for the gate/up pair) that are a multiple of
+64, or a multiple of 8 below 64 (one step over rows padded with zeros), also
 stage bf16(s B) and stream the LoRA steps through the same ring."""
 from __future__ import annotations
 
@@ -156,10 +157,12 @@ def test_staging_needs_the_workspace():
     assert torch.equal(outs[0], outs[1])
 
 
-def test_lora_ring_needs_its_workspace():
+@pytest.mark.parametrize("r", [64, 16, 8])
+def test_lora_ring_needs_its_workspace(r):
     """A workspace sized without the rank (room for the staged weight only)
-    stages the weight and runs the LoRA steps outside the ring: same result."""
-    m, n, k, r = 300, 256, 512, 64
+    stages the weight and runs the LoRA steps outside the ring: same result
+    (ranks below 64 as one ring step whose T columns past r read as zeros)."""
+    m, n, k = 300, 256, 512
     print(f"staged forward, LoRA ring with and without its workspace m={m} n={n} k={k} r={r}", flush=True)
     packed, qs, scales = _weight(n, k, 62)
     x = seeded((m, k), 63)
@@ -182,6 +185,57 @@ def test_lora_ring_needs_its_workspace():
         assert lib.molt_nf4_lora_forward_workspace(m, n, k, r) > lib.molt_nf4_lora_forward_workspace(m, n, k, 0)
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("r", [16, 8])
+def test_gateup_short_rank_ring_equals_the_unpipelined_steps(r):
+    """The gate/up pair with 2r < 64 (cfg3's r = 16): its LoRA length streams
+    through the ring as one zero-padded step; a workspace without the staged
+    B rows runs the register-staged LoRA step instead. Gate, up and h agree
+    bit for bit."""
+    m, i, h = 300, 256, 512
+    print(f"staged gate/up forward, LoRA ring with and without its workspace m={m} I={i} H={h} r={r}", flush=True)
+    pg, qg, sg = _weight(i, h, 73)
+    pu, qu, su = _weight(i, h, 74)
+    x = seeded((m, h), 75)
+    t = seeded((m, 2 * r), 76)
+    bg = seeded((i, r), 77, std=0.01, dtype=torch.float32)
+    bu = seeded((i, r), 78, std=0.01, dtype=torch.float32)
+    code = qg.code.float()
+    wg = ops._weight(pg, sg, code, i, h, 64, 1)
+    wu = ops._weight(pu, su, code, i, h, 64, 1)
+    lib = _lib.load()
+
+    def run(tt, rank):
+        nbytes = lib.molt_nf4_gateup_forward_workspace(m, i, h, rank)
+        ws = torch.empty(nbytes, device=x.device, dtype=torch.uint8)
+        o = [torch.empty((m, i), device=x.device, dtype=torch.bfloat16) for _ in range(3)]
+        _lib.check(lib.molt_nf4_gateup_forward(x.data_ptr(), h, m, ops.C.byref(wg), ops.C.byref(wu),
+                                               tt.data_ptr(), 2 * r, bg.data_ptr(), bu.data_ptr(), r, 2.0, 0.5,
+                                               o[0].data_ptr(), o[1].data_ptr(), o[2].data_ptr(), i,
+                                               ws.data_ptr(), nbytes, ops._stream(x.device)))
+        return o
+
+    # one row of T made infinite: the ring step's columns past 2r re-read the row's own T values, so
+    # the other rows stay bitwise those of the clean T, on both paths
+    bad = t.clone()
+    bad[7] = float("inf")
+    with tuning(big_tile_min=1, stage_min_mtiles=1):
+        assert lib.molt_nf4_gateup_forward_workspace(m, i, h, r) > lib.molt_nf4_gateup_forward_workspace(m, i, h, 0)
+        outs = [run(t, rank) for rank in (0, r)]
+        poisoned = [run(bad, rank) for rank in (0, r)]
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    keep = torch.arange(m, device=x.device) != 7
+    for clean, hit in zip(outs[0], poisoned[1]):
+        assert torch.equal(clean[keep], hit[keep])
+    assert not torch.isfinite(poisoned[1][0][7].float()).all()
+    # and against the oracle of the pair with its LoRA terms
+    xs, ts = bf16_values(x), bf16_values(t)
+    g_ref = xs @ oracle_weight(pg, qg).dequant_bf16().astype(np.float64).T + ts[:, :r] @ (
+        bf16_values((2.0 * bg).to(torch.bfloat16)).T)
+    assert_close_fro(np_f32(outs[1][0]), g_ref, what="gate")
 
 
 def test_paired_backward_reads_u_halves_in_place():
