@@ -195,6 +195,24 @@ int molt_lora_project_packed(const uint16_t* z, const uint16_t* z2, int64_t ldz,
                              uint16_t* out, int64_t ldo, void* workspace, size_t workspace_bytes,
                              void* stream);
 
+/* Two packed projections of one shape as one launch: out[:, :r] from (z0,
+ * z_scale0, packed0) and out[:, r:2r] from (z1, z_scale1, packed1), z_mode 0
+ * or 2 (ldo >= 2r). The split over the contraction counts both operands'
+ * row blocks, so a pair that fills the CUs together runs unsplit; each half
+ * is the projection of its own operand (fp32 sums in the order of its own
+ * launch at that split count). Operands the single launch does not take
+ * (unaligned rows, D not a multiple of 64) run as two projections. Workspace:
+ * molt_lora_project_pair_packed_workspace(M, D, r) bytes (often 0). No
+ * counterpart in the reference, which projects the gate and up gradients
+ * separately (methods/nf4_lora.py:89-90 per projection); used for
+ * U_g = bf16(s_g dg) bf16(B_g) and U_u of the fused gated MLP's backward. */
+size_t molt_lora_project_pair_packed_workspace(int64_t M, int64_t D, int32_t r);
+int molt_lora_project_pair_packed(const uint16_t* z0, const uint16_t* z1, int64_t ldz, int32_t z_mode,
+                                  float z_scale0, float z_scale1, int64_t M, int64_t D,
+                                  const uint16_t* packed0, const uint16_t* packed1, int32_t r,
+                                  uint16_t* out, int64_t ldo, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
 /* Y[M, N] = bf16( X . deq(W)^T + T . bf16(s * B)^T ), fp32 accumulation, with
  * X bf16 [M, K], T bf16 [M, r] = molt_lora_project(X, lora_a) and B fp32 [N, r]
  * (row stride r). `w->scales` must be resolved fp32 scales. r = 0 skips LoRA.

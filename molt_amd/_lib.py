@@ -86,6 +86,9 @@ SIGNATURES: dict[str, tuple] = {
     "molt_lora_pack_many": (C.c_int, [_i32, _PD, _p]),
     "molt_lora_project_packed_workspace": (_sz, [_i64, _i64, _i32]),
     "molt_lora_project_packed": (C.c_int, [_p, _p, _i64, _i32, _f32, _i64, _i64, _p, _i32, _p, _i64, _p, _sz, _p]),
+    "molt_lora_project_pair_packed_workspace": (_sz, [_i64, _i64, _i32]),
+    "molt_lora_project_pair_packed": (C.c_int, [_p, _p, _i64, _i32, _f32, _f32, _i64, _i64, _p, _p, _i32, _p, _i64,
+                                                _p, _sz, _p]),
     "molt_amd_time_next_gemm": (C.c_int, [_p, _p]),
     "molt_nf4_lora_forward_workspace": (_sz, [_i64, _i64, _i64, _i32]),
     "molt_nf4_lora_forward": (C.c_int, [_p, _i64, _i64, _W, _p, _i64, _p, _i32, _f32, _p, _i64, _p, _sz, _p]),

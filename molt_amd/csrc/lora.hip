@@ -3,6 +3,8 @@
 // [M, D] activation from HBM once; the rank-r side is small and L2-resident.
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "mfma_core.h"
 
 namespace molt {
@@ -164,7 +166,13 @@ struct ProjParams {
   const uint16_t* wp;
   uint16_t* out; int64_t ldo;
   float* part;          // K split: fp32 partials [ks][M][32 TQ]
+  // a pair launch (lora_project_dma_kernel, gridDim.z == 2): the second
+  // operand's z, packed adapter, scale, output and partials for blockIdx.z == 1
+  const uint16_t* zb; const uint16_t* wpb; float zsb; uint16_t* outb; float* partb;
 };
+
+template <typename T>
+MOLT_DEV T pick2(bool c, T a, T b) { return c ? a : b; }
 
 template <int MT, bool VEC, bool REPLAY>
 MOLT_DEV void proj_load_z(Chunk (&z)[MT][4], const ProjParams& p, int64_t s, int64_t m0, int lane) {
@@ -330,6 +338,13 @@ MOLT_DEV void pj_load_w(u32x4_t (&w)[TQ][4], __amdgpu_buffer_rsrc_t wr, int64_t 
 
 template <int TQ, int MT, int KS>
 __global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_dma_kernel(const ProjParams p) {
+  // operand blockIdx.z of a pair launch (kernel-argument values, selected in scalar registers)
+  const bool second = blockIdx.z != 0;
+  const uint16_t* const pz = pick2(second, p.zb, p.z);
+  const uint16_t* const pwp = pick2(second, p.wpb, p.wp);
+  const float pzs = pick2(second, p.zsb, p.zs);
+  uint16_t* const pout = pick2(second, p.outb, p.out);
+  float* const ppart = pick2(second, p.partb, p.part);
   // z buffers per wave: a ring of three (z two of the wave's steps ahead)
   // where the LDS allows it, else two (one step ahead). One array per ring
   // slot, selected statically: the compiler waits for every DMA that may
@@ -357,8 +372,8 @@ __global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_dma_kernel(const P
       for (int e = 0; e < 16; ++e) acc[i][t][e] = 0.0f;
 
   if (s_begin + wave < s_end) {
-    const __amdgpu_buffer_rsrc_t zr = pj_rsrc(p.z, ((p.M - 1) * p.ldz + p.D) * 2);
-    const __amdgpu_buffer_rsrc_t wr = pj_rsrc(p.wp, all_steps * TQ * 4 * 64 * 16);
+    const __amdgpu_buffer_rsrc_t zr = pj_rsrc(pz, ((p.M - 1) * p.ldz + p.D) * 2);
+    const __amdgpu_buffer_rsrc_t wr = pj_rsrc(pwp, all_steps * TQ * 4 * 64 * 16);
     uint32_t zoff[4 * MT];
 #pragma unroll
     for (int c = 0; c < 4 * MT; ++c) {
@@ -412,7 +427,7 @@ __global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_dma_kernel(const P
           if (p.mode == 2) {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              zv[e] = pack_bf16x2(bf16_lo(zv[e]) * p.zs, bf16_hi(zv[e]) * p.zs);
+              zv[e] = pack_bf16x2(bf16_lo(zv[e]) * pzs, bf16_hi(zv[e]) * pzs);
           }
           const bf16x8_t zb = __builtin_bit_cast(bf16x8_t, zv);
 #pragma unroll
@@ -450,8 +465,8 @@ __global__ __launch_bounds__(64 * PJ_WAVES) void lora_project_dma_kernel(const P
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const int q = 32 * t + 8 * (e >> 2) + 4 * h + (e & 3);
-            if (KS > 1) p.part[((int64_t)blockIdx.y * p.M + m) * (32 * TQ) + q] = v[e];
-            else if (q < p.R) p.out[m * p.ldo + q] = bf16_bits(v[e]);
+            if (KS > 1) ppart[((int64_t)blockIdx.y * p.M + m) * (32 * TQ) + q] = v[e];
+            else if (q < p.R) pout[m * p.ldo + q] = bf16_bits(v[e]);
           }
         }
       }
@@ -1004,8 +1019,8 @@ int proj_mt(int64_t M, int tq, bool vec, int z_mode) {
   return (vec && z_mode != 1 && M >= 256 * 64 && tq <= 2) ? 2 : 1;
 }
 
-int proj_ksplit(int64_t M, int64_t D, int mt) {
-  const int64_t tiles = ceil_div64(M, 32 * mt), steps = ceil_div64(D, BK);
+int proj_ksplit(int64_t M, int64_t D, int mt, int operands = 1) {
+  const int64_t tiles = operands * ceil_div64(M, 32 * mt), steps = ceil_div64(D, BK);
   int ks = 1;
   while (ks < 4 && tiles * ks < 256 && steps / (2 * ks) >= 16) ks *= 2;
   return ks;
@@ -1179,6 +1194,99 @@ extern "C" int molt_lora_project_packed(const uint16_t* z, const uint16_t* z2, i
                "%s: workspace %zu < %zu bytes (or not 16-byte aligned)", who, workspace_bytes, need);
   return launch_projection(z, z2, ldz, z_mode, z_scale, M, D, packed, r, out, ldo, workspace, (hipStream_t)stream,
                            who);
+}
+
+// Two projections of one shape over adapters already packed, as one launch
+// of the DMA kernel with gridDim.z = 2 (blockIdx.z picks the operand): the
+// split count counts both operands' row blocks, so a pair that fills the CUs
+// together runs unsplit. Same tiles, split ranges and summation order per
+// operand as its own launch with that split count. Returns MOLT_EUNSUPPORTED
+// (nothing launched) where the DMA kernel does not apply.
+static int launch_projection_pair(const uint16_t* z0, const uint16_t* z1, int64_t ldz, int32_t z_mode, float zs0,
+                                  float zs1, int64_t M, int64_t D, const uint16_t* wp0, const uint16_t* wp1,
+                                  int32_t r, uint16_t* out0, uint16_t* out1, int64_t ldo, void* part,
+                                  hipStream_t st, const char* who) {
+  const int tq = (int)proj_tq(r);
+  const bool dma = z_mode != 1 && D % BK == 0 && ldz % 8 == 0 && aligned(z0, 16) && aligned(z1, 16) &&
+                   molt::tuning_value(MOLT_TUNE_LORA_DMA) != 0;
+  if (!dma) return MOLT_EUNSUPPORTED;
+  ProjParams p{};
+  p.z = z0; p.ldz = ldz; p.mode = z_mode; p.zs = zs0;
+  p.M = M; p.D = D; p.R = r; p.wp = wp0; p.out = out0; p.ldo = ldo;
+  p.zb = z1; p.wpb = wp1; p.zsb = zs1; p.outb = out1;
+  const int mt = proj_mt(M, tq, true, z_mode);
+  const int ks = proj_ksplit(M, D, mt, 2);
+  const size_t plane = (size_t)ks * (size_t)M * (size_t)(32 * tq);
+  p.part = ks > 1 ? static_cast<float*>(part) : nullptr;
+  p.partb = ks > 1 ? static_cast<float*>(part) + plane : nullptr;
+  dim3 grid((unsigned)ceil_div64(M, 32 * mt), (unsigned)ks, 2u), block(64 * PJ_WAVES);
+#define MOLT_PJD(TQ, MT)                                                                                       \
+  do {                                                                                                         \
+    if (ks == 4) hipLaunchKernelGGL((lora_project_dma_kernel<TQ, MT, 4>), grid, block, 0, st, p);               \
+    else if (ks == 2) hipLaunchKernelGGL((lora_project_dma_kernel<TQ, MT, 2>), grid, block, 0, st, p);          \
+    else hipLaunchKernelGGL((lora_project_dma_kernel<TQ, MT, 1>), grid, block, 0, st, p);                       \
+  } while (0)
+  switch (tq * 2 + mt - 1) {
+    case 2: MOLT_PJD(1, 1); break;
+    case 3: MOLT_PJD(1, 2); break;
+    case 4: MOLT_PJD(2, 1); break;
+    case 5: MOLT_PJD(2, 2); break;
+    case 6: MOLT_PJD(3, 1); break;
+    default: MOLT_PJD(4, 1); break;
+  }
+#undef MOLT_PJD
+  if (ks > 1) {
+    int rc = check_launch(who);
+    if (rc) return rc;
+    int64_t rb = ceil_div64(M * r, 256);
+    if (rb > 4096) rb = 4096;
+    hipLaunchKernelGGL(proj_reduce_kernel, dim3((unsigned)rb), dim3(256), 0, st, p.part, ks, M, r, 32 * tq, out0, ldo);
+    rc = check_launch(who);
+    if (rc) return rc;
+    hipLaunchKernelGGL(proj_reduce_kernel, dim3((unsigned)rb), dim3(256), 0, st, p.partb, ks, M, r, 32 * tq, out1,
+                       ldo);
+  }
+  return check_launch(who);
+}
+
+// Enough for the pair launch and for the two separate projections it falls
+// back to (operands the DMA kernel does not take).
+extern "C" size_t molt_lora_project_pair_packed_workspace(int64_t M, int64_t D, int32_t r) {
+  if (D <= 0 || r <= 0 || M < 0) return 0;
+  const int ks = proj_ksplit(M, D, proj_mt(M, (int)proj_tq(r), true, 0), 2);
+  const size_t pair = ks > 1 ? 2 * (size_t)ks * (size_t)M * (size_t)(32 * proj_tq(r)) * sizeof(float) : 0;
+  return std::max(pair, molt_lora_project_packed_workspace(M, D, r));
+}
+
+extern "C" int molt_lora_project_pair_packed(const uint16_t* z0, const uint16_t* z1, int64_t ldz, int32_t z_mode,
+                                             float z_scale0, float z_scale1, int64_t M, int64_t D,
+                                             const uint16_t* packed0, const uint16_t* packed1, int32_t r,
+                                             uint16_t* out, int64_t ldo, void* workspace, size_t workspace_bytes,
+                                             void* stream) {
+  const char* who = "molt_lora_project_pair_packed";
+  MOLT_REQUIRE(z_mode == 0 || z_mode == 2, MOLT_EINVAL, "%s: bad z_mode %d (0 or 2)", who, z_mode);
+  MOLT_REQUIRE(M >= 0 && D > 0 && r > 0, MOLT_EINVAL, "%s: bad shape M=%lld D=%lld r=%d", who, (long long)M,
+               (long long)D, r);
+  MOLT_REQUIRE(r <= 32 * PJ_TQ_MAX, MOLT_EUNSUPPORTED, "%s: rank %d > %d", who, r, 32 * PJ_TQ_MAX);
+  if (M == 0) return MOLT_OK;
+  MOLT_REQUIRE(z0 && z1 && packed0 && packed1 && aligned(packed0, 16) && aligned(packed1, 16) && out && ldz >= D &&
+               ldo >= 2 * r, MOLT_EINVAL, "%s: bad pointers/strides", who);
+  hipStream_t st = (hipStream_t)stream;
+  const size_t need = molt_lora_project_pair_packed_workspace(M, D, r);
+  const bool room = need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16));
+  if (room) {
+    const int rc = launch_projection_pair(z0, z1, ldz, z_mode, z_scale0, z_scale1, M, D, packed0, packed1, r, out,
+                                          out + r, ldo, workspace, st, who);
+    if (rc != MOLT_EUNSUPPORTED) return rc;
+  }
+  // operands the pair launch does not take: one projection each (their own
+  // split counts), with the workspace their larger need asks for
+  const size_t one = molt_lora_project_packed_workspace(M, D, r);
+  MOLT_REQUIRE(one == 0 || (workspace && workspace_bytes >= one && aligned(workspace, 16)), MOLT_EWORKSPACE,
+               "%s: workspace %zu < %zu bytes (or not 16-byte aligned)", who, workspace_bytes, one);
+  int rc = launch_projection(z0, nullptr, ldz, z_mode, z_scale0, M, D, packed0, r, out, ldo, workspace, st, who);
+  if (rc) return rc;
+  return launch_projection(z1, nullptr, ldz, z_mode, z_scale1, M, D, packed1, r, out + r, ldo, workspace, st, who);
 }
 
 // The projection kernel(s) over an adapter already packed at wp (split

@@ -469,14 +469,10 @@ def lora_project_pair(z0: Tensor, z1: Tensor, zscale0: float, zscale1: float, lo
     l0, l1 = _f32(lora0), _f32(lora1)
     if l0.dim() != 2 or l0.shape[0] != d or l1.shape != l0.shape:
         raise ValueError(f"{what}: adapters {tuple(l0.shape)}, {tuple(l1.shape)} must both be [{d}, r]")
-    r = l0.shape[1]
-    out = torch.empty((m, 2 * r), device=dev, dtype=torch.bfloat16)
-    ws_bytes = _workspace("molt_lora_project_workspace", m, d, r)
-    ws = torch.empty(max(ws_bytes, 16), device=dev, dtype=torch.uint8)
-    for half, (z, zs, lw) in enumerate(((z0, zscale0, l0), (z1, zscale1, l1))):
-        _call("molt_lora_project", z.data_ptr(), None, d, 2, zs, m, d, lw.data_ptr(), 1, r,
-              out.data_ptr() + half * r * out.element_size(), 2 * r, ws.data_ptr(), ws_bytes, _stream(dev))
-    return out
+    # both adapters packed in one launch, then one projection launch for the pair
+    # (bitwise lora_project_pair_packed)
+    packs = lora_pack_many([l0, l1], [None, None], [1, 1])
+    return lora_project_pair_packed(z0, z1, zscale0, zscale1, packs[0], packs[1], l0.shape[1])
 
 
 @lora_project_pair.register_fake
@@ -561,7 +557,10 @@ def _(z, z2, mode, zscale, packed, r):
 def lora_project_pair_packed(z0: Tensor, z1: Tensor, zscale0: float, zscale1: float, packed0: Tensor,
                              packed1: Tensor, r: int) -> Tensor:
     """``lora_project_pair`` over adapters packed by ``lora_pack_many`` (layout
-    1, rank r each): no pack launches; bitwise the same output."""
+    1, rank r each) as one launch (molt_lora_project_pair_packed): no pack
+    launches, and the split over D counts both operands' row blocks. Each half
+    is that operand's projection; where the pair runs with a different split
+    count than a single projection, its fp32 sums run in another order."""
     what = "LoRA projection pair"
     dev = _require_gpu(z0, z1, packed0, packed1, what=what)
     z0 = _bf16(z0, "activations", what)
@@ -573,11 +572,10 @@ def lora_project_pair_packed(z0: Tensor, z1: Tensor, zscale0: float, zscale1: fl
     if packed0.numel() != nbytes or packed1.numel() != nbytes:
         raise ValueError(f"{what}: the packed adapters do not match width {d} and rank {r}")
     out = torch.empty((m, 2 * r), device=dev, dtype=torch.bfloat16)
-    ws_bytes = _workspace("molt_lora_project_packed_workspace", m, d, r)
+    ws_bytes = _workspace("molt_lora_project_pair_packed_workspace", m, d, r)
     ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8) if ws_bytes else None
-    for half, (z, zs, pk) in enumerate(((z0, zscale0, packed0), (z1, zscale1, packed1))):
-        _call("molt_lora_project_packed", z.data_ptr(), None, d, 2, zs, m, d, pk.data_ptr(), r,
-              out.data_ptr() + half * r * out.element_size(), 2 * r, _ptr(ws), ws_bytes, _stream(dev))
+    _call("molt_lora_project_pair_packed", z0.data_ptr(), z1.data_ptr(), d, 2, zscale0, zscale1, m, d,
+          packed0.data_ptr(), packed1.data_ptr(), r, out.data_ptr(), 2 * r, _ptr(ws), ws_bytes, _stream(dev))
     return out
 
 

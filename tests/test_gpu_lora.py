@@ -14,7 +14,7 @@ from oracle import nf4_oracle as O
 from tests._util import assert_close_fro, bf16_values, np_f32, seeded, uniform
 
 import molt_amd
-from molt_amd import ops
+from molt_amd import _lib, ops
 
 pytestmark = pytest.mark.gpu
 
@@ -97,7 +97,8 @@ def test_lora_grad_empty_rows_gives_zeros():
 @pytest.mark.parametrize("m,d,r", [(300, 4096, 64), (8192, 1024, 16), (70, 200, 8)])
 def test_lora_project_pair_is_the_two_projections_side_by_side(m, d, r):
     """The gate/up U pair written as column halves of one matrix equals the two
-    separate pre-scaled projections bit for bit."""
+    separate pre-scaled projections bit for bit (shapes where the pair launch
+    splits D as a single projection does, or falls back to two)."""
     print(f"lora_project_pair m={m} d={d} r={r}", flush=True)
     z0, z1 = seeded((m, d), 11), seeded((m, d), 12)
     b0, b1 = uniform((d, r), 13, 1 / np.sqrt(d)), uniform((d, r), 14, 1 / np.sqrt(d))
@@ -106,6 +107,35 @@ def test_lora_project_pair_is_the_two_projections_side_by_side(m, d, r):
     u1 = ops.lora_project(z1, None, 2, 2.0, b1, 1)
     assert pair.shape == (m, 2 * r)
     assert torch.equal(pair[:, :r], u0) and torch.equal(pair[:, r:], u1)
+
+
+@pytest.mark.parametrize("m,d,r,same_split", [(4096, 8960, 16, False), (2048, 2048, 32, True)])
+def test_lora_project_pair_one_launch(m, d, r, same_split):
+    """The pair as one launch (molt_lora_project_pair_packed): its split over D
+    counts both operands' row blocks, so cfg3's U_g / U_u (4096 x 8960, r = 16)
+    run unsplit where a single projection splits D in two. Each half against
+    the fp64 oracle of its pre-scaled projection, and bit for bit against the
+    single projection where the split counts agree."""
+    print(f"lora_project_pair_packed one launch m={m} d={d} r={r}", flush=True)
+    lib = _lib.load()
+    # unsplit, the pair needs no partials (only the fallback's room); split, two planes of them
+    assert (lib.molt_lora_project_pair_packed_workspace(m, d, r) > lib.molt_lora_project_packed_workspace(m, d, r)) \
+        == same_split
+    z0, z1 = seeded((m, d), 15), seeded((m, d), 16)
+    b0, b1 = uniform((d, r), 17, 1 / np.sqrt(d)), uniform((d, r), 18, 1 / np.sqrt(d))
+    packs = ops.lora_pack_many([b0, b1], [None, None], [1, 1])
+    pair = ops.lora_project_pair_packed(z0, z1, 0.5, 2.0, packs[0], packs[1], r)
+    singles = [ops.lora_project(z, None, 2, sc, b, 1) for z, sc, b in ((z0, 0.5, b0), (z1, 2.0, b1))]
+    torch.cuda.synchronize()
+    for half, (z, sc, b) in enumerate(((z0, 0.5, b0), (z1, 2.0, b1))):
+        got = pair[:, half * r:(half + 1) * r]
+        ref = _effective(z, None, 2, sc) @ bf16_values(b)
+        assert_close_fro(np_f32(got), O.bf16_round(ref), what=f"U half {half}")
+        if same_split:
+            assert torch.equal(got, singles[half])
+        else:
+            assert_close_fro(np_f32(got), np_f32(singles[half]).astype(np.float64), tol=2e-3,
+                             what=f"U half {half} vs its own launch")
 
 
 @pytest.mark.parametrize("m,p,q,layout", [(4099, 512, 64, 0), (2048, 384, 64, 1), (300, 200, 16, 0)])
