@@ -384,18 +384,20 @@ int molt_lora_grad(const uint16_t* l, const uint16_t* l2, int64_t ldl, int32_t l
                    float scale, float* out, int32_t out_layout, void* workspace,
                    size_t workspace_bytes, void* stream);
 
-/* Several LoRA weight gradients in one launch, plus one launch that sums
- * their splits (a molt_lora_grad call takes two launches per gradient). Each
- * descriptor holds the arguments of one molt_lora_grad call, and its output is
- * bitwise what that call gives: same tiles, M slices, partials and summation
- * order. It is one launch pair when every gradient has plain operands
- * (l_mode 0), 16-byte aligned rows, and P and Q multiples of 8. Otherwise the
- * gradients run one after another. 1..8 descriptors. Workspace (256-byte
- * aligned): molt_lora_grad_many_workspace(n, d) bytes. No counterpart in the
- * reference, which computes each adapter gradient as its own matmul
- * (methods/nf4_lora.py:102-103, methods/gated_replay.py:392-405); the
- * gated-MLP backward runs its five gradients, and a scheduled projection its
- * two, as one call. */
+/* Several LoRA weight gradients with one launch that sums all their splits (a
+ * molt_lora_grad call takes two launches per gradient). Each descriptor holds
+ * the arguments of one molt_lora_grad call (l_mode 0 or 1), or of one
+ * molt_lora_grad_rmsnorm call (l_mode 2: l = x, inv_rms, norm_weight of
+ * w_dtype and norm_offset; l2 unused), and its output is bitwise what that
+ * call gives: same tiles, M slices, partials and summation order. The
+ * gradients with plain operands (l_mode 0), 16-byte aligned rows and P and Q
+ * multiples of 8 share one launch; each other gradient takes a launch of its
+ * own; then one launch sums every split. 1..8 descriptors. Workspace
+ * (256-byte aligned): molt_lora_grad_many_workspace(n, d) bytes. No
+ * counterpart in the reference, which computes each adapter gradient as its
+ * own matmul (methods/nf4_lora.py:102-103, methods/gated_replay.py:392-405);
+ * the gated-MLP backward runs all its adapter gradients, and a scheduled
+ * projection its two, as one call. */
 typedef struct molt_lora_grad_desc {
   const uint16_t* l;
   const uint16_t* l2;
@@ -407,6 +409,11 @@ typedef struct molt_lora_grad_desc {
   float scale;
   float* out;
   int32_t out_layout;
+  /* l_mode 2 only */
+  const float* inv_rms;
+  const void* norm_weight;
+  int32_t w_dtype;
+  float norm_offset;
 } molt_lora_grad_desc;
 size_t molt_lora_grad_many_workspace(int32_t n, const molt_lora_grad_desc* d);
 int molt_lora_grad_many(int32_t n, const molt_lora_grad_desc* d, void* workspace, size_t workspace_bytes,

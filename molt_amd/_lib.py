@@ -51,6 +51,7 @@ class LoraGradDesc(C.Structure):
         ("rmat", C.c_void_p), ("ldr", C.c_int64),
         ("M", C.c_int64), ("P", C.c_int64), ("Q", C.c_int64),
         ("scale", C.c_float), ("out", C.c_void_p), ("out_layout", C.c_int32),
+        ("inv_rms", C.c_void_p), ("norm_weight", C.c_void_p), ("w_dtype", C.c_int32), ("norm_offset", C.c_float),
     ]
 
 

@@ -1371,19 +1371,17 @@ extern "C" size_t molt_lora_grad_workspace(int64_t M, int64_t P, int64_t Q) {
   return (size_t)grad_splits(M, P, Q) * (size_t)P * (size_t)Q * sizeof(float);
 }
 
-// Split over M, launch the gradient kernel and sum the splits (shared by
-// molt_lora_grad and molt_lora_grad_rmsnorm; p carries the operands).
-static int launch_grad(GradParams& p, bool vec, int lm, float scale, float* out, int32_t out_layout,
-                       void* workspace, size_t workspace_bytes, hipStream_t st, const char* who) {
+// M slices of one gradient (the rows each takes); returns their count.
+static int grad_slices(GradParams& p) {
+  const int S = grad_splits(p.M, p.P, p.Q);
+  p.slice = ceil_div64(ceil_div64(p.M, S), BK) * BK;
+  return (int)ceil_div64(p.M, p.slice);
+}
+
+// The gradient kernel of one gradient (slices set by grad_slices, partials at
+// p.part in p.layout), without the split sum.
+static void grad_kernel_launch(const GradParams& p, bool vec, int lm, int S_eff, hipStream_t st) {
   const int64_t M = p.M, P = p.P, Q = p.Q;
-  const int S = grad_splits(M, P, Q);
-  const size_t need = (size_t)S * P * Q * sizeof(float);
-  MOLT_REQUIRE(workspace && workspace_bytes >= need, MOLT_EWORKSPACE, "%s: workspace %zu < %zu bytes", who,
-               workspace_bytes, need);
-  p.slice = ceil_div64(ceil_div64(M, S), BK) * BK;
-  p.part = (float*)workspace;
-  p.layout = out_layout;
-  const int S_eff = (int)ceil_div64(M, p.slice);
   dim3 grid((unsigned)ceil_div64(P, GR_P), (unsigned)ceil_div64(Q, GR_Q), (unsigned)S_eff);
   // the DMA-staged kernel for plain aligned operands whose byte offsets fit the buffer resources
   const bool dma = vec && lm == L_PLAIN && molt::tuning_value(MOLT_TUNE_LORA_DMA) != 0 &&
@@ -1397,6 +1395,20 @@ static int launch_grad(GradParams& p, bool vec, int lm, float scale, float* out,
   else if (lm == L_REPLAY) hipLaunchKernelGGL((lora_grad_kernel<true, L_REPLAY>), grid, dim3(GR_NT), 0, st, p);
   else if (lm == L_NORM) hipLaunchKernelGGL((lora_grad_kernel<true, L_NORM>), grid, dim3(GR_NT), 0, st, p);
   else hipLaunchKernelGGL((lora_grad_kernel<true, L_PLAIN>), grid, dim3(GR_NT), 0, st, p);
+}
+
+// Split over M, launch the gradient kernel and sum the splits (shared by
+// molt_lora_grad and molt_lora_grad_rmsnorm; p carries the operands).
+static int launch_grad(GradParams& p, bool vec, int lm, float scale, float* out, int32_t out_layout,
+                       void* workspace, size_t workspace_bytes, hipStream_t st, const char* who) {
+  const int64_t P = p.P, Q = p.Q;
+  const size_t need = (size_t)grad_splits(p.M, P, Q) * P * Q * sizeof(float);
+  MOLT_REQUIRE(workspace && workspace_bytes >= need, MOLT_EWORKSPACE, "%s: workspace %zu < %zu bytes", who,
+               workspace_bytes, need);
+  p.part = (float*)workspace;
+  p.layout = out_layout;
+  const int S_eff = grad_slices(p);
+  grad_kernel_launch(p, vec, lm, S_eff, st);
   int rc = check_launch(who);
   if (rc) return rc;
   const int64_t n = P * Q;
@@ -1438,10 +1450,11 @@ extern "C" int molt_lora_grad(const uint16_t* l, const uint16_t* l2, int64_t ldl
   return launch_grad(p, vec, l_mode, scale, out, out_layout, workspace, workspace_bytes, st, who);
 }
 
-// Several gradients in one launch (and their split sums in a second): each
-// output is bitwise that of its own molt_lora_grad call (same tiles, slices,
-// partials and summation order). All operands plain (l_mode 0) and eligible
-// for the DMA-staged kernel, else the gradients run one after another.
+// Several gradients and one launch that sums all their splits: each output
+// is bitwise that of its own molt_lora_grad (l_mode 0, 1) or
+// molt_lora_grad_rmsnorm (l_mode 2) call (same kernel, tiles, slices, partials
+// and summation order). The gradients eligible for the DMA-staged plain
+// kernel share one launch; each other one takes its own kernel launch.
 static size_t grad_ws_bytes(int64_t M, int64_t P, int64_t Q) {
   return M > 0 ? ((size_t)grad_splits(M, P, Q) * (size_t)P * (size_t)Q * sizeof(float) + 255) / 256 * 256 : 0;
 }
@@ -1459,74 +1472,86 @@ extern "C" int molt_lora_grad_many(int32_t n, const molt_lora_grad_desc* d, void
   const char* who = "molt_lora_grad_many";
   MOLT_REQUIRE(d && n >= 1 && n <= kGradMany, MOLT_EINVAL, "%s: 1..%d gradients", who, kGradMany);
   hipStream_t st = (hipStream_t)stream;
-  GradMany gm{};
-  ReduceMany rm{};
-  bool all_dma = true;
   size_t off = 0;
   GradParams ps[kGradMany];
+  bool vecs[kGradMany], batched[kGradMany];
   for (int i = 0; i < n; ++i) {
     const molt_lora_grad_desc& g = d[i];
-    MOLT_REQUIRE(g.l_mode == 0 || g.l_mode == 1, MOLT_EINVAL, "%s: bad l_mode (gradient %d)", who, i);
+    MOLT_REQUIRE(g.l_mode >= 0 && g.l_mode <= 2, MOLT_EINVAL, "%s: bad l_mode (gradient %d)", who, i);
     MOLT_REQUIRE(g.out_layout == 0 || g.out_layout == 1, MOLT_EINVAL, "%s: bad out_layout (gradient %d)", who, i);
     MOLT_REQUIRE(g.M >= 0 && g.P > 0 && g.Q > 0, MOLT_EINVAL, "%s: bad shape (gradient %d)", who, i);
     MOLT_REQUIRE(g.out && g.ldl >= g.P && g.ldr >= g.Q, MOLT_EINVAL, "%s: bad pointers/strides (gradient %d)", who, i);
-    MOLT_REQUIRE(g.M == 0 || (g.l && g.rmat && (g.l_mode == 0 || g.l2)), MOLT_EINVAL, "%s: null operand (gradient %d)",
-                 who, i);
+    MOLT_REQUIRE(g.M == 0 || (g.l && g.rmat && (g.l_mode != 1 || g.l2)), MOLT_EINVAL,
+                 "%s: null operand (gradient %d)", who, i);
+    const bool vec = g.P % 8 == 0 && g.Q % 8 == 0 && g.ldl % 8 == 0 && g.ldr % 8 == 0 && aligned(g.l, 16) &&
+                     aligned(g.rmat, 16) && (g.l_mode != 1 || aligned(g.l2, 16));
+    if (g.l_mode == 2) {
+      MOLT_REQUIRE(g.w_dtype == MOLT_DTYPE_BF16 || g.w_dtype == MOLT_DTYPE_F32, MOLT_EINVAL,
+                   "%s: norm weight dtype must be bf16 or fp32 (gradient %d)", who, i);
+      MOLT_REQUIRE(g.M == 0 || (g.inv_rms && g.norm_weight), MOLT_EINVAL, "%s: null norm operand (gradient %d)",
+                   who, i);
+      MOLT_REQUIRE(g.M == 0 || vec, MOLT_EUNSUPPORTED,
+                   "%s: the RMSNorm replay needs 16-byte aligned rows and P, Q multiples of 8 (gradient %d)", who, i);
+    }
     GradParams& p = ps[i];
     p = GradParams{};
-    p.l = g.l; p.l2 = g.l2; p.ldl = g.ldl; p.mode = g.l_mode; p.rm = g.rmat; p.ldr = g.ldr;
+    p.l = g.l; p.l2 = g.l_mode == 1 ? g.l2 : nullptr; p.ldl = g.ldl; p.mode = g.l_mode; p.rm = g.rmat; p.ldr = g.ldr;
     p.M = g.M; p.P = g.P; p.Q = g.Q; p.layout = g.out_layout;
+    if (g.l_mode == 2) {
+      p.inv = g.inv_rms; p.nw = g.norm_weight; p.nw_f32 = g.w_dtype == MOLT_DTYPE_F32; p.noff = g.norm_offset;
+    }
     p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + off);
     off += grad_ws_bytes(g.M, g.P, g.Q);
-    const bool vec = g.P % 8 == 0 && g.Q % 8 == 0 && g.ldl % 8 == 0 && g.ldr % 8 == 0 && aligned(g.l, 16) &&
-                     aligned(g.rmat, 16);
-    all_dma = all_dma && g.M > 0 && vec && g.l_mode == 0 && molt::tuning_value(MOLT_TUNE_LORA_DMA) != 0 &&
-              ((g.M - 1) * g.ldl + g.P) * 2 < ((int64_t)1 << 31) && ((g.M - 1) * g.ldr + g.Q) * 2 < ((int64_t)1 << 31);
+    vecs[i] = vec;
+    // plain aligned operands whose byte offsets fit the buffer resources share the DMA launch
+    batched[i] = g.M > 0 && vec && g.l_mode == 0 && molt::tuning_value(MOLT_TUNE_LORA_DMA) != 0 &&
+                 ((g.M - 1) * g.ldl + g.P) * 2 < ((int64_t)1 << 31) &&
+                 ((g.M - 1) * g.ldr + g.Q) * 2 < ((int64_t)1 << 31);
   }
   MOLT_REQUIRE(workspace ? workspace_bytes >= off && aligned(workspace, 256) : off == 0, MOLT_EWORKSPACE,
                "%s: workspace %zu < %zu bytes (or not 256-byte aligned)", who, workspace_bytes, off);
-  if (!all_dma) {   // one launch pair per gradient
-    for (int i = 0; i < n; ++i) {
-      int rc;
-      if (d[i].M == 0) {
-        rc = zero_grad(d[i].out, d[i].P, d[i].Q, st, who);
-      } else {
-        const bool vec = d[i].P % 8 == 0 && d[i].Q % 8 == 0 && d[i].ldl % 8 == 0 && d[i].ldr % 8 == 0 &&
-                         aligned(d[i].l, 16) && aligned(d[i].rmat, 16) && (d[i].l_mode == 0 || aligned(d[i].l2, 16));
-        rc = launch_grad(ps[i], vec, d[i].l_mode, d[i].scale, d[i].out, d[i].out_layout, ps[i].part,
-                         grad_ws_bytes(d[i].M, d[i].P, d[i].Q), st, who);
-      }
-      if (rc) return rc;
-    }
-    return MOLT_OK;
-  }
+  GradMany gm{};
+  ReduceMany rm{};
   int blocks = 0;
   int64_t items = 0;
+  int rc;
   for (int i = 0; i < n; ++i) {
     GradParams& p = ps[i];
-    const int S = grad_splits(p.M, p.P, p.Q);
-    p.slice = ceil_div64(ceil_div64(p.M, S), BK) * BK;
-    const int S_eff = (int)ceil_div64(p.M, p.slice);
-    gm.g[i] = p;
-    gm.gx[i] = (int)ceil_div64(p.P, GR_P);
-    gm.gy[i] = (int)ceil_div64(p.Q, GR_Q);
-    gm.first[i] = blocks;
-    MOLT_REQUIRE((int64_t)blocks + (int64_t)gm.gx[i] * gm.gy[i] * S_eff < (1ll << 31), MOLT_EINVAL,
-                 "%s: problem too large", who);
-    blocks += gm.gx[i] * gm.gy[i] * S_eff;
+    if (p.M == 0) {   // nothing to sum: the gradient is zero
+      rc = zero_grad(d[i].out, p.P, p.Q, st, who);
+      if (rc) return rc;
+      continue;
+    }
+    const int S_eff = grad_slices(p);
+    if (batched[i]) {
+      const int k = gm.n++;
+      gm.g[k] = p;
+      gm.gx[k] = (int)ceil_div64(p.P, GR_P);
+      gm.gy[k] = (int)ceil_div64(p.Q, GR_Q);
+      gm.first[k] = blocks;
+      MOLT_REQUIRE((int64_t)blocks + (int64_t)gm.gx[k] * gm.gy[k] * S_eff < (1ll << 31), MOLT_EINVAL,
+                   "%s: problem too large", who);
+      blocks += gm.gx[k] * gm.gy[k] * S_eff;
+    } else {
+      grad_kernel_launch(p, vecs[i], p.mode, S_eff, st);
+      rc = check_launch(who);
+      if (rc) return rc;
+    }
+    const int k = rm.cnt++;
     const int64_t nel = p.P * p.Q;
-    rm.part[i] = p.part; rm.out[i] = d[i].out; rm.n[i] = nel; rm.scale[i] = d[i].scale; rm.S[i] = S_eff;
-    rm.vec4[i] = nel % 4 == 0 && aligned(p.part, 16) && aligned(d[i].out, 16);
-    rm.first[i] = items;
-    items += rm.vec4[i] ? nel / 4 : nel;
+    rm.part[k] = p.part; rm.out[k] = d[i].out; rm.n[k] = nel; rm.scale[k] = d[i].scale; rm.S[k] = S_eff;
+    rm.vec4[k] = nel % 4 == 0 && aligned(p.part, 16) && aligned(d[i].out, 16);
+    rm.first[k] = items;
+    items += rm.vec4[k] ? nel / 4 : nel;
   }
-  gm.first[n] = blocks;
-  gm.n = n;
-  rm.first[n] = items;
-  rm.cnt = n;
-  hipLaunchKernelGGL(lora_grad_dma_many_kernel, dim3((unsigned)blocks), dim3(GR_NT), 0, st, gm);
-  int rc = check_launch(who);
-  if (rc) return rc;
+  if (gm.n) {
+    gm.first[gm.n] = blocks;
+    hipLaunchKernelGGL(lora_grad_dma_many_kernel, dim3((unsigned)blocks), dim3(GR_NT), 0, st, gm);
+    rc = check_launch(who);
+    if (rc) return rc;
+  }
+  if (rm.cnt == 0) return MOLT_OK;
+  rm.first[rm.cnt] = items;
   int64_t rb = ceil_div64(items, 256);
   if (rb > 4096) rb = 4096;
   hipLaunchKernelGGL(lora_grad_reduce_many_kernel, dim3((unsigned)rb), dim3(256), 0, st, rm);

@@ -259,23 +259,28 @@ def _fused_backward(grad_output, flat, gate, up, gated, t_gu, t_d, gate_packed, 
         resolved_nf4_scales(up_qs), gate_qs.code, i_dim, h_dim, nibble_order(gate_qs), u_g, u_u, gate_a,
         up_a, wgt, wut)
     del wgt, wut
-    # The adapter gradients with plain operands run as one launch (and one
-    # split-sum launch), bitwise as separate calls: dB_d over dY, dB_g over dg,
-    # dB_u over du, dA_d over h when the forward kept it, and dA_gate / dA_up
-    # as one pass over X with [U_g | U_u] when X is materialised.
-    plain = [(dy, t_d, s_d, 0), (dg, t_gu[:, :r], s_g, 0), (du, t_gu[:, r:], s_u, 0)]
-    if gated is not None:   # h kept from the forward: bitwise the replayed value
-        plain.append((gated, u_d, 1.0, 1))
-    if norm is None:
-        plain.append((flat, u_gu, 1.0, 1))
-    grads = ops.direct.lora_grad_many([g[0] for g in plain], [None] * len(plain), [0] * len(plain),
-                                      [g[1] for g in plain], [float(g[2]) for g in plain], [g[3] for g in plain])
-    d_down_b, d_gate_b, d_up_b = grads[0], grads[1], grads[2]
-    d_down_a = grads[3] if gated is not None else ops.direct.lora_grad(gate, up, 1, u_d, 1.0, 1)
-    if norm is not None:
-        d_gu_a = ops.direct.lora_grad_rmsnorm(norm[0], norm[1], norm[2], norm[3], u_gu, 1.0, 1)
+    # Every adapter gradient in one call with one split-sum launch, each bitwise
+    # its own call: dB_d over dY, dB_g over dg and dB_u over du (one launch
+    # together), dA_d over h (kept from the forward, or replayed from gate and
+    # up: bitwise the same), and dA_gate / dA_up as one pass over X with
+    # [U_g | U_u] (X materialised, or the frozen RMSNorm's output replayed
+    # from its source).
+    ls, l2s, modes = [dy, dg, du], [None, None, None], [0, 0, 0]
+    rmats, scales = [t_d, t_gu[:, :r], t_gu[:, r:]], [float(s_d), float(s_g), float(s_u)]
+    if gated is not None:
+        ls.append(gated); l2s.append(None); modes.append(0)
     else:
-        d_gu_a = grads[-1]
+        ls.append(gate); l2s.append(up); modes.append(1)
+    norm_args = ()
+    if norm is None:
+        ls.append(flat); l2s.append(None); modes.append(0)
+    else:
+        ls.append(norm[0]); l2s.append(None); modes.append(2)
+        norm_args = (norm[1], norm[2], float(norm[3]))
+    rmats += [u_d, u_gu]
+    scales += [1.0, 1.0]
+    d_down_b, d_gate_b, d_up_b, d_down_a, d_gu_a = ops.direct.lora_grad_many(ls, l2s, modes, rmats, scales,
+                                                                            [0, 0, 0, 1, 1], *norm_args)
     return dx, d_gu_a[:r], d_gate_b, d_gu_a[r:], d_up_b, d_down_a, d_down_b
 
 

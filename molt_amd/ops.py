@@ -471,8 +471,8 @@ def lora_project_pair(z0: Tensor, z1: Tensor, zscale0: float, zscale1: float, lo
         raise ValueError(f"{what}: adapters {tuple(l0.shape)}, {tuple(l1.shape)} must both be [{d}, r]")
     # both adapters packed in one launch, then one projection launch for the pair
     # (bitwise lora_project_pair_packed)
-    packs = lora_pack_many([l0, l1], [None, None], [1, 1])
-    return lora_project_pair_packed(z0, z1, zscale0, zscale1, packs[0], packs[1], l0.shape[1])
+    packs = direct.lora_pack_many([l0, l1], [None, None], [1, 1])
+    return direct.lora_project_pair_packed(z0, z1, zscale0, zscale1, packs[0], packs[1], l0.shape[1])
 
 
 @lora_project_pair.register_fake
@@ -1090,34 +1090,51 @@ def _(l, l2, mode, rmat, scale, layout):
 
 @_custom_op(f"{NS}::lora_grad_many", mutates_args=())
 def lora_grad_many(ls: list[Tensor], l2s: list[Optional[Tensor]], modes: list[int], rmats: list[Tensor],
-                   scales: list[float], layouts: list[int]) -> list[Tensor]:
-    """Several ``lora_grad`` results (1..8) from one launch and one split-sum
-    launch (molt_lora_grad_many); each output is bitwise that of its own
-    ``lora_grad`` call."""
+                   scales: list[float], layouts: list[int], norm_inv: Optional[Tensor] = None,
+                   norm_weight: Optional[Tensor] = None, norm_offset: float = 0.0) -> list[Tensor]:
+    """Several (1..8) ``lora_grad`` (modes 0, 1) results and at most one
+    ``lora_grad_rmsnorm`` result (mode 2: ``ls[i]`` is the norm's input x,
+    with ``norm_inv``, ``norm_weight`` and ``norm_offset``) with one split-sum
+    launch (molt_lora_grad_many): the plain aligned ones share one launch, the
+    others take a launch each. Each output is bitwise that of its own call."""
     what = "LoRA gradients"
     n = len(ls)
     if not (1 <= n <= 8) or not (len(l2s) == len(modes) == len(rmats) == len(scales) == len(layouts) == n):
         raise ValueError(f"{what}: 1..8 gradients with one entry per argument list")
-    dev = _require_gpu(*ls, *[t for t in l2s if t is not None], *rmats, what=what)
+    n_norm = sum(1 for md in modes if int(md) == 2)
+    if n_norm > 1 or (n_norm == 1) != (norm_inv is not None and norm_weight is not None):
+        raise ValueError(f"{what}: at most one RMSNorm-replay gradient, with its inv_rms and weight")
+    dev = _require_gpu(*ls, *[t for t in l2s if t is not None], *rmats, norm_inv, norm_weight, what=what)
     keep, outs = [], []
     descs = (_lib.LoraGradDesc * n)()
     for i in range(n):
+        mode = int(modes[i])
         # a plain left operand may be a column slice of a wider matrix (its row stride is passed)
-        l = _bf16_rows(ls[i], "activations", what) if l2s[i] is None else _bf16(ls[i], "activations", what)
-        l2 = None if l2s[i] is None else _bf16(l2s[i], "activations", what)
+        l = _bf16_rows(ls[i], "activations", what) if mode == 0 else _bf16(ls[i], "activations", what)
+        l2 = _bf16(l2s[i], "activations", what) if mode == 1 else None
         rmat = _bf16_rows(rmats[i], "low-rank operand", what)
-        if l2 is not None and l2.shape != l.shape:
-            raise ValueError(f"{what}: the second operand {tuple(l2.shape)} must match {tuple(l.shape)}")
+        if mode == 1 and (l2 is None or l2.shape != l.shape):
+            raise ValueError(f"{what}: the SwiGLU replay needs an up operand of shape {tuple(l.shape)}")
         if l.dim() != 2 or rmat.dim() != 2 or l.shape[0] != rmat.shape[0]:
             raise ValueError(f"{what}: row counts differ ({tuple(l.shape)} vs {tuple(rmat.shape)})")
         m, p = l.shape
         q = rmat.shape[1]
+        inv = w = None
+        w_dtype, offset = 0, 0.0
+        if mode == 2:
+            inv, w, offset = norm_inv, norm_weight.detach().contiguous(), float(norm_offset)
+            if inv.dtype != torch.float32 or inv.shape != (m,):
+                raise ValueError(f"{what}: inv_rms must be fp32 [{m}]")
+            if w.numel() != p:
+                raise ValueError(f"{what}: norm weight has {w.numel()} elements for {p} features")
+            inv = inv.contiguous()
+            w_dtype = _rn_dtype(w, "weight")
         out = torch.empty((p, q) if layouts[i] == 0 else (q, p), device=dev, dtype=torch.float32)
-        keep += [l, l2, rmat]
+        keep += [l, l2, rmat, inv, w]
         outs.append(out)
-        descs[i] = _lib.LoraGradDesc(l.data_ptr(), _ptr(l2), max(l.stride(0), p), int(modes[i]), rmat.data_ptr(),
+        descs[i] = _lib.LoraGradDesc(l.data_ptr(), _ptr(l2), max(l.stride(0), p), mode, rmat.data_ptr(),
                                      max(rmat.stride(0), q), m, p, q, float(scales[i]), out.data_ptr(),
-                                     int(layouts[i]))
+                                     int(layouts[i]), _ptr(inv), _ptr(w), w_dtype, offset)
     ws_bytes = int(_lib.load().molt_lora_grad_many_workspace(n, descs))
     ws = torch.empty(max(ws_bytes, 256), device=dev, dtype=torch.uint8)
     _call("molt_lora_grad_many", n, descs, ws.data_ptr(), ws_bytes, _stream(dev))
@@ -1126,7 +1143,7 @@ def lora_grad_many(ls: list[Tensor], l2s: list[Optional[Tensor]], modes: list[in
 
 
 @lora_grad_many.register_fake
-def _(ls, l2s, modes, rmats, scales, layouts):
+def _(ls, l2s, modes, rmats, scales, layouts, norm_inv=None, norm_weight=None, norm_offset=0.0):
     return [l.new_empty((l.shape[1], r.shape[1]) if lay == 0 else (r.shape[1], l.shape[1]), dtype=torch.float32)
             for l, r, lay in zip(ls, rmats, layouts)]
 

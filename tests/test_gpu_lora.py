@@ -15,6 +15,7 @@ from tests._util import assert_close_fro, bf16_values, np_f32, seeded, uniform
 
 import molt_amd
 from molt_amd import _lib, ops
+from molt_amd.errors import CapabilityError
 
 pytestmark = pytest.mark.gpu
 
@@ -229,6 +230,35 @@ def test_lora_grad_many_equals_separate_calls(case):
     for a_, b_, c_ in zip(sep, many, again):
         assert a_.shape == b_.shape
         assert torch.equal(a_, b_) and torch.equal(b_, c_)
+
+
+def test_lora_grad_many_with_replayed_operands():
+    """The RMSNorm-replay recipe's adapter gradients at cfg3's shapes as one
+    call: dB over dY, dg and du (one launch together), dA_d over h replayed
+    from gate and up, dA_gate / dA_up over the RMSNorm output replayed from
+    its source, and one split-sum launch. Each is bitwise its own lora_grad /
+    lora_grad_rmsnorm call. A replayed norm whose rows the kernel cannot take
+    is refused before any launch."""
+    m, h, i, r = 4096, 1536, 8960, 16
+    print(f"lora_grad_many with SwiGLU and RMSNorm replay m={m} H={h} I={i} r={r}", flush=True)
+    dy, dg, du = seeded((m, h), 90), seeded((m, i), 91), seeded((m, i), 92)
+    g, u = seeded((m, i), 93), seeded((m, i), 94)
+    src, w = seeded((m, h), 95, std=1.3), seeded((h,), 96, std=0.3)
+    inv = ops.rmsnorm_inv(src, w, 1e-6)
+    t_d, t_gu, u_d, u_gu = seeded((m, r), 97), seeded((m, 2 * r), 98), seeded((m, r), 99), seeded((m, 2 * r), 100)
+    many = ops.lora_grad_many([dy, dg, du, g, src], [None, None, None, u, None], [0, 0, 0, 1, 2],
+                              [t_d, t_gu[:, :r], t_gu[:, r:], u_d, u_gu], [2.0, 2.0, 2.0, 1.0, 1.0],
+                              [0, 0, 0, 1, 1], inv, w, 0.25)
+    sep = [ops.lora_grad(dy, None, 0, t_d, 2.0, 0), ops.lora_grad(dg, None, 0, t_gu[:, :r], 2.0, 0),
+           ops.lora_grad(du, None, 0, t_gu[:, r:], 2.0, 0), ops.lora_grad(g, u, 1, u_d, 1.0, 1),
+           ops.lora_grad_rmsnorm(src, inv, w, 0.25, u_gu, 1.0, 1)]
+    torch.cuda.synchronize()
+    for k, (a_, b_) in enumerate(zip(sep, many)):
+        assert a_.shape == b_.shape and torch.equal(a_, b_), f"gradient {k}"
+    bad, bad_w = seeded((64, 203), 101), seeded((203,), 102)    # 203 features: rows of 406 bytes
+    with pytest.raises(CapabilityError):
+        ops.lora_grad_many([bad], [None], [2], [seeded((64, 8), 103)], [1.0], [1],
+                           torch.ones(64, device="cuda"), bad_w, 0.0)
 
 
 @pytest.mark.parametrize("m,d,r,mode,layout,stacked", [
