@@ -513,9 +513,11 @@ def lm_head_bench(dev, steps: int = 5):
     """The frozen LM head of the cfg3 decoder (Qwen2.5-1.5B: vocabulary
     151,936 x hidden 1,536, bf16) over M=4096 tokens in chunks of 256 through
     frozen_linear_cross_entropy: loss and hidden gradient (two hipBLASLt GEMMs
-    per chunk, 4*M*V*H FLOPs in all, plus the HIP row reduction). The row
-    kernel alone is timed on one [256, V] chunk against its algorithmic bytes
-    (read the logits once, write the gradient once)."""
+    per chunk, 4*M*V*H FLOPs in all, plus the HIP row reduction); also in one
+    chunk of all 4096 rows (1.2 GB of bf16 logits, which the GPU's 288 GB
+    hold; the reference's default is no chunking). The row kernel alone is
+    timed on one [256, V] chunk against its algorithmic bytes (read the logits
+    once, write the gradient once)."""
     import torch
     from molt_amd import ops
     from molt_amd.kernels.frozen_linear_cross_entropy import frozen_linear_cross_entropy
@@ -526,20 +528,23 @@ def lm_head_bench(dev, steps: int = 5):
     h = torch.randn(M, H, generator=g).to(dev, torch.bfloat16).requires_grad_()
     t = torch.randint(0, V, (M,), generator=g).to(dev)
 
-    def run():
+    def run(c):
         h.grad = None
-        frozen_linear_cross_entropy(h, w, t, chunk).backward()
+        frozen_linear_cross_entropy(h, w, t, c).backward()
 
-    for _ in range(2):
-        run()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        run()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / steps
     flop = 4 * M * V * H
-    tf = flop / (ms * 1e-3) / 1e12
+    timed = {}
+    for c in (chunk, M):
+        for _ in range(2):
+            run(c)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            run(c)
+        torch.cuda.synchronize()
+        timed[c] = (time.perf_counter() - t0) * 1e3 / steps
+    ms, ms_one = timed[chunk], timed[M]
+    tf, tf_one = flop / (ms * 1e-3) / 1e12, flop / (ms_one * 1e-3) / 1e12
     logits = torch.randn(chunk, V, generator=g).to(dev, torch.bfloat16)
     tc = t[:chunk].contiguous()
     copies = [logits.clone() for _ in range(8)]
@@ -557,9 +562,11 @@ def lm_head_bench(dev, steps: int = 5):
     gbs = nbytes / (us * 1e-6) / 1e9
     log(f"LM head V={V} H={H} M={M} chunk={chunk}: loss+grad {ms:.3f} ms, {tf:.0f} TFLOP/s "
         f"({100 * tf / PEAK_BF16_TFLOPS:.1f}%); row kernel {us:.1f} us per chunk, {gbs:.0f} GB/s "
-        f"({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM)")
+        f"({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM); one chunk of {M}: {ms_one:.3f} ms, {tf_one:.0f} TFLOP/s "
+        f"({100 * tf_one / PEAK_BF16_TFLOPS:.1f}%)")
     return {"vocab": V, "hidden": H, "tokens": M, "chunk": chunk, "ms_loss_and_grad": round(ms, 4),
             "TFLOP_s": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+            "ms_loss_and_grad_one_chunk": round(ms_one, 4), "TFLOP_s_one_chunk": round(tf_one, 1),
             "row_kernel_us_per_chunk": round(us, 2), "row_kernel_GB_s": round(gbs, 1),
             "row_kernel_frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
 
