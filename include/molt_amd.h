@@ -75,7 +75,8 @@ const char* molt_amd_version(void);
  *   MOLT_TUNE_BIG_TILE_MIN  (MOLT_AMD_BIG_TILE_MIN, default 256): fewest
  *       256 x 256 output tiles for which the GEMMs use the large-tile kernels.
  *   MOLT_TUNE_GEMV_DOT_M    (MOLT_AMD_GEMV_DOT_M, default -1 = per-shape rule,
- *       else 0..4): largest token count for the streaming dot-product GEMV.
+ *       else 0..8): largest token count for the streaming dot-product GEMV
+ *       (5..8 tokens only where K <= 4096).
  *   MOLT_TUNE_LORA_DMA      (0 when MOLT_AMD_PJ_NODMA is set, else 1): LDS DMA
  *       staging in the LoRA projection and in the (plain-operand) LoRA
  *       gradient; 0 selects the register-staged kernels (same results).

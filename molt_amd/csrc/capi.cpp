@@ -54,7 +54,7 @@ struct Tuning {
     v[MOLT_TUNE_BIG_TILE_MIN].store(e ? atoll(e) : 256);
     e = getenv("MOLT_AMD_GEMV_DOT_M");
     const int64_t m = e ? atoll(e) : -1;
-    v[MOLT_TUNE_GEMV_DOT_M].store(m < -1 ? -1 : (m > 4 ? 4 : m));
+    v[MOLT_TUNE_GEMV_DOT_M].store(m < -1 ? -1 : (m > 8 ? 8 : m));
     v[MOLT_TUNE_LORA_DMA].store(getenv("MOLT_AMD_PJ_NODMA") ? 0 : 1);
     v[MOLT_TUNE_SPLIT_K].store(getenv("MOLT_AMD_NO_SPLIT_K") ? 0 : 1);
     e = getenv("MOLT_AMD_SPLIT_MIN_STEPS");
@@ -72,7 +72,7 @@ Tuning& tuning() {
 bool tuning_ok(int32_t key, int64_t value) {
   switch (key) {
     case MOLT_TUNE_BIG_TILE_MIN: return value >= 0;
-    case MOLT_TUNE_GEMV_DOT_M: return value >= -1 && value <= 4;
+    case MOLT_TUNE_GEMV_DOT_M: return value >= -1 && value <= 8;
     case MOLT_TUNE_LORA_DMA: return value == 0 || value == 1;
     case MOLT_TUNE_SPLIT_K: return value == 0 || value == 1;
     case MOLT_TUNE_SPLIT_MIN_STEPS: return value >= 2 && value <= 4096;

@@ -1028,17 +1028,23 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
   // value (a wholly idle piece re-reads the row's last bytes and is dropped).
   // Where the MFMA kernel does not take K (not 8, or a multiple of 7 or 8,
   // chunks of 512), the dot kernel also serves M = 3, 4.
+  // M = 5..8 over at most 2048 rows and K <= 4096 (eight X rows of at most
+  // two pieces fit in LDS beside the code table): eight tokens per lookup,
+  // where the MFMA kernel, with one 16-row group per workgroup, leaves most
+  // CUs idle.
   int gm_nw_probe = 8;
   const bool gm_takes_k = gm_slices(4, w->cols, gm_nw_probe) > 0;
-  const int dot_max_m = (int)molt::tuning_value(MOLT_TUNE_GEMV_DOT_M);
-  const bool dot_m = dot_max_m >= 0 ? M <= dot_max_m
-                                    : (M <= 2 || (M <= 4 && (w->cols == 14336 || w->rows <= 2048 || !gm_takes_k)));
   const int ipr_need = (int)ceil_div64(w->cols, 2048);
+  const int dot_max_m = (int)molt::tuning_value(MOLT_TUNE_GEMV_DOT_M);
+  const bool dot_m = (dot_max_m >= 0 ? M <= dot_max_m
+                                     : (M <= 2 || (M <= 4 && (w->cols == 14336 || w->rows <= 2048 || !gm_takes_k)) ||
+                                        (M <= 8 && w->rows <= 2048))) &&
+                     (M <= 4 || ipr_need <= 2);
   if (dot_m && ipr_need <= 7 && aligned(w->packed, 16)) {
     const int ipr = ipr_need <= 3 ? ipr_need : (ipr_need <= 5 ? 5 : 7);
     const int cus = molt::device_cus();
     const int rw = 1;                                         // rows per wave per round
-    const int mx = M == 1 ? 1 : (M == 2 ? 2 : 4);             // X rows held by the kernel
+    const int mx = M == 1 ? 1 : (M == 2 ? 2 : (M <= 4 ? 4 : 8));   // X rows held by the kernel
     // One workgroup per CU, so that each wave has more rounds over the same
     // set-up work (code table, X, LoRA operands): one token 4096^2 5.2 -> 4.95
     // us, 14336 x 4096 10.5-11.2 -> 10.1-10.2 us, 8960 x 1536 6.4 -> 5.4 us;
@@ -1073,8 +1079,13 @@ extern "C" int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const mo
     else if (nested) { if (r > 0) MOLT_GDK(IPRv, MXv, true, true, 0); else MOLT_GDK(IPRv, MXv, true, false, 0); } \
     else { if (r > 0) MOLT_GDK(IPRv, MXv, false, true, 0); else MOLT_GDK(IPRv, MXv, false, false, 0); }     \
   } while (0)
-#define MOLT_GDI(IPRv) \
-  do { if (mx == 1) MOLT_GD(IPRv, 1); else if (mx == 2) MOLT_GD(IPRv, 2); else MOLT_GD(IPRv, 4); } while (0)
+#define MOLT_GDI(IPRv)                                                                               \
+  do {                                                                                                 \
+    if (mx == 1) MOLT_GD(IPRv, 1);                                                                     \
+    else if (mx == 2) MOLT_GD(IPRv, 2);                                                                \
+    else if (mx == 4) MOLT_GD(IPRv, 4);                                                                \
+    else MOLT_GD((IPRv <= 2 ? IPRv : 2), 8);   /* eight rows: at most two pieces (see dot_m) */       \
+  } while (0)
     switch (ipr) {
       case 1: MOLT_GDI(1); break;
       case 2: MOLT_GDI(2); break;

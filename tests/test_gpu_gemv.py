@@ -236,7 +236,7 @@ def test_patched_module_decode_runs_the_gemv(m):
 
 @pytest.mark.parametrize("n,k", [(1536, 1536), (256, 1536), (8960, 1536), (1536, 8960), (4864, 896), (896, 4864),
                                  (520, 2112), (300, 8192), (130, 6144), (70, 10240)])
-@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
 def test_gemv_any_k_matches_oracle_and_repeats(n, k, m):
     """K outside {4096, 14336}: the Qwen2.5-1.5B decode shapes of the reference's
     generate_qlora (training/qlora.py:1332-1358) and pieces that end inside a
