@@ -1208,7 +1208,7 @@ static int launch_projection_pair(const uint16_t* z0, const uint16_t* z1, int64_
                                   hipStream_t st, const char* who) {
   const int tq = (int)proj_tq(r);
   const bool dma = z_mode != 1 && D % BK == 0 && ldz % 8 == 0 && aligned(z0, 16) && aligned(z1, 16) &&
-                   molt::tuning_value(MOLT_TUNE_LORA_DMA) != 0;
+                   molt::tuning_value(MOLT_TUNE_LORA_DMA) != 0 && ((M - 1) * ldz + D) * 2 < ((int64_t)1 << 31);
   if (!dma) return MOLT_EUNSUPPORTED;
   ProjParams p{};
   p.z = z0; p.ldz = ldz; p.mode = z_mode; p.zs = zs0;
@@ -1313,7 +1313,9 @@ static int launch_projection(const uint16_t* z, const uint16_t* z2, int64_t ldz,
     else if (ks == 2) MOLT_PJK(TQ, MT, VEC, REPLAY, 2);     \
     else MOLT_PJK(TQ, MT, VEC, REPLAY, 1);                  \
   } while (0)
-  const bool dma = vec && z_mode != 1 && D % BK == 0 && molt::tuning_value(MOLT_TUNE_LORA_DMA) != 0;
+  // (the DMA kernel addresses z through a buffer resource: 32-bit byte offsets)
+  const bool dma = vec && z_mode != 1 && D % BK == 0 && molt::tuning_value(MOLT_TUNE_LORA_DMA) != 0 &&
+                   ((M - 1) * ldz + D) * 2 < ((int64_t)1 << 31);
 #define MOLT_PJD(TQ, MT)                                                                                       \
   do {                                                                                                         \
     if (ks == 4) hipLaunchKernelGGL((lora_project_dma_kernel<TQ, MT, 4>), grid, block, 0, st, p);               \

@@ -110,6 +110,26 @@ def test_lora_project_pair_is_the_two_projections_side_by_side(m, d, r):
     assert torch.equal(pair[:, :r], u0) and torch.equal(pair[:, r:], u1)
 
 
+def test_lora_project_of_an_activation_beyond_4gib():
+    """z of 4.3 GB: byte offsets past 2^32 do not fit the DMA kernel's 32-bit
+    buffer offsets (they wrapped before the projection checked the range), so
+    such a z takes the register kernel; its first and last rows against torch
+    over the same bf16 operands."""
+    m, d, r = 131200, 16384, 16
+    print(f"lora_project m={m} d={d} r={r} ({m * d * 2 / 2**30:.2f} GiB of z)", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(7)
+    z = torch.empty((m, d), device="cuda", dtype=torch.bfloat16)
+    z.normal_(generator=g)
+    a = uniform((r, d), 8, d ** -0.5)
+    out = ops.lora_project(z, None, 0, 1.0, a, 0)
+    ab = a.to(torch.bfloat16).float()
+    for rows in (slice(0, 128), slice(m - 128, m)):
+        ref = (z[rows].float() @ ab.T).double().cpu().numpy()
+        assert_close_fro(np_f32(out[rows]), O.bf16_round(ref), what=f"T rows {rows.start}..{rows.stop}")
+    del z
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("m,d,r,same_split", [(4096, 8960, 16, False), (2048, 2048, 32, True)])
 def test_lora_project_pair_one_launch(m, d, r, same_split):
     """The pair as one launch (molt_lora_project_pair_packed): its split over D
