@@ -700,9 +700,12 @@ MOLT_DEV bf16x8_t gd_frag(const uint16_t* __restrict__ s, int base, int stride) 
 }
 
 // One workgroup of the DMA-staged gradient: P tile bx, Q tile by, M slice bz.
+// Stages of GS_BK = 32 rows: the three-stage ring takes 36 KB of LDS, so four
+// workgroups (16 waves) share a CU and hide each other's fragment gathers.
+constexpr int GS_BK = 32, GS_LT = GS_BK * GR_P, GS_RT = GS_BK * GR_Q;
 MOLT_DEV void grad_dma_tile(const GradParams& p, int bx, int by, int bz) {
-  __shared__ __attribute__((aligned(16))) uint16_t la[GD_LT], lb[GD_LT], lc[GD_LT];
-  __shared__ __attribute__((aligned(16))) uint16_t ra[GD_RT], rb[GD_RT], rc[GD_RT];
+  __shared__ __attribute__((aligned(16))) uint16_t la[GS_LT], lb[GS_LT], lc[GS_LT];
+  __shared__ __attribute__((aligned(16))) uint16_t ra[GS_RT], rb[GS_RT], rc[GS_RT];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wp = wave & 1, wq = wave >> 1, h = lane >> 5;
@@ -710,34 +713,32 @@ MOLT_DEV void grad_dma_tile(const GradParams& p, int bx, int by, int bz) {
   const int64_t q0 = (int64_t)by * GR_Q;
   const int64_t mbeg = (int64_t)bz * p.slice;
   const int64_t mend = mbeg + p.slice < p.M ? mbeg + p.slice : p.M;
-  const int steps = (int)ceil_div64(mend - mbeg, BK);
+  const int steps = (int)ceil_div64(mend - mbeg, GS_BK);
   const __amdgpu_buffer_rsrc_t lr = pj_rsrc(p.l, ((p.M - 1) * p.ldl + p.P) * 2);
   const __amdgpu_buffer_rsrc_t rr = pj_rsrc(p.rm, ((p.M - 1) * p.ldr + p.Q) * 2);
   // DMA instruction c of L covers rows 4c .. 4c + 3 (16 lanes per 256-byte
   // row), of R rows 8c .. 8c + 7 (8 lanes per 128-byte row); a wave issues
-  // L instructions 4 wave .. + 3 and R instructions 2 wave, 2 wave + 1.
-  uint32_t loff[4], roff[2];
+  // L instructions 2 wave, 2 wave + 1 and R instruction wave.
+  uint32_t loff[2], roff;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = 4 * (4 * wave + j) + (lane >> 4);
+  for (int j = 0; j < 2; ++j) {
+    const int r = 4 * (2 * wave + j) + (lane >> 4);
     const int ch = (lane & 15) ^ (4 * ((r >> 3) & 1));
     loff[j] = (uint32_t)((r * p.ldl + p0 + 8 * ch) * 2);
   }
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int r = 8 * (2 * wave + j) + (lane >> 3);
+  {
+    const int r = 8 * wave + (lane >> 3);
     const int ch = (lane & 7) ^ (4 * ((r >> 3) & 1));
-    roff[j] = (uint32_t)((r * p.ldr + q0 + 8 * ch) * 2);
+    roff = (uint32_t)((r * p.ldr + q0 + 8 * ch) * 2);
   }
   auto dma = [&](int s, uint16_t* ld, uint16_t* rd) {
     s = s < steps ? s : steps - 1;   // past the end: the last stage again, never read
-    const int64_t m = mbeg + (int64_t)s * BK;
+    const int64_t m = mbeg + (int64_t)s * GS_BK;
     const uint32_t ls = __builtin_amdgcn_readfirstlane((uint32_t)(m * p.ldl * 2));
     const uint32_t rs = __builtin_amdgcn_readfirstlane((uint32_t)(m * p.ldr * 2));
 #pragma unroll
-    for (int j = 0; j < 4; ++j) pj_dma16(lr, ld + (4 * wave + j) * 512, loff[j], ls);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) pj_dma16(rr, rd + (2 * wave + j) * 512, roff[j], rs);
+    for (int j = 0; j < 2; ++j) pj_dma16(lr, ld + (2 * wave + j) * 512, loff[j], ls);
+    pj_dma16(rr, rd + wave * 512, roff, rs);
   };
   // fragment bases (row 8 h of the step; sub-step kk adds 16 rows, element e one row)
   int abase[2];
@@ -753,7 +754,7 @@ MOLT_DEV void grad_dma_tile(const GradParams& p, int bx, int by, int bz) {
   zero_acc(acc);
   dma(0, la, ra);
   dma(1, lb, rb);
-  pj_wait_vm<6>();                   // stage 0 landed; stage 1 may fly
+  pj_wait_vm<3>();                   // stage 0 landed; stage 1 may fly
   pj_barrier();
   int s = 0;
   // step s: stage s from (lcur, rcur); the DMA of stage s + 2 goes to the
@@ -761,14 +762,14 @@ MOLT_DEV void grad_dma_tile(const GradParams& p, int bx, int by, int bz) {
   auto step = [&](const uint16_t* lcur, const uint16_t* rcur, uint16_t* lnn, uint16_t* rnn) {
     dma(s + 2, lnn, rnn);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
+    for (int kk = 0; kk < GS_BK / 16; ++kk) {
       const bf16x8_t a0 = gd_frag(lcur, abase[0] + 16 * kk * GR_P, GR_P);
       const bf16x8_t a1 = gd_frag(lcur, abase[1] + 16 * kk * GR_P, GR_P);
       const bf16x8_t b0 = gd_frag(rcur, bbase + 16 * kk * GR_Q, GR_Q);
       acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[0][0], 0, 0, 0);
       acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
     }
-    pj_wait_vm<6>();                 // stage s + 1 landed; stage s + 2 may fly
+    pj_wait_vm<3>();                 // stage s + 1 landed; stage s + 2 may fly
     pj_barrier();
     return ++s < steps;
   };
@@ -781,7 +782,7 @@ MOLT_DEV void grad_dma_tile(const GradParams& p, int bx, int by, int bz) {
   grad_store_partial(p, acc, p0, q0, wp, wq, lane, bz);
 }
 
-__global__ __launch_bounds__(GR_NT, 2) void lora_grad_dma_kernel(const GradParams p) {
+__global__ __launch_bounds__(GR_NT, 4) void lora_grad_dma_kernel(const GradParams p) {
   grad_dma_tile(p, (int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z);
 }
 
@@ -798,7 +799,7 @@ struct GradMany {
   int n;
 };
 
-__global__ __launch_bounds__(GR_NT, 2) void lora_grad_dma_many_kernel(const GradMany m) {
+__global__ __launch_bounds__(GR_NT, 4) void lora_grad_dma_many_kernel(const GradMany m) {
   const int b = (int)blockIdx.x;
   int d = 0;
 #pragma unroll
