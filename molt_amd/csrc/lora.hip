@@ -596,8 +596,10 @@ MOLT_DEV void patch_store(const Patch& pt, const GradParams& p, const float (&wo
 // acc[i][0] is C[p][q]: column q = lane % 32, rows p = 8(e/4) + 4(lane/32) + e%4.
 // The partial is stored in the output's layout, so that the split sum is
 // element-wise; in layout 1 a lane's four consecutive p are one 16-byte store.
+// isub < 0: the wave's two 32-row subtiles acc[0], acc[1]; isub = 0 or 1:
+// only acc[0], which holds subtile isub (the narrow-Q wave layout).
 MOLT_DEV void grad_store_partial(const GradParams& p, const f32x16_t (&acc)[2][1], int64_t p0, int64_t q0, int wp,
-                                 int wq, int lane, int64_t slice) {
+                                 int wq, int lane, int64_t slice, int isub = -1) {
   float* out = p.part + slice * p.P * p.Q;
   const int64_t q = q0 + wq * GR_WCOLS + (lane & 31);
   if (q >= p.Q) return;
@@ -606,7 +608,8 @@ MOLT_DEV void grad_store_partial(const GradParams& p, const f32x16_t (&acc)[2][1
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const int64_t pp = p0 + wp * GR_WROWS + i * 32 + 8 * g + 4 * (lane >> 5);
+      if (isub >= 0 && i > 0) break;
+      const int64_t pp = p0 + wp * GR_WROWS + (isub >= 0 ? isub : i) * 32 + 8 * g + 4 * (lane >> 5);
       if (p.layout == 0) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -740,14 +743,19 @@ MOLT_DEV void grad_dma_tile(const GradParams& p, int bx, int by, int bz) {
     for (int j = 0; j < 2; ++j) pj_dma16(lr, ld + (2 * wave + j) * 512, loff[j], ls);
     pj_dma16(rr, rd + wave * 512, roff, rs);
   };
+  // Narrow Q tile (at most 32 columns, e.g. rank 16): the four waves take a
+  // 32-row P subtile each (wave w: rows 32 w ..) over the same 32 columns,
+  // instead of two waves per column half with one half past Q. Each output
+  // sums the same MFMA products in the same order either way.
+  const bool nq = p.Q - q0 <= GR_WCOLS;
   // fragment bases (row 8 h of the step; sub-step kk adds 16 rows, element e one row)
   int abase[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int pl = wp * GR_WROWS + 32 * i + (lane & 31);
+    const int pl = (nq ? 32 * wave : wp * GR_WROWS + 32 * i) + (lane & 31);
     abase[i] = 8 * h * GR_P + (((pl >> 3) ^ (4 * h)) << 3) + (pl & 7);
   }
-  const int ql = wq * GR_WCOLS + (lane & 31);
+  const int ql = (nq ? 0 : wq * GR_WCOLS) + (lane & 31);
   const int bbase = 8 * h * GR_Q + (((ql >> 3) ^ (4 * h)) << 3) + (ql & 7);
 
   f32x16_t acc[2][1];
@@ -764,10 +772,12 @@ MOLT_DEV void grad_dma_tile(const GradParams& p, int bx, int by, int bz) {
 #pragma unroll
     for (int kk = 0; kk < GS_BK / 16; ++kk) {
       const bf16x8_t a0 = gd_frag(lcur, abase[0] + 16 * kk * GR_P, GR_P);
-      const bf16x8_t a1 = gd_frag(lcur, abase[1] + 16 * kk * GR_P, GR_P);
       const bf16x8_t b0 = gd_frag(rcur, bbase + 16 * kk * GR_Q, GR_Q);
       acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[0][0], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
+      if (!nq) {                     // uniform per workgroup
+        const bf16x8_t a1 = gd_frag(lcur, abase[1] + 16 * kk * GR_P, GR_P);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
+      }
     }
     pj_wait_vm<3>();                 // stage s + 1 landed; stage s + 2 may fly
     pj_barrier();
@@ -779,7 +789,8 @@ MOLT_DEV void grad_dma_tile(const GradParams& p, int bx, int by, int bz) {
          step(lb, rb, la, ra) && step(lc, rc, lb, rb)) {
   }
   pj_wait_vm<0>();                   // the repeated stages past the end
-  grad_store_partial(p, acc, p0, q0, wp, wq, lane, bz);
+  if (nq) grad_store_partial(p, acc, p0, q0, wave >> 1, 0, lane, bz, wave & 1);
+  else grad_store_partial(p, acc, p0, q0, wp, wq, lane, bz);
 }
 
 __global__ __launch_bounds__(GR_NT, 4) void lora_grad_dma_kernel(const GradParams p) {
@@ -830,6 +841,9 @@ MOLT_DEV bf16x8_t gd_frag_replay(const uint16_t* __restrict__ g, const uint16_t*
 // one workgroup per CU), and each fragment element is replayed as it is
 // gathered. Same tiles, slices and MFMA operands as the other gradient
 // kernels: bitwise the gradient of the materialised h.
+// NQ: the narrow-Q wave layout of grad_dma_tile (Q <= 32, one column tile),
+// which also forms each replayed h element once instead of twice.
+template <bool NQ>
 __global__ __launch_bounds__(GR_NT, 2) void lora_grad_dma_replay_kernel(const GradParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t ga[GD_LT], gb[GD_LT], ua[GD_LT], ub[GD_LT];
   __shared__ __attribute__((aligned(16))) uint16_t ra[GD_RT], rb[GD_RT];
@@ -872,10 +886,10 @@ __global__ __launch_bounds__(GR_NT, 2) void lora_grad_dma_replay_kernel(const Gr
   int abase[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int pl = wp * GR_WROWS + 32 * i + (lane & 31);
+    const int pl = (NQ ? 32 * wave : wp * GR_WROWS + 32 * i) + (lane & 31);
     abase[i] = 8 * h * GR_P + (((pl >> 3) ^ (4 * h)) << 3) + (pl & 7);
   }
-  const int ql = wq * GR_WCOLS + (lane & 31);
+  const int ql = (NQ ? 0 : wq * GR_WCOLS) + (lane & 31);
   const int bbase = 8 * h * GR_Q + (((ql >> 3) ^ (4 * h)) << 3) + (ql & 7);
 
   f32x16_t acc[2][1];
@@ -892,10 +906,12 @@ __global__ __launch_bounds__(GR_NT, 2) void lora_grad_dma_replay_kernel(const Gr
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const bf16x8_t a0 = gd_frag_replay(gc, uc, abase[0] + 16 * kk * GR_P, GR_P);
-      const bf16x8_t a1 = gd_frag_replay(gc, uc, abase[1] + 16 * kk * GR_P, GR_P);
       const bf16x8_t b0 = gd_frag(rc, bbase + 16 * kk * GR_Q, GR_Q);
       acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc[0][0], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
+      if constexpr (!NQ) {
+        const bf16x8_t a1 = gd_frag_replay(gc, uc, abase[1] + 16 * kk * GR_P, GR_P);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc[1][0], 0, 0, 0);
+      }
     }
     pj_wait_vm<0>();                 // stage s + 1 landed
     pj_barrier();
@@ -903,7 +919,8 @@ __global__ __launch_bounds__(GR_NT, 2) void lora_grad_dma_replay_kernel(const Gr
   };
   while (step(ga, ua, ra, gb, ub, rb) && step(gb, ub, rb, ga, ua, ra)) {
   }
-  grad_store_partial(p, acc, p0, q0, wp, wq, lane, blockIdx.z);
+  if (NQ) grad_store_partial(p, acc, p0, q0, wave >> 1, 0, lane, blockIdx.z, wave & 1);
+  else grad_store_partial(p, acc, p0, q0, wp, wq, lane, blockIdx.z);
 }
 
 __global__ void zero_fill_kernel(float* __restrict__ out, int64_t n) {
@@ -1393,7 +1410,8 @@ static void grad_kernel_launch(const GradParams& p, bool vec, int lm, int S_eff,
                           ((M - 1) * p.ldl + P) * 2 < ((int64_t)1 << 31) &&
                           ((M - 1) * p.ldr + Q) * 2 < ((int64_t)1 << 31);
   if (dma) hipLaunchKernelGGL(lora_grad_dma_kernel, grid, dim3(GR_NT), 0, st, p);
-  else if (dma_replay) hipLaunchKernelGGL(lora_grad_dma_replay_kernel, grid, dim3(GR_NT), 0, st, p);
+  else if (dma_replay && Q <= GR_WCOLS) hipLaunchKernelGGL(lora_grad_dma_replay_kernel<true>, grid, dim3(GR_NT), 0, st, p);
+  else if (dma_replay) hipLaunchKernelGGL(lora_grad_dma_replay_kernel<false>, grid, dim3(GR_NT), 0, st, p);
   else if (!vec) hipLaunchKernelGGL((lora_grad_kernel<false, L_PLAIN>), grid, dim3(GR_NT), 0, st, p);
   else if (lm == L_REPLAY) hipLaunchKernelGGL((lora_grad_kernel<true, L_REPLAY>), grid, dim3(GR_NT), 0, st, p);
   else if (lm == L_NORM) hipLaunchKernelGGL((lora_grad_kernel<true, L_NORM>), grid, dim3(GR_NT), 0, st, p);

@@ -179,6 +179,8 @@ def test_lora_grad_reads_a_column_slice_in_place(m, p, q, layout):
     (2048, 384, 128, 1, False),   # two rank tiles
     (8192, 4096, 128, 1, True),   # cfg4's paired dA over X, U halves of one matrix
     (5000, 14336, 64, 0, False),  # long rows (dB over dg)
+    (3000, 8960, 80, 1, False),   # a 64-column rank tile, then a 16-column one (narrow-Q waves)
+    (4096, 8960, 16, 0, False),   # cfg3's dB over dg: one narrow rank tile
 ])
 def test_lora_grad_dma_kernel_equals_the_register_kernel(m, p, q, layout, strided):
     """The DMA-staged gradient kernel (plain aligned operands) has the same
@@ -196,7 +198,7 @@ def test_lora_grad_dma_kernel_equals_the_register_kernel(m, p, q, layout, stride
 
 
 @pytest.mark.parametrize("m,p,q,layout", [(300, 200, 16, 1), (4099, 512, 64, 1), (8192, 14336, 64, 1),
-                                          (2048, 384, 128, 0)])
+                                          (2048, 384, 128, 0), (4096, 8960, 16, 1), (1000, 700, 32, 0)])
 def test_lora_grad_dma_replay_equals_register_and_materialised(m, p, q, layout):
     """The DMA-staged SwiGLU-replay gradient equals the register-staged replay
     and the gradient over the materialised h = bf16(bf16(silu(g)) u), bit for bit."""
