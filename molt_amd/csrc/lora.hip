@@ -649,6 +649,12 @@ __global__ __launch_bounds__(GR_NT) void lora_grad_kernel(const GradParams p) {
   }
   f32x16_t acc[2][1];
   zero_acc(acc);
+  // a replayed operand's rank tile of at most 32 columns: four 32-row P
+  // subtiles over the same columns (wave w: rows 32 w ..), no wave on
+  // columns past Q; uniform (plain L keeps the 2 x 2 layout, whose registers
+  // allow three workgroups per CU)
+  const bool nq = LM != L_PLAIN && p.Q - q0 <= GR_WCOLS;
+  f32x16_t (&acc0)[1][1] = *reinterpret_cast<f32x16_t(*)[1][1]>(&acc[0]);
   Patch pt;
   patch_load<VEC, LM>(pt, p, wave, lane, mbeg, mend, p0, q0);
   patch_store<VEC, LM>(pt, p, wo, ls[0], rs[0], wave, lane);
@@ -657,14 +663,16 @@ __global__ __launch_bounds__(GR_NT) void lora_grad_kernel(const GradParams p) {
     for (int s = 0; s < steps; ++s) {
       const int cur = s & 1;
       if (s + 1 < steps) patch_load<VEC, LM>(pt, p, wave, lane, mbeg + (int64_t)(s + 1) * BK, mend, p0, q0);
-      mfma_step<2, 1>(ls[cur], rs[cur], wp * GR_WROWS, wq * GR_WCOLS, acc, lane);
+      if (nq) mfma_step<1, 1>(ls[cur], rs[cur], 32 * wave, 0, acc0, lane);
+      else mfma_step<2, 1>(ls[cur], rs[cur], wp * GR_WROWS, wq * GR_WCOLS, acc, lane);
       if (s + 1 < steps) patch_store<VEC, LM>(pt, p, wo, ls[cur ^ 1], rs[cur ^ 1], wave, lane);
       __syncthreads();
     }
   } else {
     for (int s = 0; s < steps; ++s) {
       if (s + 1 < steps) patch_load<VEC, LM>(pt, p, wave, lane, mbeg + (int64_t)(s + 1) * BK, mend, p0, q0);
-      mfma_step<2, 1>(ls[0], rs[0], wp * GR_WROWS, wq * GR_WCOLS, acc, lane);
+      if (nq) mfma_step<1, 1>(ls[0], rs[0], 32 * wave, 0, acc0, lane);
+      else mfma_step<2, 1>(ls[0], rs[0], wp * GR_WROWS, wq * GR_WCOLS, acc, lane);
       if (s + 1 >= steps) break;
       __syncthreads();                               // the single tile is consumed
       patch_store<VEC, LM>(pt, p, wo, ls[0], rs[0], wave, lane);
@@ -672,7 +680,8 @@ __global__ __launch_bounds__(GR_NT) void lora_grad_kernel(const GradParams p) {
     }
   }
 
-  grad_store_partial(p, acc, p0, q0, wp, wq, lane, blockIdx.z);
+  if (nq) grad_store_partial(p, acc, p0, q0, wave >> 1, 0, lane, blockIdx.z, wave & 1);
+  else grad_store_partial(p, acc, p0, q0, wp, wq, lane, blockIdx.z);
 }
 
 // ------------------------------------------------------------------------
