@@ -40,7 +40,8 @@ class _ScheduledNF4LoRA(torch.autograd.Function):
     @staticmethod
     def forward(ctx: Any, x: torch.Tensor, packed_weight: torch.Tensor, lora_a: torch.Tensor,
                 lora_b: torch.Tensor, quant_state: Any, scaling: float,
-                decoded_backward_weight: torch.Tensor | None, bias: torch.Tensor | None = None) -> torch.Tensor:
+                decoded_backward_weight: torch.Tensor | None, bias: torch.Tensor | None = None,
+                decode: bool = False) -> torch.Tensor:
         if x.device.type != "cuda" or packed_weight.device.type != "cuda":
             raise CapabilityError("scheduled NF4-LoRA requires CUDA tensors")
         if packed_weight.requires_grad:
@@ -73,8 +74,12 @@ class _ScheduledNF4LoRA(torch.autograd.Function):
             a_packed = ops.direct.lora_pack_many([lora_a], [None], [0])[0]
         low_rank = ops.direct.lora_project_packed(flat_x, None, 0, 1.0, a_packed, lora_a.shape[0])
         ctx.wt = None
-        if gemv_applies(flat_x, quant_state, lora_a.shape[0]):
-            # decode-sized batch: HBM-bound skinny-M GEMV instead of the MFMA GEMM
+        if decode and gemv_applies(flat_x, quant_state, lora_a.shape[0]):
+            # decode-sized batch with no gradient to flow: the HBM-bound skinny-M
+            # GEMV (block scale applied to each block's partial sum), the role
+            # bitsandbytes' gemv_4bit plays inside bnb.matmul_4bit. A forward that
+            # carries a gradient takes the GEMM on bf16(code * scale) per element,
+            # the dequantize_4bit + matmul function of the training forward.
             result = nf4_gemv_linear(flat_x, packed_weight, quant_state, low_rank, lora_b, scaling)
         else:
             args = (flat_x, packed_weight.reshape(-1), resolved_nf4_scales(quant_state), quant_state.code, n, k,
@@ -120,7 +125,7 @@ class _ScheduledNF4LoRA(torch.autograd.Function):
                                                    [grad_through_b, low_rank], [1.0, ctx.scaling], [1, 0])
         grad_bias = flat_grad.float().sum(0) if ctx.needs_input_grad[7] else None
         return (grad_x.reshape(ctx.input_shape), None, grad_a.to(lora_a.dtype), grad_b.to(lora_b.dtype),
-                None, None, None, grad_bias)
+                None, None, None, grad_bias, None)
 
 
 def scheduled_nf4_lora(
@@ -135,9 +140,15 @@ def scheduled_nf4_lora(
     bias: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """methods/nf4_lora.py:116-133, plus an optional base ``bias`` (keyword
-    only, so the reference's positional signature is unchanged)."""
+    only, so the reference's positional signature is unchanged).
+
+    The skinny-M GEMV serves only calls through which no gradient can flow
+    (grad mode off, or no operand requiring grad): decode. Any other call takes
+    the dequantised-weight GEMM, whatever its token count."""
+    decode = not (torch.is_grad_enabled()
+                  and any(t is not None and t.requires_grad for t in (x, lora_a, lora_b, bias)))
     return _ScheduledNF4LoRA.apply(x, packed_weight, lora_a, lora_b, quant_state, scaling,
-                                   decoded_backward_weight, bias)
+                                   decoded_backward_weight, bias, decode)
 
 
 def _scheduled_forward(module: torch.nn.Module, x: torch.Tensor, *args: Any, **kwargs: Any) -> torch.Tensor:

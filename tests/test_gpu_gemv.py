@@ -192,9 +192,11 @@ def test_gemv_rejects_rank_above_128():
 
 @pytest.mark.parametrize("m", [1, 2, 4])
 def test_patched_module_decode_runs_the_gemv(m):
-    """A decode-sized batch through a patched NF4-LoRA module (the
-    generate path of training/qlora.py:1332-1358) runs the GEMV entry point,
-    matches the oracle, and its backward still runs the NF4 dX GEMM."""
+    """A decode-sized batch through a patched NF4-LoRA module (the generate
+    path of training/qlora.py:1332-1358, no gradient) runs the GEMV entry
+    point and matches the oracle; the same batch carrying a gradient takes the
+    dequantised-weight GEMM, as bnb.matmul_4bit does for a training forward,
+    and its backward runs the NF4 dX GEMM."""
     from molt_amd.methods import enable_scheduled_nf4_lora
     from molt_amd.modules import synthetic_nf4_lora
 
@@ -202,32 +204,34 @@ def test_patched_module_decode_runs_the_gemv(m):
     mod = synthetic_nf4_lora(1024, 4096, 16, 32.0, device="cuda", generator=g)
     model = torch.nn.Sequential(mod)
     assert enable_scheduled_nf4_lora(model) == 1
-    x = seeded((1, m, 4096), 91 + m).requires_grad_()
-    calls = ops.probe_events("molt_nf4_gemv")
-    gemm = ops.probe_events("molt_nf4_lora_forward")
-    try:
-        with torch.autocast("cuda", dtype=torch.bfloat16):
-            y = model(x)
-        n_gemv, n_gemm = len(calls), len(gemm)
-    finally:
-        ops.probe_events("molt_nf4_gemv", False)
-        ops.probe_events("molt_nf4_lora_forward", False)
-    assert n_gemv == 1 and n_gemm == 0
+    x = seeded((1, m, 4096), 91 + m)
     qs = mod.base_layer.weight.quant_state
     wo = oracle_weight(mod.base_layer.weight, qs).dequant_bf16().astype(np.float64)
     a, b = mod.lora_A["default"].weight, mod.lora_B["default"].weight
     ref = O.lora_linear_forward(bf16_values(x).reshape(m, -1), wo, bf16_values(a), bf16_values(b), 2.0)
-    assert_close_fro(np_f32(y).reshape(m, -1), ref, what=f"patched decode M={m}")
+    for grad in (False, True):
+        xin = x.detach().clone().requires_grad_(grad)
+        calls = ops.probe_events("molt_nf4_gemv")
+        gemm = ops.probe_events("molt_nf4_lora_forward")
+        try:
+            with torch.set_grad_enabled(grad), torch.autocast("cuda", dtype=torch.bfloat16):
+                y = model(xin)
+            n_gemv, n_gemm = len(calls), len(gemm)
+        finally:
+            ops.probe_events("molt_nf4_gemv", False)
+            ops.probe_events("molt_nf4_lora_forward", False)
+        assert (n_gemv, n_gemm) == ((0, 1) if grad else (1, 0)), (grad, n_gemv, n_gemm)
+        assert_close_fro(np_f32(y).reshape(m, -1), ref, what=f"patched decode M={m} grad={grad}")
     dy = seeded((1, m, 1024), 92 + m)
     y.backward(dy)
     rdx, _, _ = O.lora_linear_backward(bf16_values(x).reshape(m, -1), wo, bf16_values(a), bf16_values(b), 2.0,
                                        bf16_values(dy).reshape(m, -1))
-    assert_close_fro(np_f32(x.grad).reshape(m, -1), rdx, what=f"patched decode dX M={m}")
+    assert_close_fro(np_f32(xin.grad).reshape(m, -1), rdx, what=f"patched decode dX M={m}")
     # the plain NF4 base projection under no_grad takes the GEMV as well
     calls = ops.probe_events("molt_nf4_gemv")
     try:
         with torch.no_grad():
-            base = mod.base_layer(x.detach())
+            base = mod.base_layer(x)
         assert len(calls) == 1
     finally:
         ops.probe_events("molt_nf4_gemv", False)
