@@ -465,8 +465,11 @@ int molt_nf4_gemv(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weig
  * molt_nf4_gemv_noalloc_limit() bytes (8 MiB) per GPU, held until the process
  * ends; a shape needing more (molt_nf4_gemv_workspace above the limit) returns
  * MOLT_EUNSUPPORTED before any launch. Every call on one GPU shares that GPU's
- * array: calls that overlap on one GPU (two streams, two threads) race. Same
- * results as molt_nf4_gemv, bit for bit. */
+ * array. Calls from different streams or host threads are ordered: each waits
+ * on an event the previous call recorded on its own stream. Calls made during a
+ * graph capture are not ordered that way (no wait, no record); replays of such a
+ * graph that overlap other calls on the same GPU race. Same results as
+ * molt_nf4_gemv, bit for bit. */
 size_t molt_nf4_gemv_noalloc_limit(void);
 int molt_nf4_gemv_noalloc(const uint16_t* x, int64_t ldx, int64_t M, const molt_nf4_weight* w,
                           const uint16_t* t, int64_t ldt, const float* lora_b, int32_t r,

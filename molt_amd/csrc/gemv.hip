@@ -1193,24 +1193,43 @@ static __device__ __align__(256) unsigned char scratch[GEMV_SCRATCH_BYTES];
 
 std::mutex g_scratch_mu;
 void* g_scratch_addr[GEMV_SCRATCH_DEVICES];
+// Per device: an event recorded after the last call that used the scratch, and
+// the stream that call ran on. A call on another stream waits on the event
+// first, so calls from different streams are ordered instead of racing.
+hipEvent_t g_scratch_done[GEMV_SCRATCH_DEVICES];
+hipStream_t g_scratch_stream[GEMV_SCRATCH_DEVICES];
+bool g_scratch_used[GEMV_SCRATCH_DEVICES];
 
-// The current device's address of `scratch`, looked up on the first call on
-// that device (with it current) and kept.
-int scratch_address(void** out, const char* who) {
+// Set-up on the first call on a device (with it current): the address of
+// `scratch` and the ordering event, both kept until the process ends. Returns
+// the device index through `dev_out`. The caller holds g_scratch_mu.
+int scratch_setup(int* dev_out, const char* who) {
   int dev = -1;
   const hipError_t de = hipGetDevice(&dev);
   MOLT_REQUIRE(de == hipSuccess && dev >= 0 && dev < GEMV_SCRATCH_DEVICES, MOLT_ELAUNCH,
                "%s: no current device (%s)", who, hipGetErrorString(de));
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_addr[dev] == nullptr) {
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     MOLT_REQUIRE(e == hipSuccess && p != nullptr, MOLT_ELAUNCH, "%s: scratch symbol lookup failed on device %d: %s",
                  who, dev, hipGetErrorString(e));
+    hipEvent_t ev = nullptr;
+    const hipError_t ee = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    MOLT_REQUIRE(ee == hipSuccess, MOLT_ELAUNCH, "%s: scratch ordering event on device %d: %s", who, dev,
+                 hipGetErrorString(ee));
+    g_scratch_done[dev] = ev;
     g_scratch_addr[dev] = p;
   }
-  *out = g_scratch_addr[dev];
+  *dev_out = dev;
   return MOLT_OK;
+}
+
+// True when `stream` is being captured into a graph. The legacy null stream
+// cannot be captured, so it is not asked.
+bool capturing(hipStream_t stream) {
+  if (stream == nullptr) return false;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
 }
 }  // namespace
 
@@ -1228,12 +1247,28 @@ extern "C" int molt_nf4_gemv_noalloc(const uint16_t* x, int64_t ldx, int64_t M, 
                "%s: M=%lld, %lld x %lld needs %zu bytes of split-K partials, more than the %zu-byte static scratch "
                "(use molt_nf4_gemv with a workspace)",
                who, (long long)M, (long long)w->rows, (long long)w->cols, need, GEMV_SCRATCH_BYTES);
-  void* ws = nullptr;
-  if (need > 0) {
-    const int rc = scratch_address(&ws, who);
-    if (rc != MOLT_OK) return rc;
+  if (need == 0) return molt_nf4_gemv(x, ldx, M, w, t, ldt, lora_b, r, scaling, y, ldy, nullptr, 0, stream);
+  // Wait, launch and record under one lock, so calls from several host threads
+  // are ordered as they take it. Under graph capture the graph's own order
+  // applies and the event is neither waited on nor recorded.
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  int dev = -1;
+  const int rc = scratch_setup(&dev, who);
+  if (rc != MOLT_OK) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool order = !capturing(s);
+  if (order && g_scratch_used[dev] && g_scratch_stream[dev] != s) {
+    const hipError_t e = hipStreamWaitEvent(s, g_scratch_done[dev], 0);
+    MOLT_REQUIRE(e == hipSuccess, MOLT_ELAUNCH, "%s: wait for the previous scratch user: %s", who,
+                 hipGetErrorString(e));
   }
   // Nothing in the scratch has to start at zero: every partial the reduction
   // reads is written earlier in the same call.
-  return molt_nf4_gemv(x, ldx, M, w, t, ldt, lora_b, r, scaling, y, ldy, ws, need, stream);
+  const int lrc = molt_nf4_gemv(x, ldx, M, w, t, ldt, lora_b, r, scaling, y, ldy, g_scratch_addr[dev], need, stream);
+  if (lrc != MOLT_OK || !order) return lrc;
+  const hipError_t e = hipEventRecord(g_scratch_done[dev], s);
+  MOLT_REQUIRE(e == hipSuccess, MOLT_ELAUNCH, "%s: record the scratch ordering event: %s", who, hipGetErrorString(e));
+  g_scratch_stream[dev] = s;
+  g_scratch_used[dev] = true;
+  return MOLT_OK;
 }

@@ -76,3 +76,30 @@ def test_noalloc_gemv_matches_workspace_gemv_on_two_calls():
     # the first shape again after the smaller ones: the shared scratch keeps no state that matters
     packed, qs, x, t, b = _problem(*cases[0][:4], 730)
     assert torch.equal(_run(True, packed, qs, x, t, b, s), _run(False, packed, qs, x, t, b, s))
+
+
+def test_noalloc_gemv_calls_on_two_streams_are_ordered():
+    """No-alloc calls alternating between two streams with no host
+    synchronisation between them all use the one scratch array; the entry point
+    orders each call after the previous one from another stream, so every
+    output equals its workspace-path result bit for bit."""
+    lib = _lib.load()
+    s = 2.0
+    probs = [_problem(16, 4096, 14336, 16, 740 + 10 * i) for i in range(4)]
+    want = [_run(False, *p, s) for p in probs]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    descs, outs = [], []
+    for i, (packed, qs, x, t, b) in enumerate(probs):
+        m, k = x.shape
+        n, r = b.shape
+        print(f"no-alloc GEMV on stream {i % 2}: M={m} N={n} K={k}", flush=True)
+        w = _descriptor(packed, qs)
+        y = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+        descs.append(w)
+        outs.append(y)
+        _lib.check(lib.molt_nf4_gemv_noalloc(x.data_ptr(), k, m, C.byref(w), t.data_ptr(), r, b.data_ptr(), r, s,
+                                             y.data_ptr(), n, streams[i % 2].cuda_stream))
+    torch.cuda.synchronize()
+    for i, (got, ref) in enumerate(zip(outs, want)):
+        assert torch.equal(got, ref), f"call {i} on stream {i % 2} differs from the workspace GEMV"
